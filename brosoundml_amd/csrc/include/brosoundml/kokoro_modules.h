@@ -1,0 +1,87 @@
+// Decoder-back-half module structs with the reference's fields
+// (include/brosoundml/kokoro_modules.h:127-132, 144-158, 228-244, 259-269,
+// 283-300, 312-340). Loading from safetensors and the inference forwards are
+// not part of this build; the structs are filled by the caller (tests, the
+// benchmark's model, or a loader).
+#pragma once
+
+#include <brosoundml/modules.h>
+#include <brotensor/tensor.h>
+
+#include <array>
+#include <vector>
+
+namespace brosoundml {
+
+struct AdaIN1dWeights {
+    int channels = 0;
+    int style_dim = 0;
+    float eps = 1e-5f;
+    Linear fc;  // (channels * 2, style_dim)
+};
+
+struct AdainResBlk1dWeights {
+    int channels_in = 0;
+    int channels_out = 0;
+    bool upsample = false;
+    bool learned_sc = false;  // dim_in != dim_out
+    AdaIN1dWeights norm1;     // channels_in
+    AdaIN1dWeights norm2;     // channels_out
+    Conv1d conv1;             // (channels_out, channels_in, 3)
+    Conv1d conv2;             // (channels_out, channels_out, 3)
+    Conv1d conv1x1;           // (channels_out, channels_in, 1) when learned_sc
+    brotensor::Tensor pool_W; // (channels_in, 3)  depthwise ConvTranspose1d
+    brotensor::Tensor pool_b; // (channels_in, 1)
+};
+
+struct DecoderBackbone {
+    Conv1d F0_conv;  // (1, 1, 3) stride 2 padding 1
+    Conv1d N_conv;   // (1, 1, 3) stride 2 padding 1
+    Conv1d asr_res;  // (64, 512, 1)
+    AdainResBlk1dWeights encode;
+    std::vector<AdainResBlk1dWeights> decode;  // the last upsamples 2x
+};
+
+struct AdaINResBlock1Weights {
+    int channels = 0;
+    int kernel_size = 0;
+    std::vector<int> dilations;  // length 3
+    std::array<Conv1d, 3> convs1;
+    std::array<Conv1d, 3> convs2;
+    std::array<AdaIN1dWeights, 3> adain1;
+    std::array<AdaIN1dWeights, 3> adain2;
+    std::array<brotensor::Tensor, 3> alpha1;  // (channels, 1)
+    std::array<brotensor::Tensor, 3> alpha2;
+};
+
+struct HarmonicSource {
+    int sample_rate = 24000;
+    int harmonic_num = 8;
+    int upsample_scale = 0;
+    int n_fft = 0;
+    int hop_size = 0;
+    int win_size = 0;
+    float sine_amp = 0.1f;
+    Linear l_linear;  // (1, harmonic_num + 1)
+
+    // F0_pred: (N, frame_count) Hz. har: (N, (n_fft+2) * stft_frames).
+    void forward(const brotensor::Tensor& F0_pred, int frame_count, int& signal_len,
+                 int& stft_frames, brotensor::Tensor& har) const;
+};
+
+struct Generator {
+    int n_fft = 0;
+    int hop_size = 0;
+    int win_size = 0;
+    int num_upsamples = 0;
+    int num_kernels = 0;
+    std::vector<brotensor::Tensor> ups_W;  // each (C_in, C_out*kL)
+    std::vector<brotensor::Tensor> ups_b;  // each (C_out, 1)
+    std::vector<int> ups_C_in, ups_C_out, ups_k, ups_stride, ups_pad;
+    std::vector<Conv1d> noise_convs;
+    std::vector<AdaINResBlock1Weights> noise_res;  // num_upsamples
+    std::vector<AdaINResBlock1Weights> resblocks;  // num_upsamples * num_kernels
+    Conv1d conv_post;
+};
+
+}  // namespace brosoundml

@@ -1,0 +1,239 @@
+#pragma once
+
+// Drop-in for the reference's src/kokoro_decoder_backward.h: the same entry
+// points, argument meaning and cache / affine structs in namespace
+// brosoundml::detail, implemented on gfx950 through the kdec C ABI.
+//
+// What is the same: every signature of kokoro_decoder_backward.h:37-293;
+// outputs are overwritten (or move-assigned) and caches are filled by the
+// forward and read by the matching backward; errors throw
+// std::runtime_error("brosoundml: <where>: <reason>").
+//
+// What is extended (source-compatible with the reference's call sites):
+//  - Batch: tensors may hold N > 1 utterances as N rows of C*L (the
+//    reference hard-codes N = 1, kokoro_decoder_backward.h:15-17). gamma/beta
+//    are (C,1) (shared) or N rows of C (per utterance); their grads follow
+//    the same shape (a shared affine receives the batch sum).
+//  - Every backward takes an optional trailing `const WeightGrads*`. With it
+//    the frozen-weight grads the reference never computes are accumulated:
+//    conv / conv-transpose / pool weights and biases and the Snake alphas
+//    (whose grad the reference computes and discards, :351-353, :364-366).
+//  - Cache contents: x_seq1 / x_seq2 hold the per-(n,c) instance-norm
+//    statistics (mean, rstd) instead of the normalised (L, C) sequence, and
+//    the pre-activation tensors (r_pre, n2_pre, s1_pre, s2_pre) are left
+//    empty: the fused backward kernels recompute them from the cached input,
+//    the statistics and the affine, which the extra beta fields keep. Only
+//    the matching backward reads a cache, so callers see no difference.
+//
+// Device: inputs must be HIP tensors (brotensor::Device::HIP); there is no
+// CPU path, and a CPU tensor is rejected with an error.
+
+#include <brotensor/tensor.h>
+
+#include <brosoundml/kokoro_modules.h>
+
+#include <array>
+#include <unordered_map>
+#include <vector>
+
+namespace brosoundml {
+namespace detail {
+
+// ─── north-star extension: weight grads ────────────────────────────────────
+struct WeightGrads {
+    // weight storage (Tensor::data) -> tensor its grad accumulates into
+    std::unordered_map<const void*, brotensor::Tensor*> grads;
+    void add(const brotensor::Tensor& w, brotensor::Tensor& g) { grads[w.data] = &g; }
+    brotensor::Tensor* find(const brotensor::Tensor& w) const {
+        auto it = grads.find(w.data);
+        return it == grads.end() ? nullptr : it->second;
+    }
+};
+
+// ─── AdaIN affine (instance-norm + style-conditioned scale/shift) ───────────
+//   x_ncl:(N, C*L)   gamma,beta:(C,1) or (N,C)   ->   y_ncl:(N, C*L)
+void adain_affine_forward(const brotensor::Tensor& x_ncl,
+                          const brotensor::Tensor& gamma,
+                          const brotensor::Tensor& beta,
+                          int C, int L, float eps,
+                          brotensor::Tensor& y_ncl,
+                          brotensor::Tensor& x_seq_cache);
+
+void adain_affine_backward(const brotensor::Tensor& x_ncl,
+                           const brotensor::Tensor& x_seq_cache,
+                           const brotensor::Tensor& gamma,
+                           const brotensor::Tensor& dY_ncl,
+                           int C, int L, float eps,
+                           brotensor::Tensor& dX_ncl,
+                           brotensor::Tensor& dGamma,
+                           brotensor::Tensor& dBeta);
+
+// ─── AdainResBlk1d ──────────────────────────────────────────────────────────
+struct AdainResBlkCache {
+    brotensor::Tensor x;          // block input (N, C_in*L_in)
+    brotensor::Tensor x_seq1;     // adain1 statistics (N*C_in, 2)
+    brotensor::Tensor r_pre;      // (recomputed; left empty)
+    brotensor::Tensor conv1_out;  // conv1 output = adain2 input (N, C_out*L_out)
+    brotensor::Tensor x_seq2;     // adain2 statistics (N*C_out, 2)
+    brotensor::Tensor n2_pre;     // (recomputed; left empty)
+    int L_in = 0;
+    int L_out = 0;
+    brotensor::Tensor beta1, beta2;  // affines kept for the recompute
+};
+
+void adain_resblk_1d_forward_train(const AdainResBlk1dWeights& w,
+                                   const brotensor::Tensor& x, int L_in,
+                                   const brotensor::Tensor& gamma1,
+                                   const brotensor::Tensor& beta1,
+                                   const brotensor::Tensor& gamma2,
+                                   const brotensor::Tensor& beta2,
+                                   float eps,
+                                   int& L_out, brotensor::Tensor& y,
+                                   AdainResBlkCache& cache);
+
+void adain_resblk_1d_backward(const AdainResBlk1dWeights& w,
+                              const AdainResBlkCache& cache,
+                              const brotensor::Tensor& gamma1,
+                              const brotensor::Tensor& gamma2,
+                              const brotensor::Tensor& dY, float eps,
+                              brotensor::Tensor& dX,
+                              brotensor::Tensor& dGamma1,
+                              brotensor::Tensor& dBeta1,
+                              brotensor::Tensor& dGamma2,
+                              brotensor::Tensor& dBeta2,
+                              const WeightGrads* wgrads = nullptr);
+
+// ─── AdaINResBlock1 (Snake) ─────────────────────────────────────────────────
+struct AdainResBlock1Cache {
+    std::array<brotensor::Tensor, 3> x_in;    // adain1 input per sub-block
+    std::array<brotensor::Tensor, 3> x_seq1;  // adain1 statistics
+    std::array<brotensor::Tensor, 3> s1_pre;  // (recomputed; left empty)
+    std::array<brotensor::Tensor, 3> c1_out;  // conv1 output = adain2 input
+    std::array<brotensor::Tensor, 3> x_seq2;  // adain2 statistics
+    std::array<brotensor::Tensor, 3> s2_pre;  // (recomputed; left empty)
+    int C = 0;
+    int L = 0;
+    std::array<brotensor::Tensor, 3> beta1, beta2;  // affines kept for the recompute
+};
+
+void adain_resblock1_forward_train(const AdaINResBlock1Weights& w,
+                                   const brotensor::Tensor& x_in, int C, int L,
+                                   const std::array<brotensor::Tensor, 3>& g1,
+                                   const std::array<brotensor::Tensor, 3>& b1,
+                                   const std::array<brotensor::Tensor, 3>& g2,
+                                   const std::array<brotensor::Tensor, 3>& b2,
+                                   brotensor::Tensor& x_out,
+                                   AdainResBlock1Cache& cache);
+
+void adain_resblock1_backward(const AdaINResBlock1Weights& w,
+                              const AdainResBlock1Cache& cache,
+                              const std::array<brotensor::Tensor, 3>& g1,
+                              const std::array<brotensor::Tensor, 3>& g2,
+                              const brotensor::Tensor& dX_out,
+                              brotensor::Tensor& dX_in,
+                              std::array<brotensor::Tensor, 3>& dG1,
+                              std::array<brotensor::Tensor, 3>& dB1,
+                              std::array<brotensor::Tensor, 3>& dG2,
+                              std::array<brotensor::Tensor, 3>& dB2,
+                              const WeightGrads* wgrads = nullptr);
+
+// ─── Spectral head (conv_post -> polar exp/sin -> iSTFT) ────────────────────
+struct SpectralHeadCache {
+    brotensor::Tensor x_pre;   // input to the final leaky_relu (N, C*L)
+    brotensor::Tensor post;    // conv_post output (N, (n_fft+2)*L)
+    int C = 0;
+    int L = 0;
+};
+
+void spectral_head_forward_train(const Conv1d& conv_post,
+                                 const brotensor::Tensor& x, int C, int L,
+                                 const brotensor::Tensor& window,
+                                 int n_fft, int hop, int win,
+                                 brotensor::Tensor& audio,
+                                 SpectralHeadCache& cache);
+
+void spectral_head_backward(const Conv1d& conv_post,
+                            const SpectralHeadCache& cache,
+                            const brotensor::Tensor& window,
+                            int n_fft, int hop, int win,
+                            const brotensor::Tensor& dAudio,
+                            brotensor::Tensor& dX,
+                            const WeightGrads* wgrads = nullptr);
+
+// ─── DecoderBackbone assembly ───────────────────────────────────────────────
+struct BlockAffines {
+    brotensor::Tensor g1, b1;   // affine1 — channels_in
+    brotensor::Tensor g2, b2;   // affine2 — channels_out
+};
+
+struct BackboneCache {
+    AdainResBlkCache              encode;
+    std::vector<AdainResBlkCache> decode;
+    std::vector<char>            res_applied;
+    std::vector<int>             x_channels;
+    int T = 0;
+    // kept for the front-conv weight grads (extension)
+    brotensor::Tensor asr, F0, N;
+};
+
+void decoder_backbone_forward_train(const DecoderBackbone& bb,
+                                    const brotensor::Tensor& asr,
+                                    const brotensor::Tensor& F0_pred,
+                                    const brotensor::Tensor& N_pred,
+                                    int T,
+                                    const std::vector<BlockAffines>& affines,
+                                    float eps,
+                                    brotensor::Tensor& gen_in,
+                                    BackboneCache& cache);
+
+void decoder_backbone_backward(const DecoderBackbone& bb,
+                               const BackboneCache& cache,
+                               const std::vector<BlockAffines>& affines,
+                               const brotensor::Tensor& dGenIn,
+                               float eps,
+                               std::vector<BlockAffines>& dAffines,
+                               const WeightGrads* wgrads = nullptr);
+
+// ─── Generator assembly ─────────────────────────────────────────────────────
+struct ResBlock1Affines {
+    std::array<brotensor::Tensor, 3> g1, b1;   // adain1[0..2]
+    std::array<brotensor::Tensor, 3> g2, b2;   // adain2[0..2]
+};
+
+struct GenStageCache {
+    brotensor::Tensor               x_in;
+    AdainResBlock1Cache             noise;
+    std::vector<AdainResBlock1Cache> res;
+    int C_in = 0, L_in = 0;
+    int C_out = 0, L_out = 0;
+};
+
+struct GeneratorCache {
+    std::vector<GenStageCache> stages;
+    SpectralHeadCache          head;
+    brotensor::Tensor          window;
+    // kept for the noise_convs weight grads (extension)
+    brotensor::Tensor          har;
+    int                        frames = 0;
+};
+
+void generator_forward_train(const Generator& gen,
+                             const brotensor::Tensor& gen_in, int L_in,
+                             const brotensor::Tensor& har, int frames,
+                             const std::vector<ResBlock1Affines>& noise_aff,
+                             const std::vector<ResBlock1Affines>& res_aff,
+                             brotensor::Tensor& audio,
+                             GeneratorCache& cache);
+
+void generator_backward(const Generator& gen,
+                        const GeneratorCache& cache,
+                        const std::vector<ResBlock1Affines>& noise_aff,
+                        const std::vector<ResBlock1Affines>& res_aff,
+                        const brotensor::Tensor& dAudio,
+                        brotensor::Tensor& dGenIn,
+                        std::vector<ResBlock1Affines>& dNoise_aff,
+                        std::vector<ResBlock1Affines>& dRes_aff,
+                        const WeightGrads* wgrads = nullptr);
+
+}  // namespace detail
+}  // namespace brosoundml

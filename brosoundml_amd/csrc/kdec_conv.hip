@@ -1,0 +1,758 @@
+// Conv1d / ConvTranspose1d forward, input-grad and weight-grad on gfx950 as
+// implicit GEMMs on FP32 MFMA (v_mfma_f32_32x32x2_f32).
+//
+// Forward family (one kernel, `conv_gemm`):
+//   Y[n, m, q] = sum_{c, t} A[(c, t), m] * X[n, c, q*s + t*d - p]
+// with A the weights packed K-major ([C_in_pad * k][M_pad], zero padded so
+// tiles never test bounds on the A side). It serves
+//   - conv1d forward (A = W^T),
+//   - conv1d input-grad at stride 1 (A = the flipped transpose of W,
+//     p' = d(k-1) - p: the adjoint of a correlation is a correlation),
+//   - conv-transpose input-grad (a strided correlation of dY with W viewed as
+//     (C_in, C_out*k)),
+//   - conv-transpose forward, polyphase: output phase r = (j + p) mod s sees
+//     only taps t = r + m*s, so each phase is a stride-1 correlation with
+//     ceil(k/s) taps whose outputs land at j = Q*s + r - p.
+// A 256-thread block owns a 128 (m) x 128 (q) output tile as 2x2 waves of
+// 64x64 (2x2 MFMA tiles each). Per K chunk the block stages CK input rows of
+// the haloed window [q0*s - p, (q0+127)*s + (k-1)d - p] and the matching
+// CK*k weight rows in LDS; every tap then reads a shifted window of the same
+// staged rows, so X is fetched once per chunk instead of k times.
+//
+// Weight-grad (`wgrad_gemm`): dW[m, (c, t)] = sum_{n, l} dY[n, m, l] *
+// X[n, c, l*s + t*d - p], a GEMM with the huge position axis as K. It is
+// split over K into deterministic partial tiles that a second kernel sums in
+// a fixed order.
+#include "kdec_internal.hpp"
+
+#include <algorithm>
+#include <cmath>
+
+namespace kdec {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 128;   // output-channel tile
+constexpr int BN = 128;   // output-position tile
+constexpr int NT = 256;   // threads per block (4 waves)
+
+__device__ inline int floordiv_i(int a, int b) {
+    int q = a / b;
+    if ((a % b != 0) && ((a < 0) != (b < 0))) --q;
+    return q;
+}
+
+struct GemmArgs {
+    const float* X;
+    long x_bs;
+    const float* A;          // packed weights [cin_pad*k][m_pad] per phase
+    long a_phase_stride;     // elements between phases
+    const float* bias;       // [C_out] or null
+    float* Y;
+    long y_bs;
+    const float* R;          // residual [n][m][j] or null
+    long r_bs;
+    int C_in, L_in, C_out, L_y;   // L_y: length of a Y row
+    int cin_pad, m_pad;
+    int k, s, d, p;          // correlation geometry (plain mode)
+    int n_q;                 // output columns (plain mode)
+    int CK;                  // input channels per K chunk (even)
+    float scale, beta;
+    // polyphase transposed-conv mode when n_phase > 1
+    int n_phase, ph_s, ph_p, ph_kt;
+};
+
+__global__ __launch_bounds__(NT) void conv_gemm(GemmArgs g) {
+    extern __shared__ float smem[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int l32 = lane & 31, hi = lane >> 5;
+
+    int b = blockIdx.z, k = g.k, s = g.s, d = g.d, p = g.p, n_q = g.n_q;
+    int os = 1, oo = 0;
+    const float* A = g.A;
+    if (g.n_phase > 1) {
+        const int r = blockIdx.z % g.n_phase;
+        b = blockIdx.z / g.n_phase;
+        const int qmin = -floordiv_i(r - g.ph_p, g.ph_s);          // ceil((p - r)/s)
+        const int qmax = floordiv_i(g.L_y - 1 + g.ph_p - r, g.ph_s);
+        n_q = qmax - qmin + 1;
+        k = g.ph_kt;
+        s = 1;
+        d = 1;
+        p = g.ph_kt - 1 - qmin;
+        os = g.ph_s;
+        oo = qmin * g.ph_s + r - g.ph_p;
+        A += static_cast<long>(r) * g.a_phase_stride;
+    }
+    const int m0 = blockIdx.y * BM;
+    const int q0 = blockIdx.x * BN;
+    if (q0 >= n_q) return;  // uniform per block
+
+    const int CK = g.CK;
+    const int KR = CK * k;                            // weight rows per chunk
+    const int span = (BN - 1) * s + (k - 1) * d + 1;  // staged input window
+    float* Ws = smem;                                 // [KR][BM], row = t*CK + c
+    float* Xs = smem + KR * BM;                       // [CK][span]
+
+    const float* Xb = g.X + static_cast<long>(b) * g.x_bs;
+    const int x0 = q0 * s - p;
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    const int am = wm * 64 + l32;         // A column (m) for tm = 0
+    const int bq = (wn * 64 + l32) * s;   // B column offset for tn = 0
+
+    for (int c0 = 0; c0 < g.cin_pad; c0 += CK) {
+        __syncthreads();
+        // weights: global rows (c0 + c)*k + t, BM contiguous floats each
+        const float* Ag = A + static_cast<long>(c0) * k * g.m_pad + m0;
+        for (int idx = tid; idx < KR * (BM / 4); idx += NT) {
+            const int row = idx / (BM / 4);
+            const int c4 = idx - row * (BM / 4);
+            const int c = row / k;
+            const int t = row - c * k;
+            const float4 v = *reinterpret_cast<const float4*>(
+                Ag + static_cast<long>(row) * g.m_pad + c4 * 4);
+            *reinterpret_cast<float4*>(Ws + (t * CK + c) * BM + c4 * 4) = v;
+        }
+        // haloed input rows, zero outside [0, L_in) and beyond C_in
+        for (int idx = tid; idx < CK * span; idx += NT) {
+            const int c = idx / span;
+            const int j = idx - c * span;
+            const int cg = c0 + c;
+            const int xi = x0 + j;
+            float v = 0.0f;
+            if (cg < g.C_in && xi >= 0 && xi < g.L_in)
+                v = Xb[static_cast<long>(cg) * g.L_in + xi];
+            Xs[c * span + j] = v;
+        }
+        __syncthreads();
+        for (int t = 0; t < k; ++t) {
+            const float* Wt = Ws + t * CK * BM;
+            const int toff = t * d;
+            for (int cc = 0; cc < CK; cc += 2) {
+                const int c = cc + hi;
+                const float a0 = Wt[c * BM + am];
+                const float a1 = Wt[c * BM + am + 32];
+                const float* xr = Xs + c * span + toff + bq;
+                const float b0 = xr[0];
+                const float b1 = xr[32 * s];
+                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
+                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
+                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
+                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+            }
+        }
+    }
+
+    // epilogue: lane owns column l32 and rows 8*(e/4) + 4*hi + e%4 of each tile
+    float* Yb = g.Y + static_cast<long>(b) * g.y_bs;
+    const float* Rb = g.R ? g.R + static_cast<long>(b) * g.r_bs : nullptr;
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn) {
+        const int q = q0 + wn * 64 + tn * 32 + l32;
+        if (q >= n_q) continue;
+        const long j = static_cast<long>(q) * os + oo;
+#pragma unroll
+        for (int tm = 0; tm < 2; ++tm) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int m = m0 + wm * 64 + tm * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
+                if (m >= g.C_out) continue;
+                float v = acc[tm][tn][e];
+                if (g.bias) v += g.bias[m];
+                const long yi = static_cast<long>(m) * g.L_y + j;
+                if (Rb) v += Rb[yi];
+                v *= g.scale;
+                if (g.beta != 0.0f) v += g.beta * Yb[yi];
+                Yb[yi] = v;
+            }
+        }
+    }
+}
+
+// ─── weight packing ──────────────────────────────────────────────────────
+// All packers write A[(c*kk + t)*m_pad + m] over the padded extent, zeroing
+// the padding, for the correlation they set up.
+
+// conv1d forward: A[(ci, t), co] = W[co, ci*k + t]
+__global__ void pack_fwd(const float* W, float* A, int C_in, int C_out, int k,
+                         int cin_pad, int m_pad) {
+    const long total = static_cast<long>(cin_pad) * k * m_pad;
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        const int m = static_cast<int>(i % m_pad);
+        const long row = i / m_pad;
+        const int t = static_cast<int>(row % k);
+        const int c = static_cast<int>(row / k);
+        float v = 0.0f;
+        if (m < C_out && c < C_in) v = W[(static_cast<long>(m) * C_in + c) * k + t];
+        A[i] = v;
+    }
+}
+
+// conv1d input-grad (stride 1): the correlation over dY (C_out channels) with
+// A[(co, t'), ci] = W[co, ci*k + (k-1-t')]
+__global__ void pack_dgrad(const float* W, float* A, int C_in, int C_out, int k,
+                           int cout_pad, int m_pad) {
+    const long total = static_cast<long>(cout_pad) * k * m_pad;
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        const int m = static_cast<int>(i % m_pad);  // ci
+        const long row = i / m_pad;
+        const int t = static_cast<int>(row % k);
+        const int c = static_cast<int>(row / k);    // co
+        float v = 0.0f;
+        if (m < C_in && c < C_out) v = W[(static_cast<long>(c) * C_in + m) * k + (k - 1 - t)];
+        A[i] = v;
+    }
+}
+
+// conv-transpose input-grad: correlation over dY (C_out channels) with
+// A[(co, t), ci] = W[ci, co*k + t]
+__global__ void pack_convt_dgrad(const float* W, float* A, int C_in, int C_out,
+                                 int k, int cout_pad, int m_pad) {
+    const long total = static_cast<long>(cout_pad) * k * m_pad;
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        const int m = static_cast<int>(i % m_pad);  // ci
+        const long row = i / m_pad;
+        const int t = static_cast<int>(row % k);
+        const int c = static_cast<int>(row / k);    // co
+        float v = 0.0f;
+        if (m < C_in && c < C_out) v = W[(static_cast<long>(m) * C_out + c) * k + t];
+        A[i] = v;
+    }
+}
+
+// conv-transpose forward, phase r of s: tap t' of kt covers original tap
+// t = r + (kt-1-t')*s.  A_r[(ci, t'), co] = W[ci, co*k + t] (0 if t >= k)
+__global__ void pack_convt_fwd(const float* W, float* A, int C_in, int C_out,
+                               int k, int s, int kt, int cin_pad, int m_pad,
+                               long phase_stride) {
+    const long total = phase_stride * s;
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        const int r = static_cast<int>(i / phase_stride);
+        const long w = i - r * phase_stride;
+        const int m = static_cast<int>(w % m_pad);  // co
+        const long row = w / m_pad;
+        const int tp = static_cast<int>(row % kt);
+        const int c = static_cast<int>(row / kt);   // ci
+        const int t = r + (kt - 1 - tp) * s;
+        float v = 0.0f;
+        if (m < C_out && c < C_in && t < k) v = W[(static_cast<long>(c) * C_out + m) * k + t];
+        A[i] = v;
+    }
+}
+
+// ─── weight grad ─────────────────────────────────────────────────────────
+
+constexpr int KC = 64;  // positions per K chunk
+
+struct WgradArgs {
+    const float* X;      // correlation input  [n][C_x][L_x]
+    long x_bs;
+    const float* G;      // grad rows (A side) [n][M][L_g]
+    long g_bs;
+    float* P;            // partials [split][M][NN]
+    int M, C_x, L_x, L_g, k, s, d, p;
+    int NN;              // C_x * k
+    int chunks_per_n, total_chunks, chunks_per_split;
+};
+
+// P[z, m, c*k + t] = sum over this split's positions l of
+//   G[n, m, l] * X[n, c, l*s + t*d - p]
+__global__ __launch_bounds__(NT) void wgrad_gemm(WgradArgs g) {
+    extern __shared__ float smem[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int l32 = lane & 31, hi = lane >> 5;
+    const int m0 = blockIdx.y * BM;
+    const int n0 = blockIdx.x * BN;
+    const int z = blockIdx.z;
+    const int k = g.k, s = g.s, d = g.d;
+
+    const int ci_lo = n0 / k;
+    const int XR = (BN - 1) / k + 2;                  // staged input rows
+    const int span = (KC - 1) * s + (k - 1) * d + 1;  // staged window
+    float* Gs = smem;                                 // [KC][BM + 1]
+    float* Xs = smem + KC * (BM + 1);                 // [XR][span]
+
+    // this lane's two B columns
+    int xrow[2], xoff[2];
+    bool ok[2];
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn) {
+        const int n = n0 + wn * 64 + tn * 32 + l32;
+        ok[tn] = n < g.NN;
+        const int c = n / k;
+        xrow[tn] = ok[tn] ? (c - ci_lo) : 0;
+        xoff[tn] = ok[tn] ? (n - c * k) * d : 0;
+    }
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    const int ch0 = z * g.chunks_per_split;
+    const int ch1 = min(ch0 + g.chunks_per_split, g.total_chunks);
+    for (int ch = ch0; ch < ch1; ++ch) {
+        const int b = ch / g.chunks_per_n;
+        const int l0 = (ch - b * g.chunks_per_n) * KC;
+        const float* Gb = g.G + static_cast<long>(b) * g.g_bs;
+        const float* Xb = g.X + static_cast<long>(b) * g.x_bs;
+        __syncthreads();
+        for (int idx = tid; idx < BM * KC; idx += NT) {
+            const int m = idx / KC;
+            const int kc = idx - m * KC;
+            const int mg = m0 + m, l = l0 + kc;
+            float v = 0.0f;
+            if (mg < g.M && l < g.L_g) v = Gb[static_cast<long>(mg) * g.L_g + l];
+            Gs[kc * (BM + 1) + m] = v;
+        }
+        const int x0 = l0 * s - g.p;
+        for (int idx = tid; idx < XR * span; idx += NT) {
+            const int r = idx / span;
+            const int j = idx - r * span;
+            const int c = ci_lo + r;
+            const int xi = x0 + j;
+            float v = 0.0f;
+            if (c < g.C_x && xi >= 0 && xi < g.L_x) v = Xb[static_cast<long>(c) * g.L_x + xi];
+            Xs[r * span + j] = v;
+        }
+        __syncthreads();
+        const float* xb0 = Xs + xrow[0] * span + xoff[0];
+        const float* xb1 = Xs + xrow[1] * span + xoff[1];
+        for (int kc = 0; kc < KC; kc += 2) {
+            const int kk = kc + hi;
+            const float a0 = Gs[kk * (BM + 1) + wm * 64 + l32];
+            const float a1 = Gs[kk * (BM + 1) + wm * 64 + 32 + l32];
+            const float b0 = ok[0] ? xb0[kk * s] : 0.0f;
+            const float b1 = ok[1] ? xb1[kk * s] : 0.0f;
+            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+        }
+    }
+
+    float* Pz = g.P + static_cast<long>(z) * g.M * g.NN;
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn) {
+        const int n = n0 + wn * 64 + tn * 32 + l32;
+        if (n >= g.NN) continue;
+#pragma unroll
+        for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int m = m0 + wm * 64 + tm * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
+                if (m < g.M) Pz[static_cast<long>(m) * g.NN + n] = acc[tm][tn][e];
+            }
+    }
+}
+
+// out[i] += sum_z P[z][i] in a fixed order.  `transpose_k`: when non-zero the
+// element i = m*NN + (c*k + t) is stored at the conv-transpose layout
+// [c][m*k + t] instead (M = C_out of the transpose, c = its input channel).
+__global__ void wgrad_reduce(const float* P, float* out, long MN, int splits,
+                             int transpose_k, int M, int NN) {
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < MN;
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        float acc = 0.0f;
+        for (int z = 0; z < splits; ++z) acc += P[z * MN + i];
+        long o = i;
+        if (transpose_k) {
+            const int k = transpose_k;
+            const int m = static_cast<int>(i / NN);
+            const int n = static_cast<int>(i - static_cast<long>(m) * NN);
+            const int c = n / k, t = n - (n / k) * k;
+            o = (static_cast<long>(c) * M + m) * k + t;
+        }
+        out[o] += acc;
+    }
+}
+
+// db[m] += sum_{n, l} G[n, m, l]; one block per m, fixed-order reduction.
+__global__ void bias_grad(const float* G, long g_bs, float* db, int N, int L) {
+    const int m = blockIdx.x;
+    double acc = 0.0;
+    for (int n = 0; n < N; ++n) {
+        const float* row = G + n * g_bs + static_cast<long>(m) * L;
+        for (int l = threadIdx.x; l < L; l += blockDim.x) acc += row[l];
+    }
+    __shared__ double red[256];
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+        if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) db[m] += static_cast<float>(red[0]);
+}
+
+// ─── depthwise pool: ConvTranspose1d k3 s2 p1 op1, groups = C ──────────────
+// y[2m] = b + W1 x[m];  y[2m+1] = b + W0 x[m+1] + W2 x[m]
+__global__ void pool_fwd(const float* X, long x_bs, const float* W, const float* bias,
+                         float* Y, long y_bs, int C, int L) {
+    const int row = blockIdx.y;  // n*C + c
+    const int n = row / C, c = row - n * C;
+    const float* x = X + n * x_bs + static_cast<long>(c) * L;
+    float* y = Y + n * y_bs + static_cast<long>(c) * 2 * L;
+    const float w0 = W[c * 3], w1 = W[c * 3 + 1], w2 = W[c * 3 + 2];
+    const float bb = bias ? bias[c] : 0.0f;
+    for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < 2 * L; j += gridDim.x * blockDim.x) {
+        const int m = j >> 1;
+        float v;
+        if ((j & 1) == 0) v = w1 * x[m];
+        else v = w2 * x[m] + (m + 1 < L ? w0 * x[m + 1] : 0.0f);
+        y[j] = v + bb;
+    }
+}
+
+// dx[l] = W0 dy[2l-1] + W1 dy[2l] + W2 dy[2l+1]
+__global__ void pool_dgrad(const float* W, const float* dY, long dy_bs, float* dX,
+                           long dx_bs, int C, int L) {
+    const int row = blockIdx.y;
+    const int n = row / C, c = row - n * C;
+    const float* dy = dY + n * dy_bs + static_cast<long>(c) * 2 * L;
+    float* dx = dX + n * dx_bs + static_cast<long>(c) * L;
+    const float w0 = W[c * 3], w1 = W[c * 3 + 1], w2 = W[c * 3 + 2];
+    for (int l = blockIdx.x * blockDim.x + threadIdx.x; l < L; l += gridDim.x * blockDim.x) {
+        float v = w1 * dy[2 * l] + w2 * dy[2 * l + 1];
+        if (l > 0) v += w0 * dy[2 * l - 1];
+        dx[l] = v;
+    }
+}
+
+// dW[c][t] += sum_{n,l} x[l] dy[2l + t - 1];  db[c] += sum dy. Block per c.
+__global__ void pool_wgrad(const float* X, long x_bs, const float* dY, long dy_bs,
+                           float* dW, float* db, int N, int C, int L) {
+    const int c = blockIdx.x;
+    double a0 = 0, a1 = 0, a2 = 0, ab = 0;
+    for (int n = 0; n < N; ++n) {
+        const float* x = X + n * x_bs + static_cast<long>(c) * L;
+        const float* dy = dY + n * dy_bs + static_cast<long>(c) * 2 * L;
+        for (int l = threadIdx.x; l < L; l += blockDim.x) {
+            const double xv = x[l];
+            if (l > 0) a0 += xv * dy[2 * l - 1];
+            a1 += xv * dy[2 * l];
+            a2 += xv * dy[2 * l + 1];
+            ab += static_cast<double>(dy[2 * l]) + dy[2 * l + 1];
+        }
+    }
+    __shared__ double red[4][256];
+    red[0][threadIdx.x] = a0;
+    red[1][threadIdx.x] = a1;
+    red[2][threadIdx.x] = a2;
+    red[3][threadIdx.x] = ab;
+    __syncthreads();
+    for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+        if (threadIdx.x < w)
+            for (int q = 0; q < 4; ++q) red[q][threadIdx.x] += red[q][threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        dW[c * 3 + 0] += static_cast<float>(red[0][0]);
+        dW[c * 3 + 1] += static_cast<float>(red[1][0]);
+        dW[c * 3 + 2] += static_cast<float>(red[2][0]);
+        if (db) db[c] += static_cast<float>(red[3][0]);
+    }
+}
+
+// Input channels per K chunk: a power of two in [2, 32] so that it divides
+// the 32-padded channel count of the packed weights (no chunk runs past them),
+// with CK*k near 64 weight rows per chunk.
+int pick_ck(int k) {
+    int ck = 32;
+    while (ck > 2 && ck * k > 64) ck >>= 1;
+    return ck;
+}
+
+int grid1d(long n) {
+    long g = (n + 255) / 256;
+    if (g > 65536) g = 65536;
+    if (g < 1) g = 1;
+    return static_cast<int>(g);
+}
+
+// Launches conv_gemm over an already packed A.
+int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
+             double flops) {
+    const int CK = g.CK;
+    const int kk = g.n_phase > 1 ? g.ph_kt : g.k;
+    const int ss = g.n_phase > 1 ? 1 : g.s;
+    const int dd = g.n_phase > 1 ? 1 : g.d;
+    const int span = (BN - 1) * ss + (kk - 1) * dd + 1;
+    const size_t lds = (static_cast<size_t>(CK) * kk * BM + static_cast<size_t>(CK) * span) * sizeof(float);
+    if (lds > 160 * 1024) return fail(ctx, KDEC_EINVAL, "conv: tile does not fit LDS");
+    int max_q = g.n_q;
+    if (g.n_phase > 1) max_q = static_cast<int>(cdiv(g.L_y + g.ph_s, g.ph_s)) + 1;
+    const dim3 grid(static_cast<unsigned>(cdiv(max_q, BN)), static_cast<unsigned>(m_tiles),
+                    static_cast<unsigned>(N * g.n_phase));
+    ProfScope ps(ctx, fam, flops);
+    hipLaunchKernelGGL(conv_gemm, grid, dim3(NT), lds, ctx->stream, g);
+    return launch_check(ctx, fam);
+}
+
+}  // namespace
+}  // namespace kdec
+
+using namespace kdec;
+
+extern "C" {
+
+int kdec_conv1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
+                    const float* bias, float* Y, long y_bs, int N, int C_in,
+                    int L, int C_out, int k, int stride, int pad, int dil,
+                    const float* R, long r_bs, float scale, float beta) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, X && W && Y && N > 0 && C_in > 0 && C_out > 0 && k > 0 && stride > 0 && dil > 0 && pad >= 0,
+               "kdec_conv1d_fwd: bad arguments");
+    const int L_out = (L + 2 * pad - dil * (k - 1) - 1) / stride + 1;
+    KDEC_CHECK(ctx, L > 0 && L_out > 0, "kdec_conv1d_fwd: empty output");
+    KDEC_CHECK(ctx, x_bs >= static_cast<long>(C_in) * L && y_bs >= static_cast<long>(C_out) * L_out,
+               "kdec_conv1d_fwd: batch stride too small");
+    const int CK = pick_ck(k);
+    const int cin_pad = static_cast<int>(cdiv(C_in, 32) * 32);
+    const int m_pad = static_cast<int>(cdiv(C_out, BM) * BM);
+    Workspace A(ctx, static_cast<size_t>(cin_pad) * k * m_pad * sizeof(float));
+    if (!A.p) return KDEC_ENOMEM;
+    const long tot = static_cast<long>(cin_pad) * k * m_pad;
+    hipLaunchKernelGGL(pack_fwd, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), C_in,
+                       C_out, k, cin_pad, m_pad);
+    if (int rc = launch_check(ctx, "pack_fwd")) return rc;
+    GemmArgs g{};
+    g.X = X; g.x_bs = x_bs; g.A = A.as<float>(); g.a_phase_stride = 0;
+    g.bias = bias; g.Y = Y; g.y_bs = y_bs; g.R = R; g.r_bs = r_bs;
+    g.C_in = C_in; g.L_in = L; g.C_out = C_out; g.L_y = L_out;
+    g.cin_pad = cin_pad; g.m_pad = m_pad;
+    g.k = k; g.s = stride; g.d = dil; g.p = pad; g.n_q = L_out; g.CK = CK;
+    g.scale = scale; g.beta = beta; g.n_phase = 1;
+    return run_gemm(ctx, g, N, m_pad / BM, "conv_fwd",
+                    2.0 * N * C_out * static_cast<double>(L_out) * C_in * k);
+}
+
+int kdec_conv1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
+                      long dy_bs, float* dX, long dx_bs, int N, int C_in,
+                      int L, int C_out, int k, int stride, int pad, int dil,
+                      float scale, float beta) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, W && dY && dX && N > 0 && C_in > 0 && C_out > 0 && k > 0 && dil > 0 && pad >= 0,
+               "kdec_conv1d_dgrad: bad arguments");
+    KDEC_CHECK(ctx, stride == 1, "kdec_conv1d_dgrad: only stride 1 is on the decoder path");
+    const int L_out = L + 2 * pad - dil * (k - 1);
+    KDEC_CHECK(ctx, L > 0 && L_out > 0, "kdec_conv1d_dgrad: empty output");
+    const int pp = dil * (k - 1) - pad;
+    KDEC_CHECK(ctx, pp >= 0, "kdec_conv1d_dgrad: padding larger than the receptive field");
+    KDEC_CHECK(ctx, dy_bs >= static_cast<long>(C_out) * L_out && dx_bs >= static_cast<long>(C_in) * L,
+               "kdec_conv1d_dgrad: batch stride too small");
+    const int CK = pick_ck(k);
+    const int cpad = static_cast<int>(cdiv(C_out, 32) * 32);
+    const int m_pad = static_cast<int>(cdiv(C_in, BM) * BM);
+    Workspace A(ctx, static_cast<size_t>(cpad) * k * m_pad * sizeof(float));
+    if (!A.p) return KDEC_ENOMEM;
+    const long tot = static_cast<long>(cpad) * k * m_pad;
+    hipLaunchKernelGGL(pack_dgrad, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), C_in,
+                       C_out, k, cpad, m_pad);
+    if (int rc = launch_check(ctx, "pack_dgrad")) return rc;
+    GemmArgs g{};
+    g.X = dY; g.x_bs = dy_bs; g.A = A.as<float>();
+    g.Y = dX; g.y_bs = dx_bs;
+    g.C_in = C_out; g.L_in = L_out; g.C_out = C_in; g.L_y = L;
+    g.cin_pad = cpad; g.m_pad = m_pad;
+    g.k = k; g.s = 1; g.d = dil; g.p = pp; g.n_q = L; g.CK = CK;
+    g.scale = scale; g.beta = beta; g.n_phase = 1;
+    return run_gemm(ctx, g, N, m_pad / BM, "conv_dgrad",
+                    2.0 * N * C_out * static_cast<double>(L_out) * C_in * k);
+}
+
+static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G,
+                        long g_bs, int N, int M, int C_x, int L_x, int L_g, int k,
+                        int s, int d, int p, float* out, int transpose_k,
+                        const char* fam) {
+    const int NN = C_x * k;
+    const int m_tiles = static_cast<int>(cdiv(M, BM));
+    const int n_tiles = static_cast<int>(cdiv(NN, BN));
+    const int chunks_per_n = static_cast<int>(cdiv(L_g, KC));
+    const int total_chunks = chunks_per_n * N;
+    // aim for ~2048 blocks in flight, but keep >= 4 chunks per split
+    long want = 2048 / (static_cast<long>(m_tiles) * n_tiles);
+    if (want < 1) want = 1;
+    int cps = static_cast<int>(cdiv(total_chunks, want));
+    if (cps < 4) cps = 4;
+    const int splits = static_cast<int>(cdiv(total_chunks, cps));
+    const long MN = static_cast<long>(M) * NN;
+    Workspace P(ctx, static_cast<size_t>(splits) * MN * sizeof(float));
+    if (!P.p) return KDEC_ENOMEM;
+    WgradArgs a{};
+    a.X = X; a.x_bs = x_bs; a.G = G; a.g_bs = g_bs; a.P = P.as<float>();
+    a.M = M; a.C_x = C_x; a.L_x = L_x; a.L_g = L_g; a.k = k; a.s = s; a.d = d; a.p = p;
+    a.NN = NN; a.chunks_per_n = chunks_per_n; a.total_chunks = total_chunks;
+    a.chunks_per_split = cps;
+    const int XR = (BN - 1) / k + 2;
+    const int span = (KC - 1) * s + (k - 1) * d + 1;
+    const size_t lds = (static_cast<size_t>(KC) * (BM + 1) + static_cast<size_t>(XR) * span) * sizeof(float);
+    if (lds > 160 * 1024) return fail(ctx, KDEC_EINVAL, "wgrad: tile does not fit LDS");
+    {
+        ProfScope ps(ctx, fam, 2.0 * N * M * static_cast<double>(L_g) * NN);
+        hipLaunchKernelGGL(wgrad_gemm, dim3(n_tiles, m_tiles, splits), dim3(NT), lds, ctx->stream, a);
+        if (int rc = launch_check(ctx, fam)) return rc;
+    }
+    hipLaunchKernelGGL(wgrad_reduce, dim3(grid1d(MN)), dim3(256), 0, ctx->stream, P.as<float>(), out, MN,
+                       splits, transpose_k, M, NN);
+    return launch_check(ctx, "wgrad_reduce");
+}
+
+int kdec_conv1d_wgrad(kdec_ctx* ctx, const float* X, long x_bs,
+                      const float* dY, long dy_bs, float* dW, float* db, int N,
+                      int C_in, int L, int C_out, int k, int stride, int pad,
+                      int dil) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, X && dY && N > 0 && C_in > 0 && C_out > 0 && k > 0 && stride > 0 && dil > 0,
+               "kdec_conv1d_wgrad: bad arguments");
+    const int L_out = (L + 2 * pad - dil * (k - 1) - 1) / stride + 1;
+    KDEC_CHECK(ctx, L > 0 && L_out > 0, "kdec_conv1d_wgrad: empty output");
+    if (dW)
+        if (int rc = wgrad_common(ctx, X, x_bs, dY, dy_bs, N, C_out, C_in, L, L_out, k, stride, dil,
+                                  pad, dW, 0, "conv_wgrad"))
+            return rc;
+    if (db) {
+        hipLaunchKernelGGL(bias_grad, dim3(C_out), dim3(256), 0, ctx->stream, dY, dy_bs, db, N, L_out);
+        return launch_check(ctx, "bias_grad");
+    }
+    return KDEC_OK;
+}
+
+int kdec_convt1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
+                     const float* bias, float* Y, long y_bs, int N, int C_in,
+                     int L, int C_out, int k, int stride, int pad, int op) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, X && W && Y && N > 0 && C_in > 0 && C_out > 0 && k > 0 && stride > 0 && pad >= 0 && op >= 0,
+               "kdec_convt1d_fwd: bad arguments");
+    const int L_out = (L - 1) * stride - 2 * pad + (k - 1) + op + 1;
+    KDEC_CHECK(ctx, L > 0 && L_out > 0, "kdec_convt1d_fwd: empty output");
+    KDEC_CHECK(ctx, y_bs >= static_cast<long>(C_out) * L_out && x_bs >= static_cast<long>(C_in) * L,
+               "kdec_convt1d_fwd: batch stride too small");
+    const int kt = static_cast<int>(cdiv(k, stride));
+    const int CK = pick_ck(kt);
+    const int cin_pad = static_cast<int>(cdiv(C_in, 32) * 32);
+    const int m_pad = static_cast<int>(cdiv(C_out, BM) * BM);
+    const long ph = static_cast<long>(cin_pad) * kt * m_pad;
+    Workspace A(ctx, static_cast<size_t>(ph) * stride * sizeof(float));
+    if (!A.p) return KDEC_ENOMEM;
+    hipLaunchKernelGGL(pack_convt_fwd, dim3(grid1d(ph * stride)), dim3(256), 0, ctx->stream, W,
+                       A.as<float>(), C_in, C_out, k, stride, kt, cin_pad, m_pad, ph);
+    if (int rc = launch_check(ctx, "pack_convt_fwd")) return rc;
+    GemmArgs g{};
+    g.X = X; g.x_bs = x_bs; g.A = A.as<float>(); g.a_phase_stride = ph;
+    g.bias = bias; g.Y = Y; g.y_bs = y_bs;
+    g.C_in = C_in; g.L_in = L; g.C_out = C_out; g.L_y = L_out;
+    g.cin_pad = cin_pad; g.m_pad = m_pad;
+    g.k = kt; g.s = 1; g.d = 1; g.p = 0; g.n_q = 0; g.CK = CK;
+    g.scale = 1.0f; g.beta = 0.0f;
+    g.n_phase = stride; g.ph_s = stride; g.ph_p = pad; g.ph_kt = kt;
+    if (stride == 1) {  // plain correlation: taps reversed, p' = k-1-pad
+        g.n_phase = 1; g.k = k; g.p = k - 1 - pad; g.n_q = L_out; g.a_phase_stride = 0;
+        KDEC_CHECK(ctx, g.p >= 0, "kdec_convt1d_fwd: padding larger than the kernel");
+    }
+    return run_gemm(ctx, g, N, m_pad / BM, "convt_fwd",
+                    2.0 * N * C_in * static_cast<double>(L) * C_out * k);
+}
+
+int kdec_convt1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
+                       long dy_bs, float* dX, long dx_bs, int N, int C_in,
+                       int L, int C_out, int k, int stride, int pad, int op) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, W && dY && dX && N > 0 && C_in > 0 && C_out > 0 && k > 0 && stride > 0 && pad >= 0 && op >= 0,
+               "kdec_convt1d_dgrad: bad arguments");
+    const int L_out = (L - 1) * stride - 2 * pad + (k - 1) + op + 1;
+    KDEC_CHECK(ctx, L > 0 && L_out > 0, "kdec_convt1d_dgrad: empty output");
+    const int CK = pick_ck(k);
+    const int cpad = static_cast<int>(cdiv(C_out, 32) * 32);
+    const int m_pad = static_cast<int>(cdiv(C_in, BM) * BM);
+    const long tot = static_cast<long>(cpad) * k * m_pad;
+    Workspace A(ctx, static_cast<size_t>(tot) * sizeof(float));
+    if (!A.p) return KDEC_ENOMEM;
+    hipLaunchKernelGGL(pack_convt_dgrad, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(),
+                       C_in, C_out, k, cpad, m_pad);
+    if (int rc = launch_check(ctx, "pack_convt_dgrad")) return rc;
+    GemmArgs g{};
+    g.X = dY; g.x_bs = dy_bs; g.A = A.as<float>();
+    g.Y = dX; g.y_bs = dx_bs;
+    g.C_in = C_out; g.L_in = L_out; g.C_out = C_in; g.L_y = L;
+    g.cin_pad = cpad; g.m_pad = m_pad;
+    g.k = k; g.s = stride; g.d = 1; g.p = pad; g.n_q = L; g.CK = CK;
+    g.scale = 1.0f; g.beta = 0.0f; g.n_phase = 1;
+    return run_gemm(ctx, g, N, m_pad / BM, "convt_dgrad",
+                    2.0 * N * C_in * static_cast<double>(L) * C_out * k);
+}
+
+int kdec_convt1d_wgrad(kdec_ctx* ctx, const float* X, long x_bs,
+                       const float* dY, long dy_bs, float* dW, float* db,
+                       int N, int C_in, int L, int C_out, int k, int stride,
+                       int pad, int op) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, X && dY && N > 0 && C_in > 0 && C_out > 0 && k > 0 && stride > 0 && pad >= 0,
+               "kdec_convt1d_wgrad: bad arguments");
+    const int L_out = (L - 1) * stride - 2 * pad + (k - 1) + op + 1;
+    KDEC_CHECK(ctx, L > 0 && L_out > 0, "kdec_convt1d_wgrad: empty output");
+    // dW[ci, co*k + t] = sum_l X[ci, l] dY[co, l*s + t - p]: the conv weight
+    // grad with the roles of input and output grad exchanged (M = C_in).
+    if (dW)
+        if (int rc = wgrad_common(ctx, dY, dy_bs, X, x_bs, N, C_in, C_out, L_out, L, k, stride, 1,
+                                  pad, dW, 0, "convt_wgrad"))
+            return rc;
+    if (db) {
+        hipLaunchKernelGGL(bias_grad, dim3(C_out), dim3(256), 0, ctx->stream, dY, dy_bs, db, N, L_out);
+        return launch_check(ctx, "bias_grad");
+    }
+    return KDEC_OK;
+}
+
+int kdec_pool_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
+                  const float* bias, float* Y, long y_bs, int N, int C, int L) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, X && W && Y && N > 0 && C > 0 && L > 0, "kdec_pool_fwd: bad arguments");
+    ProfScope ps(ctx, "pool", 0);
+    hipLaunchKernelGGL(pool_fwd, dim3(static_cast<unsigned>(cdiv(2 * L, 256) > 64 ? 64 : cdiv(2 * L, 256)), N * C),
+                       dim3(256), 0, ctx->stream, X, x_bs, W, bias, Y, y_bs, C, L);
+    return launch_check(ctx, "pool_fwd");
+}
+
+int kdec_pool_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
+                    long dy_bs, float* dX, long dx_bs, int N, int C, int L) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, W && dY && dX && N > 0 && C > 0 && L > 0, "kdec_pool_dgrad: bad arguments");
+    ProfScope ps(ctx, "pool", 0);
+    hipLaunchKernelGGL(pool_dgrad, dim3(static_cast<unsigned>(cdiv(L, 256) > 64 ? 64 : cdiv(L, 256)), N * C),
+                       dim3(256), 0, ctx->stream, W, dY, dy_bs, dX, dx_bs, C, L);
+    return launch_check(ctx, "pool_dgrad");
+}
+
+int kdec_pool_wgrad(kdec_ctx* ctx, const float* X, long x_bs, const float* dY,
+                    long dy_bs, float* dW, float* db, int N, int C, int L) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, X && dY && dW && N > 0 && C > 0 && L > 0, "kdec_pool_wgrad: bad arguments");
+    ProfScope ps(ctx, "pool", 0);
+    hipLaunchKernelGGL(pool_wgrad, dim3(C), dim3(256), 0, ctx->stream, X, x_bs, dY, dy_bs, dW, db, N, C, L);
+    return launch_check(ctx, "pool_wgrad");
+}
+
+}  // extern "C"

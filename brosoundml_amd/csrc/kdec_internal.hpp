@@ -1,0 +1,88 @@
+// Internal declarations shared by the HIP translation units of libkdec.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <map>
+#include <string>
+#include <unordered_map>
+#include <utility>
+#include <vector>
+
+#include "kdec.h"
+
+struct kdec_ctx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    std::string err;
+
+    // Stream-ordered caching allocator: every kernel of a context runs on one
+    // stream, so a block returned to the pool can be handed out again at once;
+    // stream order keeps the reuse behind the previous user's kernels.
+    std::multimap<size_t, void*> pool;
+    std::unordered_map<void*, size_t> live;
+    size_t pooled_bytes = 0;
+
+    // Per-kernel-family timing (HIP events on the context stream).
+    struct Family {
+        double ms = 0.0;
+        long launches = 0;
+        double flops = 0.0;
+        std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
+    };
+    bool prof = false;
+    std::map<std::string, Family> fams;
+    std::vector<hipEvent_t> event_pool;
+};
+
+namespace kdec {
+
+// Error helpers: set the context message and return the code.
+int fail(kdec_ctx* ctx, int code, const std::string& msg);
+int hip_fail(kdec_ctx* ctx, hipError_t e, const char* where);
+
+#define KDEC_HIP(ctx, expr)                                         \
+    do {                                                            \
+        hipError_t e_ = (expr);                                     \
+        if (e_ != hipSuccess) return kdec::hip_fail(ctx, e_, #expr); \
+    } while (0)
+
+#define KDEC_CHECK(ctx, cond, msg)                                  \
+    do {                                                            \
+        if (!(cond)) return kdec::fail(ctx, KDEC_EINVAL, msg);      \
+    } while (0)
+
+// Workspace from the context allocator (returns nullptr and sets the error on
+// failure); release with ws_free once the kernels that use it are enqueued.
+void* ws_alloc(kdec_ctx* ctx, size_t bytes);
+void ws_free(kdec_ctx* ctx, void* p);
+
+// RAII workspace block.
+struct Workspace {
+    kdec_ctx* ctx;
+    void* p = nullptr;
+    Workspace(kdec_ctx* c, size_t bytes) : ctx(c) { p = ws_alloc(c, bytes); }
+    ~Workspace() { if (p) ws_free(ctx, p); }
+    Workspace(const Workspace&) = delete;
+    Workspace& operator=(const Workspace&) = delete;
+    template <class T> T* as() const { return static_cast<T*>(p); }
+};
+
+// Profiling bracket around the launches of one kernel family.
+struct ProfScope {
+    kdec_ctx* ctx;
+    const char* name;
+    double flops;
+    hipEvent_t start = nullptr;
+    ProfScope(kdec_ctx* c, const char* n, double f);
+    ~ProfScope();
+};
+
+// Checks the last launch; returns KDEC_OK or the HIP error code.
+int launch_check(kdec_ctx* ctx, const char* where);
+
+inline long cdiv(long a, long b) { return (a + b - 1) / b; }
+
+}  // namespace kdec

@@ -1,0 +1,554 @@
+// Whole-decoder model over the C++ drop-in atoms: named parameters in one
+// device buffer, the per-AdaIN style projection batched over all units, and
+// the forward / backward sequence of DecoderLora (decoder_lora.cpp:211-296)
+// without the LoRA term.
+#include <map>
+#include <string>
+#include <vector>
+
+#include <hip/hip_runtime_api.h>
+
+#include "kdec.h"
+#include "kdec_internal.hpp"
+#include "kdec_model.h"
+#include "kokoro_decoder_backward.h"
+
+namespace bt = brotensor;
+using bt::Device;
+using bt::Tensor;
+namespace bd = brosoundml::detail;
+
+struct kdec_model {
+    kdec_ctx* ctx = nullptr;
+    // configuration
+    int asr_dim = 0, asr_res_dim = 0, style_dim = 0, enc_dim = 0, n_decode = 0;
+    int dec_out[8] = {}, dec_up_at = -1, n_ups = 0, ups_rates[4] = {}, ups_kernels[4] = {};
+    int n_kernels = 0, rb_kernels[4] = {}, rb_dil[4][3] = {};
+    int n_fft = 0, hop = 0, conv_post_k = 0, sample_rate = 0, harmonic_num = 0;
+
+    brosoundml::DecoderBackbone bb;
+    brosoundml::Generator gen;
+    brosoundml::HarmonicSource hs;
+
+    struct Param {
+        Tensor* value = nullptr;  // points into a module struct
+        Tensor grad;
+        int rows = 0, cols = 0;
+        long offset = 0;          // into the flat buffers
+    };
+    std::vector<std::string> order;
+    std::map<std::string, Param> params;
+    Tensor pbuf, gbuf;            // flat parameter / grad storage
+    long total = 0;
+
+    struct Unit {
+        std::string name;
+        int C = 0;
+        int offset = 0;           // row offset in the stacked fc
+    };
+    std::vector<Unit> units;
+    int rows_total = 0;
+    std::vector<brosoundml::AdaIN1dWeights*> unit_w;  // same order as units
+
+    bd::WeightGrads wg_all, wg_conv, wg_alpha;
+
+    // per forward
+    int N = 0, T = 0;
+    Tensor style_v, gb, dgb;
+    std::vector<bd::BlockAffines> bbaff, dbbaff;
+    std::vector<bd::ResBlock1Affines> naff, raff, dnaff, draff;
+    bd::BackboneCache bbc;
+    bd::GeneratorCache genc;
+    Tensor gen_in, har;
+    std::string err;
+};
+
+namespace {
+
+struct Spec {
+    std::string name;
+    Tensor* t;
+    int rows, cols;
+    int kind;  // 0 conv/convT/pool weight or bias, 1 alpha, 2 fc weight, 3 fc bias, 4 forward-only
+};
+
+void conv_geom(brosoundml::Conv1d& c, int cin, int cout, int k, int s, int p, int d) {
+    c.in_channels = cin;
+    c.out_channels = cout;
+    c.kernel_size = k;
+    c.stride = s;
+    c.padding = p;
+    c.dilation = d;
+    c.groups = 1;
+}
+
+// Errors are reported through the context's last-error message.
+int fail(kdec_model* m, int code, const std::string& msg) {
+    if (m) m->err = msg;
+    if (m && m->ctx) m->ctx->err = msg.rfind("brosoundml:", 0) == 0 ? msg : "brosoundml: kdec_model: " + msg;
+    return code;
+}
+
+// Builds the module structs and the parameter list (names, shapes, kinds).
+void build(kdec_model* m, std::vector<Spec>& specs) {
+    const int S = m->style_dim;
+    const std::string P = "decoder.module.";
+    auto conv = [&](const std::string& pfx, brosoundml::Conv1d& c, bool bias) {
+        specs.push_back({pfx + ".weight", &c.W, c.out_channels, c.in_channels * c.kernel_size, 0});
+        if (bias) specs.push_back({pfx + ".bias", &c.b, c.out_channels, 1, 0});
+    };
+    auto adain = [&](const std::string& pfx, brosoundml::AdaIN1dWeights& a, int C) {
+        a.channels = C;
+        a.style_dim = S;
+        a.eps = 1e-5f;
+        a.fc.in_features = S;
+        a.fc.out_features = 2 * C;
+        m->units.push_back({pfx, C, m->rows_total});
+        m->unit_w.push_back(&a);
+        m->rows_total += 2 * C;
+    };
+
+    conv_geom(m->bb.F0_conv, 1, 1, 3, 2, 1, 1);
+    conv_geom(m->bb.N_conv, 1, 1, 3, 2, 1, 1);
+    conv_geom(m->bb.asr_res, m->asr_dim, m->asr_res_dim, 1, 1, 0, 1);
+    conv(P + "F0_conv", m->bb.F0_conv, true);
+    conv(P + "N_conv", m->bb.N_conv, true);
+    conv(P + "asr_res.0", m->bb.asr_res, true);
+
+    auto resblk = [&](brosoundml::AdainResBlk1dWeights& w, int din, int dout, bool up, const std::string& pfx) {
+        w.channels_in = din;
+        w.channels_out = dout;
+        w.upsample = up;
+        w.learned_sc = din != dout;
+        adain(pfx + ".norm1", w.norm1, din);
+        adain(pfx + ".norm2", w.norm2, dout);
+        conv_geom(w.conv1, din, dout, 3, 1, 1, 1);
+        conv_geom(w.conv2, dout, dout, 3, 1, 1, 1);
+        conv(pfx + ".conv1", w.conv1, true);
+        conv(pfx + ".conv2", w.conv2, true);
+        if (w.learned_sc) {
+            conv_geom(w.conv1x1, din, dout, 1, 1, 0, 1);
+            conv(pfx + ".conv1x1", w.conv1x1, false);
+        }
+        if (up) {
+            specs.push_back({pfx + ".pool.weight", &w.pool_W, din, 3, 0});
+            specs.push_back({pfx + ".pool.bias", &w.pool_b, din, 1, 0});
+        }
+    };
+    resblk(m->bb.encode, m->asr_dim + 2, m->enc_dim, false, P + "encode");
+    m->bb.decode.assign(m->n_decode, brosoundml::AdainResBlk1dWeights{});
+    int prev = m->enc_dim;
+    bool res = true;
+    for (int i = 0; i < m->n_decode; ++i) {
+        const bool up = i == m->dec_up_at;
+        const int din = res ? prev + m->asr_res_dim + 2 : prev;
+        resblk(m->bb.decode[i], din, m->dec_out[i], up, P + "decode." + std::to_string(i));
+        prev = m->dec_out[i];
+        if (up) res = false;
+    }
+
+    const int init_C = m->dec_out[m->n_decode - 1];
+    const std::string G = P + "generator.";
+    auto& g = m->gen;
+    g.n_fft = m->n_fft;
+    g.hop_size = m->hop;
+    g.win_size = m->n_fft;
+    g.num_upsamples = m->n_ups;
+    g.num_kernels = m->n_kernels;
+    g.ups_W.resize(m->n_ups);
+    g.ups_b.resize(m->n_ups);
+    g.ups_C_in.resize(m->n_ups);
+    g.ups_C_out.resize(m->n_ups);
+    g.ups_k.resize(m->n_ups);
+    g.ups_stride.resize(m->n_ups);
+    g.ups_pad.resize(m->n_ups);
+    for (int i = 0; i < m->n_ups; ++i) {
+        const int ci = init_C >> i, co = init_C >> (i + 1);
+        g.ups_C_in[i] = ci;
+        g.ups_C_out[i] = co;
+        g.ups_k[i] = m->ups_kernels[i];
+        g.ups_stride[i] = m->ups_rates[i];
+        g.ups_pad[i] = (m->ups_kernels[i] - m->ups_rates[i]) / 2;
+        specs.push_back({G + "ups." + std::to_string(i) + ".weight", &g.ups_W[i], ci, co * m->ups_kernels[i], 0});
+        specs.push_back({G + "ups." + std::to_string(i) + ".bias", &g.ups_b[i], co, 1, 0});
+    }
+    g.noise_convs.resize(m->n_ups);
+    for (int i = 0; i < m->n_ups; ++i) {
+        const int co = init_C >> (i + 1);
+        if (i + 1 < m->n_ups) {
+            int sf = 1;
+            for (int j = i + 1; j < m->n_ups; ++j) sf *= m->ups_rates[j];
+            conv_geom(g.noise_convs[i], m->n_fft + 2, co, 2 * sf, sf, (sf + 1) / 2, 1);
+        } else {
+            conv_geom(g.noise_convs[i], m->n_fft + 2, co, 1, 1, 0, 1);
+        }
+        conv(G + "noise_convs." + std::to_string(i), g.noise_convs[i], true);
+    }
+    auto rb1 = [&](brosoundml::AdaINResBlock1Weights& w, int C, int k, const int* dil, const std::string& pfx,
+                   std::vector<Spec>& alpha_specs) {
+        w.channels = C;
+        w.kernel_size = k;
+        w.dilations.assign(dil, dil + 3);
+        for (int j = 0; j < 3; ++j) {
+            const std::string js = std::to_string(j);
+            conv_geom(w.convs1[j], C, C, k, 1, (k * dil[j] - dil[j]) / 2, dil[j]);
+            conv_geom(w.convs2[j], C, C, k, 1, (k - 1) / 2, 1);
+            conv(pfx + ".convs1." + js, w.convs1[j], true);
+            conv(pfx + ".convs2." + js, w.convs2[j], true);
+            alpha_specs.push_back({pfx + ".alpha1." + js, &w.alpha1[j], C, 1, 1});
+            alpha_specs.push_back({pfx + ".alpha2." + js, &w.alpha2[j], C, 1, 1});
+        }
+        for (int j = 0; j < 3; ++j) adain(pfx + ".adain1." + std::to_string(j), w.adain1[j], C);
+        for (int j = 0; j < 3; ++j) adain(pfx + ".adain2." + std::to_string(j), w.adain2[j], C);
+    };
+    const int dil135[3] = {1, 3, 5};
+    std::vector<Spec> alphas;
+    g.noise_res.resize(m->n_ups);
+    for (int i = 0; i < m->n_ups; ++i)
+        rb1(g.noise_res[i], init_C >> (i + 1), i + 1 < m->n_ups ? 7 : 11, dil135,
+            G + "noise_res." + std::to_string(i), alphas);
+    g.resblocks.resize(static_cast<std::size_t>(m->n_ups) * m->n_kernels);
+    for (int i = 0; i < m->n_ups; ++i)
+        for (int j = 0; j < m->n_kernels; ++j) {
+            const int idx = i * m->n_kernels + j;
+            rb1(g.resblocks[idx], init_C >> (i + 1), m->rb_kernels[j], m->rb_dil[j],
+                G + "resblocks." + std::to_string(idx), alphas);
+        }
+    specs.insert(specs.end(), alphas.begin(), alphas.end());
+    conv_geom(g.conv_post, init_C >> m->n_ups, m->n_fft + 2, m->conv_post_k, 1, (m->conv_post_k - 1) / 2, 1);
+    conv(G + "conv_post", g.conv_post, true);
+
+    auto& h = m->hs;
+    h.sample_rate = m->sample_rate;
+    h.harmonic_num = m->harmonic_num;
+    h.n_fft = m->n_fft;
+    h.hop_size = m->hop;
+    h.win_size = m->n_fft;
+    int upr = 1;
+    for (int i = 0; i < m->n_ups; ++i) upr *= m->ups_rates[i];
+    h.upsample_scale = upr * m->hop;
+    h.l_linear.in_features = m->harmonic_num + 1;
+    h.l_linear.out_features = 1;
+    specs.push_back({G + "m_source.l_linear.weight", &h.l_linear.W, 1, m->harmonic_num + 1, 4});
+    specs.push_back({G + "m_source.l_linear.bias", &h.l_linear.b, 1, 1, 4});
+
+    // the style fc of every unit, stacked (weights then biases) in unit order
+    for (std::size_t u = 0; u < m->units.size(); ++u) {
+        auto* a = m->unit_w[u];
+        specs.push_back({m->units[u].name + ".fc.weight", &a->fc.W, 2 * a->channels, S, 2});
+    }
+    for (std::size_t u = 0; u < m->units.size(); ++u) {
+        auto* a = m->unit_w[u];
+        specs.push_back({m->units[u].name + ".fc.bias", &a->fc.b, 2 * a->channels, 1, 3});
+    }
+}
+
+Tensor view_of(const Tensor& buf, long off, int rows, int cols) {
+    Tensor t = Tensor::view(Device::HIP, static_cast<float*>(buf.data) + off, rows, cols);
+    t.storage = buf.storage;
+    return t;
+}
+
+int check(kdec_model* m, int rc) {
+    if (rc != KDEC_OK) m->err = kdec_last_error(m->ctx);
+    return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kdec_model_create(kdec_ctx* ctx, const int* v, int n, kdec_model** out) {
+    if (!ctx || !v || !out) return KDEC_EINVAL;
+    *out = nullptr;
+    kdec_model* m = new kdec_model();
+    m->ctx = ctx;
+    int i = 0;
+    auto nx = [&]() { return i < n ? v[i++] : -1; };
+    m->asr_dim = nx(); m->asr_res_dim = nx(); m->style_dim = nx(); m->enc_dim = nx(); m->n_decode = nx();
+    for (int j = 0; j < 8; ++j) m->dec_out[j] = nx();
+    m->dec_up_at = nx(); m->n_ups = nx();
+    for (int j = 0; j < 4; ++j) m->ups_rates[j] = nx();
+    for (int j = 0; j < 4; ++j) m->ups_kernels[j] = nx();
+    m->n_kernels = nx();
+    for (int j = 0; j < 4; ++j) m->rb_kernels[j] = nx();
+    for (int j = 0; j < 4; ++j)
+        for (int q = 0; q < 3; ++q) m->rb_dil[j][q] = nx();
+    m->n_fft = nx(); m->hop = nx(); m->conv_post_k = nx(); m->sample_rate = nx(); m->harmonic_num = nx();
+    if (i != n || n != 47 || m->n_decode < 1 || m->n_decode > 8 || m->n_ups < 1 || m->n_ups > 4 ||
+        m->n_kernels < 1 || m->n_kernels > 4 || m->style_dim < 1 || m->n_fft < 2 || m->hop < 1) {
+        delete m;
+        return KDEC_EINVAL;
+    }
+    try {
+        bt::set_runtime(ctx);
+        std::vector<Spec> specs;
+        build(m, specs);
+        long total = 0;
+        for (auto& s : specs) total += static_cast<long>(s.rows) * s.cols;
+        m->total = total;
+        m->pbuf = Tensor::zeros_on(Device::HIP, 1, static_cast<int>(total));
+        m->gbuf = Tensor::zeros_on(Device::HIP, 1, static_cast<int>(total));
+        long off = 0;
+        for (auto& s : specs) {
+            kdec_model::Param p;
+            p.value = s.t;
+            p.rows = s.rows;
+            p.cols = s.cols;
+            p.offset = off;
+            *s.t = view_of(m->pbuf, off, s.rows, s.cols);
+            p.grad = view_of(m->gbuf, off, s.rows, s.cols);
+            off += static_cast<long>(s.rows) * s.cols;
+            m->order.push_back(s.name);
+            auto& slot = m->params[s.name];
+            slot = p;
+            if (s.kind == 0) {
+                m->wg_all.add(*s.t, slot.grad);
+                m->wg_conv.add(*s.t, slot.grad);
+            } else if (s.kind == 1) {
+                m->wg_all.add(*s.t, slot.grad);
+                m->wg_alpha.add(*s.t, slot.grad);
+            }
+        }
+    } catch (const std::exception& e) {
+        delete m;
+        return KDEC_EINVAL;
+    }
+    *out = m;
+    return KDEC_OK;
+}
+
+int kdec_model_destroy(kdec_model* m) {
+    delete m;
+    return KDEC_OK;
+}
+
+int kdec_model_param_count(const kdec_model* m) { return m ? static_cast<int>(m->order.size()) : 0; }
+
+const char* kdec_model_param_name(const kdec_model* m, int i) {
+    if (!m || i < 0 || i >= static_cast<int>(m->order.size())) return nullptr;
+    return m->order[i].c_str();
+}
+
+int kdec_model_param_shape(const kdec_model* m, const char* name, int* rows, int* cols) {
+    if (!m || !name) return KDEC_EINVAL;
+    auto it = m->params.find(name);
+    if (it == m->params.end()) return KDEC_EINVAL;
+    if (rows) *rows = it->second.rows;
+    if (cols) *cols = it->second.cols;
+    return KDEC_OK;
+}
+
+static int copy_param(kdec_model* m, const char* name, float* host, long n, bool to_dev, bool grad) {
+    if (!m || !name || !host) return KDEC_EINVAL;
+    auto it = m->params.find(name);
+    if (it == m->params.end()) return fail(m, KDEC_EINVAL, std::string("unknown parameter ") + name);
+    const auto& p = it->second;
+    if (n != static_cast<long>(p.rows) * p.cols) return fail(m, KDEC_EINVAL, std::string("size mismatch ") + name);
+    float* d = static_cast<float*>(grad ? m->gbuf.data : m->pbuf.data) + p.offset;
+    hipStream_t s = static_cast<hipStream_t>(kdec_get_stream(m->ctx));
+    hipError_t e = to_dev ? hipMemcpyAsync(d, host, n * sizeof(float), hipMemcpyHostToDevice, s)
+                          : hipMemcpyAsync(host, d, n * sizeof(float), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    return e == hipSuccess ? KDEC_OK : fail(m, KDEC_EHIP, hipGetErrorString(e));
+}
+
+int kdec_model_set_param(kdec_model* m, const char* name, const float* host, long n) {
+    return copy_param(m, name, const_cast<float*>(host), n, true, false);
+}
+int kdec_model_get_param(kdec_model* m, const char* name, float* host, long n) {
+    return copy_param(m, name, host, n, false, false);
+}
+int kdec_model_get_grad(kdec_model* m, const char* name, float* host, long n) {
+    return copy_param(m, name, host, n, false, true);
+}
+
+float* kdec_model_param_ptr(kdec_model* m, const char* name) {
+    if (!m || !name) return nullptr;
+    auto it = m->params.find(name);
+    return it == m->params.end() ? nullptr : static_cast<float*>(m->pbuf.data) + it->second.offset;
+}
+
+float* kdec_model_grad_ptr(kdec_model* m, const char* name) {
+    if (!m || !name) return nullptr;
+    auto it = m->params.find(name);
+    return it == m->params.end() ? nullptr : static_cast<float*>(m->gbuf.data) + it->second.offset;
+}
+
+long kdec_model_param_total(const kdec_model* m) { return m ? m->total : 0; }
+
+int kdec_model_zero_grad(kdec_model* m) {
+    if (!m) return KDEC_EINVAL;
+    return check(m, kdec_fill(m->ctx, static_cast<float*>(m->gbuf.data), m->total, 0.0f));
+}
+
+int kdec_model_unit_count(const kdec_model* m) { return m ? static_cast<int>(m->units.size()) : 0; }
+const char* kdec_model_unit_name(const kdec_model* m, int i) {
+    return (m && i >= 0 && i < static_cast<int>(m->units.size())) ? m->units[i].name.c_str() : nullptr;
+}
+int kdec_model_unit_channels(const kdec_model* m, int i) {
+    return (m && i >= 0 && i < static_cast<int>(m->units.size())) ? m->units[i].C : -1;
+}
+int kdec_model_unit_offset(const kdec_model* m, int i) {
+    return (m && i >= 0 && i < static_cast<int>(m->units.size())) ? m->units[i].offset : -1;
+}
+int kdec_model_affine_rows(const kdec_model* m) { return m ? m->rows_total : 0; }
+
+int kdec_model_get_affines(kdec_model* m, float* gb, float* dgb) {
+    if (!m || m->N == 0) return KDEC_EINVAL;
+    try {
+        if (gb && m->gb.data) {
+            auto h = m->gb.to_host_vector();
+            std::copy(h.begin(), h.end(), gb);
+        }
+        if (dgb && m->dgb.data) {
+            auto h = m->dgb.to_host_vector();
+            std::copy(h.begin(), h.end(), dgb);
+        }
+    } catch (const std::exception& e) {
+        return fail(m, KDEC_EHIP, e.what());
+    }
+    return KDEC_OK;
+}
+
+int kdec_model_lengths(const kdec_model* m, int T, int* L_gen, int* frames, int* audio_len) {
+    if (!m || T <= 0) return KDEC_EINVAL;
+    int upr = 1;
+    for (int i = 0; i < m->n_ups; ++i) upr *= m->ups_rates[i];
+    const int lg = 2 * T;
+    const int fr = lg * upr + 1;
+    if (L_gen) *L_gen = lg;
+    if (frames) *frames = fr;
+    if (audio_len) *audio_len = (fr - 1) * m->hop;
+    return KDEC_OK;
+}
+
+int kdec_model_forward(kdec_model* m, int N, int T, const float* asr, const float* F0, const float* Nn,
+                       const float* style, const float* har_in, float* audio) {
+    if (!m || N <= 0 || T <= 0 || !asr || !F0 || !Nn || !style || !audio) return KDEC_EINVAL;
+    try {
+        bt::set_runtime(m->ctx);
+        m->N = N;
+        m->T = T;
+        const int S = m->style_dim;
+        const int R = m->rows_total;
+        auto in = [&](const float* p, int cols) {
+            return Tensor::view(Device::HIP, const_cast<float*>(p), N, cols);
+        };
+        m->style_v = in(style, S);
+        // style projection for every unit at once
+        m->gb = Tensor::empty_on(Device::HIP, N, R);
+        const long fc_off = m->params.at(m->units[0].name + ".fc.weight").offset;
+        const long fcb_off = m->params.at(m->units[0].name + ".fc.bias").offset;
+        const float* W = static_cast<const float*>(m->pbuf.data) + fc_off;
+        const float* b = static_cast<const float*>(m->pbuf.data) + fcb_off;
+        if (int rc = check(m, kdec_style_proj_fwd(m->ctx, W, b, style, S, static_cast<float*>(m->gb.data), R, N, R, S)))
+            return rc;
+        auto gv = [&](const Tensor& buf, int off, int C) {
+            Tensor t = Tensor::view(Device::HIP, static_cast<float*>(buf.data) + off, N, C, bt::Dtype::FP32, R);
+            t.storage = buf.storage;
+            return t;
+        };
+        const int n_dec = m->n_decode;
+        m->bbaff.assign(1 + n_dec, bd::BlockAffines{});
+        m->naff.assign(m->n_ups, bd::ResBlock1Affines{});
+        m->raff.assign(static_cast<std::size_t>(m->n_ups) * m->n_kernels, bd::ResBlock1Affines{});
+        std::size_t u = 0;
+        auto pair = [&](Tensor& g, Tensor& bb) {
+            const auto& un = m->units[u++];
+            g = gv(m->gb, un.offset, un.C);
+            bb = gv(m->gb, un.offset + un.C, un.C);
+        };
+        for (auto& a : m->bbaff) { pair(a.g1, a.b1); pair(a.g2, a.b2); }
+        auto rb = [&](bd::ResBlock1Affines& a) {
+            for (int j = 0; j < 3; ++j) pair(a.g1[j], a.b1[j]);
+            for (int j = 0; j < 3; ++j) pair(a.g2[j], a.b2[j]);
+        };
+        for (auto& a : m->naff) rb(a);
+        for (auto& a : m->raff) rb(a);
+
+        // harmonic source
+        int sig = 0, frames = 0;
+        m->hs.forward(in(F0, 2 * T), 2 * T, sig, frames, m->har);
+        if (har_in) {
+            Tensor h = in(har_in, (m->n_fft + 2) * frames);
+            m->har = h.clone();
+        }
+        bd::decoder_backbone_forward_train(m->bb, in(asr, m->asr_dim * T), in(F0, 2 * T), in(Nn, 2 * T), T,
+                                           m->bbaff, 1e-5f, m->gen_in, m->bbc);
+        const int init_C = m->dec_out[n_dec - 1];
+        const int L_gen = m->gen_in.cols / init_C;
+        Tensor out;
+        bd::generator_forward_train(m->gen, m->gen_in, L_gen, m->har, frames, m->naff, m->raff, out, m->genc);
+        const int alen = out.cols;
+        hipStream_t s = static_cast<hipStream_t>(kdec_get_stream(m->ctx));
+        hipError_t e = hipMemcpyAsync(audio, out.data, static_cast<size_t>(N) * alen * sizeof(float),
+                                      hipMemcpyDeviceToDevice, s);
+        if (e != hipSuccess) return fail(m, KDEC_EHIP, hipGetErrorString(e));
+    } catch (const std::exception& e) {
+        return fail(m, KDEC_EINVAL, e.what());
+    }
+    return KDEC_OK;
+}
+
+int kdec_model_backward(kdec_model* m, const float* daudio, int wgrad, int dalpha, float* dstyle) {
+    if (!m || !daudio || m->N == 0) return KDEC_EINVAL;
+    try {
+        bt::set_runtime(m->ctx);
+        const int N = m->N;
+        const int R = m->rows_total;
+        const int S = m->style_dim;
+        int alen = 0;
+        kdec_model_lengths(m, m->T, nullptr, nullptr, &alen);
+        Tensor dA = Tensor::view(Device::HIP, const_cast<float*>(daudio), N, alen);
+        const bd::WeightGrads* wg = wgrad ? (dalpha ? &m->wg_all : &m->wg_conv) : (dalpha ? &m->wg_alpha : nullptr);
+        // affine grads land in place in the packed dgb buffer
+        m->dgb = Tensor::empty_on(Device::HIP, N, R);
+        auto gv = [&](int off, int C) {
+            Tensor t = Tensor::view(Device::HIP, static_cast<float*>(m->dgb.data) + off, N, C, bt::Dtype::FP32, R);
+            t.storage = m->dgb.storage;
+            return t;
+        };
+        m->dbbaff.assign(1 + m->n_decode, bd::BlockAffines{});
+        m->dnaff.assign(m->n_ups, bd::ResBlock1Affines{});
+        m->draff.assign(static_cast<std::size_t>(m->n_ups) * m->n_kernels, bd::ResBlock1Affines{});
+        std::size_t u = 0;
+        auto pair = [&](Tensor& g, Tensor& bb) {
+            const auto& un = m->units[u++];
+            g = gv(un.offset, un.C);
+            bb = gv(un.offset + un.C, un.C);
+        };
+        for (auto& a : m->dbbaff) { pair(a.g1, a.b1); pair(a.g2, a.b2); }
+        auto rb = [&](bd::ResBlock1Affines& a) {
+            for (int j = 0; j < 3; ++j) pair(a.g1[j], a.b1[j]);
+            for (int j = 0; j < 3; ++j) pair(a.g2[j], a.b2[j]);
+        };
+        for (auto& a : m->dnaff) rb(a);
+        for (auto& a : m->draff) rb(a);
+
+        Tensor dGenIn;
+        bd::generator_backward(m->gen, m->genc, m->naff, m->raff, dA, dGenIn, m->dnaff, m->draff, wg);
+        bd::decoder_backbone_backward(m->bb, m->bbc, m->bbaff, dGenIn, 1e-5f, m->dbbaff, wg);
+        // style projection adjoint over every unit
+        const long fc_off = m->params.at(m->units[0].name + ".fc.weight").offset;
+        const long fcb_off = m->params.at(m->units[0].name + ".fc.bias").offset;
+        const float* W = static_cast<const float*>(m->pbuf.data) + fc_off;
+        float* dW = wgrad ? static_cast<float*>(m->gbuf.data) + fc_off : nullptr;
+        float* db = wgrad ? static_cast<float*>(m->gbuf.data) + fcb_off : nullptr;
+        if (dstyle || dW)
+            if (int rc = check(m, kdec_style_proj_bwd(m->ctx, W, static_cast<const float*>(m->style_v.data), S,
+                                                      static_cast<const float*>(m->dgb.data), R, dstyle, S, 0.0f, dW,
+                                                      db, N, R, S)))
+                return rc;
+    } catch (const std::exception& e) {
+        return fail(m, KDEC_EINVAL, e.what());
+    }
+    return KDEC_OK;
+}
+
+const float* kdec_model_har(const kdec_model* m) { return m ? static_cast<const float*>(m->har.data) : nullptr; }
+const float* kdec_model_gen_in(const kdec_model* m) {
+    return m ? static_cast<const float*>(m->gen_in.data) : nullptr;
+}
+
+}  // extern "C"

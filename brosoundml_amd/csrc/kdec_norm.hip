@@ -1,0 +1,425 @@
+// AdaIN (instance norm + per-utterance style affine) fused with its
+// activation, forward and backward, plus the small elementwise ops of the
+// decoder (leaky ReLU, axpby, reflect pad, nearest-2x).
+//
+// Everything here is HBM-bound, so each kernel reads its operands once per
+// pass and writes one output: the reference's adain_affine_forward is five
+// full-tensor passes (group_norm, two transposes, modulate, a unit-gamma
+// upload), its backward seven (kokoro_decoder_backward.cpp:100-150).
+//
+// Statistics are per (utterance, channel) row over L, accumulated in double
+// so the result does not depend on the row length or the thread count.
+#include "kdec_internal.hpp"
+
+namespace kdec {
+namespace {
+
+constexpr int RT = 256;  // threads per row block
+
+__device__ inline double block_sum(double v, double* red) {
+    // wave reduction via shuffles, then across the block's waves
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_down(v, o, 64);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    double t = 0.0;
+    if (threadIdx.x < (blockDim.x >> 6)) t = red[threadIdx.x];
+    if (wave == 0)
+        for (int o = 32; o > 0; o >>= 1) t += __shfl_down(t, o, 64);
+    if (threadIdx.x == 0) red[0] = t;
+    __syncthreads();
+    const double r = red[0];
+    return r;
+}
+
+// stats[row] = (mean, rstd) of x[row, :L]; row = n*C + c.
+__global__ __launch_bounds__(RT) void instnorm_stats_k(const float* X, long x_bs, int C, int L,
+                                                      float eps, float2* stats) {
+    __shared__ double red[RT / 64];
+    const int row = blockIdx.x;
+    const int n = row / C, c = row - n * C;
+    const float* x = X + n * x_bs + static_cast<long>(c) * L;
+    const double x0 = x[0];  // shift for a well-conditioned variance
+    double s1 = 0.0, s2 = 0.0;
+    for (int l = threadIdx.x; l < L; l += RT) {
+        const double v = static_cast<double>(x[l]) - x0;
+        s1 += v;
+        s2 += v * v;
+    }
+    s1 = block_sum(s1, red);
+    s2 = block_sum(s2, red);
+    if (threadIdx.x == 0) {
+        const double m = s1 / L;
+        double var = s2 / L - m * m;
+        if (var < 0.0) var = 0.0;
+        stats[row] = make_float2(static_cast<float>(x0 + m),
+                                 static_cast<float>(1.0 / sqrt(var + static_cast<double>(eps))));
+    }
+}
+
+struct AdainArgs {
+    const float* X;
+    long x_bs;
+    const float2* stats;
+    const float* gamma;
+    const float* beta;
+    long gb_bs;
+    int act;
+    float slope;
+    const float* alpha;
+    int C, L;
+};
+
+__device__ inline float act_fwd(int act, float s, float slope, float a) {
+    if (act == KDEC_ACT_LEAKY) return s > 0.0f ? s : slope * s;
+    if (act == KDEC_ACT_SNAKE) {
+        const float sn = sinf(a * s);
+        return s + sn * sn / a;
+    }
+    return s;
+}
+
+// grid (chunks, N*C)
+__global__ __launch_bounds__(RT) void adain_act_fwd_k(AdainArgs g, float* Y, long y_bs, float* Yp,
+                                                     long yp_bs) {
+    const int row = blockIdx.y;
+    const int n = row / g.C, c = row - n * g.C;
+    const float2 st = g.stats[row];
+    const float g1 = 1.0f + g.gamma[n * g.gb_bs + c];
+    const float bt = g.beta ? g.beta[n * g.gb_bs + c] : 0.0f;
+    const float a = g.act == KDEC_ACT_SNAKE ? g.alpha[c] : 0.0f;
+    const long off = static_cast<long>(c) * g.L;
+    const float* x = g.X + n * g.x_bs + off;
+    float* y = Y + n * y_bs + off;
+    float* yp = Yp ? Yp + n * yp_bs + off : nullptr;
+    for (int l = blockIdx.x * RT + threadIdx.x; l < g.L; l += gridDim.x * RT) {
+        const float xh = (x[l] - st.x) * st.y;
+        const float s = g1 * xh + bt;
+        if (yp) yp[l] = s;
+        y[l] = act_fwd(g.act, s, g.slope, a);
+    }
+}
+
+// One block per (n, c) row. Pass 1 reduces sum(ds), sum(ds*xh) (and the snake
+// alpha grad); pass 2 writes dx. ds = dY * act'(s) is the grad at the affine
+// output; dgamma = sum(ds*xh), dbeta = sum(ds);
+// dx = rstd * g1 * (ds - mean(ds) - xh * mean(ds*xh)) (+ R).
+__global__ __launch_bounds__(RT) void adain_act_bwd_k(AdainArgs g, const float* dY, long dy_bs,
+                                                     const float* R, long r_bs, float* dX,
+                                                     long dx_bs, float* dgamma, float* dbeta,
+                                                     long dgb_bs, float* dalpha_part) {
+    __shared__ double red[RT / 64];
+    const int row = blockIdx.x;
+    const int n = row / g.C, c = row - n * g.C;
+    const float2 st = g.stats[row];
+    const float g1 = 1.0f + g.gamma[n * g.gb_bs + c];
+    const float bt = g.beta ? g.beta[n * g.gb_bs + c] : 0.0f;
+    const float a = g.act == KDEC_ACT_SNAKE ? g.alpha[c] : 0.0f;
+    const long off = static_cast<long>(c) * g.L;
+    const float* x = g.X + n * g.x_bs + off;
+    const float* dy = dY + n * dy_bs + off;
+    double sd = 0.0, sdx = 0.0, sa = 0.0;
+    for (int l = threadIdx.x; l < g.L; l += RT) {
+        const float xh = (x[l] - st.x) * st.y;
+        const float s = g1 * xh + bt;
+        float ds = dy[l];
+        if (g.act == KDEC_ACT_LEAKY) {
+            ds = s > 0.0f ? ds : g.slope * ds;
+        } else if (g.act == KDEC_ACT_SNAKE) {
+            const float s2 = sinf(2.0f * a * s);
+            const float sn = sinf(a * s);
+            sa += static_cast<double>(dy[l]) * (s * s2 / a - sn * sn / (a * a));
+            ds = ds * (1.0f + s2);
+        }
+        sd += ds;
+        sdx += static_cast<double>(ds) * xh;
+    }
+    sd = block_sum(sd, red);
+    sdx = block_sum(sdx, red);
+    if (g.act == KDEC_ACT_SNAKE && dalpha_part) sa = block_sum(sa, red);
+    if (threadIdx.x == 0) {
+        if (dgamma) dgamma[n * dgb_bs + c] = static_cast<float>(sdx);
+        if (dbeta) dbeta[n * dgb_bs + c] = static_cast<float>(sd);
+        if (g.act == KDEC_ACT_SNAKE && dalpha_part) dalpha_part[row] = static_cast<float>(sa);
+    }
+    const float mds = static_cast<float>(sd / g.L);
+    const float mdsx = static_cast<float>(sdx / g.L);
+    const float k1 = st.y * g1;
+    float* dx = dX + n * dx_bs + off;
+    const float* r = R ? R + n * r_bs + off : nullptr;
+    for (int l = threadIdx.x; l < g.L; l += RT) {
+        const float xh = (x[l] - st.x) * st.y;
+        const float s = g1 * xh + bt;
+        float ds = dy[l];
+        if (g.act == KDEC_ACT_LEAKY) ds = s > 0.0f ? ds : g.slope * ds;
+        else if (g.act == KDEC_ACT_SNAKE) ds = ds * (1.0f + sinf(2.0f * a * s));
+        float v = k1 * (ds - mds - xh * mdsx);
+        if (r) v += r[l];
+        dx[l] = v;
+    }
+}
+
+// dalpha[c] += sum_n part[n*C + c] (fixed order)
+__global__ void dalpha_reduce(const float* part, float* dalpha, int N, int C) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= C) return;
+    double acc = 0.0;
+    for (int n = 0; n < N; ++n) acc += part[n * C + c];
+    dalpha[c] += static_cast<float>(acc);
+}
+
+__global__ void leaky_fwd_k(const float* X, long x_bs, float* Y, long y_bs, long len, float slope) {
+    const int n = blockIdx.y;
+    const float* x = X + n * x_bs;
+    float* y = Y + n * y_bs;
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < len;
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        const float v = x[i];
+        y[i] = v > 0.0f ? v : slope * v;
+    }
+}
+
+__global__ void leaky_bwd_k(const float* X, long x_bs, const float* dY, long dy_bs, float* dX,
+                            long dx_bs, long len, float slope) {
+    const int n = blockIdx.y;
+    const float* x = X + n * x_bs;
+    const float* dy = dY + n * dy_bs;
+    float* dx = dX + n * dx_bs;
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < len;
+         i += static_cast<long>(gridDim.x) * blockDim.x)
+        dx[i] = x[i] > 0.0f ? dy[i] : slope * dy[i];
+}
+
+__global__ void axpby_k(float a, const float* A, long a_bs, float b, const float* B, long b_bs,
+                        float* Y, long y_bs, long len) {
+    const int n = blockIdx.y;
+    const float* pa = A + n * a_bs;
+    const float* pb = B ? B + n * b_bs : nullptr;
+    float* y = Y + n * y_bs;
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < len;
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        float v = a * pa[i];
+        if (pb) v += b * pb[i];
+        y[i] = v;
+    }
+}
+
+// y[c][0] = x[c][1]; y[c][j+1] = x[c][j]
+__global__ void pad_fwd_k(const float* X, long x_bs, float* Y, long y_bs, int C, int L) {
+    const int n = blockIdx.y;
+    const long tot = static_cast<long>(C) * (L + 1);
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < tot;
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        const int c = static_cast<int>(i / (L + 1));
+        const int j = static_cast<int>(i - static_cast<long>(c) * (L + 1));
+        const float* x = X + n * x_bs + static_cast<long>(c) * L;
+        Y[n * y_bs + i] = j == 0 ? x[1] : x[j - 1];
+    }
+}
+
+// dx[c][j] = dy[c][j+1] (+ dy[c][0] at j = 1)
+__global__ void pad_bwd_k(const float* dY, long dy_bs, float* dX, long dx_bs, int C, int L) {
+    const int n = blockIdx.y;
+    const long tot = static_cast<long>(C) * L;
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < tot;
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        const int c = static_cast<int>(i / L);
+        const int j = static_cast<int>(i - static_cast<long>(c) * L);
+        const float* dy = dY + n * dy_bs + static_cast<long>(c) * (L + 1);
+        float v = dy[j + 1];
+        if (j == 1) v += dy[0];
+        dX[n * dx_bs + i] = v;
+    }
+}
+
+__global__ void near2_fwd_k(const float* X, long x_bs, float* Y, long y_bs, int C, int L) {
+    const int n = blockIdx.y;
+    const long tot = static_cast<long>(C) * 2 * L;
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < tot;
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        const long c = i / (2 * L);
+        const long j = i - c * 2 * L;
+        Y[n * y_bs + i] = X[n * x_bs + c * L + (j >> 1)];
+    }
+}
+
+__global__ void near2_bwd_k(const float* dY, long dy_bs, float* dX, long dx_bs, int C, int L,
+                            float scale, float beta) {
+    const int n = blockIdx.y;
+    const long tot = static_cast<long>(C) * L;
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < tot;
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        const long c = i / L;
+        const long l = i - c * L;
+        const float* dy = dY + n * dy_bs + c * 2 * L;
+        float v = scale * (dy[2 * l] + dy[2 * l + 1]);
+        if (beta != 0.0f) v += beta * dX[n * dx_bs + i];
+        dX[n * dx_bs + i] = v;
+    }
+}
+
+__global__ void fill_k(float* Y, long n, float v) {
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<long>(gridDim.x) * blockDim.x)
+        Y[i] = v;
+}
+
+unsigned chunks(long len, long cap = 1024) {
+    long g = (len + 255) / 256;
+    if (g > cap) g = cap;
+    if (g < 1) g = 1;
+    return static_cast<unsigned>(g);
+}
+
+}  // namespace
+}  // namespace kdec
+
+using namespace kdec;
+
+extern "C" {
+
+int kdec_instnorm_stats(kdec_ctx* ctx, const float* X, long x_bs, int N,
+                        int C, int L, float eps, float* stats) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, X && stats && N > 0 && C > 0 && L > 0 && x_bs >= static_cast<long>(C) * L,
+               "kdec_instnorm_stats: bad arguments");
+    ProfScope ps(ctx, "adain_fwd", 0);
+    hipLaunchKernelGGL(instnorm_stats_k, dim3(N * C), dim3(RT), 0, ctx->stream, X, x_bs, C, L, eps,
+                       reinterpret_cast<float2*>(stats));
+    return launch_check(ctx, "instnorm_stats");
+}
+
+int kdec_adain_act_fwd(kdec_ctx* ctx, const float* X, long x_bs,
+                       const float* stats, const float* gamma,
+                       const float* beta, long gb_bs, int act,
+                       float slope, const float* alpha, float* Y, long y_bs,
+                       float* Ypre, long ypre_bs, int N, int C, int L) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, X && stats && gamma && Y && N > 0 && C > 0 && L > 0,
+               "kdec_adain_act_fwd: bad arguments");
+    KDEC_CHECK(ctx, act >= KDEC_ACT_NONE && act <= KDEC_ACT_SNAKE && (act != KDEC_ACT_SNAKE || alpha),
+               "kdec_adain_act_fwd: bad activation");
+    AdainArgs g{X, x_bs, reinterpret_cast<const float2*>(stats), gamma, beta, gb_bs, act, slope, alpha, C, L};
+    ProfScope ps(ctx, "adain_fwd", 0);
+    hipLaunchKernelGGL(adain_act_fwd_k, dim3(chunks(L, 64), N * C), dim3(RT), 0, ctx->stream, g, Y, y_bs,
+                       Ypre, ypre_bs);
+    return launch_check(ctx, "adain_act_fwd");
+}
+
+int kdec_adain_act_bwd(kdec_ctx* ctx, const float* X, long x_bs,
+                       const float* stats, const float* gamma,
+                       const float* beta, long gb_bs, int act, float slope,
+                       const float* alpha, const float* dY, long dy_bs,
+                       const float* R, long r_bs, float* dX, long dx_bs,
+                       float* dgamma, float* dbeta, long dgb_bs,
+                       float* dalpha, int N, int C, int L) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, X && stats && gamma && dY && dX && N > 0 && C > 0 && L > 0,
+               "kdec_adain_act_bwd: bad arguments");
+    KDEC_CHECK(ctx, beta || act == KDEC_ACT_NONE, "kdec_adain_act_bwd: beta needed to recompute the activation input");
+    KDEC_CHECK(ctx, act >= KDEC_ACT_NONE && act <= KDEC_ACT_SNAKE && (act != KDEC_ACT_SNAKE || alpha),
+               "kdec_adain_act_bwd: bad activation");
+    AdainArgs g{X, x_bs, reinterpret_cast<const float2*>(stats), gamma, beta, gb_bs, act, slope, alpha, C, L};
+    float* part = nullptr;
+    Workspace ws(ctx, dalpha && act == KDEC_ACT_SNAKE ? static_cast<size_t>(N) * C * sizeof(float) : 0);
+    if (dalpha && act == KDEC_ACT_SNAKE) {
+        if (!ws.p) return KDEC_ENOMEM;
+        part = ws.as<float>();
+    }
+    {
+        ProfScope ps(ctx, "adain_bwd", 0);
+        hipLaunchKernelGGL(adain_act_bwd_k, dim3(N * C), dim3(RT), 0, ctx->stream, g, dY, dy_bs, R, r_bs, dX,
+                           dx_bs, dgamma, dbeta, dgb_bs, part);
+        if (int rc = launch_check(ctx, "adain_act_bwd")) return rc;
+    }
+    if (part) {
+        hipLaunchKernelGGL(dalpha_reduce, dim3(static_cast<unsigned>(cdiv(C, 256))), dim3(256), 0, ctx->stream,
+                           part, dalpha, N, C);
+        return launch_check(ctx, "dalpha_reduce");
+    }
+    return KDEC_OK;
+}
+
+int kdec_fill(kdec_ctx* ctx, float* Y, long n, float value) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, Y && n >= 0, "kdec_fill: bad arguments");
+    if (n == 0) return KDEC_OK;
+    hipLaunchKernelGGL(fill_k, dim3(chunks(n, 4096)), dim3(256), 0, ctx->stream, Y, n, value);
+    return launch_check(ctx, "fill");
+}
+
+int kdec_leaky_fwd(kdec_ctx* ctx, const float* X, long x_bs, float* Y,
+                   long y_bs, int N, long len, float slope) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, X && Y && N > 0 && len > 0, "kdec_leaky_fwd: bad arguments");
+    ProfScope ps(ctx, "elementwise", 0);
+    hipLaunchKernelGGL(leaky_fwd_k, dim3(chunks(len), N), dim3(256), 0, ctx->stream, X, x_bs, Y, y_bs, len,
+                       slope);
+    return launch_check(ctx, "leaky_fwd");
+}
+
+int kdec_leaky_bwd(kdec_ctx* ctx, const float* X, long x_bs, const float* dY,
+                   long dy_bs, float* dX, long dx_bs, int N, long len,
+                   float slope) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, X && dY && dX && N > 0 && len > 0, "kdec_leaky_bwd: bad arguments");
+    ProfScope ps(ctx, "elementwise", 0);
+    hipLaunchKernelGGL(leaky_bwd_k, dim3(chunks(len), N), dim3(256), 0, ctx->stream, X, x_bs, dY, dy_bs, dX,
+                       dx_bs, len, slope);
+    return launch_check(ctx, "leaky_bwd");
+}
+
+int kdec_axpby(kdec_ctx* ctx, float a, const float* A, long a_bs, float b,
+               const float* B, long b_bs, float* Y, long y_bs, int N,
+               long len) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, A && Y && N > 0 && len > 0, "kdec_axpby: bad arguments");
+    ProfScope ps(ctx, "elementwise", 0);
+    hipLaunchKernelGGL(axpby_k, dim3(chunks(len), N), dim3(256), 0, ctx->stream, a, A, a_bs, b, B, b_bs, Y,
+                       y_bs, len);
+    return launch_check(ctx, "axpby");
+}
+
+int kdec_pad_reflect_left1_fwd(kdec_ctx* ctx, const float* X, long x_bs,
+                               float* Y, long y_bs, int N, int C, int L) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, X && Y && N > 0 && C > 0 && L > 1, "kdec_pad_reflect_left1_fwd: bad arguments");
+    ProfScope ps(ctx, "elementwise", 0);
+    hipLaunchKernelGGL(pad_fwd_k, dim3(chunks(static_cast<long>(C) * (L + 1)), N), dim3(256), 0, ctx->stream,
+                       X, x_bs, Y, y_bs, C, L);
+    return launch_check(ctx, "pad_fwd");
+}
+
+int kdec_pad_reflect_left1_bwd(kdec_ctx* ctx, const float* dY, long dy_bs,
+                               float* dX, long dx_bs, int N, int C, int L) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, dY && dX && N > 0 && C > 0 && L > 1, "kdec_pad_reflect_left1_bwd: bad arguments");
+    ProfScope ps(ctx, "elementwise", 0);
+    hipLaunchKernelGGL(pad_bwd_k, dim3(chunks(static_cast<long>(C) * L), N), dim3(256), 0, ctx->stream, dY,
+                       dy_bs, dX, dx_bs, C, L);
+    return launch_check(ctx, "pad_bwd");
+}
+
+int kdec_nearest2x_fwd(kdec_ctx* ctx, const float* X, long x_bs, float* Y,
+                       long y_bs, int N, int C, int L) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, X && Y && N > 0 && C > 0 && L > 0, "kdec_nearest2x_fwd: bad arguments");
+    ProfScope ps(ctx, "elementwise", 0);
+    hipLaunchKernelGGL(near2_fwd_k, dim3(chunks(static_cast<long>(C) * 2 * L), N), dim3(256), 0, ctx->stream,
+                       X, x_bs, Y, y_bs, C, L);
+    return launch_check(ctx, "nearest2x_fwd");
+}
+
+int kdec_nearest2x_bwd(kdec_ctx* ctx, const float* dY, long dy_bs, float* dX,
+                       long dx_bs, int N, int C, int L, float scale,
+                       float beta) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, dY && dX && N > 0 && C > 0 && L > 0, "kdec_nearest2x_bwd: bad arguments");
+    ProfScope ps(ctx, "elementwise", 0);
+    hipLaunchKernelGGL(near2_bwd_k, dim3(chunks(static_cast<long>(C) * L), N), dim3(256), 0, ctx->stream, dY,
+                       dy_bs, dX, dx_bs, C, L, scale, beta);
+    return launch_check(ctx, "nearest2x_bwd");
+}
+
+}  // extern "C"

@@ -1,0 +1,418 @@
+// Spectral head (polar exp/sin -> iSTFT) forward and adjoint, the harmonic
+// source, and the style projection (gamma, beta) = fc(style) with its adjoint.
+//
+// iSTFT semantics (center, not normalized, onesided; torch.istft): frame f
+// contributes window * irfft(spec[f]) at offset f*hop, the overlap-add is
+// divided by the summed squared window and the first n_fft/2 samples are
+// dropped. irfft ignores the imaginary parts of the DC and Nyquist bins.
+// The transforms are n_fft = 20 direct sums with twiddles staged in LDS:
+// far too small for an FFT to pay, and direct sums keep the order fixed.
+#include "kdec_internal.hpp"
+
+#include <cmath>
+#include <vector>
+
+namespace kdec {
+namespace {
+
+constexpr int MAXN = 64;  // largest n_fft supported by the LDS tables
+constexpr int FT = 256;   // frames per block
+
+__device__ inline float hann_at(int n, int N) {
+    // periodic Hann in float arithmetic (kokoro_decoder_backward.cpp:580-588)
+    const float kTwoPi = 6.28318530717958647692f;
+    return 0.5f - 0.5f * cosf(kTwoPi * static_cast<float>(n) / static_cast<float>(N));
+}
+
+// Twiddles cos/sin(2*pi*k*n/N) for k < F, n < N (exact reduction of k*n mod N)
+// and the window (periodic Hann when `window` is null).
+__device__ inline void load_twiddles(float* tc, float* ts, float* win, int N, int F,
+                                     const float* window) {
+    for (int i = threadIdx.x; i < F * N; i += blockDim.x) {
+        const int k = i / N, n = i - k * N;
+        const int r = (k * n) % N;
+        double sv, cv;
+        sincospi(2.0 * r / N, &sv, &cv);
+        tc[i] = static_cast<float>(cv);
+        ts[i] = static_cast<float>(sv);
+    }
+    for (int n = threadIdx.x; n < N; n += blockDim.x) win[n] = window ? window[n] : hann_at(n, N);
+}
+
+// Squared-window overlap at ola position m (frames 0..frames-1, hop).
+__device__ inline float env_at(const float* win, int m, int N, int hop, int frames) {
+    int f_hi = m / hop;
+    if (f_hi > frames - 1) f_hi = frames - 1;
+    float e = 0.0f;
+    for (int f = f_hi; f >= 0 && m - f * hop < N; --f) {
+        const float w = win[m - f * hop];
+        e += w * w;
+    }
+    return e;
+}
+
+// Per (n, frame): polar spectrum -> windowed irfft frame (N samples).
+__global__ __launch_bounds__(FT) void spec_frames_k(const float* post, long post_bs,
+                                                   const float* window, float* fbuf, int L, int N) {
+    __shared__ float tc[MAXN / 2 + 1][MAXN], ts[MAXN / 2 + 1][MAXN], win[MAXN];
+    const int F = N / 2 + 1;
+    load_twiddles(&tc[0][0], &ts[0][0], win, N, F, window);
+    __syncthreads();
+    // load_twiddles wrote F*N contiguous values; index them as [k*N + n]
+    const float* TC = &tc[0][0];
+    const float* TS = &ts[0][0];
+    const int b = blockIdx.y;
+    const int f = blockIdx.x * FT + threadIdx.x;
+    if (f >= L) return;
+    const float* P = post + b * post_bs;
+    float re[MAXN / 2 + 1], im[MAXN / 2 + 1];
+    for (int k = 0; k < F; ++k) {
+        const float mag = expf(P[static_cast<long>(k) * L + f]);
+        const float ang = sinf(P[static_cast<long>(F + k) * L + f]);
+        re[k] = mag * cosf(ang);
+        im[k] = mag * sinf(ang);
+    }
+    float* out = fbuf + (static_cast<long>(b) * L + f) * N;
+    const float invN = 1.0f / N;
+    for (int n = 0; n < N; ++n) {
+        float acc = re[0];
+        if ((N & 1) == 0) acc += (n & 1) ? -re[F - 1] : re[F - 1];
+        const int kmax = (N & 1) == 0 ? F - 1 : F;
+        for (int k = 1; k < kmax; ++k)
+            acc += 2.0f * (re[k] * TC[k * N + n] - im[k] * TS[k * N + n]);
+        out[n] = acc * invN * win[n];
+    }
+}
+
+// Per output sample: overlap-add of <= ceil(N/hop) frames over the envelope.
+__global__ void spec_ola_k(const float* fbuf, const float* window, float* audio, long audio_bs, int L,
+                           int N, int hop, int sig_len) {
+    __shared__ float win[MAXN];
+    for (int n = threadIdx.x; n < N; n += blockDim.x) win[n] = window ? window[n] : hann_at(n, N);
+    __syncthreads();
+    const int b = blockIdx.y;
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= sig_len) return;
+    const int m = j + N / 2;
+    int f_hi = m / hop;
+    if (f_hi > L - 1) f_hi = L - 1;
+    float acc = 0.0f, e = 0.0f;
+    const float* fb = fbuf + static_cast<long>(b) * L * N;
+    for (int f = f_hi; f >= 0 && m - f * hop < N; --f) {
+        const int i = m - f * hop;
+        acc += fb[static_cast<long>(f) * N + i];
+        e += win[i] * win[i];
+    }
+    audio[b * audio_bs + j] = acc / e;
+}
+
+// Per (n, frame): adjoint of the frame's windowed irfft and of the polar map.
+__global__ __launch_bounds__(FT) void spec_bwd_k(const float* post, long post_bs, const float* window,
+                                                const float* daudio, long da_bs, float* dpost,
+                                                long dp_bs, int L, int N, int hop) {
+    __shared__ float tc[MAXN / 2 + 1][MAXN], ts[MAXN / 2 + 1][MAXN], win[MAXN];
+    const int F = N / 2 + 1;
+    load_twiddles(&tc[0][0], &ts[0][0], win, N, F, window);
+    __syncthreads();
+    const float* TC = &tc[0][0];
+    const float* TS = &ts[0][0];
+    const int b = blockIdx.y;
+    const int f = blockIdx.x * FT + threadIdx.x;
+    if (f >= L) return;
+    const int sig_len = (L - 1) * hop;
+    const float* dy = daudio + b * da_bs;
+    float dfr[MAXN];
+    const float invN = 1.0f / N;
+    for (int n = 0; n < N; ++n) {
+        const int m = f * hop + n;
+        const int j = m - N / 2;
+        float v = 0.0f;
+        if (j >= 0 && j < sig_len) v = dy[j] / env_at(win, m, N, hop, L);
+        dfr[n] = v * win[n] * invN;
+    }
+    const float* P = post + b * post_bs;
+    float* D = dpost + b * dp_bs;
+    for (int k = 0; k < F; ++k) {
+        const bool edge = (k == 0) || ((N & 1) == 0 && k == F - 1);
+        const float c = edge ? 1.0f : 2.0f;
+        float re = 0.0f, im = 0.0f;
+        for (int n = 0; n < N; ++n) {
+            re += dfr[n] * TC[k * N + n];
+            im -= dfr[n] * TS[k * N + n];
+        }
+        const float dRe = c * re;
+        const float dIm = edge ? 0.0f : c * im;
+        const float pm = P[static_cast<long>(k) * L + f];
+        const float pp = P[static_cast<long>(F + k) * L + f];
+        const float mag = expf(pm);
+        const float ang = sinf(pp);
+        const float ca = cosf(ang), sa = sinf(ang);
+        const float dmag = dRe * ca + dIm * sa;
+        const float dang = mag * (-dRe * sa + dIm * ca);
+        D[static_cast<long>(k) * L + f] = dmag * mag;
+        D[static_cast<long>(F + k) * L + f] = dang * cosf(pp);
+    }
+}
+
+// ─── harmonic source ───
+// One lane per (utterance, harmonic): the reference's sequential float phase
+// recurrence (kokoro_modules.cpp:1602-1617), evaluated with contraction off so
+// each step rounds exactly as the host loop does.
+__global__ void hs_phase_k(const float* F0, long f0_bs, float* phase, int N, int H, int frame_count,
+                           int us, int sig_len, float sr) {
+#pragma clang fp contract(off)
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N * H) return;
+    const int b = i / H, h = i - b * H;
+    const float kTwoPi = 6.28318530717958647692f;
+    const float* f0r = F0 + b * f0_bs;
+    float* out = phase + static_cast<long>(i) * sig_len;
+    float ph = 0.0f;
+    for (int fr = 0; fr * us < sig_len; ++fr) {
+        const float f0 = f0r[fr < frame_count ? fr : frame_count - 1];
+        float omega = kTwoPi * static_cast<float>(h + 1);
+        omega = omega * f0;
+        omega = omega / sr;
+        const int t1 = min((fr + 1) * us, sig_len);
+        for (int t = fr * us; t < t1; ++t) {
+            ph = ph + omega;
+            if (ph > kTwoPi) ph = ph - kTwoPi;
+            out[t] = ph;
+        }
+    }
+}
+
+// merged[b, t] = tanh(lb + sum_h lW[h] * sin(phase) * amp * uv)
+__global__ void hs_merge_k(const float* phase, const float* F0, long f0_bs, const float* lW,
+                           const float* lb, float* merged, int H, int frame_count, int us,
+                           int sig_len) {
+#pragma clang fp contract(off)
+    const int b = blockIdx.y;
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= sig_len) return;
+    const int fr = t / us;
+    const float f0 = F0[b * f0_bs + (fr < frame_count ? fr : frame_count - 1)];
+    const float uv = f0 > 0.0f ? 1.0f : 0.0f;
+    double acc = lb[0];
+    for (int h = 0; h < H; ++h) {
+        const float ph = phase[(static_cast<long>(b) * H + h) * sig_len + t];
+        float sv = static_cast<float>(sin(static_cast<double>(ph)));
+        sv = sv * 0.1f;
+        sv = sv * uv;
+        acc += static_cast<double>(lW[h]) * sv;
+    }
+    merged[static_cast<long>(b) * sig_len + t] =
+        static_cast<float>(tanh(static_cast<double>(static_cast<float>(acc))));
+}
+
+// STFT (center, reflect pad) -> har[b, k, f] = |X|, har[b, F+k, f] = atan2
+__global__ __launch_bounds__(FT) void hs_stft_k(const float* merged, float* har, long har_bs,
+                                               int sig_len, int N, int hop, int frames) {
+    __shared__ float tc[MAXN / 2 + 1][MAXN], ts[MAXN / 2 + 1][MAXN], win[MAXN];
+    const int F = N / 2 + 1;
+    load_twiddles(&tc[0][0], &ts[0][0], win, N, F, nullptr);
+    __syncthreads();
+    const float* TC = &tc[0][0];
+    const float* TS = &ts[0][0];
+    const int b = blockIdx.y;
+    const int f = blockIdx.x * FT + threadIdx.x;
+    if (f >= frames) return;
+    const float* x = merged + static_cast<long>(b) * sig_len;
+    const int pad = N / 2;
+    float v[MAXN];
+    for (int n = 0; n < N; ++n) {
+        int j = f * hop + n - pad;
+        if (j < 0) j = -j;
+        if (j >= sig_len) j = 2 * (sig_len - 1) - j;
+        v[n] = win[n] * x[j];
+    }
+    float* out = har + b * har_bs;
+    for (int k = 0; k < F; ++k) {
+        double re = 0.0, im = 0.0;
+        for (int n = 0; n < N; ++n) {
+            re += static_cast<double>(v[n]) * TC[k * N + n];
+            im -= static_cast<double>(v[n]) * TS[k * N + n];
+        }
+        const float ref = static_cast<float>(re), imf = static_cast<float>(im);
+        out[static_cast<long>(k) * frames + f] =
+            static_cast<float>(sqrt(static_cast<double>(ref) * ref + static_cast<double>(imf) * imf));
+        out[static_cast<long>(F + k) * frames + f] = static_cast<float>(atan2(static_cast<double>(imf),
+                                                                             static_cast<double>(ref)));
+    }
+}
+
+// ─── style projection ───
+// out[n, r] = W[r, :] . style[n, :] + b[r]; one wave per (r, n).
+__global__ void style_fwd_k(const float* W, const float* bias, const float* style, long s_bs,
+                            float* out, long o_bs, int N, int rows, int S) {
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    if (wave >= rows * N) return;
+    const int r = wave / N, n = wave - r * N;
+    const float* w = W + static_cast<long>(r) * S;
+    const float* s = style + n * s_bs;
+    double acc = 0.0;
+    for (int j = lane; j < S; j += 64) acc += static_cast<double>(w[j]) * s[j];
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_down(acc, o, 64);
+    if (lane == 0) out[n * o_bs + r] = static_cast<float>(acc + (bias ? bias[r] : 0.0f));
+}
+
+// partial[blk, n, j] = sum_{r in block rows} W[r, j] dout[n, r]
+constexpr int SR = 128;  // rows per block
+__global__ void style_bwd_x_k(const float* W, const float* dout, long d_bs, float* part, int N,
+                              int rows, int S) {
+    const int blk = blockIdx.x;
+    const int r0 = blk * SR, r1 = min(r0 + SR, rows);
+    for (int nj = threadIdx.x; nj < N * S; nj += blockDim.x) {
+        const int n = nj / S, j = nj - n * S;
+        double acc = 0.0;
+        for (int r = r0; r < r1; ++r)
+            acc += static_cast<double>(W[static_cast<long>(r) * S + j]) * dout[n * d_bs + r];
+        part[(static_cast<long>(blk) * N + n) * S + j] = static_cast<float>(acc);
+    }
+}
+
+__global__ void style_bwd_x_reduce(const float* part, int nblk, float* dstyle, long ds_bs, float beta,
+                                   int N, int S) {
+    const int nj = blockIdx.x * blockDim.x + threadIdx.x;
+    if (nj >= N * S) return;
+    const int n = nj / S, j = nj - n * S;
+    double acc = 0.0;
+    for (int q = 0; q < nblk; ++q) acc += part[static_cast<long>(q) * N * S + nj];
+    float* d = dstyle + n * ds_bs + j;
+    *d = static_cast<float>(acc) + (beta != 0.0f ? beta * *d : 0.0f);
+}
+
+// dW[r, j] += sum_n dout[n, r] style[n, j];  db[r] += sum_n dout[n, r]
+__global__ void style_bwd_w_k(const float* style, long s_bs, const float* dout, long d_bs, float* dW,
+                              float* db, int N, int rows, int S) {
+    const long tot = static_cast<long>(rows) * S;
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < tot;
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        const int r = static_cast<int>(i / S), j = static_cast<int>(i - static_cast<long>(r) * S);
+        double acc = 0.0, accb = 0.0;
+        for (int n = 0; n < N; ++n) {
+            const double g = dout[n * d_bs + r];
+            acc += g * style[n * s_bs + j];
+            accb += g;
+        }
+        dW[i] += static_cast<float>(acc);
+        if (db && j == 0) db[r] += static_cast<float>(accb);
+    }
+}
+
+unsigned g1(long n, long per = 256, long cap = 65535) {
+    long g = (n + per - 1) / per;
+    if (g > cap) g = cap;
+    if (g < 1) g = 1;
+    return static_cast<unsigned>(g);
+}
+
+}  // namespace
+}  // namespace kdec
+
+using namespace kdec;
+
+extern "C" {
+
+int kdec_spectral_fwd(kdec_ctx* ctx, const float* post, long post_bs,
+                      const float* window, float* audio, long audio_bs, int N,
+                      int L, int n_fft, int hop) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, post && audio && N > 0 && L > 1 && n_fft >= 2 && n_fft <= MAXN && hop > 0 && hop <= n_fft,
+               "kdec_spectral_fwd: bad arguments");
+    const int sig = (L - 1) * hop;
+    Workspace fb(ctx, static_cast<size_t>(N) * L * n_fft * sizeof(float));
+    if (!fb.p) return KDEC_ENOMEM;
+    ProfScope ps(ctx, "spectral", 0);
+    hipLaunchKernelGGL(spec_frames_k, dim3(static_cast<unsigned>(cdiv(L, FT)), N), dim3(FT), 0, ctx->stream,
+                       post, post_bs, window, fb.as<float>(), L, n_fft);
+    if (int rc = launch_check(ctx, "spec_frames")) return rc;
+    hipLaunchKernelGGL(spec_ola_k, dim3(static_cast<unsigned>(cdiv(sig, 256)), N), dim3(256), 0, ctx->stream,
+                       fb.as<float>(), window, audio, audio_bs, L, n_fft, hop, sig);
+    return launch_check(ctx, "spec_ola");
+}
+
+int kdec_spectral_bwd(kdec_ctx* ctx, const float* post, long post_bs,
+                      const float* window, const float* daudio,
+                      long daudio_bs, float* dpost, long dpost_bs, int N,
+                      int L, int n_fft, int hop) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, post && daudio && dpost && N > 0 && L > 1 && n_fft >= 2 && n_fft <= MAXN && hop > 0 &&
+                        hop <= n_fft,
+               "kdec_spectral_bwd: bad arguments");
+    ProfScope ps(ctx, "spectral", 0);
+    hipLaunchKernelGGL(spec_bwd_k, dim3(static_cast<unsigned>(cdiv(L, FT)), N), dim3(FT), 0, ctx->stream, post,
+                       post_bs, window, daudio, daudio_bs, dpost, dpost_bs, L, n_fft, hop);
+    return launch_check(ctx, "spec_bwd");
+}
+
+int kdec_harmonic_source(kdec_ctx* ctx, const float* F0, long f0_bs,
+                         float* har, long har_bs, int N, int frame_count,
+                         const float* lW, const float* lb, int harmonic_num,
+                         int sample_rate, int upsample_scale, int n_fft,
+                         int hop) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, F0 && har && lW && lb && N > 0 && frame_count > 0 && harmonic_num >= 0 && sample_rate > 0 &&
+                        upsample_scale > 0 && n_fft >= 2 && n_fft <= MAXN && hop > 0,
+               "kdec_harmonic_source: bad arguments");
+    const int H = harmonic_num + 1;
+    const int sig = frame_count * upsample_scale;
+    KDEC_CHECK(ctx, sig > n_fft / 2, "kdec_harmonic_source: signal shorter than the STFT pad");
+    const int frames = sig / hop + 1;
+    KDEC_CHECK(ctx, har_bs >= static_cast<long>(n_fft + 2) * frames, "kdec_harmonic_source: har stride too small");
+    Workspace ph(ctx, static_cast<size_t>(N) * H * sig * sizeof(float));
+    Workspace mg(ctx, static_cast<size_t>(N) * sig * sizeof(float));
+    if (!ph.p || !mg.p) return KDEC_ENOMEM;
+    ProfScope ps(ctx, "harmonic_source", 0);
+    hipLaunchKernelGGL(hs_phase_k, dim3(static_cast<unsigned>(cdiv(N * H, 64))), dim3(64), 0, ctx->stream, F0,
+                       f0_bs, ph.as<float>(), N, H, frame_count, upsample_scale, sig,
+                       static_cast<float>(sample_rate));
+    if (int rc = launch_check(ctx, "hs_phase")) return rc;
+    hipLaunchKernelGGL(hs_merge_k, dim3(static_cast<unsigned>(cdiv(sig, 256)), N), dim3(256), 0, ctx->stream,
+                       ph.as<float>(), F0, f0_bs, lW, lb, mg.as<float>(), H, frame_count, upsample_scale, sig);
+    if (int rc = launch_check(ctx, "hs_merge")) return rc;
+    hipLaunchKernelGGL(hs_stft_k, dim3(static_cast<unsigned>(cdiv(frames, FT)), N), dim3(FT), 0, ctx->stream,
+                       mg.as<float>(), har, har_bs, sig, n_fft, hop, frames);
+    return launch_check(ctx, "hs_stft");
+}
+
+int kdec_style_proj_fwd(kdec_ctx* ctx, const float* W, const float* b,
+                        const float* style, long style_bs, float* out,
+                        long out_bs, int N, int rows, int S) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, W && style && out && N > 0 && rows > 0 && S > 0, "kdec_style_proj_fwd: bad arguments");
+    ProfScope ps(ctx, "style_proj", 0);
+    const long waves = static_cast<long>(rows) * N;
+    hipLaunchKernelGGL(style_fwd_k, dim3(static_cast<unsigned>(cdiv(waves * 64, 256))), dim3(256), 0,
+                       ctx->stream, W, b, style, style_bs, out, out_bs, N, rows, S);
+    return launch_check(ctx, "style_proj_fwd");
+}
+
+int kdec_style_proj_bwd(kdec_ctx* ctx, const float* W, const float* style,
+                        long style_bs, const float* dout, long dout_bs,
+                        float* dstyle, long dstyle_bs, float beta, float* dW,
+                        float* db, int N, int rows, int S) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, W && style && dout && N > 0 && rows > 0 && S > 0, "kdec_style_proj_bwd: bad arguments");
+    ProfScope ps(ctx, "style_proj", 0);
+    if (dstyle) {
+        const int nblk = static_cast<int>(cdiv(rows, SR));
+        Workspace part(ctx, static_cast<size_t>(nblk) * N * S * sizeof(float));
+        if (!part.p) return KDEC_ENOMEM;
+        hipLaunchKernelGGL(style_bwd_x_k, dim3(nblk), dim3(256), 0, ctx->stream, W, dout, dout_bs,
+                           part.as<float>(), N, rows, S);
+        if (int rc = launch_check(ctx, "style_bwd_x")) return rc;
+        hipLaunchKernelGGL(style_bwd_x_reduce, dim3(static_cast<unsigned>(cdiv(N * S, 256))), dim3(256), 0,
+                           ctx->stream, part.as<float>(), nblk, dstyle, dstyle_bs, beta, N, S);
+        if (int rc = launch_check(ctx, "style_bwd_x_reduce")) return rc;
+    }
+    if (dW) {
+        hipLaunchKernelGGL(style_bwd_w_k, dim3(g1(static_cast<long>(rows) * S)), dim3(256), 0, ctx->stream,
+                           style, style_bs, dout, dout_bs, dW, db, N, rows, S);
+        if (int rc = launch_check(ctx, "style_bwd_w")) return rc;
+    }
+    return KDEC_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,234 @@
+"""ctypes binding of libkdec.so (the gfx950 kernels, the C ABI and the C++
+drop-in layer). Torch supplies device memory and the stream; every compute
+call goes through the C ABI. There is no fallback: if the library is missing
+or no HIP device is present, construction fails loudly."""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libkdec.so")
+
+ROOT = os.path.dirname(HERE)
+HEADERS = [os.path.join(ROOT, "include", "kdec.h"), os.path.join(ROOT, "include", "kdec_model.h")]
+
+
+def _ctype(decl: str):
+    """ctypes type for a C declaration's type part (pointer-sized for any pointer)."""
+    d = decl.replace("const", " ").strip()
+    if "*" in d:
+        return ctypes.c_char_p if d.replace("*", "").split() == ["char"] else ctypes.c_void_p
+    base = d.split()[-1] if d.split() else d
+    return {"int": ctypes.c_int, "long": ctypes.c_long, "float": ctypes.c_float,
+            "double": ctypes.c_double, "size_t": ctypes.c_size_t, "void": None}[base]
+
+
+def parse_headers(paths=HEADERS) -> dict:
+    """{name: (restype, [argtypes])} for every function the C headers declare."""
+    import re
+    sigs = {}
+    for path in paths:
+        with open(path) as f:
+            text = f.read()
+        text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+        text = re.sub(r"//[^\n]*", " ", text)
+        for m in re.finditer(r"([A-Za-z_][\w\s\*]*?)\b(kdec_\w+)\s*\(([^)]*)\)\s*;", text):
+            ret, name, params = m.group(1), m.group(2), m.group(3).strip()
+            args = []
+            if params and params != "void":
+                for prm in params.split(","):
+                    prm = prm.strip()
+                    mm = re.match(r"(.*?)([A-Za-z_]\w*)$", prm)
+                    args.append(_ctype(mm.group(1) if mm and mm.group(1).strip() else prm))
+            sigs[name] = (_ctype(ret), args)
+    return sigs
+
+
+_lib = None
+
+
+def exported_symbols():
+    return list(parse_headers())
+
+
+def lib():
+    """Loads libkdec.so; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m brosoundml_amd.build`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in parse_headers().items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def ptr(t):
+    """Device (or host) address of a torch tensor, or None."""
+    if t is None:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+class KdecError(RuntimeError):
+    pass
+
+
+class Context:
+    """A kdec context bound to torch's current stream on `device`."""
+
+    def __init__(self, device: int = 0, stream=None):
+        import torch
+        if not torch.cuda.is_available():
+            raise KdecError("no HIP device: the gfx950 library has no CPU path")
+        self.L = lib()
+        h = ctypes.c_void_p()
+        rc = self.L.kdec_ctx_create(device, ctypes.byref(h))
+        if rc != 0:
+            raise KdecError(f"kdec_ctx_create failed ({rc})")
+        self.h = h
+        self.device = device
+        s = stream if stream is not None else torch.cuda.current_stream(device)
+        self.check(self.L.kdec_set_stream(self.h, ctypes.c_void_p(s.cuda_stream)))
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.kdec_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def check(self, rc):
+        if rc != 0:
+            raise KdecError(self.L.kdec_last_error(self.h).decode())
+        return rc
+
+    def call(self, name, *args):
+        return self.check(getattr(self.L, name)(self.h, *args))
+
+    def synchronize(self):
+        self.call("kdec_synchronize")
+
+    # profiling
+    def profile(self, on=True):
+        self.call("kdec_profile_enable", int(on))
+
+    def profile_reset(self):
+        self.call("kdec_profile_reset")
+
+    def profile_read(self):
+        cap = 64
+        names = (ctypes.c_char_p * cap)()
+        ms = (ctypes.c_double * cap)()
+        launches = (ctypes.c_long * cap)()
+        flops = (ctypes.c_double * cap)()
+        n = self.L.kdec_profile_read(self.h, ctypes.cast(names, ctypes.c_void_p),
+                                     ctypes.cast(ms, ctypes.c_void_p),
+                                     ctypes.cast(launches, ctypes.c_void_p),
+                                     ctypes.cast(flops, ctypes.c_void_p), cap)
+        if n < 0:
+            raise KdecError(self.L.kdec_last_error(self.h).decode())
+        return {names[i].decode(): dict(ms=ms[i], launches=launches[i], flops=flops[i])
+                for i in range(min(n, cap))}
+
+
+def config_ints(cfg: dict) -> list[int]:
+    from .config import flat_ints
+    return flat_ints(cfg)
+
+
+class Model:
+    """The whole decoder (kdec_model.h) on a Context."""
+
+    def __init__(self, ctx: Context, cfg: dict):
+        self.ctx = ctx
+        self.cfg = cfg
+        v = config_ints(cfg)
+        arr = (ctypes.c_int * len(v))(*v)
+        h = ctypes.c_void_p()
+        rc = ctx.L.kdec_model_create(ctx.h, ctypes.cast(arr, ctypes.c_void_p), len(v), ctypes.byref(h))
+        if rc != 0:
+            raise KdecError(f"kdec_model_create failed ({rc})")
+        self.h = h
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.ctx.L.kdec_model_destroy(self.h)
+            self.h = None
+
+    def _c(self, rc):
+        return self.ctx.check(rc)
+
+    def param_shapes(self) -> dict:
+        L = self.ctx.L
+        out = {}
+        for i in range(L.kdec_model_param_count(self.h)):
+            name = L.kdec_model_param_name(self.h, i)
+            r, c = ctypes.c_int(), ctypes.c_int()
+            self._c(L.kdec_model_param_shape(self.h, name, ctypes.cast(ctypes.pointer(r), ctypes.c_void_p),
+                                             ctypes.cast(ctypes.pointer(c), ctypes.c_void_p)))
+            out[name.decode()] = (r.value, c.value)
+        return out
+
+    def units(self) -> list:
+        L = self.ctx.L
+        return [(L.kdec_model_unit_name(self.h, i).decode(), L.kdec_model_unit_channels(self.h, i),
+                 L.kdec_model_unit_offset(self.h, i)) for i in range(L.kdec_model_unit_count(self.h))]
+
+    def affine_rows(self) -> int:
+        return self.ctx.L.kdec_model_affine_rows(self.h)
+
+    def set_params(self, params: dict):
+        import numpy as np
+        for name, v in params.items():
+            a = np.ascontiguousarray(v, dtype=np.float32).ravel()
+            self._c(self.ctx.L.kdec_model_set_param(self.h, name.encode(), a.ctypes.data_as(ctypes.c_void_p),
+                                                    a.size))
+
+    def grad(self, name: str, shape):
+        import numpy as np
+        g = np.zeros(int(np.prod(shape)), np.float32)
+        self._c(self.ctx.L.kdec_model_get_grad(self.h, name.encode(), g.ctypes.data_as(ctypes.c_void_p), g.size))
+        return g
+
+    def zero_grad(self):
+        self._c(self.ctx.L.kdec_model_zero_grad(self.h))
+
+    def lengths(self, T):
+        a, b, c = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        self._c(self.ctx.L.kdec_model_lengths(self.h, T, ctypes.cast(ctypes.pointer(a), ctypes.c_void_p),
+                                              ctypes.cast(ctypes.pointer(b), ctypes.c_void_p),
+                                              ctypes.cast(ctypes.pointer(c), ctypes.c_void_p)))
+        return dict(L_gen=a.value, frames=b.value, audio=c.value)
+
+    def forward(self, asr, F0, Nn, style, T, har=None, audio=None):
+        import torch
+        N = asr.shape[0]
+        if audio is None:
+            audio = torch.empty(N, self.lengths(T)["audio"], device=asr.device, dtype=torch.float32)
+        self._c(self.ctx.L.kdec_model_forward(self.h, N, T, ptr(asr), ptr(F0), ptr(Nn), ptr(style), ptr(har),
+                                              ptr(audio)))
+        return audio
+
+    def backward(self, daudio, wgrad=True, dalpha=True, dstyle=None):
+        self._c(self.ctx.L.kdec_model_backward(self.h, ptr(daudio), int(wgrad), int(dalpha), ptr(dstyle)))
+
+    def affines(self, N):
+        import numpy as np
+        R = self.affine_rows()
+        gb = np.zeros(N * R, np.float32)
+        dgb = np.zeros(N * R, np.float32)
+        self._c(self.ctx.L.kdec_model_get_affines(self.h, gb.ctypes.data_as(ctypes.c_void_p),
+                                                  dgb.ctypes.data_as(ctypes.c_void_p)))
+        return gb.reshape(N, R), dgb.reshape(N, R)
+
+    def har_ptr(self):
+        return self.ctx.L.kdec_model_har(self.h)

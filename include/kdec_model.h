@@ -1,0 +1,94 @@
+/*
+ * kdec_model.h — C ABI over the whole decoder back half (style projection,
+ * DecoderBackbone, harmonic source, Generator, spectral head) for N
+ * utterances at once, built on the C++ drop-in atoms of
+ * kokoro_decoder_backward.h.
+ *
+ * It stands in for the sequence DecoderLora::forward / ::backward runs
+ * (src/decoder_lora.cpp:211-296) with the LoRA term absent: the per-AdaIN
+ * style projection (gamma, beta) = fc(style) (kokoro_modules.cpp:563-572),
+ * decoder_backbone_forward_train / generator_forward_train, then
+ * generator_backward / decoder_backbone_backward and the projection's
+ * adjoint. The harmonic source runs first, as in decode_back_half
+ * (kokoro.cpp:369-383).
+ *
+ * Parameters are addressed by the upstream state-dict names the reference's
+ * loaders read (kokoro_modules.cpp:1021-1063, 1147-1195, 1237-1347,
+ * 1556-1572), e.g. "decoder.module.generator.resblocks.3.convs1.1.weight",
+ * with the reference's layouts. All parameters live in one device buffer
+ * and all grads in another.
+ *
+ * Activations cross this ABI as DEVICE pointers (the caller owns them and
+ * keeps forward inputs alive until backward returns); parameters and grads
+ * can be copied from / to host memory. Same error convention as kdec.h.
+ */
+#ifndef KDEC_MODEL_H
+#define KDEC_MODEL_H
+
+#include "kdec.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct kdec_model kdec_model;
+
+/* cfg: the decoder configuration as flat ints, in this order:
+ *   asr_dim, asr_res_dim, style_dim, enc_dim, n_decode, dec_out[8],
+ *   dec_up_at, n_ups, ups_rates[4], ups_kernels[4], n_kernels,
+ *   rb_kernels[4], rb_dil[4][3], n_fft, hop, conv_post_k, sample_rate,
+ *   harmonic_num
+ * (Kokoro-82M: 512, 64, 128, 1024, 4, {1024,1024,1024,512}, 3, 2, {10,6},
+ *  {20,12}, 3, {3,7,11}, {1,3,5}x3, 20, 5, 7, 24000, 8). Parameters start at
+ * zero. The context must outlive the model. */
+int kdec_model_create(kdec_ctx* ctx, const int* cfg, int n_cfg, kdec_model** out);
+int kdec_model_destroy(kdec_model* m);
+
+int kdec_model_param_count(const kdec_model* m);
+const char* kdec_model_param_name(const kdec_model* m, int i);
+int kdec_model_param_shape(const kdec_model* m, const char* name, int* rows, int* cols);
+/* Host copies (synchronous). */
+int kdec_model_set_param(kdec_model* m, const char* name, const float* host, long n);
+int kdec_model_get_param(kdec_model* m, const char* name, float* host, long n);
+int kdec_model_get_grad(kdec_model* m, const char* name, float* host, long n);
+/* Device pointers into the parameter / grad buffers. */
+float* kdec_model_param_ptr(kdec_model* m, const char* name);
+float* kdec_model_grad_ptr(kdec_model* m, const char* name);
+long kdec_model_param_total(const kdec_model* m);  /* total parameter count */
+int kdec_model_zero_grad(kdec_model* m);
+
+/* AdaIN units in canonical order (backbone, noise_res, resblocks). Unit i's
+ * gamma for utterance n is affine[n * rows_total + offset + c], beta follows
+ * at + C; the affine grads use the same layout. */
+int kdec_model_unit_count(const kdec_model* m);
+const char* kdec_model_unit_name(const kdec_model* m, int i);
+int kdec_model_unit_channels(const kdec_model* m, int i);
+int kdec_model_unit_offset(const kdec_model* m, int i);
+int kdec_model_affine_rows(const kdec_model* m);
+/* Host copies of the last forward's affines / last backward's affine grads
+ * (N * rows_total floats each; either pointer may be NULL). */
+int kdec_model_get_affines(kdec_model* m, float* gb, float* dgb);
+
+/* Per-utterance lengths for T asr frames. */
+int kdec_model_lengths(const kdec_model* m, int T, int* L_gen, int* frames, int* audio_len);
+
+/* Forward for N utterances of T frames: asr (N, asr_dim*T), F0 / Nn (N, 2T),
+ * style (N, style_dim) -> audio (N, audio_len). har_in (N, (n_fft+2)*frames)
+ * replaces the harmonic source output when non-NULL. */
+int kdec_model_forward(kdec_model* m, int N, int T, const float* asr, const float* F0,
+                       const float* Nn, const float* style, const float* har_in, float* audio);
+/* Backward of the last forward. wgrad: accumulate every conv / conv-transpose
+ * / pool / style-fc weight and bias grad; dalpha: accumulate the Snake alpha
+ * grads; dstyle (N, style_dim) may be NULL. The affine grads are always
+ * produced (the reference semantics). */
+int kdec_model_backward(kdec_model* m, const float* daudio, int wgrad, int dalpha, float* dstyle);
+/* Device pointers to the last forward's har (N, (n_fft+2)*frames) and
+ * generator input (N, init_C * L_gen). */
+const float* kdec_model_har(const kdec_model* m);
+const float* kdec_model_gen_in(const kdec_model* m);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KDEC_MODEL_H */

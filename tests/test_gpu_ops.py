@@ -1,0 +1,356 @@
+"""GPU parity of every kdec kernel family against the CPU oracle.
+
+Each test draws seeded inputs, runs the HIP kernel through the C ABI (torch
+only provides device memory and the stream) and the oracle's restatement of
+the reference op on the same inputs, utterance by utterance, and checks the
+relative L2 error. Tolerances: 1e-5 for forward values, 1e-4 for gradients
+(the bars the reference path's parity is stated at); the max abs error is
+reported on failure.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+FWD_TOL = 1e-5
+GRAD_TOL = 1e-4
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def assert_close(got, ref, tol, what):
+    e = rel_l2(got, ref)
+    mx = float(np.max(np.abs(np.asarray(got, np.float64).ravel() - np.asarray(ref, np.float64).ravel())))
+    assert e <= tol, f"{what}: rel-L2 {e:.3e} > {tol:.0e} (max-abs {mx:.3e})"
+
+
+@pytest.fixture(scope="module")
+def K():
+    from brosoundml_amd import native
+    return native.Context(0)
+
+
+_keep = []  # device inputs stay referenced until the test ends
+
+
+@pytest.fixture(autouse=True)
+def _release_inputs():
+    yield
+    torch.cuda.synchronize()
+    _keep.clear()
+
+
+def g(x):
+    t = torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+    _keep.append(t)
+    return t
+
+
+def h(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def P(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+rng = np.random.default_rng(20251201)
+
+
+def rnd(*shape, scale=1.0):
+    return (rng.standard_normal(shape) * scale).astype(np.float32)
+
+
+CONV = [
+    # N, C_in, C_out, L, k, s, p, d
+    (2, 3, 5, 37, 3, 1, 1, 1),
+    (2, 64, 64, 300, 11, 1, 25, 5),
+    (2, 128, 128, 777, 7, 1, 9, 3),
+    (1, 130, 200, 64, 3, 1, 1, 1),       # channel tails on both sides
+    (2, 22, 96, 241, 12, 6, 3, 1),       # noise_convs stage-0 geometry
+    (2, 40, 22, 150, 7, 1, 3, 1),        # conv_post geometry
+    (2, 90, 70, 50, 1, 1, 0, 1),         # 1x1 shortcut
+    (1, 1, 1, 16, 3, 2, 1, 1),           # F0_conv
+]
+
+
+@pytest.mark.parametrize("N,C_in,C_out,L,k,s,p,d", CONV)
+def test_conv1d_fwd_dgrad_wgrad(K, N, C_in, C_out, L, k, s, p, d):
+    Lo = O.conv1d_out_len(L, k, s, p, d)
+    x, W, b = rnd(N, C_in, L), rnd(C_out, C_in * k, scale=0.2), rnd(C_out)
+    R = rnd(N, C_out, Lo)
+    Y = torch.empty(N, C_out, Lo, device="cuda")
+    K.call("kdec_conv1d_fwd", P(g(x)), C_in * L, P(g(W)), P(g(b)), P(Y), C_out * Lo, N, C_in, L, C_out, k, s,
+           p, d, P(g(R)), C_out * Lo, 0.5, 0.0)
+    ref = np.stack([0.5 * (O.conv1d(x[n], W, b, C_in, L, C_out, k, s, p, d).reshape(C_out, Lo) + R[n])
+                    for n in range(N)])
+    assert_close(h(Y), ref, FWD_TOL, "conv1d forward")
+    dY = rnd(N, C_out, Lo)
+    if s == 1:
+        dX = torch.empty(N, C_in, L, device="cuda")
+        K.call("kdec_conv1d_dgrad", P(g(W)), P(g(dY)), C_out * Lo, P(dX), C_in * L, N, C_in, L, C_out, k, s, p,
+               d, 1.0, 0.0)
+        ref = np.stack([O.conv1d_dgrad(W, dY[n], C_in, L, C_out, k, s, p, d) for n in range(N)])
+        assert_close(h(dX), ref, GRAD_TOL, "conv1d backward_input")
+    dW = torch.zeros(C_out, C_in * k, device="cuda")
+    db = torch.zeros(C_out, device="cuda")
+    K.call("kdec_conv1d_wgrad", P(g(x)), C_in * L, P(g(dY)), C_out * Lo, P(dW), P(db), N, C_in, L, C_out, k, s,
+           p, d)
+    rW = np.zeros(C_out * C_in * k)
+    rb = np.zeros(C_out)
+    for n in range(N):
+        a, bb = O.conv1d_wgrad(x[n], dY[n], C_in, L, C_out, k, s, p, d)
+        rW += a
+        rb += bb
+    assert_close(h(dW), rW, GRAD_TOL, "conv1d backward_weight")
+    assert_close(h(db), rb, GRAD_TOL, "conv1d backward_bias")
+
+
+def test_conv1d_batch_stride_and_accumulate(K):
+    # outputs written into a channel slice of a wider tensor, beta accumulate
+    N, C_in, C_out, L, k = 2, 16, 8, 40, 3
+    x, W = rnd(N, C_in, L), rnd(C_out, C_in * k, scale=0.3)
+    Ywide = g(rnd(N, C_out + 5, L))
+    before = h(Ywide).copy()
+    Yv = Ywide[:, 2:2 + C_out]
+    K.call("kdec_conv1d_fwd", P(g(x)), C_in * L, P(g(W)), None, P(Yv), (C_out + 5) * L, N, C_in, L, C_out, k, 1,
+           1, 1, None, 0, 1.0, 1.0)
+    got = h(Ywide)
+    ref = before.copy()
+    for n in range(N):
+        ref[n, 2:2 + C_out] += O.conv1d(x[n], W, None, C_in, L, C_out, k, 1, 1, 1).reshape(C_out, L)
+    assert_close(got, ref, FWD_TOL, "strided accumulate")
+    assert np.array_equal(got[:, :2], before[:, :2]) and np.array_equal(got[:, 2 + C_out:], before[:, 2 + C_out:])
+
+
+CONVT = [
+    # N, C_in, C_out, L, k, s, p
+    (2, 64, 32, 40, 20, 10, 5),    # ups0 geometry
+    (2, 32, 16, 50, 12, 6, 3),     # ups1 geometry
+    (1, 5, 7, 13, 5, 3, 1),        # k not a multiple of s
+    (2, 6, 4, 9, 4, 2, 1),
+    (1, 3, 3, 11, 3, 1, 1),        # stride 1
+]
+
+
+@pytest.mark.parametrize("N,C_in,C_out,L,k,s,p", CONVT)
+def test_convt1d(K, N, C_in, C_out, L, k, s, p):
+    Lo = O.convt1d_out_len(L, k, s, p, 0, 1)
+    x, W, b = rnd(N, C_in, L), rnd(C_in, C_out * k, scale=0.2), rnd(C_out)
+    Y = torch.empty(N, C_out, Lo, device="cuda")
+    K.call("kdec_convt1d_fwd", P(g(x)), C_in * L, P(g(W)), P(g(b)), P(Y), C_out * Lo, N, C_in, L, C_out, k, s, p, 0)
+    ref = np.stack([O.convt1d(x[n], W, b, C_in, L, C_out, k, s, p) for n in range(N)])
+    assert_close(h(Y), ref, FWD_TOL, "conv_transpose1d forward")
+    dY = rnd(N, C_out, Lo)
+    dX = torch.empty(N, C_in, L, device="cuda")
+    K.call("kdec_convt1d_dgrad", P(g(W)), P(g(dY)), C_out * Lo, P(dX), C_in * L, N, C_in, L, C_out, k, s, p, 0)
+    ref = np.stack([O.convt1d_dgrad(W, dY[n], C_in, L, C_out, k, s, p) for n in range(N)])
+    assert_close(h(dX), ref, GRAD_TOL, "conv_transpose1d backward_input")
+    dW = torch.zeros(C_in, C_out * k, device="cuda")
+    db = torch.zeros(C_out, device="cuda")
+    K.call("kdec_convt1d_wgrad", P(g(x)), C_in * L, P(g(dY)), C_out * Lo, P(dW), P(db), N, C_in, L, C_out, k, s,
+           p, 0)
+    rW, rb = np.zeros(C_in * C_out * k), np.zeros(C_out)
+    for n in range(N):
+        a, bb = O.convt1d_wgrad(x[n], dY[n], C_in, L, C_out, k, s, p)
+        rW += a
+        rb += bb
+    assert_close(h(dW), rW, GRAD_TOL, "conv_transpose1d backward_weight")
+    assert_close(h(db), rb, GRAD_TOL, "conv_transpose1d backward_bias")
+
+
+def test_pool(K):
+    N, C, L = 2, 9, 33
+    x, W, b = rnd(N, C, L), rnd(C, 3), rnd(C)
+    Y = torch.empty(N, C, 2 * L, device="cuda")
+    K.call("kdec_pool_fwd", P(g(x)), C * L, P(g(W)), P(g(b)), P(Y), 2 * C * L, N, C, L)
+    ref = np.stack([O.convt1d(x[n], W, b, C, L, C, 3, 2, 1, 1, 1, C) for n in range(N)])
+    assert_close(h(Y), ref, FWD_TOL, "pool forward")
+    dY = rnd(N, C, 2 * L)
+    dX = torch.empty(N, C, L, device="cuda")
+    K.call("kdec_pool_dgrad", P(g(W)), P(g(dY)), 2 * C * L, P(dX), C * L, N, C, L)
+    ref = np.stack([O.convt1d_dgrad(W, dY[n], C, L, C, 3, 2, 1, 1, 1, C) for n in range(N)])
+    assert_close(h(dX), ref, GRAD_TOL, "pool backward_input")
+    dW = torch.zeros(C, 3, device="cuda")
+    db = torch.zeros(C, device="cuda")
+    K.call("kdec_pool_wgrad", P(g(x)), C * L, P(g(dY)), 2 * C * L, P(dW), P(db), N, C, L)
+    rW, rb = np.zeros(C * 3), np.zeros(C)
+    for n in range(N):
+        a, bb = O.convt1d_wgrad(x[n], dY[n], C, L, C, 3, 2, 1, 1, 1, C)
+        rW += a
+        rb += bb
+    assert_close(h(dW), rW, GRAD_TOL, "pool backward_weight")
+    assert_close(h(db), rb, GRAD_TOL, "pool backward_bias")
+
+
+ACTS = {"none": 0, "leaky": 1, "snake": 2}
+
+
+@pytest.mark.parametrize("act", ["none", "leaky", "snake"])
+@pytest.mark.parametrize("C,L", [(5, 31), (16, 4099)])
+def test_adain_act(K, act, C, L):
+    N = 2
+    x = rnd(N, C, L, scale=1.7) + 0.3
+    gm, bt = rnd(N, C, scale=0.4), rnd(N, C, scale=0.3)
+    alpha = rng.uniform(0.5, 2.0, C).astype(np.float32)
+    st = torch.empty(N * C, 2, device="cuda")
+    K.call("kdec_instnorm_stats", P(g(x)), C * L, N, C, L, 1e-5, P(st))
+    Y = torch.empty(N, C, L, device="cuda")
+    K.call("kdec_adain_act_fwd", P(g(x)), C * L, P(st), P(g(gm)), P(g(bt)), C, ACTS[act], 0.2, P(g(alpha)), P(Y),
+           C * L, None, 0, N, C, L)
+    refs = []
+    for n in range(N):
+        y = O.adain_affine(x[n], gm[n], bt[n], C, L)
+        if act == "leaky":
+            y = O.leaky(y, 0.2)
+        elif act == "snake":
+            y = O.snake(y, alpha, C, L)
+        refs.append(y)
+    assert_close(h(Y), np.stack(refs), FWD_TOL, f"adain+{act} forward")
+
+    dY = rnd(N, C, L)
+    R = rnd(N, C, L)
+    dX = torch.empty(N, C, L, device="cuda")
+    dg = torch.empty(N, C, device="cuda")
+    db = torch.empty(N, C, device="cuda")
+    da = torch.zeros(C, device="cuda")
+    K.call("kdec_adain_act_bwd", P(g(x)), C * L, P(st), P(g(gm)), P(g(bt)), C, ACTS[act], 0.2, P(g(alpha)),
+           P(g(dY)), C * L, P(g(R)), C * L, P(dX), C * L, P(dg), P(db), C, P(da), N, C, L)
+    rdx, rdg, rdb, rda = [], [], [], np.zeros(C)
+    for n in range(N):
+        s = O.adain_affine(x[n], gm[n], bt[n], C, L)
+        ds = dY[n].ravel()
+        if act == "leaky":
+            ds = O.leaky_bwd(s, ds, 0.2)
+        elif act == "snake":
+            ds, a_ = O.snake_bwd(s, alpha, ds, C, L)
+            rda += a_
+        dx, dgg, dbb = O.adain_affine_bwd(x[n], gm[n], ds, C, L)
+        rdx.append(dx + R[n].ravel())
+        rdg.append(dgg)
+        rdb.append(dbb)
+    assert_close(h(dX), np.stack(rdx), GRAD_TOL, f"adain+{act} dX")
+    assert_close(h(dg), np.stack(rdg), GRAD_TOL, f"adain+{act} dGamma")
+    assert_close(h(db), np.stack(rdb), GRAD_TOL, f"adain+{act} dBeta")
+    if act == "snake":
+        assert_close(h(da), rda, GRAD_TOL, "snake dAlpha")
+
+
+def test_elementwise(K):
+    N, C, L = 2, 3, 17
+    x = rnd(N, C, L)
+    Y = torch.empty(N, C, L + 1, device="cuda")
+    K.call("kdec_pad_reflect_left1_fwd", P(g(x)), C * L, P(Y), C * (L + 1), N, C, L)
+    assert np.array_equal(h(Y), np.stack([O.pad_reflect_left1(x[n], C, L).reshape(C, L + 1) for n in range(N)]))
+    dY = rnd(N, C, L + 1)
+    dX = torch.empty(N, C, L, device="cuda")
+    K.call("kdec_pad_reflect_left1_bwd", P(g(dY)), C * (L + 1), P(dX), C * L, N, C, L)
+    assert_close(h(dX), np.stack([O.pad_reflect_left1_bwd(dY[n], C, L) for n in range(N)]), 1e-7, "pad bwd")
+    Y2 = torch.empty(N, C, 2 * L, device="cuda")
+    K.call("kdec_nearest2x_fwd", P(g(x)), C * L, P(Y2), 2 * C * L, N, C, L)
+    assert np.array_equal(h(Y2), np.repeat(x, 2, axis=2))
+    d2 = rnd(N, C, 2 * L)
+    dx2 = torch.empty(N, C, L, device="cuda")
+    K.call("kdec_nearest2x_bwd", P(g(d2)), 2 * C * L, P(dx2), C * L, N, C, L, 1.0, 0.0)
+    assert_close(h(dx2), d2[..., 0::2] + d2[..., 1::2], 1e-7, "nearest2x bwd")
+    Yl = torch.empty(N, C * L, device="cuda")
+    K.call("kdec_leaky_fwd", P(g(x)), C * L, P(Yl), C * L, N, C * L, 0.1)
+    assert np.array_equal(h(Yl).ravel(), O.leaky(x.ravel(), 0.1))
+    F = torch.empty(1000, device="cuda")
+    K.call("kdec_fill", P(F), 1000, 3.5)
+    assert np.all(h(F) == 3.5)
+
+
+@pytest.mark.parametrize("n_fft,hop,L,C", [(20, 5, 301, 24), (8, 2, 65, 6)])
+def test_spectral_head(K, n_fft, hop, L, C):
+    N = 2
+    k = 7
+    x = rnd(N, C, L, scale=0.8)
+    W = rnd(n_fft + 2, C * k, scale=0.3 / np.sqrt(C * k))
+    b = rnd(n_fft + 2, scale=0.1)
+    xl = torch.empty(N, C * L, device="cuda")
+    K.call("kdec_leaky_fwd", P(g(x)), C * L, P(xl), C * L, N, C * L, 0.01)
+    post = torch.empty(N, n_fft + 2, L, device="cuda")
+    K.call("kdec_conv1d_fwd", P(xl), C * L, P(g(W)), P(g(b)), P(post), (n_fft + 2) * L, N, C, L, n_fft + 2, k, 1,
+           3, 1, None, 0, 1.0, 0.0)
+    S = (L - 1) * hop
+    audio = torch.empty(N, S, device="cuda")
+    K.call("kdec_spectral_fwd", P(post), (n_fft + 2) * L, None, P(audio), S, N, L, n_fft, hop)
+    ref = [O.spectral_head(x[n], C, L, W, b, k, n_fft, hop) for n in range(N)]
+    assert_close(h(audio), np.stack([r[0] for r in ref]), FWD_TOL, "spectral head forward")
+    dA = rnd(N, S)
+    dpost = torch.empty(N, n_fft + 2, L, device="cuda")
+    K.call("kdec_spectral_bwd", P(post), (n_fft + 2) * L, None, P(g(dA)), S, P(dpost), (n_fft + 2) * L, N, L, n_fft,
+           hop)
+    dxl = torch.empty(N, C, L, device="cuda")
+    K.call("kdec_conv1d_dgrad", P(g(W)), P(dpost), (n_fft + 2) * L, P(dxl), C * L, N, C, L, n_fft + 2, k, 1, 3, 1,
+           1.0, 0.0)
+    dx = torch.empty(N, C, L, device="cuda")
+    K.call("kdec_leaky_bwd", P(g(x)), C * L, P(dxl), C * L, P(dx), C * L, N, C * L, 0.01)
+    rdx = np.stack([O.spectral_head_bwd(x[n], C, L, W, b, k, n_fft, hop, dA[n])[0] for n in range(N)])
+    assert_close(h(dx), rdx, GRAD_TOL, "spectral head backward")
+
+
+def test_harmonic_source(K):
+    # F0 with unvoiced (zero) frames; magnitudes compare tightly, phases only
+    # where the bin holds energy (atan2 of a ~1e-8 bin is noise in any float
+    # evaluation, CPU or GPU).
+    N, fc, us, n_fft, hop = 2, 16, 60, 20, 5
+    F0 = rng.uniform(80, 300, (N, fc)).astype(np.float32)
+    F0[0, 3:6] = 0.0
+    F0[1, 10] = 0.0
+    lW = rnd(9, scale=0.3)
+    lb = rnd(1, scale=0.1)
+    frames = fc * us // hop + 1
+    har = torch.empty(N, n_fft + 2, frames, device="cuda")
+    K.call("kdec_harmonic_source", P(g(F0)), fc, P(har), (n_fft + 2) * frames, N, fc, P(g(lW)), P(g(lb)), 8, 24000,
+           us, n_fft, hop)
+    got = h(har)
+    F = n_fft // 2 + 1
+    for n in range(N):
+        ref, fr = O.harmonic_source(F0[n], lW, lb, 8, 24000, us, n_fft, hop)
+        assert fr == frames
+        ref = ref.reshape(2 * F, frames)
+        mag_ref, mag = ref[:F], got[n, :F]
+        assert_close(mag, mag_ref, 1e-5, "harmonic source magnitude")
+        strong = mag_ref > 1e-3 * mag_ref.max()
+        dphi = np.angle(np.exp(1j * (got[n, F:][strong].astype(np.float64) - ref[F:][strong])))
+        assert np.max(np.abs(dphi)) < 1e-3, f"phase error {np.max(np.abs(dphi))}"
+
+
+def test_style_projection(K):
+    N, rows, S = 3, 700, 128
+    W, b = rnd(rows, S, scale=0.1), rnd(rows)
+    st = rnd(N, S, scale=0.3)
+    out = torch.empty(N, rows, device="cuda")
+    K.call("kdec_style_proj_fwd", P(g(W)), P(g(b)), P(g(st)), S, P(out), rows, N, rows, S)
+    ref = st.astype(np.float64) @ W.T.astype(np.float64) + b
+    assert_close(h(out), ref, FWD_TOL, "style projection")
+    dout = rnd(N, rows)
+    dst = torch.empty(N, S, device="cuda")
+    dW = torch.zeros(rows, S, device="cuda")
+    db = torch.zeros(rows, device="cuda")
+    K.call("kdec_style_proj_bwd", P(g(W)), P(g(st)), S, P(g(dout)), rows, P(dst), S, 0.0, P(dW), P(db), N, rows, S)
+    assert_close(h(dst), dout.astype(np.float64) @ W.astype(np.float64), GRAD_TOL, "d(style)")
+    assert_close(h(dW), dout.T.astype(np.float64) @ st.astype(np.float64), GRAD_TOL, "d(fc.weight)")
+    assert_close(h(db), dout.sum(0), GRAD_TOL, "d(fc.bias)")
+
+
+def test_error_paths(K):
+    from brosoundml_amd import native
+    # shape errors are reported, not launched
+    with pytest.raises(native.KdecError, match="stride 1"):
+        K.call("kdec_conv1d_dgrad", P(g(rnd(4, 6))), P(g(rnd(1, 4, 8))), 32, P(g(rnd(1, 2, 16))), 32, 1, 2, 16, 4,
+               3, 2, 1, 1, 1.0, 0.0)
+    with pytest.raises(native.KdecError):
+        K.call("kdec_conv1d_fwd", None, 0, None, None, None, 0, 1, 1, 1, 1, 1, 1, 0, 1, None, 0, 1.0, 0.0)
