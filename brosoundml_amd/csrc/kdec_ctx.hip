@@ -51,6 +51,12 @@ void ws_free(kdec_ctx* ctx, void* p) {
     if (!p) return;
     auto it = ctx->live.find(p);
     if (it == ctx->live.end()) return;
+    if (ctx->destroyed) {
+        hipFree(p);
+        ctx->live.erase(it);
+        if (ctx->live.empty()) delete ctx;
+        return;
+    }
     ctx->pool.emplace(it->second, p);
     ctx->pooled_bytes += it->second;
     ctx->live.erase(it);
@@ -119,19 +125,27 @@ int kdec_ctx_create(int device, kdec_ctx** out) {
 }
 
 int kdec_ctx_destroy(kdec_ctx* ctx) {
-    if (!ctx) return KDEC_OK;
+    if (!ctx || ctx->destroyed) return KDEC_OK;
+    kdec::forget_runtime(ctx);
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
     for (auto& kv : ctx->pool) hipFree(kv.second);
-    for (auto& kv : ctx->live) hipFree(kv.first);
+    ctx->pool.clear();
     for (auto& f : ctx->fams)
         for (auto& pr : f.second.pending) {
             hipEventDestroy(pr.first);
             hipEventDestroy(pr.second);
         }
+    ctx->fams.clear();
     for (hipEvent_t e : ctx->event_pool) hipEventDestroy(e);
+    ctx->event_pool.clear();
     if (ctx->own_stream) hipStreamDestroy(ctx->own_stream);
-    delete ctx;
+    ctx->own_stream = nullptr;
+    ctx->stream = nullptr;
+    // Blocks still owned by live tensors are freed as those tensors go; the
+    // last one releases the context (see ws_free).
+    if (ctx->live.empty()) delete ctx;
+    else ctx->destroyed = true;
     return KDEC_OK;
 }
 

@@ -24,6 +24,9 @@ struct kdec_ctx {
     std::multimap<size_t, void*> pool;
     std::unordered_map<void*, size_t> live;
     size_t pooled_bytes = 0;
+    // Set by kdec_ctx_destroy while blocks are still live (tensors that
+    // outlive their context): the last ws_free then releases the context.
+    bool destroyed = false;
 
     // Per-kernel-family timing (HIP events on the context stream).
     struct Family {
@@ -79,6 +82,10 @@ struct ProfScope {
     ProfScope(kdec_ctx* c, const char* n, double f);
     ~ProfScope();
 };
+
+// Drops `ctx` as the C++ layer's runtime context if it is the current one
+// (defined with the brotensor runtime, tensor.cpp).
+void forget_runtime(kdec_ctx* ctx);
 
 // Checks the last launch; returns KDEC_OK or the HIP error code.
 int launch_check(kdec_ctx* ctx, const char* where);

@@ -275,7 +275,7 @@ int kdec_model_create(kdec_ctx* ctx, const int* v, int n, kdec_model** out) {
     for (int j = 0; j < 4; ++j)
         for (int q = 0; q < 3; ++q) m->rb_dil[j][q] = nx();
     m->n_fft = nx(); m->hop = nx(); m->conv_post_k = nx(); m->sample_rate = nx(); m->harmonic_num = nx();
-    if (i != n || n != 47 || m->n_decode < 1 || m->n_decode > 8 || m->n_ups < 1 || m->n_ups > 4 ||
+    if (i != n || n != 45 || m->n_decode < 1 || m->n_decode > 8 || m->n_ups < 1 || m->n_ups > 4 ||
         m->n_kernels < 1 || m->n_kernels > 4 || m->style_dim < 1 || m->n_fft < 2 || m->hop < 1) {
         delete m;
         return KDEC_EINVAL;

@@ -12,9 +12,9 @@
 
 namespace brotensor {
 
-namespace {
+kdec_ctx* g_ctx = nullptr;  // the runtime context (see init / set_runtime)
 
-kdec_ctx* g_ctx = nullptr;
+namespace {
 
 [[noreturn]] void fail(const std::string& where, const std::string& msg) {
     throw std::runtime_error("brosoundml: " + where + ": " + msg);
@@ -55,6 +55,16 @@ kdec_ctx* runtime() {
 }
 
 void set_runtime(kdec_ctx* ctx) { g_ctx = ctx; }
+
+}  // namespace brotensor
+
+namespace kdec {
+void forget_runtime(kdec_ctx* ctx) {
+    if (brotensor::g_ctx == ctx) brotensor::g_ctx = nullptr;
+}
+}  // namespace kdec
+
+namespace brotensor {
 
 void sync(Device dev) {
     if (dev == Device::HIP && g_ctx) kdec_synchronize(g_ctx);
