@@ -1,0 +1,216 @@
+"""Kokoro-82M iSTFTNet decoder forward + backward throughput on one MI355X.
+
+One step is the full decoder back half for B = 8 independent utterances of
+T = 512 asr frames (12.8 s of 24 kHz audio each, 102.4 audio-seconds per
+step): harmonic source, style projection, DecoderBackbone, Generator,
+spectral head / iSTFT forward, then the backward with every extension on
+(conv / conv-transpose / pool / style-fc weight grads, Snake alpha grads and
+d(style)) besides the reference's AdaIN affine grads. Inputs are synthetic
+(asr ~ N(0,1), F0 ~ U(80, 300) Hz with 20% unvoiced zeros, N ~ N(0, 0.5),
+style ~ N(0, 0.3), dL/dwav ~ N(0, 1)) and the weights are random-init FP32
+at the real shapes; everything is resident in HBM before the timed region.
+
+Prints one JSON line (rank 0). Usage: python bench.py [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP32_MFMA = 157.3e12   # MI355X dense FP32 matrix, FLOP/s
+PEAK_HBM = 8.0e12           # MI355X HBM3E, B/s
+B, T = 8, 512
+
+
+def make_inputs(cfg, N, T, tag, unvoiced=0.2):
+    from brosoundml_amd import config as C, synth
+    asr = synth.normal(f"{tag}.asr", (N, cfg["asr_dim"], T))
+    F0 = synth.uniform(f"{tag}.F0", (N, 2 * T), 80.0, 300.0)
+    F0[synth.uniform(f"{tag}.uv", (N, 2 * T), 0.0, 1.0) < unvoiced] = 0.0
+    Nn = synth.normal(f"{tag}.N", (N, 2 * T), 0.5)
+    style = synth.normal(f"{tag}.style", (N, cfg["style_dim"]), 0.3)
+    dA = synth.normal(f"{tag}.daudio", (N, C.lengths(cfg, T)["audio"]), 1.0)
+    return asr, F0, Nn, style, dA
+
+
+def cpu_baseline(cfg, params):
+    """The oracle (CPU restatement of the reference path, OpenMP) on config 0:
+    one utterance of T = 64 frames (1.6 s of audio), forward + backward with the
+    same extensions, timed on this host's cores. A reported baseline."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    from brosoundml_amd import config as C
+    T0 = 64
+    om = O.OracleModel(cfg)
+    om.set_params(params)
+    asr, F0, Nn, style, dA = make_inputs(cfg, 1, T0, "bench.cpu")
+    times = []
+    for rep in range(4):  # one warm-up, then the median of three
+        t0 = time.perf_counter()
+        om.zero_grad()
+        om.forward(asr[0], F0[0], Nn[0], style[0], T0)
+        om.backward(dA[0], wgrad=True, dalpha=True, dstyle=True)
+        if rep:
+            times.append(time.perf_counter() - t0)
+    dt = sorted(times)[1]
+    audio_s = C.lengths(cfg, T0)["audio_seconds"]
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(audio_s / dt, 5), "unit": "audio-s/s", "cores": threads, "kind": "port",
+            "seconds": round(dt, 3),
+            "sample": f"1 utterance, T={T0} (1.6 audio-s), decoder fwd+bwd with wgrad/dalpha/dstyle, "
+                      f"CPU oracle (double-accumulating C++, OpenMP {threads} threads); median of 3 "
+                      f"after one warm-up"}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--ref-steps", type=int, default=3, help="steps of the reference-semantics mode")
+    a = ap.parse_args(argv)
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if a.gpus != 1 or world != 1:
+        print("bench.py measures one MI355X: the decoder path shards by utterance with no exchange, "
+              "and this build runs on a single GPU; use --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+    from brosoundml_amd import config as C, native, synth
+
+    cfg = C.KOKORO
+    lens = C.lengths(cfg, T)
+    ctx = native.Context(0)
+    model = native.Model(ctx, cfg)
+    shapes = model.param_shapes()
+    params = synth.init_params(shapes)
+    model.set_params(params)
+    asr, F0, Nn, style, dA = make_inputs(cfg, B, T, "bench")
+    dev = lambda x: torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+    t_asr, t_F0, t_N, t_style, t_dA = (dev(x) for x in (asr, F0, Nn, style, dA))
+    audio = torch.empty(B, lens["audio"], device="cuda")
+    dstyle = torch.empty_like(t_style)
+
+    def step(full=True):
+        model.zero_grad()
+        model.forward(t_asr, t_F0, t_N, t_style, T, audio=audio)
+        model.backward(t_dA, wgrad=full, dalpha=full, dstyle=dstyle if full else None)
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    ctx.profile(True)
+    ctx.profile_reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    if not torch.isfinite(audio).all() or not torch.isfinite(dstyle).all():
+        print("non-finite output", file=sys.stderr)
+        return 1
+
+    # reference semantics (conv dgrad only, alpha grad dropped, no d(style))
+    ref = {}
+    if a.ref_steps > 0:
+        step(False)
+        torch.cuda.synchronize()
+        r0 = time.perf_counter()
+        for _ in range(a.ref_steps):
+            step(False)
+        torch.cuda.synchronize()
+        rdt = (time.perf_counter() - r0) / a.ref_steps
+        ref = {"ms_per_step": round(rdt * 1e3, 3), "value": round(B * lens["audio_seconds"] / rdt, 3)}
+
+    ms = dt / a.steps * 1e3
+    audio_per_step = B * lens["audio_seconds"]
+    value = audio_per_step / (dt / a.steps)
+
+    # dominant kernel: the conv implicit GEMM family with the most time
+    conv_fams = {k: v for k, v in prof.items() if k in ("conv_fwd", "conv_dgrad", "convt_fwd", "convt_dgrad")}
+    gemm_ms = sum(v["ms"] for v in conv_fams.values())
+    gemm_flops = sum(v["flops"] for v in conv_fams.values())
+    gemm_launches = sum(v["launches"] for v in conv_fams.values())
+    wg = prof.get("conv_wgrad", {"ms": 0, "flops": 0, "launches": 0})
+    wgt = prof.get("convt_wgrad", {"ms": 0, "flops": 0, "launches": 0})
+    achieved = gemm_flops / (gemm_ms * 1e-3) if gemm_ms else 0.0
+    total_conv_flops = gemm_flops + wg["flops"] + wgt["flops"]
+    # step roofline: every conv FLOP at the FP32-MFMA peak plus the compulsory
+    # elementwise bytes (8 B/elem forward, 12 B/elem backward over the AdaIN
+    # units' elements) at the HBM peak
+    elems = adain_elements(cfg, T) * B
+    ideal_s = (total_conv_flops / a.steps) / PEAK_FP32_MFMA + 20.0 * elems / PEAK_HBM
+    out = {
+        "metric": "Kokoro decoder fwd+bwd audio-sec/s (T=512,B=8); % of FP32-MFMA/HBM roofline",
+        "value": round(value, 3),
+        "unit": "audio-s/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic inputs, random-init FP32 weights at Kokoro-82M shapes",
+        "config": {"workload": "Kokoro-82M iSTFTNet decoder back half fwd+bwd incl. harmonic source and "
+                               "iSTFT backward, with conv/convT/pool/fc weight grads, Snake alpha grads, d(style)",
+                   "batch": B, "T": T, "audio_s_per_utterance": lens["audio_seconds"],
+                   "audio_s_per_step": audio_per_step, "params": int(sum(np.prod(s) for s in shapes.values()))},
+        "roofline": {"bound": "mfma", "kernel": "conv_gemm (conv1d fwd / dgrad, convT fwd / dgrad)",
+                     "achieved": round(achieved / 1e12, 3), "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": None,
+                     "launches_per_step": gemm_launches // a.steps,
+                     "ms_per_step": round(gemm_ms / a.steps, 3),
+                     "flop_per_step": gemm_flops / a.steps},
+        "wgrad_roofline": {"kernel": "wgrad_gemm", "achieved": round(
+            (wg["flops"] + wgt["flops"]) / max((wg["ms"] + wgt["ms"]) * 1e-3, 1e-12) / 1e12, 3),
+            "unit": "TFLOP/s", "ms_per_step": round((wg["ms"] + wgt["ms"]) / a.steps, 3)},
+        "step_roofline": {"ideal_ms": round(ideal_s * 1e3, 3), "frac": round(ideal_s * 1e3 / ms, 4),
+                          "conv_tflop_per_step": round(total_conv_flops / a.steps / 1e12, 4),
+                          "elementwise_gb_per_step": round(20.0 * elems / 1e9, 3)},
+        "families_ms_per_step": {k: round(v["ms"] / a.steps, 3) for k, v in sorted(prof.items())},
+        "reference_semantics": ref,
+    }
+    if not a.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(cfg, params)
+    print(json.dumps(out))
+    return 0
+
+
+def adain_elements(cfg, T):
+    """Elements passing through AdaIN(+activation) units per utterance."""
+    lg = 2 * T
+    e = (cfg["asr_dim"] + 2) * T + cfg["enc_dim"] * T          # encode norm1, norm2
+    prev, res, Lnow = cfg["enc_dim"], True, T
+    for i in range(cfg["n_decode"]):
+        din = prev + cfg["asr_res_dim"] + 2 if res else prev
+        up = i == cfg["dec_up_at"]
+        Lout = 2 * Lnow if up else Lnow
+        e += din * Lnow + cfg["dec_out"][i] * Lout
+        prev, Lnow = cfg["dec_out"][i], Lout
+        if up:
+            res = False
+    init_C = cfg["dec_out"][cfg["n_decode"] - 1]
+    L = lg
+    for i in range(cfg["n_ups"]):
+        L = L * cfg["ups_rates"][i] + (1 if i == cfg["n_ups"] - 1 else 0)
+        Cc = init_C >> (i + 1)
+        e += (1 + cfg["n_kernels"]) * 6 * Cc * L
+    return e
+
+
+if __name__ == "__main__":
+    sys.exit(main())

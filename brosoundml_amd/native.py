@@ -18,7 +18,8 @@ def _ctype(decl: str):
     """ctypes type for a C declaration's type part (pointer-sized for any pointer)."""
     d = decl.replace("const", " ").strip()
     if "*" in d:
-        return ctypes.c_char_p if d.replace("*", "").split() == ["char"] else ctypes.c_void_p
+        single_char = d.count("*") == 1 and d.replace("*", "").split() == ["char"]
+        return ctypes.c_char_p if single_char else ctypes.c_void_p
     base = d.split()[-1] if d.split() else d
     return {"int": ctypes.c_int, "long": ctypes.c_long, "float": ctypes.c_float,
             "double": ctypes.c_double, "size_t": ctypes.c_size_t, "void": None}[base]
@@ -58,6 +59,13 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m brosoundml_amd.build`")
+        # torch ships its own libamdhip64 with the same soname as ROCm's;
+        # loading torch first makes libkdec bind to that one runtime instead
+        # of bringing a second HIP runtime into the process.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in parse_headers().items():
             fn = getattr(L, name)
