@@ -61,8 +61,28 @@ struct GemmArgs {
     float scale, beta;
     // polyphase transposed-conv mode when n_phase > 1
     int n_phase, ph_s, ph_p, ph_kt;
+    int m_tiles, q_tiles;
 };
 
+// Logical block order with consecutive ids on one XCD: the dispatcher deals
+// workgroups to the 8 XCDs round-robin, so without this remap the blocks that
+// share an operand tile (one X tile across output-channel tiles, one dY tile
+// across weight-grad column tiles) would each miss in a different L2.
+__device__ inline int xcd_remap(int pid, int total) {
+    constexpr int X = 8;
+    const int per = (total + X - 1) / X;
+    int tall = total % X;
+    if (tall == 0) tall = X;
+    const int xcd = pid % X, local = pid / X;
+    if (xcd < tall) return xcd * per + local;
+    return tall * per + (xcd - tall) * (per - 1) + local;
+}
+
+// 1-D grid of m_tiles * q_tiles * (N * n_phase) blocks. Two LDS stages: the
+// next chunk's weights / input window are fetched into registers before the
+// MFMA loop on the current stage and stored to the other stage after it, so
+// global latency hides behind the MFMAs with one barrier per chunk.
+template <int XPT>
 __global__ __launch_bounds__(NT) void conv_gemm(GemmArgs g) {
     extern __shared__ float smem[];
     const int tid = threadIdx.x;
@@ -71,12 +91,18 @@ __global__ __launch_bounds__(NT) void conv_gemm(GemmArgs g) {
     const int wm = wave & 1, wn = wave >> 1;
     const int l32 = lane & 31, hi = lane >> 5;
 
-    int b = blockIdx.z, k = g.k, s = g.s, d = g.d, p = g.p, n_q = g.n_q;
+    int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int mt = lid % g.m_tiles;
+    lid /= g.m_tiles;
+    const int qt = lid % g.q_tiles;
+    const int zz = lid / g.q_tiles;
+
+    int b = zz, k = g.k, s = g.s, d = g.d, p = g.p, n_q = g.n_q;
     int os = 1, oo = 0;
     const float* A = g.A;
     if (g.n_phase > 1) {
-        const int r = blockIdx.z % g.n_phase;
-        b = blockIdx.z / g.n_phase;
+        const int r = zz % g.n_phase;
+        b = zz / g.n_phase;
         const int qmin = -floordiv_i(r - g.ph_p, g.ph_s);          // ceil((p - r)/s)
         const int qmax = floordiv_i(g.L_y - 1 + g.ph_p - r, g.ph_s);
         n_q = qmax - qmin + 1;
@@ -88,18 +114,61 @@ __global__ __launch_bounds__(NT) void conv_gemm(GemmArgs g) {
         oo = qmin * g.ph_s + r - g.ph_p;
         A += static_cast<long>(r) * g.a_phase_stride;
     }
-    const int m0 = blockIdx.y * BM;
-    const int q0 = blockIdx.x * BN;
+    const int m0 = mt * BM;
+    const int q0 = qt * BN;
     if (q0 >= n_q) return;  // uniform per block
 
     const int CK = g.CK;
     const int KR = CK * k;                            // weight rows per chunk
     const int span = (BN - 1) * s + (k - 1) * d + 1;  // staged input window
-    float* Ws = smem;                                 // [KR][BM], row = t*CK + c
-    float* Xs = smem + KR * BM;                       // [CK][span]
+    const int stage = KR * BM + CK * span;
+    const int nw4 = KR * (BM / 4);
+    const int nx = CK * span;
 
     const float* Xb = g.X + static_cast<long>(b) * g.x_bs;
     const int x0 = q0 * s - p;
+
+    float4 wr[8];
+    float xr[XPT];
+    auto gload = [&](int c0) {
+        const float* Ag = A + static_cast<long>(c0) * k * g.m_pad + m0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int idx = tid + i * NT;
+            if (idx < nw4)
+                wr[i] = *reinterpret_cast<const float4*>(Ag + static_cast<long>(idx >> 5) * g.m_pad +
+                                                         (idx & 31) * 4);
+        }
+#pragma unroll
+        for (int j = 0; j < XPT; ++j) {
+            const int idx = tid + j * NT;
+            float v = 0.0f;
+            if (idx < nx) {
+                const int c = idx / span;
+                const int cg = c0 + c;
+                const int xi = x0 + (idx - c * span);
+                if (cg < g.C_in && xi >= 0 && xi < g.L_in) v = Xb[static_cast<long>(cg) * g.L_in + xi];
+            }
+            xr[j] = v;
+        }
+    };
+    auto lstore = [&](float* Ws, float* Xs) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int idx = tid + i * NT;
+            if (idx < nw4) {
+                const int row = idx >> 5;  // (c, t) = (row / k, row % k)
+                const int c = row / k;
+                const int t = row - c * k;
+                *reinterpret_cast<float4*>(Ws + (t * CK + c) * BM + (idx & 31) * 4) = wr[i];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < XPT; ++j) {
+            const int idx = tid + j * NT;
+            if (idx < nx) Xs[idx] = xr[j];
+        }
+    };
 
     f32x16 acc[2][2];
 #pragma unroll
@@ -111,32 +180,15 @@ __global__ __launch_bounds__(NT) void conv_gemm(GemmArgs g) {
 
     const int am = wm * 64 + l32;         // A column (m) for tm = 0
     const int bq = (wn * 64 + l32) * s;   // B column offset for tn = 0
+    const int nchunks = g.cin_pad / CK;
 
-    for (int c0 = 0; c0 < g.cin_pad; c0 += CK) {
-        __syncthreads();
-        // weights: global rows (c0 + c)*k + t, BM contiguous floats each
-        const float* Ag = A + static_cast<long>(c0) * k * g.m_pad + m0;
-        for (int idx = tid; idx < KR * (BM / 4); idx += NT) {
-            const int row = idx / (BM / 4);
-            const int c4 = idx - row * (BM / 4);
-            const int c = row / k;
-            const int t = row - c * k;
-            const float4 v = *reinterpret_cast<const float4*>(
-                Ag + static_cast<long>(row) * g.m_pad + c4 * 4);
-            *reinterpret_cast<float4*>(Ws + (t * CK + c) * BM + c4 * 4) = v;
-        }
-        // haloed input rows, zero outside [0, L_in) and beyond C_in
-        for (int idx = tid; idx < CK * span; idx += NT) {
-            const int c = idx / span;
-            const int j = idx - c * span;
-            const int cg = c0 + c;
-            const int xi = x0 + j;
-            float v = 0.0f;
-            if (cg < g.C_in && xi >= 0 && xi < g.L_in)
-                v = Xb[static_cast<long>(cg) * g.L_in + xi];
-            Xs[c * span + j] = v;
-        }
-        __syncthreads();
+    gload(0);
+    lstore(smem, smem + KR * BM);
+    __syncthreads();
+    for (int ch = 0; ch < nchunks; ++ch) {
+        const float* Ws = smem + (ch & 1) * stage;
+        const float* Xs = Ws + KR * BM;
+        if (ch + 1 < nchunks) gload((ch + 1) * CK);
         for (int t = 0; t < k; ++t) {
             const float* Wt = Ws + t * CK * BM;
             const int toff = t * d;
@@ -144,15 +196,20 @@ __global__ __launch_bounds__(NT) void conv_gemm(GemmArgs g) {
                 const int c = cc + hi;
                 const float a0 = Wt[c * BM + am];
                 const float a1 = Wt[c * BM + am + 32];
-                const float* xr = Xs + c * span + toff + bq;
-                const float b0 = xr[0];
-                const float b1 = xr[32 * s];
+                const float* xp = Xs + c * span + toff + bq;
+                const float b0 = xp[0];
+                const float b1 = xp[32 * s];
                 acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
                 acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
                 acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
                 acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
             }
         }
+        if (ch + 1 < nchunks) {
+            float* Wn = smem + ((ch + 1) & 1) * stage;
+            lstore(Wn, Wn + KR * BM);
+        }
+        __syncthreads();
     }
 
     // epilogue: lane owns column l32 and rows 8*(e/4) + 4*hi + e%4 of each tile
@@ -258,7 +315,7 @@ __global__ void pack_convt_fwd(const float* W, float* A, int C_in, int C_out,
 
 // ─── weight grad ─────────────────────────────────────────────────────────
 
-constexpr int KC = 64;  // positions per K chunk
+constexpr int KC = 32;  // positions per K chunk
 
 struct WgradArgs {
     const float* X;      // correlation input  [n][C_x][L_x]
@@ -266,13 +323,19 @@ struct WgradArgs {
     const float* G;      // grad rows (A side) [n][M][L_g]
     long g_bs;
     float* P;            // partials [split][M][NN]
+    float* Pb;           // bias partials [split][M] (sum of G), or null
     int M, C_x, L_x, L_g, k, s, d, p;
     int NN;              // C_x * k
     int chunks_per_n, total_chunks, chunks_per_split;
+    int n_tiles, m_tiles;
 };
 
 // P[z, m, c*k + t] = sum over this split's positions l of
 //   G[n, m, l] * X[n, c, l*s + t*d - p]
+// (and Pb[z, m] = sum of G over the same positions, from the n-tile-0 blocks).
+// 1-D grid of n_tiles * m_tiles * splits blocks, two LDS stages as in
+// conv_gemm.
+template <int XPT>
 __global__ __launch_bounds__(NT) void wgrad_gemm(WgradArgs g) {
     extern __shared__ float smem[];
     const int tid = threadIdx.x;
@@ -280,16 +343,23 @@ __global__ __launch_bounds__(NT) void wgrad_gemm(WgradArgs g) {
     const int wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
     const int l32 = lane & 31, hi = lane >> 5;
-    const int m0 = blockIdx.y * BM;
-    const int n0 = blockIdx.x * BN;
-    const int z = blockIdx.z;
+
+    int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int nt = lid % g.n_tiles;
+    lid /= g.n_tiles;
+    const int mt = lid % g.m_tiles;
+    const int z = lid / g.m_tiles;
+    const int m0 = mt * BM;
+    const int n0 = nt * BN;
     const int k = g.k, s = g.s, d = g.d;
 
     const int ci_lo = n0 / k;
     const int XR = (BN - 1) / k + 2;                  // staged input rows
     const int span = (KC - 1) * s + (k - 1) * d + 1;  // staged window
-    float* Gs = smem;                                 // [KC][BM + 1]
-    float* Xs = smem + KC * (BM + 1);                 // [XR][span]
+    const int gsz = KC * (BM + 1);
+    const int stage = gsz + XR * span;
+    const int nx = XR * span;
+    const bool do_bias = g.Pb && nt == 0;
 
     // this lane's two B columns
     int xrow[2], xoff[2];
@@ -303,6 +373,47 @@ __global__ __launch_bounds__(NT) void wgrad_gemm(WgradArgs g) {
         xoff[tn] = ok[tn] ? (n - c * k) * d : 0;
     }
 
+    static_assert(BM * KC % NT == 0, "G tile must split evenly over the block");
+    float gr[BM * KC / NT];
+    float xr[XPT];
+    auto gload = [&](int ch) {
+        const int b = ch / g.chunks_per_n;
+        const int l0 = (ch - b * g.chunks_per_n) * KC;
+        const float* Gb = g.G + static_cast<long>(b) * g.g_bs;
+        const float* Xb = g.X + static_cast<long>(b) * g.x_bs;
+#pragma unroll
+        for (int i = 0; i < BM * KC / NT; ++i) {
+            const int idx = tid + i * NT;
+            const int mg = m0 + idx / KC, l = l0 + idx % KC;
+            gr[i] = (mg < g.M && l < g.L_g) ? Gb[static_cast<long>(mg) * g.L_g + l] : 0.0f;
+        }
+        const int x0 = l0 * s - g.p;
+#pragma unroll
+        for (int j = 0; j < XPT; ++j) {
+            const int idx = tid + j * NT;
+            float v = 0.0f;
+            if (idx < nx) {
+                const int r = idx / span;
+                const int c = ci_lo + r;
+                const int xi = x0 + (idx - r * span);
+                if (c < g.C_x && xi >= 0 && xi < g.L_x) v = Xb[static_cast<long>(c) * g.L_x + xi];
+            }
+            xr[j] = v;
+        }
+    };
+    auto lstore = [&](float* Gs, float* Xs) {
+#pragma unroll
+        for (int i = 0; i < BM * KC / NT; ++i) {
+            const int idx = tid + i * NT;
+            Gs[(idx % KC) * (BM + 1) + idx / KC] = gr[i];
+        }
+#pragma unroll
+        for (int j = 0; j < XPT; ++j) {
+            const int idx = tid + j * NT;
+            if (idx < nx) Xs[idx] = xr[j];
+        }
+    };
+
     f32x16 acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -310,34 +421,25 @@ __global__ __launch_bounds__(NT) void wgrad_gemm(WgradArgs g) {
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    double bsum = 0.0;
 
     const int ch0 = z * g.chunks_per_split;
     const int ch1 = min(ch0 + g.chunks_per_split, g.total_chunks);
+    if (ch0 < ch1) {
+        gload(ch0);
+        lstore(smem, smem + gsz);
+    }
+    __syncthreads();
     for (int ch = ch0; ch < ch1; ++ch) {
-        const int b = ch / g.chunks_per_n;
-        const int l0 = (ch - b * g.chunks_per_n) * KC;
-        const float* Gb = g.G + static_cast<long>(b) * g.g_bs;
-        const float* Xb = g.X + static_cast<long>(b) * g.x_bs;
-        __syncthreads();
-        for (int idx = tid; idx < BM * KC; idx += NT) {
-            const int m = idx / KC;
-            const int kc = idx - m * KC;
-            const int mg = m0 + m, l = l0 + kc;
-            float v = 0.0f;
-            if (mg < g.M && l < g.L_g) v = Gb[static_cast<long>(mg) * g.L_g + l];
-            Gs[kc * (BM + 1) + m] = v;
+        const int cur = (ch - ch0) & 1;
+        const float* Gs = smem + cur * stage;
+        const float* Xs = Gs + gsz;
+        if (ch + 1 < ch1) gload(ch + 1);
+        if (do_bias && tid < BM) {
+            float t = 0.0f;
+            for (int kc = 0; kc < KC; ++kc) t += Gs[kc * (BM + 1) + tid];
+            bsum += t;
         }
-        const int x0 = l0 * s - g.p;
-        for (int idx = tid; idx < XR * span; idx += NT) {
-            const int r = idx / span;
-            const int j = idx - r * span;
-            const int c = ci_lo + r;
-            const int xi = x0 + j;
-            float v = 0.0f;
-            if (c < g.C_x && xi >= 0 && xi < g.L_x) v = Xb[static_cast<long>(c) * g.L_x + xi];
-            Xs[r * span + j] = v;
-        }
-        __syncthreads();
         const float* xb0 = Xs + xrow[0] * span + xoff[0];
         const float* xb1 = Xs + xrow[1] * span + xoff[1];
         for (int kc = 0; kc < KC; kc += 2) {
@@ -351,6 +453,11 @@ __global__ __launch_bounds__(NT) void wgrad_gemm(WgradArgs g) {
             acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
             acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
         }
+        if (ch + 1 < ch1) {
+            float* Gn = smem + (cur ^ 1) * stage;
+            lstore(Gn, Gn + gsz);
+        }
+        __syncthreads();
     }
 
     float* Pz = g.P + static_cast<long>(z) * g.M * g.NN;
@@ -366,6 +473,8 @@ __global__ __launch_bounds__(NT) void wgrad_gemm(WgradArgs g) {
                 if (m < g.M) Pz[static_cast<long>(m) * g.NN + n] = acc[tm][tn][e];
             }
     }
+    if (do_bias && tid < BM && m0 + tid < g.M)
+        g.Pb[static_cast<long>(z) * g.M + m0 + tid] = static_cast<float>(bsum);
 }
 
 // out[i] += sum_z P[z][i] in a fixed order.  `transpose_k`: when non-zero the
@@ -389,13 +498,17 @@ __global__ void wgrad_reduce(const float* P, float* out, long MN, int splits,
     }
 }
 
-// db[m] += sum_{n, l} G[n, m, l]; one block per m, fixed-order reduction.
-__global__ void bias_grad(const float* G, long g_bs, float* db, int N, int L) {
-    const int m = blockIdx.x;
+// part[y, m] = sum of G[n, m, l] over the y-th slice of the (n, l) range;
+// grid (M, S). Reduced over y by bias_reduce in a fixed order.
+__global__ void bias_partial(const float* G, long g_bs, float* part, int N, int M, int L) {
+    const int m = blockIdx.x, y = blockIdx.y, S = gridDim.y;
+    const long tot = static_cast<long>(N) * L;
+    const long per = (tot + S - 1) / S;
+    const long i0 = y * per, i1 = min(tot, i0 + per);
     double acc = 0.0;
-    for (int n = 0; n < N; ++n) {
-        const float* row = G + n * g_bs + static_cast<long>(m) * L;
-        for (int l = threadIdx.x; l < L; l += blockDim.x) acc += row[l];
+    for (long i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+        const long n = i / L, l = i - n * L;
+        acc += G[n * g_bs + static_cast<long>(m) * L + l];
     }
     __shared__ double red[256];
     red[threadIdx.x] = acc;
@@ -404,7 +517,16 @@ __global__ void bias_grad(const float* G, long g_bs, float* db, int N, int L) {
         if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
         __syncthreads();
     }
-    if (threadIdx.x == 0) db[m] += static_cast<float>(red[0]);
+    if (threadIdx.x == 0) part[static_cast<long>(y) * M + m] = static_cast<float>(red[0]);
+}
+
+// db[m] += sum_y part[y, m]
+__global__ void bias_reduce(const float* part, float* db, int M, int S) {
+    const int m = blockIdx.x * blockDim.x + threadIdx.x;
+    if (m >= M) return;
+    double acc = 0.0;
+    for (int y = 0; y < S; ++y) acc += part[static_cast<long>(y) * M + m];
+    db[m] += static_cast<float>(acc);
 }
 
 // ─── depthwise pool: ConvTranspose1d k3 s2 p1 op1, groups = C ──────────────
@@ -492,6 +614,32 @@ int grid1d(long n) {
     return static_cast<int>(g);
 }
 
+// Registers per thread that stage the input window (XPT) for a chunk of
+// `n` floats; each instance covers n <= XPT * NT.
+template <template <int> class F, class... Args>
+int with_xpt(int n, Args&&... args) {
+    if (n <= 4 * NT) return F<4>::run(args...);
+    if (n <= 8 * NT) return F<8>::run(args...);
+    if (n <= 16 * NT) return F<16>::run(args...);
+    if (n <= 24 * NT) return F<24>::run(args...);
+    if (n <= 40 * NT) return F<40>::run(args...);
+    return -100;
+}
+
+template <int XPT>
+struct LaunchConv {
+    static int run(kdec_ctx* ctx, const GemmArgs& g, unsigned blocks, size_t lds) {
+        static bool attr = false;
+        if (!attr) {
+            hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_gemm<XPT>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+            attr = true;
+        }
+        hipLaunchKernelGGL(conv_gemm<XPT>, dim3(blocks), dim3(NT), lds, ctx->stream, g);
+        return 0;
+    }
+};
+
 // Launches conv_gemm over an already packed A.
 int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
              double flops) {
@@ -499,17 +647,36 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
     const int kk = g.n_phase > 1 ? g.ph_kt : g.k;
     const int ss = g.n_phase > 1 ? 1 : g.s;
     const int dd = g.n_phase > 1 ? 1 : g.d;
+    if (CK * kk > 64) return fail(ctx, KDEC_EINVAL, "conv: kernel too long for the weight stage");
     const int span = (BN - 1) * ss + (kk - 1) * dd + 1;
-    const size_t lds = (static_cast<size_t>(CK) * kk * BM + static_cast<size_t>(CK) * span) * sizeof(float);
+    const size_t stage = static_cast<size_t>(CK) * kk * BM + static_cast<size_t>(CK) * span;
+    const size_t lds = 2 * stage * sizeof(float);
     if (lds > 160 * 1024) return fail(ctx, KDEC_EINVAL, "conv: tile does not fit LDS");
     int max_q = g.n_q;
     if (g.n_phase > 1) max_q = static_cast<int>(cdiv(g.L_y + g.ph_s, g.ph_s)) + 1;
-    const dim3 grid(static_cast<unsigned>(cdiv(max_q, BN)), static_cast<unsigned>(m_tiles),
-                    static_cast<unsigned>(N * g.n_phase));
+    g.m_tiles = m_tiles;
+    g.q_tiles = static_cast<int>(cdiv(max_q, BN));
+    const long blocks = static_cast<long>(g.m_tiles) * g.q_tiles * N * g.n_phase;
+    if (blocks > 0x7fffffffL) return fail(ctx, KDEC_EINVAL, "conv: grid too large");
     ProfScope ps(ctx, fam, flops);
-    hipLaunchKernelGGL(conv_gemm, grid, dim3(NT), lds, ctx->stream, g);
+    const int rc = with_xpt<LaunchConv>(CK * span, ctx, g, static_cast<unsigned>(blocks), lds);
+    if (rc == -100) return fail(ctx, KDEC_EINVAL, "conv: input window too large");
     return launch_check(ctx, fam);
 }
+
+template <int XPT>
+struct LaunchWgrad {
+    static int run(kdec_ctx* ctx, const WgradArgs& a, unsigned blocks, size_t lds) {
+        static bool attr = false;
+        if (!attr) {
+            hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_gemm<XPT>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+            attr = true;
+        }
+        hipLaunchKernelGGL(wgrad_gemm<XPT>, dim3(blocks), dim3(NT), lds, ctx->stream, a);
+        return 0;
+    }
+};
 
 }  // namespace
 }  // namespace kdec
@@ -583,41 +750,70 @@ int kdec_conv1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
                     2.0 * N * C_out * static_cast<double>(L_out) * C_in * k);
 }
 
+// out (M x C_x*k) += the weight grad; db (M) += the row sums of G when
+// non-null (fused into the GEMM's n-tile-0 blocks).
 static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G,
                         long g_bs, int N, int M, int C_x, int L_x, int L_g, int k,
-                        int s, int d, int p, float* out, int transpose_k,
-                        const char* fam) {
+                        int s, int d, int p, float* out, float* db, const char* fam) {
     const int NN = C_x * k;
     const int m_tiles = static_cast<int>(cdiv(M, BM));
     const int n_tiles = static_cast<int>(cdiv(NN, BN));
     const int chunks_per_n = static_cast<int>(cdiv(L_g, KC));
     const int total_chunks = chunks_per_n * N;
-    // aim for ~2048 blocks in flight, but keep >= 4 chunks per split
+    // aim for ~2048 blocks in flight, but keep >= 8 chunks per split
     long want = 2048 / (static_cast<long>(m_tiles) * n_tiles);
     if (want < 1) want = 1;
     int cps = static_cast<int>(cdiv(total_chunks, want));
-    if (cps < 4) cps = 4;
+    if (cps < 8) cps = 8;
     const int splits = static_cast<int>(cdiv(total_chunks, cps));
     const long MN = static_cast<long>(M) * NN;
     Workspace P(ctx, static_cast<size_t>(splits) * MN * sizeof(float));
-    if (!P.p) return KDEC_ENOMEM;
+    Workspace Pb(ctx, db ? static_cast<size_t>(splits) * M * sizeof(float) : 0);
+    if (!P.p || (db && !Pb.p)) return KDEC_ENOMEM;
     WgradArgs a{};
     a.X = X; a.x_bs = x_bs; a.G = G; a.g_bs = g_bs; a.P = P.as<float>();
+    a.Pb = db ? Pb.as<float>() : nullptr;
     a.M = M; a.C_x = C_x; a.L_x = L_x; a.L_g = L_g; a.k = k; a.s = s; a.d = d; a.p = p;
     a.NN = NN; a.chunks_per_n = chunks_per_n; a.total_chunks = total_chunks;
     a.chunks_per_split = cps;
+    a.n_tiles = n_tiles;
+    a.m_tiles = m_tiles;
     const int XR = (BN - 1) / k + 2;
     const int span = (KC - 1) * s + (k - 1) * d + 1;
-    const size_t lds = (static_cast<size_t>(KC) * (BM + 1) + static_cast<size_t>(XR) * span) * sizeof(float);
+    const size_t stage = static_cast<size_t>(KC) * (BM + 1) + static_cast<size_t>(XR) * span;
+    const size_t lds = 2 * stage * sizeof(float);
     if (lds > 160 * 1024) return fail(ctx, KDEC_EINVAL, "wgrad: tile does not fit LDS");
+    const long blocks = static_cast<long>(n_tiles) * m_tiles * splits;
     {
         ProfScope ps(ctx, fam, 2.0 * N * M * static_cast<double>(L_g) * NN);
-        hipLaunchKernelGGL(wgrad_gemm, dim3(n_tiles, m_tiles, splits), dim3(NT), lds, ctx->stream, a);
-        if (int rc = launch_check(ctx, fam)) return rc;
+        const int rc = with_xpt<LaunchWgrad>(XR * span, ctx, a, static_cast<unsigned>(blocks), lds);
+        if (rc == -100) return fail(ctx, KDEC_EINVAL, "wgrad: input window too large");
+        if (int rc2 = launch_check(ctx, fam)) return rc2;
     }
     hipLaunchKernelGGL(wgrad_reduce, dim3(grid1d(MN)), dim3(256), 0, ctx->stream, P.as<float>(), out, MN,
-                       splits, transpose_k, M, NN);
-    return launch_check(ctx, "wgrad_reduce");
+                       splits, 0, M, NN);
+    if (int rc = launch_check(ctx, "wgrad_reduce")) return rc;
+    if (db) {
+        hipLaunchKernelGGL(bias_reduce, dim3(static_cast<unsigned>(cdiv(M, 256))), dim3(256), 0, ctx->stream,
+                           Pb.as<float>(), db, M, splits);
+        return launch_check(ctx, "bias_reduce");
+    }
+    return KDEC_OK;
+}
+
+// db (M) += sum over (n, l) of G[n, m, l]
+static int bias_grad_only(kdec_ctx* ctx, const float* G, long g_bs, float* db, int N, int M, int L) {
+    long S = (static_cast<long>(N) * L + 32767) / 32768;
+    if (S > 64) S = 64;
+    if (S < 1) S = 1;
+    Workspace part(ctx, static_cast<size_t>(S) * M * sizeof(float));
+    if (!part.p) return KDEC_ENOMEM;
+    hipLaunchKernelGGL(bias_partial, dim3(M, static_cast<unsigned>(S)), dim3(256), 0, ctx->stream, G, g_bs,
+                       part.as<float>(), N, M, L);
+    if (int rc = launch_check(ctx, "bias_partial")) return rc;
+    hipLaunchKernelGGL(bias_reduce, dim3(static_cast<unsigned>(cdiv(M, 256))), dim3(256), 0, ctx->stream,
+                       part.as<float>(), db, M, static_cast<int>(S));
+    return launch_check(ctx, "bias_reduce");
 }
 
 int kdec_conv1d_wgrad(kdec_ctx* ctx, const float* X, long x_bs,
@@ -630,13 +826,9 @@ int kdec_conv1d_wgrad(kdec_ctx* ctx, const float* X, long x_bs,
     const int L_out = (L + 2 * pad - dil * (k - 1) - 1) / stride + 1;
     KDEC_CHECK(ctx, L > 0 && L_out > 0, "kdec_conv1d_wgrad: empty output");
     if (dW)
-        if (int rc = wgrad_common(ctx, X, x_bs, dY, dy_bs, N, C_out, C_in, L, L_out, k, stride, dil,
-                                  pad, dW, 0, "conv_wgrad"))
-            return rc;
-    if (db) {
-        hipLaunchKernelGGL(bias_grad, dim3(C_out), dim3(256), 0, ctx->stream, dY, dy_bs, db, N, L_out);
-        return launch_check(ctx, "bias_grad");
-    }
+        return wgrad_common(ctx, X, x_bs, dY, dy_bs, N, C_out, C_in, L, L_out, k, stride, dil, pad, dW, db,
+                            "conv_wgrad");
+    if (db) return bias_grad_only(ctx, dY, dy_bs, db, N, C_out, L_out);
     return KDEC_OK;
 }
 
@@ -716,13 +908,10 @@ int kdec_convt1d_wgrad(kdec_ctx* ctx, const float* X, long x_bs,
     // dW[ci, co*k + t] = sum_l X[ci, l] dY[co, l*s + t - p]: the conv weight
     // grad with the roles of input and output grad exchanged (M = C_in).
     if (dW)
-        if (int rc = wgrad_common(ctx, dY, dy_bs, X, x_bs, N, C_in, C_out, L_out, L, k, stride, 1,
-                                  pad, dW, 0, "convt_wgrad"))
+        if (int rc = wgrad_common(ctx, dY, dy_bs, X, x_bs, N, C_in, C_out, L_out, L, k, stride, 1, pad, dW,
+                                  nullptr, "convt_wgrad"))
             return rc;
-    if (db) {
-        hipLaunchKernelGGL(bias_grad, dim3(C_out), dim3(256), 0, ctx->stream, dY, dy_bs, db, N, L_out);
-        return launch_check(ctx, "bias_grad");
-    }
+    if (db) return bias_grad_only(ctx, dY, dy_bs, db, N, C_out, L_out);
     return KDEC_OK;
 }
 
