@@ -17,7 +17,12 @@
 // 64x64 (2x2 MFMA tiles each). Per K chunk the block stages CK input rows of
 // the haloed window [q0*s - p, (q0+127)*s + (k-1)d - p] and the matching
 // CK*k weight rows in LDS; every tap then reads a shifted window of the same
-// staged rows, so X is fetched once per chunk instead of k times.
+// staged rows, so X is fetched once per chunk instead of k times. Staging is
+// direct global->LDS (global_load_lds_dwordx4 for the weight panel,
+// buffer_load_dword ... lds for the input rows, whose buffer range turns
+// out-of-row positions into zeros), double-buffered so the next chunk's loads
+// fly during the current chunk's MFMAs; no VGPRs hold staged data, which keeps
+// the kernel at ~80 VGPRs and 4-6 waves per SIMD.
 //
 // Weight-grad (`wgrad_gemm`): dW[m, (c, t)] = sum_{n, l} dY[n, m, l] *
 // X[n, c, l*s + t*d - p], a GEMM with the huge position axis as K. It is
@@ -36,6 +41,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int BM = 128;   // output-channel tile
 constexpr int BN = 128;   // output-position tile
 constexpr int NT = 256;   // threads per block (4 waves)
+// Buffer descriptor word 3 for raw 32-bit buffer loads (DATA_FORMAT = 32).
+constexpr int kBufDword3 = 0x00020000;
 
 __device__ inline int floordiv_i(int a, int b) {
     int q = a / b;
@@ -78,16 +85,20 @@ __device__ inline int xcd_remap(int pid, int total) {
     return tall * per + (xcd - tall) * (per - 1) + local;
 }
 
-// 1-D grid of m_tiles * q_tiles * (N * n_phase) blocks. Two LDS stages: the
-// next chunk's weights / input window are fetched into registers before the
-// MFMA loop on the current stage and stored to the other stage after it, so
-// global latency hides behind the MFMAs with one barrier per chunk.
-template <int XPT>
-__global__ __launch_bounds__(NT) void conv_gemm(GemmArgs g) {
+// 1-D grid of m_tiles * q_tiles * (N * n_phase) blocks. Two LDS stages;
+// weights arrive packed chunk-major (row ((chunk*k + t)*CK + c_local)), so a
+// chunk's KR = CK*k rows are one contiguous slab of the panel.
+//
+// Inner loop: the chunk's KR/2 k-steps (2 packed rows each) run as a
+// ping-pong over two register sets, each step's LDS reads issued between the
+// MFMAs of the step before, so the read latency hides behind matrix work.
+template <int CK>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4)))
+void conv_gemm(GemmArgs g) {
     extern __shared__ float smem[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave & 1, wn = wave >> 1;
     const int l32 = lane & 31, hi = lane >> 5;
 
@@ -118,55 +129,31 @@ __global__ __launch_bounds__(NT) void conv_gemm(GemmArgs g) {
     const int q0 = qt * BN;
     if (q0 >= n_q) return;  // uniform per block
 
-    const int CK = g.CK;
     const int KR = CK * k;                            // weight rows per chunk
     const int span = (BN - 1) * s + (k - 1) * d + 1;  // staged input window
-    const int stage = KR * BM + CK * span;
-    const int nw4 = KR * (BM / 4);
-    const int nx = CK * span;
-
+    const int span_p = (span + 63) & ~63;             // LDS row stride
+    const int segs = span_p >> 6;
+    const int stage = KR * BM + CK * span_p;
     const float* Xb = g.X + static_cast<long>(b) * g.x_bs;
     const int x0 = q0 * s - p;
+    const int a_lane = (lane >> 5) * g.m_pad + (lane & 31) * 4;
+    const int nitems = CK * segs;
 
-    float4 wr[8];
-    float xr[XPT];
-    auto gload = [&](int c0) {
-        const float* Ag = A + static_cast<long>(c0) * k * g.m_pad + m0;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int idx = tid + i * NT;
-            if (idx < nw4)
-                wr[i] = *reinterpret_cast<const float4*>(Ag + static_cast<long>(idx >> 5) * g.m_pad +
-                                                         (idx & 31) * 4);
-        }
-#pragma unroll
-        for (int j = 0; j < XPT; ++j) {
-            const int idx = tid + j * NT;
-            float v = 0.0f;
-            if (idx < nx) {
-                const int c = idx / span;
-                const int cg = c0 + c;
-                const int xi = x0 + (idx - c * span);
-                if (cg < g.C_in && xi >= 0 && xi < g.L_in) v = Xb[static_cast<long>(cg) * g.L_in + xi];
-            }
-            xr[j] = v;
-        }
-    };
-    auto lstore = [&](float* Ws, float* Xs) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int idx = tid + i * NT;
-            if (idx < nw4) {
-                const int row = idx >> 5;  // (c, t) = (row / k, row % k)
-                const int c = row / k;
-                const int t = row - c * k;
-                *reinterpret_cast<float4*>(Ws + (t * CK + c) * BM + (idx & 31) * 4) = wr[i];
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < XPT; ++j) {
-            const int idx = tid + j * NT;
-            if (idx < nx) Xs[idx] = xr[j];
+    // Stage chunk `ch` at LDS float offset `sb`: the weight slab two rows
+    // (1 KB) per instruction, the input window 64 positions per instruction.
+    auto issue = [&](int ch, int sb) {
+        const float* Ag = A + static_cast<long>(ch) * KR * g.m_pad + m0;
+        for (int pr = wave; pr < KR / 2; pr += 4)
+            __builtin_amdgcn_global_load_lds(Ag + static_cast<long>(2 * pr) * g.m_pad + a_lane,
+                                             smem + sb + pr * 256, 16, 0, 0);
+        for (int it = wave; it < nitems; it += 4) {
+            const int r = it / segs, sg = it - r * segs;
+            const int c = ch * CK + r;
+            const float* rowp = Xb + static_cast<long>(c) * g.L_in;
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(rowp), static_cast<short>(0), c < g.C_in ? g.L_in * 4 : 0, kBufDword3);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, smem + sb + KR * BM + r * span_p + sg * 64, 4,
+                                                     (x0 + sg * 64 + lane) * 4, 0, 0, 0);
         }
     };
 
@@ -181,34 +168,55 @@ __global__ __launch_bounds__(NT) void conv_gemm(GemmArgs g) {
     const int am = wm * 64 + l32;         // A column (m) for tm = 0
     const int bq = (wn * 64 + l32) * s;   // B column offset for tn = 0
     const int nchunks = g.cin_pad / CK;
+    const int S = KR / 2;                 // k-steps per chunk
+    constexpr int HS = CK / 2;
 
-    gload(0);
-    lstore(smem, smem + KR * BM);
+    issue(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);  // staging loads landed in LDS
     __syncthreads();
     for (int ch = 0; ch < nchunks; ++ch) {
-        const float* Ws = smem + (ch & 1) * stage;
-        const float* Xs = Ws + KR * BM;
-        if (ch + 1 < nchunks) gload((ch + 1) * CK);
-        for (int t = 0; t < k; ++t) {
-            const float* Wt = Ws + t * CK * BM;
-            const int toff = t * d;
-            for (int cc = 0; cc < CK; cc += 2) {
-                const int c = cc + hi;
-                const float a0 = Wt[c * BM + am];
-                const float a1 = Wt[c * BM + am + 32];
-                const float* xp = Xs + c * span + toff + bq;
-                const float b0 = xp[0];
-                const float b1 = xp[32 * s];
-                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
-            }
+        const int sb = (ch & 1) * stage;
+        if (ch + 1 < nchunks) issue(ch + 1, stage - sb);
+        const int wb = sb + hi * BM + am;
+        const int xb = sb + KR * BM + hi * span_p + bq;
+        // step u reads packed rows 2u + hi: tap t = u / HS, channel 2(u % HS) + hi
+        auto ld = [&](int u, float& a0, float& a1, float& b0, float& b1) {
+            u = min(u, S - 1);
+            const int t = u / HS;
+            const int cc = (u - t * HS) * 2;
+            int wo = wb + u * 2 * BM;
+            int xo = xb + cc * span_p + t * d;
+            // opaque offsets keep each step's reads where they are placed
+            asm volatile("" : "+v"(wo), "+v"(xo));
+            a0 = smem[wo];
+            a1 = smem[wo + 32];
+            b0 = smem[xo];
+            b1 = smem[xo + 32 * s];
+        };
+        auto mm = [&](float a0, float a1, float b0, float b1) {
+            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+        };
+        float pa0, pa1, pb0, pb1, qa0, qa1, qb0, qb1;
+        ld(0, pa0, pa1, pb0, pb1);
+        int u = 0;
+        for (; u + 1 < S; u += 2) {
+            ld(u + 1, qa0, qa1, qb0, qb1);
+            mm(pa0, pa1, pb0, pb1);
+            ld(u + 2, pa0, pa1, pb0, pb1);
+            mm(qa0, qa1, qb0, qb1);
+            // 1 MFMA, the next step's reads, 3 MFMAs (twice)
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
         }
-        if (ch + 1 < nchunks) {
-            float* Wn = smem + ((ch + 1) & 1) * stage;
-            lstore(Wn, Wn + KR * BM);
-        }
+        if (u < S) mm(pa0, pa1, pb0, pb1);
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's staging loads landed
         __syncthreads();
     }
 
@@ -239,19 +247,26 @@ __global__ __launch_bounds__(NT) void conv_gemm(GemmArgs g) {
 }
 
 // ─── weight packing ──────────────────────────────────────────────────────
-// All packers write A[(c*kk + t)*m_pad + m] over the padded extent, zeroing
-// the padding, for the correlation they set up.
+// All packers write the zero-padded panel A[row][m_pad] in chunk-major row
+// order: row = ((c / CK) * kk + t) * CK + c % CK for input channel c and
+// tap t, so that one K chunk (CK channels x kk taps) is a contiguous slab.
+
+__device__ inline void panel_row(long row, int CK, int kk, int& c, int& t) {
+    const int cl = static_cast<int>(row % CK);
+    const long r2 = row / CK;
+    t = static_cast<int>(r2 % kk);
+    c = static_cast<int>(r2 / kk) * CK + cl;
+}
 
 // conv1d forward: A[(ci, t), co] = W[co, ci*k + t]
 __global__ void pack_fwd(const float* W, float* A, int C_in, int C_out, int k,
-                         int cin_pad, int m_pad) {
+                         int cin_pad, int m_pad, int CK) {
     const long total = static_cast<long>(cin_pad) * k * m_pad;
     for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < total;
          i += static_cast<long>(gridDim.x) * blockDim.x) {
         const int m = static_cast<int>(i % m_pad);
-        const long row = i / m_pad;
-        const int t = static_cast<int>(row % k);
-        const int c = static_cast<int>(row / k);
+        int c, t;
+        panel_row(i / m_pad, CK, k, c, t);
         float v = 0.0f;
         if (m < C_out && c < C_in) v = W[(static_cast<long>(m) * C_in + c) * k + t];
         A[i] = v;
@@ -261,14 +276,13 @@ __global__ void pack_fwd(const float* W, float* A, int C_in, int C_out, int k,
 // conv1d input-grad (stride 1): the correlation over dY (C_out channels) with
 // A[(co, t'), ci] = W[co, ci*k + (k-1-t')]
 __global__ void pack_dgrad(const float* W, float* A, int C_in, int C_out, int k,
-                           int cout_pad, int m_pad) {
+                           int cout_pad, int m_pad, int CK) {
     const long total = static_cast<long>(cout_pad) * k * m_pad;
     for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < total;
          i += static_cast<long>(gridDim.x) * blockDim.x) {
         const int m = static_cast<int>(i % m_pad);  // ci
-        const long row = i / m_pad;
-        const int t = static_cast<int>(row % k);
-        const int c = static_cast<int>(row / k);    // co
+        int c, t;                                   // c = co
+        panel_row(i / m_pad, CK, k, c, t);
         float v = 0.0f;
         if (m < C_in && c < C_out) v = W[(static_cast<long>(c) * C_in + m) * k + (k - 1 - t)];
         A[i] = v;
@@ -278,14 +292,13 @@ __global__ void pack_dgrad(const float* W, float* A, int C_in, int C_out, int k,
 // conv-transpose input-grad: correlation over dY (C_out channels) with
 // A[(co, t), ci] = W[ci, co*k + t]
 __global__ void pack_convt_dgrad(const float* W, float* A, int C_in, int C_out,
-                                 int k, int cout_pad, int m_pad) {
+                                 int k, int cout_pad, int m_pad, int CK) {
     const long total = static_cast<long>(cout_pad) * k * m_pad;
     for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < total;
          i += static_cast<long>(gridDim.x) * blockDim.x) {
         const int m = static_cast<int>(i % m_pad);  // ci
-        const long row = i / m_pad;
-        const int t = static_cast<int>(row % k);
-        const int c = static_cast<int>(row / k);    // co
+        int c, t;                                   // c = co
+        panel_row(i / m_pad, CK, k, c, t);
         float v = 0.0f;
         if (m < C_in && c < C_out) v = W[(static_cast<long>(m) * C_out + c) * k + t];
         A[i] = v;
@@ -296,16 +309,15 @@ __global__ void pack_convt_dgrad(const float* W, float* A, int C_in, int C_out,
 // t = r + (kt-1-t')*s.  A_r[(ci, t'), co] = W[ci, co*k + t] (0 if t >= k)
 __global__ void pack_convt_fwd(const float* W, float* A, int C_in, int C_out,
                                int k, int s, int kt, int cin_pad, int m_pad,
-                               long phase_stride) {
+                               long phase_stride, int CK) {
     const long total = phase_stride * s;
     for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < total;
          i += static_cast<long>(gridDim.x) * blockDim.x) {
         const int r = static_cast<int>(i / phase_stride);
         const long w = i - r * phase_stride;
         const int m = static_cast<int>(w % m_pad);  // co
-        const long row = w / m_pad;
-        const int tp = static_cast<int>(row % kt);
-        const int c = static_cast<int>(row / kt);   // ci
+        int c, tp;                                  // c = ci
+        panel_row(w / m_pad, CK, kt, c, tp);
         const int t = r + (kt - 1 - tp) * s;
         float v = 0.0f;
         if (m < C_out && c < C_in && t < k) v = W[(static_cast<long>(c) * C_out + m) * k + t];
@@ -600,10 +612,10 @@ __global__ void pool_wgrad(const float* X, long x_bs, const float* dY, long dy_b
 
 // Input channels per K chunk: a power of two in [2, 32] so that it divides
 // the 32-padded channel count of the packed weights (no chunk runs past them),
-// with CK*k near 64 weight rows per chunk.
+// with CK*k near 32 weight rows per chunk (small stages: 4-6 blocks per CU).
 int pick_ck(int k) {
     int ck = 32;
-    while (ck > 2 && ck * k > 64) ck >>= 1;
+    while (ck > 2 && ck * k > 32) ck >>= 1;
     return ck;
 }
 
@@ -626,19 +638,17 @@ int with_xpt(int n, Args&&... args) {
     return -100;
 }
 
-template <int XPT>
-struct LaunchConv {
-    static int run(kdec_ctx* ctx, const GemmArgs& g, unsigned blocks, size_t lds) {
-        static bool attr = false;
-        if (!attr) {
-            hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_gemm<XPT>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-            attr = true;
-        }
-        hipLaunchKernelGGL(conv_gemm<XPT>, dim3(blocks), dim3(NT), lds, ctx->stream, g);
-        return 0;
+template <int CK>
+int launch_conv(kdec_ctx* ctx, const GemmArgs& g, unsigned blocks, size_t lds) {
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_gemm<CK>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        attr = true;
     }
-};
+    hipLaunchKernelGGL(conv_gemm<CK>, dim3(blocks), dim3(NT), lds, ctx->stream, g);
+    return 0;
+}
 
 // Launches conv_gemm over an already packed A.
 int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
@@ -647,11 +657,13 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
     const int kk = g.n_phase > 1 ? g.ph_kt : g.k;
     const int ss = g.n_phase > 1 ? 1 : g.s;
     const int dd = g.n_phase > 1 ? 1 : g.d;
-    if (CK * kk > 64) return fail(ctx, KDEC_EINVAL, "conv: kernel too long for the weight stage");
-    const int span = (BN - 1) * ss + (kk - 1) * dd + 1;
-    const size_t stage = static_cast<size_t>(CK) * kk * BM + static_cast<size_t>(CK) * span;
+    if (CK * kk > 64 || (CK * kk) % 2) return fail(ctx, KDEC_EINVAL, "conv: kernel too long for the weight stage");
+    const long span = static_cast<long>(BN - 1) * ss + static_cast<long>(kk - 1) * dd + 1;
+    const long span_p = (span + 63) / 64 * 64;
+    const size_t stage = static_cast<size_t>(CK) * kk * BM + static_cast<size_t>(CK) * span_p;
     const size_t lds = 2 * stage * sizeof(float);
     if (lds > 160 * 1024) return fail(ctx, KDEC_EINVAL, "conv: tile does not fit LDS");
+    if (static_cast<long>(g.L_in) * 4 > 0x7fffffffL) return fail(ctx, KDEC_EINVAL, "conv: input rows too long");
     int max_q = g.n_q;
     if (g.n_phase > 1) max_q = static_cast<int>(cdiv(g.L_y + g.ph_s, g.ph_s)) + 1;
     g.m_tiles = m_tiles;
@@ -659,8 +671,15 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
     const long blocks = static_cast<long>(g.m_tiles) * g.q_tiles * N * g.n_phase;
     if (blocks > 0x7fffffffL) return fail(ctx, KDEC_EINVAL, "conv: grid too large");
     ProfScope ps(ctx, fam, flops);
-    const int rc = with_xpt<LaunchConv>(CK * span, ctx, g, static_cast<unsigned>(blocks), lds);
-    if (rc == -100) return fail(ctx, KDEC_EINVAL, "conv: input window too large");
+    const unsigned nb = static_cast<unsigned>(blocks);
+    switch (CK) {
+        case 2: launch_conv<2>(ctx, g, nb, lds); break;
+        case 4: launch_conv<4>(ctx, g, nb, lds); break;
+        case 8: launch_conv<8>(ctx, g, nb, lds); break;
+        case 16: launch_conv<16>(ctx, g, nb, lds); break;
+        case 32: launch_conv<32>(ctx, g, nb, lds); break;
+        default: return fail(ctx, KDEC_EINVAL, "conv: unsupported channel chunk");
+    }
     return launch_check(ctx, fam);
 }
 
@@ -703,7 +722,7 @@ int kdec_conv1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
     if (!A.p) return KDEC_ENOMEM;
     const long tot = static_cast<long>(cin_pad) * k * m_pad;
     hipLaunchKernelGGL(pack_fwd, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), C_in,
-                       C_out, k, cin_pad, m_pad);
+                       C_out, k, cin_pad, m_pad, CK);
     if (int rc = launch_check(ctx, "pack_fwd")) return rc;
     GemmArgs g{};
     g.X = X; g.x_bs = x_bs; g.A = A.as<float>(); g.a_phase_stride = 0;
@@ -737,7 +756,7 @@ int kdec_conv1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
     if (!A.p) return KDEC_ENOMEM;
     const long tot = static_cast<long>(cpad) * k * m_pad;
     hipLaunchKernelGGL(pack_dgrad, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), C_in,
-                       C_out, k, cpad, m_pad);
+                       C_out, k, cpad, m_pad, CK);
     if (int rc = launch_check(ctx, "pack_dgrad")) return rc;
     GemmArgs g{};
     g.X = dY; g.x_bs = dy_bs; g.A = A.as<float>();
@@ -850,7 +869,7 @@ int kdec_convt1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
     Workspace A(ctx, static_cast<size_t>(ph) * stride * sizeof(float));
     if (!A.p) return KDEC_ENOMEM;
     hipLaunchKernelGGL(pack_convt_fwd, dim3(grid1d(ph * stride)), dim3(256), 0, ctx->stream, W,
-                       A.as<float>(), C_in, C_out, k, stride, kt, cin_pad, m_pad, ph);
+                       A.as<float>(), C_in, C_out, k, stride, kt, cin_pad, m_pad, ph, CK);
     if (int rc = launch_check(ctx, "pack_convt_fwd")) return rc;
     GemmArgs g{};
     g.X = X; g.x_bs = x_bs; g.A = A.as<float>(); g.a_phase_stride = ph;
@@ -883,7 +902,7 @@ int kdec_convt1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
     Workspace A(ctx, static_cast<size_t>(tot) * sizeof(float));
     if (!A.p) return KDEC_ENOMEM;
     hipLaunchKernelGGL(pack_convt_dgrad, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(),
-                       C_in, C_out, k, cpad, m_pad);
+                       C_in, C_out, k, cpad, m_pad, CK);
     if (int rc = launch_check(ctx, "pack_convt_dgrad")) return rc;
     GemmArgs g{};
     g.X = dY; g.x_bs = dy_bs; g.A = A.as<float>();
