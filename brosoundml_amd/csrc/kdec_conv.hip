@@ -27,7 +27,7 @@
 // Weight-grad (`wgrad_gemm`): dW[m, (c, t)] = sum_{n, l} dY[n, m, l] *
 // X[n, c, l*s + t*d - p], a GEMM with the huge position axis as K. It is
 // split over K into deterministic partial tiles that a second kernel sums in
-// a fixed order.
+// a fixed order; the bias grad (row sums of dY) rides along in the same pass.
 #include "kdec_internal.hpp"
 
 #include <algorithm>
@@ -138,6 +138,10 @@ void conv_gemm(GemmArgs g) {
     const int x0 = q0 * s - p;
     const int a_lane = (lane >> 5) * g.m_pad + (lane & 31) * 4;
     const int nitems = CK * segs;
+    // one descriptor for this utterance's input; rows, positions out of range
+    // get an out-of-bounds offset and stage as zeros
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(Xb), static_cast<short>(0), g.C_in * g.L_in * 4, kBufDword3);
 
     // Stage chunk `ch` at LDS float offset `sb`: the weight slab two rows
     // (1 KB) per instruction, the input window 64 positions per instruction.
@@ -149,11 +153,11 @@ void conv_gemm(GemmArgs g) {
         for (int it = wave; it < nitems; it += 4) {
             const int r = it / segs, sg = it - r * segs;
             const int c = ch * CK + r;
-            const float* rowp = Xb + static_cast<long>(c) * g.L_in;
-            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<float*>(rowp), static_cast<short>(0), c < g.C_in ? g.L_in * 4 : 0, kBufDword3);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, smem + sb + KR * BM + r * span_p + sg * 64, 4,
-                                                     (x0 + sg * 64 + lane) * 4, 0, 0, 0);
+            const int pos = x0 + sg * 64 + lane;
+            const unsigned off = (c < g.C_in && pos >= 0 && pos < g.L_in)
+                                     ? static_cast<unsigned>(c * g.L_in + pos) * 4u : 0x80000000u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + KR * BM + r * span_p + sg * 64, 4,
+                                                     static_cast<int>(off), 0, 0, 0);
         }
     };
 
@@ -327,7 +331,14 @@ __global__ void pack_convt_fwd(const float* W, float* A, int C_in, int C_out,
 
 // ─── weight grad ─────────────────────────────────────────────────────────
 
-constexpr int KC = 32;  // positions per K chunk
+constexpr int KC = 32;       // positions per K chunk
+constexpr int WG_WN = 4;                 // waves along n (2 along m)
+constexpr int WG_NT = 128 * WG_WN;       // threads per wgrad block
+constexpr int WG_BN = 64 * WG_WN;        // n columns per wgrad block
+// G tile in LDS: 64 row pairs (m, m + 64) of 2*KC positions at an odd pair
+// stride, so a column read across 32 consecutive m hits 32 distinct banks
+// and one 64-lane load fills a whole pair.
+constexpr int GP = 2 * KC + 1;
 
 struct WgradArgs {
     const float* X;      // correlation input  [n][C_x][L_x]
@@ -340,19 +351,25 @@ struct WgradArgs {
     int NN;              // C_x * k
     int chunks_per_n, total_chunks, chunks_per_split;
     int n_tiles, m_tiles;
+    int XR;              // staged input rows per n-tile
+    int segw, segs;      // input-row staging: segs loads of segw (32 or 64) positions
+    int rs;              // LDS row stride of the staged input rows
 };
 
 // P[z, m, c*k + t] = sum over this split's positions l of
 //   G[n, m, l] * X[n, c, l*s + t*d - p]
 // (and Pb[z, m] = sum of G over the same positions, from the n-tile-0 blocks).
-// 1-D grid of n_tiles * m_tiles * splits blocks, two LDS stages as in
-// conv_gemm.
-template <int XPT>
-__global__ __launch_bounds__(NT) void wgrad_gemm(WgradArgs g) {
+// 1-D grid of n_tiles * m_tiles * splits blocks. Both operands run along the
+// position axis in memory, so they are staged row by row straight into LDS
+// (buffer_load_dword ... lds, zero past each row's end): G as 128 rows of KC
+// positions at an odd row stride, the input window as XR channel rows at a
+// stride rs chosen so that column n = c*k + t lands on bank n*d.
+__global__ __launch_bounds__(WG_NT) __attribute__((amdgpu_waves_per_eu(4)))
+void wgrad_gemm(WgradArgs g) {
     extern __shared__ float smem[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave & 1, wn = wave >> 1;
     const int l32 = lane & 31, hi = lane >> 5;
 
@@ -362,67 +379,53 @@ __global__ __launch_bounds__(NT) void wgrad_gemm(WgradArgs g) {
     const int mt = lid % g.m_tiles;
     const int z = lid / g.m_tiles;
     const int m0 = mt * BM;
-    const int n0 = nt * BN;
+    const int n0 = nt * WG_BN;
     const int k = g.k, s = g.s, d = g.d;
-
     const int ci_lo = n0 / k;
-    const int XR = (BN - 1) / k + 2;                  // staged input rows
-    const int span = (KC - 1) * s + (k - 1) * d + 1;  // staged window
-    const int gsz = KC * (BM + 1);
-    const int stage = gsz + XR * span;
-    const int nx = XR * span;
+    const int gsz = 64 * GP;
+    const int stage = gsz + g.XR * g.rs;
     const bool do_bias = g.Pb && nt == 0;
+    constexpr unsigned OOB = 0x80000000u;  // any offset >= the buffer size reads 0
 
-    // this lane's two B columns
-    int xrow[2], xoff[2];
-    bool ok[2];
+    // this lane's two B columns: staged row offset of (c - ci_lo, t)
+    int xcol[2];
 #pragma unroll
     for (int tn = 0; tn < 2; ++tn) {
         const int n = n0 + wn * 64 + tn * 32 + l32;
-        ok[tn] = n < g.NN;
         const int c = n / k;
-        xrow[tn] = ok[tn] ? (c - ci_lo) : 0;
-        xoff[tn] = ok[tn] ? (n - c * k) * d : 0;
+        xcol[tn] = (c - ci_lo) * g.rs + (n - c * k) * d;
     }
+    const int g_row_lane = lane >> 5;      // 0: row m0 + i, 1: row m0 + i + 64
+    const int g_pos_lane = lane & 31;
 
-    static_assert(BM * KC % NT == 0, "G tile must split evenly over the block");
-    float gr[BM * KC / NT];
-    float xr[XPT];
-    auto gload = [&](int ch) {
+    // One buffer descriptor per utterance; rows, positions and channels out
+    // of range get an out-of-bounds offset and stage as zeros.
+    auto issue = [&](int ch, int sb) {
         const int b = ch / g.chunks_per_n;
         const int l0 = (ch - b * g.chunks_per_n) * KC;
-        const float* Gb = g.G + static_cast<long>(b) * g.g_bs;
-        const float* Xb = g.X + static_cast<long>(b) * g.x_bs;
-#pragma unroll
-        for (int i = 0; i < BM * KC / NT; ++i) {
-            const int idx = tid + i * NT;
-            const int mg = m0 + idx / KC, l = l0 + idx % KC;
-            gr[i] = (mg < g.M && l < g.L_g) ? Gb[static_cast<long>(mg) * g.L_g + l] : 0.0f;
+        const __amdgpu_buffer_rsrc_t grs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(g.G + static_cast<long>(b) * g.g_bs), static_cast<short>(0), g.M * g.L_g * 4,
+            kBufDword3);
+        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(g.X + static_cast<long>(b) * g.x_bs), static_cast<short>(0), g.C_x * g.L_x * 4,
+            kBufDword3);
+        const int l = l0 + g_pos_lane;
+        for (int i = wave; i < 64; i += 2 * WG_WN) {
+            const int m = m0 + i + 64 * g_row_lane;
+            const unsigned off = (m < g.M && l < g.L_g) ? static_cast<unsigned>(m * g.L_g + l) * 4u : OOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(grs, smem + sb + i * GP, 4, static_cast<int>(off), 0, 0, 0);
         }
         const int x0 = l0 * s - g.p;
-#pragma unroll
-        for (int j = 0; j < XPT; ++j) {
-            const int idx = tid + j * NT;
-            float v = 0.0f;
-            if (idx < nx) {
-                const int r = idx / span;
-                const int c = ci_lo + r;
-                const int xi = x0 + (idx - r * span);
-                if (c < g.C_x && xi >= 0 && xi < g.L_x) v = Xb[static_cast<long>(c) * g.L_x + xi];
-            }
-            xr[j] = v;
-        }
-    };
-    auto lstore = [&](float* Gs, float* Xs) {
-#pragma unroll
-        for (int i = 0; i < BM * KC / NT; ++i) {
-            const int idx = tid + i * NT;
-            Gs[(idx % KC) * (BM + 1) + idx / KC] = gr[i];
-        }
-#pragma unroll
-        for (int j = 0; j < XPT; ++j) {
-            const int idx = tid + j * NT;
-            if (idx < nx) Xs[idx] = xr[j];
+        const int nitems = g.XR * g.segs;
+        for (int it = wave; it < nitems; it += 2 * WG_WN) {
+            const int r = it / g.segs, sg = it - r * g.segs;
+            const int c = ci_lo + r;
+            const int pos = x0 + sg * g.segw + lane;
+            const unsigned off = (c < g.C_x && pos >= 0 && pos < g.L_x)
+                                     ? static_cast<unsigned>(c * g.L_x + pos) * 4u : OOB;
+            if (lane < g.segw)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + gsz + r * g.rs + sg * g.segw, 4,
+                                                         static_cast<int>(off), 0, 0, 0);
         }
     };
 
@@ -437,38 +440,54 @@ __global__ __launch_bounds__(NT) void wgrad_gemm(WgradArgs g) {
 
     const int ch0 = z * g.chunks_per_split;
     const int ch1 = min(ch0 + g.chunks_per_split, g.total_chunks);
-    if (ch0 < ch1) {
-        gload(ch0);
-        lstore(smem, smem + gsz);
-    }
+    if (ch0 < ch1) issue(ch0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (int ch = ch0; ch < ch1; ++ch) {
-        const int cur = (ch - ch0) & 1;
-        const float* Gs = smem + cur * stage;
-        const float* Xs = Gs + gsz;
-        if (ch + 1 < ch1) gload(ch + 1);
+        const int sb = ((ch - ch0) & 1) * stage;
+        if (ch + 1 < ch1) issue(ch + 1, stage - sb);
         if (do_bias && tid < BM) {
             float t = 0.0f;
-            for (int kc = 0; kc < KC; ++kc) t += Gs[kc * (BM + 1) + tid];
+            const int row = sb + (tid & 63) * GP + (tid >> 6) * KC;
+            for (int kc = 0; kc < KC; ++kc) t += smem[row + kc];
             bsum += t;
         }
-        const float* xb0 = Xs + xrow[0] * span + xoff[0];
-        const float* xb1 = Xs + xrow[1] * span + xoff[1];
-        for (int kc = 0; kc < KC; kc += 2) {
-            const int kk = kc + hi;
-            const float a0 = Gs[kk * (BM + 1) + wm * 64 + l32];
-            const float a1 = Gs[kk * (BM + 1) + wm * 64 + 32 + l32];
-            const float b0 = ok[0] ? xb0[kk * s] : 0.0f;
-            const float b1 = ok[1] ? xb1[kk * s] : 0.0f;
+        const int ga = sb + l32 * GP + wm * KC + hi;
+        const int xa0 = sb + gsz + xcol[0] + hi * s;
+        const int xa1 = sb + gsz + xcol[1] + hi * s;
+        auto ld = [&](int u, float& a0, float& a1, float& b0, float& b1) {
+            u = min(u, KC / 2 - 1);
+            int go = ga + 2 * u;
+            int xo0 = xa0 + 2 * u * s;
+            int xo1 = xa1 + 2 * u * s;
+            asm volatile("" : "+v"(go), "+v"(xo0), "+v"(xo1));
+            a0 = smem[go];
+            a1 = smem[go + 32 * GP];
+            b0 = smem[xo0];
+            b1 = smem[xo1];
+        };
+        auto mm = [&](float a0, float a1, float b0, float b1) {
             acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
             acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
             acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
             acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+        };
+        float pa0, pa1, pb0, pb1, qa0, qa1, qb0, qb1;
+        ld(0, pa0, pa1, pb0, pb1);
+#pragma unroll
+        for (int u = 0; u < KC / 2; u += 2) {
+            ld(u + 1, qa0, qa1, qb0, qb1);
+            mm(pa0, pa1, pb0, pb1);
+            ld(u + 2, pa0, pa1, pb0, pb1);
+            mm(qa0, qa1, qb0, qb1);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
         }
-        if (ch + 1 < ch1) {
-            float* Gn = smem + (cur ^ 1) * stage;
-            lstore(Gn, Gn + gsz);
-        }
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's staging loads landed
         __syncthreads();
     }
 
@@ -497,7 +516,15 @@ __global__ void wgrad_reduce(const float* P, float* out, long MN, int splits,
     for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < MN;
          i += static_cast<long>(gridDim.x) * blockDim.x) {
         float acc = 0.0f;
-        for (int z = 0; z < splits; ++z) acc += P[z * MN + i];
+        int z = 0;
+        for (; z + 8 <= splits; z += 8) {  // 8 loads in flight, summed in order
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = P[(z + j) * MN + i];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc += v[j];
+        }
+        for (; z < splits; ++z) acc += P[z * MN + i];
         long o = i;
         if (transpose_k) {
             const int k = transpose_k;
@@ -626,18 +653,6 @@ int grid1d(long n) {
     return static_cast<int>(g);
 }
 
-// Registers per thread that stage the input window (XPT) for a chunk of
-// `n` floats; each instance covers n <= XPT * NT.
-template <template <int> class F, class... Args>
-int with_xpt(int n, Args&&... args) {
-    if (n <= 4 * NT) return F<4>::run(args...);
-    if (n <= 8 * NT) return F<8>::run(args...);
-    if (n <= 16 * NT) return F<16>::run(args...);
-    if (n <= 24 * NT) return F<24>::run(args...);
-    if (n <= 40 * NT) return F<40>::run(args...);
-    return -100;
-}
-
 template <int CK>
 int launch_conv(kdec_ctx* ctx, const GemmArgs& g, unsigned blocks, size_t lds) {
     static bool attr = false;
@@ -663,7 +678,8 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
     const size_t stage = static_cast<size_t>(CK) * kk * BM + static_cast<size_t>(CK) * span_p;
     const size_t lds = 2 * stage * sizeof(float);
     if (lds > 160 * 1024) return fail(ctx, KDEC_EINVAL, "conv: tile does not fit LDS");
-    if (static_cast<long>(g.L_in) * 4 > 0x7fffffffL) return fail(ctx, KDEC_EINVAL, "conv: input rows too long");
+    if (static_cast<long>(g.C_in) * g.L_in * 4 > 0x7fffffffL)
+        return fail(ctx, KDEC_EINVAL, "conv: input too large for one buffer descriptor");
     int max_q = g.n_q;
     if (g.n_phase > 1) max_q = static_cast<int>(cdiv(g.L_y + g.ph_s, g.ph_s)) + 1;
     g.m_tiles = m_tiles;
@@ -682,20 +698,6 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
     }
     return launch_check(ctx, fam);
 }
-
-template <int XPT>
-struct LaunchWgrad {
-    static int run(kdec_ctx* ctx, const WgradArgs& a, unsigned blocks, size_t lds) {
-        static bool attr = false;
-        if (!attr) {
-            hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_gemm<XPT>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-            attr = true;
-        }
-        hipLaunchKernelGGL(wgrad_gemm<XPT>, dim3(blocks), dim3(NT), lds, ctx->stream, a);
-        return 0;
-    }
-};
 
 }  // namespace
 }  // namespace kdec
@@ -769,6 +771,61 @@ int kdec_conv1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
                     2.0 * N * C_out * static_cast<double>(L_out) * C_in * k);
 }
 
+// LDS bytes of one wgrad_gemm block (two stages) and its input-row layout.
+struct WgradLayout {
+    int XR, segw, segs, rs;
+    size_t lds;
+};
+
+WgradLayout wgrad_layout(int k, int s, int d) {
+    WgradLayout w{};
+    w.XR = (WG_BN - 1) / k + 2;
+    const long span = static_cast<long>(KC - 1) * s + static_cast<long>(k - 1) * d + 1;
+    w.segw = span <= 32 ? 32 : 64;
+    w.segs = static_cast<int>(cdiv(span, w.segw));
+    // column n = c*k + t sits at c*rs + t*d: rs = k*d (mod 64) puts it on
+    // bank n*d, distinct across 32 lanes for odd d; for k = 1 any odd rs.
+    const long base = static_cast<long>(w.segs) * w.segw;
+    long rs = base;
+    if (k == 1) {
+        if (rs % 2 == 0) ++rs;
+    } else {
+        const long want = (static_cast<long>(k) * d) % 64;
+        rs = base + ((want - base % 64) % 64 + 64) % 64;
+    }
+    w.rs = static_cast<int>(rs);
+    w.lds = 2 * (static_cast<size_t>(64) * GP + static_cast<size_t>(w.XR) * w.rs) * sizeof(float);
+    return w;
+}
+
+size_t wgrad_lds_bytes(int k, int s, int d) { return wgrad_layout(k, s, d).lds; }
+
+#ifndef WG_ROUNDS
+#define WG_ROUNDS 4
+#endif
+void wgrad_allow_large_lds() {
+    static bool done = false;
+    if (!done) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_gemm),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        done = true;
+    }
+}
+
+int wgrad_splits(kdec_ctx* ctx, int total_chunks, long tiles, size_t lds) {
+    wgrad_allow_large_lds();
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&wgrad_gemm), WG_NT,
+                                                     lds) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    const long slots = static_cast<long>(ctx->num_cus) * per_cu * WG_ROUNDS;
+    long splits = (slots + tiles - 1) / tiles;
+    if (splits < 1) splits = 1;
+    if (splits > total_chunks) splits = total_chunks;
+    const long cps = (total_chunks + splits - 1) / splits;
+    return static_cast<int>((total_chunks + cps - 1) / cps);
+}
+
 // out (M x C_x*k) += the weight grad; db (M) += the row sums of G when
 // non-null (fused into the GEMM's n-tile-0 blocks).
 static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G,
@@ -776,15 +833,14 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
                         int s, int d, int p, float* out, float* db, const char* fam) {
     const int NN = C_x * k;
     const int m_tiles = static_cast<int>(cdiv(M, BM));
-    const int n_tiles = static_cast<int>(cdiv(NN, BN));
+    const int n_tiles = static_cast<int>(cdiv(NN, WG_BN));
     const int chunks_per_n = static_cast<int>(cdiv(L_g, KC));
     const int total_chunks = chunks_per_n * N;
-    // aim for ~2048 blocks in flight, but keep >= 8 chunks per split
-    long want = 2048 / (static_cast<long>(m_tiles) * n_tiles);
-    if (want < 1) want = 1;
-    int cps = static_cast<int>(cdiv(total_chunks, want));
-    if (cps < 8) cps = 8;
-    const int splits = static_cast<int>(cdiv(total_chunks, cps));
+    // one round of resident blocks: the fewest splits (least partial traffic)
+    // that still fills every CU
+    const int splits = wgrad_splits(ctx, total_chunks, static_cast<long>(m_tiles) * n_tiles,
+                                    wgrad_lds_bytes(k, s, d));
+    const int cps = static_cast<int>(cdiv(total_chunks, splits));
     const long MN = static_cast<long>(M) * NN;
     Workspace P(ctx, static_cast<size_t>(splits) * MN * sizeof(float));
     Workspace Pb(ctx, db ? static_cast<size_t>(splits) * M * sizeof(float) : 0);
@@ -797,16 +853,22 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
     a.chunks_per_split = cps;
     a.n_tiles = n_tiles;
     a.m_tiles = m_tiles;
-    const int XR = (BN - 1) / k + 2;
-    const int span = (KC - 1) * s + (k - 1) * d + 1;
-    const size_t stage = static_cast<size_t>(KC) * (BM + 1) + static_cast<size_t>(XR) * span;
-    const size_t lds = 2 * stage * sizeof(float);
+    const WgradLayout lay = wgrad_layout(k, s, d);
+    a.XR = lay.XR;
+    a.segw = lay.segw;
+    a.segs = lay.segs;
+    a.rs = lay.rs;
+    if (static_cast<long>(L_x) * 4 > 0x7fffffffL || static_cast<long>(L_g) * 4 > 0x7fffffffL)
+        return fail(ctx, KDEC_EINVAL, "wgrad: rows too long");
+    if (static_cast<long>(M) * L_g * 4 > 0x7fffffffL || static_cast<long>(C_x) * L_x * 4 > 0x7fffffffL)
+        return fail(ctx, KDEC_EINVAL, "wgrad: operand too large for one buffer descriptor");
+    const size_t lds = lay.lds;
     if (lds > 160 * 1024) return fail(ctx, KDEC_EINVAL, "wgrad: tile does not fit LDS");
     const long blocks = static_cast<long>(n_tiles) * m_tiles * splits;
     {
         ProfScope ps(ctx, fam, 2.0 * N * M * static_cast<double>(L_g) * NN);
-        const int rc = with_xpt<LaunchWgrad>(XR * span, ctx, a, static_cast<unsigned>(blocks), lds);
-        if (rc == -100) return fail(ctx, KDEC_EINVAL, "wgrad: input window too large");
+        wgrad_allow_large_lds();
+        hipLaunchKernelGGL(wgrad_gemm, dim3(static_cast<unsigned>(blocks)), dim3(WG_NT), lds, ctx->stream, a);
         if (int rc2 = launch_check(ctx, fam)) return rc2;
     }
     hipLaunchKernelGGL(wgrad_reduce, dim3(grid1d(MN)), dim3(256), 0, ctx->stream, P.as<float>(), out, MN,

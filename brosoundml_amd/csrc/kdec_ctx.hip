@@ -114,6 +114,9 @@ int kdec_ctx_create(int device, kdec_ctx** out) {
     if (e != hipSuccess) return KDEC_EHIP;
     kdec_ctx* c = new kdec_ctx();
     c->device = device;
+    if (hipDeviceGetAttribute(&c->num_cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+        c->num_cus <= 0)
+        c->num_cus = 256;
     e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         delete c;

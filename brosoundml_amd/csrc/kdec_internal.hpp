@@ -14,6 +14,7 @@
 
 struct kdec_ctx {
     int device = 0;
+    int num_cus = 0;  // compute units of the device
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     std::string err;
