@@ -190,6 +190,7 @@ int kdec_free(kdec_ctx* ctx, void* ptr) {
 int kdec_profile_enable(kdec_ctx* ctx, int on) {
     if (!ctx) return KDEC_EINVAL;
     ctx->prof = on != 0;
+    for (kdec_ctx* p : ctx->peers) kdec_profile_enable(p, on);
     return KDEC_OK;
 }
 
@@ -202,6 +203,8 @@ int kdec_profile_reset(kdec_ctx* ctx) {
             ctx->event_pool.push_back(pr.second);
         }
     ctx->fams.clear();
+    for (kdec_ctx* p : ctx->peers)
+        if (int rc = kdec_profile_reset(p)) return rc;
     return KDEC_OK;
 }
 
@@ -209,6 +212,17 @@ int kdec_profile_read(kdec_ctx* ctx, const char** names, double* ms,
                       long* launches, double* flops, int cap) {
     if (!ctx) return KDEC_EINVAL;
     KDEC_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    // fold the peers' families in (their events are on their own streams)
+    for (kdec_ctx* p : ctx->peers) {
+        if (kdec_profile_read(p, nullptr, nullptr, nullptr, nullptr, 0) < 0) return KDEC_EHIP;
+        for (auto& kv : p->fams) {
+            auto& f = ctx->fams[kv.first];
+            f.ms += kv.second.ms;
+            f.launches += kv.second.launches;
+            f.flops += kv.second.flops;
+        }
+        p->fams.clear();
+    }
     int i = 0;
     for (auto& kv : ctx->fams) {
         auto& f = kv.second;

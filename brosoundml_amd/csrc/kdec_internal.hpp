@@ -39,6 +39,9 @@ struct kdec_ctx {
     bool prof = false;
     std::map<std::string, Family> fams;
     std::vector<hipEvent_t> event_pool;
+    // Contexts whose streams run work forked from this one (a model's side
+    // stream); their profiles follow this context's enable / reset / read.
+    std::vector<kdec_ctx*> peers;
 };
 
 namespace kdec {

@@ -61,6 +61,12 @@ struct kdec_model {
     bd::GeneratorCache genc;
     Tensor gen_in, har;
     std::string err;
+
+    // The harmonic source depends only on F0: it runs on a side context's
+    // stream, forked after the inputs and joined before the generator, so it
+    // overlaps the style projection and the backbone.
+    kdec_ctx* side = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
 };
 
 namespace {
@@ -280,6 +286,14 @@ int kdec_model_create(kdec_ctx* ctx, const int* v, int n, kdec_model** out) {
         delete m;
         return KDEC_EINVAL;
     }
+    if (kdec_ctx_create(ctx->device, &m->side) != KDEC_OK ||
+        hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&m->ev_join, hipEventDisableTiming) != hipSuccess) {
+        kdec_model_destroy(m);
+        return kdec::fail(ctx, KDEC_EHIP, "kdec_model_create: side stream");
+    }
+    m->side->prof = ctx->prof;
+    ctx->peers.push_back(m->side);
     try {
         bt::set_runtime(ctx);
         std::vector<Spec> specs;
@@ -319,6 +333,20 @@ int kdec_model_create(kdec_ctx* ctx, const int* v, int n, kdec_model** out) {
 }
 
 int kdec_model_destroy(kdec_model* m) {
+    if (!m) return KDEC_OK;
+    if (m->side) {
+        hipStreamSynchronize(m->side->stream);
+        auto& pv = m->ctx->peers;
+        for (auto it = pv.begin(); it != pv.end(); ++it)
+            if (*it == m->side) {
+                pv.erase(it);
+                break;
+            }
+        kdec_ctx_destroy(m->side);
+        m->side = nullptr;
+    }
+    if (m->ev_fork) hipEventDestroy(m->ev_fork);
+    if (m->ev_join) hipEventDestroy(m->ev_join);
     delete m;
     return KDEC_OK;
 }
@@ -467,15 +495,34 @@ int kdec_model_forward(kdec_model* m, int N, int T, const float* asr, const floa
         for (auto& a : m->naff) rb(a);
         for (auto& a : m->raff) rb(a);
 
-        // harmonic source
-        int sig = 0, frames = 0;
-        m->hs.forward(in(F0, 2 * T), 2 * T, sig, frames, m->har);
+        // harmonic source (side stream) -- HarmonicSource::forward's work
+        const auto& hs = m->hs;
+        const int sig = 2 * T * hs.upsample_scale;
+        const int frames = sig / hs.hop_size + 1;
+        hipStream_t ms = static_cast<hipStream_t>(kdec_get_stream(m->ctx));
+        bool forked = false;
         if (har_in) {
             Tensor h = in(har_in, (m->n_fft + 2) * frames);
             m->har = h.clone();
+        } else {
+            m->har = Tensor::empty_on(Device::HIP, N, (m->n_fft + 2) * frames);
+            if (hipEventRecord(m->ev_fork, ms) != hipSuccess ||
+                hipStreamWaitEvent(m->side->stream, m->ev_fork, 0) != hipSuccess)
+                return fail(m, KDEC_EHIP, "kdec_model_forward: fork");
+            const int rc = kdec_harmonic_source(m->side, F0, 2 * T, static_cast<float*>(m->har.data),
+                                                (m->n_fft + 2) * frames, N, 2 * T,
+                                                static_cast<const float*>(hs.l_linear.W.data),
+                                                static_cast<const float*>(hs.l_linear.b.data), hs.harmonic_num,
+                                                hs.sample_rate, hs.upsample_scale, hs.n_fft, hs.hop_size);
+            if (rc != KDEC_OK) return fail(m, rc, std::string("harmonic source: ") + kdec_last_error(m->side));
+            if (hipEventRecord(m->ev_join, m->side->stream) != hipSuccess)
+                return fail(m, KDEC_EHIP, "kdec_model_forward: join");
+            forked = true;
         }
         bd::decoder_backbone_forward_train(m->bb, in(asr, m->asr_dim * T), in(F0, 2 * T), in(Nn, 2 * T), T,
                                            m->bbaff, 1e-5f, m->gen_in, m->bbc);
+        if (forked && hipStreamWaitEvent(ms, m->ev_join, 0) != hipSuccess)
+            return fail(m, KDEC_EHIP, "kdec_model_forward: join");
         const int init_C = m->dec_out[n_dec - 1];
         const int L_gen = m->gen_in.cols / init_C;
         Tensor out;

@@ -155,36 +155,64 @@ __global__ __launch_bounds__(FT) void spec_bwd_k(const float* post, long post_bs
 }
 
 // ─── harmonic source ───
-// One lane per (utterance, harmonic): the reference's sequential float phase
-// recurrence (kokoro_modules.cpp:1602-1617), evaluated with contraction off so
-// each step rounds exactly as the host loop does.
+// One lane per (utterance, harmonic) chain i = b*H + h: the reference's
+// sequential float phase recurrence (kokoro_modules.cpp:1602-1617), evaluated
+// with contraction off so each step rounds exactly as the host loop does.
+// Layout groups four steps per chain: phase[((t/4)*NH + i)*4 + t%4], so a
+// wave writes four steps of all its chains with one contiguous float4 store
+// (a store per step would leave the lone wave waiting on its store queue).
+__device__ inline long hs_index(int t, int i, int NH) {
+    return (static_cast<long>(t >> 2) * NH + i) * 4 + (t & 3);
+}
+
 __global__ void hs_phase_k(const float* F0, long f0_bs, float* phase, int N, int H, int frame_count,
                            int us, int sig_len, float sr) {
 #pragma clang fp contract(off)
+    const int NH = N * H;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= N * H) return;
+    if (i >= NH) return;
     const int b = i / H, h = i - b * H;
     const float kTwoPi = 6.28318530717958647692f;
     const float* f0r = F0 + b * f0_bs;
-    float* out = phase + static_cast<long>(i) * sig_len;
     float ph = 0.0f;
     for (int fr = 0; fr * us < sig_len; ++fr) {
         const float f0 = f0r[fr < frame_count ? fr : frame_count - 1];
         float omega = kTwoPi * static_cast<float>(h + 1);
         omega = omega * f0;
         omega = omega / sr;
-        const int t1 = min((fr + 1) * us, sig_len);
-        for (int t = fr * us; t < t1; ++t) {
+        const int t0 = fr * us;
+        const int t1 = min(t0 + us, sig_len);
+        int t = t0;
+        if ((t0 & 3) == 0) {
+            float4* out4 = reinterpret_cast<float4*>(phase) + static_cast<long>(t0 >> 2) * NH + i;
+            for (; t + 4 <= t1; t += 4, out4 += NH) {
+                float4 v;
+                ph = ph + omega;
+                if (ph > kTwoPi) ph = ph - kTwoPi;
+                v.x = ph;
+                ph = ph + omega;
+                if (ph > kTwoPi) ph = ph - kTwoPi;
+                v.y = ph;
+                ph = ph + omega;
+                if (ph > kTwoPi) ph = ph - kTwoPi;
+                v.z = ph;
+                ph = ph + omega;
+                if (ph > kTwoPi) ph = ph - kTwoPi;
+                v.w = ph;
+                *out4 = v;
+            }
+        }
+        for (; t < t1; ++t) {
             ph = ph + omega;
             if (ph > kTwoPi) ph = ph - kTwoPi;
-            out[t] = ph;
+            phase[hs_index(t, i, NH)] = ph;
         }
     }
 }
 
 // merged[b, t] = tanh(lb + sum_h lW[h] * sin(phase) * amp * uv)
 __global__ void hs_merge_k(const float* phase, const float* F0, long f0_bs, const float* lW,
-                           const float* lb, float* merged, int H, int frame_count, int us,
+                           const float* lb, float* merged, int N, int H, int frame_count, int us,
                            int sig_len) {
 #pragma clang fp contract(off)
     const int b = blockIdx.y;
@@ -195,7 +223,7 @@ __global__ void hs_merge_k(const float* phase, const float* F0, long f0_bs, cons
     const float uv = f0 > 0.0f ? 1.0f : 0.0f;
     double acc = lb[0];
     for (int h = 0; h < H; ++h) {
-        const float ph = phase[(static_cast<long>(b) * H + h) * sig_len + t];
+        const float ph = phase[hs_index(t, b * H + h, N * H)];
         float sv = static_cast<float>(sin(static_cast<double>(ph)));
         sv = sv * 0.1f;
         sv = sv * uv;
@@ -361,7 +389,7 @@ int kdec_harmonic_source(kdec_ctx* ctx, const float* F0, long f0_bs,
     KDEC_CHECK(ctx, sig > n_fft / 2, "kdec_harmonic_source: signal shorter than the STFT pad");
     const int frames = sig / hop + 1;
     KDEC_CHECK(ctx, har_bs >= static_cast<long>(n_fft + 2) * frames, "kdec_harmonic_source: har stride too small");
-    Workspace ph(ctx, static_cast<size_t>(N) * H * sig * sizeof(float));
+    Workspace ph(ctx, static_cast<size_t>(N) * H * ((sig + 3) / 4 * 4) * sizeof(float));
     Workspace mg(ctx, static_cast<size_t>(N) * sig * sizeof(float));
     if (!ph.p || !mg.p) return KDEC_ENOMEM;
     ProfScope ps(ctx, "harmonic_source", 0);
@@ -370,7 +398,7 @@ int kdec_harmonic_source(kdec_ctx* ctx, const float* F0, long f0_bs,
                        static_cast<float>(sample_rate));
     if (int rc = launch_check(ctx, "hs_phase")) return rc;
     hipLaunchKernelGGL(hs_merge_k, dim3(static_cast<unsigned>(cdiv(sig, 256)), N), dim3(256), 0, ctx->stream,
-                       ph.as<float>(), F0, f0_bs, lW, lb, mg.as<float>(), H, frame_count, upsample_scale, sig);
+                       ph.as<float>(), F0, f0_bs, lW, lb, mg.as<float>(), N, H, frame_count, upsample_scale, sig);
     if (int rc = launch_check(ctx, "hs_merge")) return rc;
     hipLaunchKernelGGL(hs_stft_k, dim3(static_cast<unsigned>(cdiv(frames, FT)), N), dim3(FT), 0, ctx->stream,
                        mg.as<float>(), har, har_bs, sig, n_fft, hop, frames);

@@ -149,3 +149,32 @@ def test_backward_is_linear_in_daudio(ctx):
         if "m_source" in n:
             continue
         np.testing.assert_allclose(outs[1][n], 2.0 * outs[0][n], rtol=1e-5, atol=1e-6)
+
+
+def test_in_model_harmonic_source_matches_op(ctx):
+    # The model runs the harmonic source on a side stream joined before the
+    # generator; its waveform must equal, bit for bit, a forward fed the
+    # harmonic-source op's output computed on its own. T is long enough that
+    # the side-stream work outlasts the (tiny) backbone, so a missing join
+    # would show.
+    from brosoundml_amd import native
+    cfg, N, T = C.TINY, 2, 96
+    m = native.Model(ctx, cfg)
+    shapes = m.param_shapes()
+    params = synth.init_params(shapes)
+    m.set_params(params)
+    asr, F0, Nn, style, _ = inputs(cfg, N, T, "gm.hs")
+    F0[0, 5:9] = 0.0
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    t = [dev(a) for a in (asr, F0, Nn, style)]
+    a1 = m.forward(*t, T).clone()
+    L = C.lengths(cfg, T)
+    us = int(np.prod(cfg["ups_rates"][:cfg["n_ups"]])) * cfg["hop"]
+    har = torch.empty(N, (cfg["n_fft"] + 2) * L["frames"], device="cuda")
+    g = "decoder.module.generator.m_source.l_linear."
+    lW, lb = dev(params[g + "weight"]), dev(params[g + "bias"])
+    ctx.call("kdec_harmonic_source", native.ptr(t[1]), 2 * T, native.ptr(har), har.shape[1], N, 2 * T,
+             native.ptr(lW), native.ptr(lb), cfg["harmonic_num"], cfg["sample_rate"], us, cfg["n_fft"], cfg["hop"])
+    a2 = m.forward(*t, T, har=har)
+    torch.cuda.synchronize()
+    assert torch.equal(a1, a2)
