@@ -33,29 +33,58 @@ __device__ inline double block_sum(double v, double* red) {
     return r;
 }
 
-// stats[row] = (mean, rstd) of x[row, :L]; row = n*C + c.
-__global__ __launch_bounds__(RT) void instnorm_stats_k(const float* X, long x_bs, int C, int L,
-                                                      float eps, float2* stats) {
+// Rows are cut into chunks of CH elements (EPT per thread, all loads issued
+// before use so each thread keeps EPT reads in flight); per-chunk partial
+// sums are reduced per row in a fixed order.
+constexpr int EPT = 16;
+constexpr int CH = RT * EPT;
+
+// part[row*nch + ch] = (sum(x - x0), sum((x - x0)^2)) over chunk ch, with the
+// row's first element x0 as shift (a well-conditioned variance); row = n*C + c.
+__global__ __launch_bounds__(RT) void instnorm_part_k(const float* X, long x_bs, int C, int L, int nch,
+                                                     double2* part) {
     __shared__ double red[RT / 64];
-    const int row = blockIdx.x;
+    const int row = blockIdx.y, ch = blockIdx.x;
     const int n = row / C, c = row - n * C;
     const float* x = X + n * x_bs + static_cast<long>(c) * L;
-    const double x0 = x[0];  // shift for a well-conditioned variance
+    const float x0f = x[0];
+    const double x0 = x0f;
+    const int l0 = ch * CH + threadIdx.x;
+    float v[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int l = l0 + j * RT;
+        v[j] = l < L ? x[l] : x0f;  // padding adds exact zeros
+    }
     double s1 = 0.0, s2 = 0.0;
-    for (int l = threadIdx.x; l < L; l += RT) {
-        const double v = static_cast<double>(x[l]) - x0;
-        s1 += v;
-        s2 += v * v;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const double d = static_cast<double>(v[j]) - x0;
+        s1 += d;
+        s2 += d * d;
     }
     s1 = block_sum(s1, red);
     s2 = block_sum(s2, red);
-    if (threadIdx.x == 0) {
-        const double m = s1 / L;
-        double var = s2 / L - m * m;
-        if (var < 0.0) var = 0.0;
-        stats[row] = make_float2(static_cast<float>(x0 + m),
-                                 static_cast<float>(1.0 / sqrt(var + static_cast<double>(eps))));
+    if (threadIdx.x == 0) part[static_cast<long>(row) * nch + ch] = make_double2(s1, s2);
+}
+
+// stats[row] = (mean, 1/sqrt(var + eps)) from the row's chunk partials.
+__global__ void instnorm_fin_k(const float* X, long x_bs, int C, int L, int rows, int nch, const double2* part,
+                               float eps, float2* stats) {
+    const int row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= rows) return;
+    const int n = row / C, c = row - n * C;
+    const double x0 = X[n * x_bs + static_cast<long>(c) * L];
+    double s1 = 0.0, s2 = 0.0;
+    for (int ch = 0; ch < nch; ++ch) {
+        const double2 p = part[static_cast<long>(row) * nch + ch];
+        s1 += p.x;
+        s2 += p.y;
     }
+    const double m = s1 / L;
+    double var = s2 / L - m * m;
+    if (var < 0.0) var = 0.0;
+    stats[row] = make_float2(static_cast<float>(x0 + m), static_cast<float>(1.0 / sqrt(var + static_cast<double>(eps))));
 }
 
 struct AdainArgs {
@@ -80,7 +109,7 @@ __device__ inline float act_fwd(int act, float s, float slope, float a) {
     return s;
 }
 
-// grid (chunks, N*C)
+// grid (chunks of CH, N*C)
 __global__ __launch_bounds__(RT) void adain_act_fwd_k(AdainArgs g, float* Y, long y_bs, float* Yp,
                                                      long yp_bs) {
     const int row = blockIdx.y;
@@ -93,24 +122,42 @@ __global__ __launch_bounds__(RT) void adain_act_fwd_k(AdainArgs g, float* Y, lon
     const float* x = g.X + n * g.x_bs + off;
     float* y = Y + n * y_bs + off;
     float* yp = Yp ? Yp + n * yp_bs + off : nullptr;
-    for (int l = blockIdx.x * RT + threadIdx.x; l < g.L; l += gridDim.x * RT) {
-        const float xh = (x[l] - st.x) * st.y;
+    const int l0 = blockIdx.x * CH + threadIdx.x;
+    float v[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int l = l0 + j * RT;
+        v[j] = l < g.L ? x[l] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int l = l0 + j * RT;
+        if (l >= g.L) break;
+        const float xh = (v[j] - st.x) * st.y;
         const float s = g1 * xh + bt;
         if (yp) yp[l] = s;
         y[l] = act_fwd(g.act, s, g.slope, a);
     }
 }
 
-// One block per (n, c) row. Pass 1 reduces sum(ds), sum(ds*xh) (and the snake
-// alpha grad); pass 2 writes dx. ds = dY * act'(s) is the grad at the affine
-// output; dgamma = sum(ds*xh), dbeta = sum(ds);
-// dx = rstd * g1 * (ds - mean(ds) - xh * mean(ds*xh)) (+ R).
-__global__ __launch_bounds__(RT) void adain_act_bwd_k(AdainArgs g, const float* dY, long dy_bs,
-                                                     const float* R, long r_bs, float* dX,
-                                                     long dx_bs, float* dgamma, float* dbeta,
-                                                     long dgb_bs, float* dalpha_part) {
+// ds = dY * act'(s): the grad at the affine output, s = g1 * xh + beta.
+__device__ inline float act_bwd(int act, float dy, float s, float slope, float a, double& sa) {
+    if (act == KDEC_ACT_LEAKY) return s > 0.0f ? dy : slope * dy;
+    if (act == KDEC_ACT_SNAKE) {
+        const float s2 = sinf(2.0f * a * s);
+        const float sn = sinf(a * s);
+        sa += static_cast<double>(dy) * (s * s2 / a - sn * sn / (a * a));
+        return dy * (1.0f + s2);
+    }
+    return dy;
+}
+
+// part[(row*nch + ch)*3 + {0,1,2}] = chunk sums of ds, ds*xh and (SNAKE) the
+// alpha-grad integrand; dgamma = sum(ds*xh), dbeta = sum(ds).
+__global__ __launch_bounds__(RT) void adain_bwd_part_k(AdainArgs g, const float* dY, long dy_bs, int nch,
+                                                      double* part) {
     __shared__ double red[RT / 64];
-    const int row = blockIdx.x;
+    const int row = blockIdx.y, ch = blockIdx.x;
     const int n = row / g.C, c = row - n * g.C;
     const float2 st = g.stats[row];
     const float g1 = 1.0f + g.gamma[n * g.gb_bs + c];
@@ -119,43 +166,93 @@ __global__ __launch_bounds__(RT) void adain_act_bwd_k(AdainArgs g, const float* 
     const long off = static_cast<long>(c) * g.L;
     const float* x = g.X + n * g.x_bs + off;
     const float* dy = dY + n * dy_bs + off;
+    const int l0 = ch * CH + threadIdx.x;
+    float xv[EPT], dv[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int l = l0 + j * RT;
+        const bool in = l < g.L;
+        xv[j] = in ? x[l] : st.x;   // xh = 0 and ds = 0 past the row: no contribution
+        dv[j] = in ? dy[l] : 0.0f;
+    }
     double sd = 0.0, sdx = 0.0, sa = 0.0;
-    for (int l = threadIdx.x; l < g.L; l += RT) {
-        const float xh = (x[l] - st.x) * st.y;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const float xh = (xv[j] - st.x) * st.y;
         const float s = g1 * xh + bt;
-        float ds = dy[l];
-        if (g.act == KDEC_ACT_LEAKY) {
-            ds = s > 0.0f ? ds : g.slope * ds;
-        } else if (g.act == KDEC_ACT_SNAKE) {
-            const float s2 = sinf(2.0f * a * s);
-            const float sn = sinf(a * s);
-            sa += static_cast<double>(dy[l]) * (s * s2 / a - sn * sn / (a * a));
-            ds = ds * (1.0f + s2);
-        }
+        const float ds = act_bwd(g.act, dv[j], s, g.slope, a, sa);
         sd += ds;
         sdx += static_cast<double>(ds) * xh;
     }
     sd = block_sum(sd, red);
     sdx = block_sum(sdx, red);
-    if (g.act == KDEC_ACT_SNAKE && dalpha_part) sa = block_sum(sa, red);
+    if (g.act == KDEC_ACT_SNAKE) sa = block_sum(sa, red);
     if (threadIdx.x == 0) {
-        if (dgamma) dgamma[n * dgb_bs + c] = static_cast<float>(sdx);
-        if (dbeta) dbeta[n * dgb_bs + c] = static_cast<float>(sd);
-        if (g.act == KDEC_ACT_SNAKE && dalpha_part) dalpha_part[row] = static_cast<float>(sa);
+        double* p = part + (static_cast<long>(row) * nch + ch) * 3;
+        p[0] = sd;
+        p[1] = sdx;
+        p[2] = sa;
     }
-    const float mds = static_cast<float>(sd / g.L);
-    const float mdsx = static_cast<float>(sdx / g.L);
+}
+
+// Per row: dgamma / dbeta (overwritten), the row's alpha-grad share, and the
+// two means the input grad needs.
+__global__ void adain_bwd_fin_k(const double* part, int rows, int nch, int C, int L, float* dgamma, float* dbeta,
+                                long dgb_bs, float* dalpha_part, float2* rowv) {
+    const int row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= rows) return;
+    const int n = row / C, c = row - n * C;
+    double sd = 0.0, sdx = 0.0, sa = 0.0;
+    for (int ch = 0; ch < nch; ++ch) {
+        const double* p = part + (static_cast<long>(row) * nch + ch) * 3;
+        sd += p[0];
+        sdx += p[1];
+        sa += p[2];
+    }
+    if (dgamma) dgamma[n * dgb_bs + c] = static_cast<float>(sdx);
+    if (dbeta) dbeta[n * dgb_bs + c] = static_cast<float>(sd);
+    if (dalpha_part) dalpha_part[row] = static_cast<float>(sa);
+    rowv[row] = make_float2(static_cast<float>(sd / L), static_cast<float>(sdx / L));
+}
+
+// dx = rstd * g1 * (ds - mean(ds) - xh * mean(ds*xh)) (+ R); grid (chunks, N*C)
+__global__ __launch_bounds__(RT) void adain_bwd_apply_k(AdainArgs g, const float* dY, long dy_bs,
+                                                       const float* R, long r_bs, float* dX, long dx_bs,
+                                                       const float2* rowv) {
+    const int row = blockIdx.y;
+    const int n = row / g.C, c = row - n * g.C;
+    const float2 st = g.stats[row];
+    const float g1 = 1.0f + g.gamma[n * g.gb_bs + c];
+    const float bt = g.beta ? g.beta[n * g.gb_bs + c] : 0.0f;
+    const float a = g.act == KDEC_ACT_SNAKE ? g.alpha[c] : 0.0f;
+    const float2 mv = rowv[row];
     const float k1 = st.y * g1;
-    float* dx = dX + n * dx_bs + off;
+    const long off = static_cast<long>(c) * g.L;
+    const float* x = g.X + n * g.x_bs + off;
+    const float* dy = dY + n * dy_bs + off;
     const float* r = R ? R + n * r_bs + off : nullptr;
-    for (int l = threadIdx.x; l < g.L; l += RT) {
-        const float xh = (x[l] - st.x) * st.y;
+    float* dx = dX + n * dx_bs + off;
+    const int l0 = blockIdx.x * CH + threadIdx.x;
+    float xv[EPT], dv[EPT], rv[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int l = l0 + j * RT;
+        const bool in = l < g.L;
+        xv[j] = in ? x[l] : 0.0f;
+        dv[j] = in ? dy[l] : 0.0f;
+        rv[j] = (in && r) ? r[l] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int l = l0 + j * RT;
+        if (l >= g.L) break;
+        const float xh = (xv[j] - st.x) * st.y;
         const float s = g1 * xh + bt;
-        float ds = dy[l];
+        float ds = dv[j];
         if (g.act == KDEC_ACT_LEAKY) ds = s > 0.0f ? ds : g.slope * ds;
         else if (g.act == KDEC_ACT_SNAKE) ds = ds * (1.0f + sinf(2.0f * a * s));
-        float v = k1 * (ds - mds - xh * mdsx);
-        if (r) v += r[l];
+        float v = k1 * (ds - mv.x - xh * mv.y);
+        if (r) v += rv[j];
         dx[l] = v;
     }
 }
@@ -284,10 +381,17 @@ int kdec_instnorm_stats(kdec_ctx* ctx, const float* X, long x_bs, int N,
     if (!ctx) return KDEC_EINVAL;
     KDEC_CHECK(ctx, X && stats && N > 0 && C > 0 && L > 0 && x_bs >= static_cast<long>(C) * L,
                "kdec_instnorm_stats: bad arguments");
+    const int rows = N * C;
+    const int nch = static_cast<int>(cdiv(L, CH));
+    Workspace part(ctx, static_cast<size_t>(rows) * nch * sizeof(double2));
+    if (!part.p) return KDEC_ENOMEM;
     ProfScope ps(ctx, "adain_fwd", 0);
-    hipLaunchKernelGGL(instnorm_stats_k, dim3(N * C), dim3(RT), 0, ctx->stream, X, x_bs, C, L, eps,
-                       reinterpret_cast<float2*>(stats));
-    return launch_check(ctx, "instnorm_stats");
+    hipLaunchKernelGGL(instnorm_part_k, dim3(nch, rows), dim3(RT), 0, ctx->stream, X, x_bs, C, L, nch,
+                       part.as<double2>());
+    if (int rc = launch_check(ctx, "instnorm_part")) return rc;
+    hipLaunchKernelGGL(instnorm_fin_k, dim3(static_cast<unsigned>(cdiv(rows, 256))), dim3(256), 0, ctx->stream, X,
+                       x_bs, C, L, rows, nch, part.as<double2>(), eps, reinterpret_cast<float2*>(stats));
+    return launch_check(ctx, "instnorm_fin");
 }
 
 int kdec_adain_act_fwd(kdec_ctx* ctx, const float* X, long x_bs,
@@ -302,8 +406,8 @@ int kdec_adain_act_fwd(kdec_ctx* ctx, const float* X, long x_bs,
                "kdec_adain_act_fwd: bad activation");
     AdainArgs g{X, x_bs, reinterpret_cast<const float2*>(stats), gamma, beta, gb_bs, act, slope, alpha, C, L};
     ProfScope ps(ctx, "adain_fwd", 0);
-    hipLaunchKernelGGL(adain_act_fwd_k, dim3(chunks(L, 64), N * C), dim3(RT), 0, ctx->stream, g, Y, y_bs,
-                       Ypre, ypre_bs);
+    hipLaunchKernelGGL(adain_act_fwd_k, dim3(static_cast<unsigned>(cdiv(L, CH)), N * C), dim3(RT), 0, ctx->stream,
+                       g, Y, y_bs, Ypre, ypre_bs);
     return launch_check(ctx, "adain_act_fwd");
 }
 
@@ -321,21 +425,29 @@ int kdec_adain_act_bwd(kdec_ctx* ctx, const float* X, long x_bs,
     KDEC_CHECK(ctx, act >= KDEC_ACT_NONE && act <= KDEC_ACT_SNAKE && (act != KDEC_ACT_SNAKE || alpha),
                "kdec_adain_act_bwd: bad activation");
     AdainArgs g{X, x_bs, reinterpret_cast<const float2*>(stats), gamma, beta, gb_bs, act, slope, alpha, C, L};
-    float* part = nullptr;
-    Workspace ws(ctx, dalpha && act == KDEC_ACT_SNAKE ? static_cast<size_t>(N) * C * sizeof(float) : 0);
-    if (dalpha && act == KDEC_ACT_SNAKE) {
-        if (!ws.p) return KDEC_ENOMEM;
-        part = ws.as<float>();
-    }
+    const int rows = N * C;
+    const int nch = static_cast<int>(cdiv(L, CH));
+    const bool want_alpha = dalpha && act == KDEC_ACT_SNAKE;
+    Workspace part(ctx, static_cast<size_t>(rows) * nch * 3 * sizeof(double));
+    Workspace rowv(ctx, static_cast<size_t>(rows) * sizeof(float2));
+    Workspace apart(ctx, want_alpha ? static_cast<size_t>(rows) * sizeof(float) : 0);
+    if (!part.p || !rowv.p || (want_alpha && !apart.p)) return KDEC_ENOMEM;
     {
         ProfScope ps(ctx, "adain_bwd", 0);
-        hipLaunchKernelGGL(adain_act_bwd_k, dim3(N * C), dim3(RT), 0, ctx->stream, g, dY, dy_bs, R, r_bs, dX,
-                           dx_bs, dgamma, dbeta, dgb_bs, part);
-        if (int rc = launch_check(ctx, "adain_act_bwd")) return rc;
+        hipLaunchKernelGGL(adain_bwd_part_k, dim3(nch, rows), dim3(RT), 0, ctx->stream, g, dY, dy_bs, nch,
+                           part.as<double>());
+        if (int rc = launch_check(ctx, "adain_bwd_part")) return rc;
+        hipLaunchKernelGGL(adain_bwd_fin_k, dim3(static_cast<unsigned>(cdiv(rows, 256))), dim3(256), 0,
+                           ctx->stream, part.as<double>(), rows, nch, C, L, dgamma, dbeta, dgb_bs,
+                           want_alpha ? apart.as<float>() : nullptr, rowv.as<float2>());
+        if (int rc = launch_check(ctx, "adain_bwd_fin")) return rc;
+        hipLaunchKernelGGL(adain_bwd_apply_k, dim3(nch, rows), dim3(RT), 0, ctx->stream, g, dY, dy_bs, R, r_bs,
+                           dX, dx_bs, rowv.as<float2>());
+        if (int rc = launch_check(ctx, "adain_bwd_apply")) return rc;
     }
-    if (part) {
+    if (want_alpha) {
         hipLaunchKernelGGL(dalpha_reduce, dim3(static_cast<unsigned>(cdiv(C, 256))), dim3(256), 0, ctx->stream,
-                           part, dalpha, N, C);
+                           apart.as<float>(), dalpha, N, C);
         return launch_check(ctx, "dalpha_reduce");
     }
     return KDEC_OK;
