@@ -559,13 +559,16 @@ __global__ void bias_partial(const float* G, long g_bs, float* part, int N, int 
     if (threadIdx.x == 0) part[static_cast<long>(y) * M + m] = static_cast<float>(red[0]);
 }
 
-// db[m] += sum_y part[y, m]
+// db[m] += sum_y part[y, m]: one wave per m; lane j sums y = j, j+64, ... in
+// order, then a fixed shuffle tree adds the 64 lane sums.
 __global__ void bias_reduce(const float* part, float* db, int M, int S) {
-    const int m = blockIdx.x * blockDim.x + threadIdx.x;
+    const int m = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     if (m >= M) return;
     double acc = 0.0;
-    for (int y = 0; y < S; ++y) acc += part[static_cast<long>(y) * M + m];
-    db[m] += static_cast<float>(acc);
+    for (int y = lane; y < S; y += 64) acc += part[static_cast<long>(y) * M + m];
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_down(acc, o, 64);
+    if (lane == 0) db[m] += static_cast<float>(acc);
 }
 
 // ─── depthwise pool: ConvTranspose1d k3 s2 p1 op1, groups = C ──────────────
@@ -875,7 +878,7 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
                        splits, 0, M, NN);
     if (int rc = launch_check(ctx, "wgrad_reduce")) return rc;
     if (db) {
-        hipLaunchKernelGGL(bias_reduce, dim3(static_cast<unsigned>(cdiv(M, 256))), dim3(256), 0, ctx->stream,
+        hipLaunchKernelGGL(bias_reduce, dim3(static_cast<unsigned>(cdiv(M, 4))), dim3(256), 0, ctx->stream,
                            Pb.as<float>(), db, M, splits);
         return launch_check(ctx, "bias_reduce");
     }
@@ -892,7 +895,7 @@ static int bias_grad_only(kdec_ctx* ctx, const float* G, long g_bs, float* db, i
     hipLaunchKernelGGL(bias_partial, dim3(M, static_cast<unsigned>(S)), dim3(256), 0, ctx->stream, G, g_bs,
                        part.as<float>(), N, M, L);
     if (int rc = launch_check(ctx, "bias_partial")) return rc;
-    hipLaunchKernelGGL(bias_reduce, dim3(static_cast<unsigned>(cdiv(M, 256))), dim3(256), 0, ctx->stream,
+    hipLaunchKernelGGL(bias_reduce, dim3(static_cast<unsigned>(cdiv(M, 4))), dim3(256), 0, ctx->stream,
                        part.as<float>(), db, M, static_cast<int>(S));
     return launch_check(ctx, "bias_reduce");
 }

@@ -144,8 +144,9 @@ __global__ __launch_bounds__(RT) void adain_act_fwd_k(AdainArgs g, float* Y, lon
 __device__ inline float act_bwd(int act, float dy, float s, float slope, float a, double& sa) {
     if (act == KDEC_ACT_LEAKY) return s > 0.0f ? dy : slope * dy;
     if (act == KDEC_ACT_SNAKE) {
-        const float s2 = sinf(2.0f * a * s);
-        const float sn = sinf(a * s);
+        float sn, cs;
+        sincosf(a * s, &sn, &cs);
+        const float s2 = 2.0f * sn * cs;  // sin(2as) from one shared range reduction
         sa += static_cast<double>(dy) * (s * s2 / a - sn * sn / (a * a));
         return dy * (1.0f + s2);
     }
@@ -250,7 +251,11 @@ __global__ __launch_bounds__(RT) void adain_bwd_apply_k(AdainArgs g, const float
         const float s = g1 * xh + bt;
         float ds = dv[j];
         if (g.act == KDEC_ACT_LEAKY) ds = s > 0.0f ? ds : g.slope * ds;
-        else if (g.act == KDEC_ACT_SNAKE) ds = ds * (1.0f + sinf(2.0f * a * s));
+        else if (g.act == KDEC_ACT_SNAKE) {
+            float sn, cs;
+            sincosf(a * s, &sn, &cs);
+            ds = ds * (1.0f + 2.0f * sn * cs);
+        }
         float v = k1 * (ds - mv.x - xh * mv.y);
         if (r) v += rv[j];
         dx[l] = v;
