@@ -44,6 +44,18 @@ constexpr int NT = 256;   // threads per block (4 waves)
 // Buffer descriptor word 3 for raw 32-bit buffer loads (DATA_FORMAT = 32).
 constexpr int kBufDword3 = 0x00020000;
 
+// Raw buffer descriptor over [base, base + bytes), built from wave-uniform
+// (scalar) values: a descriptor the compiler cannot prove uniform would be
+// wrapped in a per-lane "waterfall" loop around every buffer load.
+__device__ inline __amdgpu_buffer_rsrc_t uniform_rsrc(const float* base, int bytes) {
+    const unsigned long long a = reinterpret_cast<unsigned long long>(base);
+    const unsigned lo = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(a));
+    const unsigned hi = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(a >> 32));
+    const int n = __builtin_amdgcn_readfirstlane(bytes);
+    float* p = reinterpret_cast<float*>((static_cast<unsigned long long>(hi) << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(p, static_cast<short>(0), n, kBufDword3);
+}
+
 __device__ inline int floordiv_i(int a, int b) {
     int q = a / b;
     if ((a % b != 0) && ((a < 0) != (b < 0))) --q;
@@ -102,11 +114,24 @@ void conv_gemm(GemmArgs g) {
     const int wm = wave & 1, wn = wave >> 1;
     const int l32 = lane & 31, hi = lane >> 5;
 
+    // Logical order: m-tile fastest, then q-tile, then (utterance, phase),
+    // with every last q-tile (usually partly empty: its idle waves skip
+    // their MFMAs) moved to the end so that the short tiles form the tail.
     int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int mt = lid % g.m_tiles;
-    lid /= g.m_tiles;
-    const int qt = lid % g.q_tiles;
-    const int zz = lid / g.q_tiles;
+    const int nz = gridDim.x / (g.m_tiles * g.q_tiles);
+    const int full = (g.q_tiles - 1) * g.m_tiles * nz;
+    int mt, qt, zz;
+    if (lid < full) {
+        mt = lid % g.m_tiles;
+        lid /= g.m_tiles;
+        qt = lid % (g.q_tiles - 1);
+        zz = lid / (g.q_tiles - 1);
+    } else {
+        lid -= full;
+        mt = lid % g.m_tiles;
+        zz = lid / g.m_tiles;
+        qt = g.q_tiles - 1;
+    }
 
     int b = zz, k = g.k, s = g.s, d = g.d, p = g.p, n_q = g.n_q;
     int os = 1, oo = 0;
@@ -140,8 +165,7 @@ void conv_gemm(GemmArgs g) {
     const int nitems = CK * segs;
     // one descriptor for this utterance's input; rows, positions out of range
     // get an out-of-bounds offset and stage as zeros
-    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(Xb), static_cast<short>(0), g.C_in * g.L_in * 4, kBufDword3);
+    const __amdgpu_buffer_rsrc_t xrs = uniform_rsrc(Xb, g.C_in * g.L_in * 4);
 
     // Stage chunk `ch` at LDS float offset `sb`: the weight slab two rows
     // (1 KB) per instruction, the input window 64 positions per instruction.
@@ -173,6 +197,7 @@ void conv_gemm(GemmArgs g) {
     const int bq = (wn * 64 + l32) * s;   // B column offset for tn = 0
     const int nchunks = g.cin_pad / CK;
     const int S = KR / 2;                 // k-steps per chunk
+    const bool live = q0 + wn * 64 < n_q;  // wave-uniform
     constexpr int HS = CK / 2;
 
     issue(0, 0);
@@ -205,7 +230,7 @@ void conv_gemm(GemmArgs g) {
         };
         float pa0, pa1, pb0, pb1, qa0, qa1, qb0, qb1;
         ld(0, pa0, pa1, pb0, pb1);
-        int u = 0;
+        int u = live ? 0 : S;  // a wave whose columns all lie past n_q only stages
         for (; u + 1 < S; u += 2) {
             ld(u + 1, qa0, qa1, qb0, qb1);
             mm(pa0, pa1, pb0, pb1);
@@ -219,7 +244,7 @@ void conv_gemm(GemmArgs g) {
             __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
         }
-        if (u < S) mm(pa0, pa1, pb0, pb1);
+        if (live && u < S) mm(pa0, pa1, pb0, pb1);
         __builtin_amdgcn_s_waitcnt(0);  // this wave's staging loads landed
         __syncthreads();
     }
@@ -403,12 +428,8 @@ void wgrad_gemm(WgradArgs g) {
     auto issue = [&](int ch, int sb) {
         const int b = ch / g.chunks_per_n;
         const int l0 = (ch - b * g.chunks_per_n) * KC;
-        const __amdgpu_buffer_rsrc_t grs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float*>(g.G + static_cast<long>(b) * g.g_bs), static_cast<short>(0), g.M * g.L_g * 4,
-            kBufDword3);
-        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float*>(g.X + static_cast<long>(b) * g.x_bs), static_cast<short>(0), g.C_x * g.L_x * 4,
-            kBufDword3);
+        const __amdgpu_buffer_rsrc_t grs = uniform_rsrc(g.G + static_cast<long>(b) * g.g_bs, g.M * g.L_g * 4);
+        const __amdgpu_buffer_rsrc_t xrs = uniform_rsrc(g.X + static_cast<long>(b) * g.x_bs, g.C_x * g.L_x * 4);
         const int l = l0 + g_pos_lane;
         for (int i = wave; i < 64; i += 2 * WG_WN) {
             const int m = m0 + i + 64 * g_row_lane;
