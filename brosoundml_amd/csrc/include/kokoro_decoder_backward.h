@@ -114,6 +114,9 @@ struct AdainResBlock1Cache {
     int C = 0;
     int L = 0;
     std::array<brotensor::Tensor, 3> beta1, beta2;  // affines kept for the recompute
+    // Snake outputs (the convs' inputs), kept for the weight grads so the
+    // backward does not recompute them.
+    std::array<brotensor::Tensor, 3> act1, act2;
 };
 
 void adain_resblock1_forward_train(const AdaINResBlock1Weights& w,

@@ -489,10 +489,11 @@ void resblock1_fwd(const AdaINResBlock1Weights& w, const Tensor& x_in, int C, in
         cache.x_seq1[i] = in_stats(x, C, L, eps1);
         Tensor xt1 = adain_act(x, cache.x_seq1[i], g1[i], b1[i], C, L, KDEC_ACT_SNAKE, 0.0f, &w.alpha1[i], where);
         cache.c1_out[i] = conv_fwd(w.convs1[i], xt1, L);
-        xt1 = Tensor();
+        cache.act1[i] = xt1;
         cache.x_seq2[i] = in_stats(cache.c1_out[i], C, L, eps2);
         Tensor xt2 = adain_act(cache.c1_out[i], cache.x_seq2[i], g2[i], b2[i], C, L, KDEC_ACT_SNAKE, 0.0f,
                                &w.alpha2[i], where);
+        cache.act2[i] = xt2;
         if (i < 2) {
             Tensor xn = dev(N, C * L);
             conv_fwd(w.convs2[i], xt2, L, mp(xn), rs(xn), cp(x), rs(x), 1.0f, 0.0f);
@@ -514,8 +515,9 @@ Tensor resblock1_bwd(const AdaINResBlock1Weights& w, const AdainResBlock1Cache& 
         // convs2[i] -> snake2 -> adain2
         Tensor d_xt2 = conv_dgrad(w.convs2[i], dx, L);
         if (wg && (grad_of(wg, w.convs2[i].W) || grad_of(wg, w.convs2[i].b))) {
-            Tensor xt2 = adain_act(cache.c1_out[i], cache.x_seq2[i], g2[i], cache.beta2[i], C, L, KDEC_ACT_SNAKE,
-                                   0.0f, &w.alpha2[i], where);
+            const Tensor xt2 = cache.act2[i].data ? cache.act2[i]
+                                                  : adain_act(cache.c1_out[i], cache.x_seq2[i], g2[i], cache.beta2[i],
+                                                              C, L, KDEC_ACT_SNAKE, 0.0f, &w.alpha2[i], where);
             conv_wgrad(w.convs2[i], wg, xt2, L, dx);
         }
         Tensor d_c1 = adain_act_bwd(cache.c1_out[i], cache.x_seq2[i], g2[i], &cache.beta2[i], C, L,
@@ -525,8 +527,9 @@ Tensor resblock1_bwd(const AdaINResBlock1Weights& w, const AdainResBlock1Cache& 
         // convs1[i] -> snake1 -> adain1 (+ the residual skip)
         Tensor d_xt1 = conv_dgrad(w.convs1[i], d_c1, L);
         if (wg && (grad_of(wg, w.convs1[i].W) || grad_of(wg, w.convs1[i].b))) {
-            Tensor xt1 = adain_act(cache.x_in[i], cache.x_seq1[i], g1[i], cache.beta1[i], C, L, KDEC_ACT_SNAKE,
-                                   0.0f, &w.alpha1[i], where);
+            const Tensor xt1 = cache.act1[i].data ? cache.act1[i]
+                                                  : adain_act(cache.x_in[i], cache.x_seq1[i], g1[i], cache.beta1[i],
+                                                              C, L, KDEC_ACT_SNAKE, 0.0f, &w.alpha1[i], where);
             conv_wgrad(w.convs1[i], wg, xt1, L, d_c1);
         }
         d_c1 = Tensor();
