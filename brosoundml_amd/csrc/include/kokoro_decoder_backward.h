@@ -50,6 +50,14 @@ struct WeightGrads {
     }
 };
 
+// ─── extension: a second stream for the conv weight grads ──────────────────
+// While set, conv weight grads run on `side`'s stream, forked from the runtime
+// stream after their inputs exist; join_wgrad_lane() makes the runtime stream
+// wait for all of them (call it before reading or zeroing the grads).
+// nullptr restores the runtime stream (after a join).
+void set_wgrad_lane(kdec_ctx* side);
+void join_wgrad_lane();
+
 // ─── AdaIN affine (instance-norm + style-conditioned scale/shift) ───────────
 //   x_ncl:(N, C*L)   gamma,beta:(C,1) or (N,C)   ->   y_ncl:(N, C*L)
 void adain_affine_forward(const brotensor::Tensor& x_ncl,

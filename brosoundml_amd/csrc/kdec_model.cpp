@@ -574,8 +574,20 @@ int kdec_model_backward(kdec_model* m, const float* daudio, int wgrad, int dalph
         for (auto& a : m->draff) rb(a);
 
         Tensor dGenIn;
+        // conv weight grads overlap the input-grad chain on the side stream
+        struct LaneGuard {
+            explicit LaneGuard(kdec_ctx* side) { bd::set_wgrad_lane(side); }
+            ~LaneGuard() {
+                try {
+                    bd::join_wgrad_lane();
+                    bd::set_wgrad_lane(nullptr);
+                } catch (...) {
+                }
+            }
+        } lane(wg ? m->side : nullptr);
         bd::generator_backward(m->gen, m->genc, m->naff, m->raff, dA, dGenIn, m->dnaff, m->draff, wg);
         bd::decoder_backbone_backward(m->bb, m->bbc, m->bbaff, dGenIn, 1e-5f, m->dbbaff, wg);
+        bd::join_wgrad_lane();
         // style projection adjoint over every unit
         const long fc_off = m->params.at(m->units[0].name + ".fc.weight").offset;
         const long fcb_off = m->params.at(m->units[0].name + ".fc.bias").offset;

@@ -15,8 +15,12 @@
 //  - nearest2x, exp/sin and the Hann window never touch the host.
 #include "kokoro_decoder_backward.h"
 
+#include <hip/hip_runtime_api.h>
+
 #include <cmath>
+#include <deque>
 #include <string>
+#include <vector>
 
 #include "kdec.h"
 
@@ -52,7 +56,9 @@ long rs(const Tensor& t) { return t.row_stride(); }
 
 // A view of channels [c0, c0+C) of an (N, Ctot*L) tensor.
 Tensor chan_view(const Tensor& t, int c0, int C, int L) {
-    return Tensor::view(t.device, mp(t) + static_cast<long>(c0) * L, t.rows, C * L, t.dtype, rs(t));
+    Tensor v = Tensor::view(t.device, mp(t) + static_cast<long>(c0) * L, t.rows, C * L, t.dtype, rs(t));
+    v.storage = t.storage;  // the view keeps its buffer alive
+    return v;
 }
 
 const float* bias_of(const Conv1d& c) {
@@ -102,13 +108,79 @@ Tensor conv_dgrad(const Conv1d& c, const Tensor& dY, int L, float scale = 1.0f) 
     return dX;
 }
 
+// Weight-grad lane: while set, conv weight grads run on a second context's
+// stream, forked from the runtime stream after their inputs are produced, so
+// the MFMA-bound weight grads overlap the input-grad chain. Their inputs are
+// held until the lane's event for them has completed (then no later kernel
+// of the runtime stream can still race with their reads), and join() makes
+// the runtime stream wait for everything the lane has queued.
+struct WgradLane {
+    kdec_ctx* side = nullptr;
+    struct Held {
+        hipEvent_t ev;
+        Tensor a, b;
+    };
+    std::deque<Held> held;
+    std::vector<hipEvent_t> free_ev;
+
+    hipEvent_t event() {
+        hipEvent_t e = nullptr;
+        if (!free_ev.empty()) {
+            e = free_ev.back();
+            free_ev.pop_back();
+        } else if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+            fail("wgrad lane", "hipEventCreate failed");
+        }
+        return e;
+    }
+    void release_done() {
+        while (!held.empty() && hipEventQuery(held.front().ev) == hipSuccess) {
+            free_ev.push_back(held.front().ev);
+            held.pop_front();
+        }
+    }
+    void fork() {
+        hipEvent_t e = event();
+        hipStream_t ms = static_cast<hipStream_t>(kdec_get_stream(kctx()));
+        if (hipEventRecord(e, ms) != hipSuccess ||
+            hipStreamWaitEvent(static_cast<hipStream_t>(kdec_get_stream(side)), e, 0) != hipSuccess)
+            fail("wgrad lane", "fork failed");
+        free_ev.push_back(e);  // reusable once recorded again later (record order is stream order)
+    }
+    void done(const Tensor& a, const Tensor& b) {
+        hipEvent_t e = event();
+        if (hipEventRecord(e, static_cast<hipStream_t>(kdec_get_stream(side))) != hipSuccess)
+            fail("wgrad lane", "event record failed");
+        held.push_back({e, a, b});
+        release_done();
+    }
+    void join() {
+        if (!side) return;
+        hipEvent_t e = event();
+        if (hipEventRecord(e, static_cast<hipStream_t>(kdec_get_stream(side))) != hipSuccess ||
+            hipStreamWaitEvent(static_cast<hipStream_t>(kdec_get_stream(kctx())), e, 0) != hipSuccess)
+            fail("wgrad lane", "join failed");
+        // everything queued on the runtime stream from here on runs after the lane's work
+        for (auto& h : held) free_ev.push_back(h.ev);
+        held.clear();
+        free_ev.push_back(e);
+    }
+};
+WgradLane g_lane;
+
 void conv_wgrad(const Conv1d& c, const detail::WeightGrads* wg, const Tensor& X, int L, const Tensor& dY) {
     float* dW = grad_of(wg, c.W);
     float* db = bias_of(c) ? grad_of(wg, c.b) : nullptr;
     if (!dW && !db) return;
-    ck(kdec_conv1d_wgrad(kctx(), cp(X), rs(X), cp(dY), rs(dY), dW, db, X.rows, c.in_channels, L, c.out_channels,
-                         c.kernel_size, c.stride, c.padding, c.dilation),
-       "conv1d backward_weight");
+    kdec_ctx* k = kctx();
+    if (g_lane.side) {
+        g_lane.fork();
+        k = g_lane.side;
+    }
+    const int rc = kdec_conv1d_wgrad(k, cp(X), rs(X), cp(dY), rs(dY), dW, db, X.rows, c.in_channels, L,
+                                     c.out_channels, c.kernel_size, c.stride, c.padding, c.dilation);
+    if (rc != KDEC_OK) fail("conv1d backward_weight", kdec_last_error(k));
+    if (g_lane.side) g_lane.done(X, dY);
 }
 
 // ─── AdaIN ───
@@ -287,6 +359,13 @@ void HarmonicSource::forward(const Tensor& F0_pred, int frame_count, int& signal
 }
 
 namespace detail {
+
+void set_wgrad_lane(kdec_ctx* side) {
+    if (g_lane.side && g_lane.side != side) g_lane.join();
+    g_lane.side = side;
+}
+
+void join_wgrad_lane() { g_lane.join(); }
 
 // ─── AdaIN affine ───────────────────────────────────────────────────────────
 
