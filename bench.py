@@ -70,6 +70,105 @@ def cpu_baseline(cfg, params):
                       f"after one warm-up"}
 
 
+def micro_benches(ctx, reps=10):
+    """The per-kernel-class cases quoted beside the headline: Snake + AdaIN1d
+    backward (x [1,256,48000]), Conv1d 512->512 k3 backward (dgrad + wgrad,
+    dilations 1/3/5, X [4,512,2048]) and the two ConvTranspose1d upsampler
+    backwards, each timed alone with HIP events on the context stream and
+    priced against its roofline (algorithmic bytes at 8 TB/s or FLOP at the
+    FP32-MFMA peak)."""
+    import torch
+    from brosoundml_amd import native, synth
+    P = native.ptr
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        for _ in range(reps):
+            fn()
+        s1.record()
+        torch.cuda.synchronize()
+        return s0.elapsed_time(s1) / reps * 1e-3
+
+    out = {}
+    # Snake + AdaIN1d backward: dX, dgamma, dbeta, dalpha (12 B/elem: dY, x in; dX out)
+    C, L = 256, 48000
+    x = dev(synth.normal("micro.x", (1, C, L)))
+    dy = dev(synth.normal("micro.dy", (1, C, L)))
+    alpha = dev(synth.uniform("micro.alpha", (C,), 0.5, 2.0))
+    gb = dev(synth.normal("micro.gb", (1, 2 * C), 0.3))
+    stats = torch.empty(C, 2, device="cuda")
+    y = torch.empty_like(x)
+    dx = torch.empty_like(x)
+    dgb = torch.empty(1, 2 * C, device="cuda")
+    da = torch.zeros(C, device="cuda")
+    ctx.call("kdec_instnorm_stats", P(x), C * L, 1, C, L, 1e-5, P(stats))
+    g_ptr, b_ptr = P(gb), native.ctypes.c_void_p(gb.data_ptr() + 4 * C)
+    dg_ptr, db_ptr = P(dgb), native.ctypes.c_void_p(dgb.data_ptr() + 4 * C)
+    t = timed(lambda: ctx.call("kdec_adain_act_bwd", P(x), C * L, P(stats), g_ptr, b_ptr, 0, 2, 0.0, P(alpha),
+                               P(dy), C * L, None, 0, P(dx), C * L, dg_ptr, db_ptr, 0, P(da), 1, C, L))
+    by = 12.0 * C * L
+    out["snake_adain_bwd_x1x256x48000"] = {"ms": round(t * 1e3, 4), "GB/s": round(by / t / 1e9, 1),
+                                          "frac_hbm": round(by / t / PEAK_HBM, 4),
+                                          "algorithmic_bytes": by}
+    t = timed(lambda: (ctx.call("kdec_instnorm_stats", P(x), C * L, 1, C, L, 1e-5, P(stats)),
+                       ctx.call("kdec_adain_act_fwd", P(x), C * L, P(stats), g_ptr, b_ptr, 0, 2, 0.0, P(alpha),
+                                P(y), C * L, None, 0, 1, C, L)))
+    by = 8.0 * C * L
+    out["snake_adain_fwd_x1x256x48000"] = {"ms": round(t * 1e3, 4), "GB/s": round(by / t / 1e9, 1),
+                                          "frac_hbm": round(by / t / PEAK_HBM, 4),
+                                          "algorithmic_bytes": by}
+    del x, dy, y, dx
+
+    # Conv1d 512 -> 512, k = 3, same padding, dilations 1, 3, 5: dgrad + wgrad
+    N, C, L, k = 4, 512, 2048, 3
+    X = dev(synth.normal("micro.cx", (N, C, L)))
+    G = dev(synth.normal("micro.cg", (N, C, L)))
+    W = dev(synth.uniform("micro.cw", (C, C * k), -1 / np.sqrt(C * k), 1 / np.sqrt(C * k)))
+    dX = torch.empty_like(X)
+    dW = torch.zeros_like(W)
+    db = torch.zeros(C, device="cuda")
+    tot_t, tot_f = 0.0, 0.0
+    for d in (1, 3, 5):
+        def run(d=d):
+            ctx.call("kdec_conv1d_dgrad", P(W), P(G), C * L, P(dX), C * L, N, C, L, C, k, 1, d, d, 1.0, 0.0)
+            ctx.call("kdec_conv1d_wgrad", P(X), C * L, P(G), C * L, P(dW), P(db), N, C, L, C, k, 1, d, d)
+        t = timed(run)
+        tot_t += t
+        tot_f += 2 * 2.0 * N * C * C * k * L
+    out["conv1d_bwd_512x512_k3_d135_x4x2048"] = {"ms": round(tot_t * 1e3, 4),
+                                                 "TFLOP/s": round(tot_f / tot_t / 1e12, 2),
+                                                 "frac_mfma": round(tot_f / tot_t / PEAK_FP32_MFMA, 4),
+                                                 "flop": tot_f}
+    del X, G, W, dX, dW
+
+    # ConvTranspose1d upsampler backwards (dgrad + wgrad)
+    res = {}
+    for name, (Ci, Co, Lin, kk, ss, pp) in {"ups0_512to256_k20_s10_x4x512": (512, 256, 512, 20, 10, 5),
+                                          "ups1_256to128_k12_s6_x4x5120": (256, 128, 5120, 12, 6, 3)}.items():
+        Lo = (Lin - 1) * ss - 2 * pp + kk
+        Xt = dev(synth.normal(f"micro.{name}.x", (4, Ci, Lin)))
+        Gt = dev(synth.normal(f"micro.{name}.g", (4, Co, Lo)))
+        Wt = dev(synth.uniform(f"micro.{name}.w", (Ci, Co * kk), -0.05, 0.05))
+        dXt = torch.empty_like(Xt)
+        dWt = torch.zeros_like(Wt)
+        dbt = torch.zeros(Co, device="cuda")
+
+        def run():
+            ctx.call("kdec_convt1d_dgrad", P(Wt), P(Gt), Co * Lo, P(dXt), Ci * Lin, 4, Ci, Lin, Co, kk, ss, pp, 0)
+            ctx.call("kdec_convt1d_wgrad", P(Xt), Ci * Lin, P(Gt), Co * Lo, P(dWt), P(dbt), 4, Ci, Lin, Co, kk, ss,
+                     pp, 0)
+        t = timed(run)
+        fl = 2 * 2.0 * 4 * Ci * Co * kk * Lin
+        res[name] = {"ms": round(t * 1e3, 4), "TFLOP/s": round(fl / t / 1e12, 2),
+                     "frac_mfma": round(fl / t / PEAK_FP32_MFMA, 4), "flop": fl}
+    out["convT_bwd"] = res
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -77,6 +176,10 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ref-steps", type=int, default=3, help="steps of the reference-semantics mode")
+    ap.add_argument("--no-micro", action="store_true", help="skip the per-kernel-class microbenchmarks")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="first run a plain device copy of this many MiB (3 times): the reference kernel for "
+                         "scaling HBM byte counters")
     a = ap.parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
@@ -89,6 +192,14 @@ def main(argv=None):
 
     cfg = C.KOKORO
     lens = C.lengths(cfg, T)
+    if a.calib_copy_mib > 0:
+        n = a.calib_copy_mib * (1 << 20) // 4
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     ctx = native.Context(0)
     model = native.Model(ctx, cfg)
     shapes = model.param_shapes()
@@ -142,7 +253,13 @@ def main(argv=None):
     conv_fams = {k: v for k, v in prof.items() if k in ("conv_fwd", "conv_dgrad", "convt_fwd", "convt_dgrad")}
     gemm_ms = sum(v["ms"] for v in conv_fams.values())
     gemm_flops = sum(v["flops"] for v in conv_fams.values())
+    gemm_bytes = sum(v["bytes"] for v in conv_fams.values())
     gemm_launches = sum(v["launches"] for v in conv_fams.values())
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    if os.path.exists(tpath):  # measured HBM bytes per launch (rocprofv3 FETCH_SIZE / WRITE_SIZE passes)
+        with open(tpath) as f:
+            traffic = json.load(f).get("conv_gemm", {}).get("bytes_per_launch")
     wg = prof.get("conv_wgrad", {"ms": 0, "flops": 0, "launches": 0})
     wgt = prof.get("convt_wgrad", {"ms": 0, "flops": 0, "launches": 0})
     achieved = gemm_flops / (gemm_ms * 1e-3) if gemm_ms else 0.0
@@ -171,7 +288,8 @@ def main(argv=None):
                    "audio_s_per_step": audio_per_step, "params": int(sum(np.prod(s) for s in shapes.values()))},
         "roofline": {"bound": "mfma", "kernel": "conv_gemm (conv1d fwd / dgrad, convT fwd / dgrad)",
                      "achieved": round(achieved / 1e12, 3), "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": traffic,
+                     "algorithmic_bytes_per_launch": round(gemm_bytes / max(gemm_launches, 1)),
                      "launches_per_step": gemm_launches // a.steps,
                      "ms_per_step": round(gemm_ms / a.steps, 3),
                      "flop_per_step": gemm_flops / a.steps},
@@ -184,6 +302,8 @@ def main(argv=None):
         "families_ms_per_step": {k: round(v["ms"] / a.steps, 3) for k, v in sorted(prof.items())},
         "reference_semantics": ref,
     }
+    if not a.no_micro:
+        out["micro"] = micro_benches(ctx)
     if not a.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(cfg, params)
     print(json.dumps(out))

@@ -710,7 +710,13 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
     g.q_tiles = static_cast<int>(cdiv(max_q, BN));
     const long blocks = static_cast<long>(g.m_tiles) * g.q_tiles * N * g.n_phase;
     if (blocks > 0x7fffffffL) return fail(ctx, KDEC_EINVAL, "conv: grid too large");
-    ProfScope ps(ctx, fam, flops);
+    // algorithmic HBM bytes: input and weights read once, output written once
+    // (read too when accumulating), residual read once
+    const int kk_all = g.n_phase > 1 ? g.ph_kt * g.n_phase : g.k;
+    double bytes = 4.0 * (static_cast<double>(N) * g.C_in * g.L_in + static_cast<double>(g.C_in) * kk_all * g.C_out +
+                          static_cast<double>(N) * g.C_out * g.L_y * (g.beta != 0.0f ? 2 : 1));
+    if (g.R) bytes += 4.0 * static_cast<double>(N) * g.C_out * g.L_y;
+    ProfScope ps(ctx, fam, flops, bytes);
     const unsigned nb = static_cast<unsigned>(blocks);
     switch (CK) {
         case 2: launch_conv<2>(ctx, g, nb, lds); break;
@@ -890,7 +896,9 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
     if (lds > 160 * 1024) return fail(ctx, KDEC_EINVAL, "wgrad: tile does not fit LDS");
     const long blocks = static_cast<long>(n_tiles) * m_tiles * splits;
     {
-        ProfScope ps(ctx, fam, 2.0 * N * M * static_cast<double>(L_g) * NN);
+        ProfScope ps(ctx, fam, 2.0 * N * M * static_cast<double>(L_g) * NN,
+                     4.0 * (static_cast<double>(N) * C_x * L_x + static_cast<double>(N) * M * L_g +
+                            static_cast<double>(M) * NN));
         wgrad_allow_large_lds();
         hipLaunchKernelGGL(wgrad_gemm, dim3(static_cast<unsigned>(blocks)), dim3(WG_NT), lds, ctx->stream, a);
         if (int rc2 = launch_check(ctx, fam)) return rc2;

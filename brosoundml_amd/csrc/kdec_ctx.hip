@@ -73,8 +73,8 @@ static hipEvent_t get_event(kdec_ctx* ctx) {
     return e;
 }
 
-ProfScope::ProfScope(kdec_ctx* c, const char* n, double f)
-    : ctx(c), name(n), flops(f) {
+ProfScope::ProfScope(kdec_ctx* c, const char* n, double f, double b)
+    : ctx(c), name(n), flops(f), bytes(b) {
     if (ctx->prof) {
         start = get_event(ctx);
         hipEventRecord(start, ctx->stream);
@@ -89,6 +89,7 @@ ProfScope::~ProfScope() {
     f.pending.emplace_back(start, stop);
     f.launches += 1;
     f.flops += flops;
+    f.bytes += bytes;
 }
 
 int launch_check(kdec_ctx* ctx, const char* where) {
@@ -209,17 +210,18 @@ int kdec_profile_reset(kdec_ctx* ctx) {
 }
 
 int kdec_profile_read(kdec_ctx* ctx, const char** names, double* ms,
-                      long* launches, double* flops, int cap) {
+                      long* launches, double* flops, double* bytes, int cap) {
     if (!ctx) return KDEC_EINVAL;
     KDEC_HIP(ctx, hipStreamSynchronize(ctx->stream));
     // fold the peers' families in (their events are on their own streams)
     for (kdec_ctx* p : ctx->peers) {
-        if (kdec_profile_read(p, nullptr, nullptr, nullptr, nullptr, 0) < 0) return KDEC_EHIP;
+        if (kdec_profile_read(p, nullptr, nullptr, nullptr, nullptr, nullptr, 0) < 0) return KDEC_EHIP;
         for (auto& kv : p->fams) {
             auto& f = ctx->fams[kv.first];
             f.ms += kv.second.ms;
             f.launches += kv.second.launches;
             f.flops += kv.second.flops;
+            f.bytes += kv.second.bytes;
         }
         p->fams.clear();
     }
@@ -239,6 +241,7 @@ int kdec_profile_read(kdec_ctx* ctx, const char** names, double* ms,
             if (ms) ms[i] = f.ms;
             if (launches) launches[i] = f.launches;
             if (flops) flops[i] = f.flops;
+            if (bytes) bytes[i] = f.bytes;
         }
         ++i;
     }

@@ -34,6 +34,7 @@ struct kdec_ctx {
         double ms = 0.0;
         long launches = 0;
         double flops = 0.0;
+        double bytes = 0.0;
         std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
     };
     bool prof = false;
@@ -81,9 +82,9 @@ struct Workspace {
 struct ProfScope {
     kdec_ctx* ctx;
     const char* name;
-    double flops;
+    double flops, bytes;
     hipEvent_t start = nullptr;
-    ProfScope(kdec_ctx* c, const char* n, double f);
+    ProfScope(kdec_ctx* c, const char* n, double f, double b = 0.0);
     ~ProfScope();
 };
 

@@ -138,13 +138,15 @@ class Context:
         ms = (ctypes.c_double * cap)()
         launches = (ctypes.c_long * cap)()
         flops = (ctypes.c_double * cap)()
+        nbytes = (ctypes.c_double * cap)()
         n = self.L.kdec_profile_read(self.h, ctypes.cast(names, ctypes.c_void_p),
                                      ctypes.cast(ms, ctypes.c_void_p),
                                      ctypes.cast(launches, ctypes.c_void_p),
-                                     ctypes.cast(flops, ctypes.c_void_p), cap)
+                                     ctypes.cast(flops, ctypes.c_void_p),
+                                     ctypes.cast(nbytes, ctypes.c_void_p), cap)
         if n < 0:
             raise KdecError(self.L.kdec_last_error(self.h).decode())
-        return {names[i].decode(): dict(ms=ms[i], launches=launches[i], flops=flops[i])
+        return {names[i].decode(): dict(ms=ms[i], launches=launches[i], flops=flops[i], bytes=nbytes[i])
                 for i in range(min(n, cap))}
 
 

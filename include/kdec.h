@@ -66,9 +66,10 @@ int kdec_malloc(kdec_ctx* ctx, size_t bytes, void** out);
 int kdec_free(kdec_ctx* ctx, void* ptr);
 /* Per-kernel-family timing with HIP events on the context stream (0 = off). */
 int kdec_profile_enable(kdec_ctx* ctx, int on);
-/* Fills names/ms/launches for up to `cap` families; returns the count. */
+/* Fills names / ms / launches / algorithmic FLOP / algorithmic HBM bytes
+ * (any may be NULL) for up to `cap` families; returns the count. */
 int kdec_profile_read(kdec_ctx* ctx, const char** names, double* ms,
-                      long* launches, double* flops, int cap);
+                      long* launches, double* flops, double* bytes, int cap);
 int kdec_profile_reset(kdec_ctx* ctx);
 
 /* ─── convolutions (implicit GEMM on FP32 MFMA) ───────────────────────── */
