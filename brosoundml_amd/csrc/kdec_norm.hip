@@ -33,6 +33,23 @@ __device__ inline double block_sum(double v, double* red) {
     return r;
 }
 
+// Block-wide double sum over NTB threads in a fixed order (shuffle tree per
+// wave, then wave 0 over the per-wave sums); every thread gets the total.
+template <int NTB>
+__device__ inline double block_sum_n(double v, double* red) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_down(v, o, 64);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    double t = threadIdx.x < NTB / 64 ? red[threadIdx.x] : 0.0;
+    if (wave == 0)
+        for (int o = 32; o > 0; o >>= 1) t += __shfl_down(t, o, 64);
+    if (threadIdx.x == 0) red[0] = t;
+    __syncthreads();
+    return red[0];
+}
+
 // Rows are cut into chunks of CH elements (EPT per thread, all loads issued
 // before use so each thread keeps EPT reads in flight); per-chunk partial
 // sums are reduced per row in a fixed order.
@@ -262,6 +279,161 @@ __global__ __launch_bounds__(RT) void adain_bwd_apply_k(AdainArgs g, const float
     }
 }
 
+// ─── one block per row, the row held in registers ───────────────────────
+// For rows of up to NTB*EPR elements: the forward reads x once (statistics
+// and the affine+activation in one pass, 8 B/elem), the backward reads x and
+// dY once (12 B/elem + the residual) when both fit (BOTH), else keeps x and
+// reads dY twice. Rows go through raw buffer loads / stores over exactly the
+// row: element j of a thread is voffset + j*NTB*4 with the j term a scalar
+// offset, so no per-element address registers are needed, and lanes past the
+// row read zeros and drop their stores.
+
+__device__ inline __amdgpu_buffer_rsrc_t row_rsrc(const float* base, int L) {
+    const unsigned long long a = reinterpret_cast<unsigned long long>(base);
+    const unsigned lo = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(a));
+    const unsigned hi = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(a >> 32));
+    float* p = reinterpret_cast<float*>((static_cast<unsigned long long>(hi) << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(p, static_cast<short>(0), __builtin_amdgcn_readfirstlane(L * 4),
+                                             0x00020000);
+}
+
+__device__ inline float row_ld(__amdgpu_buffer_rsrc_t r, int voff, int j, int ntb) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, j * ntb * 4, 0));
+}
+
+__device__ inline void row_st(__amdgpu_buffer_rsrc_t r, float v, int voff, int j, int ntb) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, voff, j * ntb * 4, 0);
+}
+
+// stats[row] = (mean, rstd); Y = act((1 + gamma) * xhat + beta). KEEP holds
+// the row in registers between the two passes; otherwise the second pass
+// reads it again, right after the first (from cache, not HBM, in practice).
+template <int NTB, int EPR, bool KEEP>
+__global__ __launch_bounds__(NTB) void adain_fwd_row_k(AdainArgs g, float eps, float2* stats, float* Y, long y_bs,
+                                                      float* Yp, long yp_bs) {
+    __shared__ double red[NTB / 64];
+    const int row = blockIdx.x;
+    const int n = row / g.C, c = row - n * g.C;
+    const long off = static_cast<long>(c) * g.L;
+    const float* x = g.X + n * g.x_bs + off;
+    const __amdgpu_buffer_rsrc_t xr = row_rsrc(x, g.L);
+    const int vo = threadIdx.x * 4;
+    const double x0 = x[0];  // shift for a well-conditioned variance
+    float v[KEEP ? EPR : 1];
+    double s1 = 0.0, s2 = 0.0;
+    if (KEEP) {
+#pragma unroll
+        for (int j = 0; j < EPR; ++j) v[KEEP ? j : 0] = row_ld(xr, vo, j, NTB);
+    }
+    constexpr int UN = KEEP ? EPR : 16;  // streaming: 16 loads in flight, not the whole row
+#pragma unroll UN
+    for (int j = 0; j < EPR; ++j) {
+        const float xj = KEEP ? v[KEEP ? j : 0] : row_ld(xr, vo, j, NTB);
+        const double d = (threadIdx.x + j * NTB < g.L) ? static_cast<double>(xj) - x0 : 0.0;
+        s1 += d;
+        s2 += d * d;
+    }
+    s1 = block_sum_n<NTB>(s1, red);
+    s2 = block_sum_n<NTB>(s2, red);
+    const double m = s1 / g.L;
+    double var = s2 / g.L - m * m;
+    if (var < 0.0) var = 0.0;
+    const float2 st = make_float2(static_cast<float>(x0 + m), static_cast<float>(1.0 / sqrt(var + static_cast<double>(eps))));
+    if (threadIdx.x == 0) stats[row] = st;
+    const float g1 = 1.0f + g.gamma[n * g.gb_bs + c];
+    const float bt = g.beta ? g.beta[n * g.gb_bs + c] : 0.0f;
+    const float a = g.act == KDEC_ACT_SNAKE ? g.alpha[c] : 0.0f;
+    const __amdgpu_buffer_rsrc_t yr = row_rsrc(Y + n * y_bs + off, g.L);
+    const __amdgpu_buffer_rsrc_t pr = row_rsrc(Yp ? Yp + n * yp_bs + off : Y, Yp ? g.L : 0);
+#pragma unroll UN
+    for (int j = 0; j < EPR; ++j) {
+        const float xj = KEEP ? v[KEEP ? j : 0] : row_ld(xr, vo, j, NTB);
+        const float xh = (xj - st.x) * st.y;
+        const float s = g1 * xh + bt;
+        row_st(yr, act_fwd(g.act, s, g.slope, a), vo, j, NTB);
+        row_st(pr, s, vo, j, NTB);  // dropped without a pre-activation output
+    }
+}
+
+// ds = dY * act'(s) for the backward row kernel, with the per-thread alpha-grad
+// term accumulated in float (the block reduction is in double). The Snake
+// derivative uses the hardware sin / cos (|a*s| stays small here, where their
+// error is ~1e-6 absolute, far inside the gradient tolerance).
+__device__ inline float act_bwd_fast(int act, float dy, float s, float slope, float a, float& sa) {
+    if (act == KDEC_ACT_LEAKY) return s > 0.0f ? dy : slope * dy;
+    if (act == KDEC_ACT_SNAKE) {
+        const float th = a * s;
+        const float sn = __sinf(th), cs = __cosf(th);
+        const float s2 = 2.0f * sn * cs;
+        sa += dy * (s * s2 / a - sn * sn / (a * a));
+        return dy * (1.0f + s2);
+    }
+    return dy;
+}
+
+template <int NTB, int EPR, bool BOTH>
+__global__ __launch_bounds__(NTB) void adain_bwd_row_k(AdainArgs g, const float* dY, long dy_bs, const float* R,
+                                                      long r_bs, float* dX, long dx_bs, float* dgamma,
+                                                      float* dbeta, long dgb_bs, float* dalpha_part) {
+    __shared__ double red[NTB / 64];
+    const int row = blockIdx.x;
+    const int n = row / g.C, c = row - n * g.C;
+    const float2 st = g.stats[row];
+    const float g1 = 1.0f + g.gamma[n * g.gb_bs + c];
+    const float bt = g.beta ? g.beta[n * g.gb_bs + c] : 0.0f;
+    const float a = g.act == KDEC_ACT_SNAKE ? g.alpha[c] : 0.0f;
+    const long off = static_cast<long>(c) * g.L;
+    const __amdgpu_buffer_rsrc_t xr = row_rsrc(g.X + n * g.x_bs + off, g.L);
+    const __amdgpu_buffer_rsrc_t dr = row_rsrc(dY + n * dy_bs + off, g.L);
+    const int vo = threadIdx.x * 4;
+    float xv[EPR], dv[BOTH ? EPR : 1];
+#pragma unroll
+    for (int j = 0; j < EPR; ++j) {
+        xv[j] = row_ld(xr, vo, j, NTB);
+        if (BOTH) dv[j] = row_ld(dr, vo, j, NTB);  // zero past the row: no contribution
+    }
+    // per-thread sums of at most EPR terms in float, across the block in double
+    float fsd = 0.0f, fsdx = 0.0f, fsa = 0.0f;
+#pragma unroll
+    for (int j = 0; j < EPR; ++j) {
+        const float dyj = BOTH ? dv[j] : row_ld(dr, vo, j, NTB);
+        const float xh = (xv[j] - st.x) * st.y;
+        const float s = g1 * xh + bt;
+        const float ds = act_bwd_fast(g.act, dyj, s, g.slope, a, fsa);
+        if (BOTH) dv[j] = ds;
+        fsd += ds;
+        fsdx += ds * xh;
+    }
+    const double sd = block_sum_n<NTB>(fsd, red);
+    const double sdx = block_sum_n<NTB>(fsdx, red);
+    const double sa = g.act == KDEC_ACT_SNAKE ? block_sum_n<NTB>(fsa, red) : 0.0;
+    if (threadIdx.x == 0) {
+        if (dgamma) dgamma[n * dgb_bs + c] = static_cast<float>(sdx);
+        if (dbeta) dbeta[n * dgb_bs + c] = static_cast<float>(sd);
+        if (dalpha_part) dalpha_part[row] = static_cast<float>(sa);
+    }
+    const float mds = static_cast<float>(sd / g.L);
+    const float mdsx = static_cast<float>(sdx / g.L);
+    const float k1 = st.y * g1;
+    const __amdgpu_buffer_rsrc_t xo = row_rsrc(dX + n * dx_bs + off, g.L);
+    // without a residual the descriptor covers nothing and its loads read 0
+    const __amdgpu_buffer_rsrc_t rr = row_rsrc(R ? R + n * r_bs + off : dY, R ? g.L : 0);
+#pragma unroll
+    for (int j = 0; j < EPR; ++j) {
+        const float xh = (xv[j] - st.x) * st.y;
+        float ds;
+        if (BOTH) {
+            ds = dv[j];
+        } else {
+            float unused = 0.0f;
+            ds = act_bwd_fast(g.act, row_ld(dr, vo, j, NTB), g1 * xh + bt, g.slope, a, unused);
+        }
+        float val = k1 * (ds - mds - xh * mdsx);
+        val += row_ld(rr, vo, j, NTB);
+        row_st(xo, val, vo, j, NTB);
+    }
+}
+
 // dalpha[c] += sum_n part[n*C + c] (fixed order)
 __global__ void dalpha_reduce(const float* part, float* dalpha, int N, int C) {
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
@@ -367,6 +539,57 @@ __global__ void fill_k(float* Y, long n, float v) {
         Y[i] = v;
 }
 
+// Row-kernel shape for a row of L elements: {threads, elements per thread};
+// {0, 0} where the chunked multi-block kernels are faster (measured on the
+// decoder's shapes: the forward up to 4096, the backward up to 49152 with
+// x and dY both held).
+struct RowShape {
+    int ntb, epr;
+};
+RowShape row_shape_fwd(int L) {
+    if (L <= 1024) return {256, 4};
+    if (L <= 4096) return {256, 16};
+    return {0, 0};
+}
+RowShape row_shape_bwd(int L) {
+    if (L <= 1024) return {256, 4};
+    if (L <= 4096) return {256, 16};
+    if (L <= 16384) return {1024, 16};
+    if (L <= 49152) return {1024, 48};
+    return {0, 0};
+}
+
+int launch_fwd_row(kdec_ctx* ctx, RowShape rsh, unsigned rows, const AdainArgs& g, float eps, float2* st, float* Y,
+                   long y_bs, float* Yp, long yp_bs) {
+#define KDEC_FWD_ROW(T, E, K)                                                                                \
+    if (rsh.ntb == T && rsh.epr == E) {                                                                      \
+        hipLaunchKernelGGL((adain_fwd_row_k<T, E, K>), dim3(rows), dim3(T), 0, ctx->stream, g, eps, st, Y,    \
+                           y_bs, Yp, yp_bs);                                                                 \
+        return launch_check(ctx, "adain_fwd_row");                                                          \
+    }
+    KDEC_FWD_ROW(256, 4, true)
+    KDEC_FWD_ROW(256, 16, true)
+#undef KDEC_FWD_ROW
+    return fail(ctx, KDEC_EINVAL, "adain forward: no row kernel for this length");
+}
+
+int launch_bwd_row(kdec_ctx* ctx, RowShape rsh, unsigned rows, const AdainArgs& g, const float* dY, long dy_bs,
+                   const float* R, long r_bs, float* dX, long dx_bs, float* dgamma, float* dbeta, long dgb_bs,
+                   float* apart) {
+#define KDEC_BWD_ROW(T, E, B)                                                                                    \
+    if (rsh.ntb == T && rsh.epr == E) {                                                                          \
+        hipLaunchKernelGGL((adain_bwd_row_k<T, E, B>), dim3(rows), dim3(T), 0, ctx->stream, g, dY, dy_bs, R, r_bs, \
+                           dX, dx_bs, dgamma, dbeta, dgb_bs, apart);                                             \
+        return launch_check(ctx, "adain_bwd_row");                                                              \
+    }
+    KDEC_BWD_ROW(256, 4, true)
+    KDEC_BWD_ROW(256, 16, true)
+    KDEC_BWD_ROW(1024, 16, true)
+    KDEC_BWD_ROW(1024, 48, true)
+#undef KDEC_BWD_ROW
+    return fail(ctx, KDEC_EINVAL, "adain backward: no row kernel for this length");
+}
+
 unsigned chunks(long len, long cap = 1024) {
     long g = (len + 255) / 256;
     if (g > cap) g = cap;
@@ -416,6 +639,27 @@ int kdec_adain_act_fwd(kdec_ctx* ctx, const float* X, long x_bs,
     return launch_check(ctx, "adain_act_fwd");
 }
 
+int kdec_adain_act_fwd_stats(kdec_ctx* ctx, const float* X, long x_bs, float eps, float* stats,
+                             const float* gamma, const float* beta, long gb_bs, int act, float slope,
+                             const float* alpha, float* Y, long y_bs, float* Ypre, long ypre_bs, int N, int C,
+                             int L) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, X && stats && gamma && Y && N > 0 && C > 0 && L > 0 && x_bs >= static_cast<long>(C) * L,
+               "kdec_adain_act_fwd_stats: bad arguments");
+    KDEC_CHECK(ctx, act >= KDEC_ACT_NONE && act <= KDEC_ACT_SNAKE && (act != KDEC_ACT_SNAKE || alpha),
+               "kdec_adain_act_fwd_stats: bad activation");
+    const RowShape rsh = row_shape_fwd(L);
+    if (!rsh.ntb) {  // long rows: statistics pass, then the affine pass
+        if (int rc = kdec_instnorm_stats(ctx, X, x_bs, N, C, L, eps, stats)) return rc;
+        return kdec_adain_act_fwd(ctx, X, x_bs, stats, gamma, beta, gb_bs, act, slope, alpha, Y, y_bs, Ypre, ypre_bs,
+                                  N, C, L);
+    }
+    AdainArgs g{X, x_bs, reinterpret_cast<const float2*>(stats), gamma, beta, gb_bs, act, slope, alpha, C, L};
+    ProfScope ps(ctx, "adain_fwd", 0, 4.0 * static_cast<double>(N) * C * L * (Ypre ? 3 : 2));
+    return launch_fwd_row(ctx, rsh, static_cast<unsigned>(N * C), g, eps, reinterpret_cast<float2*>(stats), Y, y_bs,
+                          Ypre, ypre_bs);
+}
+
 int kdec_adain_act_bwd(kdec_ctx* ctx, const float* X, long x_bs,
                        const float* stats, const float* gamma,
                        const float* beta, long gb_bs, int act, float slope,
@@ -433,12 +677,30 @@ int kdec_adain_act_bwd(kdec_ctx* ctx, const float* X, long x_bs,
     const int rows = N * C;
     const int nch = static_cast<int>(cdiv(L, CH));
     const bool want_alpha = dalpha && act == KDEC_ACT_SNAKE;
+    const RowShape rsh = row_shape_bwd(L);
+    Workspace apart(ctx, want_alpha ? static_cast<size_t>(rows) * sizeof(float) : 0);
+    if (want_alpha && !apart.p) return KDEC_ENOMEM;
+    const double bytes = 4.0 * static_cast<double>(rows) * L * 3 +
+                         (R ? 4.0 * static_cast<double>(rows) * L : 0.0);
+    if (rsh.ntb) {
+        {
+            ProfScope ps(ctx, "adain_bwd", 0, bytes);
+            if (int rc = launch_bwd_row(ctx, rsh, static_cast<unsigned>(rows), g, dY, dy_bs, R, r_bs, dX, dx_bs,
+                                        dgamma, dbeta, dgb_bs, want_alpha ? apart.as<float>() : nullptr))
+                return rc;
+        }
+        if (want_alpha) {
+            hipLaunchKernelGGL(dalpha_reduce, dim3(static_cast<unsigned>(cdiv(C, 256))), dim3(256), 0, ctx->stream,
+                               apart.as<float>(), dalpha, N, C);
+            return launch_check(ctx, "dalpha_reduce");
+        }
+        return KDEC_OK;
+    }
     Workspace part(ctx, static_cast<size_t>(rows) * nch * 3 * sizeof(double));
     Workspace rowv(ctx, static_cast<size_t>(rows) * sizeof(float2));
-    Workspace apart(ctx, want_alpha ? static_cast<size_t>(rows) * sizeof(float) : 0);
-    if (!part.p || !rowv.p || (want_alpha && !apart.p)) return KDEC_ENOMEM;
+    if (!part.p || !rowv.p) return KDEC_ENOMEM;
     {
-        ProfScope ps(ctx, "adain_bwd", 0);
+        ProfScope ps(ctx, "adain_bwd", 0, 4.0 * static_cast<double>(rows) * L * 5);
         hipLaunchKernelGGL(adain_bwd_part_k, dim3(nch, rows), dim3(RT), 0, ctx->stream, g, dY, dy_bs, nch,
                            part.as<double>());
         if (int rc = launch_check(ctx, "adain_bwd_part")) return rc;

@@ -272,6 +272,21 @@ Tensor adain_act(const Tensor& x, const Tensor& st, const Tensor& g, const Tenso
     return y;
 }
 
+// Y = act(adain(x)) with the statistics (st, (mean, rstd) per row) computed in
+// the same pass over x
+Tensor adain_act_stats(const Tensor& x, float eps, Tensor& st, const Tensor& g, const Tensor& b, int C, int L, int act,
+                       float slope, const Tensor* alpha, const char* where) {
+    const int N = x.rows;
+    const Affine ga = affine_in(g, N, C, where), ba = affine_in(b, N, C, where);
+    if (ga.bs != ba.bs) fail(where, "gamma and beta must share one layout");
+    st = dev(N * C, 2);
+    Tensor y = dev(N, C * L);
+    ck(kdec_adain_act_fwd_stats(kctx(), cp(x), rs(x), eps, mp(st), ga.p, ba.p, ga.bs, act, slope,
+                                alpha ? cp(*alpha) : nullptr, mp(y), rs(y), nullptr, 0, N, C, L),
+       where);
+    return y;
+}
+
 // dX = adain_backward(act_backward(dY)) (+ R)
 Tensor adain_act_bwd(const Tensor& x, const Tensor& st, const Tensor& g, const Tensor* b, int C, int L, int act,
                      float slope, const Tensor* alpha, const Tensor& dY, const Tensor* R, Tensor& dG,
@@ -372,8 +387,8 @@ void join_wgrad_lane() { g_lane.join(); }
 void adain_affine_forward(const Tensor& x_ncl, const Tensor& gamma, const Tensor& beta, int C, int L,
                           float eps, Tensor& y_ncl, Tensor& x_seq_cache) {
     check_batch(x_ncl, C, L, "adain_affine_forward");
-    Tensor st = in_stats(x_ncl, C, L, eps);
-    y_ncl = adain_act(x_ncl, st, gamma, beta, C, L, KDEC_ACT_NONE, 0.0f, nullptr, "adain_affine_forward");
+    Tensor st;
+    y_ncl = adain_act_stats(x_ncl, eps, st, gamma, beta, C, L, KDEC_ACT_NONE, 0.0f, nullptr, "adain_affine_forward");
     x_seq_cache = st;
 }
 
@@ -424,15 +439,13 @@ void adain_resblk_1d_forward_train(const AdainResBlk1dWeights& w, const Tensor& 
     cache.n2_pre = Tensor();
 
     // residual: adain1 -> leaky 0.2 -> [pool] -> conv1 -> adain2 -> leaky -> conv2
-    cache.x_seq1 = in_stats(x, C_in, L_in, eps);
-    Tensor r = adain_act(x, cache.x_seq1, gamma1, beta1, C_in, L_in, KDEC_ACT_LEAKY, 0.2f, nullptr, where);
+    Tensor r = adain_act_stats(x, eps, cache.x_seq1, gamma1, beta1, C_in, L_in, KDEC_ACT_LEAKY, 0.2f, nullptr, where);
     Tensor pooled = w.upsample ? pool_fwd(w, r, L_in) : r;
     r = Tensor();
     cache.conv1_out = conv_fwd(w.conv1, pooled, L_out);
     pooled = Tensor();
-    cache.x_seq2 = in_stats(cache.conv1_out, C_out, L_out, eps);
-    Tensor n2 = adain_act(cache.conv1_out, cache.x_seq2, gamma2, beta2, C_out, L_out, KDEC_ACT_LEAKY, 0.2f,
-                          nullptr, where);
+    Tensor n2 = adain_act_stats(cache.conv1_out, eps, cache.x_seq2, gamma2, beta2, C_out, L_out, KDEC_ACT_LEAKY, 0.2f,
+                                nullptr, where);
 
     // shortcut: [nearest2x] -> [conv1x1]  (1x1 applied before the upsample)
     Tensor sc;
@@ -565,13 +578,12 @@ void resblock1_fwd(const AdaINResBlock1Weights& w, const Tensor& x_in, int C, in
         cache.s2_pre[i] = Tensor();
         const float eps1 = w.adain1[i].eps > 0.0f ? w.adain1[i].eps : 1e-5f;
         const float eps2 = w.adain2[i].eps > 0.0f ? w.adain2[i].eps : 1e-5f;
-        cache.x_seq1[i] = in_stats(x, C, L, eps1);
-        Tensor xt1 = adain_act(x, cache.x_seq1[i], g1[i], b1[i], C, L, KDEC_ACT_SNAKE, 0.0f, &w.alpha1[i], where);
+        Tensor xt1 = adain_act_stats(x, eps1, cache.x_seq1[i], g1[i], b1[i], C, L, KDEC_ACT_SNAKE, 0.0f, &w.alpha1[i],
+                                     where);
         cache.c1_out[i] = conv_fwd(w.convs1[i], xt1, L);
         cache.act1[i] = xt1;
-        cache.x_seq2[i] = in_stats(cache.c1_out[i], C, L, eps2);
-        Tensor xt2 = adain_act(cache.c1_out[i], cache.x_seq2[i], g2[i], b2[i], C, L, KDEC_ACT_SNAKE, 0.0f,
-                               &w.alpha2[i], where);
+        Tensor xt2 = adain_act_stats(cache.c1_out[i], eps2, cache.x_seq2[i], g2[i], b2[i], C, L, KDEC_ACT_SNAKE,
+                                     0.0f, &w.alpha2[i], where);
         cache.act2[i] = xt2;
         if (i < 2) {
             Tensor xn = dev(N, C * L);

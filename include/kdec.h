@@ -149,6 +149,19 @@ int kdec_adain_act_fwd(kdec_ctx* ctx, const float* X, long x_bs,
                        float slope, const float* alpha, float* Y, long y_bs,
                        float* Ypre, long ypre_bs, int N, int C, int L);
 
+/* Statistics and the affine + activation in one pass: stats (N*C (mean,
+ * rstd) pairs, as kdec_instnorm_stats) are written and used at once. Short
+ * rows are held in registers, so x is read once (the two-call sequence reads
+ * it twice); longer rows take the two passes. Replaces the
+ * group_norm + modulate + activation sequence of kokoro_decoder_backward.cpp
+ * :100-120 with :172/:190 (leaky) or :305-306/:313-314 (snake). */
+int kdec_adain_act_fwd_stats(kdec_ctx* ctx, const float* X, long x_bs,
+                             float eps, float* stats, const float* gamma,
+                             const float* beta, long gb_bs, int act,
+                             float slope, const float* alpha, float* Y,
+                             long y_bs, float* Ypre, long ypre_bs, int N,
+                             int C, int L);
+
 /* Backward of kdec_adain_act_fwd given dY (grad at the activation output):
  *   dX = adain_backward(act_backward(dY)) + (R ? R : 0)
  *   dgamma/dbeta (N*C at gb_bs rows) overwritten; dalpha (C) accumulated

@@ -197,7 +197,9 @@ ACTS = {"none": 0, "leaky": 1, "snake": 2}
 
 
 @pytest.mark.parametrize("act", ["none", "leaky", "snake"])
-@pytest.mark.parametrize("C,L", [(5, 31), (16, 4099)])
+# lengths cover every row-kernel shape (256x4, 256x16, 1024x16, 1024x48,
+# 1024x64 streaming) and the chunked path for longer rows
+@pytest.mark.parametrize("C,L", [(5, 31), (3, 1500), (16, 4099), (2, 48000), (2, 61441), (2, 70000)])
 def test_adain_act(K, act, C, L):
     N = 2
     x = rnd(N, C, L, scale=1.7) + 0.3
@@ -217,6 +219,13 @@ def test_adain_act(K, act, C, L):
             y = O.snake(y, alpha, C, L)
         refs.append(y)
     assert_close(h(Y), np.stack(refs), FWD_TOL, f"adain+{act} forward")
+    # statistics and affine + activation in one pass
+    st2 = torch.empty(N * C, 2, device="cuda")
+    Y2 = torch.empty(N, C, L, device="cuda")
+    K.call("kdec_adain_act_fwd_stats", P(g(x)), C * L, 1e-5, P(st2), P(g(gm)), P(g(bt)), C, ACTS[act], 0.2,
+           P(g(alpha)), P(Y2), C * L, None, 0, N, C, L)
+    assert_close(h(st2), h(st), 1e-6, f"adain+{act} fused statistics")
+    assert_close(h(Y2), np.stack(refs), FWD_TOL, f"adain+{act} fused forward")
 
     dY = rnd(N, C, L)
     R = rnd(N, C, L)
