@@ -850,8 +850,11 @@ int wgrad_splits(kdec_ctx* ctx, int total_chunks, long tiles, size_t lds) {
         per_cu = 1;
     const long slots = static_cast<long>(ctx->num_cus) * per_cu * WG_ROUNDS;
     long splits = (slots + tiles - 1) / tiles;
+    // at least 8 chunks per split: shorter runs spend more on the partial
+    // tile's write-out and reduction than on the GEMM
+    const long max_splits = (total_chunks + 7) / 8;
+    if (splits > max_splits) splits = max_splits;
     if (splits < 1) splits = 1;
-    if (splits > total_chunks) splits = total_chunks;
     const long cps = (total_chunks + splits - 1) / splits;
     return static_cast<int>((total_chunks + cps - 1) / cps);
 }
