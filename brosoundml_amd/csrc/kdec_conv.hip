@@ -81,6 +81,12 @@ struct GemmArgs {
     // polyphase transposed-conv mode when n_phase > 1
     int n_phase, ph_s, ph_p, ph_kt;
     int m_tiles, q_tiles;
+    // split-K over the channel chunks (small grids): part sp of `splits`
+    // writes raw sums to P + sp * p_split (laid out like Y, batch stride
+    // C_out * L_y) and split_reduce applies the epilogue
+    int splits;
+    float* P;
+    long p_split;
 };
 
 // Logical block order with consecutive ids on one XCD: the dispatcher deals
@@ -133,6 +139,8 @@ void conv_gemm(GemmArgs g) {
         qt = g.q_tiles - 1;
     }
 
+    const int sp = zz % g.splits;
+    zz /= g.splits;
     int b = zz, k = g.k, s = g.s, d = g.d, p = g.p, n_q = g.n_q;
     int os = 1, oo = 0;
     const float* A = g.A;
@@ -196,16 +204,19 @@ void conv_gemm(GemmArgs g) {
     const int am = wm * 64 + l32;         // A column (m) for tm = 0
     const int bq = (wn * 64 + l32) * s;   // B column offset for tn = 0
     const int nchunks = g.cin_pad / CK;
+    const int cps = (nchunks + g.splits - 1) / g.splits;
+    const int ch0 = sp * cps;
+    const int ch1 = min(nchunks, ch0 + cps);
     const int S = KR / 2;                 // k-steps per chunk
     const bool live = q0 + wn * 64 < n_q;  // wave-uniform
     constexpr int HS = CK / 2;
 
-    issue(0, 0);
+    if (ch0 < ch1) issue(ch0, 0);
     __builtin_amdgcn_s_waitcnt(0);  // staging loads landed in LDS
     __syncthreads();
-    for (int ch = 0; ch < nchunks; ++ch) {
-        const int sb = (ch & 1) * stage;
-        if (ch + 1 < nchunks) issue(ch + 1, stage - sb);
+    for (int ch = ch0; ch < ch1; ++ch) {
+        const int sb = ((ch - ch0) & 1) * stage;
+        if (ch + 1 < ch1) issue(ch + 1, stage - sb);
         const int wb = sb + hi * BM + am;
         const int xb = sb + KR * BM + hi * span_p + bq;
         // step u reads packed rows 2u + hi: tap t = u / HS, channel 2(u % HS) + hi
@@ -250,6 +261,23 @@ void conv_gemm(GemmArgs g) {
     }
 
     // epilogue: lane owns column l32 and rows 8*(e/4) + 4*hi + e%4 of each tile
+    if (g.splits > 1) {
+        float* Pb = g.P + sp * g.p_split + static_cast<long>(b) * g.C_out * g.L_y;
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn) {
+            const int q = q0 + wn * 64 + tn * 32 + l32;
+            if (q >= n_q) continue;
+            const long j = static_cast<long>(q) * os + oo;
+#pragma unroll
+            for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int m = m0 + wm * 64 + tm * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
+                    if (m < g.C_out) Pb[static_cast<long>(m) * g.L_y + j] = acc[tm][tn][e];
+                }
+        }
+        return;
+    }
     float* Yb = g.Y + static_cast<long>(b) * g.y_bs;
     const float* Rb = g.R ? g.R + static_cast<long>(b) * g.r_bs : nullptr;
 #pragma unroll
@@ -272,6 +300,26 @@ void conv_gemm(GemmArgs g) {
                 Yb[yi] = v;
             }
         }
+    }
+}
+
+// Y = scale * (sum_sp P[sp] + bias + R) + beta * Y over the split-K parts, in
+// part order.
+__global__ void split_reduce(const float* P, int splits, long p_split, float* Y, long y_bs, const float* bias,
+                             const float* R, long r_bs, float scale, float beta, int C, int L) {
+    const int n = blockIdx.y;
+    const long tot = static_cast<long>(C) * L;
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < tot;
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        const float* pp = P + n * tot + i;
+        float v = 0.0f;
+        for (int s = 0; s < splits; ++s) v += pp[s * p_split];
+        if (bias) v += bias[i / L];
+        if (R) v += R[n * r_bs + i];
+        v *= scale;
+        float* y = Y + n * y_bs + i;
+        if (beta != 0.0f) v += beta * *y;
+        *y = v;
     }
 }
 
@@ -708,8 +756,26 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
     if (g.n_phase > 1) max_q = static_cast<int>(cdiv(g.L_y + g.ph_s, g.ph_s)) + 1;
     g.m_tiles = m_tiles;
     g.q_tiles = static_cast<int>(cdiv(max_q, BN));
-    const long blocks = static_cast<long>(g.m_tiles) * g.q_tiles * N * g.n_phase;
+    // small grids (fewer blocks than two per CU) split the channel chunks,
+    // at least 4 chunks a part, towards four blocks per CU
+    const long tiles = static_cast<long>(g.m_tiles) * g.q_tiles * N * g.n_phase;
+    const int nchunks = g.cin_pad / CK;
+    int splits = 1;
+    if (tiles < 2L * ctx->num_cus) {
+        const long want = cdiv(4L * ctx->num_cus, tiles);
+        const long most = std::max(1, nchunks / 4);
+        splits = static_cast<int>(std::min(std::min(want, most), 16L));
+        splits = static_cast<int>(cdiv(nchunks, cdiv(nchunks, splits)));  // no empty parts
+    }
+    g.splits = splits;
+    const long blocks = tiles * splits;
     if (blocks > 0x7fffffffL) return fail(ctx, KDEC_EINVAL, "conv: grid too large");
+    Workspace part(ctx, splits > 1 ? static_cast<size_t>(splits) * N * g.C_out * g.L_y * sizeof(float) : 0);
+    if (splits > 1) {
+        if (!part.p) return KDEC_ENOMEM;
+        g.P = part.as<float>();
+        g.p_split = static_cast<long>(N) * g.C_out * g.L_y;
+    }
     // algorithmic HBM bytes: input and weights read once, output written once
     // (read too when accumulating), residual read once
     const int kk_all = g.n_phase > 1 ? g.ph_kt * g.n_phase : g.k;
@@ -726,7 +792,14 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
         case 32: launch_conv<32>(ctx, g, nb, lds); break;
         default: return fail(ctx, KDEC_EINVAL, "conv: unsupported channel chunk");
     }
-    return launch_check(ctx, fam);
+    if (int rc = launch_check(ctx, fam)) return rc;
+    if (splits > 1) {
+        const long tot = static_cast<long>(g.C_out) * g.L_y;
+        hipLaunchKernelGGL(split_reduce, dim3(grid1d(tot), N), dim3(256), 0, ctx->stream, g.P, splits, g.p_split, g.Y,
+                           g.y_bs, g.bias, g.R, g.r_bs, g.scale, g.beta, g.C_out, g.L_y);
+        return launch_check(ctx, "split_reduce");
+    }
+    return KDEC_OK;
 }
 
 }  // namespace
