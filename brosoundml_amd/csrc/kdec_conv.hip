@@ -32,6 +32,10 @@
 
 #include <algorithm>
 #include <cmath>
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
 
 namespace kdec {
 namespace {
@@ -81,12 +85,14 @@ struct GemmArgs {
     // polyphase transposed-conv mode when n_phase > 1
     int n_phase, ph_s, ph_p, ph_kt;
     int m_tiles, q_tiles;
-    // split-K over the channel chunks (small grids): part sp of `splits`
-    // writes raw sums to P + sp * p_split (laid out like Y, batch stride
-    // C_out * L_y) and split_reduce applies the epilogue
-    int splits;
+    int nz;                  // N * n_phase
+    // Tiles in logical order: the first `full_tiles` run over all channel
+    // chunks; the remaining `split_tiles` run as `fsplit` chunk ranges each,
+    // whose raw sums go to P[(tile - full_tiles) * fsplit + part][BM * BN]
+    // and are summed, in part order, by tile_reduce.
+    int full_tiles, split_tiles, fsplit;
+    int full_per_xcd, parts_per_xcd;  // block slots per XCD for each kind
     float* P;
-    long p_split;
 };
 
 // Logical block order with consecutive ids on one XCD: the dispatcher deals
@@ -103,7 +109,71 @@ __device__ inline int xcd_remap(int pid, int total) {
     return tall * per + (xcd - tall) * (per - 1) + local;
 }
 
-// 1-D grid of m_tiles * q_tiles * (N * n_phase) blocks. Two LDS stages;
+// Geometry of one output tile (wave-uniform).
+struct TileGeo {
+    int b, m0, q0, n_q, os, oo, k, s, d, p;
+    const float* A;
+};
+
+// Logical tile order: m-tile fastest, then q-tile, then (utterance, phase),
+// with every last q-tile (usually partly empty: its idle waves skip their
+// MFMAs) moved to the end so that the short tiles come last.
+__device__ inline void decode_tile(const GemmArgs& g, int tile, TileGeo& T) {
+    const int full = (g.q_tiles - 1) * g.m_tiles * g.nz;
+    int mt, qt, zz, lid = tile;
+    if (lid < full) {
+        mt = lid % g.m_tiles;
+        lid /= g.m_tiles;
+        qt = lid % (g.q_tiles - 1);
+        zz = lid / (g.q_tiles - 1);
+    } else {
+        lid -= full;
+        mt = lid % g.m_tiles;
+        zz = lid / g.m_tiles;
+        qt = g.q_tiles - 1;
+    }
+    T.b = zz; T.k = g.k; T.s = g.s; T.d = g.d; T.p = g.p; T.n_q = g.n_q;
+    T.os = 1; T.oo = 0;
+    T.A = g.A;
+    if (g.n_phase > 1) {
+        const int r = zz % g.n_phase;
+        T.b = zz / g.n_phase;
+        const int qmin = -floordiv_i(r - g.ph_p, g.ph_s);          // ceil((p - r)/s)
+        const int qmax = floordiv_i(g.L_y - 1 + g.ph_p - r, g.ph_s);
+        T.n_q = qmax - qmin + 1;
+        T.k = g.ph_kt;
+        T.s = 1;
+        T.d = 1;
+        T.p = g.ph_kt - 1 - qmin;
+        T.os = g.ph_s;
+        T.oo = qmin * g.ph_s + r - g.ph_p;
+        T.A += static_cast<long>(r) * g.a_phase_stride;
+    }
+    T.m0 = mt * BM;
+    T.q0 = qt * BN;
+}
+
+// Block -> work: the dispatcher deals workgroups to the 8 XCDs round-robin,
+// so block i runs on XCD i % 8. Each XCD gets full_per_xcd slots for a
+// contiguous range of whole tiles (neighbouring tiles share operand tiles in
+// its L2) and then parts_per_xcd slots for split-tile parts; the whole-tile
+// rounds and the short split-part round are thus the same on every XCD.
+// Returns false for a padding slot.
+__device__ inline bool block_work(const GemmArgs& g, int& tile, int& part) {
+    const int x = blockIdx.x & 7, local = blockIdx.x >> 3;
+    if (local < g.full_per_xcd) {
+        tile = x * g.full_per_xcd + local;
+        part = -1;
+        return tile < g.full_tiles;
+    }
+    const int j = x * g.parts_per_xcd + (local - g.full_per_xcd);
+    if (j >= g.split_tiles * g.fsplit) return false;
+    tile = g.full_tiles + j % g.split_tiles;
+    part = j / g.split_tiles;
+    return true;
+}
+
+// Grid of 8 * (full_per_xcd + parts_per_xcd) blocks. Two LDS stages;
 // weights arrive packed chunk-major (row ((chunk*k + t)*CK + c_local)), so a
 // chunk's KR = CK*k rows are one contiguous slab of the panel.
 //
@@ -120,46 +190,14 @@ void conv_gemm(GemmArgs g) {
     const int wm = wave & 1, wn = wave >> 1;
     const int l32 = lane & 31, hi = lane >> 5;
 
-    // Logical order: m-tile fastest, then q-tile, then (utterance, phase),
-    // with every last q-tile (usually partly empty: its idle waves skip
-    // their MFMAs) moved to the end so that the short tiles form the tail.
-    int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int nz = gridDim.x / (g.m_tiles * g.q_tiles);
-    const int full = (g.q_tiles - 1) * g.m_tiles * nz;
-    int mt, qt, zz;
-    if (lid < full) {
-        mt = lid % g.m_tiles;
-        lid /= g.m_tiles;
-        qt = lid % (g.q_tiles - 1);
-        zz = lid / (g.q_tiles - 1);
-    } else {
-        lid -= full;
-        mt = lid % g.m_tiles;
-        zz = lid / g.m_tiles;
-        qt = g.q_tiles - 1;
-    }
-
-    const int sp = zz % g.splits;
-    zz /= g.splits;
-    int b = zz, k = g.k, s = g.s, d = g.d, p = g.p, n_q = g.n_q;
-    int os = 1, oo = 0;
-    const float* A = g.A;
-    if (g.n_phase > 1) {
-        const int r = zz % g.n_phase;
-        b = zz / g.n_phase;
-        const int qmin = -floordiv_i(r - g.ph_p, g.ph_s);          // ceil((p - r)/s)
-        const int qmax = floordiv_i(g.L_y - 1 + g.ph_p - r, g.ph_s);
-        n_q = qmax - qmin + 1;
-        k = g.ph_kt;
-        s = 1;
-        d = 1;
-        p = g.ph_kt - 1 - qmin;
-        os = g.ph_s;
-        oo = qmin * g.ph_s + r - g.ph_p;
-        A += static_cast<long>(r) * g.a_phase_stride;
-    }
-    const int m0 = mt * BM;
-    const int q0 = qt * BN;
+    int tile, part;
+    if (!block_work(g, tile, part)) return;  // uniform per block
+    TileGeo T;
+    decode_tile(g, tile, T);
+    const int b = T.b, k = T.k, s = T.s, d = T.d, p = T.p, n_q = T.n_q, os = T.os, oo = T.oo;
+    const float* A = T.A;
+    const int m0 = T.m0;
+    const int q0 = T.q0;
     if (q0 >= n_q) return;  // uniform per block
 
     const int KR = CK * k;                            // weight rows per chunk
@@ -204,9 +242,10 @@ void conv_gemm(GemmArgs g) {
     const int am = wm * 64 + l32;         // A column (m) for tm = 0
     const int bq = (wn * 64 + l32) * s;   // B column offset for tn = 0
     const int nchunks = g.cin_pad / CK;
-    const int cps = (nchunks + g.splits - 1) / g.splits;
-    const int ch0 = sp * cps;
-    const int ch1 = min(nchunks, ch0 + cps);
+    const int nparts = part < 0 ? 1 : g.fsplit;
+    const int pp = part < 0 ? 0 : part;
+    const int ch0 = pp * nchunks / nparts;
+    const int ch1 = (pp + 1) * nchunks / nparts;
     const int S = KR / 2;                 // k-steps per chunk
     const bool live = q0 + wn * 64 < n_q;  // wave-uniform
     constexpr int HS = CK / 2;
@@ -261,21 +300,17 @@ void conv_gemm(GemmArgs g) {
     }
 
     // epilogue: lane owns column l32 and rows 8*(e/4) + 4*hi + e%4 of each tile
-    if (g.splits > 1) {
-        float* Pb = g.P + sp * g.p_split + static_cast<long>(b) * g.C_out * g.L_y;
+    if (part >= 0) {  // raw sums of this chunk range, tile-local [m][q]
+        float* Pt = g.P + (static_cast<long>(tile - g.full_tiles) * g.fsplit + part) * (BM * BN);
 #pragma unroll
-        for (int tn = 0; tn < 2; ++tn) {
-            const int q = q0 + wn * 64 + tn * 32 + l32;
-            if (q >= n_q) continue;
-            const long j = static_cast<long>(q) * os + oo;
+        for (int tn = 0; tn < 2; ++tn)
 #pragma unroll
             for (int tm = 0; tm < 2; ++tm)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    const int m = m0 + wm * 64 + tm * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
-                    if (m < g.C_out) Pb[static_cast<long>(m) * g.L_y + j] = acc[tm][tn][e];
+                    const int ml = wm * 64 + tm * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
+                    Pt[ml * BN + wn * 64 + tn * 32 + l32] = acc[tm][tn][e];
                 }
-        }
         return;
     }
     float* Yb = g.Y + static_cast<long>(b) * g.y_bs;
@@ -303,23 +338,27 @@ void conv_gemm(GemmArgs g) {
     }
 }
 
-// Y = scale * (sum_sp P[sp] + bias + R) + beta * Y over the split-K parts, in
-// part order.
-__global__ void split_reduce(const float* P, int splits, long p_split, float* Y, long y_bs, const float* bias,
-                             const float* R, long r_bs, float scale, float beta, int C, int L) {
-    const int n = blockIdx.y;
-    const long tot = static_cast<long>(C) * L;
-    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < tot;
-         i += static_cast<long>(gridDim.x) * blockDim.x) {
-        const float* pp = P + n * tot + i;
+// Split tiles: Y = scale * (sum of the parts in order + bias + R) + beta * Y.
+// Grid (BM * BN / 256, split_tiles).
+__global__ void tile_reduce(GemmArgs g) {
+    const int ti = blockIdx.y;
+    TileGeo T;
+    decode_tile(g, g.full_tiles + ti, T);
+    if (T.q0 >= T.n_q) return;
+    const float* Pt = g.P + static_cast<long>(ti) * g.fsplit * (BM * BN);
+    float* Yb = g.Y + static_cast<long>(T.b) * g.y_bs;
+    const float* Rb = g.R ? g.R + static_cast<long>(T.b) * g.r_bs : nullptr;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < BM * BN; e += gridDim.x * blockDim.x) {
+        const int m = T.m0 + e / BN, q = T.q0 + e % BN;
+        if (m >= g.C_out || q >= T.n_q) continue;
         float v = 0.0f;
-        for (int s = 0; s < splits; ++s) v += pp[s * p_split];
-        if (bias) v += bias[i / L];
-        if (R) v += R[n * r_bs + i];
-        v *= scale;
-        float* y = Y + n * y_bs + i;
-        if (beta != 0.0f) v += beta * *y;
-        *y = v;
+        for (int sp = 0; sp < g.fsplit; ++sp) v += Pt[sp * (BM * BN) + e];
+        if (g.bias) v += g.bias[m];
+        const long yi = static_cast<long>(m) * g.L_y + static_cast<long>(q) * T.os + T.oo;
+        if (Rb) v += Rb[yi];
+        v *= g.scale;
+        if (g.beta != 0.0f) v += g.beta * Yb[yi];
+        Yb[yi] = v;
     }
 }
 
@@ -422,7 +461,7 @@ struct WgradArgs {
     float* Pb;           // bias partials [split][M] (sum of G), or null
     int M, C_x, L_x, L_g, k, s, d, p;
     int NN;              // C_x * k
-    int chunks_per_n, total_chunks, chunks_per_split;
+    int chunks_per_n, total_chunks, splits;
     int n_tiles, m_tiles;
     int XR;              // staged input rows per n-tile
     int segw, segs;      // input-row staging: segs loads of segw (32 or 64) positions
@@ -458,6 +497,8 @@ void wgrad_gemm(WgradArgs g) {
     const int gsz = 64 * GP;
     const int stage = gsz + g.XR * g.rs;
     const bool do_bias = g.Pb && nt == 0;
+    // a wave whose 64 columns all lie past NN (the last n-tile) only stages
+    const bool live = n0 + wn * 64 < g.NN;
     constexpr unsigned OOB = 0x80000000u;  // any offset >= the buffer size reads 0
 
     // this lane's two B columns: staged row offset of (c - ci_lo, t)
@@ -507,8 +548,9 @@ void wgrad_gemm(WgradArgs g) {
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
     double bsum = 0.0;
 
-    const int ch0 = z * g.chunks_per_split;
-    const int ch1 = min(ch0 + g.chunks_per_split, g.total_chunks);
+    // split z: chunks [z * total / splits, (z + 1) * total / splits)
+    const int ch0 = static_cast<int>(static_cast<long>(z) * g.total_chunks / g.splits);
+    const int ch1 = static_cast<int>(static_cast<long>(z + 1) * g.total_chunks / g.splits);
     if (ch0 < ch1) issue(ch0, 0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -541,20 +583,22 @@ void wgrad_gemm(WgradArgs g) {
             acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
             acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
         };
-        float pa0, pa1, pb0, pb1, qa0, qa1, qb0, qb1;
-        ld(0, pa0, pa1, pb0, pb1);
+        if (live) {
+            float pa0, pa1, pb0, pb1, qa0, qa1, qb0, qb1;
+            ld(0, pa0, pa1, pb0, pb1);
 #pragma unroll
-        for (int u = 0; u < KC / 2; u += 2) {
-            ld(u + 1, qa0, qa1, qb0, qb1);
-            mm(pa0, pa1, pb0, pb1);
-            ld(u + 2, pa0, pa1, pb0, pb1);
-            mm(qa0, qa1, qb0, qb1);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+            for (int u = 0; u < KC / 2; u += 2) {
+                ld(u + 1, qa0, qa1, qb0, qb1);
+                mm(pa0, pa1, pb0, pb1);
+                ld(u + 2, pa0, pa1, pb0, pb1);
+                mm(qa0, qa1, qb0, qb1);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+            }
         }
         __builtin_amdgcn_s_waitcnt(0);  // this wave's staging loads landed
         __syncthreads();
@@ -709,12 +753,22 @@ __global__ void pool_wgrad(const float* X, long x_bs, const float* dY, long dy_b
     }
 }
 
+// LDS bytes of one conv_gemm block (two stages) for chunk CK and an effective
+// correlation of kk taps at stride ss and dilation dd.
+size_t conv_lds_bytes(int CK, int kk, int ss, int dd) {
+    const long span = static_cast<long>(BN - 1) * ss + static_cast<long>(kk - 1) * dd + 1;
+    const long span_p = (span + 63) / 64 * 64;
+    return 2 * (static_cast<size_t>(CK) * kk * BM + static_cast<size_t>(CK) * span_p) * sizeof(float);
+}
+
 // Input channels per K chunk: a power of two in [2, 32] so that it divides
 // the 32-padded channel count of the packed weights (no chunk runs past them),
-// with CK*k near 32 weight rows per chunk (small stages: 4-6 blocks per CU).
-int pick_ck(int k) {
+// at most 32 weight rows (CK*k) per chunk, and the largest such chunk whose two
+// stages fit 32 KB of LDS: five blocks per CU, the most the kernel's ~96 VGPRs
+// allow. Only when even CK = 2 is larger does the stage size set occupancy.
+int pick_ck(int k, int s, int d) {
     int ck = 32;
-    while (ck > 2 && ck * k > 32) ck >>= 1;
+    while (ck > 2 && (ck * k > 32 || conv_lds_bytes(ck, k, s, d) > 32 * 1024)) ck >>= 1;
     return ck;
 }
 
@@ -726,18 +780,50 @@ int grid1d(long n) {
 }
 
 template <int CK>
-int launch_conv(kdec_ctx* ctx, const GemmArgs& g, unsigned blocks, size_t lds) {
+const void* conv_kernel() {
     static bool attr = false;
     if (!attr) {
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_gemm<CK>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         attr = true;
     }
-    hipLaunchKernelGGL(conv_gemm<CK>, dim3(blocks), dim3(NT), lds, ctx->stream, g);
-    return 0;
+    return reinterpret_cast<const void*>(&conv_gemm<CK>);
+}
+
+const void* conv_kernel_for(int CK) {
+    switch (CK) {
+        case 2: return conv_kernel<2>();
+        case 4: return conv_kernel<4>();
+        case 8: return conv_kernel<8>();
+        case 16: return conv_kernel<16>();
+        case 32: return conv_kernel<32>();
+        default: return nullptr;
+    }
+}
+
+// Resident conv_gemm blocks per CU for chunk CK and `lds` bytes (cached).
+int conv_blocks_per_cu(int CK, size_t lds) {
+    static std::mutex mu;
+    static std::map<std::pair<int, size_t>, int> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    const auto key = std::make_pair(CK, lds);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv_kernel_for(CK), NT, lds) != hipSuccess ||
+        per_cu < 1)
+        per_cu = 1;
+    cache[key] = per_cu;
+    return per_cu;
 }
 
 // Launches conv_gemm over an already packed A.
+//
+// Work plan: with S resident blocks, T tiles take T / S whole rounds plus a
+// last round of r = T mod S tiles. When r is well below S, the last r tiles
+// (in logical order) are split over their channel chunks into f parts,
+// f <= S / r, so that the last round costs about 1/f of a tile instead of a
+// whole one; their partial sums are reduced by tile_reduce.
 int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
              double flops) {
     const int CK = g.CK;
@@ -745,36 +831,35 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
     const int ss = g.n_phase > 1 ? 1 : g.s;
     const int dd = g.n_phase > 1 ? 1 : g.d;
     if (CK * kk > 64 || (CK * kk) % 2) return fail(ctx, KDEC_EINVAL, "conv: kernel too long for the weight stage");
-    const long span = static_cast<long>(BN - 1) * ss + static_cast<long>(kk - 1) * dd + 1;
-    const long span_p = (span + 63) / 64 * 64;
-    const size_t stage = static_cast<size_t>(CK) * kk * BM + static_cast<size_t>(CK) * span_p;
-    const size_t lds = 2 * stage * sizeof(float);
+    const size_t lds = conv_lds_bytes(CK, kk, ss, dd);
     if (lds > 160 * 1024) return fail(ctx, KDEC_EINVAL, "conv: tile does not fit LDS");
     if (static_cast<long>(g.C_in) * g.L_in * 4 > 0x7fffffffL)
         return fail(ctx, KDEC_EINVAL, "conv: input too large for one buffer descriptor");
+    const void* kern = conv_kernel_for(CK);
+    if (!kern) return fail(ctx, KDEC_EINVAL, "conv: unsupported channel chunk");
     int max_q = g.n_q;
     if (g.n_phase > 1) max_q = static_cast<int>(cdiv(g.L_y + g.ph_s, g.ph_s)) + 1;
     g.m_tiles = m_tiles;
     g.q_tiles = static_cast<int>(cdiv(max_q, BN));
-    // small grids (fewer blocks than two per CU) split the channel chunks,
-    // at least 4 chunks a part, towards four blocks per CU
-    const long tiles = static_cast<long>(g.m_tiles) * g.q_tiles * N * g.n_phase;
+    g.nz = N * g.n_phase;
+    const long tiles = static_cast<long>(g.m_tiles) * g.q_tiles * g.nz;
+    if (tiles > 0x7fffffffL / 16) return fail(ctx, KDEC_EINVAL, "conv: grid too large");
+    const long slots = static_cast<long>(conv_blocks_per_cu(CK, lds)) * ctx->num_cus;
     const int nchunks = g.cin_pad / CK;
-    int splits = 1;
-    if (tiles < 2L * ctx->num_cus) {
-        const long want = cdiv(4L * ctx->num_cus, tiles);
-        const long most = std::max(1, nchunks / 4);
-        splits = static_cast<int>(std::min(std::min(want, most), 16L));
-        splits = static_cast<int>(cdiv(nchunks, cdiv(nchunks, splits)));  // no empty parts
-    }
-    g.splits = splits;
-    const long blocks = tiles * splits;
-    if (blocks > 0x7fffffffL) return fail(ctx, KDEC_EINVAL, "conv: grid too large");
-    Workspace part(ctx, splits > 1 ? static_cast<size_t>(splits) * N * g.C_out * g.L_y * sizeof(float) : 0);
-    if (splits > 1) {
+    const long rem = tiles % slots;
+    long f = 1;
+    if (rem > 0) f = std::min(std::min(slots / rem, static_cast<long>(nchunks / 4)), 16L);
+    if (f < 2) f = 1;
+    g.fsplit = static_cast<int>(f);
+    g.split_tiles = f > 1 ? static_cast<int>(rem) : 0;
+    g.full_tiles = static_cast<int>(tiles - g.split_tiles);
+    g.full_per_xcd = static_cast<int>(cdiv(g.full_tiles, 8));
+    g.parts_per_xcd = static_cast<int>(cdiv(static_cast<long>(g.split_tiles) * g.fsplit, 8));
+    const long blocks = 8L * (g.full_per_xcd + g.parts_per_xcd);
+    Workspace part(ctx, static_cast<size_t>(g.split_tiles) * g.fsplit * BM * BN * sizeof(float));
+    if (g.split_tiles > 0) {
         if (!part.p) return KDEC_ENOMEM;
         g.P = part.as<float>();
-        g.p_split = static_cast<long>(N) * g.C_out * g.L_y;
     }
     // algorithmic HBM bytes: input and weights read once, output written once
     // (read too when accumulating), residual read once
@@ -783,21 +868,13 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
                           static_cast<double>(N) * g.C_out * g.L_y * (g.beta != 0.0f ? 2 : 1));
     if (g.R) bytes += 4.0 * static_cast<double>(N) * g.C_out * g.L_y;
     ProfScope ps(ctx, fam, flops, bytes);
-    const unsigned nb = static_cast<unsigned>(blocks);
-    switch (CK) {
-        case 2: launch_conv<2>(ctx, g, nb, lds); break;
-        case 4: launch_conv<4>(ctx, g, nb, lds); break;
-        case 8: launch_conv<8>(ctx, g, nb, lds); break;
-        case 16: launch_conv<16>(ctx, g, nb, lds); break;
-        case 32: launch_conv<32>(ctx, g, nb, lds); break;
-        default: return fail(ctx, KDEC_EINVAL, "conv: unsupported channel chunk");
-    }
+    void* args[] = {&g};
+    if (hipLaunchKernel(kern, dim3(static_cast<unsigned>(blocks)), dim3(NT), args, lds, ctx->stream) != hipSuccess)
+        return fail(ctx, KDEC_EHIP, std::string(fam) + ": launch failed");
     if (int rc = launch_check(ctx, fam)) return rc;
-    if (splits > 1) {
-        const long tot = static_cast<long>(g.C_out) * g.L_y;
-        hipLaunchKernelGGL(split_reduce, dim3(grid1d(tot), N), dim3(256), 0, ctx->stream, g.P, splits, g.p_split, g.Y,
-                           g.y_bs, g.bias, g.R, g.r_bs, g.scale, g.beta, g.C_out, g.L_y);
-        return launch_check(ctx, "split_reduce");
+    if (g.split_tiles > 0) {
+        hipLaunchKernelGGL(tile_reduce, dim3(BM * BN / 256, g.split_tiles), dim3(256), 0, ctx->stream, g);
+        return launch_check(ctx, "tile_reduce");
     }
     return KDEC_OK;
 }
@@ -820,7 +897,7 @@ int kdec_conv1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
     KDEC_CHECK(ctx, L > 0 && L_out > 0, "kdec_conv1d_fwd: empty output");
     KDEC_CHECK(ctx, x_bs >= static_cast<long>(C_in) * L && y_bs >= static_cast<long>(C_out) * L_out,
                "kdec_conv1d_fwd: batch stride too small");
-    const int CK = pick_ck(k);
+    const int CK = pick_ck(k, stride, dil);
     const int cin_pad = static_cast<int>(cdiv(C_in, 32) * 32);
     const int m_pad = static_cast<int>(cdiv(C_out, BM) * BM);
     Workspace A(ctx, static_cast<size_t>(cin_pad) * k * m_pad * sizeof(float));
@@ -854,7 +931,7 @@ int kdec_conv1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
     KDEC_CHECK(ctx, pp >= 0, "kdec_conv1d_dgrad: padding larger than the receptive field");
     KDEC_CHECK(ctx, dy_bs >= static_cast<long>(C_out) * L_out && dx_bs >= static_cast<long>(C_in) * L,
                "kdec_conv1d_dgrad: batch stride too small");
-    const int CK = pick_ck(k);
+    const int CK = pick_ck(k, 1, dil);
     const int cpad = static_cast<int>(cdiv(C_out, 32) * 32);
     const int m_pad = static_cast<int>(cdiv(C_in, BM) * BM);
     Workspace A(ctx, static_cast<size_t>(cpad) * k * m_pad * sizeof(float));
@@ -921,15 +998,17 @@ int wgrad_splits(kdec_ctx* ctx, int total_chunks, long tiles, size_t lds) {
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&wgrad_gemm), WG_NT,
                                                      lds) != hipSuccess || per_cu < 1)
         per_cu = 1;
+    // WG_ROUNDS rounds of resident blocks, never one block more: every block
+    // gets the same number of chunks (within one), so a block past the last
+    // full round would cost a whole extra round
     const long slots = static_cast<long>(ctx->num_cus) * per_cu * WG_ROUNDS;
-    long splits = (slots + tiles - 1) / tiles;
+    long splits = slots / tiles;
     // at least 8 chunks per split: shorter runs spend more on the partial
     // tile's write-out and reduction than on the GEMM
-    const long max_splits = (total_chunks + 7) / 8;
+    const long max_splits = total_chunks / 8;
     if (splits > max_splits) splits = max_splits;
     if (splits < 1) splits = 1;
-    const long cps = (total_chunks + splits - 1) / splits;
-    return static_cast<int>((total_chunks + cps - 1) / cps);
+    return static_cast<int>(splits);
 }
 
 // out (M x C_x*k) += the weight grad; db (M) += the row sums of G when
@@ -942,11 +1021,10 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
     const int n_tiles = static_cast<int>(cdiv(NN, WG_BN));
     const int chunks_per_n = static_cast<int>(cdiv(L_g, KC));
     const int total_chunks = chunks_per_n * N;
-    // one round of resident blocks: the fewest splits (least partial traffic)
-    // that still fills every CU
+    // split the position chunks so that the blocks fill WG_ROUNDS rounds of
+    // the resident slots
     const int splits = wgrad_splits(ctx, total_chunks, static_cast<long>(m_tiles) * n_tiles,
                                     wgrad_lds_bytes(k, s, d));
-    const int cps = static_cast<int>(cdiv(total_chunks, splits));
     const long MN = static_cast<long>(M) * NN;
     Workspace P(ctx, static_cast<size_t>(splits) * MN * sizeof(float));
     Workspace Pb(ctx, db ? static_cast<size_t>(splits) * M * sizeof(float) : 0);
@@ -956,7 +1034,7 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
     a.Pb = db ? Pb.as<float>() : nullptr;
     a.M = M; a.C_x = C_x; a.L_x = L_x; a.L_g = L_g; a.k = k; a.s = s; a.d = d; a.p = p;
     a.NN = NN; a.chunks_per_n = chunks_per_n; a.total_chunks = total_chunks;
-    a.chunks_per_split = cps;
+    a.splits = splits;
     a.n_tiles = n_tiles;
     a.m_tiles = m_tiles;
     const WgradLayout lay = wgrad_layout(k, s, d);
@@ -1032,7 +1110,7 @@ int kdec_convt1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
     KDEC_CHECK(ctx, y_bs >= static_cast<long>(C_out) * L_out && x_bs >= static_cast<long>(C_in) * L,
                "kdec_convt1d_fwd: batch stride too small");
     const int kt = static_cast<int>(cdiv(k, stride));
-    const int CK = pick_ck(kt);
+    const int CK = pick_ck(kt, 1, 1);
     const int cin_pad = static_cast<int>(cdiv(C_in, 32) * 32);
     const int m_pad = static_cast<int>(cdiv(C_out, BM) * BM);
     const long ph = static_cast<long>(cin_pad) * kt * m_pad;
@@ -1065,7 +1143,7 @@ int kdec_convt1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
                "kdec_convt1d_dgrad: bad arguments");
     const int L_out = (L - 1) * stride - 2 * pad + (k - 1) + op + 1;
     KDEC_CHECK(ctx, L > 0 && L_out > 0, "kdec_convt1d_dgrad: empty output");
-    const int CK = pick_ck(k);
+    const int CK = pick_ck(k, stride, 1);
     const int cpad = static_cast<int>(cdiv(C_out, 32) * 32);
     const int m_pad = static_cast<int>(cdiv(C_in, BM) * BM);
     const long tot = static_cast<long>(cpad) * k * m_pad;

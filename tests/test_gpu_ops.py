@@ -116,6 +116,32 @@ def test_conv1d_fwd_dgrad_wgrad(K, N, C_in, C_out, L, k, s, p, d):
     assert_close(h(db), rb, GRAD_TOL, "conv1d backward_bias")
 
 
+@pytest.mark.parametrize("k,d", [(7, 3), (3, 1)])
+def test_conv1d_grid_beyond_one_round(K, k, d):
+    # 1301 output tiles: more than one round of resident blocks, so the last
+    # tiles run as channel-chunk parts reduced by tile_reduce while the others
+    # run whole. Reference: torch's float64 conv1d on the CPU (the C oracle
+    # covers the same kernel at the small sizes above).
+    N, C_in, C_out, L = 1, 32, 128, 128 * 1300 + 1
+    p = d * (k - 1) // 2
+    x, W, b = rnd(N, C_in, L), rnd(C_out, C_in * k, scale=0.2), rnd(C_out)
+    R = rnd(N, C_out, L)
+    Y = torch.empty(N, C_out, L, device="cuda")
+    K.call("kdec_conv1d_fwd", P(g(x)), C_in * L, P(g(W)), P(g(b)), P(Y), C_out * L, N, C_in, L, C_out, k, 1,
+           p, d, P(g(R)), C_out * L, 0.5, 0.0)
+    F = torch.nn.functional
+    xt = torch.from_numpy(x).double()
+    Wt = torch.from_numpy(W).double().reshape(C_out, C_in, k)
+    ref = 0.5 * (F.conv1d(xt, Wt, torch.from_numpy(b).double(), padding=p, dilation=d) + torch.from_numpy(R).double())
+    assert_close(h(Y), ref.numpy(), FWD_TOL, "conv1d forward, split tail tiles")
+    dY = rnd(N, C_out, L)
+    dX = torch.empty(N, C_in, L, device="cuda")
+    K.call("kdec_conv1d_dgrad", P(g(W)), P(g(dY)), C_out * L, P(dX), C_in * L, N, C_in, L, C_out, k, 1, p, d,
+           1.0, 0.0)
+    ref = F.conv_transpose1d(torch.from_numpy(dY).double(), Wt, padding=p, dilation=d)
+    assert_close(h(dX), ref.numpy(), GRAD_TOL, "conv1d backward_input, split tail tiles")
+
+
 def test_conv1d_batch_stride_and_accumulate(K):
     # outputs written into a channel slice of a wider tensor, beta accumulate
     N, C_in, C_out, L, k = 2, 16, 8, 40, 3
