@@ -117,13 +117,37 @@ struct AdainArgs {
     int C, L;
 };
 
-__device__ inline float act_fwd(int act, float s, float slope, float a) {
+// ia = 1 / alpha, formed once per row
+__device__ inline float act_fwd(int act, float s, float slope, float a, float ia) {
     if (act == KDEC_ACT_LEAKY) return s > 0.0f ? s : slope * s;
     if (act == KDEC_ACT_SNAKE) {
         const float sn = sinf(a * s);
-        return s + sn * sn / a;
+        return s + sn * sn * ia;
     }
     return s;
+}
+
+// ds = dY * act'(s), the grad at the affine output s = g1 * xh + beta. For
+// Snake, y = s + sin^2(th) / a with th = a * s:
+//   dy/ds = 1 + sin(2 th),   dy/da = (th * sin(2 th) - sin^2(th)) / a^2,
+// and `sa` accumulates dY times the numerator (the row sum is scaled by 1/a^2
+// once). sin / cos are the hardware ones: |th| stays small here, where their
+// error is ~1e-6 absolute, far inside the gradient tolerance.
+__device__ inline float act_bwd(int act, float dy, float s, float slope, float a, float& sa) {
+    if (act == KDEC_ACT_LEAKY) return s > 0.0f ? dy : slope * dy;
+    if (act == KDEC_ACT_SNAKE) {
+        const float th = a * s;
+        const float sn = __sinf(th), cs = __cosf(th);
+        const float s2 = 2.0f * sn * cs;
+        sa += dy * (th * s2 - sn * sn);
+        return dy * (1.0f + s2);
+    }
+    return dy;
+}
+
+// the 1/a^2 of the Snake alpha-grad, applied to a row (or chunk) sum
+__device__ inline double alpha_scale(int act, float a) {
+    return act == KDEC_ACT_SNAKE ? 1.0 / (static_cast<double>(a) * a) : 0.0;
 }
 
 // grid (chunks of CH, N*C)
@@ -134,7 +158,8 @@ __global__ __launch_bounds__(RT) void adain_act_fwd_k(AdainArgs g, float* Y, lon
     const float2 st = g.stats[row];
     const float g1 = 1.0f + g.gamma[n * g.gb_bs + c];
     const float bt = g.beta ? g.beta[n * g.gb_bs + c] : 0.0f;
-    const float a = g.act == KDEC_ACT_SNAKE ? g.alpha[c] : 0.0f;
+    const float a = g.act == KDEC_ACT_SNAKE ? g.alpha[c] : 1.0f;
+    const float ia = 1.0f / a;
     const long off = static_cast<long>(c) * g.L;
     const float* x = g.X + n * g.x_bs + off;
     float* y = Y + n * y_bs + off;
@@ -153,21 +178,8 @@ __global__ __launch_bounds__(RT) void adain_act_fwd_k(AdainArgs g, float* Y, lon
         const float xh = (v[j] - st.x) * st.y;
         const float s = g1 * xh + bt;
         if (yp) yp[l] = s;
-        y[l] = act_fwd(g.act, s, g.slope, a);
+        y[l] = act_fwd(g.act, s, g.slope, a, ia);
     }
-}
-
-// ds = dY * act'(s): the grad at the affine output, s = g1 * xh + beta.
-__device__ inline float act_bwd(int act, float dy, float s, float slope, float a, double& sa) {
-    if (act == KDEC_ACT_LEAKY) return s > 0.0f ? dy : slope * dy;
-    if (act == KDEC_ACT_SNAKE) {
-        float sn, cs;
-        sincosf(a * s, &sn, &cs);
-        const float s2 = 2.0f * sn * cs;  // sin(2as) from one shared range reduction
-        sa += static_cast<double>(dy) * (s * s2 / a - sn * sn / (a * a));
-        return dy * (1.0f + s2);
-    }
-    return dy;
 }
 
 // part[(row*nch + ch)*3 + {0,1,2}] = chunk sums of ds, ds*xh and (SNAKE) the
@@ -193,18 +205,19 @@ __global__ __launch_bounds__(RT) void adain_bwd_part_k(AdainArgs g, const float*
         xv[j] = in ? x[l] : st.x;   // xh = 0 and ds = 0 past the row: no contribution
         dv[j] = in ? dy[l] : 0.0f;
     }
-    double sd = 0.0, sdx = 0.0, sa = 0.0;
+    // per-thread sums of EPT terms in float, across the block in double
+    float fsd = 0.0f, fsdx = 0.0f, fsa = 0.0f;
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
         const float xh = (xv[j] - st.x) * st.y;
         const float s = g1 * xh + bt;
-        const float ds = act_bwd(g.act, dv[j], s, g.slope, a, sa);
-        sd += ds;
-        sdx += static_cast<double>(ds) * xh;
+        const float ds = act_bwd(g.act, dv[j], s, g.slope, a, fsa);
+        fsd += ds;
+        fsdx += ds * xh;
     }
-    sd = block_sum(sd, red);
-    sdx = block_sum(sdx, red);
-    if (g.act == KDEC_ACT_SNAKE) sa = block_sum(sa, red);
+    const double sd = block_sum(fsd, red);
+    const double sdx = block_sum(fsdx, red);
+    const double sa = g.act == KDEC_ACT_SNAKE ? block_sum(fsa, red) * alpha_scale(g.act, a) : 0.0;
     if (threadIdx.x == 0) {
         double* p = part + (static_cast<long>(row) * nch + ch) * 3;
         p[0] = sd;
@@ -266,13 +279,8 @@ __global__ __launch_bounds__(RT) void adain_bwd_apply_k(AdainArgs g, const float
         if (l >= g.L) break;
         const float xh = (xv[j] - st.x) * st.y;
         const float s = g1 * xh + bt;
-        float ds = dv[j];
-        if (g.act == KDEC_ACT_LEAKY) ds = s > 0.0f ? ds : g.slope * ds;
-        else if (g.act == KDEC_ACT_SNAKE) {
-            float sn, cs;
-            sincosf(a * s, &sn, &cs);
-            ds = ds * (1.0f + 2.0f * sn * cs);
-        }
+        float unused = 0.0f;
+        const float ds = act_bwd(g.act, dv[j], s, g.slope, a, unused);
         float v = k1 * (ds - mv.x - xh * mv.y);
         if (r) v += rv[j];
         dx[l] = v;
@@ -342,7 +350,8 @@ __global__ __launch_bounds__(NTB) void adain_fwd_row_k(AdainArgs g, float eps, f
     if (threadIdx.x == 0) stats[row] = st;
     const float g1 = 1.0f + g.gamma[n * g.gb_bs + c];
     const float bt = g.beta ? g.beta[n * g.gb_bs + c] : 0.0f;
-    const float a = g.act == KDEC_ACT_SNAKE ? g.alpha[c] : 0.0f;
+    const float a = g.act == KDEC_ACT_SNAKE ? g.alpha[c] : 1.0f;
+    const float ia = 1.0f / a;
     const __amdgpu_buffer_rsrc_t yr = row_rsrc(Y + n * y_bs + off, g.L);
     const __amdgpu_buffer_rsrc_t pr = row_rsrc(Yp ? Yp + n * yp_bs + off : Y, Yp ? g.L : 0);
 #pragma unroll UN
@@ -350,31 +359,16 @@ __global__ __launch_bounds__(NTB) void adain_fwd_row_k(AdainArgs g, float eps, f
         const float xj = KEEP ? v[KEEP ? j : 0] : row_ld(xr, vo, j, NTB);
         const float xh = (xj - st.x) * st.y;
         const float s = g1 * xh + bt;
-        row_st(yr, act_fwd(g.act, s, g.slope, a), vo, j, NTB);
+        row_st(yr, act_fwd(g.act, s, g.slope, a, ia), vo, j, NTB);
         row_st(pr, s, vo, j, NTB);  // dropped without a pre-activation output
     }
-}
-
-// ds = dY * act'(s) for the backward row kernel, with the per-thread alpha-grad
-// term accumulated in float (the block reduction is in double). The Snake
-// derivative uses the hardware sin / cos (|a*s| stays small here, where their
-// error is ~1e-6 absolute, far inside the gradient tolerance).
-__device__ inline float act_bwd_fast(int act, float dy, float s, float slope, float a, float& sa) {
-    if (act == KDEC_ACT_LEAKY) return s > 0.0f ? dy : slope * dy;
-    if (act == KDEC_ACT_SNAKE) {
-        const float th = a * s;
-        const float sn = __sinf(th), cs = __cosf(th);
-        const float s2 = 2.0f * sn * cs;
-        sa += dy * (s * s2 / a - sn * sn / (a * a));
-        return dy * (1.0f + s2);
-    }
-    return dy;
 }
 
 template <int NTB, int EPR, bool BOTH>
 __global__ __launch_bounds__(NTB) void adain_bwd_row_k(AdainArgs g, const float* dY, long dy_bs, const float* R,
                                                       long r_bs, float* dX, long dx_bs, float* dgamma,
-                                                      float* dbeta, long dgb_bs, float* dalpha_part) {
+                                                      float* dbeta, long dgb_bs, float* dalpha_part,
+                                                      float* dalpha_acc) {
     __shared__ double red[NTB / 64];
     const int row = blockIdx.x;
     const int n = row / g.C, c = row - n * g.C;
@@ -399,18 +393,19 @@ __global__ __launch_bounds__(NTB) void adain_bwd_row_k(AdainArgs g, const float*
         const float dyj = BOTH ? dv[j] : row_ld(dr, vo, j, NTB);
         const float xh = (xv[j] - st.x) * st.y;
         const float s = g1 * xh + bt;
-        const float ds = act_bwd_fast(g.act, dyj, s, g.slope, a, fsa);
+        const float ds = act_bwd(g.act, dyj, s, g.slope, a, fsa);
         if (BOTH) dv[j] = ds;
         fsd += ds;
         fsdx += ds * xh;
     }
     const double sd = block_sum_n<NTB>(fsd, red);
     const double sdx = block_sum_n<NTB>(fsdx, red);
-    const double sa = g.act == KDEC_ACT_SNAKE ? block_sum_n<NTB>(fsa, red) : 0.0;
+    const double sa = g.act == KDEC_ACT_SNAKE ? block_sum_n<NTB>(fsa, red) * alpha_scale(g.act, a) : 0.0;
     if (threadIdx.x == 0) {
         if (dgamma) dgamma[n * dgb_bs + c] = static_cast<float>(sdx);
         if (dbeta) dbeta[n * dgb_bs + c] = static_cast<float>(sd);
         if (dalpha_part) dalpha_part[row] = static_cast<float>(sa);
+        if (dalpha_acc) dalpha_acc[c] += static_cast<float>(sa);  // one utterance: one row per channel
     }
     const float mds = static_cast<float>(sd / g.L);
     const float mdsx = static_cast<float>(sdx / g.L);
@@ -426,7 +421,7 @@ __global__ __launch_bounds__(NTB) void adain_bwd_row_k(AdainArgs g, const float*
             ds = dv[j];
         } else {
             float unused = 0.0f;
-            ds = act_bwd_fast(g.act, row_ld(dr, vo, j, NTB), g1 * xh + bt, g.slope, a, unused);
+            ds = act_bwd(g.act, row_ld(dr, vo, j, NTB), g1 * xh + bt, g.slope, a, unused);
         }
         float val = k1 * (ds - mds - xh * mdsx);
         val += row_ld(rr, vo, j, NTB);
@@ -575,11 +570,11 @@ int launch_fwd_row(kdec_ctx* ctx, RowShape rsh, unsigned rows, const AdainArgs& 
 
 int launch_bwd_row(kdec_ctx* ctx, RowShape rsh, unsigned rows, const AdainArgs& g, const float* dY, long dy_bs,
                    const float* R, long r_bs, float* dX, long dx_bs, float* dgamma, float* dbeta, long dgb_bs,
-                   float* apart) {
+                   float* apart, float* aacc) {
 #define KDEC_BWD_ROW(T, E, B)                                                                                    \
     if (rsh.ntb == T && rsh.epr == E) {                                                                          \
         hipLaunchKernelGGL((adain_bwd_row_k<T, E, B>), dim3(rows), dim3(T), 0, ctx->stream, g, dY, dy_bs, R, r_bs, \
-                           dX, dx_bs, dgamma, dbeta, dgb_bs, apart);                                             \
+                           dX, dx_bs, dgamma, dbeta, dgb_bs, apart, aacc);                                       \
         return launch_check(ctx, "adain_bwd_row");                                                              \
     }
     KDEC_BWD_ROW(256, 4, true)
@@ -683,13 +678,17 @@ int kdec_adain_act_bwd(kdec_ctx* ctx, const float* X, long x_bs,
     const double bytes = 4.0 * static_cast<double>(rows) * L * 3 +
                          (R ? 4.0 * static_cast<double>(rows) * L : 0.0);
     if (rsh.ntb) {
+        // one utterance: each channel's alpha grad comes from one row, which
+        // adds it directly; otherwise per-row shares are summed in order
+        const bool direct = want_alpha && N == 1;
         {
             ProfScope ps(ctx, "adain_bwd", 0, bytes);
             if (int rc = launch_bwd_row(ctx, rsh, static_cast<unsigned>(rows), g, dY, dy_bs, R, r_bs, dX, dx_bs,
-                                        dgamma, dbeta, dgb_bs, want_alpha ? apart.as<float>() : nullptr))
+                                        dgamma, dbeta, dgb_bs, want_alpha && !direct ? apart.as<float>() : nullptr,
+                                        direct ? dalpha : nullptr))
                 return rc;
         }
-        if (want_alpha) {
+        if (want_alpha && !direct) {
             hipLaunchKernelGGL(dalpha_reduce, dim3(static_cast<unsigned>(cdiv(C, 256))), dim3(256), 0, ctx->stream,
                                apart.as<float>(), dalpha, N, C);
             return launch_check(ctx, "dalpha_reduce");
