@@ -181,7 +181,7 @@ __device__ inline bool block_work(const GemmArgs& g, int& tile, int& part) {
 // ping-pong over two register sets, each step's LDS reads issued between the
 // MFMAs of the step before, so the read latency hides behind matrix work.
 template <int CK>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(5)))
 void conv_gemm(GemmArgs g) {
     extern __shared__ float smem[];
     const int tid = threadIdx.x;
