@@ -998,17 +998,17 @@ int wgrad_splits(kdec_ctx* ctx, int total_chunks, long tiles, size_t lds) {
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&wgrad_gemm), WG_NT,
                                                      lds) != hipSuccess || per_cu < 1)
         per_cu = 1;
-    // WG_ROUNDS rounds of resident blocks, never one block more: every block
-    // gets the same number of chunks (within one), so a block past the last
-    // full round would cost a whole extra round
-    const long slots = static_cast<long>(ctx->num_cus) * per_cu * WG_ROUNDS;
-    long splits = slots / tiles;
-    // at least 8 chunks per split: shorter runs spend more on the partial
-    // tile's write-out and reduction than on the GEMM
-    const long max_splits = total_chunks / 8;
-    if (splits > max_splits) splits = max_splits;
-    if (splits < 1) splits = 1;
-    return static_cast<int>(splits);
+    // The most whole rounds of resident blocks, up to WG_ROUNDS, whose splits
+    // keep at least 8 chunks each (shorter runs spend more on the partial
+    // tile's write-out and reduction than on the GEMM); never a block past the
+    // last whole round: blocks carry equal work (within one chunk), so one
+    // more would cost a whole extra round.
+    const long slots = static_cast<long>(ctx->num_cus) * per_cu;
+    for (int r = WG_ROUNDS; r >= 1; --r) {
+        const long splits = r * slots / tiles;
+        if (splits >= 1 && total_chunks / splits >= 8) return static_cast<int>(splits);
+    }
+    return static_cast<int>(std::max(1L, std::min(slots / tiles, static_cast<long>(total_chunks / 8))));
 }
 
 // out (M x C_x*k) += the weight grad; db (M) += the row sums of G when
