@@ -464,7 +464,7 @@ struct WgradArgs {
     int chunks_per_n, total_chunks, splits;
     int n_tiles, m_tiles;
     int XR;              // staged input rows per n-tile
-    int segw, segs;      // input-row staging: segs loads of segw (32 or 64) positions
+    int span, segs;      // input-row staging: `span` positions as segs loads of up to 64
     int rs;              // LDS row stride of the staged input rows
 };
 
@@ -530,11 +530,11 @@ void wgrad_gemm(WgradArgs g) {
         for (int it = wave; it < nitems; it += 2 * WG_WN) {
             const int r = it / g.segs, sg = it - r * g.segs;
             const int c = ci_lo + r;
-            const int pos = x0 + sg * g.segw + lane;
+            const int pos = x0 + sg * 64 + lane;
             const unsigned off = (c < g.C_x && pos >= 0 && pos < g.L_x)
                                      ? static_cast<unsigned>(c * g.L_x + pos) * 4u : OOB;
-            if (lane < g.segw)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + gsz + r * g.rs + sg * g.segw, 4,
+            if (sg * 64 + lane < g.span)  // exactly the row's span: rows pack at stride rs >= span
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + gsz + r * g.rs + sg * 64, 4,
                                                          static_cast<int>(off), 0, 0, 0);
         }
     };
@@ -953,25 +953,25 @@ int kdec_conv1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
 
 // LDS bytes of one wgrad_gemm block (two stages) and its input-row layout.
 struct WgradLayout {
-    int XR, segw, segs, rs;
+    int XR, span, segs, rs;
     size_t lds;
 };
 
 WgradLayout wgrad_layout(int k, int s, int d) {
     WgradLayout w{};
     w.XR = (WG_BN - 1) / k + 2;
-    const long span = static_cast<long>(KC - 1) * s + static_cast<long>(k - 1) * d + 1;
-    w.segw = span <= 32 ? 32 : 64;
-    w.segs = static_cast<int>(cdiv(span, w.segw));
-    // column n = c*k + t sits at c*rs + t*d: rs = k*d (mod 64) puts it on
-    // bank n*d, distinct across 32 lanes for odd d; for k = 1 any odd rs.
-    const long base = static_cast<long>(w.segs) * w.segw;
-    long rs = base;
+    w.span = static_cast<int>(static_cast<long>(KC - 1) * s + static_cast<long>(k - 1) * d + 1);
+    w.segs = static_cast<int>(cdiv(w.span, 64));
+    // Column n = c*k + t sits at c*rs + t*d: with rs = k*d (mod 32) that is
+    // n*d (mod 32), distinct banks across 32 lanes for odd d; for k = 1 any
+    // odd rs. The smallest such rs >= span keeps the stage small (two blocks
+    // per CU for the k = 3 dilated convs).
+    long rs = w.span;
     if (k == 1) {
         if (rs % 2 == 0) ++rs;
     } else {
-        const long want = (static_cast<long>(k) * d) % 64;
-        rs = base + ((want - base % 64) % 64 + 64) % 64;
+        const long want = (static_cast<long>(k) * d) % 32;
+        rs += ((want - rs % 32) % 32 + 32) % 32;
     }
     w.rs = static_cast<int>(rs);
     w.lds = 2 * (static_cast<size_t>(64) * GP + static_cast<size_t>(w.XR) * w.rs) * sizeof(float);
@@ -1039,7 +1039,7 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
     a.m_tiles = m_tiles;
     const WgradLayout lay = wgrad_layout(k, s, d);
     a.XR = lay.XR;
-    a.segw = lay.segw;
+    a.span = lay.span;
     a.segs = lay.segs;
     a.rs = lay.rs;
     if (static_cast<long>(L_x) * 4 > 0x7fffffffL || static_cast<long>(L_g) * 4 > 0x7fffffffL)
