@@ -42,32 +42,29 @@ def make_inputs(cfg, N, T, tag, unvoiced=0.2):
 
 
 def cpu_baseline(cfg, params):
-    """The oracle (CPU restatement of the reference path, OpenMP) on config 0:
-    one utterance of T = 64 frames (1.6 s of audio), forward + backward with the
-    same extensions, timed on this host's cores. A reported baseline."""
+    """The oracle (CPU restatement of the reference path, OpenMP) on a bounded
+    sample of the benchmarked workload: one of the B utterances at the same
+    T = 512 (12.8 s of audio), forward + backward with the same extensions,
+    timed once on this host's cores (about half a minute). A reported
+    baseline, not the target."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
     from brosoundml_amd import config as C
-    T0 = 64
     om = O.OracleModel(cfg)
     om.set_params(params)
-    asr, F0, Nn, style, dA = make_inputs(cfg, 1, T0, "bench.cpu")
-    times = []
-    for rep in range(4):  # one warm-up, then the median of three
-        t0 = time.perf_counter()
-        om.zero_grad()
-        om.forward(asr[0], F0[0], Nn[0], style[0], T0)
-        om.backward(dA[0], wgrad=True, dalpha=True, dstyle=True)
-        if rep:
-            times.append(time.perf_counter() - t0)
-    dt = sorted(times)[1]
-    audio_s = C.lengths(cfg, T0)["audio_seconds"]
+    asr, F0, Nn, style, dA = make_inputs(cfg, 1, T, "bench.cpu")
+    t0 = time.perf_counter()
+    om.zero_grad()
+    om.forward(asr[0], F0[0], Nn[0], style[0], T)
+    om.backward(dA[0], wgrad=True, dalpha=True, dstyle=True)
+    dt = time.perf_counter() - t0
+    audio_s = C.lengths(cfg, T)["audio_seconds"]
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     return {"value": round(audio_s / dt, 5), "unit": "audio-s/s", "cores": threads, "kind": "port",
             "seconds": round(dt, 3),
-            "sample": f"1 utterance, T={T0} (1.6 audio-s), decoder fwd+bwd with wgrad/dalpha/dstyle, "
-                      f"CPU oracle (double-accumulating C++, OpenMP {threads} threads); median of 3 "
-                      f"after one warm-up"}
+            "sample": f"1 of the {B} utterances at T={T} ({audio_s} audio-s), decoder fwd+bwd with "
+                      f"wgrad/dalpha/dstyle, CPU oracle (double-accumulating C++, OpenMP {threads} threads), "
+                      f"one timed run"}
 
 
 def micro_benches(ctx, reps=10):

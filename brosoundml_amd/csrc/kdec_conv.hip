@@ -981,7 +981,7 @@ WgradLayout wgrad_layout(int k, int s, int d) {
 size_t wgrad_lds_bytes(int k, int s, int d) { return wgrad_layout(k, s, d).lds; }
 
 #ifndef WG_ROUNDS
-#define WG_ROUNDS 4
+#define WG_ROUNDS 2
 #endif
 void wgrad_allow_large_lds() {
     static bool done = false;
