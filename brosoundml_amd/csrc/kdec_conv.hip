@@ -202,7 +202,11 @@ void conv_gemm(GemmArgs g) {
 
     const int KR = CK * k;                            // weight rows per chunk
     const int span = (BN - 1) * s + (k - 1) * d + 1;  // staged input window
-    const int span_p = (span + 63) & ~63;             // LDS row stride
+    // Stride-1 correlations stage input rows 16 B per lane (256 positions per
+    // instruction) at a row stride that is a multiple of 256; others 4 B per
+    // lane at a multiple of 64.
+    const bool wide = s == 1;
+    const int span_p = wide ? ((span + 3 + 255) & ~255) : ((span + 63) & ~63);  // LDS row stride
     const int segs = span_p >> 6;
     const int stage = KR * BM + CK * span_p;
     const float* Xb = g.X + static_cast<long>(b) * g.x_bs;
@@ -212,14 +216,35 @@ void conv_gemm(GemmArgs g) {
     // one descriptor for this utterance's input; rows, positions out of range
     // get an out-of-bounds offset and stage as zeros
     const __amdgpu_buffer_rsrc_t xrs = uniform_rsrc(Xb, g.C_in * g.L_in * 4);
+    // Interior tiles (window inside the row, x0 >= 3) take the 16-B path: row c
+    // is staged from the 16-B aligned position x0 - dc, dc = (c*L_in + x0 +
+    // the base's float offset) mod 4, and its reads shift by dc. Lm = xm = 0
+    // elsewhere makes every shift 0.
+    const bool x4 = wide && x0 >= 3 && x0 + span <= g.L_in;  // uniform per tile
+    const int base_f = static_cast<int>((reinterpret_cast<unsigned long long>(Xb) >> 2) & 3);
+    const int Lm = x4 ? (g.L_in & 3) : 0;
+    const int xm = x4 ? ((base_f + x0) & 3) : 0;
 
     // Stage chunk `ch` at LDS float offset `sb`: the weight slab two rows
-    // (1 KB) per instruction, the input window 64 positions per instruction.
+    // (1 KB) per instruction, the input window 256 (16-B path) or 64 positions
+    // per instruction.
     auto issue = [&](int ch, int sb) {
         const float* Ag = A + static_cast<long>(ch) * KR * g.m_pad + m0;
         for (int pr = wave; pr < KR / 2; pr += 4)
             __builtin_amdgcn_global_load_lds(Ag + static_cast<long>(2 * pr) * g.m_pad + a_lane,
                                              smem + sb + pr * 256, 16, 0, 0);
+        if (x4) {
+            const int seg4 = span_p >> 8;
+            for (int it = wave; it < CK * seg4; it += 4) {
+                const int r = it / seg4, sg = it - r * seg4;
+                const int c = ch * CK + r;
+                const int pos = x0 - ((c * Lm + xm) & 3) + sg * 256 + lane * 4;
+                const unsigned off = c < g.C_in ? static_cast<unsigned>(c * g.L_in + pos) * 4u : 0x80000000u;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + KR * BM + r * span_p + sg * 256, 16,
+                                                         static_cast<int>(off), 0, 0, 0);
+            }
+            return;
+        }
         for (int it = wave; it < nitems; it += 4) {
             const int r = it / segs, sg = it - r * segs;
             const int c = ch * CK + r;
@@ -258,13 +283,14 @@ void conv_gemm(GemmArgs g) {
         if (ch + 1 < ch1) issue(ch + 1, stage - sb);
         const int wb = sb + hi * BM + am;
         const int xb = sb + KR * BM + hi * span_p + bq;
+        const int dl = (ch * CK + hi) * Lm + xm;  // row shift of the 16-B path: (dl + cc*Lm) mod 4
         // step u reads packed rows 2u + hi: tap t = u / HS, channel 2(u % HS) + hi
         auto ld = [&](int u, float& a0, float& a1, float& b0, float& b1) {
             u = min(u, S - 1);
             const int t = u / HS;
             const int cc = (u - t * HS) * 2;
             int wo = wb + u * 2 * BM;
-            int xo = xb + cc * span_p + t * d;
+            int xo = xb + cc * span_p + t * d + ((dl + cc * Lm) & 3);
             // opaque offsets keep each step's reads where they are placed
             asm volatile("" : "+v"(wo), "+v"(xo));
             a0 = smem[wo];
@@ -757,7 +783,7 @@ __global__ void pool_wgrad(const float* X, long x_bs, const float* dY, long dy_b
 // correlation of kk taps at stride ss and dilation dd.
 size_t conv_lds_bytes(int CK, int kk, int ss, int dd) {
     const long span = static_cast<long>(BN - 1) * ss + static_cast<long>(kk - 1) * dd + 1;
-    const long span_p = (span + 63) / 64 * 64;
+    const long span_p = ss == 1 ? (span + 3 + 255) / 256 * 256 : (span + 63) / 64 * 64;  // as conv_gemm
     return 2 * (static_cast<size_t>(CK) * kk * BM + static_cast<size_t>(CK) * span_p) * sizeof(float);
 }
 
