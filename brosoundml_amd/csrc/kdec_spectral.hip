@@ -329,6 +329,98 @@ __global__ void style_bwd_w_k(const float* style, long s_bs, const float* dout, 
     }
 }
 
+// ─── LoRA term of the style projection ───────────────────────────────────
+// Units are stacked row-wise: unit u owns rows [off[u], off[u+1]) of W, b, B
+// and rows [u*rank, (u+1)*rank) of A; H[n, u*rank + j] = A[u*rank + j] . s[n].
+
+// the unit owning row r (binary search over the units+1 offsets)
+__device__ inline int unit_of(const int* off, int units, int r) {
+    int lo = 0, hi = units;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (off[mid] <= r) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// out[n, r] = W[r] . s[n] + b[r] + scale * sum_j B[r, j] g[n, j] H[n, u(r)*rank + j];
+// one wave per (r, n)
+__global__ void lora_fwd_k(const float* W, const float* bias, const float* B, const float* g, long g_bs,
+                           float scale, const int* unit_off, int units, int rank, const float* style, long s_bs,
+                           const float* H, float* out, long o_bs, int N, int rows, int S) {
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    if (wave >= rows * N) return;
+    const int r = wave / N, n = wave - r * N;
+    const float* w = W + static_cast<long>(r) * S;
+    const float* s = style + n * s_bs;
+    double acc = 0.0, lo = 0.0;
+    for (int j = lane; j < S; j += 64) acc += static_cast<double>(w[j]) * s[j];
+    const int u = unit_of(unit_off, units, r);
+    const float* hr = H + (static_cast<long>(n) * units + u) * rank;
+    for (int j = lane; j < rank; j += 64)
+        lo += static_cast<double>(B[static_cast<long>(r) * rank + j]) * (g[n * g_bs + j] * hr[j]);
+    for (int o = 32; o > 0; o >>= 1) {
+        acc += __shfl_down(acc, o, 64);
+        lo += __shfl_down(lo, o, 64);
+    }
+    if (lane == 0) out[n * o_bs + r] = static_cast<float>(acc + (bias ? bias[r] : 0.0f) + scale * lo);
+}
+
+// For c = u*rank + j: dHG = scale * sum_{r in u} B[r, j] dout[n, r];
+// dH[n, c] = dHG * g[n, j] (the grad at A s), gp[n, c] = dHG * H[n, c] (the
+// unit's share of the gate grad). One wave per (n, c).
+__global__ void lora_dh_k(const float* B, const float* g, long g_bs, float scale, const int* unit_off, int units,
+                          int rank, const float* H, const float* dout, long d_bs, float* dH, float* gp, int N) {
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    const int UR = units * rank;
+    if (wave >= N * UR) return;
+    const int n = wave / UR, c = wave - n * UR;
+    const int u = c / rank, j = c - u * rank;
+    double acc = 0.0;
+    for (int r = unit_off[u] + lane; r < unit_off[u + 1]; r += 64)
+        acc += static_cast<double>(B[static_cast<long>(r) * rank + j]) * dout[n * d_bs + r];
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_down(acc, o, 64);
+    if (lane == 0) {
+        const double dhg = scale * acc;
+        const long i = static_cast<long>(n) * UR + c;
+        dH[i] = static_cast<float>(dhg * g[n * g_bs + j]);
+        gp[i] = static_cast<float>(dhg * H[i]);
+    }
+}
+
+// dG[n, j] += sum_u gp[n, u*rank + j] at the gate's stride; a shared gate
+// (g_bs = 0) also sums over the utterances, in order.
+__global__ void lora_dg_k(const float* gp, float* dG, long g_bs, int N, int units, int rank) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    const int NG = g_bs ? N : 1;
+    if (t >= NG * rank) return;
+    const int n0 = t / rank, j = t - n0 * rank;
+    const int na = g_bs ? n0 : 0, nb = g_bs ? n0 + 1 : N;
+    double acc = 0.0;
+    for (int n = na; n < nb; ++n)
+        for (int u = 0; u < units; ++u) acc += gp[(static_cast<long>(n) * units + u) * rank + j];
+    dG[n0 * g_bs + j] += static_cast<float>(acc);
+}
+
+// dB[r, j] += scale * sum_n dout[n, r] g[n, j] H[n, u(r)*rank + j]
+__global__ void lora_db_k(const float* g, long g_bs, float scale, const int* unit_off, int units, int rank,
+                          const float* H, const float* dout, long d_bs, float* dB, int N, int rows) {
+    const long tot = static_cast<long>(rows) * rank;
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < tot;
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        const int r = static_cast<int>(i / rank), j = static_cast<int>(i - static_cast<long>(r) * rank);
+        const int u = unit_of(unit_off, units, r);
+        double acc = 0.0;
+        for (int n = 0; n < N; ++n)
+            acc += static_cast<double>(dout[n * d_bs + r]) *
+                   (g[n * g_bs + j] * H[(static_cast<long>(n) * units + u) * rank + j]);
+        dB[i] += static_cast<float>(scale * acc);
+    }
+}
+
 unsigned g1(long n, long per = 256, long cap = 65535) {
     long g = (n + per - 1) / per;
     if (g > cap) g = cap;
@@ -440,6 +532,65 @@ int kdec_style_proj_bwd(kdec_ctx* ctx, const float* W, const float* style,
                            style, style_bs, dout, dout_bs, dW, db, N, rows, S);
         if (int rc = launch_check(ctx, "style_bwd_w")) return rc;
     }
+    return KDEC_OK;
+}
+
+int kdec_lora_proj_fwd(kdec_ctx* ctx, const float* W, const float* b, const float* A, const float* B,
+                       const float* g, long g_bs, float scale, const int* unit_off, int units, int rank,
+                       const float* style, long style_bs, float* H, float* out, long out_bs, int N, int rows,
+                       int S) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, W && A && B && g && unit_off && style && H && out && N > 0 && rows > 0 && S > 0 && units > 0 &&
+                        rank > 0 && g_bs >= 0,
+               "kdec_lora_proj_fwd: bad arguments");
+    ProfScope ps(ctx, "style_proj", 0);
+    const long UR = static_cast<long>(units) * rank;
+    hipLaunchKernelGGL(style_fwd_k, dim3(static_cast<unsigned>(cdiv(UR * N * 64, 256))), dim3(256), 0, ctx->stream,
+                       A, nullptr, style, style_bs, H, UR, N, static_cast<int>(UR), S);
+    if (int rc = launch_check(ctx, "lora_h")) return rc;
+    const long waves = static_cast<long>(rows) * N;
+    hipLaunchKernelGGL(lora_fwd_k, dim3(static_cast<unsigned>(cdiv(waves * 64, 256))), dim3(256), 0, ctx->stream, W,
+                       b, B, g, g_bs, scale, unit_off, units, rank, style, style_bs, H, out, out_bs, N, rows, S);
+    return launch_check(ctx, "lora_fwd");
+}
+
+int kdec_lora_proj_bwd(kdec_ctx* ctx, const float* W, const float* A, const float* B, const float* g, long g_bs,
+                       float scale, const int* unit_off, int units, int rank, const float* style, long style_bs,
+                       const float* H, const float* dout, long dout_bs, float* dstyle, long dstyle_bs, float beta,
+                       float* dW, float* db, float* dA, float* dB, float* dG, int N, int rows, int S) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, W && A && B && g && unit_off && style && H && dout && N > 0 && rows > 0 && S > 0 && units > 0 &&
+                        rank > 0 && g_bs >= 0,
+               "kdec_lora_proj_bwd: bad arguments");
+    // the base projection's share: dstyle = beta*dstyle + W^T dout, dW, db
+    if (dstyle || dW)
+        if (int rc = kdec_style_proj_bwd(ctx, W, style, style_bs, dout, dout_bs, dstyle, dstyle_bs, beta, dW, db, N,
+                                         rows, S))
+            return rc;
+    ProfScope ps(ctx, "style_proj", 0);
+    const long UR = static_cast<long>(units) * rank;
+    if (dB) {
+        hipLaunchKernelGGL(lora_db_k, dim3(g1(static_cast<long>(rows) * rank)), dim3(256), 0, ctx->stream, g, g_bs,
+                           scale, unit_off, units, rank, H, dout, dout_bs, dB, N, rows);
+        if (int rc = launch_check(ctx, "lora_db")) return rc;
+    }
+    if (!dA && !dG && !dstyle) return KDEC_OK;
+    Workspace dH(ctx, static_cast<size_t>(N) * UR * sizeof(float));
+    Workspace gp(ctx, static_cast<size_t>(N) * UR * sizeof(float));
+    if (!dH.p || !gp.p) return KDEC_ENOMEM;
+    hipLaunchKernelGGL(lora_dh_k, dim3(static_cast<unsigned>(cdiv(UR * N * 64, 256))), dim3(256), 0, ctx->stream, B,
+                       g, g_bs, scale, unit_off, units, rank, H, dout, dout_bs, dH.as<float>(), gp.as<float>(), N);
+    if (int rc = launch_check(ctx, "lora_dh")) return rc;
+    if (dG) {
+        const long NG = g_bs ? N : 1;
+        hipLaunchKernelGGL(lora_dg_k, dim3(static_cast<unsigned>(cdiv(NG * rank, 256))), dim3(256), 0, ctx->stream,
+                           gp.as<float>(), dG, g_bs, N, units, rank);
+        if (int rc = launch_check(ctx, "lora_dg")) return rc;
+    }
+    // dA += dH^T style and dstyle += A^T dH: the style projection's adjoint over A
+    if (dA || dstyle)
+        return kdec_style_proj_bwd(ctx, A, style, style_bs, dH.as<float>(), UR, dstyle, dstyle_bs, 1.0f, dA, nullptr,
+                                   N, static_cast<int>(UR), S);
     return KDEC_OK;
 }
 

@@ -253,6 +253,38 @@ int kdec_style_proj_bwd(kdec_ctx* ctx, const float* W, const float* style,
                         float* dstyle, long dstyle_bs, float beta, float* dW,
                         float* db, int N, int rows, int S);
 
+/* LoRA-adapted style projection (DecoderLora's adapter_fwd,
+ * decoder_lora.cpp:184-194, over bt::lora_forward; the adapter contract of
+ * decoder_lora.h:63-77): for `units` AdaIN units stacked row-wise, unit u
+ * owning rows [unit_off[u], unit_off[u+1]) (unit_off: units+1 ints, device),
+ *   H[n, u*rank + j] = A[u*rank + j, :] . style[n, :]
+ *   out[n, r] = W[r, :] . style[n, :] + b[r]
+ *               + scale * sum_j B[r, j] * g[n, j] * H[n, u(r)*rank + j]
+ * A (units*rank, S), B (rows, rank), g the gate (N, rank) at batch stride
+ * g_bs (0: one gate for every utterance). H (N, units*rank) is written for
+ * the backward. */
+int kdec_lora_proj_fwd(kdec_ctx* ctx, const float* W, const float* b,
+                       const float* A, const float* B, const float* g,
+                       long g_bs, float scale, const int* unit_off, int units,
+                       int rank, const float* style, long style_bs, float* H,
+                       float* out, long out_bs, int N, int rows, int S);
+/* Its adjoint (adapter_bwd, decoder_lora.cpp:198-207, over bt::lora_backward)
+ * plus the north-star d(style). With dHG[n, u*rank+j] = scale * sum_{r in u}
+ * B[r, j] dout[n, r]:
+ *   dB[r, j] += scale * sum_n dout[n, r] g[n, j] H[n, u(r)*rank + j]
+ *   dG[n, j] += sum_u dHG[n, u*rank+j] H[n, u*rank+j]   (summed over n when g_bs = 0)
+ *   dA[u*rank+j, :] += sum_n dHG[n, u*rank+j] g[n, j] style[n, :]
+ *   dstyle[n, :] = beta*dstyle + W^T dout[n] + A^T (dHG g)[n]
+ *   dW, db as kdec_style_proj_bwd.
+ * Any of dstyle, dW, db, dA, dB, dG may be NULL. */
+int kdec_lora_proj_bwd(kdec_ctx* ctx, const float* W, const float* A,
+                       const float* B, const float* g, long g_bs, float scale,
+                       const int* unit_off, int units, int rank,
+                       const float* style, long style_bs, const float* H,
+                       const float* dout, long dout_bs, float* dstyle,
+                       long dstyle_bs, float beta, float* dW, float* db,
+                       float* dA, float* dB, float* dG, int N, int rows, int S);
+
 #ifdef __cplusplus
 }
 #endif

@@ -470,4 +470,66 @@ int stft(const Real* x, int len, const Real* window, int n_fft, int hop,
     return frames;
 }
 
+// decoder_lora.h:63-77, decoder_lora.cpp:184-194
+void lora_forward(const Real* W, const Real* b, const Real* A, const Real* B,
+                  const Real* g, float scale, const Real* s, int rows, int rank,
+                  int S, Real* y, Real* h) {
+    for (int j = 0; j < rank; ++j) {
+        double acc = 0.0;
+        for (int k = 0; k < S; ++k) acc += static_cast<double>(A[static_cast<std::size_t>(j) * S + k]) * s[k];
+        h[j] = static_cast<Real>(acc);
+    }
+    for (int r = 0; r < rows; ++r) {
+        double acc = b ? static_cast<double>(b[r]) : 0.0;
+        for (int k = 0; k < S; ++k) acc += static_cast<double>(W[static_cast<std::size_t>(r) * S + k]) * s[k];
+        double lo = 0.0;
+        for (int j = 0; j < rank; ++j)
+            lo += static_cast<double>(B[static_cast<std::size_t>(r) * rank + j]) * (static_cast<double>(g[j]) * h[j]);
+        y[r] = static_cast<Real>(acc + static_cast<double>(scale) * lo);
+    }
+}
+
+// decoder_lora.cpp:198-207 (lora_backward), plus d(style)
+void lora_backward(const Real* W, const Real* A, const Real* B, const Real* g,
+                   float scale, const Real* s, const Real* h, const Real* dy,
+                   int rows, int rank, int S, Real* dstyle, Real* dW, Real* db,
+                   Real* dA, Real* dB, Real* dG) {
+    std::vector<double> dhg(static_cast<std::size_t>(rank), 0.0);
+    for (int r = 0; r < rows; ++r)
+        for (int j = 0; j < rank; ++j)
+            dhg[j] += static_cast<double>(scale) * B[static_cast<std::size_t>(r) * rank + j] * dy[r];
+    if (dB)
+        for (int r = 0; r < rows; ++r)
+            for (int j = 0; j < rank; ++j) {
+                const std::size_t i = static_cast<std::size_t>(r) * rank + j;
+                dB[i] = static_cast<Real>(dB[i] + static_cast<double>(scale) * dy[r] * (static_cast<double>(g[j]) * h[j]));
+            }
+    if (dG)
+        for (int j = 0; j < rank; ++j) dG[j] = static_cast<Real>(dG[j] + dhg[j] * h[j]);
+    std::vector<double> dh(static_cast<std::size_t>(rank));
+    for (int j = 0; j < rank; ++j) dh[j] = dhg[j] * g[j];
+    if (dA)
+        for (int j = 0; j < rank; ++j)
+            for (int k = 0; k < S; ++k) {
+                const std::size_t i = static_cast<std::size_t>(j) * S + k;
+                dA[i] = static_cast<Real>(dA[i] + dh[j] * s[k]);
+            }
+    if (dW || db)
+        for (int r = 0; r < rows; ++r) {
+            if (dW)
+                for (int k = 0; k < S; ++k) {
+                    const std::size_t i = static_cast<std::size_t>(r) * S + k;
+                    dW[i] = static_cast<Real>(dW[i] + static_cast<double>(dy[r]) * s[k]);
+                }
+            if (db) db[r] = static_cast<Real>(db[r] + dy[r]);
+        }
+    if (dstyle)
+        for (int k = 0; k < S; ++k) {
+            double acc = 0.0;
+            for (int r = 0; r < rows; ++r) acc += static_cast<double>(W[static_cast<std::size_t>(r) * S + k]) * dy[r];
+            for (int j = 0; j < rank; ++j) acc += static_cast<double>(A[static_cast<std::size_t>(j) * S + k]) * dh[j];
+            dstyle[k] = static_cast<Real>(dstyle[k] + acc);
+        }
+}
+
 }  // namespace KDO_NS

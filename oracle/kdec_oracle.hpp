@@ -115,6 +115,23 @@ void istft_backward(const Real* dout, const Real* window, int frames,
 int stft(const Real* x, int len, const Real* window, int n_fft, int hop,
          int win, Vec& spec);
 
+// One DecoderLora adapter on one AdaIN fc for one utterance (the adapter
+// contract of decoder_lora.h:63-77, adapter_fwd / adapter_bwd at
+// decoder_lora.cpp:184-207 over bt::lora_forward / lora_backward):
+//   h = A s (rank), hg = g * h, y = W s + b + scale * B hg (rows = 2C).
+// W (rows, S), A (rank, S), B (rows, rank); h is kept for the backward.
+void lora_forward(const Real* W, const Real* b, const Real* A, const Real* B,
+                  const Real* g, float scale, const Real* s, int rows, int rank,
+                  int S, Real* y, Real* h);
+// Adjoint: dB += scale dy hg^T, dhg = scale B^T dy, dG += dhg * h,
+// dA += (dhg * g) s^T, and dstyle += W^T dy + A^T (dhg * g) when requested
+// (the reference passes dX = nullptr); dW / db accumulate the frozen fc's
+// grads when non-null. Any output may be null.
+void lora_backward(const Real* W, const Real* A, const Real* B, const Real* g,
+                   float scale, const Real* s, const Real* h, const Real* dy,
+                   int rows, int rank, int S, Real* dstyle, Real* dW, Real* db,
+                   Real* dA, Real* dB, Real* dG);
+
 // ─── module weight structs (mirror modules.h / kokoro_modules.h) ───────────
 
 struct Conv1d {

@@ -102,6 +102,15 @@ int ko_snake_bwd(const float* x, const float* alpha, const float* dy, float* dx,
                  float* dalpha, int C, int L) {
     return guard([&] { snake_backward(x, alpha, dy, C, L, dx, dalpha); });
 }
+int ko_lora_fwd(const float* W, const float* b, const float* A, const float* B, const float* g, float scale,
+                const float* s, int rows, int rank, int S, float* y, float* h) {
+    return guard([&] { lora_forward(W, b, A, B, g, scale, s, rows, rank, S, y, h); });
+}
+int ko_lora_bwd(const float* W, const float* A, const float* B, const float* g, float scale, const float* s,
+                const float* h, const float* dy, int rows, int rank, int S, float* dstyle, float* dW, float* db,
+                float* dA, float* dB, float* dG) {
+    return guard([&] { lora_backward(W, A, B, g, scale, s, h, dy, rows, rank, S, dstyle, dW, db, dA, dB, dG); });
+}
 int ko_leaky_fwd(const float* x, float slope, long n, float* y) {
     return guard([&] { leaky_forward(x, slope, static_cast<std::size_t>(n), y); });
 }

@@ -259,6 +259,30 @@ def spectral_head_bwd(x, C, L, W, b, k, n_fft, hop, daudio, want_wgrad=True):
     return dx, dW, db
 
 
+def lora_fwd(W, b, A, B, g, scale, s):
+    """One adapter, one utterance: y = W s + b + scale * B (g * (A s)); returns (y, h)."""
+    rows, S = W.shape
+    rank = A.shape[0]
+    y = np.zeros(rows, np.float32)
+    h = np.zeros(rank, np.float32)
+    check(lib().ko_lora_fwd(P(f32(W)), P(None if b is None else f32(b)), P(f32(A)), P(f32(B)), P(f32(g)),
+                            ctypes.c_float(scale), P(f32(s)), rows, rank, S, P(y), P(h)))
+    return y, h
+
+
+def lora_bwd(W, A, B, g, scale, s, h, dy):
+    """Adjoint of lora_fwd: returns dict of dstyle, dW, db, dA, dB, dG."""
+    rows, S = W.shape
+    rank = A.shape[0]
+    out = {"dstyle": np.zeros(S, np.float32), "dW": np.zeros((rows, S), np.float32),
+           "db": np.zeros(rows, np.float32), "dA": np.zeros((rank, S), np.float32),
+           "dB": np.zeros((rows, rank), np.float32), "dG": np.zeros(rank, np.float32)}
+    check(lib().ko_lora_bwd(P(f32(W)), P(f32(A)), P(f32(B)), P(f32(g)), ctypes.c_float(scale), P(f32(s)),
+                            P(f32(h)), P(f32(dy)), rows, rank, S, P(out["dstyle"]), P(out["dW"]), P(out["db"]),
+                            P(out["dA"]), P(out["dB"]), P(out["dG"])))
+    return out
+
+
 def harmonic_source(F0, lW, lb, harmonic_num, sample_rate, upsample_scale, n_fft, hop):
     F0 = f32(F0)
     F = n_fft // 2 + 1

@@ -389,3 +389,54 @@ def test_error_paths(K):
                3, 2, 1, 1, 1.0, 0.0)
     with pytest.raises(native.KdecError):
         K.call("kdec_conv1d_fwd", None, 0, None, None, None, 0, 1, 1, 1, 1, 1, 1, 0, 1, None, 0, 1.0, 0.0)
+
+
+@pytest.mark.parametrize("shared_gate", [False, True])
+def test_lora_projection(K, shared_gate):
+    # three AdaIN units (2C = 6, 10, 4 rows) stacked, N = 3 utterances, rank 5
+    N, S, rank, scale = 3, 16, 5, 0.9
+    sizes = [6, 10, 4]
+    off = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    R, U = int(off[-1]), len(sizes)
+    W, b = rnd(R, S, scale=0.3), rnd(R, scale=0.2)
+    A, B = rnd(U * rank, S, scale=0.3), rnd(R, rank, scale=0.3)
+    style = rnd(N, S)
+    gate = rnd(1 if shared_gate else N, rank)
+    g_bs = 0 if shared_gate else rank
+    offd = torch.from_numpy(off).cuda()
+    H = torch.empty(N, U * rank, device="cuda")
+    out = torch.empty(N, R, device="cuda")
+    K.call("kdec_lora_proj_fwd", P(g(W)), P(g(b)), P(g(A)), P(g(B)), P(g(gate)), g_bs, scale, P(offd), U, rank,
+           P(g(style)), S, P(H), P(out), R, N, R, S)
+    ref_y = np.zeros((N, R))
+    ref_h = np.zeros((N, U * rank))
+    for n in range(N):
+        gn = gate[0 if shared_gate else n]
+        for u in range(U):
+            r0, r1 = off[u], off[u + 1]
+            y, hh = O.lora_fwd(W[r0:r1], b[r0:r1], A[u * rank:(u + 1) * rank], B[r0:r1], gn, scale, style[n])
+            ref_y[n, r0:r1] = y
+            ref_h[n, u * rank:(u + 1) * rank] = hh
+    assert_close(h(out), ref_y, FWD_TOL, "lora projection forward")
+    dout = rnd(N, R)
+    dstyle = torch.empty(N, S, device="cuda")
+    dW = torch.zeros(R, S, device="cuda")
+    db = torch.zeros(R, device="cuda")
+    dA = torch.zeros(U * rank, S, device="cuda")
+    dB = torch.zeros(R, rank, device="cuda")
+    dG = torch.zeros(gate.shape[0], rank, device="cuda")
+    K.call("kdec_lora_proj_bwd", P(g(W)), P(g(A)), P(g(B)), P(g(gate)), g_bs, scale, P(offd), U, rank,
+           P(g(style)), S, P(H), P(g(dout)), R, P(dstyle), S, 0.0, P(dW), P(db), P(dA), P(dB), P(dG), N, R, S)
+    rs = np.zeros((N, S)); rW = np.zeros((R, S)); rb = np.zeros(R)
+    rA = np.zeros((U * rank, S)); rB = np.zeros((R, rank)); rG = np.zeros(gate.shape)
+    for n in range(N):
+        gi = 0 if shared_gate else n
+        for u in range(U):
+            r0, r1 = off[u], off[u + 1]
+            gr = O.lora_bwd(W[r0:r1], A[u * rank:(u + 1) * rank], B[r0:r1], gate[gi], scale, style[n],
+                            ref_h[n, u * rank:(u + 1) * rank].astype(np.float32), dout[n, r0:r1])
+            rs[n] += gr["dstyle"]; rW[r0:r1] += gr["dW"]; rb[r0:r1] += gr["db"]
+            rA[u * rank:(u + 1) * rank] += gr["dA"]; rB[r0:r1] += gr["dB"]; rG[gi] += gr["dG"]
+    for name, got, ref in (("dstyle", dstyle, rs), ("dW", dW, rW), ("db", db, rb), ("dA", dA, rA), ("dB", dB, rB),
+                           ("dG", dG, rG)):
+        assert_close(h(got), ref, GRAD_TOL, f"lora projection {name}")

@@ -267,3 +267,50 @@ def test_istft_brute_force_dft():
     sig = (frames - 1) * hop
     ref = (ola / np.where(env > 1e-11, env, 1))[n_fft // 2:n_fft // 2 + sig]
     close(O.istft(spec, O.hann(n_fft), frames, sig, n_fft, hop), ref, rtol=1e-5)
+
+
+def _lora_case(rows=10, rank=4, S=16):
+    W, b = rnd(rows, S, scale=0.3), rnd(rows, scale=0.2)
+    A, B = rnd(rank, S, scale=0.3), rnd(rows, rank, scale=0.3)
+    g, s = rnd(rank), rnd(S)
+    return W, b, A, B, g, s
+
+
+def test_lora_closed_forms():
+    # the adapter contract (decoder_lora.h:63-77): a zero gate or a zero B
+    # leaves the frozen projection exactly; otherwise y = W s + b + scale B (g * A s)
+    W, b, A, B, g, s = _lora_case()
+    base = (W.astype(np.float64) @ s + b)
+    y0, _ = O.lora_fwd(W, b, A, B, np.zeros_like(g), 0.7, s)
+    close(y0, base, rtol=1e-6, atol=1e-6)
+    y1, _ = O.lora_fwd(W, b, A, np.zeros_like(B), g, 0.7, s)
+    close(y1, base, rtol=1e-6, atol=1e-6)
+    # the LoRA term is linear in scale
+    ya, _ = O.lora_fwd(W, b, A, B, g, 0.5, s)
+    yb, _ = O.lora_fwd(W, b, A, B, g, 1.5, s)
+    close(yb - base, 3.0 * (ya - base), rtol=1e-5, atol=1e-5)
+
+
+def test_lora_adjoint_identities():
+    # y is linear in each of B, A, g and s with the others fixed, so for any
+    # direction D: <dy, y(X + D) - y(X)> = <dX, D> (up to float rounding).
+    W, b, A, B, g, s = _lora_case()
+    scale = 0.8
+    y, h = O.lora_fwd(W, b, A, B, g, scale, s)
+    dy = rnd(W.shape[0])
+    gr = O.lora_bwd(W, A, B, g, scale, s, h, dy)
+
+    def inner(y2):
+        return float(np.dot(dy.astype(np.float64), y2.astype(np.float64) - y.astype(np.float64)))
+
+    for name, args_fn, D in (
+        ("B", lambda D: (W, b, A, B + D, g, scale, s), rnd(*B.shape)),
+        ("A", lambda D: (W, b, A + D, B, g, scale, s), rnd(*A.shape)),
+        ("G", lambda D: (W, b, A, B, g + D, scale, s), rnd(*g.shape)),
+        ("style", lambda D: (W, b, A, B, g, scale, s + D), rnd(*s.shape)),
+        ("W", lambda D: (W + D, b, A, B, g, scale, s), rnd(*W.shape)),
+        ("b", lambda D: (W, b + D, A, B, g, scale, s), rnd(*b.shape)),
+    ):
+        lhs = inner(O.lora_fwd(*args_fn(D))[0])
+        rhs = float(np.sum(gr["d" + name].astype(np.float64) * D))
+        assert abs(lhs - rhs) <= 1e-4 * max(1.0, abs(rhs)), (name, lhs, rhs)
