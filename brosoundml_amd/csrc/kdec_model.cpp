@@ -67,6 +67,17 @@ struct kdec_model {
     // overlaps the style projection and the backbone.
     kdec_ctx* side = nullptr;
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+
+    // DecoderLora adapters (off at lora_rank 0): A (units*rank, S), B
+    // (rows_total, rank), their grads, the unit row offsets (units+1 int32
+    // in a 4-byte-element buffer), the gate set for the forwards and the
+    // bottleneck H (N, units*rank) of the last forward.
+    int lora_rank = 0;
+    float lora_scale = 0.0f;
+    Tensor loraA, loraB, dloraA, dloraB, unit_off, lora_H;
+    const float* gate = nullptr;
+    long gate_bs = 0;
+    float* dgate = nullptr;
 };
 
 namespace {
@@ -407,7 +418,59 @@ long kdec_model_param_total(const kdec_model* m) { return m ? m->total : 0; }
 
 int kdec_model_zero_grad(kdec_model* m) {
     if (!m) return KDEC_EINVAL;
+    if (m->lora_rank > 0) {
+        if (int rc = check(m, kdec_fill(m->ctx, static_cast<float*>(m->dloraA.data),
+                                        static_cast<long>(m->dloraA.rows) * m->dloraA.cols, 0.0f)))
+            return rc;
+        if (int rc = check(m, kdec_fill(m->ctx, static_cast<float*>(m->dloraB.data),
+                                        static_cast<long>(m->dloraB.rows) * m->dloraB.cols, 0.0f)))
+            return rc;
+    }
     return check(m, kdec_fill(m->ctx, static_cast<float*>(m->gbuf.data), m->total, 0.0f));
+}
+
+int kdec_model_lora_enable(kdec_model* m, int rank, float scale) {
+    if (!m || rank <= 0) return KDEC_EINVAL;
+    try {
+        bt::set_runtime(m->ctx);
+        const int U = static_cast<int>(m->units.size());
+        m->lora_rank = rank;
+        m->lora_scale = scale;
+        m->loraA = Tensor::zeros_on(Device::HIP, U * rank, m->style_dim);
+        m->dloraA = Tensor::zeros_on(Device::HIP, U * rank, m->style_dim);
+        m->loraB = Tensor::zeros_on(Device::HIP, m->rows_total, rank);
+        m->dloraB = Tensor::zeros_on(Device::HIP, m->rows_total, rank);
+        std::vector<int> off(static_cast<std::size_t>(U) + 1);
+        for (int i = 0; i < U; ++i) off[i] = m->units[i].offset;
+        off[U] = m->rows_total;
+        m->unit_off = Tensor::empty_on(Device::HIP, 1, U + 1);
+        if (hipMemcpyAsync(m->unit_off.data, off.data(), off.size() * sizeof(int), hipMemcpyHostToDevice,
+                           m->ctx->stream) != hipSuccess ||
+            hipStreamSynchronize(m->ctx->stream) != hipSuccess)
+            return fail(m, KDEC_EHIP, "kdec_model_lora_enable: upload of the unit offsets");
+    } catch (const std::exception& e) {
+        return fail(m, KDEC_ENOMEM, e.what());
+    }
+    return KDEC_OK;
+}
+
+float* kdec_model_lora_ptr(kdec_model* m, int which) {
+    if (!m || m->lora_rank <= 0) return nullptr;
+    switch (which) {
+        case 0: return static_cast<float*>(m->loraA.data);
+        case 1: return static_cast<float*>(m->loraB.data);
+        case 2: return static_cast<float*>(m->dloraA.data);
+        case 3: return static_cast<float*>(m->dloraB.data);
+        default: return nullptr;
+    }
+}
+
+int kdec_model_lora_gate(kdec_model* m, const float* g, long g_bs, float* dG) {
+    if (!m || m->lora_rank <= 0 || !g || g_bs < 0) return KDEC_EINVAL;
+    m->gate = g;
+    m->gate_bs = g_bs;
+    m->dgate = dG;
+    return KDEC_OK;
 }
 
 int kdec_model_unit_count(const kdec_model* m) { return m ? static_cast<int>(m->units.size()) : 0; }
@@ -470,8 +533,21 @@ int kdec_model_forward(kdec_model* m, int N, int T, const float* asr, const floa
         const long fcb_off = m->params.at(m->units[0].name + ".fc.bias").offset;
         const float* W = static_cast<const float*>(m->pbuf.data) + fc_off;
         const float* b = static_cast<const float*>(m->pbuf.data) + fcb_off;
-        if (int rc = check(m, kdec_style_proj_fwd(m->ctx, W, b, style, S, static_cast<float*>(m->gb.data), R, N, R, S)))
+        if (m->lora_rank > 0) {
+            if (!m->gate) return fail(m, KDEC_EINVAL, "kdec_model_forward: LoRA enabled but no gate set");
+            const int UR = static_cast<int>(m->units.size()) * m->lora_rank;
+            m->lora_H = Tensor::empty_on(Device::HIP, N, UR);
+            if (int rc = check(m, kdec_lora_proj_fwd(m->ctx, W, b, static_cast<const float*>(m->loraA.data),
+                                                     static_cast<const float*>(m->loraB.data), m->gate, m->gate_bs,
+                                                     m->lora_scale, static_cast<const int*>(m->unit_off.data),
+                                                     static_cast<int>(m->units.size()), m->lora_rank, style, S,
+                                                     static_cast<float*>(m->lora_H.data),
+                                                     static_cast<float*>(m->gb.data), R, N, R, S)))
+                return rc;
+        } else if (int rc = check(m, kdec_style_proj_fwd(m->ctx, W, b, style, S, static_cast<float*>(m->gb.data), R,
+                                                          N, R, S))) {
             return rc;
+        }
         auto gv = [&](const Tensor& buf, int off, int C) {
             Tensor t = Tensor::view(Device::HIP, static_cast<float*>(buf.data) + off, N, C, bt::Dtype::FP32, R);
             t.storage = buf.storage;
@@ -594,11 +670,24 @@ int kdec_model_backward(kdec_model* m, const float* daudio, int wgrad, int dalph
         const float* W = static_cast<const float*>(m->pbuf.data) + fc_off;
         float* dW = wgrad ? static_cast<float*>(m->gbuf.data) + fc_off : nullptr;
         float* db = wgrad ? static_cast<float*>(m->gbuf.data) + fcb_off : nullptr;
-        if (dstyle || dW)
+        if (m->lora_rank > 0) {
+            // adapter_bwd on every unit: dA, dB, the gate grad, d(style), fc grads
+            if (int rc = check(m, kdec_lora_proj_bwd(
+                                      m->ctx, W, static_cast<const float*>(m->loraA.data),
+                                      static_cast<const float*>(m->loraB.data), m->gate, m->gate_bs, m->lora_scale,
+                                      static_cast<const int*>(m->unit_off.data), static_cast<int>(m->units.size()),
+                                      m->lora_rank, static_cast<const float*>(m->style_v.data), S,
+                                      static_cast<const float*>(m->lora_H.data),
+                                      static_cast<const float*>(m->dgb.data), R, dstyle, S, 0.0f, dW, db,
+                                      static_cast<float*>(m->dloraA.data), static_cast<float*>(m->dloraB.data),
+                                      m->dgate, N, R, S)))
+                return rc;
+        } else if (dstyle || dW) {
             if (int rc = check(m, kdec_style_proj_bwd(m->ctx, W, static_cast<const float*>(m->style_v.data), S,
                                                       static_cast<const float*>(m->dgb.data), R, dstyle, S, 0.0f, dW,
                                                       db, N, R, S)))
                 return rc;
+        }
     } catch (const std::exception& e) {
         return fail(m, KDEC_EINVAL, e.what());
     }

@@ -231,6 +231,50 @@ class Model:
     def backward(self, daudio, wgrad=True, dalpha=True, dstyle=None):
         self._c(self.ctx.L.kdec_model_backward(self.h, ptr(daudio), int(wgrad), int(dalpha), ptr(dstyle)))
 
+    # ─── DecoderLora adapters (kdec_model_lora_*) ───
+    def lora_enable(self, rank: int, scale: float):
+        self.lora_rank = rank
+        self._c(self.ctx.L.kdec_model_lora_enable(self.h, rank, scale))
+
+    def _lora_shape(self, which: int):
+        if which % 2 == 0:
+            return len(self.units()) * self.lora_rank, self.cfg["style_dim"]
+        return self.affine_rows(), self.lora_rank
+
+    def lora_set(self, A=None, B=None):
+        """Copies A (units*rank, style_dim) and / or B (affine_rows, rank) into the model (device copy)."""
+        import torch
+        for which, v in ((0, A), (1, B)):
+            if v is None:
+                continue
+            t = torch.as_tensor(v, dtype=torch.float32).reshape(self._lora_shape(which)).contiguous().cuda()
+            dst = self.ctx.L.kdec_model_lora_ptr(self.h, which)
+            if not dst:
+                raise KdecError("kdec_model_lora_ptr: adapters not enabled")
+            self.ctx.check(self.ctx.L.kdec_axpby(self.ctx.h, 1.0, ptr(t), 0, 0.0, None, 0, ctypes.c_void_p(dst), 0,
+                                                 1, t.numel()))
+            self.ctx.synchronize()
+
+    def lora_grads(self):
+        """(dA, dB) as host arrays."""
+        import torch
+        out = []
+        for which in (2, 3):
+            shape = self._lora_shape(which)
+            t = torch.empty(shape, dtype=torch.float32, device="cuda")
+            src = self.ctx.L.kdec_model_lora_ptr(self.h, which)
+            self.ctx.check(self.ctx.L.kdec_axpby(self.ctx.h, 1.0, ctypes.c_void_p(src), 0, 0.0, None, 0, ptr(t), 0,
+                                                 1, t.numel()))
+            self.ctx.synchronize()
+            out.append(t.cpu().numpy())
+        return tuple(out)
+
+    def lora_gate(self, g, dG=None):
+        """g: torch cuda (N, rank) or (rank,) for one gate shared by every utterance."""
+        g_bs = self.lora_rank if g.dim() == 2 else 0
+        self._lora_keep = (g, dG)
+        self._c(self.ctx.L.kdec_model_lora_gate(self.h, ptr(g), g_bs, ptr(dG)))
+
     def affines(self, N):
         import numpy as np
         R = self.affine_rows()

@@ -5,8 +5,9 @@
  * kokoro_decoder_backward.h.
  *
  * It stands in for the sequence DecoderLora::forward / ::backward runs
- * (src/decoder_lora.cpp:211-296) with the LoRA term absent: the per-AdaIN
- * style projection (gamma, beta) = fc(style) (kokoro_modules.cpp:563-572),
+ * (src/decoder_lora.cpp:211-296): the per-AdaIN style projection
+ * (gamma, beta) = fc(style) (kokoro_modules.cpp:563-572), plus the LoRA term
+ * when adapters are enabled (kdec_model_lora_enable),
  * decoder_backbone_forward_train / generator_forward_train, then
  * generator_backward / decoder_backbone_backward and the projection's
  * adjoint. The harmonic source runs first, as in decode_back_half
@@ -82,6 +83,23 @@ int kdec_model_forward(kdec_model* m, int N, int T, const float* asr, const floa
  * grads; dstyle (N, style_dim) may be NULL. The affine grads are always
  * produced (the reference semantics). */
 int kdec_model_backward(kdec_model* m, const float* daudio, int wgrad, int dalpha, float* dstyle);
+/* DecoderLora's adapters on every AdaIN unit (the adapter contract of
+ * decoder_lora.h:63-77; the adapter_fwd / adapter_bwd sequence of
+ * decoder_lora.cpp:184-207): (gamma, beta) = fc(style) + scale * B_i (g *
+ * (A_i style)) for unit i. rank > 0 allocates A (units*rank, style_dim; unit
+ * i's rows i*rank..) and B (affine_rows, rank; unit i's rows at its affine
+ * offset), both zero, and their grads; forwards then need a gate
+ * (kdec_model_lora_gate) and every backward accumulates dA and dB. */
+int kdec_model_lora_enable(kdec_model* m, int rank, float scale);
+/* Device pointers: which 0 = A, 1 = B, 2 = dA, 3 = dB (kdec_model_zero_grad
+ * clears dA and dB); NULL before kdec_model_lora_enable. */
+float* kdec_model_lora_ptr(kdec_model* m, int which);
+/* The gate for the following forwards: g (device, N x rank at batch stride
+ * g_bs; g_bs = 0: one gate for every utterance). Backwards accumulate the
+ * gate grad into dG (device, same layout) when it is not NULL. The caller
+ * keeps both alive. */
+int kdec_model_lora_gate(kdec_model* m, const float* g, long g_bs, float* dG);
+
 /* Device pointers to the last forward's har (N, (n_fft+2)*frames) and
  * generator input (N, init_C * L_gen). */
 const float* kdec_model_har(const kdec_model* m);

@@ -262,7 +262,14 @@ void Model::build() {
     draff.assign(raff.size(), ResBlock1Affines{});
     auto add_unit = [&](const std::string& nm, AdaIN1dWeights* w, Vec* g, Vec* b,
                         Vec* dg, Vec* db) {
-        units.push_back(AffineUnit{nm, w, g, b, dg, db});
+        AffineUnit u;
+        u.name = nm;
+        u.w = w;
+        u.gamma = g;
+        u.beta = b;
+        u.dgamma = dg;
+        u.dbeta = db;
+        units.push_back(std::move(u));
     };
     add_unit(P + "encode.norm1", &bb.encode.norm1, &bbaff[0].g1, &bbaff[0].b1, &dbbaff[0].g1, &dbbaff[0].b1);
     add_unit(P + "encode.norm2", &bb.encode.norm2, &bbaff[0].g2, &bbaff[0].b2, &dbbaff[0].g2, &dbbaff[0].b2);
@@ -286,13 +293,48 @@ void Model::build() {
 
 void Model::zero_grad() {
     for (auto& kv : params) std::fill(kv.second.grad->begin(), kv.second.grad->end(), 0.0f);
+    for (auto& u : units) {
+        std::fill(u.dA.begin(), u.dA.end(), 0.0f);
+        std::fill(u.dB.begin(), u.dB.end(), 0.0f);
+    }
+    std::fill(dgate.begin(), dgate.end(), 0.0f);
+}
+
+// Adapters start at A = 0, B = 0 (the base decoder) with a zero gate.
+void Model::lora_enable(int rank, float scale) {
+    if (rank <= 0) throw std::runtime_error("kdo::Model::lora_enable: rank must be positive");
+    lora_rank = rank;
+    lora_scale = scale;
+    const std::size_t S = static_cast<std::size_t>(cfg.style_dim);
+    for (auto& u : units) {
+        const std::size_t rows = 2 * static_cast<std::size_t>(u.w->channels);
+        u.A.assign(rank * S, 0.0f);
+        u.B.assign(rows * rank, 0.0f);
+        u.dA.assign(u.A.size(), 0.0f);
+        u.dB.assign(u.B.size(), 0.0f);
+        u.h.assign(static_cast<std::size_t>(rank), 0.0f);
+    }
+    gate.assign(static_cast<std::size_t>(rank), 0.0f);
+    dgate.assign(static_cast<std::size_t>(rank), 0.0f);
 }
 
 void Model::forward(const Vec& asr, const Vec& F0, const Vec& N,
                     const Vec& style_in, int T_in, const Vec* har_in) {
     T = T_in;
     style = style_in;
-    for (auto& u : units) style_affine(*u.w, style, *u.gamma, *u.beta);
+    for (auto& u : units) {
+        if (lora_rank > 0) {
+            // adapter_fwd (decoder_lora.cpp:184-194): (gamma, beta) = chunk(lora_forward(...))
+            const int C = u.w->channels;
+            Vec y(static_cast<std::size_t>(2 * C));
+            lora_forward(u.w->fcW.data(), u.w->fcb.data(), u.A.data(), u.B.data(), gate.data(), lora_scale,
+                         style.data(), 2 * C, lora_rank, cfg.style_dim, y.data(), u.h.data());
+            u.gamma->assign(y.begin(), y.begin() + C);
+            u.beta->assign(y.begin() + C, y.end());
+        } else {
+            style_affine(*u.w, style, *u.gamma, *u.beta);
+        }
+    }
     // Harmonic source from F0 (decode_back_half, kokoro.cpp:369-383).
     int sig = 0;
     harmonic_source_forward(hs, F0, 2 * T, sig, frames, har);
@@ -316,9 +358,25 @@ void Model::backward(const Vec& dAudio, const Ext& ext, bool want_dstyle) {
     decoder_backbone_backward(bb, bbc, bbaff, dGenIn, 1e-5f, db, &ext);
     for (std::size_t i = 0; i < db.size(); ++i) dbbaff[i] = db[i];
     std::vector<double> ds(static_cast<std::size_t>(cfg.style_dim), 0.0);
-    for (auto& u : units)
-        style_affine_backward(*u.w, style, *u.dgamma, *u.dbeta,
-                              want_dstyle ? ds.data() : nullptr, ext.wgrad);
+    if (lora_rank > 0) {
+        // adapter_bwd (decoder_lora.cpp:198-207) per unit, the gate grad
+        // accumulated over all units, plus d(style) and the frozen fc grads
+        Vec dsv(static_cast<std::size_t>(cfg.style_dim), 0.0f);
+        for (auto& u : units) {
+            const int C = u.w->channels;
+            Vec dy(u.dgamma->begin(), u.dgamma->end());
+            dy.insert(dy.end(), u.dbeta->begin(), u.dbeta->end());
+            lora_backward(u.w->fcW.data(), u.A.data(), u.B.data(), gate.data(), lora_scale, style.data(),
+                          u.h.data(), dy.data(), 2 * C, lora_rank, cfg.style_dim,
+                          want_dstyle ? dsv.data() : nullptr, ext.wgrad ? u.w->dfcW.data() : nullptr,
+                          ext.wgrad ? u.w->dfcb.data() : nullptr, u.dA.data(), u.dB.data(), dgate.data());
+        }
+        for (std::size_t j = 0; j < ds.size(); ++j) ds[j] = dsv[j];
+    } else {
+        for (auto& u : units)
+            style_affine_backward(*u.w, style, *u.dgamma, *u.dbeta,
+                                  want_dstyle ? ds.data() : nullptr, ext.wgrad);
+    }
     dstyle.assign(ds.size(), 0.0f);
     for (std::size_t j = 0; j < ds.size(); ++j) dstyle[j] = static_cast<Real>(ds[j]);
 }

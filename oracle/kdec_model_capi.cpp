@@ -121,6 +121,37 @@ int KO_FN(model_get_affine)(void* m, int i, float* gamma, float* beta, float* dg
         if (dbeta) out(dbeta, *u.dbeta);
     });
 }
+// ─── LoRA adapters (decoder_lora.h:63-77) ───
+int KO_FN(model_lora_enable)(void* m, int rank, float scale) {
+    return guard([&] { static_cast<Model*>(m)->lora_enable(rank, scale); });
+}
+// unit i's A (rank*style_dim) and B (2C*rank) as doubles (stored at the
+// oracle's precision, so the FP64 shadow takes finite-difference steps);
+// either may be NULL
+int KO_FN(model_lora_set)(void* mp, int i, const double* A, const double* B) {
+    return guard([&] {
+        AffineUnit& u = static_cast<Model*>(mp)->units.at(i);
+        if (A) u.A.assign(A, A + u.A.size());
+        if (B) u.B.assign(B, B + u.B.size());
+    });
+}
+int KO_FN(model_lora_get_grad)(void* mp, int i, float* dA, float* dB) {
+    return guard([&] {
+        const AffineUnit& u = static_cast<Model*>(mp)->units.at(i);
+        if (dA) out(dA, u.dA);
+        if (dB) out(dB, u.dB);
+    });
+}
+int KO_FN(model_lora_gate)(void* mp, const double* g) {
+    return guard([&] {
+        Model& m = *static_cast<Model*>(mp);
+        m.gate.assign(g, g + m.gate.size());
+    });
+}
+int KO_FN(model_lora_get_dgate)(void* mp, float* dG) {
+    return guard([&] { out(dG, static_cast<Model*>(mp)->dgate); });
+}
+
 int KO_FN(model_zero_grad)(void* m) { return guard([&] { static_cast<Model*>(m)->zero_grad(); }); }
 // asr (asr_dim*T), F0/N (2T), style (style_dim); har_in optional (frames*(n_fft+2)).
 int KO_FN(model_forward)(void* mp, const float* asr, const float* F0, const float* N,

@@ -342,6 +342,10 @@ struct AffineUnit {
     Vec* beta = nullptr;
     Vec* dgamma = nullptr;   // backward (C)
     Vec* dbeta = nullptr;
+    // DecoderLora adapter on this unit's fc (decoder_lora.h:63-77), when the
+    // model's lora_rank > 0: A (rank, style_dim), B (2C, rank), grads, and
+    // the bottleneck h = A s of the last forward.
+    Vec A, B, dA, dB, h;
 };
 
 struct Model {
@@ -362,6 +366,11 @@ struct Model {
     GeneratorCache genc;
     Vec gen_in, har, audio, dstyle;
     int frames = 0;
+    // LoRA adapters on every unit with a shared gate g (rank); off at rank 0.
+    int lora_rank = 0;
+    float lora_scale = 0.0f;
+    Vec gate, dgate;
+    void lora_enable(int rank, float scale);
 
     explicit Model(const Config& c);
     Model(const Model&) = delete;

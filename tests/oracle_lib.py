@@ -62,6 +62,11 @@ def lib():
             f("model_forward_style_f64").argtypes = [ctypes.c_void_p, _fp, _fp, _fp, _dp, ctypes.c_int,
                                                      _fp]
             f("model_get_audio_f64").argtypes = [ctypes.c_void_p, _dp]
+            f("model_lora_enable").argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_float]
+            f("model_lora_set").argtypes = [ctypes.c_void_p, ctypes.c_int, _dp, _dp]
+            f("model_lora_get_grad").argtypes = [ctypes.c_void_p, ctypes.c_int, _fp, _fp]
+            f("model_lora_gate").argtypes = [ctypes.c_void_p, _dp]
+            f("model_lora_get_dgate").argtypes = [ctypes.c_void_p, _fp]
         L.ko_leaky_fwd.argtypes = [_fp, ctypes.c_float, ctypes.c_long, _fp]
         L.ko_leaky_bwd.argtypes = [_fp, _fp, ctypes.c_float, ctypes.c_long, _fp]
         for fn in ("ko_instnorm_fwd", "ko_adain_affine_fwd"):
@@ -390,6 +395,34 @@ class OracleModel:
         self._check(self._f("model_backward")(self.h, P(f32(daudio)), int(wgrad), int(dalpha),
                                               P(ds)))
         return ds
+
+    # ─── LoRA adapters on every AdaIN unit (decoder_lora.h:63-77) ───
+    def lora_enable(self, rank, scale):
+        self.lora_rank = rank
+        self._check(self._f("model_lora_enable")(self.h, rank, ctypes.c_float(scale)))
+
+    def lora_set(self, i, A=None, B=None):
+        dp = ctypes.POINTER(ctypes.c_double)
+        a = None if A is None else np.ascontiguousarray(A, np.float64)
+        b = None if B is None else np.ascontiguousarray(B, np.float64)
+        self._check(self._f("model_lora_set")(self.h, i, None if a is None else a.ctypes.data_as(dp),
+                                              None if b is None else b.ctypes.data_as(dp)))
+
+    def lora_gate(self, g):
+        gg = np.ascontiguousarray(g, np.float64)
+        self._check(self._f("model_lora_gate")(self.h, gg.ctypes.data_as(ctypes.POINTER(ctypes.c_double))))
+
+    def lora_grads(self, i, C):
+        S, r = self.cfg["style_dim"], self.lora_rank
+        dA = np.zeros((r, S), np.float32)
+        dB = np.zeros((2 * C, r), np.float32)
+        self._check(self._f("model_lora_get_grad")(self.h, i, P(dA), P(dB)))
+        return dA, dB
+
+    def lora_dgate(self):
+        d = np.zeros(self.lora_rank, np.float32)
+        self._check(self._f("model_lora_get_dgate")(self.h, P(d)))
+        return d
 
     def affine(self, i, C):
         g, b, dg, db = (np.zeros(C, np.float32) for _ in range(4))

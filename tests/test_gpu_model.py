@@ -42,7 +42,7 @@ def ctx():
     return native.Context(0)
 
 
-def run_pair(ctx, cfg, N, T, tag, wgrad=True, dalpha=True):
+def run_pair(ctx, cfg, N, T, tag, wgrad=True, dalpha=True, lora=None):
     from brosoundml_amd import native
     m = native.Model(ctx, cfg)
     shapes = m.param_shapes()
@@ -52,24 +52,49 @@ def run_pair(ctx, cfg, N, T, tag, wgrad=True, dalpha=True):
     m.set_params(params)
     om.set_params(params)
     asr, F0, Nn, style, dA = inputs(cfg, N, T, tag)
+    units = om.units()
+    if lora:  # DecoderLora adapters on every unit, a gate per utterance
+        rank, scale = lora
+        S = cfg["style_dim"]
+        m.lora_enable(rank, scale)
+        om.lora_enable(rank, scale)
+        offs = [u[2] for u in m.units()]
+        A = synth.normal(f"{tag}.loraA", (len(units) * rank, S), 0.2)
+        B = synth.normal(f"{tag}.loraB", (m.affine_rows(), rank), 0.2)
+        gates = synth.normal(f"{tag}.gate", (N, rank), 1.0)
+        m.lora_set(A, B)
+        for i, (_, c) in enumerate(units):
+            om.lora_set(i, A[i * rank:(i + 1) * rank], B[offs[i]:offs[i] + 2 * c])
+        ref_dA, ref_dB, ref_dG = np.zeros_like(A, np.float64), np.zeros_like(B, np.float64), []
 
     # oracle, utterance by utterance
     ref_audio, ref_har, ref_dstyle, ref_aff = [], [], [], []
     ref_grads = {n: np.zeros(int(np.prod(s))) for n, s in shapes.items()}
     for n in range(N):
         om.zero_grad()
+        if lora:
+            om.lora_gate(gates[n])
         a = om.forward(asr[n], F0[n], Nn[n], style[n], T)
         ref_audio.append(a)
         ref_har.append(om.har())
         ref_dstyle.append(om.backward(dA[n], wgrad=wgrad, dalpha=dalpha, dstyle=True))
         for name, s in shapes.items():
             ref_grads[name] += om.grad(name, s)
-        units = om.units()
         ref_aff.append([om.affine(i, c) for i, (_, c) in enumerate(units)])
+        if lora:
+            for i, (_, c) in enumerate(units):
+                gA, gB = om.lora_grads(i, c)
+                ref_dA[i * rank:(i + 1) * rank] += gA
+                ref_dB[offs[i]:offs[i] + 2 * c] += gB
+            ref_dG.append(om.lora_dgate())
 
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
     t_asr, t_F0, t_N, t_style = dev(asr), dev(F0), dev(Nn), dev(style)
     t_har = dev(np.stack(ref_har))
+    if lora:
+        t_gate = dev(gates)
+        t_dG = torch.zeros_like(t_gate)
+        m.lora_gate(t_gate, t_dG)
     m.zero_grad()
     audio = m.forward(t_asr, t_F0, t_N, t_style, T, har=t_har)
     dstyle = torch.empty_like(t_style)
@@ -78,9 +103,13 @@ def run_pair(ctx, cfg, N, T, tag, wgrad=True, dalpha=True):
     torch.cuda.synchronize()
     got_grads = {n: m.grad(n, s) for n, s in shapes.items()}
     gb, dgb = m.affines(N)
-    return dict(m=m, om=om, shapes=shapes, audio=audio.cpu().numpy(), ref_audio=np.stack(ref_audio),
-                dstyle=dstyle.cpu().numpy(), ref_dstyle=np.stack(ref_dstyle), grads=got_grads,
-                ref_grads=ref_grads, dgb=dgb, ref_aff=ref_aff, units=m.units(), oracle_units=om.units())
+    r = dict(m=m, om=om, shapes=shapes, audio=audio.cpu().numpy(), ref_audio=np.stack(ref_audio),
+             dstyle=dstyle.cpu().numpy(), ref_dstyle=np.stack(ref_dstyle), grads=got_grads,
+             ref_grads=ref_grads, dgb=dgb, ref_aff=ref_aff, units=m.units(), oracle_units=om.units())
+    if lora:
+        gA, gB = m.lora_grads()
+        r.update(lora_got=(gA, gB, t_dG.cpu().numpy()), lora_ref=(ref_dA, ref_dB, np.stack(ref_dG)))
+    return r
 
 
 def check_pair(r, wgrad=True):
@@ -116,6 +145,16 @@ def check_pair(r, wgrad=True):
 
 def test_tiny_full_extension(ctx):
     check_pair(run_pair(ctx, C.TINY, 2, 4, "gm.tiny"))
+
+
+def test_tiny_with_lora_adapters(ctx):
+    # DecoderLora adapters (rank 3) on every AdaIN unit, one gate per utterance:
+    # the waveform, every grad above, and dA, dB and the gate grad
+    r = run_pair(ctx, C.TINY, 2, 4, "gm.lora", lora=(3, 0.7))
+    check_pair(r)
+    for name, got, ref in zip(("dA", "dB", "dG"), r["lora_got"], r["lora_ref"]):
+        e = rel_l2(got, ref)
+        assert e <= 1e-4, f"LoRA {name} rel-L2 {e:.3e}"
 
 
 def test_small_full_extension(ctx):

@@ -223,3 +223,74 @@ def test_harmonic_source_closed_form():
     mag = har[: F * frames].reshape(F, frames)
     mid = mag[:, frames // 4: 3 * frames // 4]
     assert np.all(np.argmax(mid, axis=0) == 3)
+
+
+@pytest.fixture(scope="module")
+def lora64():
+    # DecoderLora adapters on every unit (rank 3, scale 0.7) with nonzero A, B
+    # and gate, so every LoRA path carries signal
+    cfg = C.TINY
+    m = O.OracleModel(cfg, fp64=True)
+    shapes = m.param_shapes()
+    params = synth.init_params(shapes)
+    m.set_params(params)
+    rank, S = 3, cfg["style_dim"]
+    m.lora_enable(rank, 0.7)
+    units = m.units()
+    lora = {}
+    for i, (_, Cu) in enumerate(units):
+        A = synth.normal(f"lora.A.{i}", (rank, S), 0.2).astype(np.float64)
+        B = synth.normal(f"lora.B.{i}", (2 * Cu, rank), 0.2).astype(np.float64)
+        m.lora_set(i, A, B)
+        lora[i] = (A, B)
+    gate = synth.normal("lora.gate", (rank,), 1.0).astype(np.float64)
+    m.lora_gate(gate)
+    inputs = make_inputs(cfg, T)
+    har = shared_har(cfg)
+    L0, audio = loss64(m, inputs, har)
+    m.zero_grad()
+    dstyle = m.backward((audio - inputs[4]).astype(np.float32))
+    grads = {i: m.lora_grads(i, Cu) for i, (_, Cu) in enumerate(units)}
+    return dict(m=m, units=units, lora=lora, gate=gate, inputs=inputs, har=har, grads=grads,
+                dgate=m.lora_dgate(), dstyle=dstyle)
+
+
+def test_fd_lora_adapters(lora64):
+    r = lora64
+    m = r["m"]
+    fails = []
+    for i in (0, 3, len(r["units"]) - 1):
+        A, B = r["lora"][i]
+        for which, base, an_grad in (("A", A, r["grads"][i][0]), ("B", B, r["grads"][i][1])):
+            v = synth.uniform(f"dir.lora.{which}.{i}", base.shape, -1.0, 1.0).astype(np.float64)
+
+            def loss_at(hh, which=which, base=base, v=v):
+                m.lora_set(i, **{which: base + hh * v})
+                return loss64(m, r["inputs"], r["har"])[0]
+
+            fd = central(loss_at)
+            m.lora_set(i, **{which: base})
+            an = float(np.sum(an_grad.astype(np.float64) * v))
+            if abs(an - fd) > TOL * max(abs(an), abs(fd), 1e-2):
+                fails.append((i, which, an, fd))
+    assert not fails, fails
+
+
+def test_fd_lora_gate_and_style(lora64):
+    r = lora64
+    m = r["m"]
+    v = synth.uniform("dir.lora.gate", r["gate"].shape, -1.0, 1.0).astype(np.float64)
+
+    def loss_gate(hh):
+        m.lora_gate(r["gate"] + hh * v)
+        return loss64(m, r["inputs"], r["har"])[0]
+
+    fd = central(loss_gate)
+    m.lora_gate(r["gate"])
+    an = float(np.dot(r["dgate"].astype(np.float64), v))
+    assert abs(an - fd) <= TOL * max(abs(an), abs(fd), 1e-2), ("gate", an, fd)
+    style = r["inputs"][3].astype(np.float64)
+    vs = synth.uniform("dir.lora.style", style.shape, -1.0, 1.0).astype(np.float64)
+    fd = central(lambda hh: loss64(m, r["inputs"], r["har"], style + hh * vs)[0])
+    an = float(np.dot(r["dstyle"].astype(np.float64), vs))
+    assert abs(an - fd) <= TOL * max(abs(an), abs(fd), 1e-2), ("style", an, fd)
