@@ -93,6 +93,8 @@ struct GemmArgs {
     int full_tiles, split_tiles, fsplit;
     int full_per_xcd, parts_per_xcd;  // block slots per XCD for each kind
     float* P;
+    // octet mode (corr_gemm): K chunk = one input-channel octet x up to G taps
+    int G, n_tg, n_oct, span8;  // taps per chunk, tap groups, octets, staged positions
 };
 
 // Logical block order with consecutive ids on one XCD: the dispatcher deals
@@ -173,6 +175,51 @@ __device__ inline bool block_work(const GemmArgs& g, int& tile, int& part) {
     return true;
 }
 
+// Tile epilogue shared by the GEMM kernels: lane owns column l32 and rows
+// 8*(e/4) + 4*hi + e%4 of each 32x32 MFMA tile. A split part writes its raw
+// sums to its compact partial tile; a whole tile applies bias, residual,
+// scale and beta and stores Y.
+__device__ inline void store_tile(const GemmArgs& g, const TileGeo& T, int tile, int part, const f32x16 (&acc)[2][2],
+                                  int wm, int wn, int hi, int l32) {
+    const int b = T.b, n_q = T.n_q, os = T.os, oo = T.oo, m0 = T.m0, q0 = T.q0;
+    if (part >= 0) {  // raw sums of this chunk range, tile-local [m][q]
+        float* Pt = g.P + (static_cast<long>(tile - g.full_tiles) * g.fsplit + part) * (BM * BN);
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn)
+#pragma unroll
+            for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int ml = wm * 64 + tm * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
+                    Pt[ml * BN + wn * 64 + tn * 32 + l32] = acc[tm][tn][e];
+                }
+        return;
+    }
+    float* Yb = g.Y + static_cast<long>(b) * g.y_bs;
+    const float* Rb = g.R ? g.R + static_cast<long>(b) * g.r_bs : nullptr;
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn) {
+        const int q = q0 + wn * 64 + tn * 32 + l32;
+        if (q >= n_q) continue;
+        const long j = static_cast<long>(q) * os + oo;
+#pragma unroll
+        for (int tm = 0; tm < 2; ++tm) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int m = m0 + wm * 64 + tm * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
+                if (m >= g.C_out) continue;
+                float v = acc[tm][tn][e];
+                if (g.bias) v += g.bias[m];
+                const long yi = static_cast<long>(m) * g.L_y + j;
+                if (Rb) v += Rb[yi];
+                v *= g.scale;
+                if (g.beta != 0.0f) v += g.beta * Yb[yi];
+                Yb[yi] = v;
+            }
+        }
+    }
+}
+
 // Grid of 8 * (full_per_xcd + parts_per_xcd) blocks. Two LDS stages;
 // weights arrive packed chunk-major (row ((chunk*k + t)*CK + c_local)), so a
 // chunk's KR = CK*k rows are one contiguous slab of the panel.
@@ -240,8 +287,9 @@ void conv_gemm(GemmArgs g) {
                 const int c = ch * CK + r;
                 const int pos = x0 - ((c * Lm + xm) & 3) + sg * 256 + lane * 4;
                 const unsigned off = c < g.C_in ? static_cast<unsigned>(c * g.L_in + pos) * 4u : 0x80000000u;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + KR * BM + r * span_p + sg * 256, 16,
-                                                         static_cast<int>(off), 0, 0, 0);
+                if (sg * 256 + lane * 4 < span + 3)  // lanes past the window stay idle
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + KR * BM + r * span_p + sg * 256, 16,
+                                                             static_cast<int>(off), 0, 0, 0);
             }
             return;
         }
@@ -251,8 +299,9 @@ void conv_gemm(GemmArgs g) {
             const int pos = x0 + sg * 64 + lane;
             const unsigned off = (c < g.C_in && pos >= 0 && pos < g.L_in)
                                      ? static_cast<unsigned>(c * g.L_in + pos) * 4u : 0x80000000u;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + KR * BM + r * span_p + sg * 64, 4,
-                                                     static_cast<int>(off), 0, 0, 0);
+            if (sg * 64 + lane < span)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + KR * BM + r * span_p + sg * 64, 4,
+                                                         static_cast<int>(off), 0, 0, 0);
         }
     };
 
@@ -325,43 +374,150 @@ void conv_gemm(GemmArgs g) {
         __syncthreads();
     }
 
-    // epilogue: lane owns column l32 and rows 8*(e/4) + 4*hi + e%4 of each tile
-    if (part >= 0) {  // raw sums of this chunk range, tile-local [m][q]
-        float* Pt = g.P + (static_cast<long>(tile - g.full_tiles) * g.fsplit + part) * (BM * BN);
+    store_tile(g, T, tile, part, acc, wm, wn, hi, l32);
+}
+
+// Stride-1 correlation (conv forward, conv input-grad, each transposed-conv
+// phase) as an implicit GEMM whose operands are read 16 B per lane.
+//
+// K runs over (input channel c, tap t). A chunk is one channel octet
+// o (c = 8o + 4h + e, h in {0, 1}, e in 0..3) times a group of up to G taps.
+// In one 32x32x2 MFMA step e of tap t, lanes of half h contribute
+// k = (8o + 4h + e, t), so each lane needs, per tap, four consecutive
+// channels: the weights are packed as [o][t][h][m_pad][4] (a chunk's rows
+// are whole 2 KB runs per (t, h) and a block's 128 columns), and the input
+// window is staged channels-last, [h][position][4], by a gathering DMA
+// (lane i of a 64-lane load fetches channel 4h + i%4 at position i/4 and
+// lands at LDS float i of the block). One ds_read_b128 then feeds four
+// MFMA steps: per tap a wave reads 2 A and 2 B vectors for 16 MFMAs.
+// Grid, tile order, split parts and epilogue as conv_gemm.
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4)))
+void corr_gemm(GemmArgs g) {
+    extern __shared__ float smem[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, wn = wave >> 1;
+    const int l32 = lane & 31, hi = lane >> 5;
+
+    int tile, part;
+    if (!block_work(g, tile, part)) return;  // uniform per block
+    TileGeo T;
+    decode_tile(g, tile, T);
+    const int k = T.k, d = T.d;
+    if (T.q0 >= T.n_q) return;  // uniform per block
+
+    const int G = g.G, n_tg = g.n_tg, span8 = g.span8;
+    const int a_st = G * 1024;             // A floats per stage: G taps x 2 halves x 128 x 4
+    const int stage = a_st + 8 * span8;    // + input window: 2 halves x span8 positions x 4
+    const float* Xb = g.X + static_cast<long>(T.b) * g.x_bs;
+    const __amdgpu_buffer_rsrc_t xrs = uniform_rsrc(Xb, g.C_in * g.L_in * 4);
+    const int x0 = T.q0 - T.p;             // input position of column q0 at tap 0
+    // weight staging: wave w copies quarter w of every (tap, half) run:
+    // half w>>1, 256-float piece w&1 of the block's 512 floats
+    const long a_row = 8L * g.m_pad;       // floats per (octet, tap) = 2 halves x m_pad x 4
+    const float* Aw = T.A + static_cast<long>(T.m0) * 4 + (wave >> 1) * g.m_pad * 4 + (wave & 1) * 256 + lane * 4;
+    const int a_lds = (wave >> 1) * 512 + (wave & 1) * 256;
+    // input staging: wave w fetches half w&1, 16-position blocks (w>>1) + 2j
+    const int nb = span8 >> 4;
+    const int lane_c = (wave & 1) * 4 + (lane & 3);
+    const int lane_p = lane >> 2;
+    const int x_lds = a_st + (wave & 1) * span8 * 4;
+
+    auto issue = [&](int o, int tg, int sb) {
+        const int t0 = tg * G;
+        const int gt = min(G, k - t0);
+        const float* Ag = Aw + (static_cast<long>(o) * k + t0) * a_row;
+        for (int j = 0; j < gt; ++j)
+            __builtin_amdgcn_global_load_lds(Ag + j * a_row, smem + sb + j * 1024 + a_lds, 16, 0, 0);
+        const int xs = x0 + t0 * d;
+        const int c = o * 8 + lane_c;
+        const bool inner = o * 8 + 8 <= g.C_in && xs >= 0 && xs + span8 <= g.L_in;  // uniform
+        for (int blk = wave >> 1; blk < nb; blk += 2) {
+            const int pos = xs + blk * 16 + lane_p;
+            const unsigned off = (inner || (c < g.C_in && pos >= 0 && pos < g.L_in))
+                                     ? static_cast<unsigned>(c * g.L_in + pos) * 4u : 0x80000000u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + x_lds + blk * 64, 4,
+                                                     static_cast<int>(off), 0, 0, 0);
+        }
+    };
+
+    f32x16 acc[2][2];
 #pragma unroll
-        for (int tn = 0; tn < 2; ++tn)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int tm = 0; tm < 2; ++tm)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int ml = wm * 64 + tm * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
-                    Pt[ml * BN + wn * 64 + tn * 32 + l32] = acc[tm][tn][e];
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    const int nchunks = g.n_oct * n_tg;
+    const int nparts = part < 0 ? 1 : g.fsplit;
+    const int pp = part < 0 ? 0 : part;
+    const int ch0 = pp * nchunks / nparts;
+    const int ch1 = (pp + 1) * nchunks / nparts;
+    const bool live = T.q0 + wn * 64 < T.n_q;  // wave-uniform
+    // lane reads: A at m = wm*64 + tm*32 + l32, B at column n = wn*64 + tn*32 + l32 (+ tap shift)
+    const int a_rd = hi * 512 + (wm * 64 + l32) * 4;
+    const int b_rd = a_st + hi * span8 * 4 + (wn * 64 + l32) * 4;
+
+    int o = ch0 / n_tg, tg = ch0 - (ch0 / n_tg) * n_tg;  // chunk ch = o * n_tg + tg
+    if (ch0 < ch1) issue(o, tg, 0);
+    __builtin_amdgcn_s_waitcnt(0);  // staging loads landed in LDS
+    __syncthreads();
+    for (int ch = ch0; ch < ch1; ++ch) {
+        const int sb = ((ch - ch0) & 1) * stage;
+        const int no = tg + 1 == n_tg ? o + 1 : o, ntg = tg + 1 == n_tg ? 0 : tg + 1;
+        if (ch + 1 < ch1) issue(no, ntg, stage - sb);
+        const int gt = min(G, k - tg * G);
+        const int ab = sb + a_rd, bb = sb + b_rd;
+        auto ld = [&](int tl, float4 (&a)[2], float4 (&bv)[2]) {
+            tl = min(tl, gt - 1);
+            int ao = ab + tl * 1024, bo = bb + tl * d * 4;
+            // opaque offsets keep each tap's reads where they are placed
+            asm volatile("" : "+v"(ao), "+v"(bo));
+            a[0] = *reinterpret_cast<const float4*>(smem + ao);
+            a[1] = *reinterpret_cast<const float4*>(smem + ao + 128);
+            bv[0] = *reinterpret_cast<const float4*>(smem + bo);
+            bv[1] = *reinterpret_cast<const float4*>(smem + bo + 128);
+        };
+        auto mm = [&](const float4 (&a)[2], const float4 (&bv)[2]) {
+            const float a0[4] = {a[0].x, a[0].y, a[0].z, a[0].w};
+            const float a1[4] = {a[1].x, a[1].y, a[1].z, a[1].w};
+            const float b0[4] = {bv[0].x, bv[0].y, bv[0].z, bv[0].w};
+            const float b1[4] = {bv[1].x, bv[1].y, bv[1].z, bv[1].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[e], b0[e], acc[0][0], 0, 0, 0);
+                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[e], b1[e], acc[0][1], 0, 0, 0);
+                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[e], b0[e], acc[1][0], 0, 0, 0);
+                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[e], b1[e], acc[1][1], 0, 0, 0);
+            }
+        };
+        float4 pa[2], pb[2], qa[2], qb[2];
+        ld(0, pa, pb);
+        int tl = live ? 0 : gt;  // a wave whose columns all lie past n_q only stages
+        for (; tl + 1 < gt; tl += 2) {
+            ld(tl + 1, qa, qb);
+            mm(pa, pb);
+            ld(tl + 2, pa, pb);
+            mm(qa, qb);
+            // (1 MFMA, 1 read) x 4, then 12 MFMAs; twice
+            for (int r = 0; r < 2; ++r) {
+                for (int i = 0; i < 4; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 }
-        return;
-    }
-    float* Yb = g.Y + static_cast<long>(b) * g.y_bs;
-    const float* Rb = g.R ? g.R + static_cast<long>(b) * g.r_bs : nullptr;
-#pragma unroll
-    for (int tn = 0; tn < 2; ++tn) {
-        const int q = q0 + wn * 64 + tn * 32 + l32;
-        if (q >= n_q) continue;
-        const long j = static_cast<long>(q) * os + oo;
-#pragma unroll
-        for (int tm = 0; tm < 2; ++tm) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int m = m0 + wm * 64 + tm * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
-                if (m >= g.C_out) continue;
-                float v = acc[tm][tn][e];
-                if (g.bias) v += g.bias[m];
-                const long yi = static_cast<long>(m) * g.L_y + j;
-                if (Rb) v += Rb[yi];
-                v *= g.scale;
-                if (g.beta != 0.0f) v += g.beta * Yb[yi];
-                Yb[yi] = v;
+                __builtin_amdgcn_sched_group_barrier(0x008, 12, 0);
             }
         }
+        if (live && tl < gt) mm(pa, pb);
+        o = no;
+        tg = ntg;
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's staging loads landed
+        __syncthreads();
     }
+
+    store_tile(g, T, tile, part, acc, wm, wn, hi, l32);
 }
 
 // Split tiles: Y = scale * (sum of the parts in order + bias + R) + beta * Y.
@@ -463,6 +619,40 @@ __global__ void pack_convt_fwd(const float* W, float* A, int C_in, int C_out,
         const int t = r + (kt - 1 - tp) * s;
         float v = 0.0f;
         if (m < C_out && c < C_in && t < k) v = W[(static_cast<long>(c) * C_out + m) * k + t];
+        A[i] = v;
+    }
+}
+
+// corr_gemm panel [o][t][h][m_pad][4] for channel c = 8o + 4h + e and tap
+// t < kt (per phase, phase_stride floats each). `mode` is the weight map:
+// 0 conv forward            A[(c, t), m] = W[m, c*k + t]       (m < C_out, c < C_in)
+// 1 conv input-grad         A[(c, t), m] = W[c, m*k + k-1-t]   (m < C_in, c < C_out)
+// 2 conv-transpose forward, phase r of s: tap t covers original tap
+//   r + (kt-1-t)*s, A_r[(c, t), m] = W[c, m*k + that] or 0   (m < C_out, c < C_in)
+__global__ void pack_octet(const float* W, float* A, int mode, int C_in, int C_out, int k, int s, int kt,
+                           int m_pad, long phase_stride, int n_phase) {
+    const long total = phase_stride * n_phase;
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        const int r = static_cast<int>(i / phase_stride);
+        const long w = i - r * phase_stride;
+        const int e = static_cast<int>(w & 3);
+        const long w4 = w >> 2;
+        const int m = static_cast<int>(w4 % m_pad);
+        const long rest = w4 / m_pad;
+        const int h = static_cast<int>(rest & 1);
+        const int t = static_cast<int>((rest >> 1) % kt);
+        const int o = static_cast<int>((rest >> 1) / kt);
+        const int c = o * 8 + h * 4 + e;
+        float v = 0.0f;
+        if (mode == 0) {
+            if (m < C_out && c < C_in) v = W[(static_cast<long>(m) * C_in + c) * k + t];
+        } else if (mode == 1) {
+            if (m < C_in && c < C_out) v = W[(static_cast<long>(c) * C_in + m) * k + (k - 1 - t)];
+        } else {
+            const int tt = r + (kt - 1 - t) * s;
+            if (m < C_out && c < C_in && tt < k) v = W[(static_cast<long>(c) * C_out + m) * k + tt];
+        }
         A[i] = v;
     }
 }
@@ -827,20 +1017,59 @@ const void* conv_kernel_for(int CK) {
     }
 }
 
-// Resident conv_gemm blocks per CU for chunk CK and `lds` bytes (cached).
-int conv_blocks_per_cu(int CK, size_t lds) {
+// Resident blocks per CU of GEMM kernel `kern` with `lds` bytes (cached).
+int blocks_per_cu(const void* kern, size_t lds) {
     static std::mutex mu;
-    static std::map<std::pair<int, size_t>, int> cache;
+    static std::map<std::pair<const void*, size_t>, int> cache;
     std::lock_guard<std::mutex> lock(mu);
-    const auto key = std::make_pair(CK, lds);
+    const auto key = std::make_pair(kern, lds);
     auto it = cache.find(key);
     if (it != cache.end()) return it->second;
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv_kernel_for(CK), NT, lds) != hipSuccess ||
-        per_cu < 1)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, NT, lds) != hipSuccess || per_cu < 1)
         per_cu = 1;
     cache[key] = per_cu;
     return per_cu;
+}
+
+const void* corr_kernel() {
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&corr_gemm),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        attr = true;
+    }
+    return reinterpret_cast<const void*>(&corr_gemm);
+}
+
+// Octet-mode geometry for a stride-1 correlation of k taps at dilation d
+// over C channels: chunks of up to 4 taps (three for k = 3), the staged
+// window of a 4-tap chunk rounded to 16 positions.
+void octet_setup(GemmArgs& g, int C, int k, int d) {
+    g.G = k < 4 ? k : 4;
+    g.n_tg = static_cast<int>(cdiv(k, g.G));
+    g.span8 = static_cast<int>(cdiv(BN + (g.G - 1) * d, 16) * 16);
+    g.n_oct = static_cast<int>(cdiv(C, 8));
+    g.cin_pad = g.n_oct * 8;
+    g.CK = 0;
+}
+
+// K chunking for a stride-1 correlation over C channels, kk taps at dilation
+// dd, `tiles` output tiles. corr_gemm (octet chunks, 16-B operand reads) is
+// the faster kernel where the grid is smaller than one round of conv_gemm's
+// resident blocks (where conv_gemm would need a split plan); on larger grids
+// conv_gemm's five resident waves per SIMD hide the chunk transitions better.
+void choose_chunks(kdec_ctx* ctx, GemmArgs& g, int C, int kk, int dd, long tiles) {
+    const int ck = pick_ck(kk, 1, dd);
+    const long slots = static_cast<long>(blocks_per_cu(conv_kernel_for(ck), conv_lds_bytes(ck, kk, 1, dd))) *
+                       ctx->num_cus;
+    if (tiles < slots) {
+        octet_setup(g, C, kk, dd);
+        return;
+    }
+    g.G = 0;
+    g.CK = ck;
+    g.cin_pad = static_cast<int>(cdiv(C, 32) * 32);
 }
 
 // Launches conv_gemm over an already packed A.
@@ -853,15 +1082,19 @@ int conv_blocks_per_cu(int CK, size_t lds) {
 int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
              double flops) {
     const int CK = g.CK;
+    const bool octet = g.G > 0;
     const int kk = g.n_phase > 1 ? g.ph_kt : g.k;
     const int ss = g.n_phase > 1 ? 1 : g.s;
     const int dd = g.n_phase > 1 ? 1 : g.d;
-    if (CK * kk > 64 || (CK * kk) % 2) return fail(ctx, KDEC_EINVAL, "conv: kernel too long for the weight stage");
-    const size_t lds = conv_lds_bytes(CK, kk, ss, dd);
+    if (octet ? (ss != 1 || g.G > kk || g.span8 < BN + (g.G - 1) * dd || g.span8 % 16)
+              : (CK * kk > 64 || (CK * kk) % 2))
+        return fail(ctx, KDEC_EINVAL, "conv: bad chunk geometry");
+    const size_t lds = octet ? 2 * (static_cast<size_t>(g.G) * 1024 + 8 * static_cast<size_t>(g.span8)) * sizeof(float)
+                             : conv_lds_bytes(CK, kk, ss, dd);
     if (lds > 160 * 1024) return fail(ctx, KDEC_EINVAL, "conv: tile does not fit LDS");
     if (static_cast<long>(g.C_in) * g.L_in * 4 > 0x7fffffffL)
         return fail(ctx, KDEC_EINVAL, "conv: input too large for one buffer descriptor");
-    const void* kern = conv_kernel_for(CK);
+    const void* kern = octet ? corr_kernel() : conv_kernel_for(CK);
     if (!kern) return fail(ctx, KDEC_EINVAL, "conv: unsupported channel chunk");
     int max_q = g.n_q;
     if (g.n_phase > 1) max_q = static_cast<int>(cdiv(g.L_y + g.ph_s, g.ph_s)) + 1;
@@ -870,8 +1103,8 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
     g.nz = N * g.n_phase;
     const long tiles = static_cast<long>(g.m_tiles) * g.q_tiles * g.nz;
     if (tiles > 0x7fffffffL / 16) return fail(ctx, KDEC_EINVAL, "conv: grid too large");
-    const long slots = static_cast<long>(conv_blocks_per_cu(CK, lds)) * ctx->num_cus;
-    const int nchunks = g.cin_pad / CK;
+    const long slots = static_cast<long>(blocks_per_cu(kern, lds)) * ctx->num_cus;
+    const int nchunks = octet ? g.n_oct * g.n_tg : g.cin_pad / CK;
     const long rem = tiles % slots;
     long f = 1;
     if (rem > 0) f = std::min(std::min(slots / rem, static_cast<long>(nchunks / 4)), 16L);
@@ -923,22 +1156,31 @@ int kdec_conv1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
     KDEC_CHECK(ctx, L > 0 && L_out > 0, "kdec_conv1d_fwd: empty output");
     KDEC_CHECK(ctx, x_bs >= static_cast<long>(C_in) * L && y_bs >= static_cast<long>(C_out) * L_out,
                "kdec_conv1d_fwd: batch stride too small");
-    const int CK = pick_ck(k, stride, dil);
-    const int cin_pad = static_cast<int>(cdiv(C_in, 32) * 32);
     const int m_pad = static_cast<int>(cdiv(C_out, BM) * BM);
-    Workspace A(ctx, static_cast<size_t>(cin_pad) * k * m_pad * sizeof(float));
-    if (!A.p) return KDEC_ENOMEM;
-    const long tot = static_cast<long>(cin_pad) * k * m_pad;
-    hipLaunchKernelGGL(pack_fwd, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), C_in,
-                       C_out, k, cin_pad, m_pad, CK);
-    if (int rc = launch_check(ctx, "pack_fwd")) return rc;
     GemmArgs g{};
-    g.X = X; g.x_bs = x_bs; g.A = A.as<float>(); g.a_phase_stride = 0;
+    g.X = X; g.x_bs = x_bs; g.a_phase_stride = 0;
     g.bias = bias; g.Y = Y; g.y_bs = y_bs; g.R = R; g.r_bs = r_bs;
     g.C_in = C_in; g.L_in = L; g.C_out = C_out; g.L_y = L_out;
-    g.cin_pad = cin_pad; g.m_pad = m_pad;
-    g.k = k; g.s = stride; g.d = dil; g.p = pad; g.n_q = L_out; g.CK = CK;
+    g.m_pad = m_pad;
+    g.k = k; g.s = stride; g.d = dil; g.p = pad; g.n_q = L_out;
     g.scale = scale; g.beta = beta; g.n_phase = 1;
+    if (stride == 1) {
+        choose_chunks(ctx, g, C_in, k, dil, cdiv(C_out, BM) * cdiv(L_out, BN) * N);
+    } else {
+        g.CK = pick_ck(k, stride, dil);
+        g.cin_pad = static_cast<int>(cdiv(C_in, 32) * 32);
+    }
+    const long tot = static_cast<long>(g.cin_pad) * k * m_pad;
+    Workspace A(ctx, static_cast<size_t>(tot) * sizeof(float));
+    if (!A.p) return KDEC_ENOMEM;
+    g.A = A.as<float>();
+    if (g.G > 0)
+        hipLaunchKernelGGL(pack_octet, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), 0, C_in,
+                           C_out, k, 1, k, m_pad, tot, 1);
+    else
+        hipLaunchKernelGGL(pack_fwd, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), C_in,
+                           C_out, k, g.cin_pad, m_pad, g.CK);
+    if (int rc = launch_check(ctx, "pack_fwd")) return rc;
     return run_gemm(ctx, g, N, m_pad / BM, "conv_fwd",
                     2.0 * N * C_out * static_cast<double>(L_out) * C_in * k);
 }
@@ -957,22 +1199,26 @@ int kdec_conv1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
     KDEC_CHECK(ctx, pp >= 0, "kdec_conv1d_dgrad: padding larger than the receptive field");
     KDEC_CHECK(ctx, dy_bs >= static_cast<long>(C_out) * L_out && dx_bs >= static_cast<long>(C_in) * L,
                "kdec_conv1d_dgrad: batch stride too small");
-    const int CK = pick_ck(k, 1, dil);
-    const int cpad = static_cast<int>(cdiv(C_out, 32) * 32);
     const int m_pad = static_cast<int>(cdiv(C_in, BM) * BM);
-    Workspace A(ctx, static_cast<size_t>(cpad) * k * m_pad * sizeof(float));
-    if (!A.p) return KDEC_ENOMEM;
-    const long tot = static_cast<long>(cpad) * k * m_pad;
-    hipLaunchKernelGGL(pack_dgrad, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), C_in,
-                       C_out, k, cpad, m_pad, CK);
-    if (int rc = launch_check(ctx, "pack_dgrad")) return rc;
     GemmArgs g{};
-    g.X = dY; g.x_bs = dy_bs; g.A = A.as<float>();
+    g.X = dY; g.x_bs = dy_bs;
     g.Y = dX; g.y_bs = dx_bs;
     g.C_in = C_out; g.L_in = L_out; g.C_out = C_in; g.L_y = L;
-    g.cin_pad = cpad; g.m_pad = m_pad;
-    g.k = k; g.s = 1; g.d = dil; g.p = pp; g.n_q = L; g.CK = CK;
+    g.m_pad = m_pad;
+    g.k = k; g.s = 1; g.d = dil; g.p = pp; g.n_q = L;
     g.scale = scale; g.beta = beta; g.n_phase = 1;
+    choose_chunks(ctx, g, C_out, k, dil, cdiv(C_in, BM) * cdiv(L, BN) * N);
+    const long tot = static_cast<long>(g.cin_pad) * k * m_pad;
+    Workspace A(ctx, static_cast<size_t>(tot) * sizeof(float));
+    if (!A.p) return KDEC_ENOMEM;
+    g.A = A.as<float>();
+    if (g.G > 0)
+        hipLaunchKernelGGL(pack_octet, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), 1, C_in,
+                           C_out, k, 1, k, m_pad, tot, 1);
+    else
+        hipLaunchKernelGGL(pack_dgrad, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), C_in,
+                           C_out, k, g.cin_pad, m_pad, g.CK);
+    if (int rc = launch_check(ctx, "pack_dgrad")) return rc;
     return run_gemm(ctx, g, N, m_pad / BM, "conv_dgrad",
                     2.0 * N * C_out * static_cast<double>(L_out) * C_in * k);
 }
@@ -1136,21 +1382,26 @@ int kdec_convt1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
     KDEC_CHECK(ctx, y_bs >= static_cast<long>(C_out) * L_out && x_bs >= static_cast<long>(C_in) * L,
                "kdec_convt1d_fwd: batch stride too small");
     const int kt = static_cast<int>(cdiv(k, stride));
-    const int CK = pick_ck(kt, 1, 1);
-    const int cin_pad = static_cast<int>(cdiv(C_in, 32) * 32);
     const int m_pad = static_cast<int>(cdiv(C_out, BM) * BM);
-    const long ph = static_cast<long>(cin_pad) * kt * m_pad;
+    GemmArgs g{};
+    // output tiles: per phase at most L_out / stride + 2 columns (as run_gemm)
+    const long q_tiles = stride > 1 ? cdiv(cdiv(L_out + stride, stride) + 1, BN) : cdiv(L_out, BN);
+    choose_chunks(ctx, g, C_in, kt, 1, cdiv(C_out, BM) * q_tiles * N * stride);
+    const long ph = static_cast<long>(g.cin_pad) * kt * m_pad;
     Workspace A(ctx, static_cast<size_t>(ph) * stride * sizeof(float));
     if (!A.p) return KDEC_ENOMEM;
-    hipLaunchKernelGGL(pack_convt_fwd, dim3(grid1d(ph * stride)), dim3(256), 0, ctx->stream, W,
-                       A.as<float>(), C_in, C_out, k, stride, kt, cin_pad, m_pad, ph, CK);
+    if (g.G > 0)
+        hipLaunchKernelGGL(pack_octet, dim3(grid1d(ph * stride)), dim3(256), 0, ctx->stream, W, A.as<float>(), 2,
+                           C_in, C_out, k, stride, kt, m_pad, ph, stride);
+    else
+        hipLaunchKernelGGL(pack_convt_fwd, dim3(grid1d(ph * stride)), dim3(256), 0, ctx->stream, W,
+                           A.as<float>(), C_in, C_out, k, stride, kt, g.cin_pad, m_pad, ph, g.CK);
     if (int rc = launch_check(ctx, "pack_convt_fwd")) return rc;
-    GemmArgs g{};
     g.X = X; g.x_bs = x_bs; g.A = A.as<float>(); g.a_phase_stride = ph;
     g.bias = bias; g.Y = Y; g.y_bs = y_bs;
     g.C_in = C_in; g.L_in = L; g.C_out = C_out; g.L_y = L_out;
-    g.cin_pad = cin_pad; g.m_pad = m_pad;
-    g.k = kt; g.s = 1; g.d = 1; g.p = 0; g.n_q = 0; g.CK = CK;
+    g.m_pad = m_pad;
+    g.k = kt; g.s = 1; g.d = 1; g.p = 0; g.n_q = 0;
     g.scale = 1.0f; g.beta = 0.0f;
     g.n_phase = stride; g.ph_s = stride; g.ph_p = pad; g.ph_kt = kt;
     if (stride == 1) {  // plain correlation: taps reversed, p' = k-1-pad

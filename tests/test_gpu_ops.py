@@ -142,6 +142,30 @@ def test_conv1d_grid_beyond_one_round(K, k, d):
     assert_close(h(dX), ref.numpy(), GRAD_TOL, "conv1d backward_input, split tail tiles")
 
 
+@pytest.mark.parametrize("k,d", [(3, 5), (11, 1)])
+def test_conv1d_small_grid_split_parts(K, k, d):
+    # 200 (forward) and 400 (input-grad) output tiles: fewer than one round of
+    # resident blocks, so every tile runs as channel-chunk parts (octet chunks
+    # of up to four taps) summed by tile_reduce. Reference: torch float64.
+    N, C_in, C_out, L = 2, 256, 128, 128 * 100 - 7
+    p = d * (k - 1) // 2
+    x, W, b = rnd(N, C_in, L), rnd(C_out, C_in * k, scale=0.1), rnd(C_out)
+    Y = torch.empty(N, C_out, L, device="cuda")
+    K.call("kdec_conv1d_fwd", P(g(x)), C_in * L, P(g(W)), P(g(b)), P(Y), C_out * L, N, C_in, L, C_out, k, 1,
+           p, d, None, 0, 1.0, 0.0)
+    F = torch.nn.functional
+    xt = torch.from_numpy(x).double()
+    Wt = torch.from_numpy(W).double().reshape(C_out, C_in, k)
+    ref = F.conv1d(xt, Wt, torch.from_numpy(b).double(), padding=p, dilation=d)
+    assert_close(h(Y), ref.numpy(), FWD_TOL, "conv1d forward, split parts")
+    dY = rnd(N, C_out, L)
+    dX = torch.empty(N, C_in, L, device="cuda")
+    K.call("kdec_conv1d_dgrad", P(g(W)), P(g(dY)), C_out * L, P(dX), C_in * L, N, C_in, L, C_out, k, 1, p, d,
+           1.0, 0.0)
+    ref = F.conv_transpose1d(torch.from_numpy(dY).double(), Wt, padding=p, dilation=d)
+    assert_close(h(dX), ref.numpy(), GRAD_TOL, "conv1d backward_input, split parts")
+
+
 def test_conv1d_batch_stride_and_accumulate(K):
     # outputs written into a channel slice of a wider tensor, beta accumulate
     N, C_in, C_out, L, k = 2, 16, 8, 40, 3
