@@ -630,28 +630,30 @@ __global__ void pack_convt_fwd(const float* W, float* A, int C_in, int C_out,
 // 2 conv-transpose forward, phase r of s: tap t covers original tap
 //   r + (kt-1-t)*s, A_r[(c, t), m] = W[c, m*k + that] or 0   (m < C_out, c < C_in)
 __global__ void pack_octet(const float* W, float* A, int mode, int C_in, int C_out, int k, int s, int kt,
-                           int m_pad, long phase_stride, int n_phase) {
-    const long total = phase_stride * n_phase;
-    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < total;
-         i += static_cast<long>(gridDim.x) * blockDim.x) {
-        const int r = static_cast<int>(i / phase_stride);
-        const long w = i - r * phase_stride;
+                           int m_pad, int phase_stride, int n_phase) {
+    // 32-bit index math: the host keeps phase_stride * n_phase below 2^31
+    const unsigned total = static_cast<unsigned>(phase_stride) * n_phase;
+    const unsigned mp = static_cast<unsigned>(m_pad);
+    for (unsigned i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+        const unsigned r = i / static_cast<unsigned>(phase_stride);
+        const unsigned w = i - r * static_cast<unsigned>(phase_stride);
         const int e = static_cast<int>(w & 3);
-        const long w4 = w >> 2;
-        const int m = static_cast<int>(w4 % m_pad);
-        const long rest = w4 / m_pad;
+        const unsigned w4 = w >> 2;
+        const unsigned rest = w4 / mp;
+        const int m = static_cast<int>(w4 - rest * mp);
         const int h = static_cast<int>(rest & 1);
-        const int t = static_cast<int>((rest >> 1) % kt);
-        const int o = static_cast<int>((rest >> 1) / kt);
+        const unsigned ot = rest >> 1;
+        const int o = static_cast<int>(ot / static_cast<unsigned>(kt));
+        const int t = static_cast<int>(ot) - o * kt;
         const int c = o * 8 + h * 4 + e;
         float v = 0.0f;
         if (mode == 0) {
-            if (m < C_out && c < C_in) v = W[(static_cast<long>(m) * C_in + c) * k + t];
+            if (m < C_out && c < C_in) v = W[(m * C_in + c) * k + t];
         } else if (mode == 1) {
-            if (m < C_in && c < C_out) v = W[(static_cast<long>(c) * C_in + m) * k + (k - 1 - t)];
+            if (m < C_in && c < C_out) v = W[(c * C_in + m) * k + (k - 1 - t)];
         } else {
-            const int tt = r + (kt - 1 - t) * s;
-            if (m < C_out && c < C_in && tt < k) v = W[(static_cast<long>(c) * C_out + m) * k + tt];
+            const int tt = static_cast<int>(r) + (kt - 1 - t) * s;
+            if (m < C_out && c < C_in && tt < k) v = W[(c * C_out + m) * k + tt];
         }
         A[i] = v;
     }
@@ -663,10 +665,11 @@ constexpr int KC = 32;       // positions per K chunk
 constexpr int WG_WN = 4;                 // waves along n (2 along m)
 constexpr int WG_NT = 128 * WG_WN;       // threads per wgrad block
 constexpr int WG_BN = 64 * WG_WN;        // n columns per wgrad block
-// G tile in LDS: 64 row pairs (m, m + 64) of 2*KC positions at an odd pair
-// stride, so a column read across 32 consecutive m hits 32 distinct banks
-// and one 64-lane load fills a whole pair.
-constexpr int GP = 2 * KC + 1;
+// G tile in LDS: 64 row pairs (m, m + 64) of 2*KC positions at a pair stride
+// of 2*KC + 4 floats: one 64-lane load fills a whole pair, rows stay 16-B
+// aligned for ds_read_b128, and 16 consecutive m of one such read cover all
+// 64 banks once.
+constexpr int GP = 2 * KC + 4;
 
 struct WgradArgs {
     const float* X;      // correlation input  [n][C_x][L_x]
@@ -692,6 +695,7 @@ struct WgradArgs {
 // (buffer_load_dword ... lds, zero past each row's end): G as 128 rows of KC
 // positions at an odd row stride, the input window as XR channel rows at a
 // stride rs chosen so that column n = c*k + t lands on bank n*d.
+template <bool S1>  // S1: stride 1 (the four input values of a group are adjacent)
 __global__ __launch_bounds__(WG_NT) __attribute__((amdgpu_waves_per_eu(4)))
 void wgrad_gemm(WgradArgs g) {
     extern __shared__ float smem[];
@@ -708,7 +712,7 @@ void wgrad_gemm(WgradArgs g) {
     const int z = lid / g.m_tiles;
     const int m0 = mt * BM;
     const int n0 = nt * WG_BN;
-    const int k = g.k, s = g.s, d = g.d;
+    const int k = g.k, s = S1 ? 1 : g.s, d = g.d;
     const int ci_lo = n0 / k;
     const int gsz = 64 * GP;
     const int stage = gsz + g.XR * g.rs;
@@ -729,29 +733,35 @@ void wgrad_gemm(WgradArgs g) {
     const int g_pos_lane = lane & 31;
 
     // One buffer descriptor per utterance; rows, positions and channels out
-    // of range get an out-of-bounds offset and stage as zeros.
+    // of range get an out-of-bounds offset and stage as zeros. Wave w stages
+    // G row pairs w, w + 8, ... and input rows w, w + 8, ... (all segments of
+    // each), with the range checks skipped for chunks wholly inside.
+    const bool g_rows_in = m0 + BM <= g.M;
     auto issue = [&](int ch, int sb) {
         const int b = ch / g.chunks_per_n;
         const int l0 = (ch - b * g.chunks_per_n) * KC;
         const __amdgpu_buffer_rsrc_t grs = uniform_rsrc(g.G + static_cast<long>(b) * g.g_bs, g.M * g.L_g * 4);
         const __amdgpu_buffer_rsrc_t xrs = uniform_rsrc(g.X + static_cast<long>(b) * g.x_bs, g.C_x * g.L_x * 4);
         const int l = l0 + g_pos_lane;
+        const bool g_in = g_rows_in && l0 + KC <= g.L_g;  // uniform
         for (int i = wave; i < 64; i += 2 * WG_WN) {
             const int m = m0 + i + 64 * g_row_lane;
-            const unsigned off = (m < g.M && l < g.L_g) ? static_cast<unsigned>(m * g.L_g + l) * 4u : OOB;
+            const unsigned off = (g_in || (m < g.M && l < g.L_g)) ? static_cast<unsigned>(m * g.L_g + l) * 4u : OOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(grs, smem + sb + i * GP, 4, static_cast<int>(off), 0, 0, 0);
         }
         const int x0 = l0 * s - g.p;
-        const int nitems = g.XR * g.segs;
-        for (int it = wave; it < nitems; it += 2 * WG_WN) {
-            const int r = it / g.segs, sg = it - r * g.segs;
+        const bool x_in = x0 >= 0 && x0 + g.span <= g.L_x;  // uniform
+        for (int r = wave; r < g.XR; r += 2 * WG_WN) {
             const int c = ci_lo + r;
-            const int pos = x0 + sg * 64 + lane;
-            const unsigned off = (c < g.C_x && pos >= 0 && pos < g.L_x)
-                                     ? static_cast<unsigned>(c * g.L_x + pos) * 4u : OOB;
-            if (sg * 64 + lane < g.span)  // exactly the row's span: rows pack at stride rs >= span
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + gsz + r * g.rs + sg * 64, 4,
-                                                         static_cast<int>(off), 0, 0, 0);
+            const bool c_in = c < g.C_x;  // uniform
+            int pos = x0 + lane;
+            for (int sg = 0; sg < g.segs; ++sg, pos += 64) {
+                const unsigned off = (c_in && (x_in || (pos >= 0 && pos < g.L_x)))
+                                         ? static_cast<unsigned>(c * g.L_x + pos) * 4u : OOB;
+                if (sg * 64 + lane < g.span)  // exactly the row's span: rows pack at stride rs >= span
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + gsz + r * g.rs + sg * 64, 4,
+                                                             static_cast<int>(off), 0, 0, 0);
+            }
         }
     };
 
@@ -779,41 +789,56 @@ void wgrad_gemm(WgradArgs g) {
             for (int kc = 0; kc < KC; ++kc) t += smem[row + kc];
             bsum += t;
         }
-        const int ga = sb + l32 * GP + wm * KC + hi;
-        const int xa0 = sb + gsz + xcol[0] + hi * s;
-        const int xa1 = sb + gsz + xcol[1] + hi * s;
-        auto ld = [&](int u, float& a0, float& a1, float& b0, float& b1) {
-            u = min(u, KC / 2 - 1);
-            int go = ga + 2 * u;
-            int xo0 = xa0 + 2 * u * s;
-            int xo1 = xa1 + 2 * u * s;
+        // group gi covers positions l0 + 8*gi + 4*h + e (e = 0..3) for lanes of
+        // half h: one ds_read_b128 per A row, four adjacent (stride s) input
+        // values per B column, then 16 MFMAs
+        const int ga = sb + l32 * GP + wm * KC + hi * 4;
+        const int xa0 = sb + gsz + xcol[0] + hi * 4 * s;
+        const int xa1 = sb + gsz + xcol[1] + hi * 4 * s;
+        auto ld = [&](int gi, float4 (&a)[2], float (&bv)[2][4]) {
+            gi = min(gi, KC / 8 - 1);
+            int go = ga + gi * 8;
+            int xo0 = xa0 + gi * 8 * s;
+            int xo1 = xa1 + gi * 8 * s;
             asm volatile("" : "+v"(go), "+v"(xo0), "+v"(xo1));
-            a0 = smem[go];
-            a1 = smem[go + 32 * GP];
-            b0 = smem[xo0];
-            b1 = smem[xo1];
+            a[0] = *reinterpret_cast<const float4*>(smem + go);
+            a[1] = *reinterpret_cast<const float4*>(smem + go + 32 * GP);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                bv[0][e] = smem[xo0 + e * s];
+                bv[1][e] = smem[xo1 + e * s];
+            }
         };
-        auto mm = [&](float a0, float a1, float b0, float b1) {
-            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+        auto mm = [&](const float4 (&a)[2], const float (&bv)[2][4]) {
+            const float a0[4] = {a[0].x, a[0].y, a[0].z, a[0].w};
+            const float a1[4] = {a[1].x, a[1].y, a[1].z, a[1].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[e], bv[0][e], acc[0][0], 0, 0, 0);
+                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[e], bv[1][e], acc[0][1], 0, 0, 0);
+                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[e], bv[0][e], acc[1][0], 0, 0, 0);
+                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[e], bv[1][e], acc[1][1], 0, 0, 0);
+            }
         };
         if (live) {
-            float pa0, pa1, pb0, pb1, qa0, qa1, qb0, qb1;
-            ld(0, pa0, pa1, pb0, pb1);
+            constexpr int NR = S1 ? 6 : 10;  // LDS reads per group
+            float4 pa[2], qa[2];
+            float pb[2][4], qb[2][4];
+            ld(0, pa, pb);
 #pragma unroll
-            for (int u = 0; u < KC / 2; u += 2) {
-                ld(u + 1, qa0, qa1, qb0, qb1);
-                mm(pa0, pa1, pb0, pb1);
-                ld(u + 2, pa0, pa1, pb0, pb1);
-                mm(qa0, qa1, qb0, qb1);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+            for (int gi = 0; gi < KC / 8; gi += 2) {
+                ld(gi + 1, qa, qb);
+                mm(pa, pb);
+                ld(gi + 2, pa, pb);
+                mm(qa, qb);
+                // (1 MFMA, 1 read) x NR, then the group's other MFMAs; twice
+                for (int r = 0; r < 2; ++r) {
+                    for (int i = 0; i < NR; ++i) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    }
+                    __builtin_amdgcn_sched_group_barrier(0x008, 16 - NR, 0);
+                }
             }
         }
         __builtin_amdgcn_s_waitcnt(0);  // this wave's staging loads landed
@@ -1174,9 +1199,11 @@ int kdec_conv1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
     Workspace A(ctx, static_cast<size_t>(tot) * sizeof(float));
     if (!A.p) return KDEC_ENOMEM;
     g.A = A.as<float>();
+    KDEC_CHECK(ctx, tot <= 0x7fffffffL && static_cast<long>(C_out) * C_in * k <= 0x7fffffffL,
+               "kdec_conv1d_fwd: weights too large");
     if (g.G > 0)
         hipLaunchKernelGGL(pack_octet, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), 0, C_in,
-                           C_out, k, 1, k, m_pad, tot, 1);
+                           C_out, k, 1, k, m_pad, static_cast<int>(tot), 1);
     else
         hipLaunchKernelGGL(pack_fwd, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), C_in,
                            C_out, k, g.cin_pad, m_pad, g.CK);
@@ -1212,9 +1239,11 @@ int kdec_conv1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
     Workspace A(ctx, static_cast<size_t>(tot) * sizeof(float));
     if (!A.p) return KDEC_ENOMEM;
     g.A = A.as<float>();
+    KDEC_CHECK(ctx, tot <= 0x7fffffffL && static_cast<long>(C_out) * C_in * k <= 0x7fffffffL,
+               "kdec_conv1d_dgrad: weights too large");
     if (g.G > 0)
         hipLaunchKernelGGL(pack_octet, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), 1, C_in,
-                           C_out, k, 1, k, m_pad, tot, 1);
+                           C_out, k, 1, k, m_pad, static_cast<int>(tot), 1);
     else
         hipLaunchKernelGGL(pack_dgrad, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), C_in,
                            C_out, k, g.cin_pad, m_pad, g.CK);
@@ -1255,20 +1284,22 @@ size_t wgrad_lds_bytes(int k, int s, int d) { return wgrad_layout(k, s, d).lds; 
 #ifndef WG_ROUNDS
 #define WG_ROUNDS 2
 #endif
-void wgrad_allow_large_lds() {
+const void* wgrad_kernel(bool s1) {
     static bool done = false;
     if (!done) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_gemm),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_gemm<true>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_gemm<false>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         done = true;
     }
+    return s1 ? reinterpret_cast<const void*>(&wgrad_gemm<true>) : reinterpret_cast<const void*>(&wgrad_gemm<false>);
 }
 
-int wgrad_splits(kdec_ctx* ctx, int total_chunks, long tiles, size_t lds) {
-    wgrad_allow_large_lds();
+int wgrad_splits(kdec_ctx* ctx, int total_chunks, long tiles, size_t lds, bool s1) {
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&wgrad_gemm), WG_NT,
-                                                     lds) != hipSuccess || per_cu < 1)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, wgrad_kernel(s1), WG_NT, lds) != hipSuccess ||
+        per_cu < 1)
         per_cu = 1;
     // The most whole rounds of resident blocks, up to WG_ROUNDS, whose splits
     // keep at least 8 chunks each (shorter runs spend more on the partial
@@ -1296,7 +1327,7 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
     // split the position chunks so that the blocks fill WG_ROUNDS rounds of
     // the resident slots
     const int splits = wgrad_splits(ctx, total_chunks, static_cast<long>(m_tiles) * n_tiles,
-                                    wgrad_lds_bytes(k, s, d));
+                                    wgrad_lds_bytes(k, s, d), s == 1);
     const long MN = static_cast<long>(M) * NN;
     Workspace P(ctx, static_cast<size_t>(splits) * MN * sizeof(float));
     Workspace Pb(ctx, db ? static_cast<size_t>(splits) * M * sizeof(float) : 0);
@@ -1325,8 +1356,10 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
         ProfScope ps(ctx, fam, 2.0 * N * M * static_cast<double>(L_g) * NN,
                      4.0 * (static_cast<double>(N) * C_x * L_x + static_cast<double>(N) * M * L_g +
                             static_cast<double>(M) * NN));
-        wgrad_allow_large_lds();
-        hipLaunchKernelGGL(wgrad_gemm, dim3(static_cast<unsigned>(blocks)), dim3(WG_NT), lds, ctx->stream, a);
+        void* args[] = {&a};
+        if (hipLaunchKernel(wgrad_kernel(s == 1), dim3(static_cast<unsigned>(blocks)), dim3(WG_NT), args, lds,
+                            ctx->stream) != hipSuccess)
+            return fail(ctx, KDEC_EHIP, std::string(fam) + ": launch failed");
         if (int rc2 = launch_check(ctx, fam)) return rc2;
     }
     hipLaunchKernelGGL(wgrad_reduce, dim3(grid1d(MN)), dim3(256), 0, ctx->stream, P.as<float>(), out, MN,
@@ -1390,9 +1423,11 @@ int kdec_convt1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
     const long ph = static_cast<long>(g.cin_pad) * kt * m_pad;
     Workspace A(ctx, static_cast<size_t>(ph) * stride * sizeof(float));
     if (!A.p) return KDEC_ENOMEM;
+    KDEC_CHECK(ctx, ph * stride <= 0x7fffffffL && static_cast<long>(C_out) * C_in * k <= 0x7fffffffL,
+               "kdec_convt1d_fwd: weights too large");
     if (g.G > 0)
         hipLaunchKernelGGL(pack_octet, dim3(grid1d(ph * stride)), dim3(256), 0, ctx->stream, W, A.as<float>(), 2,
-                           C_in, C_out, k, stride, kt, m_pad, ph, stride);
+                           C_in, C_out, k, stride, kt, m_pad, static_cast<int>(ph), stride);
     else
         hipLaunchKernelGGL(pack_convt_fwd, dim3(grid1d(ph * stride)), dim3(256), 0, ctx->stream, W,
                            A.as<float>(), C_in, C_out, k, stride, kt, g.cin_pad, m_pad, ph, g.CK);
