@@ -174,6 +174,8 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ref-steps", type=int, default=3, help="steps of the reference-semantics mode")
     ap.add_argument("--no-micro", action="store_true", help="skip the per-kernel-class microbenchmarks")
+    ap.add_argument("--serial", action="store_true",
+                    help="one stream (no harmonic-source / weight-grad overlap): per-family times without sharing")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB (3 times): the reference kernel for "
                          "scaling HBM byte counters")
@@ -202,6 +204,8 @@ def main(argv=None):
     shapes = model.param_shapes()
     params = synth.init_params(shapes)
     model.set_params(params)
+    if a.serial:
+        model.set_overlap(False)
     asr, F0, Nn, style, dA = make_inputs(cfg, B, T, "bench")
     dev = lambda x: torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
     t_asr, t_F0, t_N, t_style, t_dA = (dev(x) for x in (asr, F0, Nn, style, dA))
@@ -298,6 +302,7 @@ def main(argv=None):
                           "elementwise_gb_per_step": round(20.0 * elems / 1e9, 3)},
         "families_ms_per_step": {k: round(v["ms"] / a.steps, 3) for k, v in sorted(prof.items())},
         "reference_semantics": ref,
+        "streams": 1 if a.serial else 2,
     }
     if not a.no_micro:
         out["micro"] = micro_benches(ctx)

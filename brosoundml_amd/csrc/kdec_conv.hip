@@ -891,17 +891,20 @@ __global__ void wgrad_reduce(const float* P, float* out, long MN, int splits,
     }
 }
 
-// part[y, m] = sum of G[n, m, l] over the y-th slice of the (n, l) range;
-// grid (M, S). Reduced over y by bias_reduce in a fixed order.
-__global__ void bias_partial(const float* G, long g_bs, float* part, int N, int M, int L) {
-    const int m = blockIdx.x, y = blockIdx.y, S = gridDim.y;
-    const long tot = static_cast<long>(N) * L;
-    const long per = (tot + S - 1) / S;
-    const long i0 = y * per, i1 = min(tot, i0 + per);
+// part[y, m] = sum of G[n, m, l] over every utterance n and the y-th slice
+// [y*per, (y+1)*per) of the positions; grid (M, S). Each thread walks its
+// positions of each row with a fixed stride (no per-element index division)
+// and the block sums the thread partials in a fixed tree; bias_reduce then
+// adds the slices in order.
+__global__ void bias_partial(const float* G, long g_bs, float* part, int N, int M, int L, int per) {
+    const int m = blockIdx.x, y = blockIdx.y;
+    const int l0 = y * per, l1 = min(L, l0 + per);
     double acc = 0.0;
-    for (long i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
-        const long n = i / L, l = i - n * L;
-        acc += G[n * g_bs + static_cast<long>(m) * L + l];
+    for (int n = 0; n < N; ++n) {
+        const float* row = G + n * g_bs + static_cast<long>(m) * L;
+        float t = 0.0f;
+        for (int l = l0 + threadIdx.x; l < l1; l += blockDim.x) t += row[l];
+        acc += t;
     }
     __shared__ double red[256];
     red[threadIdx.x] = acc;
@@ -1375,13 +1378,16 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
 
 // db (M) += sum over (n, l) of G[n, m, l]
 static int bias_grad_only(kdec_ctx* ctx, const float* G, long g_bs, float* db, int N, int M, int L) {
-    long S = (static_cast<long>(N) * L + 32767) / 32768;
-    if (S > 64) S = 64;
+    // slices of at least 1024 positions, enough of them for ~4 blocks per CU
+    long S = std::min(cdiv(4L * ctx->num_cus, M), cdiv(L, 1024));
+    if (S > 256) S = 256;
     if (S < 1) S = 1;
+    const int per = static_cast<int>(cdiv(L, S));
+    S = cdiv(L, per);
     Workspace part(ctx, static_cast<size_t>(S) * M * sizeof(float));
     if (!part.p) return KDEC_ENOMEM;
     hipLaunchKernelGGL(bias_partial, dim3(M, static_cast<unsigned>(S)), dim3(256), 0, ctx->stream, G, g_bs,
-                       part.as<float>(), N, M, L);
+                       part.as<float>(), N, M, L, per);
     if (int rc = launch_check(ctx, "bias_partial")) return rc;
     hipLaunchKernelGGL(bias_reduce, dim3(static_cast<unsigned>(cdiv(M, 4))), dim3(256), 0, ctx->stream,
                        part.as<float>(), db, M, static_cast<int>(S));

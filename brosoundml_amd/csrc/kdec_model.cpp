@@ -66,6 +66,7 @@ struct kdec_model {
     // stream, forked after the inputs and joined before the generator, so it
     // overlaps the style projection and the backbone.
     kdec_ctx* side = nullptr;
+    bool overlap = true;  // use `side` at all (kdec_model_set_overlap)
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
 
     // DecoderLora adapters (off at lora_rank 0): A (units*rank, S), B
@@ -580,6 +581,14 @@ int kdec_model_forward(kdec_model* m, int N, int T, const float* asr, const floa
         if (har_in) {
             Tensor h = in(har_in, (m->n_fft + 2) * frames);
             m->har = h.clone();
+        } else if (!m->overlap) {
+            m->har = Tensor::empty_on(Device::HIP, N, (m->n_fft + 2) * frames);
+            const int rc = kdec_harmonic_source(m->ctx, F0, 2 * T, static_cast<float*>(m->har.data),
+                                                (m->n_fft + 2) * frames, N, 2 * T,
+                                                static_cast<const float*>(hs.l_linear.W.data),
+                                                static_cast<const float*>(hs.l_linear.b.data), hs.harmonic_num,
+                                                hs.sample_rate, hs.upsample_scale, hs.n_fft, hs.hop_size);
+            if (rc != KDEC_OK) return rc;
         } else {
             m->har = Tensor::empty_on(Device::HIP, N, (m->n_fft + 2) * frames);
             if (hipEventRecord(m->ev_fork, ms) != hipSuccess ||
@@ -660,7 +669,7 @@ int kdec_model_backward(kdec_model* m, const float* daudio, int wgrad, int dalph
                 } catch (...) {
                 }
             }
-        } lane(wg ? m->side : nullptr);
+        } lane(wg && m->overlap ? m->side : nullptr);
         bd::generator_backward(m->gen, m->genc, m->naff, m->raff, dA, dGenIn, m->dnaff, m->draff, wg);
         bd::decoder_backbone_backward(m->bb, m->bbc, m->bbaff, dGenIn, 1e-5f, m->dbbaff, wg);
         bd::join_wgrad_lane();
@@ -691,6 +700,12 @@ int kdec_model_backward(kdec_model* m, const float* daudio, int wgrad, int dalph
     } catch (const std::exception& e) {
         return fail(m, KDEC_EINVAL, e.what());
     }
+    return KDEC_OK;
+}
+
+int kdec_model_set_overlap(kdec_model* m, int on) {
+    if (!m) return KDEC_EINVAL;
+    m->overlap = on != 0;
     return KDEC_OK;
 }
 

@@ -231,6 +231,11 @@ class Model:
     def backward(self, daudio, wgrad=True, dalpha=True, dstyle=None):
         self._c(self.ctx.L.kdec_model_backward(self.h, ptr(daudio), int(wgrad), int(dalpha), ptr(dstyle)))
 
+    def set_overlap(self, on: bool):
+        """True (default): harmonic source and conv weight grads on a second
+        stream; False: every launch on the context's stream in program order."""
+        self._c(self.ctx.L.kdec_model_set_overlap(self.h, int(on)))
+
     # ─── DecoderLora adapters (kdec_model_lora_*) ───
     def lora_enable(self, rank: int, scale: float):
         self.lora_rank = rank

@@ -83,6 +83,12 @@ int kdec_model_forward(kdec_model* m, int N, int T, const float* asr, const floa
  * grads; dstyle (N, style_dim) may be NULL. The affine grads are always
  * produced (the reference semantics). */
 int kdec_model_backward(kdec_model* m, const float* daudio, int wgrad, int dalpha, float* dstyle);
+/* Stream overlap (no counterpart in the reference, whose calls are
+ * synchronous): on = 1 (the default) runs the harmonic source and the conv
+ * weight grads on a second stream beside the main chain; on = 0 keeps every
+ * launch on the context's stream, in program order. Results are identical
+ * either way (every reduction sums in a fixed order). */
+int kdec_model_set_overlap(kdec_model* m, int on);
 /* DecoderLora's adapters on every AdaIN unit (the adapter contract of
  * decoder_lora.h:63-77; the adapter_fwd / adapter_bwd sequence of
  * decoder_lora.cpp:184-207): (gamma, beta) = fc(style) + scale * B_i (g *

@@ -217,3 +217,31 @@ def test_in_model_harmonic_source_matches_op(ctx):
     a2 = m.forward(*t, T, har=har)
     torch.cuda.synchronize()
     assert torch.equal(a1, a2)
+
+
+def test_single_stream_equals_overlapped(ctx):
+    # kdec_model_set_overlap(0) keeps every launch on one stream; with the
+    # default two-stream schedule the waveform, d(style) and every grad are
+    # the same bits (all reductions sum in a fixed order).
+    from brosoundml_amd import native
+    cfg, N, T = C.SMALL, 2, 6
+    m = native.Model(ctx, cfg)
+    shapes = m.param_shapes()
+    m.set_params(synth.init_params(shapes))
+    asr, F0, Nn, style, dA = inputs(cfg, N, T, "gm.ovl")
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    t = [dev(a) for a in (asr, F0, Nn, style)]
+    d = dev(dA)
+    res = []
+    for on in (True, False):
+        m.set_overlap(on)
+        m.zero_grad()
+        audio = m.forward(*t, T).clone()
+        ds = torch.empty_like(t[3])
+        m.backward(d, wgrad=True, dalpha=True, dstyle=ds)
+        torch.cuda.synchronize()
+        res.append((audio.cpu().numpy(), ds.cpu().numpy(), {n: m.grad(n, s) for n, s in shapes.items()}))
+    np.testing.assert_array_equal(res[0][0], res[1][0])
+    np.testing.assert_array_equal(res[0][1], res[1][1])
+    for n in shapes:
+        np.testing.assert_array_equal(res[0][2][n], res[1][2][n], err_msg=n)
