@@ -670,6 +670,9 @@ constexpr int WG_BN = 64 * WG_WN;        // n columns per wgrad block
 // aligned for ds_read_b128, and 16 consecutive m of one such read cover all
 // 64 banks once.
 constexpr int GP = 2 * KC + 4;
+// Packed input-window DMA instructions per wave on the fast staging path
+// (windows of up to WG_XI * 8 * 64 floats; larger ones take the checked path).
+constexpr int WG_XI = 8;
 
 struct WgradArgs {
     const float* X;      // correlation input  [n][C_x][L_x]
@@ -715,7 +718,7 @@ void wgrad_gemm(WgradArgs g) {
     const int k = g.k, s = S1 ? 1 : g.s, d = g.d;
     const int ci_lo = n0 / k;
     const int gsz = 64 * GP;
-    const int stage = gsz + g.XR * g.rs;
+    const int stage = gsz + (g.XR * g.rs + 63) / 64 * 64;  // as wgrad_layout
     const bool do_bias = g.Pb && nt == 0;
     // a wave whose 64 columns all lie past NN (the last n-tile) only stages
     const bool live = n0 + wn * 64 < g.NN;
@@ -736,32 +739,67 @@ void wgrad_gemm(WgradArgs g) {
     // of range get an out-of-bounds offset and stage as zeros. Wave w stages
     // G row pairs w, w + 8, ... and input rows w, w + 8, ... (all segments of
     // each), with the range checks skipped for chunks wholly inside.
-    const bool g_rows_in = m0 + BM <= g.M;
+    // Fast staging plan for chunks wholly inside their rows: per-lane byte
+    // offsets at chunk position 0, fixed for the block, with the chunk's start
+    // in the scalar offset, so one DMA costs one M0 write and the load. The
+    // input window is staged packed: instruction j fills LDS floats
+    // [64j, 64j + 64) of the [row][rs] window, lanes past a row's span (and
+    // rows past C_x) read out of range and stage zeros.
+    constexpr int GI = 64 / (2 * WG_WN);  // G pair rows per wave
+    const bool g_rows_in = m0 + BM <= g.M;  // uniform: whole m-tile (else the checked path)
+    // pair row wave + 8j of this lane: g_off + j * 8 * L_g * 4
+    const unsigned g_off = static_cast<unsigned>((m0 + wave + 64 * g_row_lane) * g.L_g + g_pos_lane) * 4u;
+    const unsigned g_step = static_cast<unsigned>(2 * WG_WN * g.L_g) * 4u;
+    const int x_slots = g.XR * g.rs;
+    const int nxi = (x_slots + 63) / 64;  // packed-window instructions
+    const bool fast_x = nxi <= WG_XI * 2 * WG_WN;  // uniform per launch
+    unsigned x_off[WG_XI];
+#pragma unroll
+    for (int j = 0; j < WG_XI; ++j) {
+        const int slot = (wave + 2 * WG_WN * j) * 64 + lane;
+        const int r = slot / g.rs, pos = slot - r * g.rs;
+        const int c = ci_lo + r;
+        x_off[j] = (slot < x_slots && pos < g.span && c < g.C_x) ? static_cast<unsigned>(c * g.L_x + pos) * 4u : OOB;
+    }
     auto issue = [&](int ch, int sb) {
         const int b = ch / g.chunks_per_n;
         const int l0 = (ch - b * g.chunks_per_n) * KC;
         const __amdgpu_buffer_rsrc_t grs = uniform_rsrc(g.G + static_cast<long>(b) * g.g_bs, g.M * g.L_g * 4);
         const __amdgpu_buffer_rsrc_t xrs = uniform_rsrc(g.X + static_cast<long>(b) * g.x_bs, g.C_x * g.L_x * 4);
-        const int l = l0 + g_pos_lane;
-        const bool g_in = g_rows_in && l0 + KC <= g.L_g;  // uniform
+        const int x0 = l0 * s - g.p;
+        if (fast_x && x0 >= 0 && x0 + g.span <= g.L_x) {  // uniform
+#pragma unroll
+            for (int j = 0; j < WG_XI; ++j)
+                if (wave + 2 * WG_WN * j < nxi)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + gsz + (wave + 2 * WG_WN * j) * 64, 4,
+                                                             static_cast<int>(x_off[j]), x0 * 4, 0, 0);
+        } else {
+            const bool x_in = x0 >= 0 && x0 + g.span <= g.L_x;  // uniform
+            for (int r = wave; r < g.XR; r += 2 * WG_WN) {
+                const int c = ci_lo + r;
+                const bool c_in = c < g.C_x;  // uniform
+                int pos = x0 + lane;
+                for (int sg = 0; sg < g.segs; ++sg, pos += 64) {
+                    const unsigned off = (c_in && (x_in || (pos >= 0 && pos < g.L_x)))
+                                             ? static_cast<unsigned>(c * g.L_x + pos) * 4u : OOB;
+                    if (sg * 64 + lane < g.span)  // exactly the row's span: rows pack at stride rs >= span
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + gsz + r * g.rs + sg * 64, 4,
+                                                                 static_cast<int>(off), 0, 0, 0);
+                }
+            }
+        }
+        if (g_rows_in && l0 + KC <= g.L_g) {  // uniform
+#pragma unroll
+            for (int j = 0; j < GI; ++j)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(grs, smem + sb + (wave + 2 * WG_WN * j) * GP, 4,
+                                                         static_cast<int>(g_off + j * g_step), l0 * 4, 0, 0);
+            return;
+        }
+        const int l = l0 + g_pos_lane;  // a partial m-tile or the last chunk of a row: checked
         for (int i = wave; i < 64; i += 2 * WG_WN) {
             const int m = m0 + i + 64 * g_row_lane;
-            const unsigned off = (g_in || (m < g.M && l < g.L_g)) ? static_cast<unsigned>(m * g.L_g + l) * 4u : OOB;
+            const unsigned off = (m < g.M && l < g.L_g) ? static_cast<unsigned>(m * g.L_g + l) * 4u : OOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(grs, smem + sb + i * GP, 4, static_cast<int>(off), 0, 0, 0);
-        }
-        const int x0 = l0 * s - g.p;
-        const bool x_in = x0 >= 0 && x0 + g.span <= g.L_x;  // uniform
-        for (int r = wave; r < g.XR; r += 2 * WG_WN) {
-            const int c = ci_lo + r;
-            const bool c_in = c < g.C_x;  // uniform
-            int pos = x0 + lane;
-            for (int sg = 0; sg < g.segs; ++sg, pos += 64) {
-                const unsigned off = (c_in && (x_in || (pos >= 0 && pos < g.L_x)))
-                                         ? static_cast<unsigned>(c * g.L_x + pos) * 4u : OOB;
-                if (sg * 64 + lane < g.span)  // exactly the row's span: rows pack at stride rs >= span
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + gsz + r * g.rs + sg * 64, 4,
-                                                             static_cast<int>(off), 0, 0, 0);
-            }
         }
     };
 
@@ -1278,7 +1316,9 @@ WgradLayout wgrad_layout(int k, int s, int d) {
         rs += ((want - rs % 32) % 32 + 32) % 32;
     }
     w.rs = static_cast<int>(rs);
-    w.lds = 2 * (static_cast<size_t>(64) * GP + static_cast<size_t>(w.XR) * w.rs) * sizeof(float);
+    // the packed staging writes whole 64-float runs: round the window up
+    const size_t xsz = (static_cast<size_t>(w.XR) * w.rs + 63) / 64 * 64;
+    w.lds = 2 * (static_cast<size_t>(64) * GP + xsz) * sizeof(float);
     return w;
 }
 
