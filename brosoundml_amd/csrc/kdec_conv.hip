@@ -1192,12 +1192,16 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
     double bytes = 4.0 * (static_cast<double>(N) * g.C_in * g.L_in + static_cast<double>(g.C_in) * kk_all * g.C_out +
                           static_cast<double>(N) * g.C_out * g.L_y * (g.beta != 0.0f ? 2 : 1));
     if (g.R) bytes += 4.0 * static_cast<double>(N) * g.C_out * g.L_y;
-    ProfScope ps(ctx, fam, flops, bytes);
-    void* args[] = {&g};
-    if (hipLaunchKernel(kern, dim3(static_cast<unsigned>(blocks)), dim3(NT), args, lds, ctx->stream) != hipSuccess)
-        return fail(ctx, KDEC_EHIP, std::string(fam) + ": launch failed");
-    if (int rc = launch_check(ctx, fam)) return rc;
+    {  // the GEMM kernel alone (the profile's FLOP rate is this launch's)
+        ProfScope ps(ctx, fam, flops, bytes);
+        void* args[] = {&g};
+        if (hipLaunchKernel(kern, dim3(static_cast<unsigned>(blocks)), dim3(NT), args, lds, ctx->stream) !=
+            hipSuccess)
+            return fail(ctx, KDEC_EHIP, std::string(fam) + ": launch failed");
+        if (int rc = launch_check(ctx, fam)) return rc;
+    }
     if (g.split_tiles > 0) {
+        ProfScope ps(ctx, "tile_reduce", 0.0);
         hipLaunchKernelGGL(tile_reduce, dim3(BM * BN / 256, g.split_tiles), dim3(256), 0, ctx->stream, g);
         return launch_check(ctx, "tile_reduce");
     }
@@ -1405,6 +1409,7 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
             return fail(ctx, KDEC_EHIP, std::string(fam) + ": launch failed");
         if (int rc2 = launch_check(ctx, fam)) return rc2;
     }
+    ProfScope ps(ctx, "wgrad_reduce", 0.0);
     hipLaunchKernelGGL(wgrad_reduce, dim3(grid1d(MN)), dim3(256), 0, ctx->stream, P.as<float>(), out, MN,
                        splits, 0, M, NN);
     if (int rc = launch_check(ctx, "wgrad_reduce")) return rc;
