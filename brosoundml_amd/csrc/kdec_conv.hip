@@ -249,11 +249,9 @@ void conv_gemm(GemmArgs g) {
 
     const int KR = CK * k;                            // weight rows per chunk
     const int span = (BN - 1) * s + (k - 1) * d + 1;  // staged input window
-    // Stride-1 correlations stage input rows 16 B per lane (256 positions per
-    // instruction) at a row stride that is a multiple of 256; others 4 B per
-    // lane at a multiple of 64.
-    const bool wide = s == 1;
-    const int span_p = wide ? ((span + 3 + 255) & ~255) : ((span + 63) & ~63);  // LDS row stride
+    // Input rows are staged 16 B per lane (256 positions per instruction) at
+    // a row stride that is a multiple of 256.
+    const int span_p = (span + 3 + 255) & ~255;  // LDS row stride
     const int segs = span_p >> 6;
     const int stage = KR * BM + CK * span_p;
     const float* Xb = g.X + static_cast<long>(b) * g.x_bs;
@@ -267,7 +265,7 @@ void conv_gemm(GemmArgs g) {
     // is staged from the 16-B aligned position x0 - dc, dc = (c*L_in + x0 +
     // the base's float offset) mod 4, and its reads shift by dc. Lm = xm = 0
     // elsewhere makes every shift 0.
-    const bool x4 = wide && x0 >= 3 && x0 + span <= g.L_in;  // uniform per tile
+    const bool x4 = x0 >= 3 && x0 + span <= g.L_in;  // uniform per tile
     const int base_f = static_cast<int>((reinterpret_cast<unsigned long long>(Xb) >> 2) & 3);
     const int Lm = x4 ? (g.L_in & 3) : 0;
     const int xm = x4 ? ((base_f + x0) & 3) : 0;
@@ -670,8 +668,7 @@ constexpr int WG_BN = 64 * WG_WN;        // n columns per wgrad block
 // aligned for ds_read_b128, and 16 consecutive m of one such read cover all
 // 64 banks once.
 constexpr int GP = 2 * KC + 4;
-// Packed input-window DMA instructions per wave on the fast staging path
-// (windows of up to WG_XI * 8 * 64 floats; larger ones take the checked path).
+// Held packed input-window offsets per wave on the stride-1 fast path.
 constexpr int WG_XI = 8;
 
 struct WgradArgs {
@@ -750,29 +747,53 @@ void wgrad_gemm(WgradArgs g) {
     // pair row wave + 8j of this lane: g_off + j * 8 * L_g * 4
     const unsigned g_off = static_cast<unsigned>((m0 + wave + 64 * g_row_lane) * g.L_g + g_pos_lane) * 4u;
     const unsigned g_step = static_cast<unsigned>(2 * WG_WN * g.L_g) * 4u;
-    const int x_slots = g.XR * g.rs;
-    const int nxi = (x_slots + 63) / 64;  // packed-window instructions
-    const bool fast_x = nxi <= WG_XI * 2 * WG_WN;  // uniform per launch
-    unsigned x_off[WG_XI];
+    // Stride 1: the wave's packed-instruction offsets are held (windows of up
+    // to WG_XI * 8 * 64 floats; larger ones take the checked path). Strided:
+    // this lane's slot of the wave's first instruction as (row, position),
+    // each further instruction of the wave 8 * 64 slots on.
+    const int nxi = (g.XR * g.rs + 63) / 64;  // packed-window instructions
+    const bool fast_x = !S1 || nxi <= WG_XI * 2 * WG_WN;  // uniform per launch
+    unsigned x_off[S1 ? WG_XI : 1];
+    if (S1) {
 #pragma unroll
-    for (int j = 0; j < WG_XI; ++j) {
-        const int slot = (wave + 2 * WG_WN * j) * 64 + lane;
-        const int r = slot / g.rs, pos = slot - r * g.rs;
-        const int c = ci_lo + r;
-        x_off[j] = (slot < x_slots && pos < g.span && c < g.C_x) ? static_cast<unsigned>(c * g.L_x + pos) * 4u : OOB;
+        for (int j = 0; j < WG_XI; ++j) {
+            const int slot = (wave + 2 * WG_WN * j) * 64 + lane;
+            const int r = slot / g.rs, pos = slot - r * g.rs;
+            const int c = ci_lo + r;
+            x_off[S1 ? j : 0] = (r < g.XR && pos < g.span && c < g.C_x)
+                                    ? static_cast<unsigned>(c * g.L_x + pos) * 4u : OOB;
+        }
     }
+    const int xs0 = wave * 64 + lane;
+    const int xr0 = xs0 / g.rs, xp0 = xs0 - xr0 * g.rs;
+    const int xqd = (2 * WG_WN * 64) / g.rs, xrd = (2 * WG_WN * 64) - xqd * g.rs;
     auto issue = [&](int ch, int sb) {
         const int b = ch / g.chunks_per_n;
         const int l0 = (ch - b * g.chunks_per_n) * KC;
         const __amdgpu_buffer_rsrc_t grs = uniform_rsrc(g.G + static_cast<long>(b) * g.g_bs, g.M * g.L_g * 4);
         const __amdgpu_buffer_rsrc_t xrs = uniform_rsrc(g.X + static_cast<long>(b) * g.x_bs, g.C_x * g.L_x * 4);
         const int x0 = l0 * s - g.p;
-        if (fast_x && x0 >= 0 && x0 + g.span <= g.L_x) {  // uniform
+        if (S1 && fast_x && x0 >= 0 && x0 + g.span <= g.L_x) {  // uniform
 #pragma unroll
             for (int j = 0; j < WG_XI; ++j)
                 if (wave + 2 * WG_WN * j < nxi)
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + gsz + (wave + 2 * WG_WN * j) * 64, 4,
-                                                             static_cast<int>(x_off[j]), x0 * 4, 0, 0);
+                                                             static_cast<int>(x_off[S1 ? j : 0]), x0 * 4, 0, 0);
+        } else if (!S1 && x0 >= 0 && x0 + g.span <= g.L_x) {  // uniform
+            int r = xr0, pp = xp0;
+            for (int jj = wave; jj < nxi; jj += 2 * WG_WN) {
+                const int c = ci_lo + r;
+                const unsigned off = (r < g.XR && pp < g.span && c < g.C_x)
+                                         ? static_cast<unsigned>(c * g.L_x + pp) * 4u : OOB;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + gsz + jj * 64, 4, static_cast<int>(off),
+                                                         x0 * 4, 0, 0);
+                pp += xrd;
+                r += xqd;
+                if (pp >= g.rs) {
+                    pp -= g.rs;
+                    ++r;
+                }
+            }
         } else {
             const bool x_in = x0 >= 0 && x0 + g.span <= g.L_x;  // uniform
             for (int r = wave; r < g.XR; r += 2 * WG_WN) {
@@ -1039,7 +1060,7 @@ __global__ void pool_wgrad(const float* X, long x_bs, const float* dY, long dy_b
 // correlation of kk taps at stride ss and dilation dd.
 size_t conv_lds_bytes(int CK, int kk, int ss, int dd) {
     const long span = static_cast<long>(BN - 1) * ss + static_cast<long>(kk - 1) * dd + 1;
-    const long span_p = ss == 1 ? (span + 3 + 255) / 256 * 256 : (span + 63) / 64 * 64;  // as conv_gemm
+    const long span_p = (span + 3 + 255) / 256 * 256;  // as conv_gemm
     return 2 * (static_cast<size_t>(CK) * kk * BM + static_cast<size_t>(CK) * span_p) * sizeof(float);
 }
 
