@@ -11,6 +11,7 @@
 #include "kdec.h"
 #include "kdec_internal.hpp"
 #include "kdec_model.h"
+#include "brosoundml/decoder_lora.h"
 #include "kokoro_decoder_backward.h"
 
 namespace bt = brotensor;
@@ -713,5 +714,161 @@ const float* kdec_model_har(const kdec_model* m) { return m ? static_cast<const 
 const float* kdec_model_gen_in(const kdec_model* m) {
     return m ? static_cast<const float*>(m->gen_in.data) : nullptr;
 }
+
+// ─── DecoderLora over the model's weights ───────────────────────────────────
+
+struct kdec_dlora {
+    kdec_model* m = nullptr;
+    brosoundml::DecoderLora lora;
+    Tensor audio, cond, har;
+    int N = 0, T = 0;
+};
+
+namespace {
+int dlora_fail(kdec_dlora* d, int code, const std::string& msg) {
+    if (d && d->m) return fail(d->m, code, msg);
+    return code;
+}
+}  // namespace
+
+int kdec_dlora_create(kdec_model* m, int rank, float scale, unsigned long long seed, kdec_dlora** out) {
+    if (!m || !out || rank <= 0) return KDEC_EINVAL;
+    try {
+        bt::set_runtime(m->ctx);
+        auto* d = new kdec_dlora();
+        d->m = m;
+        d->lora = brosoundml::DecoderLora::make(m->bb, m->gen, rank, scale, Device::HIP, seed);
+        *out = d;
+    } catch (const std::exception& e) {
+        return fail(m, KDEC_EINVAL, e.what());
+    }
+    return KDEC_OK;
+}
+
+int kdec_dlora_destroy(kdec_dlora* d) {
+    if (!d) return KDEC_EINVAL;
+    bt::set_runtime(d->m->ctx);
+    hipStreamSynchronize(static_cast<hipStream_t>(kdec_get_stream(d->m->ctx)));
+    delete d;
+    return KDEC_OK;
+}
+
+int kdec_dlora_forward(kdec_dlora* d, int N, int T, const float* asr, const float* F0, const float* Nn,
+                       const float* ref_s, long ref_bs, const float* har, const float* cond, float* audio) {
+    if (!d || N <= 0 || T <= 0 || !asr || !F0 || !Nn || !ref_s || !cond || !audio) return KDEC_EINVAL;
+    kdec_model* m = d->m;
+    if (ref_bs < m->style_dim) return dlora_fail(d, KDEC_EINVAL, "kdec_dlora_forward: ref_s stride below style_dim");
+    try {
+        bt::set_runtime(m->ctx);
+        int frames = 0, alen = 0;
+        kdec_model_lengths(m, T, nullptr, &frames, &alen);
+        const int har_cols = (m->n_fft + 2) * frames;
+        auto in = [&](const float* p, int cols) { return Tensor::view(Device::HIP, const_cast<float*>(p), N, cols); };
+        Tensor h;
+        if (har) {
+            h = in(har, har_cols);
+        } else {  // HarmonicSource::forward on the model's l_linear
+            d->har = Tensor::empty_on(Device::HIP, N, har_cols);
+            const auto& hs = m->hs;
+            if (int rc = kdec_harmonic_source(m->ctx, F0, 2 * T, d->har.f32(), har_cols, N, 2 * T,
+                                              static_cast<const float*>(hs.l_linear.W.data),
+                                              static_cast<const float*>(hs.l_linear.b.data), hs.harmonic_num,
+                                              hs.sample_rate, hs.upsample_scale, hs.n_fft, hs.hop_size))
+                return rc;
+            h = d->har;
+        }
+        const Tensor asr_t = in(asr, m->asr_dim * T), F0_t = in(F0, 2 * T), N_t = in(Nn, 2 * T);
+        const Tensor rs = Tensor::view(Device::HIP, const_cast<float*>(ref_s), N, m->style_dim, bt::Dtype::FP32, ref_bs);
+        brosoundml::DecoderLoraContext c{&asr_t, &F0_t, &N_t, &rs, &h, T, frames};
+        d->cond = Tensor::view(Device::HIP, const_cast<float*>(cond), N, d->lora.gate().in_dim);
+        d->lora.forward(m->bb, m->gen, c, d->cond, d->audio);
+        d->N = N;
+        d->T = T;
+        if (hipMemcpyAsync(audio, d->audio.data, static_cast<size_t>(N) * alen * sizeof(float),
+                           hipMemcpyDeviceToDevice, static_cast<hipStream_t>(kdec_get_stream(m->ctx))) != hipSuccess)
+            return dlora_fail(d, KDEC_EHIP, "kdec_dlora_forward: output copy");
+    } catch (const std::exception& e) {
+        return dlora_fail(d, KDEC_EINVAL, e.what());
+    }
+    return KDEC_OK;
+}
+
+int kdec_dlora_backward(kdec_dlora* d, const float* daudio) {
+    if (!d || !daudio || d->N == 0) return KDEC_EINVAL;
+    kdec_model* m = d->m;
+    try {
+        bt::set_runtime(m->ctx);
+        int alen = 0;
+        kdec_model_lengths(m, d->T, nullptr, nullptr, &alen);
+        const Tensor dA = Tensor::view(Device::HIP, const_cast<float*>(daudio), d->N, alen);
+        d->lora.backward(m->bb, m->gen, d->cond, dA);
+    } catch (const std::exception& e) {
+        return dlora_fail(d, KDEC_EINVAL, e.what());
+    }
+    return KDEC_OK;
+}
+
+int kdec_dlora_zero_grad(kdec_dlora* d) {
+    if (!d) return KDEC_EINVAL;
+    try {
+        bt::set_runtime(d->m->ctx);
+        d->lora.zero_grad();
+    } catch (const std::exception& e) {
+        return dlora_fail(d, KDEC_EINVAL, e.what());
+    }
+    return KDEC_OK;
+}
+
+int kdec_dlora_adam_step(kdec_dlora* d, float lr, float beta1, float beta2, float eps) {
+    if (!d) return KDEC_EINVAL;
+    try {
+        bt::set_runtime(d->m->ctx);
+        d->lora.adam_step(lr, beta1, beta2, eps);
+    } catch (const std::exception& e) {
+        return dlora_fail(d, KDEC_EINVAL, e.what());
+    }
+    return KDEC_OK;
+}
+
+int kdec_dlora_save(kdec_dlora* d, const char* path) {
+    if (!d || !path) return KDEC_EINVAL;
+    try {
+        bt::set_runtime(d->m->ctx);
+        d->lora.save(path);
+    } catch (const std::exception& e) {
+        return dlora_fail(d, KDEC_EINVAL, e.what());
+    }
+    return KDEC_OK;
+}
+
+int kdec_dlora_load(kdec_dlora* d, const char* path) {
+    if (!d || !path) return KDEC_EINVAL;
+    try {
+        bt::set_runtime(d->m->ctx);
+        d->lora.load(path);
+    } catch (const std::exception& e) {
+        return dlora_fail(d, KDEC_EINVAL, e.what());
+    }
+    return KDEC_OK;
+}
+
+float* kdec_dlora_ptr(kdec_dlora* d, int which, int* rows, int* cols) {
+    if (!d) return nullptr;
+    const Tensor* t = nullptr;
+    auto& g = d->lora.gate();
+    switch (which) {
+        case 0: case 1: case 2: case 3: t = &d->lora.stacked(which); break;
+        case 4: t = &g.W1; break;
+        case 5: t = &g.W2; break;
+        case 6: t = &g.dW1; break;
+        case 7: t = &g.dW2; break;
+        default: return nullptr;
+    }
+    if (rows) *rows = t->rows;
+    if (cols) *cols = t->cols;
+    return t->f32();
+}
+
+float kdec_dlora_scale(const kdec_dlora* d) { return d ? d->lora.scale() : 0.0f; }
 
 }  // extern "C"

@@ -291,3 +291,85 @@ class Model:
 
     def har_ptr(self):
         return self.ctx.L.kdec_model_har(self.h)
+
+
+class DecoderLora:
+    """DecoderLora (kdec_dlora_*) over a Model's frozen weights: the LoRA on
+    every AdaIN unit's style projection with the shared conditioning gate,
+    Adam state and the ELRA1 checkpoint."""
+
+    NAMES = {"A": 0, "B": 1, "dA": 2, "dB": 3, "W1": 4, "W2": 5, "dW1": 6, "dW2": 7}
+
+    def __init__(self, model: "Model", rank: int, scale: float, seed: int = 0):
+        self.model = model
+        self.ctx = model.ctx
+        h = ctypes.c_void_p()
+        model._c(self.ctx.L.kdec_dlora_create(model.h, rank, scale, seed, ctypes.byref(h)))
+        self.h = h
+        self.rank = rank
+
+    def __del__(self):
+        try:
+            if getattr(self, "h", None):
+                self.ctx.L.kdec_dlora_destroy(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+    def _c(self, rc):
+        return self.model._c(rc)
+
+    def tensor(self, name):
+        """(device pointer, rows, cols) of A, B, dA, dB, W1, W2, dW1 or dW2."""
+        r, c = ctypes.c_int(), ctypes.c_int()
+        p = self.ctx.L.kdec_dlora_ptr(self.h, self.NAMES[name], ctypes.cast(ctypes.pointer(r), ctypes.c_void_p),
+                                      ctypes.cast(ctypes.pointer(c), ctypes.c_void_p))
+        if not p:
+            raise KdecError(f"kdec_dlora_ptr({name}) failed")
+        return p, r.value, c.value
+
+    def get(self, name):
+        import torch
+        p, r, c = self.tensor(name)
+        torch.cuda.synchronize()
+        t = torch.empty((r, c), dtype=torch.float32, device="cuda")
+        self.ctx.check(self.ctx.L.kdec_axpby(self.ctx.h, 1.0, ctypes.c_void_p(p), c, 0.0, None, 0, ptr(t), c, r, c))
+        return t.cpu().numpy()
+
+    def set(self, name, value):
+        import numpy as np
+        import torch
+        p, r, c = self.tensor(name)
+        v = np.ascontiguousarray(value, np.float32).reshape(r, c)
+        t = torch.from_numpy(v).cuda()
+        self.ctx.check(self.ctx.L.kdec_axpby(self.ctx.h, 1.0, ptr(t), c, 0.0, None, 0, ctypes.c_void_p(p), c, r, c))
+        torch.cuda.synchronize()
+
+    def forward(self, asr, F0, Nn, ref_s, T, cond, har=None, audio=None):
+        import torch
+        N = asr.shape[0]
+        if audio is None:
+            audio = torch.empty(N, self.model.lengths(T)["audio"], device=asr.device, dtype=torch.float32)
+        self._keep = (asr, F0, Nn, ref_s, cond, har)
+        self._c(self.ctx.L.kdec_dlora_forward(self.h, N, T, ptr(asr), ptr(F0), ptr(Nn), ptr(ref_s),
+                                              ref_s.stride(0), ptr(har), ptr(cond), ptr(audio)))
+        return audio
+
+    def backward(self, daudio):
+        self._c(self.ctx.L.kdec_dlora_backward(self.h, ptr(daudio)))
+
+    def zero_grad(self):
+        self._c(self.ctx.L.kdec_dlora_zero_grad(self.h))
+
+    def adam_step(self, lr, beta1=0.9, beta2=0.999, eps=1e-8):
+        self._c(self.ctx.L.kdec_dlora_adam_step(self.h, lr, beta1, beta2, eps))
+
+    def save(self, path):
+        self._c(self.ctx.L.kdec_dlora_save(self.h, os.fsencode(path)))
+
+    def load(self, path):
+        self._c(self.ctx.L.kdec_dlora_load(self.h, os.fsencode(path)))
+
+    @property
+    def scale(self):
+        return self.ctx.L.kdec_dlora_scale(self.h)

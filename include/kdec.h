@@ -285,6 +285,31 @@ int kdec_lora_proj_bwd(kdec_ctx* ctx, const float* W, const float* A,
                        long dstyle_bs, float beta, float* dW, float* db,
                        float* dA, float* dB, float* dG, int N, int rows, int S);
 
+/* DecoderLora's conditioning gate g(v) = W2 tanh(W1 v), bias-free
+ * (ConditioningGate::forward, decoder_lora.cpp:56-66): for N condition
+ * vectors v (in_dim each, batch stride v_bs) writes act = tanh(W1 v)
+ * (N, hidden; kept for the backward) and g (N, rank) at batch stride g_bs.
+ * W1 (hidden, in_dim), W2 (rank, hidden). N * hidden <= 16384. */
+int kdec_lora_gate_fwd(kdec_ctx* ctx, const float* W1, const float* W2,
+                       const float* v, long v_bs, int N, int in_dim,
+                       int hidden, int rank, float* act, float* g,
+                       long g_bs);
+/* Its adjoint (ConditioningGate::backward, decoder_lora.cpp:68-80): with the
+ * forward's act and the gate grad dG (N, rank at batch stride dg_bs),
+ * accumulates dW2 += dG^T act and dW1 += ((1 - act^2) * (dG W2))^T v. The
+ * condition is an input, not a trainable: no dv. */
+int kdec_lora_gate_bwd(kdec_ctx* ctx, const float* W2, const float* v,
+                       long v_bs, const float* act, const float* dG,
+                       long dg_bs, int N, int in_dim, int hidden, int rank,
+                       float* dW1, float* dW2);
+/* One Adam step over n parameters (bt::adam_step as DecoderLora::adam_step
+ * calls it, decoder_lora.cpp:305-314): m = b1 m + (1-b1) g,
+ * v = b2 v + (1-b2) g^2, p -= lr (m / (1 - b1^step)) /
+ * (sqrt(v / (1 - b2^step)) + eps). step >= 1. */
+int kdec_adam_step(kdec_ctx* ctx, float* p, const float* g, float* m,
+                   float* v, long n, float lr, float beta1, float beta2,
+                   float eps, int step);
+
 #ifdef __cplusplus
 }
 #endif

@@ -106,6 +106,36 @@ float* kdec_model_lora_ptr(kdec_model* m, int which);
  * keeps both alive. */
 int kdec_model_lora_gate(kdec_model* m, const float* g, long g_bs, float* dG);
 
+/* ─── DecoderLora (decoder_lora.h:97-181, decoder_lora.cpp:108-396) ───
+ * The trainable LoRA over every AdaIN unit's style projection with the
+ * shared conditioning gate g(v) = W2 tanh(W1 v) (in_dim 3, hidden 16,
+ * rank wide), Adam state and the ELRA1 checkpoint, over this model's frozen
+ * weights: DecoderLora::make / forward / backward / zero_grad / adam_step /
+ * save / load. Units are in kdec_model_unit_name order. Errors read through
+ * kdec_last_error of the model's context. */
+typedef struct kdec_dlora kdec_dlora;
+/* A, B Glorot-uniform from `seed`, gate W2 zero (the base decoder exactly
+ * at init and for cond = 0). */
+int kdec_dlora_create(kdec_model* m, int rank, float scale, unsigned long long seed, kdec_dlora** out);
+int kdec_dlora_destroy(kdec_dlora* d);
+/* DecoderLora::forward over the model's weights: device pointers, N
+ * utterances; ref_s (N rows at stride ref_bs >= style_dim, the style is the
+ * first style_dim values), cond (N, 3), har (N, (n_fft+2)*frames) or NULL
+ * to run the model's harmonic source on F0; audio (N, audio_len). */
+int kdec_dlora_forward(kdec_dlora* d, int N, int T, const float* asr, const float* F0, const float* Nn,
+                       const float* ref_s, long ref_bs, const float* har, const float* cond, float* audio);
+/* DecoderLora::backward of the last forward (its cond): accumulates dA, dB,
+ * the gate's dW1, dW2. */
+int kdec_dlora_backward(kdec_dlora* d, const float* daudio);
+int kdec_dlora_zero_grad(kdec_dlora* d);
+int kdec_dlora_adam_step(kdec_dlora* d, float lr, float beta1, float beta2, float eps);
+int kdec_dlora_save(kdec_dlora* d, const char* path);
+int kdec_dlora_load(kdec_dlora* d, const char* path);
+/* Device tensors: 0 A (units*rank, S), 1 B (affine_rows, rank), 2 dA, 3 dB,
+ * 4 gate W1 (16, 3), 5 W2 (rank, 16), 6 dW1, 7 dW2; shape in rows, cols. */
+float* kdec_dlora_ptr(kdec_dlora* d, int which, int* rows, int* cols);
+float kdec_dlora_scale(const kdec_dlora* d);
+
 /* Device pointers to the last forward's har (N, (n_fft+2)*frames) and
  * generator input (N, init_C * L_gen). */
 const float* kdec_model_har(const kdec_model* m);
