@@ -704,6 +704,8 @@ int kdec_model_backward(kdec_model* m, const float* daudio, int wgrad, int dalph
     return KDEC_OK;
 }
 
+kdec_ctx* kdec_model_context(const kdec_model* m) { return m ? m->ctx : nullptr; }
+
 int kdec_model_set_overlap(kdec_model* m, int on) {
     if (!m) return KDEC_EINVAL;
     m->overlap = on != 0;

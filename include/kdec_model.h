@@ -57,6 +57,21 @@ float* kdec_model_param_ptr(kdec_model* m, const char* name);
 float* kdec_model_grad_ptr(kdec_model* m, const char* name);
 long kdec_model_param_total(const kdec_model* m);  /* total parameter count */
 int kdec_model_zero_grad(kdec_model* m);
+/* The context the model was created on (its stream and last error). */
+kdec_ctx* kdec_model_context(const kdec_model* m);
+/* Every parameter from a safetensors file under its upstream state-dict key
+ * (DecoderBackbone / Generator / HarmonicSource::load_from over
+ * brotensor::safetensors, kokoro_modules.cpp:99-122 `upload`, 1021-1063,
+ * 1147-1195, 1237-1347, 1556-1572): F32 tensors of exactly the parameter's
+ * element count, else KDEC_EINVAL with the reference's messages ("missing
+ * safetensors key '...'", "... is not F32 ...", "... has n elements;
+ * expected m"). A weight found only as weight_g / weight_v (the upstream
+ * weight-norm form, fused offline by scripts/convert-kokoro.py:71-110) is
+ * fused on load: weight[r] = g[r] v[r] / max(|v[r]|, 1e-12). */
+int kdec_model_load_safetensors(kdec_model* m, const char* path);
+/* Tensors in a safetensors file, or KDEC_EINVAL when it does not parse
+ * (host only: needs no device). */
+int kdec_safetensors_count(const char* path);
 
 /* AdaIN units in canonical order (backbone, noise_res, resblocks). Unit i's
  * gamma for utterance n is affine[n * rows_total + offset + c], beta follows
