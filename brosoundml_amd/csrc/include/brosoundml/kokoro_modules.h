@@ -1,14 +1,15 @@
 // Decoder-back-half module structs with the reference's fields
 // (include/brosoundml/kokoro_modules.h:127-132, 144-158, 228-244, 259-269,
-// 283-300, 312-340). Loading from safetensors and the inference forwards are
-// not part of this build; the structs are filled by the caller (tests, the
-// benchmark's model, or a loader).
+// 283-300, 312-340), with the inference forwards of DecoderBackbone and
+// Generator. The structs are filled by the caller (tests, the whole-decoder
+// model, whose kdec_model_load_safetensors reads the upstream keys).
 #pragma once
 
 #include <brosoundml/modules.h>
 #include <brotensor/tensor.h>
 
 #include <array>
+#include <functional>
 #include <vector>
 
 namespace brosoundml {
@@ -40,6 +41,12 @@ struct DecoderBackbone {
     Conv1d asr_res;  // (64, 512, 1)
     AdainResBlk1dWeights encode;
     std::vector<AdainResBlk1dWeights> decode;  // the last upsamples 2x
+
+    // Inference forward (kokoro_modules.cpp:1087-1141): style = the first
+    // style_dim values of each ref_s row; asr (N, 512*T), F0_pred / N_pred
+    // (N, 2T) -> gen_in (N, 512*2T). No training caches are kept.
+    void forward(const brotensor::Tensor& asr, const brotensor::Tensor& F0_pred, const brotensor::Tensor& N_pred,
+                 const brotensor::Tensor& ref_s, int T, brotensor::Tensor& gen_in) const;
 };
 
 struct AdaINResBlock1Weights {
@@ -82,6 +89,13 @@ struct Generator {
     std::vector<AdaINResBlock1Weights> noise_res;  // num_upsamples
     std::vector<AdaINResBlock1Weights> resblocks;  // num_upsamples * num_kernels
     Conv1d conv_post;
+
+    // Inference forward (kokoro_modules.cpp:1400-1552): gen_in (N, C*L_in),
+    // har (N, (n_fft+2)*frames), style (N, style_dim) -> audio (N, samples).
+    // `cancel` returning true before a stage leaves `audio` empty.
+    void forward(const brotensor::Tensor& gen_in, int L_in, const brotensor::Tensor& har, int frames,
+                 const brotensor::Tensor& style, brotensor::Tensor& audio,
+                 const std::function<bool()>& cancel = {}) const;
 };
 
 }  // namespace brosoundml

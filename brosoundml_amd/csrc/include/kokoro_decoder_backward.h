@@ -185,6 +185,9 @@ struct BackboneCache {
     int T = 0;
     // kept for the front-conv weight grads (extension)
     brotensor::Tensor asr, F0, N;
+    // Extension: false drops each block's cache as soon as the block is done
+    // (an inference forward; the backward then cannot run on this cache).
+    bool keep = true;
 };
 
 void decoder_backbone_forward_train(const DecoderBackbone& bb,
@@ -226,6 +229,8 @@ struct GeneratorCache {
     // kept for the noise_convs weight grads (extension)
     brotensor::Tensor          har;
     int                        frames = 0;
+    // Extension: false drops each block's cache as soon as the block is done.
+    bool                       keep = true;
 };
 
 void generator_forward_train(const Generator& gen,

@@ -625,7 +625,8 @@ int kdec_model_forward(kdec_model* m, int N, int T, const float* asr, const floa
 }
 
 int kdec_model_backward(kdec_model* m, const float* daudio, int wgrad, int dalpha, float* dstyle) {
-    if (!m || !daudio || m->N == 0) return KDEC_EINVAL;
+    if (!m || !daudio) return KDEC_EINVAL;
+    if (m->N == 0) return fail(m, KDEC_EINVAL, "kdec_model_backward: no training forward to differentiate");
     try {
         bt::set_runtime(m->ctx);
         const int N = m->N;
@@ -705,6 +706,44 @@ int kdec_model_backward(kdec_model* m, const float* daudio, int wgrad, int dalph
 }
 
 kdec_ctx* kdec_model_context(const kdec_model* m) { return m ? m->ctx : nullptr; }
+
+int kdec_model_infer(kdec_model* m, int N, int T, const float* asr, const float* F0, const float* Nn,
+                     const float* style, const float* har, float* audio) {
+    if (!m) return KDEC_EINVAL;
+    // the training forward with every block's cache dropped once the block is done
+    m->bbc.keep = false;
+    m->genc.keep = false;
+    const int rc = kdec_model_forward(m, N, T, asr, F0, Nn, style, har, audio);
+    m->bbc.keep = true;
+    m->genc.keep = true;
+    m->N = 0;  // nothing to differentiate
+    return rc;
+}
+
+int kdec_model_decode_back_half(kdec_model* m, int N, int T, const float* asr, const float* F0, const float* Nn,
+                                const float* ref_s, long ref_bs, float* audio) {
+    if (!m || N <= 0 || T <= 0 || !asr || !F0 || !Nn || !ref_s || !audio) return KDEC_EINVAL;
+    if (ref_bs < m->style_dim) return fail(m, KDEC_EINVAL, "kdec_model_decode_back_half: ref_s stride below style_dim");
+    if (m->lora_rank > 0) return fail(m, KDEC_EINVAL, "kdec_model_decode_back_half: the base decoder has no adapters");
+    try {
+        bt::set_runtime(m->ctx);
+        auto in = [&](const float* p, int cols, long ld = 0) {
+            return Tensor::view(Device::HIP, const_cast<float*>(p), N, cols, bt::Dtype::FP32, ld);
+        };
+        const Tensor rs = in(ref_s, m->style_dim, ref_bs);
+        Tensor gen_in, har, out;
+        m->bb.forward(in(asr, m->asr_dim * T), in(F0, 2 * T), in(Nn, 2 * T), rs, T, gen_in);
+        int sig = 0, frames = 0;
+        m->hs.forward(in(F0, 2 * T), 2 * T, sig, frames, har);
+        m->gen.forward(gen_in, 2 * T, har, frames, rs, out);
+        if (hipMemcpyAsync(audio, out.data, out.size() * sizeof(float), hipMemcpyDeviceToDevice,
+                           static_cast<hipStream_t>(kdec_get_stream(m->ctx))) != hipSuccess)
+            return fail(m, KDEC_EHIP, "kdec_model_decode_back_half: output copy");
+    } catch (const std::exception& e) {
+        return fail(m, KDEC_EINVAL, e.what());
+    }
+    return KDEC_OK;
+}
 
 int kdec_model_set_overlap(kdec_model* m, int on) {
     if (!m) return KDEC_EINVAL;

@@ -716,9 +716,11 @@ void decoder_backbone_forward_train(const DecoderBackbone& bb, const Tensor& asr
     cache.decode.assign(n_dec, AdainResBlkCache{});
     cache.res_applied.assign(n_dec, 0);
     cache.x_channels.assign(n_dec, 0);
-    cache.asr = asr;
-    cache.F0 = F0_pred;
-    cache.N = N_pred;
+    if (cache.keep) {
+        cache.asr = asr;
+        cache.F0 = F0_pred;
+        cache.N = N_pred;
+    }
 
     Tensor F0_dn = conv_fwd(bb.F0_conv, F0_pred, 2 * T);
     Tensor N_dn = conv_fwd(bb.N_conv, N_pred, 2 * T);
@@ -735,6 +737,7 @@ void decoder_backbone_forward_train(const DecoderBackbone& bb, const Tensor& asr
     Tensor x;
     adain_resblk_1d_forward_train(bb.encode, dec_pre, T, aff[0].g1, aff[0].b1, aff[0].g2, aff[0].b2, eps, L_after,
                                   x, cache.encode);
+    if (!cache.keep) cache.encode = AdainResBlkCache{};
     int L_now = L_after;
     bool res = true;
     for (int i = 0; i < n_dec; ++i) {
@@ -755,6 +758,7 @@ void decoder_backbone_forward_train(const DecoderBackbone& bb, const Tensor& asr
         Tensor y;
         adain_resblk_1d_forward_train(bb.decode[i], blk_in, L_now, aff[1 + i].g1, aff[1 + i].b1, aff[1 + i].g2,
                                       aff[1 + i].b2, eps, L_next, y, cache.decode[i]);
+        if (!cache.keep) cache.decode[i] = AdainResBlkCache{};
         x = y;
         L_now = L_next;
         if (bb.decode[i].upsample) res = false;
@@ -829,14 +833,14 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
     check_batch(har, gen.n_fft + 2, frames, where);
     const int N = gen_in.rows;
     cache.stages.resize(U);
-    cache.har = har;
+    if (cache.keep) cache.har = har;
     cache.frames = frames;
 
     Tensor x = gen_in;
     int L = L_in;
     for (int i = 0; i < U; ++i) {
         GenStageCache& sc = cache.stages[i];
-        sc.x_in = x;
+        if (cache.keep) sc.x_in = x;
         sc.C_in = gen.ups_C_in[i];
         sc.L_in = L;
         const int C_out = gen.ups_C_out[i];
@@ -848,6 +852,7 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
         Tensor src;
         adain_resblock1_forward_train(gen.noise_res[i], x_source, C_out, L_src, naff[i].g1, naff[i].b1, naff[i].g2,
                                       naff[i].b2, src, sc.noise);
+        if (!cache.keep) sc.noise = AdainResBlock1Cache{};
 
         // ups (+ left reflect pad on the last stage)
         const int kL = gen.ups_k[i], s = gen.ups_stride[i], p = gen.ups_pad[i];
@@ -878,6 +883,7 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
             const ResBlock1Affines& ra = raff[static_cast<std::size_t>(i) * K + j];
             resblock1_fwd(gen.resblocks[static_cast<std::size_t>(i) * K + j], u, C_out, L_x, ra.g1, ra.b1, ra.g2,
                           ra.b2, mp(xs), rs(xs), 1.0f / static_cast<float>(K), j == 0 ? 0.0f : 1.0f, sc.res[j]);
+            if (!cache.keep) sc.res[j] = AdainResBlock1Cache{};
         }
         x = xs;
         L = L_x;
@@ -885,6 +891,7 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
     cache.window = hann_periodic_dev(gen.win_size);
     spectral_head_forward_train(gen.conv_post, x, gen.ups_C_out[U - 1], L, cache.window, gen.n_fft, gen.hop_size,
                                 gen.win_size, audio, cache.head);
+    if (!cache.keep) cache.head = SpectralHeadCache{};
 }
 
 void generator_backward(const Generator& gen, const GeneratorCache& cache, const std::vector<ResBlock1Affines>& naff,

@@ -98,6 +98,22 @@ int kdec_model_forward(kdec_model* m, int N, int T, const float* asr, const floa
  * grads; dstyle (N, style_dim) may be NULL. The affine grads are always
  * produced (the reference semantics). */
 int kdec_model_backward(kdec_model* m, const float* daudio, int wgrad, int dalpha, float* dstyle);
+/* Inference forward (decode_back_half, kokoro.cpp:352-407: the
+ * DecoderBackbone / HarmonicSource / Generator forwards of
+ * kokoro_modules.cpp:1087-1141, 1400-1552, 1574-1665): the same arithmetic
+ * as kdec_model_forward, arguments as there, without training caches (each
+ * block's are dropped once it is done, so device memory stays at about one
+ * stage's activations). The adapters apply when LoRA is on. A following
+ * kdec_model_backward is refused until the next kdec_model_forward. */
+int kdec_model_infer(kdec_model* m, int N, int T, const float* asr, const float* F0, const float* Nn,
+                     const float* style, const float* har, float* audio);
+/* Kokoro::Impl::decode_back_half (kokoro.cpp:352-407) over the model's
+ * weights through the C++ inference forwards: DecoderBackbone::forward,
+ * HarmonicSource::forward on F0, Generator::forward with the style = the
+ * first style_dim values of each ref_s row (N rows at stride ref_bs);
+ * audio (N, audio_len). For the base decoder (LoRA off). */
+int kdec_model_decode_back_half(kdec_model* m, int N, int T, const float* asr, const float* F0, const float* Nn,
+                                const float* ref_s, long ref_bs, float* audio);
 /* Stream overlap (no counterpart in the reference, whose calls are
  * synchronous): on = 1 (the default) runs the harmonic source and the conv
  * weight grads on a second stream beside the main chain; on = 0 keeps every

@@ -245,3 +245,39 @@ def test_single_stream_equals_overlapped(ctx):
     np.testing.assert_array_equal(res[0][1], res[1][1])
     for n in shapes:
         np.testing.assert_array_equal(res[0][2][n], res[1][2][n], err_msg=n)
+
+
+def test_inference_forwards(ctx):
+    # kdec_model_infer (no training caches) and decode_back_half (the C++
+    # DecoderBackbone / HarmonicSource / Generator forwards) give the
+    # training forward's waveform bit for bit; a backward after an inference
+    # forward is refused.
+    import ctypes
+    from brosoundml_amd import native
+    cfg, N, T = C.SMALL, 2, 6
+    m = native.Model(ctx, cfg)
+    shapes = m.param_shapes()
+    m.set_params(synth.init_params(shapes))
+    asr, F0, Nn, style, dA = inputs(cfg, N, T, "gm.inf")
+    F0[1, 3:7] = 0.0
+    S = cfg["style_dim"]
+    ref_s = np.concatenate([style, synth.normal("gm.inf.ref2", (N, S), 0.3)], axis=1)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    t = [dev(a) for a in (asr, F0, Nn, style)]
+    t_ref = dev(ref_s)
+    a_train = m.forward(*t, T).clone()
+    a_inf = torch.empty_like(a_train)
+    P = native.ptr
+    m._c(ctx.L.kdec_model_infer(m.h, N, T, P(t[0]), P(t[1]), P(t[2]), P(t[3]), None, P(a_inf)))
+    a_dbh = torch.empty_like(a_train)
+    m._c(ctx.L.kdec_model_decode_back_half(m.h, N, T, P(t[0]), P(t[1]), P(t[2]), P(t_ref), 2 * S, P(a_dbh)))
+    torch.cuda.synchronize()
+    assert torch.equal(a_inf, a_train)
+    assert torch.equal(a_dbh, a_train)
+    with pytest.raises(native.KdecError, match="no training forward"):
+        m.backward(dev(dA))
+    # a training forward makes the backward available again
+    m.forward(*t, T)
+    m.backward(dev(dA))
+    torch.cuda.synchronize()
+    del ctypes
