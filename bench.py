@@ -304,12 +304,62 @@ def main(argv=None):
         "reference_semantics": ref,
         "streams": 1 if a.serial else 2,
     }
+    out["inference"] = inference_bench(ctx, model, t_asr, t_F0, t_N, t_style, audio, audio_per_step)
+    out["lora_train_step"] = lora_bench(model, t_asr, t_F0, t_N, t_style, t_dA, audio_per_step)
     if not a.no_micro:
         out["micro"] = micro_benches(ctx)
     if not a.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(cfg, params)
     print(json.dumps(out))
     return 0
+
+
+def inference_bench(ctx, model, asr, F0, Nn, style, audio, audio_per_step, reps=5):
+    """The serving path: the decoder back half forward only (harmonic source,
+    backbone, generator, iSTFT) without training caches, B utterances of T
+    frames, as decode_back_half runs it."""
+    import torch
+    from brosoundml_amd import native
+    P = native.ptr
+    run = lambda: model._c(ctx.L.kdec_model_infer(model.h, B, T, P(asr), P(F0), P(Nn), P(style), None, P(audio)))
+    run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        run()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    return {"ms_per_step": round(dt * 1e3, 3), "value": round(audio_per_step / dt, 2), "unit": "audio-s/s",
+            "workload": f"decoder back half forward only (no caches), B={B}, T={T}"}
+
+
+def lora_bench(model, asr, F0, Nn, style, dA, audio_per_step, reps=3):
+    """One DecoderLora training step (decoder_lora.cpp:211-314): gate,
+    forward with the adapters on every AdaIN unit, backward to the affine
+    grads and through the adapters and gate (frozen decoder: no weight
+    grads), Adam over A, B and the gate; rank 4, one condition per utterance."""
+    import torch
+    from brosoundml_amd import native
+    d = native.DecoderLora(model, 4, 1.0, seed=11)
+    d.set("W2", np.full((4, 16), 0.05, np.float32))
+    cond = torch.full((B, 3), 0.3, device="cuda")
+    ref_s = torch.cat([style, style], dim=1).contiguous()
+
+    def step():
+        d.zero_grad()
+        d.forward(asr, F0, Nn, ref_s, T, cond)
+        d.backward(dA)
+        d.adam_step(1e-4)
+    step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    del d
+    return {"ms_per_step": round(dt * 1e3, 3), "value": round(audio_per_step / dt, 2), "unit": "audio-s/s",
+            "workload": f"DecoderLora step (rank 4, frozen decoder), B={B}, T={T}"}
 
 
 def adain_elements(cfg, T):
