@@ -310,6 +310,17 @@ int kdec_adam_step(kdec_ctx* ctx, float* p, const float* g, float* m,
                    float* v, long n, float lr, float beta1, float beta2,
                    float eps, int step);
 
+/* Length regulation (the host loop of Kokoro::prepare_decode_context /
+ * synthesize, kokoro.cpp:667-689): asr[n, c, t] = t_en[n, c, l] for the
+ * phoneme l whose duration run covers frame t (runs in token order,
+ * negative durations count as zero), zero for t >= the utterance's total.
+ * t_en (N, C, L) at batch stride te_bs, dur (N, L) int32 (device) at dur_bs,
+ * asr (N, C, T) at asr_bs; totals (N int32, device) receives each total
+ * when not NULL. L <= 4096. */
+int kdec_length_regulate(kdec_ctx* ctx, const float* t_en, long te_bs,
+                         const int* dur, long dur_bs, int N, int C, int L,
+                         float* asr, long asr_bs, int T, int* totals);
+
 #ifdef __cplusplus
 }
 #endif

@@ -464,3 +464,30 @@ def test_lora_projection(K, shared_gate):
     for name, got, ref in (("dstyle", dstyle, rs), ("dW", dW, rW), ("db", db, rb), ("dA", dA, rA), ("dB", dB, rB),
                            ("dG", dG, rG)):
         assert_close(h(got), ref, GRAD_TOL, f"lora projection {name}")
+
+
+def test_length_regulate(K):
+    # the reference's host loop is a per-phoneme repeat: np.repeat pins it;
+    # two utterances of different totals in one padded batch, zero and
+    # negative durations, frames past a total zero
+    from brosoundml_amd import native
+    r = np.random.default_rng(21)
+    N, C, L, T = 2, 40, 37, 150
+    te = r.normal(size=(N, C, L)).astype(np.float32)
+    dur = r.integers(0, 5, size=(N, L)).astype(np.int32)
+    dur[0, 3] = -2
+    dur[1, :5] = 0
+    out = torch.full((N, C, T), 7.0, device="cuda")
+    totals = torch.zeros(N, dtype=torch.int32, device="cuda")
+    t_dur = torch.from_numpy(dur).cuda()
+    K.call("kdec_length_regulate", P(g(te)), C * L, P(t_dur), L, N, C, L, P(out), C * T, T, P(totals))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for n in range(N):
+        d = np.maximum(dur[n], 0)
+        ref = np.repeat(te[n], d, axis=1)[:, :T]
+        assert totals[n].item() == d.sum()
+        np.testing.assert_array_equal(got[n, :, :ref.shape[1]], ref)
+        assert np.all(got[n, :, ref.shape[1]:] == 0.0)
+    with pytest.raises(native.KdecError):
+        K.call("kdec_length_regulate", P(g(te)), C * L - 1, P(t_dur), L, N, C, L, P(out), C * T, T, P(totals))
