@@ -135,16 +135,16 @@ def test_neutral_identity(ctx):
     assert torch.equal(audio, audio2)
 
 
-@pytest.mark.parametrize("N", [1, 2])
-def test_grads_against_oracle(ctx, N):
+@pytest.mark.parametrize("cfg_name,N,T", [("TINY", 1, 4), ("TINY", 2, 4), ("SMALL", 2, 6)])
+def test_grads_against_oracle(ctx, cfg_name, N, T):
     from brosoundml_amd import native
-    cfg, T, rank, scale = C.TINY, 4, 3, 0.7
+    cfg, rank, scale = getattr(C, cfg_name), 3, 0.7
     m, om = make_model(ctx, cfg, "dl.g")
     d = native.DecoderLora(m, rank, scale, seed=77)
     W2 = np.random.default_rng(8).uniform(-0.3, 0.3, (rank, 16)).astype(np.float32)
     d.set("W2", W2)
     A, B, W1 = d.get("A"), d.get("B"), d.get("W1")
-    asr, F0, Nn, ref_s, cond, dA = inputs(cfg, N, T, f"dl.g{N}")
+    asr, F0, Nn, ref_s, cond, dA = inputs(cfg, N, T, f"dl.g{cfg_name}{N}")
     S = cfg["style_dim"]
     units = om.units()
     offs = [u[2] for u in m.units()]
