@@ -111,9 +111,9 @@ def micro_benches(ctx, reps=10):
     out["snake_adain_bwd_x1x256x48000"] = {"ms": round(t * 1e3, 4), "GB/s": round(by / t / 1e9, 1),
                                           "frac_hbm": round(by / t / PEAK_HBM, 4),
                                           "algorithmic_bytes": by}
-    t = timed(lambda: (ctx.call("kdec_instnorm_stats", P(x), C * L, 1, C, L, 1e-5, P(stats)),
-                       ctx.call("kdec_adain_act_fwd", P(x), C * L, P(stats), g_ptr, b_ptr, 0, 2, 0.0, P(alpha),
-                                P(y), C * L, None, 0, 1, C, L)))
+    # forward: statistics, affine and Snake in one pass (the training forward's entry)
+    t = timed(lambda: ctx.call("kdec_adain_act_fwd_stats", P(x), C * L, 1e-5, P(stats), g_ptr, b_ptr, 0, 2, 0.0,
+                               P(alpha), P(y), C * L, None, 0, 1, C, L))
     by = 8.0 * C * L
     out["snake_adain_fwd_x1x256x48000"] = {"ms": round(t * 1e3, 4), "GB/s": round(by / t / 1e9, 1),
                                           "frac_hbm": round(by / t / PEAK_HBM, 4),

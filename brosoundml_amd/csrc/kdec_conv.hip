@@ -93,6 +93,7 @@ struct GemmArgs {
     int full_tiles, split_tiles, fsplit;
     int full_per_xcd, parts_per_xcd;  // block slots per XCD for each kind
     float* P;
+    int ybuf;                // (C_out + BM) * L_y * 4 < 2^31: the epilogue addresses Y through a descriptor
     // octet mode (corr_gemm): K chunk = one input-channel octet x up to G taps
     int G, n_tg, n_oct, span8;  // taps per chunk, tap groups, octets, staged positions
 };
@@ -197,6 +198,41 @@ __device__ inline void store_tile(const GemmArgs& g, const TileGeo& T, int tile,
     }
     float* Yb = g.Y + static_cast<long>(b) * g.y_bs;
     const float* Rb = g.R ? g.R + static_cast<long>(b) * g.r_bs : nullptr;
+    if (g.ybuf) {
+        // Y, R and the bias through descriptors over exactly their rows: rows
+        // at or past C_out fall outside and their stores drop, their loads
+        // read 0. The whole byte offset goes in the VGPR offset, since the
+        // scalar offset of a buffer access is not range checked; ybuf keeps
+        // it below 2^31 for every row of the tile.
+        const int rowb = g.C_out * g.L_y * 4;
+        const __amdgpu_buffer_rsrc_t yr = uniform_rsrc(Yb, rowb);
+        const __amdgpu_buffer_rsrc_t rr = uniform_rsrc(Rb ? Rb : Yb, Rb ? rowb : 0);
+        const __amdgpu_buffer_rsrc_t br = uniform_rsrc(g.bias ? g.bias : Yb, g.bias ? g.C_out * 4 : 0);
+        const int mrow = m0 + wm * 64 + 4 * hi;  // the lane's first row
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn) {
+            const int q = q0 + wn * 64 + tn * 32 + l32;
+            if (q >= n_q) continue;
+            const int vo = (mrow * g.L_y + q * os + oo) * 4;
+#pragma unroll
+            for (int tm = 0; tm < 2; ++tm) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int dm = tm * 32 + 8 * (e >> 2) + (e & 3);  // uniform row step
+                    const int o = vo + dm * g.L_y * 4;
+                    float v = acc[tm][tn][e];
+                    if (g.bias)
+                        v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(br, (mrow + dm) * 4, 0, 0));
+                    if (Rb) v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, o, 0, 0));
+                    v *= g.scale;
+                    if (g.beta != 0.0f)
+                        v += g.beta * __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(yr, o, 0, 0));
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), yr, o, 0, 0);
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int tn = 0; tn < 2; ++tn) {
         const int q = q0 + wn * 64 + tn * 32 + l32;
@@ -1196,6 +1232,7 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
     if (lds > 160 * 1024) return fail(ctx, KDEC_EINVAL, "conv: tile does not fit LDS");
     if (static_cast<long>(g.C_in) * g.L_in * 4 > 0x7fffffffL)
         return fail(ctx, KDEC_EINVAL, "conv: input too large for one buffer descriptor");
+    g.ybuf = (static_cast<long>(g.C_out) + BM) * g.L_y * 4 < 0x7fffffffL ? 1 : 0;
     const void* kern = octet ? corr_kernel() : conv_kernel_for(CK);
     if (!kern) return fail(ctx, KDEC_EINVAL, "conv: unsupported channel chunk");
     int max_q = g.n_q;

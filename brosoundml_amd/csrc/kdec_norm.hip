@@ -10,6 +10,7 @@
 // Statistics are per (utterance, channel) row over L, accumulated in double
 // so the result does not depend on the row length or the thread count.
 #include "kdec_internal.hpp"
+#include "kdec_snake_math.hpp"
 
 namespace kdec {
 namespace {
@@ -120,10 +121,7 @@ struct AdainArgs {
 // ia = 1 / alpha, formed once per row
 __device__ inline float act_fwd(int act, float s, float slope, float a, float ia) {
     if (act == KDEC_ACT_LEAKY) return s > 0.0f ? s : slope * s;
-    if (act == KDEC_ACT_SNAKE) {
-        const float sn = sinf(a * s);
-        return s + sn * sn * ia;
-    }
+    if (act == KDEC_ACT_SNAKE) return s + snake_sin2(a * s) * ia;
     return s;
 }
 
@@ -313,33 +311,68 @@ __device__ inline void row_st(__amdgpu_buffer_rsrc_t r, float v, int voff, int j
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, voff, j * ntb * 4, 0);
 }
 
-// stats[row] = (mean, rstd); Y = act((1 + gamma) * xhat + beta). KEEP holds
-// the row in registers between the two passes; otherwise the second pass
-// reads it again, right after the first (from cache, not HBM, in practice).
-template <int NTB, int EPR, bool KEEP>
+// Element e of a thread's row share: with V = 1, element e*NTB + t; with
+// V = 4 (rows of a multiple of 4 floats on 16-B aligned bases), element
+// 4*((e/4)*NTB + t) + e%4, one 16-B access per four elements. Past the row
+// the descriptor reads 0 and drops stores, a float4 wholly in either case.
+// The float4 buffer access is declared on the LLVM intrinsic itself: with
+// this compiler, __builtin_amdgcn_raw_buffer_load_b128 (and _b64) whose
+// elements are read one by one is narrowed to a single-dword load and every
+// element then reads element 0.
+using f32x4 = float __attribute__((ext_vector_type(4)));
+__device__ f32x4 buf_ld_f4(__amdgpu_buffer_rsrc_t r, int voff, int soff, int aux)
+    __asm("llvm.amdgcn.raw.ptr.buffer.load.v4f32");
+__device__ void buf_st_f4(f32x4 v, __amdgpu_buffer_rsrc_t r, int voff, int soff, int aux)
+    __asm("llvm.amdgcn.raw.ptr.buffer.store.v4f32");
+
+template <int V, int NTB>
+__device__ inline void row_ld_grp(__amdgpu_buffer_rsrc_t r, int j, float* v) {
+    if constexpr (V == 1) {
+        v[0] = row_ld(r, threadIdx.x * 4, j, NTB);
+    } else {
+        const f32x4 q = buf_ld_f4(r, threadIdx.x * 16, j * NTB * 16, 0);
+        v[0] = q.x;
+        v[1] = q.y;
+        v[2] = q.z;
+        v[3] = q.w;
+    }
+}
+template <int V, int NTB>
+__device__ inline void row_st_grp(__amdgpu_buffer_rsrc_t r, int j, const float* v) {
+    if constexpr (V == 1) {
+        row_st(r, v[0], threadIdx.x * 4, j, NTB);
+    } else {
+        buf_st_f4(f32x4{v[0], v[1], v[2], v[3]}, r, threadIdx.x * 16, j * NTB * 16, 0);
+    }
+}
+
+// stats[row] = (mean, rstd); Y = act((1 + gamma) * xhat + beta), the row held
+// in registers between the statistics and the affine pass (V as for the
+// backward: 16-B groups on aligned rows of a multiple of 4 floats).
+template <int NTB, int EPR, int V>
 __global__ __launch_bounds__(NTB) void adain_fwd_row_k(AdainArgs g, float eps, float2* stats, float* Y, long y_bs,
                                                       float* Yp, long yp_bs) {
+    static_assert(EPR % V == 0, "whole groups per thread");
     __shared__ double red[NTB / 64];
     const int row = blockIdx.x;
     const int n = row / g.C, c = row - n * g.C;
     const long off = static_cast<long>(c) * g.L;
     const float* x = g.X + n * g.x_bs + off;
     const __amdgpu_buffer_rsrc_t xr = row_rsrc(x, g.L);
-    const int vo = threadIdx.x * 4;
     const double x0 = x[0];  // shift for a well-conditioned variance
-    float v[KEEP ? EPR : 1];
-    double s1 = 0.0, s2 = 0.0;
-    if (KEEP) {
+    float v[EPR];
 #pragma unroll
-        for (int j = 0; j < EPR; ++j) v[KEEP ? j : 0] = row_ld(xr, vo, j, NTB);
-    }
-    constexpr int UN = KEEP ? EPR : 16;  // streaming: 16 loads in flight, not the whole row
-#pragma unroll UN
-    for (int j = 0; j < EPR; ++j) {
-        const float xj = KEEP ? v[KEEP ? j : 0] : row_ld(xr, vo, j, NTB);
-        const double d = (threadIdx.x + j * NTB < g.L) ? static_cast<double>(xj) - x0 : 0.0;
-        s1 += d;
-        s2 += d * d;
+    for (int j = 0; j < EPR / V; ++j) row_ld_grp<V, NTB>(xr, j, v + V * j);
+    double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+    for (int j = 0; j < EPR / V; ++j) {
+        if (V * (j * NTB + threadIdx.x) >= g.L) continue;  // past the row (a group lies wholly in or out)
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            const double d = static_cast<double>(v[V * j + e]) - x0;
+            s1 += d;
+            s2 += d * d;
+        }
     }
     s1 = block_sum_n<NTB>(s1, red);
     s2 = block_sum_n<NTB>(s2, red);
@@ -354,17 +387,21 @@ __global__ __launch_bounds__(NTB) void adain_fwd_row_k(AdainArgs g, float eps, f
     const float ia = 1.0f / a;
     const __amdgpu_buffer_rsrc_t yr = row_rsrc(Y + n * y_bs + off, g.L);
     const __amdgpu_buffer_rsrc_t pr = row_rsrc(Yp ? Yp + n * yp_bs + off : Y, Yp ? g.L : 0);
-#pragma unroll UN
-    for (int j = 0; j < EPR; ++j) {
-        const float xj = KEEP ? v[KEEP ? j : 0] : row_ld(xr, vo, j, NTB);
-        const float xh = (xj - st.x) * st.y;
-        const float s = g1 * xh + bt;
-        row_st(yr, act_fwd(g.act, s, g.slope, a, ia), vo, j, NTB);
-        row_st(pr, s, vo, j, NTB);  // dropped without a pre-activation output
+#pragma unroll
+    for (int j = 0; j < EPR / V; ++j) {
+        float yv[V], sv[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            const float xh = (v[V * j + e] - st.x) * st.y;
+            sv[e] = g1 * xh + bt;
+            yv[e] = act_fwd(g.act, sv[e], g.slope, a, ia);
+        }
+        row_st_grp<V, NTB>(yr, j, yv);
+        row_st_grp<V, NTB>(pr, j, sv);  // dropped without a pre-activation output
     }
 }
 
-template <int NTB, int EPR, bool BOTH>
+template <int NTB, int EPR, bool BOTH, int V>
 __global__ __launch_bounds__(NTB) void adain_bwd_row_k(AdainArgs g, const float* dY, long dy_bs, const float* R,
                                                       long r_bs, float* dX, long dx_bs, float* dgamma,
                                                       float* dbeta, long dgb_bs, float* dalpha_part,
@@ -379,12 +416,13 @@ __global__ __launch_bounds__(NTB) void adain_bwd_row_k(AdainArgs g, const float*
     const long off = static_cast<long>(c) * g.L;
     const __amdgpu_buffer_rsrc_t xr = row_rsrc(g.X + n * g.x_bs + off, g.L);
     const __amdgpu_buffer_rsrc_t dr = row_rsrc(dY + n * dy_bs + off, g.L);
+    static_assert(V == 1 || (BOTH && EPR % 4 == 0), "16-B row access holds both rows");
     const int vo = threadIdx.x * 4;
     float xv[EPR], dv[BOTH ? EPR : 1];
 #pragma unroll
-    for (int j = 0; j < EPR; ++j) {
-        xv[j] = row_ld(xr, vo, j, NTB);
-        if (BOTH) dv[j] = row_ld(dr, vo, j, NTB);  // zero past the row: no contribution
+    for (int j = 0; j < EPR / V; ++j) {
+        row_ld_grp<V, NTB>(xr, j, xv + V * j);
+        if (BOTH) row_ld_grp<V, NTB>(dr, j, dv + V * j);  // zero past the row: no contribution
     }
     // per-thread sums of at most EPR terms in float, across the block in double
     float fsd = 0.0f, fsdx = 0.0f, fsa = 0.0f;
@@ -414,18 +452,23 @@ __global__ __launch_bounds__(NTB) void adain_bwd_row_k(AdainArgs g, const float*
     // without a residual the descriptor covers nothing and its loads read 0
     const __amdgpu_buffer_rsrc_t rr = row_rsrc(R ? R + n * r_bs + off : dY, R ? g.L : 0);
 #pragma unroll
-    for (int j = 0; j < EPR; ++j) {
-        const float xh = (xv[j] - st.x) * st.y;
-        float ds;
-        if (BOTH) {
-            ds = dv[j];
-        } else {
-            float unused = 0.0f;
-            ds = act_bwd(g.act, row_ld(dr, vo, j, NTB), g1 * xh + bt, g.slope, a, unused);
+    for (int j = 0; j < EPR / V; ++j) {
+        float val[V];
+        row_ld_grp<V, NTB>(rr, j, val);
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            const int i = V * j + e;
+            const float xh = (xv[i] - st.x) * st.y;
+            float ds;
+            if (BOTH) {
+                ds = dv[i];
+            } else {
+                float unused = 0.0f;
+                ds = act_bwd(g.act, row_ld(dr, vo, j, NTB), g1 * xh + bt, g.slope, a, unused);
+            }
+            val[e] += k1 * (ds - mds - xh * mdsx);
         }
-        float val = k1 * (ds - mds - xh * mdsx);
-        val += row_ld(rr, vo, j, NTB);
-        row_st(xo, val, vo, j, NTB);
+        row_st_grp<V, NTB>(xo, j, val);
     }
 }
 
@@ -536,15 +579,24 @@ __global__ void fill_k(float* Y, long n, float v) {
 
 // Row-kernel shape for a row of L elements: {threads, elements per thread};
 // {0, 0} where the chunked multi-block kernels are faster (measured on the
-// decoder's shapes: the forward up to 4096, the backward up to 49152 with
-// x and dY both held).
+// decoder's shapes: the forward up to 4096 with 4-byte accesses, up to 49152
+// with 16-byte ones; the backward up to 49152 with x and dY both held).
 struct RowShape {
     int ntb, epr;
 };
-RowShape row_shape_fwd(int L) {
+bool aligned16(const void* p) { return (reinterpret_cast<unsigned long long>(p) & 15) == 0; }
+
+RowShape row_shape_fwd(int L, bool v4) {
     if (L <= 1024) return {256, 4};
     if (L <= 4096) return {256, 16};
+    if (!v4) return {0, 0};
+    if (L <= 16384) return {1024, 16};
+    if (L <= 49152) return {1024, 48};
     return {0, 0};
+}
+bool fwd_v4(const AdainArgs& g, const float* Y, long y_bs, const float* Yp, long yp_bs) {
+    return g.L % 4 == 0 && g.x_bs % 4 == 0 && y_bs % 4 == 0 && aligned16(g.X) && aligned16(Y) &&
+           (!Yp || (yp_bs % 4 == 0 && aligned16(Yp)));
 }
 RowShape row_shape_bwd(int L) {
     if (L <= 1024) return {256, 4};
@@ -556,14 +608,19 @@ RowShape row_shape_bwd(int L) {
 
 int launch_fwd_row(kdec_ctx* ctx, RowShape rsh, unsigned rows, const AdainArgs& g, float eps, float2* st, float* Y,
                    long y_bs, float* Yp, long yp_bs) {
-#define KDEC_FWD_ROW(T, E, K)                                                                                \
-    if (rsh.ntb == T && rsh.epr == E) {                                                                      \
-        hipLaunchKernelGGL((adain_fwd_row_k<T, E, K>), dim3(rows), dim3(T), 0, ctx->stream, g, eps, st, Y,    \
-                           y_bs, Yp, yp_bs);                                                                 \
-        return launch_check(ctx, "adain_fwd_row");                                                          \
+    const bool v4 = fwd_v4(g, Y, y_bs, Yp, yp_bs);
+#define KDEC_FWD_ROW(T, E, V)                                                                                  \
+    if (rsh.ntb == T && rsh.epr == E && (V == 4) == v4) {                                                      \
+        hipLaunchKernelGGL((adain_fwd_row_k<T, E, V>), dim3(rows), dim3(T), 0, ctx->stream, g, eps, st, Y, y_bs, \
+                           Yp, yp_bs);                                                                         \
+        return launch_check(ctx, "adain_fwd_row");                                                            \
     }
-    KDEC_FWD_ROW(256, 4, true)
-    KDEC_FWD_ROW(256, 16, true)
+    KDEC_FWD_ROW(256, 4, 1)
+    KDEC_FWD_ROW(256, 16, 1)
+    KDEC_FWD_ROW(256, 4, 4)
+    KDEC_FWD_ROW(256, 16, 4)
+    KDEC_FWD_ROW(1024, 16, 4)
+    KDEC_FWD_ROW(1024, 48, 4)
 #undef KDEC_FWD_ROW
     return fail(ctx, KDEC_EINVAL, "adain forward: no row kernel for this length");
 }
@@ -571,11 +628,18 @@ int launch_fwd_row(kdec_ctx* ctx, RowShape rsh, unsigned rows, const AdainArgs& 
 int launch_bwd_row(kdec_ctx* ctx, RowShape rsh, unsigned rows, const AdainArgs& g, const float* dY, long dy_bs,
                    const float* R, long r_bs, float* dX, long dx_bs, float* dgamma, float* dbeta, long dgb_bs,
                    float* apart, float* aacc) {
-#define KDEC_BWD_ROW(T, E, B)                                                                                    \
-    if (rsh.ntb == T && rsh.epr == E) {                                                                          \
-        hipLaunchKernelGGL((adain_bwd_row_k<T, E, B>), dim3(rows), dim3(T), 0, ctx->stream, g, dY, dy_bs, R, r_bs, \
-                           dX, dx_bs, dgamma, dbeta, dgb_bs, apart, aacc);                                       \
-        return launch_check(ctx, "adain_bwd_row");                                                              \
+    // 16-B accesses when every row of every tensor starts on 16 B
+    const bool v4 = g.L % 4 == 0 && g.x_bs % 4 == 0 && dy_bs % 4 == 0 && dx_bs % 4 == 0 && aligned16(g.X) &&
+                    aligned16(dY) && aligned16(dX) && (!R || (r_bs % 4 == 0 && aligned16(R)));
+#define KDEC_BWD_ROW(T, E, B)                                                                                  \
+    if (rsh.ntb == T && rsh.epr == E) {                                                                        \
+        if (v4)                                                                                                \
+            hipLaunchKernelGGL((adain_bwd_row_k<T, E, B, 4>), dim3(rows), dim3(T), 0, ctx->stream, g, dY, dy_bs, \
+                               R, r_bs, dX, dx_bs, dgamma, dbeta, dgb_bs, apart, aacc);                        \
+        else                                                                                                   \
+            hipLaunchKernelGGL((adain_bwd_row_k<T, E, B, 1>), dim3(rows), dim3(T), 0, ctx->stream, g, dY, dy_bs, \
+                               R, r_bs, dX, dx_bs, dgamma, dbeta, dgb_bs, apart, aacc);                        \
+        return launch_check(ctx, "adain_bwd_row");                                                            \
     }
     KDEC_BWD_ROW(256, 4, true)
     KDEC_BWD_ROW(256, 16, true)
@@ -643,13 +707,13 @@ int kdec_adain_act_fwd_stats(kdec_ctx* ctx, const float* X, long x_bs, float eps
                "kdec_adain_act_fwd_stats: bad arguments");
     KDEC_CHECK(ctx, act >= KDEC_ACT_NONE && act <= KDEC_ACT_SNAKE && (act != KDEC_ACT_SNAKE || alpha),
                "kdec_adain_act_fwd_stats: bad activation");
-    const RowShape rsh = row_shape_fwd(L);
+    AdainArgs g{X, x_bs, reinterpret_cast<const float2*>(stats), gamma, beta, gb_bs, act, slope, alpha, C, L};
+    const RowShape rsh = row_shape_fwd(L, fwd_v4(g, Y, y_bs, Ypre, ypre_bs));
     if (!rsh.ntb) {  // long rows: statistics pass, then the affine pass
         if (int rc = kdec_instnorm_stats(ctx, X, x_bs, N, C, L, eps, stats)) return rc;
         return kdec_adain_act_fwd(ctx, X, x_bs, stats, gamma, beta, gb_bs, act, slope, alpha, Y, y_bs, Ypre, ypre_bs,
                                   N, C, L);
     }
-    AdainArgs g{X, x_bs, reinterpret_cast<const float2*>(stats), gamma, beta, gb_bs, act, slope, alpha, C, L};
     ProfScope ps(ctx, "adain_fwd", 0, 4.0 * static_cast<double>(N) * C * L * (Ypre ? 3 : 2));
     return launch_fwd_row(ctx, rsh, static_cast<unsigned>(N * C), g, eps, reinterpret_cast<float2*>(stats), Y, y_bs,
                           Ypre, ypre_bs);

@@ -1,0 +1,41 @@
+// sin^2 for the Snake activation y = s + sin^2(a s) / a on gfx950.
+//
+// Cody-Waite reduction of th by pi/2 with a three-part split of pi/2 (each
+// product folded in by fma), then the Taylor series of sin or of cos on
+// [-pi/4, pi/4], chosen by the parity of the quadrant (sin^2 needs no sign).
+// The series' truncation is below 3e-9 relative (the r^11 / 11! and r^12 / 12!
+// terms at pi/4), so the result is float-rounding limited for |th| < 2^15.
+// About 20 VALU operations against the library sinf's reduction with its
+// large-argument path.
+#pragma once
+
+#ifndef __HIPCC__
+#include <cmath>
+#define KDEC_HD
+#else
+#define KDEC_HD __host__ __device__
+#endif
+
+namespace kdec {
+
+KDEC_HD inline float snake_sin2(float th) {
+    const float q = rintf(th * 0.636619746685028076f);  // nearest multiple of pi/2
+    float r = fmaf(-q, 1.57079637050628662f, th);        // pi/2 = c1 + c2 + c3
+    r = fmaf(-q, -4.37113882867379300e-08f, r);
+    r = fmaf(-q, -1.71512451000588190e-15f, r);
+    const float w = r * r;
+    // sin r = r + r w (-1/3! + w (1/5! + w (-1/7! + w / 9!)))
+    const float ps = fmaf(w, fmaf(w, fmaf(w, 2.75573188e-06f, -1.98412701e-04f), 8.33333377e-03f), -1.66666672e-01f);
+    const float sn = fmaf(r * w, ps, r);
+    // cos r = 1 + w (-1/2! + w (1/4! + w (-1/6! + w (1/8! - w / 10!))))
+    const float pc = fmaf(w, fmaf(w, fmaf(w, fmaf(w, -2.75573199e-07f, 2.48015876e-05f), -1.38888892e-03f),
+                                  4.16666679e-02f),
+                          -0.5f);
+    const float cs = fmaf(w, pc, 1.0f);
+    const float v = (static_cast<int>(q) & 1) ? cs : sn;
+    return v * v;
+}
+
+}  // namespace kdec
+
+#undef KDEC_HD

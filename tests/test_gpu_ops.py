@@ -249,7 +249,7 @@ ACTS = {"none": 0, "leaky": 1, "snake": 2}
 @pytest.mark.parametrize("act", ["none", "leaky", "snake"])
 # lengths cover every row-kernel shape (256x4, 256x16, 1024x16, 1024x48,
 # 1024x64 streaming) and the chunked path for longer rows
-@pytest.mark.parametrize("C,L", [(5, 31), (3, 1500), (16, 4099), (2, 48000), (2, 61441), (2, 70000)])
+@pytest.mark.parametrize("C,L", [(5, 31), (3, 1500), (16, 4099), (3, 8192), (2, 48000), (2, 61441), (2, 70000)])
 def test_adain_act(K, act, C, L):
     N = 2
     x = rnd(N, C, L, scale=1.7) + 0.3
