@@ -651,6 +651,73 @@ __global__ void pack_convt_dgrad(const float* W, float* A, int C_in, int C_out,
     }
 }
 
+// The panel row of (channel c, tap t) for CK-channel chunks, the inverse of
+// panel_row: row = ((c / CK) * kk + t) * CK + c % CK.
+__device__ inline long panel_index(int c, int t, int CK, int kk) {
+    return (static_cast<long>(c / CK) * kk + t) * CK + (c % CK);
+}
+
+// A[panel_index(c, t)][m] = W[m][c*k + t] (0 unless m < Mv and c < Cv): the
+// conv1d forward panel (m = co, c = ci) and the conv-transpose input-grad
+// panel (m = ci, c = co). A 64 (m) x 64 (j = c*k + t) tile passes through LDS:
+// W is read along its rows (j), A written along its rows (m). Grid
+// (cdiv(cpad*k, 64), m_pad / 64); cpad a multiple of CK, m_pad of 64.
+__global__ __launch_bounds__(256) void pack_rows_t(const float* W, float* A, int Mv, int Cv, int k, int cpad,
+                                                   int m_pad, int CK) {
+    __shared__ float tile[64][65];
+    const int j0 = blockIdx.x * 64, m0 = blockIdx.y * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const long ld = static_cast<long>(Cv) * k;  // W row length
+    // fixed trip counts, unrolled: all 16 loads of a thread are in flight at once
+    float v[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int m = m0 + ty + 4 * r, j = j0 + tx;
+        v[r] = (m < Mv && j < ld) ? W[m * ld + j] : 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) tile[tx][ty + 4 * r] = v[r];
+    __syncthreads();
+    const long rows = static_cast<long>(cpad) * k;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int i = ty + 4 * r, j = j0 + i;
+        if (j < rows) {
+            const int c = j / k, t = j - c * k;
+            A[panel_index(c, t, CK, k) * m_pad + m0 + tx] = tile[i][tx];
+        }
+    }
+}
+
+// A[panel_index(c, t)][m] = W[c][m*k + k-1-t] (0 unless m < C_in, c < C_out):
+// the conv1d input-grad panel. Each wave takes one output channel c and a
+// 64-column m slice: it reads that slice's contiguous 64*k floats of W[c]
+// into LDS, then writes its k panel rows along m. Grid (cdiv(cpad, 4),
+// m_pad / 64), dynamic LDS 4 * 64 * k floats; cpad a multiple of CK.
+__global__ __launch_bounds__(256) void pack_dgrad_t(const float* W, float* A, int C_in, int C_out, int k,
+                                                    int cpad, int m_pad, int CK) {
+    extern __shared__ float seg_all[];
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const int c = blockIdx.x * 4 + ty, m0 = blockIdx.y * 64;
+    float* seg = seg_all + ty * 64 * k;
+    const long base = static_cast<long>(c) * C_in * k + static_cast<long>(m0) * k;
+    const long lim = static_cast<long>(C_in) * k;  // valid part of row c
+    // k <= 32: a fixed trip count, unrolled, so the loads overlap
+    float v[32];
+#pragma unroll
+    for (int r = 0; r < 32; ++r) {
+        const int e = tx + 64 * r;
+        v[r] = (r < k && c < C_out && static_cast<long>(m0) * k + e < lim) ? W[base + e] : 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < 32; ++r)
+        if (r < k) seg[tx + 64 * r] = v[r];
+    __syncthreads();
+    if (c >= cpad) return;
+    for (int t = 0; t < k; ++t)
+        A[panel_index(c, t, CK, k) * m_pad + m0 + tx] = seg[tx * k + (k - 1 - t)];
+}
+
 // conv-transpose forward, phase r of s: tap t' of kt covers original tap
 // t = r + (kt-1-t')*s.  A_r[(ci, t'), co] = W[ci, co*k + t] (0 if t >= k)
 __global__ void pack_convt_fwd(const float* W, float* A, int C_in, int C_out,
@@ -1005,6 +1072,9 @@ __global__ void wgrad_reduce(const float* P, float* out, long MN, int splits,
 // positions of each row with a fixed stride (no per-element index division)
 // and the block sums the thread partials in a fixed tree; bias_reduce then
 // adds the slices in order.
+// V = 4: rows of a multiple of 4 floats on a 16-B aligned base and slices of
+// a multiple of 4 positions, read as float4.
+template <int V>
 __global__ void bias_partial(const float* G, long g_bs, float* part, int N, int M, int L, int per) {
     const int m = blockIdx.x, y = blockIdx.y;
     const int l0 = y * per, l1 = min(L, l0 + per);
@@ -1012,8 +1082,17 @@ __global__ void bias_partial(const float* G, long g_bs, float* part, int N, int 
     for (int n = 0; n < N; ++n) {
         const float* row = G + n * g_bs + static_cast<long>(m) * L;
         float t = 0.0f;
+        if constexpr (V == 4) {
+            const float4* r4 = reinterpret_cast<const float4*>(row);
+#pragma unroll 4
+            for (int l = l0 / 4 + threadIdx.x; l < l1 / 4; l += blockDim.x) {
+                const float4 q = r4[l];
+                t += (q.x + q.y) + (q.z + q.w);
+            }
+        } else {
 #pragma unroll 8
-        for (int l = l0 + threadIdx.x; l < l1; l += blockDim.x) t += row[l];
+            for (int l = l0 + threadIdx.x; l < l1; l += blockDim.x) t += row[l];
+        }
         acc += t;
     }
     __shared__ double red[256];
@@ -1323,8 +1402,13 @@ int kdec_conv1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
         hipLaunchKernelGGL(pack_octet, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), 0, C_in,
                            C_out, k, 1, k, m_pad, static_cast<int>(tot), 1);
     else
-        hipLaunchKernelGGL(pack_fwd, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), C_in,
-                           C_out, k, g.cin_pad, m_pad, g.CK);
+        if (g.cin_pad % g.CK == 0 && m_pad % 64 == 0)
+            hipLaunchKernelGGL(pack_rows_t, dim3(static_cast<unsigned>(cdiv(static_cast<long>(g.cin_pad) * k, 64)),
+                                                 static_cast<unsigned>(m_pad / 64)),
+                               dim3(256), 0, ctx->stream, W, A.as<float>(), C_out, C_in, k, g.cin_pad, m_pad, g.CK);
+        else
+            hipLaunchKernelGGL(pack_fwd, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), C_in,
+                               C_out, k, g.cin_pad, m_pad, g.CK);
     if (int rc = launch_check(ctx, "pack_fwd")) return rc;
     return run_gemm(ctx, g, N, m_pad / BM, "conv_fwd",
                     2.0 * N * C_out * static_cast<double>(L_out) * C_in * k);
@@ -1363,8 +1447,14 @@ int kdec_conv1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
         hipLaunchKernelGGL(pack_octet, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), 1, C_in,
                            C_out, k, 1, k, m_pad, static_cast<int>(tot), 1);
     else
-        hipLaunchKernelGGL(pack_dgrad, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), C_in,
-                           C_out, k, g.cin_pad, m_pad, g.CK);
+        if (g.cin_pad % g.CK == 0 && m_pad % 64 == 0 && k <= 32)
+            hipLaunchKernelGGL(pack_dgrad_t, dim3(static_cast<unsigned>(cdiv(g.cin_pad, 4)),
+                                                  static_cast<unsigned>(m_pad / 64)),
+                               dim3(256), 4 * 64 * k * sizeof(float), ctx->stream, W, A.as<float>(), C_in, C_out, k,
+                               g.cin_pad, m_pad, g.CK);
+        else
+            hipLaunchKernelGGL(pack_dgrad, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), C_in,
+                               C_out, k, g.cin_pad, m_pad, g.CK);
     if (int rc = launch_check(ctx, "pack_dgrad")) return rc;
     return run_gemm(ctx, g, N, m_pad / BM, "conv_dgrad",
                     2.0 * N * C_out * static_cast<double>(L_out) * C_in * k);
@@ -1500,12 +1590,18 @@ static int bias_grad_only(kdec_ctx* ctx, const float* G, long g_bs, float* db, i
     long S = std::min(cdiv(4L * ctx->num_cus, M), cdiv(L, 1024));
     if (S > 256) S = 256;
     if (S < 1) S = 1;
-    const int per = static_cast<int>(cdiv(L, S));
+    const bool v4 = L % 4 == 0 && g_bs % 4 == 0 && (reinterpret_cast<unsigned long long>(G) & 15) == 0;
+    int per = static_cast<int>(cdiv(L, S));
+    if (v4) per = (per + 3) & ~3;
     S = cdiv(L, per);
     Workspace part(ctx, static_cast<size_t>(S) * M * sizeof(float));
     if (!part.p) return KDEC_ENOMEM;
-    hipLaunchKernelGGL(bias_partial, dim3(M, static_cast<unsigned>(S)), dim3(256), 0, ctx->stream, G, g_bs,
-                       part.as<float>(), N, M, L, per);
+    if (v4)
+        hipLaunchKernelGGL(bias_partial<4>, dim3(M, static_cast<unsigned>(S)), dim3(256), 0, ctx->stream, G, g_bs,
+                           part.as<float>(), N, M, L, per);
+    else
+        hipLaunchKernelGGL(bias_partial<1>, dim3(M, static_cast<unsigned>(S)), dim3(256), 0, ctx->stream, G, g_bs,
+                           part.as<float>(), N, M, L, per);
     if (int rc = launch_check(ctx, "bias_partial")) return rc;
     hipLaunchKernelGGL(bias_reduce, dim3(static_cast<unsigned>(cdiv(M, 4))), dim3(256), 0, ctx->stream,
                        part.as<float>(), db, M, static_cast<int>(S));
@@ -1585,8 +1681,13 @@ int kdec_convt1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
     const long tot = static_cast<long>(cpad) * k * m_pad;
     Workspace A(ctx, static_cast<size_t>(tot) * sizeof(float));
     if (!A.p) return KDEC_ENOMEM;
-    hipLaunchKernelGGL(pack_convt_dgrad, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(),
-                       C_in, C_out, k, cpad, m_pad, CK);
+    if (cpad % CK == 0 && m_pad % 64 == 0)
+        hipLaunchKernelGGL(pack_rows_t, dim3(static_cast<unsigned>(cdiv(static_cast<long>(cpad) * k, 64)),
+                                             static_cast<unsigned>(m_pad / 64)),
+                           dim3(256), 0, ctx->stream, W, A.as<float>(), C_in, C_out, k, cpad, m_pad, CK);
+    else
+        hipLaunchKernelGGL(pack_convt_dgrad, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(),
+                           C_in, C_out, k, cpad, m_pad, CK);
     if (int rc = launch_check(ctx, "pack_convt_dgrad")) return rc;
     GemmArgs g{};
     g.X = dY; g.x_bs = dy_bs; g.A = A.as<float>();
