@@ -174,6 +174,10 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ref-steps", type=int, default=3, help="steps of the reference-semantics mode")
     ap.add_argument("--no-micro", action="store_true", help="skip the per-kernel-class microbenchmarks")
+    ap.add_argument("--no-serving", action="store_true",
+                    help="skip the inference-forward and DecoderLora-step lines (profiles of the training step)")
+    ap.add_argument("--micro-only", action="store_true",
+                    help="run only the per-kernel-class microbenchmarks and print their JSON (for profiling them)")
     ap.add_argument("--serial", action="store_true",
                     help="one stream (no harmonic-source / weight-grad overlap): per-family times without sharing")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -200,6 +204,9 @@ def main(argv=None):
         torch.cuda.synchronize()
         del src, dst
     ctx = native.Context(0)
+    if a.micro_only:
+        print(json.dumps({"micro": micro_benches(ctx)}), flush=True)
+        return 0
     model = native.Model(ctx, cfg)
     shapes = model.param_shapes()
     params = synth.init_params(shapes)
@@ -304,8 +311,9 @@ def main(argv=None):
         "reference_semantics": ref,
         "streams": 1 if a.serial else 2,
     }
-    out["inference"] = inference_bench(ctx, model, t_asr, t_F0, t_N, t_style, audio, audio_per_step)
-    out["lora_train_step"] = lora_bench(model, t_asr, t_F0, t_N, t_style, t_dA, audio_per_step)
+    if not a.no_serving:
+        out["inference"] = inference_bench(ctx, model, t_asr, t_F0, t_N, t_style, audio, audio_per_step)
+        out["lora_train_step"] = lora_bench(model, t_asr, t_F0, t_N, t_style, t_dA, audio_per_step)
     if not a.no_micro:
         out["micro"] = micro_benches(ctx)
     if not a.no_cpu_baseline:
