@@ -31,14 +31,8 @@ B, T = 8, 512
 
 
 def make_inputs(cfg, N, T, tag, unvoiced=0.2):
-    from brosoundml_amd import config as C, synth
-    asr = synth.normal(f"{tag}.asr", (N, cfg["asr_dim"], T))
-    F0 = synth.uniform(f"{tag}.F0", (N, 2 * T), 80.0, 300.0)
-    F0[synth.uniform(f"{tag}.uv", (N, 2 * T), 0.0, 1.0) < unvoiced] = 0.0
-    Nn = synth.normal(f"{tag}.N", (N, 2 * T), 0.5)
-    style = synth.normal(f"{tag}.style", (N, cfg["style_dim"]), 0.3)
-    dA = synth.normal(f"{tag}.daudio", (N, C.lengths(cfg, T)["audio"]), 1.0)
-    return asr, F0, Nn, style, dA
+    from brosoundml_amd import synth
+    return synth.decoder_inputs(cfg, N, T, tag, unvoiced)
 
 
 def cpu_baseline(cfg, params):

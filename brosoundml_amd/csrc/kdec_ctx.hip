@@ -3,7 +3,9 @@
 // this state implicitly.
 #include "kdec_internal.hpp"
 
+#include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 
 namespace kdec {
 
@@ -17,49 +19,118 @@ int hip_fail(kdec_ctx* ctx, hipError_t e, const char* where) {
                 std::string(where) + ": " + hipGetErrorString(e));
 }
 
+namespace {
+
+constexpr size_t kGuard = 64 << 10;         // bytes of each guard band
+constexpr unsigned kGuardWord = 0x7FBADBADu;  // a quiet-NaN bit pattern
+
+// Fills both guard bands of a block handed out at `user` (bytes long).
+void guard_fill(kdec_ctx* ctx, const kdec_ctx::Block& b) {
+    char* base = static_cast<char*>(b.base);
+    hipMemsetD32Async(base, static_cast<int>(kGuardWord), kGuard / 4, ctx->stream);
+    hipMemsetD32Async(base + kGuard + b.bytes, static_cast<int>(kGuardWord), kGuard / 4, ctx->stream);
+}
+
+// Checks both bands of one block (the stream must be synchronised); returns
+// the number of overwritten bands and reports each.
+int guard_check(kdec_ctx* ctx, void* user, const kdec_ctx::Block& b, const char* where) {
+    static std::vector<unsigned> h(kGuard / 4);
+    int hits = 0;
+    for (int side = 0; side < 2; ++side) {
+        const char* band = static_cast<const char*>(b.base) + (side ? kGuard + b.bytes : 0);
+        if (hipMemcpy(h.data(), band, kGuard, hipMemcpyDeviceToHost) != hipSuccess) return hits;
+        size_t first = h.size(), last = 0, n = 0;
+        for (size_t i = 0; i < h.size(); ++i)
+            if (h[i] != kGuardWord) {
+                first = std::min(first, i);
+                last = i;
+                ++n;
+            }
+        if (!n) continue;
+        ++hits;
+        char msg[320];
+        std::snprintf(msg, sizeof(msg),
+                      "guard band %s the %zu-byte block at %p overwritten (%zu words, band words %zu..%zu), "
+                      "found at %s",
+                      side ? "after" : "before", b.bytes, user, n, first, last, where);
+        std::fprintf(stderr, "kdec: %s\n", msg);
+        ctx->err = std::string("brosoundml: ") + msg;
+        // restore the band so a later check reports only new writes
+        hipMemsetD32(const_cast<char*>(band), static_cast<int>(kGuardWord), kGuard / 4);
+    }
+    return hits;
+}
+
+}  // namespace
+
+int guard_mode() {
+    static const int mode = [] {
+        const char* e = std::getenv("KDEC_GUARD");
+        return e ? std::atoi(e) : 0;
+    }();
+    return mode;
+}
+
+int guard_check_all(kdec_ctx* ctx, const char* where) {
+    if (!guard_mode()) return 0;
+    hipStreamSynchronize(ctx->stream);
+    int hits = 0;
+    for (const auto& kv : ctx->live) hits += guard_check(ctx, kv.first, kv.second, where);
+    return hits;
+}
+
 void* ws_alloc(kdec_ctx* ctx, size_t bytes) {
     if (bytes == 0) bytes = 256;
     bytes = (bytes + 255) & ~size_t(255);
-    // Reuse a pooled block of at least `bytes` but not absurdly larger.
-    auto it = ctx->pool.lower_bound(bytes);
-    if (it != ctx->pool.end() && it->first <= bytes * 2 + (1 << 20)) {
-        void* p = it->second;
-        ctx->live[p] = it->first;
+    const size_t need = guard_mode() ? bytes + 2 * kGuard : bytes;
+    void* base = nullptr;
+    size_t size = need;
+    // Reuse a pooled block of at least `need` bytes but not absurdly larger.
+    auto it = ctx->pool.lower_bound(need);
+    if (it != ctx->pool.end() && it->first <= need * 2 + (1 << 20)) {
+        base = it->second;
+        size = it->first;
         ctx->pooled_bytes -= it->first;
         ctx->pool.erase(it);
-        return p;
-    }
-    void* p = nullptr;
-    hipError_t e = hipMalloc(&p, bytes);
-    if (e != hipSuccess) {
-        // Return every pooled block to the driver and try once more.
-        hipStreamSynchronize(ctx->stream);
-        for (auto& kv : ctx->pool) hipFree(kv.second);
-        ctx->pool.clear();
-        ctx->pooled_bytes = 0;
-        e = hipMalloc(&p, bytes);
+    } else {
+        hipError_t e = hipMalloc(&base, need);
         if (e != hipSuccess) {
-            hip_fail(ctx, e, "hipMalloc");
-            return nullptr;
+            // Return every pooled block to the driver and try once more.
+            hipStreamSynchronize(ctx->stream);
+            for (auto& kv : ctx->pool) hipFree(kv.second);
+            ctx->pool.clear();
+            ctx->pooled_bytes = 0;
+            e = hipMalloc(&base, need);
+            if (e != hipSuccess) {
+                hip_fail(ctx, e, "hipMalloc");
+                return nullptr;
+            }
         }
     }
-    ctx->live[p] = bytes;
-    return p;
+    const kdec_ctx::Block blk{base, size, bytes};
+    void* user = guard_mode() ? static_cast<char*>(base) + kGuard : base;
+    if (guard_mode()) guard_fill(ctx, blk);
+    ctx->live[user] = blk;
+    return user;
 }
 
 void ws_free(kdec_ctx* ctx, void* p) {
     if (!p) return;
     auto it = ctx->live.find(p);
     if (it == ctx->live.end()) return;
+    const kdec_ctx::Block blk = it->second;
+    if (guard_mode()) {
+        hipStreamSynchronize(ctx->stream);
+        guard_check(ctx, p, blk, "free");
+    }
+    ctx->live.erase(it);
     if (ctx->destroyed) {
-        hipFree(p);
-        ctx->live.erase(it);
+        hipFree(blk.base);
         if (ctx->live.empty()) delete ctx;
         return;
     }
-    ctx->pool.emplace(it->second, p);
-    ctx->pooled_bytes += it->second;
-    ctx->live.erase(it);
+    ctx->pool.emplace(blk.size, blk.base);
+    ctx->pooled_bytes += blk.size;
 }
 
 static hipEvent_t get_event(kdec_ctx* ctx) {
@@ -75,14 +146,14 @@ static hipEvent_t get_event(kdec_ctx* ctx) {
 
 ProfScope::ProfScope(kdec_ctx* c, const char* n, double f, double b)
     : ctx(c), name(n), flops(f), bytes(b) {
-    if (ctx->prof) {
+    if (ctx && ctx->prof) {
         start = get_event(ctx);
         hipEventRecord(start, ctx->stream);
     }
 }
 
 ProfScope::~ProfScope() {
-    if (!ctx->prof || !start) return;
+    if (!ctx || !ctx->prof || !start) return;
     hipEvent_t stop = get_event(ctx);
     hipEventRecord(stop, ctx->stream);
     auto& f = ctx->fams[name];
@@ -95,6 +166,7 @@ ProfScope::~ProfScope() {
 int launch_check(kdec_ctx* ctx, const char* where) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(ctx, e, where);
+    if (guard_mode() >= 2 && guard_check_all(ctx, where)) return KDEC_EHIP;
     return KDEC_OK;
 }
 
@@ -173,6 +245,7 @@ void* kdec_get_stream(const kdec_ctx* ctx) { return ctx ? ctx->stream : nullptr;
 int kdec_synchronize(kdec_ctx* ctx) {
     if (!ctx) return KDEC_EINVAL;
     KDEC_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (guard_check_all(ctx, "kdec_synchronize")) return KDEC_EHIP;
     return KDEC_OK;
 }
 

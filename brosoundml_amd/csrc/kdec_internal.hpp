@@ -22,8 +22,13 @@ struct kdec_ctx {
     // Stream-ordered caching allocator: every kernel of a context runs on one
     // stream, so a block returned to the pool can be handed out again at once;
     // stream order keeps the reuse behind the previous user's kernels.
-    std::multimap<size_t, void*> pool;
-    std::unordered_map<void*, size_t> live;
+    std::multimap<size_t, void*> pool;  // block size -> block base
+    struct Block {
+        void* base;    // start of the device block
+        size_t size;   // bytes of the device block
+        size_t bytes;  // bytes handed out (after the front guard in guard mode)
+    };
+    std::unordered_map<void*, Block> live;  // handed-out pointer -> its block
     size_t pooled_bytes = 0;
     // Set by kdec_ctx_destroy while blocks are still live (tensors that
     // outlive their context): the last ws_free then releases the context.
@@ -78,7 +83,8 @@ struct Workspace {
     template <class T> T* as() const { return static_cast<T*>(p); }
 };
 
-// Profiling bracket around the launches of one kernel family.
+// Profiling bracket around the launches of one kernel family (a null
+// context records nothing).
 struct ProfScope {
     kdec_ctx* ctx;
     const char* name;
@@ -92,8 +98,18 @@ struct ProfScope {
 // (defined with the brotensor runtime, tensor.cpp).
 void forget_runtime(kdec_ctx* ctx);
 
-// Checks the last launch; returns KDEC_OK or the HIP error code.
+// Checks the last launch; returns KDEC_OK or the HIP error code. In guard
+// mode 2 it also synchronises and checks every live block's guard bands.
 int launch_check(kdec_ctx* ctx, const char* where);
+
+// Guard mode (environment KDEC_GUARD=1 or 2): every workspace block sits
+// between two guard bands of a fixed word pattern; a write past either end
+// of a block lands in a band and is reported (stderr and the context error)
+// when the block is freed, at kdec_synchronize, and with KDEC_GUARD=2 after
+// every launch, naming that launch. A debugging aid: it costs a device sync
+// per check. Returns the number of overwritten bands found.
+int guard_mode();
+int guard_check_all(kdec_ctx* ctx, const char* where);
 
 inline long cdiv(long a, long b) { return (a + b - 1) / b; }
 

@@ -756,6 +756,81 @@ const float* kdec_model_gen_in(const kdec_model* m) {
     return m ? static_cast<const float*>(m->gen_in.data) : nullptr;
 }
 
+// ─── leaky-ReLU sites (inspection) ──────────────────────────────────────────
+
+int kdec_model_leaky_site_count(const kdec_model* m) {
+    return m ? 2 * (1 + m->n_decode) + m->n_ups + 1 : 0;
+}
+
+long kdec_model_leaky_size(kdec_model* m, int site) {
+    if (!m || m->N == 0 || m->genc.stages.empty() || site < 0 || site >= kdec_model_leaky_site_count(m)) {
+        if (m) fail(m, KDEC_EINVAL, "kdec_model_leaky_size: no training forward or site out of range");
+        return -1;
+    }
+    const int n_blocks = 1 + m->n_decode;
+    if (site < 2 * n_blocks) {
+        const int b = site / 2;
+        const bd::AdainResBlkCache& c = b == 0 ? m->bbc.encode : m->bbc.decode[b - 1];
+        const brosoundml::AdainResBlk1dWeights& w = b == 0 ? m->bb.encode : m->bb.decode[b - 1];
+        return site % 2 ? static_cast<long>(m->N) * w.channels_out * c.L_out
+                        : static_cast<long>(m->N) * w.channels_in * c.L_in;
+    }
+    const Tensor& t = site < 2 * n_blocks + m->n_ups ? m->genc.stages[site - 2 * n_blocks].x_in : m->genc.head.x_pre;
+    return static_cast<long>(t.size());
+}
+
+int kdec_model_leaky_input(kdec_model* m, int site, float* host, long n) {
+    if (!m || !host) return KDEC_EINVAL;
+    if (m->N == 0 || m->genc.stages.empty())
+        return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: no training forward to inspect");
+    const int n_blocks = 1 + m->n_decode;
+    if (site < 0 || site >= kdec_model_leaky_site_count(m))
+        return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: site out of range");
+    try {
+        bt::set_runtime(m->ctx);
+        const int N = m->N;
+        Tensor t;
+        if (site < 2 * n_blocks) {
+            // an AdaIN residual block's norm output, recomputed from the cached
+            // input and statistics as the backward recomputes it
+            const int b = site / 2;
+            const bool second = site % 2;
+            const bd::AdainResBlkCache& c = b == 0 ? m->bbc.encode : m->bbc.decode[b - 1];
+            const brosoundml::AdainResBlk1dWeights& w = b == 0 ? m->bb.encode : m->bb.decode[b - 1];
+            const bd::BlockAffines& a = m->bbaff[b];
+            const Tensor& x = second ? c.conv1_out : c.x;
+            const Tensor& st = second ? c.x_seq2 : c.x_seq1;
+            const Tensor& g = second ? a.g2 : a.g1;
+            const Tensor& be = second ? a.b2 : a.b1;
+            const int C = second ? w.channels_out : w.channels_in;
+            const int L = second ? c.L_out : c.L_in;
+            if (!x.data || !st.data) return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: no cache for this site");
+            t = Tensor::empty_on(Device::HIP, N, C * L);
+            const long gbs = N == 1 ? 0 : g.row_stride();
+            if (int rc = check(m, kdec_adain_act_fwd(m->ctx, static_cast<const float*>(x.data), x.row_stride(),
+                                                     static_cast<const float*>(st.data),
+                                                     static_cast<const float*>(g.data),
+                                                     static_cast<const float*>(be.data), gbs, KDEC_ACT_NONE, 0.0f,
+                                                     nullptr, static_cast<float*>(t.data), t.row_stride(), nullptr,
+                                                     0, N, C, L)))
+                return rc;
+        } else if (site < 2 * n_blocks + m->n_ups) {
+            t = m->genc.stages[site - 2 * n_blocks].x_in;  // the stage input (leaky 0.1)
+        } else {
+            t = m->genc.head.x_pre;  // the spectral head input (leaky 0.01)
+        }
+        if (!t.data) return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: no cache for this site");
+        if (n != static_cast<long>(t.size()))
+            return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: site holds " + std::to_string(t.size()) +
+                                            " values, not " + std::to_string(n));
+        const std::vector<float> h = t.to_host_vector();
+        std::copy(h.begin(), h.end(), host);
+    } catch (const std::exception& e) {
+        return fail(m, KDEC_EHIP, e.what());
+    }
+    return KDEC_OK;
+}
+
 // ─── DecoderLora over the model's weights ───────────────────────────────────
 
 struct kdec_dlora {

@@ -226,6 +226,7 @@ class Model:
             audio = torch.empty(N, self.lengths(T)["audio"], device=asr.device, dtype=torch.float32)
         self._c(self.ctx.L.kdec_model_forward(self.h, N, T, ptr(asr), ptr(F0), ptr(Nn), ptr(style), ptr(har),
                                               ptr(audio)))
+        self.N_last = N
         return audio
 
     def backward(self, daudio, wgrad=True, dalpha=True, dstyle=None):
@@ -291,6 +292,31 @@ class Model:
 
     def har_ptr(self):
         return self.ctx.L.kdec_model_har(self.h)
+
+    def leaky_inputs(self):
+        """Host copies of every leaky-ReLU site's input of the last training
+        forward (kdec_model_leaky_input), in site order: a list of (N, C*L) arrays."""
+        import numpy as np
+        L = self.ctx.L
+        res = []
+        for site in range(L.kdec_model_leaky_site_count(self.h)):
+            n = L.kdec_model_leaky_size(self.h, site)
+            if n < 0:
+                raise KdecError(L.kdec_last_error(self.ctx.h).decode())
+            a = np.empty(n, np.float32)
+            self._c(L.kdec_model_leaky_input(self.h, site, a.ctypes.data_as(ctypes.c_void_p), n))
+            res.append(a.reshape(self.N_last, -1))
+        return res
+
+    def har(self, N, T):
+        """Host copy of the last forward's harmonic-source output (N, (n_fft+2)*frames)."""
+        import torch
+        n = (self.cfg["n_fft"] + 2) * self.lengths(T)["frames"]
+        t = torch.empty((N, n), dtype=torch.float32, device="cuda")
+        self.ctx.check(self.ctx.L.kdec_axpby(self.ctx.h, 1.0, ctypes.c_void_p(self.har_ptr()), n, 0.0, None, 0,
+                                             ptr(t), n, N, n))
+        self.ctx.synchronize()
+        return t.cpu().numpy()
 
 
 class DecoderLora:

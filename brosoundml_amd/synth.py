@@ -87,3 +87,20 @@ def init_params(shapes, base: int = BASE_SEED) -> dict:
         bound = 1.0 / math.sqrt(max(fan_in, 1))
         out[name] = uniform(name, (rows, cols), -bound, bound, base)
     return out
+
+
+def decoder_inputs(cfg: dict, N: int, T: int, tag: str, unvoiced: float = 0.0):
+    """Synthetic decoder inputs for N utterances of T asr frames, each tensor
+    from its own named sub-seed: asr ~ N(0, 1) (N, asr_dim, T), F0 ~ U(80, 300)
+    Hz (N, 2T) with a fraction `unvoiced` of frames set to 0, the N curve ~
+    N(0, 0.5) (N, 2T), style ~ N(0, 0.3) (N, style_dim) and dL/dwav ~ N(0, 1)
+    (N, audio_len)."""
+    from .config import lengths
+    asr = normal(f"{tag}.asr", (N, cfg["asr_dim"], T))
+    F0 = uniform(f"{tag}.F0", (N, 2 * T), 80.0, 300.0)
+    if unvoiced > 0.0:
+        F0[uniform(f"{tag}.uv", (N, 2 * T), 0.0, 1.0) < unvoiced] = 0.0
+    Nn = normal(f"{tag}.N", (N, 2 * T), 0.5)
+    style = normal(f"{tag}.style", (N, cfg["style_dim"]), 0.3)
+    dA = normal(f"{tag}.daudio", (N, lengths(cfg, T)["audio"]), 1.0)
+    return asr, F0, Nn, style, dA

@@ -167,6 +167,22 @@ int kdec_dlora_load(kdec_dlora* d, const char* path);
 float* kdec_dlora_ptr(kdec_dlora* d, int which, int* rows, int* cols);
 float kdec_dlora_scale(const kdec_dlora* d);
 
+/* Leaky-ReLU sites of the decoder, in the order the forward visits them:
+ * per AdaIN residual block (encode, decode.0, ...) the norm1 output and the
+ * norm2 output (slope 0.2, kokoro_decoder_backward.cpp:172, 190), per
+ * generator stage the stage input (0.1, :613), then the spectral head input
+ * (0.01, :388). These are the decoder's only non-smooth points.
+ * kdec_model_leaky_input copies site `site`'s input (the value whose sign
+ * picks the slope, as the backward evaluates it) of the last training
+ * forward to host: N rows of C*L floats, n = N*C*L. An inspection aid in the
+ * spirit of the reference's KokoroTrace (kokoro.h): two float
+ * implementations can disagree on the sign of an input within rounding of
+ * zero, and a comparison of their grads needs to know where. */
+int kdec_model_leaky_site_count(const kdec_model* m);
+/* N*C*L of site `site` after the last training forward, or -1. */
+long kdec_model_leaky_size(kdec_model* m, int site);
+int kdec_model_leaky_input(kdec_model* m, int site, float* host, long n);
+
 /* Device pointers to the last forward's har (N, (n_fft+2)*frames) and
  * generator input (N, init_C * L_gen). */
 const float* kdec_model_har(const kdec_model* m);

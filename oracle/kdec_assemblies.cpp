@@ -11,7 +11,22 @@
 
 namespace KDO_NS {
 
+KinkMasks* g_kinks = nullptr;
+int g_kink_block = -1;
+int g_kink_gen = -1;
+
 namespace {
+
+// The mask of leaky site `site` when one is set for a tensor of n elements.
+const signed char* kink_mask(int site, std::size_t n) {
+    if (!g_kinks || site < 0 || site >= static_cast<int>(g_kinks->masks.size())) return nullptr;
+    const auto& m = g_kinks->masks[static_cast<std::size_t>(site)];
+    return m.size() == n ? m.data() : nullptr;
+}
+int block_site(int k) { return g_kink_block < 0 ? -1 : g_kink_block + k; }
+// site of the spectral head, set by the generator around its head calls
+int g_kink_head = -1;
+int gen_site(int k) { return g_kink_gen < 0 ? -1 : g_kink_gen + k; }
 
 Vec ones(int C) { return Vec(static_cast<std::size_t>(C), 1.0f); }
 Vec zeros(std::size_t n) { return Vec(n, 0.0f); }
@@ -49,14 +64,32 @@ void scale_inplace(Vec& a, float s) {
     for (auto& v : a) v *= s;
 }
 
-void leaky(const Vec& x, float slope, Vec& y) {
+// Leaky ReLU at `site` (-1: none); `count` tallies the elements whose own
+// sign a mask overrides (once per site and forward).
+void leaky(const Vec& x, float slope, Vec& y, int site = -1, bool count = false) {
     y.resize(x.size());
-    leaky_forward(x.data(), slope, x.size(), y.data());
+    const signed char* m = kink_mask(site, x.size());
+    if (!m) {
+        leaky_forward(x.data(), slope, x.size(), y.data());
+        return;
+    }
+    long flips = 0;
+    for (std::size_t i = 0; i < x.size(); ++i) {
+        const bool pos = m[i] != 0;
+        flips += pos != (x[i] > 0.0f);
+        y[i] = pos ? x[i] : slope * x[i];
+    }
+    if (count) g_kinks->flips[static_cast<std::size_t>(site)] += flips;
 }
 
-void leaky_bwd(const Vec& x, const Vec& dy, float slope, Vec& dx) {
+void leaky_bwd(const Vec& x, const Vec& dy, float slope, Vec& dx, int site = -1) {
     dx.resize(x.size());
-    leaky_backward(x.data(), dy.data(), slope, x.size(), dx.data());
+    const signed char* m = kink_mask(site, x.size());
+    if (!m) {
+        leaky_backward(x.data(), dy.data(), slope, x.size(), dx.data());
+        return;
+    }
+    for (std::size_t i = 0; i < x.size(); ++i) dx[i] = m[i] ? dy[i] : slope * dy[i];
 }
 
 // Channel concat of (C_i, L) parts (kokoro_decoder_backward.cpp:465-478).
@@ -125,7 +158,7 @@ void adain_resblk_1d_forward_train(const AdainResBlk1dWeights& w, const Vec& x,
 
     adain_affine_forward(x, g1, b1, C_in, L_in, eps, cache.r_pre, cache.x_seq1);
     Vec r;
-    leaky(cache.r_pre, 0.2f, r);
+    leaky(cache.r_pre, 0.2f, r, block_site(0), true);
     Vec pooled;
     if (w.upsample) {
         pooled.assign(static_cast<std::size_t>(C_in) * L_out, 0.0f);
@@ -138,7 +171,7 @@ void adain_resblk_1d_forward_train(const AdainResBlk1dWeights& w, const Vec& x,
     adain_affine_forward(cache.conv1_out, g2, b2, C_out, L_out, eps,
                          cache.n2_pre, cache.x_seq2);
     Vec n2;
-    leaky(cache.n2_pre, 0.2f, n2);
+    leaky(cache.n2_pre, 0.2f, n2, block_site(1), true);
     Vec conv2_out;
     conv_fwd(w.conv2, n2, L_out, conv2_out);
 
@@ -178,11 +211,11 @@ void adain_resblk_1d_backward(AdainResBlk1dWeights& w,
     conv_dgrad(w.conv2, d_branch, L_out, d_n2);
     if (wg) {
         Vec n2;
-        leaky(cache.n2_pre, 0.2f, n2);
+        leaky(cache.n2_pre, 0.2f, n2, block_site(1));
         conv_wgrad(w.conv2, n2, L_out, d_branch);
     }
     Vec d_n2_pre;
-    leaky_bwd(cache.n2_pre, d_n2, 0.2f, d_n2_pre);
+    leaky_bwd(cache.n2_pre, d_n2, 0.2f, d_n2_pre, block_site(1));
     Vec d_conv1_out;
     adain_affine_backward(cache.conv1_out, cache.x_seq2, g2, d_n2_pre, C_out,
                           L_out, eps, d_conv1_out, dG2, dB2);
@@ -190,7 +223,7 @@ void adain_resblk_1d_backward(AdainResBlk1dWeights& w,
     Vec d_pooled;
     conv_dgrad(w.conv1, d_conv1_out, L_out, d_pooled);
     Vec r;
-    if (wg || w.upsample) leaky(cache.r_pre, 0.2f, r);
+    if (wg || w.upsample) leaky(cache.r_pre, 0.2f, r, block_site(0));
     if (wg) {
         Vec pooled;
         if (w.upsample) {
@@ -218,7 +251,7 @@ void adain_resblk_1d_backward(AdainResBlk1dWeights& w,
         d_r = d_pooled;
     }
     Vec d_r_pre;
-    leaky_bwd(cache.r_pre, d_r, 0.2f, d_r_pre);
+    leaky_bwd(cache.r_pre, d_r, 0.2f, d_r_pre, block_site(0));
     Vec dX_res;
     adain_affine_backward(cache.x, cache.x_seq1, g1, d_r_pre, C_in, L_in, eps,
                           dX_res, dG1, dB1);
@@ -344,7 +377,7 @@ void spectral_head_forward_train(const Conv1d& conv_post, const Vec& x, int C,
     cache.L = L;
     cache.x_pre = x;
     Vec xl;
-    leaky(x, 0.01f, xl);
+    leaky(x, 0.01f, xl, g_kink_head, true);
     conv_fwd(conv_post, xl, L, cache.post);
     const int F = n_fft / 2 + 1;
     Vec spec(static_cast<std::size_t>(L) * 2 * F);
@@ -394,10 +427,10 @@ void spectral_head_backward(Conv1d& conv_post, const SpectralHeadCache& cache,
     conv_dgrad(conv_post, dpost, L, dXl);
     if (ext && ext->wgrad) {
         Vec xl;
-        leaky(cache.x_pre, 0.01f, xl);
+        leaky(cache.x_pre, 0.01f, xl, g_kink_head);
         conv_wgrad(conv_post, xl, L, dpost);
     }
-    leaky_bwd(cache.x_pre, dXl, 0.01f, dX);
+    leaky_bwd(cache.x_pre, dXl, 0.01f, dX, g_kink_head);
     (void)C;
 }
 
@@ -423,6 +456,7 @@ void decoder_backbone_forward_train(const DecoderBackbone& bb, const Vec& asr,
     Vec dec_pre = cat_channels({&asr, &cache.F0_dn, &cache.N_dn});
     int L_after = 0;
     Vec x;
+    g_kink_block = g_kinks ? 0 : -1;
     adain_resblk_1d_forward_train(bb.encode, dec_pre, T, aff[0].g1, aff[0].b1,
                                   aff[0].g2, aff[0].b2, eps, L_after, x,
                                   cache.encode);
@@ -439,6 +473,7 @@ void decoder_backbone_forward_train(const DecoderBackbone& bb, const Vec& asr,
         }
         int L_next = 0;
         Vec y;
+        g_kink_block = g_kinks ? 2 * (1 + i) : -1;
         adain_resblk_1d_forward_train(bb.decode[i], blk_in, L_now, aff[1 + i].g1,
                                       aff[1 + i].b1, aff[1 + i].g2,
                                       aff[1 + i].b2, eps, L_next, y,
@@ -447,6 +482,7 @@ void decoder_backbone_forward_train(const DecoderBackbone& bb, const Vec& asr,
         L_now = L_next;
         if (bb.decode[i].upsample) res = false;
     }
+    g_kink_block = -1;
     gen_in = x;
 }
 
@@ -470,6 +506,7 @@ void decoder_backbone_backward(DecoderBackbone& bb, const BackboneCache& cache,
     for (int i = n_dec - 1; i >= 0; --i) {
         Vec blk_dX;
         BlockAffines& g = dAff[1 + i];
+        g_kink_block = g_kinks ? 2 * (1 + i) : -1;
         adain_resblk_1d_backward(bb.decode[i], cache.decode[i], aff[1 + i].g1,
                                  aff[1 + i].g2, dX, eps, blk_dX, g.g1, g.b1,
                                  g.g2, g.b2, ext);
@@ -491,8 +528,10 @@ void decoder_backbone_backward(DecoderBackbone& bb, const BackboneCache& cache,
     }
     Vec enc_dX;
     BlockAffines& ge = dAff[0];
+    g_kink_block = g_kinks ? 0 : -1;
     adain_resblk_1d_backward(bb.encode, cache.encode, aff[0].g1, aff[0].g2, dX,
                              eps, enc_dX, ge.g1, ge.b1, ge.g2, ge.b2, ext);
+    g_kink_block = -1;
     if (wg) {
         const std::size_t n_asr = cache.asr.size();
         const Real* base = enc_dX.data() + n_asr;
@@ -523,7 +562,7 @@ void generator_forward_train(const Generator& gen, const Vec& gen_in, int L_in,
         sc.C_in = gen.ups_C_in[i];
         sc.L_in = L;
         Vec a;
-        leaky(x, 0.1f, a);
+        leaky(x, 0.1f, a, gen_site(i), true);
 
         Vec x_source;
         conv_fwd(gen.noise_convs[i], har, frames, x_source);
@@ -568,9 +607,11 @@ void generator_forward_train(const Generator& gen, const Vec& gen_in, int L_in,
         L = L_x;
     }
     cache.window = hann_periodic(gen.win_size);
+    g_kink_head = gen_site(gen.num_upsamples);
     spectral_head_forward_train(gen.conv_post, x, gen.ups_C_out[gen.num_upsamples - 1],
                                 L, cache.window, gen.n_fft, gen.hop_size,
                                 gen.win_size, audio, cache.head);
+    g_kink_head = -1;
 }
 
 // kokoro_decoder_backward.cpp:669-737. With ext->wgrad the noise branch's dX
@@ -588,8 +629,10 @@ void generator_backward(Generator& gen, const GeneratorCache& cache,
     draff.assign(static_cast<std::size_t>(U) * K, ResBlock1Affines{});
 
     Vec dX;
+    g_kink_head = gen_site(U);
     spectral_head_backward(gen.conv_post, cache.head, cache.window, gen.n_fft,
                            gen.hop_size, gen.win_size, dAudio, dX, ext);
+    g_kink_head = -1;
     for (int i = U - 1; i >= 0; --i) {
         const GenStageCache& sc = cache.stages[i];
         const int L = sc.L_out;
@@ -627,7 +670,7 @@ void generator_backward(Generator& gen, const GeneratorCache& cache,
                                gen.ups_pad[i], 0, 1, 1, da.data());
         if (wg) {
             Vec a;
-            leaky(sc.x_in, 0.1f, a);
+            leaky(sc.x_in, 0.1f, a, gen_site(i));
             if (gen.dups_W[i].size() != gen.ups_W[i].size()) gen.dups_W[i].assign(gen.ups_W[i].size(), 0.0f);
             if (gen.dups_b[i].size() != gen.ups_b[i].size()) gen.dups_b[i].assign(gen.ups_b[i].size(), 0.0f);
             convt1d_backward_weight(a.data(), du.data(), sc.C_in, sc.L_in,
@@ -636,7 +679,7 @@ void generator_backward(Generator& gen, const GeneratorCache& cache,
                                     gen.dups_W[i].data(), gen.dups_b[i].data());
         }
         Vec dx_in;
-        leaky_bwd(sc.x_in, da, 0.1f, dx_in);
+        leaky_bwd(sc.x_in, da, 0.1f, dx_in, gen_site(i));
         dX = dx_in;
     }
     dGenIn = dX;

@@ -318,8 +318,25 @@ void Model::lora_enable(int rank, float scale) {
     dgate.assign(static_cast<std::size_t>(rank), 0.0f);
 }
 
+namespace {
+// Installs a model's leaky-site masks for the duration of a pass.
+struct KinkScope {
+    explicit KinkScope(Model& m) {
+        if (m.kinks.masks.empty()) return;
+        g_kinks = &m.kinks;
+        g_kink_gen = 2 * (1 + m.cfg.n_decode);
+    }
+    ~KinkScope() {
+        g_kinks = nullptr;
+        g_kink_gen = -1;
+    }
+};
+}  // namespace
+
 void Model::forward(const Vec& asr, const Vec& F0, const Vec& N,
                     const Vec& style_in, int T_in, const Vec* har_in) {
+    KinkScope ks(*this);
+    kinks.flips.assign(kinks.masks.size(), 0);
     T = T_in;
     style = style_in;
     for (auto& u : units) {
@@ -349,6 +366,7 @@ void Model::forward(const Vec& asr, const Vec& F0, const Vec& N,
 }
 
 void Model::backward(const Vec& dAudio, const Ext& ext, bool want_dstyle) {
+    KinkScope ks(*this);
     Vec dGenIn;
     std::vector<ResBlock1Affines> dn, dr;
     generator_backward(gen, genc, naff, raff, dAudio, dGenIn, dn, dr, &ext);

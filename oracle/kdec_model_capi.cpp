@@ -33,6 +33,17 @@ int guard(F&& f) {
 }
 
 Vec vec(const float* p, std::size_t n) { return Vec(p, p + n); }
+// The oracle's own input at leaky site `site` after a forward.
+const Vec& leaky_site_input(Model& m, int site) {
+    const int nb = 1 + m.cfg.n_decode;
+    if (site >= 0 && site < 2 * nb) {
+        const AdainResBlkCache& c = site / 2 == 0 ? m.bbc.encode : m.bbc.decode[static_cast<std::size_t>(site / 2 - 1)];
+        return site % 2 ? c.n2_pre : c.r_pre;
+    }
+    if (site >= 2 * nb && site < 2 * nb + m.cfg.n_ups) return m.genc.stages[static_cast<std::size_t>(site - 2 * nb)].x_in;
+    if (site == 2 * nb + m.cfg.n_ups) return m.genc.head.x_pre;
+    throw std::runtime_error("ko_model_leaky_input: site out of range");
+}
 void out(float* dst, const Vec& v) {
     for (std::size_t i = 0; i < v.size(); ++i) dst[i] = static_cast<float>(v[i]);
 }
@@ -198,6 +209,54 @@ int KO_FN(model_get_audio_f64)(void* m, double* dst) {
     return 0;
 }
 long KO_FN(model_audio_len)(void* m) { return static_cast<long>(static_cast<Model*>(m)->audio.size()); }
+// Leaky-site masks (KinkMasks): site count; set site `site` from the signs
+// of `pre` (n values; the site's input as another implementation computed
+// it); clear all; elements whose own sign the last forward overrode at
+// `site` (-1: all sites).
+int KO_FN(model_kink_site_count)(void* m) { return static_cast<Model*>(m)->kink_site_count(); }
+int KO_FN(model_set_kink)(void* mp, int site, const float* pre, long n) {
+    return guard([&] {
+        Model& m = *static_cast<Model*>(mp);
+        if (site < 0 || site >= m.kink_site_count()) throw std::runtime_error("ko_model_set_kink: site out of range");
+        m.kinks.masks.resize(static_cast<std::size_t>(m.kink_site_count()));
+        auto& mk = m.kinks.masks[static_cast<std::size_t>(site)];
+        mk.resize(static_cast<std::size_t>(n));
+        for (long i = 0; i < n; ++i) mk[static_cast<std::size_t>(i)] = pre[i] > 0.0f ? 1 : 0;
+    });
+}
+int KO_FN(model_clear_kinks)(void* m) {
+    static_cast<Model*>(m)->kinks = KinkMasks{};
+    return 0;
+}
+long KO_FN(model_kink_flips)(void* mp, int site) {
+    const Model& m = *static_cast<Model*>(mp);
+    long total = 0;
+    for (std::size_t s = 0; s < m.kinks.flips.size(); ++s)
+        if (site < 0 || static_cast<int>(s) == site) total += m.kinks.flips[s];
+    return total;
+}
+
+
+long KO_FN(model_leaky_size)(void* mp, int site) {
+    try {
+        return static_cast<long>(leaky_site_input(*static_cast<Model*>(mp), site).size());
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
+// The oracle's own input at leaky site `site` after a forward (n values).
+int KO_FN(model_leaky_input)(void* mp, int site, float* dst, long n) {
+    return guard([&] {
+        Model& m = *static_cast<Model*>(mp);
+        const Vec* v = &leaky_site_input(m, site);
+        if (static_cast<long>(v->size()) != n)
+            throw std::runtime_error("ko_model_leaky_input: site holds " + std::to_string(v->size()) + " values");
+        out(dst, *v);
+    });
+}
+
 long KO_FN(model_har_len)(void* m) { return static_cast<long>(static_cast<Model*>(m)->har.size()); }
 long KO_FN(model_gen_in_len)(void* m) { return static_cast<long>(static_cast<Model*>(m)->gen_in.size()); }
 int KO_FN(model_get_audio)(void* m, float* dst) {

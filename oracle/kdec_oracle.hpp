@@ -200,6 +200,30 @@ struct Ext {
     bool dalpha = false;  // snake alpha grads
 };
 
+// Kink overrides. The leaky ReLUs are the decoder's only non-smooth points.
+// Two float evaluations of the same forward can put an input that lies within
+// rounding of zero on opposite sides of the kink; the slope's derivative then
+// differs by (1 - slope) at that element and the difference spreads into
+// every grad upstream of it (one such element among the 983 168 inputs of the
+// spectral head at T = 64 moves every AdaIN affine grad by about 2e-3). With
+// masks set on a Model, each leaky site takes its branch (x > 0) from the
+// mask, in the forward and in the backward, so the oracle is evaluated on the
+// same linear piece as the implementation the mask came from. Sites, in
+// forward order: per AdaIN residual block (encode, decode.0, ...) the norm1
+// output then the norm2 output (slope 0.2); per generator stage the stage
+// input (0.1); the spectral head input (0.01).
+struct KinkMasks {
+    std::vector<std::vector<signed char>> masks;  // per site, empty = own sign
+    std::vector<long> flips;                      // per site: own signs overridden
+};
+// Set while Model::forward / ::backward run with masks: the model's masks,
+// the site of the AdaIN residual block being run (its norm1; norm2 is + 1),
+// and the site of generator stage 0 (stage i at + i, the spectral head at
+// + num_upsamples). -1: no override.
+extern KinkMasks* g_kinks;
+extern int g_kink_block;
+extern int g_kink_gen;
+
 // ─── assembly atoms (kokoro_decoder_backward.h) ─────────────────────────────
 
 void adain_affine_forward(const Vec& x, const Vec& gamma, const Vec& beta,
@@ -371,6 +395,9 @@ struct Model {
     float lora_scale = 0.0f;
     Vec gate, dgate;
     void lora_enable(int rank, float scale);
+    // Leaky-site masks (see KinkMasks); none by default.
+    KinkMasks kinks;
+    int kink_site_count() const { return 2 * (1 + cfg.n_decode) + cfg.n_ups + 1; }
 
     explicit Model(const Config& c);
     Model(const Model&) = delete;

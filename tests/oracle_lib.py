@@ -67,6 +67,14 @@ def lib():
             f("model_lora_get_grad").argtypes = [ctypes.c_void_p, ctypes.c_int, _fp, _fp]
             f("model_lora_gate").argtypes = [ctypes.c_void_p, _dp]
             f("model_lora_get_dgate").argtypes = [ctypes.c_void_p, _fp]
+            f("model_kink_site_count").argtypes = [ctypes.c_void_p]
+            f("model_set_kink").argtypes = [ctypes.c_void_p, ctypes.c_int, _fp, ctypes.c_long]
+            f("model_clear_kinks").argtypes = [ctypes.c_void_p]
+            f("model_kink_flips").restype = ctypes.c_long
+            f("model_kink_flips").argtypes = [ctypes.c_void_p, ctypes.c_int]
+            f("model_leaky_input").argtypes = [ctypes.c_void_p, ctypes.c_int, _fp, ctypes.c_long]
+            f("model_leaky_size").restype = ctypes.c_long
+            f("model_leaky_size").argtypes = [ctypes.c_void_p, ctypes.c_int]
         L.ko_leaky_fwd.argtypes = [_fp, ctypes.c_float, ctypes.c_long, _fp]
         L.ko_leaky_bwd.argtypes = [_fp, _fp, ctypes.c_float, ctypes.c_long, _fp]
         for fn in ("ko_instnorm_fwd", "ko_adain_affine_fwd"):
@@ -423,6 +431,32 @@ class OracleModel:
         d = np.zeros(self.lora_rank, np.float32)
         self._check(self._f("model_lora_get_dgate")(self.h, P(d)))
         return d
+
+    # ─── leaky-site masks (see KinkMasks in oracle/kdec_oracle.hpp) ───
+    def kink_site_count(self):
+        return self._f("model_kink_site_count")(self.h)
+
+    def set_kinks(self, pre):
+        """Take every leaky site's branch from the signs of `pre` (a list of
+        per-site inputs computed by another implementation), forward and backward."""
+        self._f("model_clear_kinks")(self.h)
+        for site, v in enumerate(pre):
+            v = f32(v).ravel()
+            self._check(self._f("model_set_kink")(self.h, site, P(v), v.size))
+
+    def leaky_input(self, site):
+        """The oracle's own input at leaky site `site` after a forward."""
+        n = self._check(self._f("model_leaky_size")(self.h, site))
+        v = np.zeros(n, np.float32)
+        self._check(self._f("model_leaky_input")(self.h, site, P(v), n))
+        return v
+
+    def clear_kinks(self):
+        self._f("model_clear_kinks")(self.h)
+
+    def kink_flips(self, site=-1):
+        """Elements whose own sign the last forward overrode (site -1: all)."""
+        return self._f("model_kink_flips")(self.h, site)
 
     def affine(self, i, C):
         g, b, dg, db = (np.zeros(C, np.float32) for _ in range(4))

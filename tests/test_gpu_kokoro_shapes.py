@@ -1,0 +1,310 @@
+"""GPU parity at the real Kokoro-82M shapes.
+
+* Config 0: the whole decoder, B = 1, T = 64 (38 400 samples), against the
+  oracle: waveform, every parameter grad, the AdaIN affine grads, d(style),
+  and the in-model harmonic source at full length.
+* Config 1: Snake + AdaIN1d forward and backward on x [1, 256, 48000] with
+  (gamma, beta) from a 128 -> 512 style projection: dX, d(alpha), d(style).
+* Config 2: Conv1d 512 -> 512, k 3, dilations 1 / 3 / 5 on [4, 512, 2048]:
+  forward, input grad, weight and bias grads against torch float64 on the
+  CPU.
+* Config 3: the two ConvTranspose1d upsamplers (ups0 on [4, 512, 512], ups1
+  on [4, 256, 5120] and on [4, 256, 512]) likewise.
+* Config 4: one utterance at T = 512 (307 200 samples, 20 % unvoiced F0)
+  against the oracle, and B = 8 at T = 512 against eight B = 1 runs of the
+  same model (batch independence; the weight grads of the batch equal the
+  sum of the single-utterance grads).
+* The weight-grad GEMM at production K (8 x 61 441 positions).
+* The inference forwards (kdec_model_infer, kdec_model_decode_back_half)
+  against the oracle's forward.
+
+Each comparison prints its rel-L2 and max-abs error.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from brosoundml_amd import config as C
+from brosoundml_amd import synth
+from model_parity import FWD_TOL, GRAD_TOL, check_har, check_pair, dev, inputs, max_abs, rel_l2, run_pair
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+F = torch.nn.functional
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from brosoundml_amd import native
+    return native.Context(0)
+
+
+@pytest.fixture(scope="module")
+def kokoro_params():
+    shapes = O.OracleModel(C.KOKORO).param_shapes()
+    return synth.init_params(shapes)
+
+
+def P(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def close(got, ref, tol, what):
+    e, m = rel_l2(got, ref), max_abs(got, ref)
+    print(f"{what}: rel-L2 {e:.3e} max-abs {m:.3e}", flush=True)
+    assert e <= tol, f"{what}: rel-L2 {e:.3e} > {tol:.0e} (max-abs {m:.3e})"
+
+
+def report(name, rep):
+    print(f"{name}: " + ", ".join(f"{k}={v}" for k, v in rep.items()), flush=True)
+
+
+def model_har(ctx, m, cfg, N, T, ins):
+    """The model's own harmonic source for these inputs (a forward without har_in)."""
+    asr, F0, Nn, style = (dev(a) for a in ins[:4])
+    m.forward(asr, F0, Nn, style, T)
+    torch.cuda.synchronize()
+    return m.har(N, T)
+
+
+# ─── config 0 ───
+
+def test_config0_whole_decoder(ctx, kokoro_params):
+    cfg, N, T = C.KOKORO, 1, 64
+    r = run_pair(ctx, cfg, N, T, "cfg0", params=kokoro_params)
+    report("config0 B=1 T=64", check_pair(r))
+    har = model_har(ctx, r["m"], cfg, N, T, r["inputs"])
+    report("config0 in-model harmonic source", check_har(har[0], r["ref_har"][0], cfg["n_fft"]))
+
+
+# ─── config 1 ───
+
+def test_config1_snake_adain(ctx):
+    C_, L, S = 256, 48000, 128
+    x = synth.normal("cfg1.x", (1, C_, L))
+    alpha = synth.uniform("cfg1.alpha", (C_,), 0.5, 2.0)
+    style = synth.normal("cfg1.style", (1, S), 0.3)
+    bound = 1.0 / np.sqrt(S)
+    W = synth.uniform("cfg1.fcW", (2 * C_, S), -bound, bound)
+    b = synth.uniform("cfg1.fcb", (2 * C_,), -bound, bound)
+    dY = synth.normal("cfg1.dy", (1, C_, L))
+    tx, tW, tb, ts, ta, tdy = (dev(a) for a in (x, W, b, style, alpha, dY))
+    gb = torch.empty(1, 2 * C_, device="cuda")
+    ctx.call("kdec_style_proj_fwd", P(tW), P(tb), P(ts), S, P(gb), 2 * C_, 1, 2 * C_, S)
+    st = torch.empty(C_, 2, device="cuda")
+    y = torch.empty(1, C_, L, device="cuda")
+    g_p, b_p = P(gb), ctypes.c_void_p(gb.data_ptr() + 4 * C_)
+    ctx.call("kdec_adain_act_fwd_stats", P(tx), C_ * L, 1e-5, P(st), g_p, b_p, 2 * C_, 2, 0.0, P(ta), P(y), C_ * L,
+             None, 0, 1, C_, L)
+    dx = torch.empty_like(tx)
+    dgb = torch.empty(1, 2 * C_, device="cuda")
+    da = torch.zeros(C_, device="cuda")
+    ctx.call("kdec_adain_act_bwd", P(tx), C_ * L, P(st), g_p, b_p, 2 * C_, 2, 0.0, P(ta), P(tdy), C_ * L, None, 0,
+             P(dx), C_ * L, P(dgb), ctypes.c_void_p(dgb.data_ptr() + 4 * C_), 2 * C_, P(da), 1, C_, L)
+    dstyle = torch.empty(1, S, device="cuda")
+    dW = torch.zeros(2 * C_, S, device="cuda")
+    dbias = torch.zeros(2 * C_, device="cuda")
+    ctx.call("kdec_style_proj_bwd", P(tW), P(ts), S, P(dgb), 2 * C_, P(dstyle), S, 0.0, P(dW), P(dbias), 1,
+             2 * C_, S)
+    torch.cuda.synchronize()
+    # oracle: projection in float64, AdaIN and Snake by the C restatement
+    gb_ref = W.astype(np.float64) @ style[0].astype(np.float64) + b
+    close(gb.cpu().numpy()[0], gb_ref, FWD_TOL, "config1 style projection")
+    gam, bet = gb_ref[:C_].astype(np.float32), gb_ref[C_:].astype(np.float32)
+    s = O.adain_affine(x[0], gam, bet, C_, L)
+    close(y.cpu().numpy(), O.snake(s, alpha, C_, L), FWD_TOL, "config1 forward y")
+    ds, rda = O.snake_bwd(s, alpha, dY[0], C_, L)
+    rdx, rdg, rdb = O.adain_affine_bwd(x[0], gam, ds, C_, L)
+    close(dx.cpu().numpy(), rdx, GRAD_TOL, "config1 dX")
+    close(da.cpu().numpy(), rda, GRAD_TOL, "config1 d(alpha)")
+    rdgb = np.concatenate([rdg, rdb]).astype(np.float64)
+    close(dgb.cpu().numpy()[0], rdgb, GRAD_TOL, "config1 d(gamma, beta)")
+    close(dstyle.cpu().numpy()[0], W.astype(np.float64).T @ rdgb, GRAD_TOL, "config1 d(style)")
+    close(dW.cpu().numpy(), np.outer(rdgb, style[0].astype(np.float64)), GRAD_TOL, "config1 d(fc.weight)")
+
+
+# ─── config 2 ───
+
+@pytest.mark.parametrize("d", [1, 3, 5])
+def test_config2_conv1d_512(ctx, d):
+    N, Cc, L, k = 4, 512, 2048, 3
+    bound = 1.0 / np.sqrt(Cc * k)
+    x = synth.normal(f"cfg2.x{d}", (N, Cc, L))
+    W = synth.uniform(f"cfg2.W{d}", (Cc, Cc * k), -bound, bound)
+    b = synth.uniform(f"cfg2.b{d}", (Cc,), -bound, bound)
+    dY = synth.normal(f"cfg2.dy{d}", (N, Cc, L))
+    tx, tW, tb, tdy = (dev(a) for a in (x, W, b, dY))
+    Y = torch.empty(N, Cc, L, device="cuda")
+    ctx.call("kdec_conv1d_fwd", P(tx), Cc * L, P(tW), P(tb), P(Y), Cc * L, N, Cc, L, Cc, k, 1, d, d, None, 0, 1.0,
+             0.0)
+    dX = torch.empty(N, Cc, L, device="cuda")
+    ctx.call("kdec_conv1d_dgrad", P(tW), P(tdy), Cc * L, P(dX), Cc * L, N, Cc, L, Cc, k, 1, d, d, 1.0, 0.0)
+    dW = torch.zeros(Cc, Cc * k, device="cuda")
+    db = torch.zeros(Cc, device="cuda")
+    ctx.call("kdec_conv1d_wgrad", P(tx), Cc * L, P(tdy), Cc * L, P(dW), P(db), N, Cc, L, Cc, k, 1, d, d)
+    torch.cuda.synchronize()
+    xd, Wd, dyd = (torch.from_numpy(a).double() for a in (x, W.reshape(Cc, Cc, k), dY))
+    close(Y.cpu().numpy(), F.conv1d(xd, Wd, torch.from_numpy(b).double(), padding=d, dilation=d).numpy(), FWD_TOL,
+          f"config2 d={d} forward")
+    close(dX.cpu().numpy(), F.conv_transpose1d(dyd, Wd, padding=d, dilation=d).numpy(), GRAD_TOL,
+          f"config2 d={d} input grad")
+    rW = torch.nn.grad.conv1d_weight(xd, Wd.shape, dyd, padding=d, dilation=d).reshape(Cc, Cc * k)
+    close(dW.cpu().numpy(), rW.numpy(), GRAD_TOL, f"config2 d={d} weight grad")
+    close(db.cpu().numpy(), dyd.sum(dim=(0, 2)).numpy(), GRAD_TOL, f"config2 d={d} bias grad")
+
+
+# ─── config 3 ───
+
+@pytest.mark.parametrize("name,Cin,Cout,L,k,s,p", [
+    ("ups0", 512, 256, 512, 20, 10, 5),
+    ("ups1", 256, 128, 5120, 12, 6, 3),
+    ("ups1_unchained", 256, 128, 512, 12, 6, 3),
+])
+def test_config3_convt(ctx, name, Cin, Cout, L, k, s, p):
+    N = 4
+    Lo = O.convt1d_out_len(L, k, s, p, 0, 1)
+    bound = 1.0 / np.sqrt(Cout * k)
+    x = synth.normal(f"cfg3.{name}.x", (N, Cin, L))
+    W = synth.uniform(f"cfg3.{name}.W", (Cin, Cout * k), -bound, bound)
+    b = synth.uniform(f"cfg3.{name}.b", (Cout,), -bound, bound)
+    dY = synth.normal(f"cfg3.{name}.dy", (N, Cout, Lo))
+    tx, tW, tb, tdy = (dev(a) for a in (x, W, b, dY))
+    Y = torch.empty(N, Cout, Lo, device="cuda")
+    ctx.call("kdec_convt1d_fwd", P(tx), Cin * L, P(tW), P(tb), P(Y), Cout * Lo, N, Cin, L, Cout, k, s, p, 0)
+    dX = torch.empty(N, Cin, L, device="cuda")
+    ctx.call("kdec_convt1d_dgrad", P(tW), P(tdy), Cout * Lo, P(dX), Cin * L, N, Cin, L, Cout, k, s, p, 0)
+    dW = torch.zeros(Cin, Cout * k, device="cuda")
+    db = torch.zeros(Cout, device="cuda")
+    ctx.call("kdec_convt1d_wgrad", P(tx), Cin * L, P(tdy), Cout * Lo, P(dW), P(db), N, Cin, L, Cout, k, s, p, 0)
+    torch.cuda.synchronize()
+    xd = torch.from_numpy(x).double()
+    Wd = torch.from_numpy(W.reshape(Cin, Cout, k)).double().requires_grad_(True)
+    dyd = torch.from_numpy(dY).double()
+    y = F.conv_transpose1d(xd, Wd, torch.from_numpy(b).double(), stride=s, padding=p)
+    assert y.shape[-1] == Lo
+    close(Y.cpu().numpy(), y.detach().numpy(), FWD_TOL, f"config3 {name} forward")
+    y.backward(dyd)
+    close(dX.cpu().numpy(), F.conv1d(dyd, Wd.detach(), stride=s, padding=p).numpy(), GRAD_TOL,
+          f"config3 {name} input grad")
+    close(dW.cpu().numpy(), Wd.grad.reshape(Cin, Cout * k).numpy(), GRAD_TOL, f"config3 {name} weight grad")
+    close(db.cpu().numpy(), dyd.sum(dim=(0, 2)).numpy(), GRAD_TOL, f"config3 {name} bias grad")
+
+
+# ─── weight grads at production K ───
+
+@pytest.mark.parametrize("k,d", [(11, 5), (3, 1)])
+def test_wgrad_production_k(ctx, k, d):
+    # stage-1 ResBlock1 geometry of a B = 8, T = 512 step: C = 128, L = 61441,
+    # K = 8 x 61441 positions (split-K over rounds of resident blocks, the
+    # in-row fast staging path and the boundary chunks)
+    N, Cc, L = 8, 128, 61441
+    p = d * (k - 1) // 2
+    x = synth.normal(f"wgk.x{k}", (N, Cc, L))
+    dY = synth.normal(f"wgk.dy{k}", (N, Cc, L))
+    tx, tdy = dev(x), dev(dY)
+    dW = torch.zeros(Cc, Cc * k, device="cuda")
+    db = torch.zeros(Cc, device="cuda")
+    ctx.call("kdec_conv1d_wgrad", P(tx), Cc * L, P(tdy), Cc * L, P(dW), P(db), N, Cc, L, Cc, k, 1, p, d)
+    torch.cuda.synchronize()
+    xd, dyd = torch.from_numpy(x).double(), torch.from_numpy(dY).double()
+    rW = torch.nn.grad.conv1d_weight(xd, (Cc, Cc, k), dyd, padding=p, dilation=d).reshape(Cc, Cc * k)
+    close(dW.cpu().numpy(), rW.numpy(), GRAD_TOL, f"wgrad N=8 L=61441 k={k} d={d}")
+    close(db.cpu().numpy(), dyd.sum(dim=(0, 2)).numpy(), GRAD_TOL, f"bias grad N=8 L=61441 k={k}")
+
+
+# ─── config 4 ───
+
+def test_config4_one_utterance(ctx, kokoro_params):
+    cfg, N, T = C.KOKORO, 1, 512
+    r = run_pair(ctx, cfg, N, T, "cfg4", params=kokoro_params, unvoiced=0.2)
+    report("config4 B=1 T=512", check_pair(r))
+    har = model_har(ctx, r["m"], cfg, N, T, r["inputs"])
+    report("config4 in-model harmonic source (307200 samples)", check_har(har[0], r["ref_har"][0], cfg["n_fft"]))
+
+
+def test_config4_batch_of_8(ctx, kokoro_params):
+    # The benchmark's workload (B = 8, T = 512, 20 % unvoiced F0).
+    # Forward: every utterance's waveform and every leaky-ReLU site input in
+    # the batch equal a B = 1 run of that utterance (the GEMMs split
+    # differently per batch size, so to rounding); the harmonic source is
+    # per-utterance lane work and equal bit for bit.
+    # Backward: utterance 0's d(style) and AdaIN affine grads in the batch
+    # against the oracle differentiated on the batch run's own linear pieces
+    # (its leaky-site inputs), the per-utterance outputs of a batched backward.
+    from brosoundml_amd import native
+    cfg, N, T = C.KOKORO, 8, 512
+    m = native.Model(ctx, cfg)
+    m.set_params(kokoro_params)
+    asr, F0, Nn, style, dA = inputs(cfg, N, T, "bench", unvoiced=0.2)  # the benchmark's inputs
+    m.zero_grad()
+    audio = m.forward(dev(asr), dev(F0), dev(Nn), dev(style), T).cpu().numpy()
+    har8 = m.har(N, T)
+    pre8 = m.leaky_inputs()
+    dst8 = torch.empty(N, cfg["style_dim"], device="cuda")
+    m.backward(dev(dA), wgrad=True, dalpha=True, dstyle=dst8)
+    torch.cuda.synchronize()
+    dst8 = dst8.cpu().numpy()
+    _, dgb8 = m.affines(N)
+    for n in range(N):
+        sl = slice(n, n + 1)
+        a1 = m.forward(dev(asr[sl]), dev(F0[sl]), dev(Nn[sl]), dev(style[sl]), T).cpu().numpy()
+        assert np.array_equal(m.har(1, T)[0], har8[n]), f"utterance {n}: harmonic source depends on the batch"
+        close(audio[n], a1[0], FWD_TOL, f"config4 utterance {n} waveform, B=8 vs B=1")
+        pre1 = m.leaky_inputs()
+        worst = max(rel_l2(p8[n], p1[0]) for p8, p1 in zip(pre8, pre1))
+        assert worst <= FWD_TOL, f"utterance {n}: leaky-site inputs B=8 vs B=1 rel-L2 {worst:.3e}"
+    # utterance 0 of the batched backward against the oracle
+    om = O.OracleModel(cfg)
+    om.set_params(kokoro_params)
+    om.set_kinks([p[0] for p in pre8])
+    ra = om.forward(asr[0], F0[0], Nn[0], style[0], T, har=har8[0])
+    print(f"config4 utterance 0: kink flips reconciled {om.kink_flips()}", flush=True)
+    close(audio[0], ra, FWD_TOL, "config4 B=8 utterance 0 waveform vs oracle (GPU harmonic source)")
+    rds = om.backward(dA[0], wgrad=True, dalpha=True, dstyle=True)
+    close(dst8[0], rds, GRAD_TOL, "config4 B=8 utterance 0 d(style) vs oracle")
+    got = np.concatenate([dgb8[0, off:off + 2 * c] for _, c, off in m.units()])
+    ref = np.concatenate([np.concatenate(om.affine(i, c)[2:]) for i, (_, c) in enumerate(om.units())])
+    close(got, ref, GRAD_TOL, "config4 B=8 utterance 0 AdaIN affine grads vs oracle")
+
+
+# ─── inference forwards ───
+
+@pytest.mark.parametrize("cfg_name,N,T", [("SMALL", 2, 6), ("KOKORO", 1, 64)])
+def test_inference_forwards_vs_oracle(ctx, kokoro_params, cfg_name, N, T):
+    from brosoundml_amd import native
+    cfg = getattr(C, cfg_name)
+    m = native.Model(ctx, cfg)
+    om = O.OracleModel(cfg)
+    params = kokoro_params if cfg_name == "KOKORO" else synth.init_params(m.param_shapes())
+    m.set_params(params)
+    om.set_params(params)
+    asr, F0, Nn, style, _ = inputs(cfg, N, T, f"inf.{cfg_name}", unvoiced=0.2)
+    S = cfg["style_dim"]
+    ref_s = np.concatenate([style, synth.normal(f"inf.{cfg_name}.ref2", (N, S), 0.3)], axis=1)
+    t = [dev(a) for a in (asr, F0, Nn, style)]
+    L = C.lengths(cfg, T)
+    Pn = native.ptr
+    # the model's own harmonic source (the op the inference forwards run)
+    us = C.upsample_prod(cfg) * cfg["hop"]
+    har = torch.empty(N, (cfg["n_fft"] + 2) * L["frames"], device="cuda")
+    g = "decoder.module.generator.m_source.l_linear."
+    lW, lb = dev(params[g + "weight"]), dev(params[g + "bias"])
+    ctx.call("kdec_harmonic_source", Pn(t[1]), 2 * T, Pn(har), har.shape[1], N, 2 * T, Pn(lW), Pn(lb),
+             cfg["harmonic_num"], cfg["sample_rate"], us, cfg["n_fft"], cfg["hop"])
+    a_inf = torch.empty(N, L["audio"], device="cuda")
+    m._c(ctx.L.kdec_model_infer(m.h, N, T, Pn(t[0]), Pn(t[1]), Pn(t[2]), Pn(t[3]), None, Pn(a_inf)))
+    a_dbh = torch.empty(N, L["audio"], device="cuda")
+    t_ref = dev(ref_s)
+    m._c(ctx.L.kdec_model_decode_back_half(m.h, N, T, Pn(t[0]), Pn(t[1]), Pn(t[2]), Pn(t_ref), 2 * S, Pn(a_dbh)))
+    torch.cuda.synchronize()
+    h_gpu = har.cpu().numpy()
+    for n in range(N):
+        om.forward(asr[n], F0[n], Nn[n], style[n], T)
+        report(f"{cfg_name} harmonic source utt {n}", check_har(h_gpu[n], om.har(), cfg["n_fft"]))
+        # the waveform's reference takes the GPU's harmonic source, so the
+        # comparison covers the backbone and generator composition exactly
+        ref = om.forward(asr[n], F0[n], Nn[n], style[n], T, har=h_gpu[n])
+        close(a_inf[n].cpu().numpy(), ref, FWD_TOL, f"{cfg_name} kdec_model_infer utt {n} vs oracle")
+        close(a_dbh[n].cpu().numpy(), ref, FWD_TOL, f"{cfg_name} decode_back_half utt {n} vs oracle")

@@ -12,135 +12,18 @@ harmonic source itself is compared in test_gpu_ops).
 import numpy as np
 import pytest
 
-import oracle_lib as O
 from brosoundml_amd import config as C
 from brosoundml_amd import synth
+from model_parity import check_pair, inputs, rel_l2, run_pair
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
-
-
-def rel_l2(a, b):
-    a = np.asarray(a, np.float64).ravel()
-    b = np.asarray(b, np.float64).ravel()
-    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
-
-
-def inputs(cfg, N, T, tag):
-    asr = synth.normal(f"{tag}.asr", (N, cfg["asr_dim"], T))
-    F0 = synth.uniform(f"{tag}.F0", (N, 2 * T), 80.0, 300.0)
-    Nn = synth.normal(f"{tag}.N", (N, 2 * T), 0.5)
-    style = synth.normal(f"{tag}.style", (N, cfg["style_dim"]), 0.3)
-    L = C.lengths(cfg, T)
-    dA = synth.normal(f"{tag}.daudio", (N, L["audio"]), 1.0)
-    return asr, F0, Nn, style, dA
 
 
 @pytest.fixture(scope="module")
 def ctx():
     from brosoundml_amd import native
     return native.Context(0)
-
-
-def run_pair(ctx, cfg, N, T, tag, wgrad=True, dalpha=True, lora=None):
-    from brosoundml_amd import native
-    m = native.Model(ctx, cfg)
-    shapes = m.param_shapes()
-    om = O.OracleModel(cfg)
-    assert shapes == om.param_shapes()
-    params = synth.init_params(shapes)
-    m.set_params(params)
-    om.set_params(params)
-    asr, F0, Nn, style, dA = inputs(cfg, N, T, tag)
-    units = om.units()
-    if lora:  # DecoderLora adapters on every unit, a gate per utterance
-        rank, scale = lora
-        S = cfg["style_dim"]
-        m.lora_enable(rank, scale)
-        om.lora_enable(rank, scale)
-        offs = [u[2] for u in m.units()]
-        A = synth.normal(f"{tag}.loraA", (len(units) * rank, S), 0.2)
-        B = synth.normal(f"{tag}.loraB", (m.affine_rows(), rank), 0.2)
-        gates = synth.normal(f"{tag}.gate", (N, rank), 1.0)
-        m.lora_set(A, B)
-        for i, (_, c) in enumerate(units):
-            om.lora_set(i, A[i * rank:(i + 1) * rank], B[offs[i]:offs[i] + 2 * c])
-        ref_dA, ref_dB, ref_dG = np.zeros_like(A, np.float64), np.zeros_like(B, np.float64), []
-
-    # oracle, utterance by utterance
-    ref_audio, ref_har, ref_dstyle, ref_aff = [], [], [], []
-    ref_grads = {n: np.zeros(int(np.prod(s))) for n, s in shapes.items()}
-    for n in range(N):
-        om.zero_grad()
-        if lora:
-            om.lora_gate(gates[n])
-        a = om.forward(asr[n], F0[n], Nn[n], style[n], T)
-        ref_audio.append(a)
-        ref_har.append(om.har())
-        ref_dstyle.append(om.backward(dA[n], wgrad=wgrad, dalpha=dalpha, dstyle=True))
-        for name, s in shapes.items():
-            ref_grads[name] += om.grad(name, s)
-        ref_aff.append([om.affine(i, c) for i, (_, c) in enumerate(units)])
-        if lora:
-            for i, (_, c) in enumerate(units):
-                gA, gB = om.lora_grads(i, c)
-                ref_dA[i * rank:(i + 1) * rank] += gA
-                ref_dB[offs[i]:offs[i] + 2 * c] += gB
-            ref_dG.append(om.lora_dgate())
-
-    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
-    t_asr, t_F0, t_N, t_style = dev(asr), dev(F0), dev(Nn), dev(style)
-    t_har = dev(np.stack(ref_har))
-    if lora:
-        t_gate = dev(gates)
-        t_dG = torch.zeros_like(t_gate)
-        m.lora_gate(t_gate, t_dG)
-    m.zero_grad()
-    audio = m.forward(t_asr, t_F0, t_N, t_style, T, har=t_har)
-    dstyle = torch.empty_like(t_style)
-    t_dA = dev(dA)
-    m.backward(t_dA, wgrad=wgrad, dalpha=dalpha, dstyle=dstyle)
-    torch.cuda.synchronize()
-    got_grads = {n: m.grad(n, s) for n, s in shapes.items()}
-    gb, dgb = m.affines(N)
-    r = dict(m=m, om=om, shapes=shapes, audio=audio.cpu().numpy(), ref_audio=np.stack(ref_audio),
-             dstyle=dstyle.cpu().numpy(), ref_dstyle=np.stack(ref_dstyle), grads=got_grads,
-             ref_grads=ref_grads, dgb=dgb, ref_aff=ref_aff, units=m.units(), oracle_units=om.units())
-    if lora:
-        gA, gB = m.lora_grads()
-        r.update(lora_got=(gA, gB, t_dG.cpu().numpy()), lora_ref=(ref_dA, ref_dB, np.stack(ref_dG)))
-    return r
-
-
-def check_pair(r, wgrad=True):
-    e = rel_l2(r["audio"], r["ref_audio"])
-    assert e <= 1e-5, f"waveform rel-L2 {e:.3e}"
-    assert [u[0] for u in r["units"]] == [u[0] for u in r["oracle_units"]]
-    # affine grads (the reference semantics' outputs)
-    for n, aff in enumerate(r["ref_aff"]):
-        for (name, Cc, off), (_, _, dg, db) in zip(r["units"], aff):
-            got = r["dgb"][n, off:off + 2 * Cc]
-            ref = np.concatenate([dg, db])
-            err = np.linalg.norm(got - ref)
-            assert err <= 1e-4 * np.linalg.norm(ref) + 1e-6 * np.sqrt(ref.size), (n, name, err)
-    e = rel_l2(r["dstyle"], r["ref_dstyle"])
-    assert e <= 1e-4, f"d(style) rel-L2 {e:.3e}"
-    worst = []
-    for name, ref in r["ref_grads"].items():
-        got = r["grads"][name].astype(np.float64)
-        err = np.linalg.norm(got - ref)
-        tol = 1e-4 * np.linalg.norm(ref) + 1e-6 * np.sqrt(ref.size)
-        wname = name[:-len(".bias")] + ".weight"
-        if name.endswith(".bias") and wname in r["ref_grads"]:
-            # a bias in front of an instance norm has an identically zero
-            # grad; what remains is float rounding of a cancelling sum, which
-            # scales with the layer's weight grad
-            tol += 1e-7 * np.linalg.norm(r["ref_grads"][wname])
-        worst.append((err / max(tol, 1e-30), name, err, np.linalg.norm(ref)))
-        if not wgrad and ".alpha" not in name:
-            assert not np.any(got), f"{name}: grad produced in reference semantics"
-    worst.sort(reverse=True)
-    assert worst[0][0] <= 1.0, worst[:5]
 
 
 def test_tiny_full_extension(ctx):

@@ -247,8 +247,9 @@ ACTS = {"none": 0, "leaky": 1, "snake": 2}
 
 
 @pytest.mark.parametrize("act", ["none", "leaky", "snake"])
-# lengths cover every row-kernel shape (256x4, 256x16, 1024x16, 1024x48,
-# 1024x64 streaming) and the chunked path for longer rows
+# lengths cover every row-kernel shape (256x4, 256x16, 1024x16, 1024x48),
+# with 4-byte accesses (L not a multiple of 4) and 16-byte ones, and the
+# chunked path for longer rows
 @pytest.mark.parametrize("C,L", [(5, 31), (3, 1500), (16, 4099), (3, 8192), (2, 48000), (2, 61441), (2, 70000)])
 def test_adain_act(K, act, C, L):
     N = 2
@@ -303,6 +304,26 @@ def test_adain_act(K, act, C, L):
     assert_close(h(db), np.stack(rdb), GRAD_TOL, f"adain+{act} dBeta")
     if act == "snake":
         assert_close(h(da), rda, GRAD_TOL, "snake dAlpha")
+
+
+@pytest.mark.parametrize("act", ["leaky", "snake"])
+# 4-byte row kernel (1500), 16-byte row kernel (8192), chunked passes (70000)
+@pytest.mark.parametrize("C,L", [(3, 1500), (4, 8192), (2, 70000)])
+def test_adain_act_pre_activation_output(K, act, C, L):
+    # Ypre, the AdaIN output before the activation, written beside Y
+    N = 2
+    x = rnd(N, C, L, scale=1.3) - 0.2
+    gm, bt = rnd(N, C, scale=0.4), rnd(N, C, scale=0.3)
+    alpha = rng.uniform(0.5, 2.0, C).astype(np.float32)
+    st = torch.empty(N * C, 2, device="cuda")
+    Y = torch.empty(N, C, L, device="cuda")
+    Yp = torch.empty(N, C, L, device="cuda")
+    K.call("kdec_adain_act_fwd_stats", P(g(x)), C * L, 1e-5, P(st), P(g(gm)), P(g(bt)), C, ACTS[act], 0.2,
+           P(g(alpha)), P(Y), C * L, P(Yp), C * L, N, C, L)
+    pre = np.stack([O.adain_affine(x[n], gm[n], bt[n], C, L) for n in range(N)])
+    assert_close(h(Yp).reshape(N, -1), pre, FWD_TOL, f"adain+{act} pre-activation output")
+    post = np.stack([O.leaky(pre[n], 0.2) if act == "leaky" else O.snake(pre[n], alpha, C, L) for n in range(N)])
+    assert_close(h(Y).reshape(N, -1), post, FWD_TOL, f"adain+{act} output beside Ypre")
 
 
 def test_elementwise(K):
