@@ -190,6 +190,10 @@ int kdec_ctx_create(int device, kdec_ctx** out) {
     if (hipDeviceGetAttribute(&c->num_cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
         c->num_cus <= 0)
         c->num_cus = 256;
+    // This device's copy of the no-allocation entry point's scratch; a
+    // failure here only disables that entry point (it reports why).
+    if (kdec::noalloc_scratch_setup(c) != KDEC_OK) c->scratch_err = c->err;
+    c->err.clear();
     e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         delete c;

@@ -48,6 +48,8 @@ struct kdec_ctx {
     // Contexts whose streams run work forked from this one (a model's side
     // stream); their profiles follow this context's enable / reset / read.
     std::vector<kdec_ctx*> peers;
+    // Why this device's no-allocation scratch is unavailable ("" if it is).
+    std::string scratch_err;
 };
 
 namespace kdec {
@@ -93,6 +95,12 @@ struct ProfScope {
     ProfScope(kdec_ctx* c, const char* n, double f, double b = 0.0);
     ~ProfScope();
 };
+
+// Looks up, once per device and with that device current, the address of
+// this device's copy of the no-allocation scratch array (kdec_norm.hip).
+int noalloc_scratch_setup(kdec_ctx* ctx);
+// That address for ctx's device, or nullptr when the lookup failed.
+void* noalloc_scratch(kdec_ctx* ctx);
 
 // Drops `ctx` as the C++ layer's runtime context if it is the current one
 // (defined with the brotensor runtime, tensor.cpp).

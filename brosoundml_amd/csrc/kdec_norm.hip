@@ -12,6 +12,9 @@
 #include "kdec_internal.hpp"
 #include "kdec_snake_math.hpp"
 
+#include <mutex>
+#include <string>
+
 namespace kdec {
 namespace {
 
@@ -649,6 +652,40 @@ int launch_bwd_row(kdec_ctx* ctx, RowShape rsh, unsigned rows, const AdainArgs& 
     return fail(ctx, KDEC_EINVAL, "adain backward: no row kernel for this length");
 }
 
+// Scratch of the AdaIN backward: the per-row alpha-grad shares, and for rows
+// longer than the row kernels take the chunk partial sums and the per-row
+// means. Every word a launch reads is written earlier in the same call, so
+// a reused buffer needs no clearing.
+struct BwdScratchLayout {
+    size_t apart = 0, part = 0, rowv = 0, total = 0;  // byte offsets, total size
+};
+size_t round256(size_t b) { return (b + 255) & ~size_t(255); }
+BwdScratchLayout bwd_scratch_layout(int N, int C, int L, bool want_alpha) {
+    const size_t rows = static_cast<size_t>(N) * C;
+    BwdScratchLayout s;
+    size_t off = 0;
+    s.apart = off;
+    off += want_alpha ? round256(rows * sizeof(float)) : 0;
+    if (!row_shape_bwd(L).ntb) {
+        s.part = off;
+        off += round256(rows * static_cast<size_t>(cdiv(L, CH)) * 3 * sizeof(double));
+        s.rowv = off;
+        off += round256(rows * sizeof(float2));
+    }
+    s.total = off;
+    return s;
+}
+struct BwdScratch {
+    float* apart;
+    double* part;
+    float2* rowv;
+};
+BwdScratch bwd_scratch(void* base, const BwdScratchLayout& s) {
+    char* b = static_cast<char*>(base);
+    return {reinterpret_cast<float*>(b + s.apart), reinterpret_cast<double*>(b + s.part),
+            reinterpret_cast<float2*>(b + s.rowv)};
+}
+
 unsigned chunks(long len, long cap = 1024) {
     long g = (len + 255) / 256;
     if (g > cap) g = cap;
@@ -656,10 +693,101 @@ unsigned chunks(long len, long cap = 1024) {
     return static_cast<unsigned>(g);
 }
 
+int bwd_check(kdec_ctx* ctx, const AdainArgs& g, const float* dY, const float* dX, int N, const char* where) {
+    const std::string w(where);
+    KDEC_CHECK(ctx, g.X && g.stats && g.gamma && dY && dX && N > 0 && g.C > 0 && g.L > 0, w + ": bad arguments");
+    KDEC_CHECK(ctx, g.beta || g.act == KDEC_ACT_NONE, w + ": beta needed to recompute the activation input");
+    KDEC_CHECK(ctx, g.act >= KDEC_ACT_NONE && g.act <= KDEC_ACT_SNAKE && (g.act != KDEC_ACT_SNAKE || g.alpha),
+               w + ": bad activation");
+    return KDEC_OK;
+}
+
+// The AdaIN(+activation) backward over caller-provided scratch (laid out by
+// bwd_scratch_layout for the same N, C, L and alpha-grad flag).
+int bwd_run(kdec_ctx* ctx, const AdainArgs& g, const float* dY, long dy_bs, const float* R, long r_bs, float* dX,
+            long dx_bs, float* dgamma, float* dbeta, long dgb_bs, float* dalpha, int N, BwdScratch sc, bool prof) {
+    const int C = g.C, L = g.L;
+    const int rows = N * C;
+    const int nch = static_cast<int>(cdiv(L, CH));
+    const bool want_alpha = dalpha && g.act == KDEC_ACT_SNAKE;
+    const RowShape rsh = row_shape_bwd(L);
+    const double bytes = 4.0 * static_cast<double>(rows) * L * 3 +
+                         (R ? 4.0 * static_cast<double>(rows) * L : 0.0);
+    if (rsh.ntb) {
+        // one utterance: each channel's alpha grad comes from one row, which
+        // adds it directly; otherwise per-row shares are summed in order
+        const bool direct = want_alpha && N == 1;
+        {
+            ProfScope ps(prof ? ctx : nullptr, "adain_bwd", 0, bytes);
+            if (int rc = launch_bwd_row(ctx, rsh, static_cast<unsigned>(rows), g, dY, dy_bs, R, r_bs, dX, dx_bs,
+                                        dgamma, dbeta, dgb_bs, want_alpha && !direct ? sc.apart : nullptr,
+                                        direct ? dalpha : nullptr))
+                return rc;
+        }
+        if (want_alpha && !direct) {
+            hipLaunchKernelGGL(dalpha_reduce, dim3(static_cast<unsigned>(cdiv(C, 256))), dim3(256), 0, ctx->stream,
+                               sc.apart, dalpha, N, C);
+            return launch_check(ctx, "dalpha_reduce");
+        }
+        return KDEC_OK;
+    }
+    {
+        ProfScope ps(prof ? ctx : nullptr, "adain_bwd", 0, 4.0 * static_cast<double>(rows) * L * 5);
+        hipLaunchKernelGGL(adain_bwd_part_k, dim3(nch, rows), dim3(RT), 0, ctx->stream, g, dY, dy_bs, nch, sc.part);
+        if (int rc = launch_check(ctx, "adain_bwd_part")) return rc;
+        hipLaunchKernelGGL(adain_bwd_fin_k, dim3(static_cast<unsigned>(cdiv(rows, 256))), dim3(256), 0,
+                           ctx->stream, sc.part, rows, nch, C, L, dgamma, dbeta, dgb_bs,
+                           want_alpha ? sc.apart : nullptr, sc.rowv);
+        if (int rc = launch_check(ctx, "adain_bwd_fin")) return rc;
+        hipLaunchKernelGGL(adain_bwd_apply_k, dim3(nch, rows), dim3(RT), 0, ctx->stream, g, dY, dy_bs, R, r_bs,
+                           dX, dx_bs, sc.rowv);
+        if (int rc = launch_check(ctx, "adain_bwd_apply")) return rc;
+    }
+    if (want_alpha) {
+        hipLaunchKernelGGL(dalpha_reduce, dim3(static_cast<unsigned>(cdiv(C, 256))), dim3(256), 0, ctx->stream,
+                           sc.apart, dalpha, N, C);
+        return launch_check(ctx, "dalpha_reduce");
+    }
+    return KDEC_OK;
+}
+
 }  // namespace
 }  // namespace kdec
 
 using namespace kdec;
+
+// Scratch of kdec_adain_act_bwd_noalloc: a file-scope device array, one copy
+// per GPU (each at its own address), held until the process ends. Host code
+// never uses its name as an address: at context creation, with the device
+// current, hipGetSymbolAddress gives this GPU's copy, kept per device.
+static __device__ __align__(256) unsigned char scratch[KDEC_NOALLOC_SCRATCH_BYTES];
+
+namespace kdec {
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+int noalloc_scratch_setup(kdec_ctx* ctx) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (ctx->device < 0 || ctx->device >= kMaxDevices)
+        return fail(ctx, KDEC_EINVAL, "no-allocation scratch: device index out of range");
+    if (g_scratch_ptr[ctx->device]) return KDEC_OK;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(ctx, KDEC_EHIP, "hipGetSymbolAddress(scratch) returned no address");
+    g_scratch_ptr[ctx->device] = p;
+    return KDEC_OK;
+}
+
+void* noalloc_scratch(kdec_ctx* ctx) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    return ctx->device >= 0 && ctx->device < kMaxDevices ? g_scratch_ptr[ctx->device] : nullptr;
+}
+
+}  // namespace kdec
 
 extern "C" {
 
@@ -727,60 +855,37 @@ int kdec_adain_act_bwd(kdec_ctx* ctx, const float* X, long x_bs,
                        float* dgamma, float* dbeta, long dgb_bs,
                        float* dalpha, int N, int C, int L) {
     if (!ctx) return KDEC_EINVAL;
-    KDEC_CHECK(ctx, X && stats && gamma && dY && dX && N > 0 && C > 0 && L > 0,
-               "kdec_adain_act_bwd: bad arguments");
-    KDEC_CHECK(ctx, beta || act == KDEC_ACT_NONE, "kdec_adain_act_bwd: beta needed to recompute the activation input");
-    KDEC_CHECK(ctx, act >= KDEC_ACT_NONE && act <= KDEC_ACT_SNAKE && (act != KDEC_ACT_SNAKE || alpha),
-               "kdec_adain_act_bwd: bad activation");
     AdainArgs g{X, x_bs, reinterpret_cast<const float2*>(stats), gamma, beta, gb_bs, act, slope, alpha, C, L};
-    const int rows = N * C;
-    const int nch = static_cast<int>(cdiv(L, CH));
-    const bool want_alpha = dalpha && act == KDEC_ACT_SNAKE;
-    const RowShape rsh = row_shape_bwd(L);
-    Workspace apart(ctx, want_alpha ? static_cast<size_t>(rows) * sizeof(float) : 0);
-    if (want_alpha && !apart.p) return KDEC_ENOMEM;
-    const double bytes = 4.0 * static_cast<double>(rows) * L * 3 +
-                         (R ? 4.0 * static_cast<double>(rows) * L : 0.0);
-    if (rsh.ntb) {
-        // one utterance: each channel's alpha grad comes from one row, which
-        // adds it directly; otherwise per-row shares are summed in order
-        const bool direct = want_alpha && N == 1;
-        {
-            ProfScope ps(ctx, "adain_bwd", 0, bytes);
-            if (int rc = launch_bwd_row(ctx, rsh, static_cast<unsigned>(rows), g, dY, dy_bs, R, r_bs, dX, dx_bs,
-                                        dgamma, dbeta, dgb_bs, want_alpha && !direct ? apart.as<float>() : nullptr,
-                                        direct ? dalpha : nullptr))
-                return rc;
-        }
-        if (want_alpha && !direct) {
-            hipLaunchKernelGGL(dalpha_reduce, dim3(static_cast<unsigned>(cdiv(C, 256))), dim3(256), 0, ctx->stream,
-                               apart.as<float>(), dalpha, N, C);
-            return launch_check(ctx, "dalpha_reduce");
-        }
-        return KDEC_OK;
-    }
-    Workspace part(ctx, static_cast<size_t>(rows) * nch * 3 * sizeof(double));
-    Workspace rowv(ctx, static_cast<size_t>(rows) * sizeof(float2));
-    if (!part.p || !rowv.p) return KDEC_ENOMEM;
-    {
-        ProfScope ps(ctx, "adain_bwd", 0, 4.0 * static_cast<double>(rows) * L * 5);
-        hipLaunchKernelGGL(adain_bwd_part_k, dim3(nch, rows), dim3(RT), 0, ctx->stream, g, dY, dy_bs, nch,
-                           part.as<double>());
-        if (int rc = launch_check(ctx, "adain_bwd_part")) return rc;
-        hipLaunchKernelGGL(adain_bwd_fin_k, dim3(static_cast<unsigned>(cdiv(rows, 256))), dim3(256), 0,
-                           ctx->stream, part.as<double>(), rows, nch, C, L, dgamma, dbeta, dgb_bs,
-                           want_alpha ? apart.as<float>() : nullptr, rowv.as<float2>());
-        if (int rc = launch_check(ctx, "adain_bwd_fin")) return rc;
-        hipLaunchKernelGGL(adain_bwd_apply_k, dim3(nch, rows), dim3(RT), 0, ctx->stream, g, dY, dy_bs, R, r_bs,
-                           dX, dx_bs, rowv.as<float2>());
-        if (int rc = launch_check(ctx, "adain_bwd_apply")) return rc;
-    }
-    if (want_alpha) {
-        hipLaunchKernelGGL(dalpha_reduce, dim3(static_cast<unsigned>(cdiv(C, 256))), dim3(256), 0, ctx->stream,
-                           apart.as<float>(), dalpha, N, C);
-        return launch_check(ctx, "dalpha_reduce");
-    }
-    return KDEC_OK;
+    if (int rc = bwd_check(ctx, g, dY, dX, N, "kdec_adain_act_bwd")) return rc;
+    const BwdScratchLayout lay = bwd_scratch_layout(N, C, L, dalpha && act == KDEC_ACT_SNAKE);
+    Workspace ws(ctx, lay.total);
+    if (lay.total && !ws.p) return KDEC_ENOMEM;
+    return bwd_run(ctx, g, dY, dy_bs, R, r_bs, dX, dx_bs, dgamma, dbeta, dgb_bs, dalpha, N,
+                   bwd_scratch(ws.p, lay), true);
+}
+
+int kdec_adain_act_bwd_noalloc(kdec_ctx* ctx, const float* X, long x_bs,
+                               const float* stats, const float* gamma,
+                               const float* beta, long gb_bs, int act, float slope,
+                               const float* alpha, const float* dY, long dy_bs,
+                               const float* R, long r_bs, float* dX, long dx_bs,
+                               float* dgamma, float* dbeta, long dgb_bs,
+                               float* dalpha, int N, int C, int L) {
+    if (!ctx) return KDEC_EINVAL;
+    AdainArgs g{X, x_bs, reinterpret_cast<const float2*>(stats), gamma, beta, gb_bs, act, slope, alpha, C, L};
+    if (int rc = bwd_check(ctx, g, dY, dX, N, "kdec_adain_act_bwd_noalloc")) return rc;
+    const BwdScratchLayout lay = bwd_scratch_layout(N, C, L, dalpha && act == KDEC_ACT_SNAKE);
+    if (lay.total > static_cast<size_t>(KDEC_NOALLOC_SCRATCH_BYTES))
+        return fail(ctx, KDEC_EINVAL,
+                    "kdec_adain_act_bwd_noalloc: N*C = " + std::to_string(static_cast<long>(N) * C) + ", L = " +
+                        std::to_string(L) + " needs " + std::to_string(lay.total) +
+                        " bytes of scratch; the limit is " + std::to_string(KDEC_NOALLOC_SCRATCH_BYTES));
+    void* base = noalloc_scratch(ctx);
+    if (!base) return fail(ctx, KDEC_EHIP,
+                                "kdec_adain_act_bwd_noalloc: no scratch on this device: " + ctx->scratch_err);
+    // the profiling bracket creates events, so it stays off here
+    return bwd_run(ctx, g, dY, dy_bs, R, r_bs, dX, dx_bs, dgamma, dbeta, dgb_bs, dalpha, N, bwd_scratch(base, lay),
+                   false);
 }
 
 int kdec_fill(kdec_ctx* ctx, float* Y, long n, float value) {

@@ -178,6 +178,28 @@ int kdec_adain_act_bwd(kdec_ctx* ctx, const float* X, long x_bs,
                        float* dgamma, float* dbeta, long dgb_bs,
                        float* dalpha, int N, int C, int L);
 
+/* kdec_adain_act_bwd without any allocation: same arguments, kernels and
+ * results. No counterpart in the reference; it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Its scratch (the per-row alpha-grad
+ * shares, and for rows longer than 49152 the chunk partial sums and row
+ * means: 4 B per row with dalpha, plus 24 B per row and 4096-sample chunk
+ * and 8 B per row) lives in a device array of KDEC_NOALLOC_SCRATCH_BYTES per
+ * GPU, held until the process ends; a call that needs more returns
+ * KDEC_EINVAL with the sizes in kdec_last_error. It calls no hipMalloc /
+ * hipFree and records no profiling events. Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (any two streams or
+ * contexts) race and must be serialised by the caller. */
+#define KDEC_NOALLOC_SCRATCH_BYTES (4 << 20)
+int kdec_adain_act_bwd_noalloc(kdec_ctx* ctx, const float* X, long x_bs,
+                               const float* stats, const float* gamma,
+                               const float* beta, long gb_bs, int act,
+                               float slope, const float* alpha,
+                               const float* dY, long dy_bs, const float* R,
+                               long r_bs, float* dX, long dx_bs,
+                               float* dgamma, float* dbeta, long dgb_bs,
+                               float* dalpha, int N, int C, int L);
+
 /* ─── elementwise ─────────────────────────────────────────────────────── */
 
 /* Y[i] = value for i < n (a kernel, not hipMemset, so it can be captured). */
