@@ -1,7 +1,7 @@
 // Decoder-back-half module structs with the reference's fields
 // (include/brosoundml/kokoro_modules.h:127-132, 144-158, 228-244, 259-269,
 // 283-300, 312-340), with the inference forwards of DecoderBackbone and
-// Generator. The structs are filled by the caller (tests, the whole-decoder
+// Generator and the inference building blocks they are made of. The structs are filled by the caller (tests, the whole-decoder
 // model, whose kdec_model_load_safetensors reads the upstream keys).
 #pragma once
 
@@ -97,5 +97,19 @@ struct Generator {
                  const brotensor::Tensor& style, brotensor::Tensor& audio,
                  const std::function<bool()>& cancel = {}) const;
 };
+
+// The reference's inference building blocks (kokoro_modules.cpp:596-620,
+// 651-706, 1197-1231), on N style rows (style (N, >= style_dim) at its row
+// stride; gamma, beta = chunk(fc(style)) for every utterance):
+//   ada_in_1d_styled: y = (1 + gamma) * instance_norm(x) + beta, x (N, C*L)
+//   adain_resblk_1d_forward: (residual + shortcut) / sqrt(2), L_out = 2 L_in
+//     for the upsampling block
+//   adain_resblock1_forward: x <- the three dilated AdaIN + Snake stages
+void ada_in_1d_styled(const AdaIN1dWeights& w, int N, int C, int L, const brotensor::Tensor& x_ncl,
+                      const brotensor::Tensor& style, brotensor::Tensor& y_ncl);
+void adain_resblk_1d_forward(const AdainResBlk1dWeights& w, const brotensor::Tensor& x, int L_in,
+                             const brotensor::Tensor& style, int& L_out, brotensor::Tensor& y);
+void adain_resblock1_forward(const AdaINResBlock1Weights& w, brotensor::Tensor& x, int C, int L,
+                             const brotensor::Tensor& style);
 
 }  // namespace brosoundml

@@ -2,6 +2,7 @@
 // device buffer, the per-AdaIN style projection batched over all units, and
 // the forward / backward sequence of DecoderLora (decoder_lora.cpp:211-296)
 // without the LoRA term.
+#include <functional>
 #include <map>
 #include <string>
 #include <vector>
@@ -12,6 +13,7 @@
 #include "kdec_internal.hpp"
 #include "kdec_model.h"
 #include "brosoundml/decoder_lora.h"
+#include "brosoundml/kokoro.h"
 #include "kokoro_decoder_backward.h"
 
 namespace bt = brotensor;
@@ -720,11 +722,19 @@ int kdec_model_infer(kdec_model* m, int N, int T, const float* asr, const float*
     return rc;
 }
 
-int kdec_model_decode_back_half(kdec_model* m, int N, int T, const float* asr, const float* F0, const float* Nn,
-                                const float* ref_s, long ref_bs, float* audio) {
+namespace {
+
+// Kokoro::Impl::decode_back_half (kokoro.cpp:352-407): DecoderBackbone,
+// HarmonicSource and Generator inference forwards; `cancel` is polled before
+// the generator (:387) and by the generator before each upsample stage.
+int decode_back_half(kdec_model* m, int N, int T, const float* asr, const float* F0, const float* Nn,
+                     const float* ref_s, long ref_bs, float* audio, const std::function<bool()>& cancel,
+                     int* cancelled) {
+    const char* where = "kdec_model_decode_back_half";
+    if (cancelled) *cancelled = 0;
     if (!m || N <= 0 || T <= 0 || !asr || !F0 || !Nn || !ref_s || !audio) return KDEC_EINVAL;
-    if (ref_bs < m->style_dim) return fail(m, KDEC_EINVAL, "kdec_model_decode_back_half: ref_s stride below style_dim");
-    if (m->lora_rank > 0) return fail(m, KDEC_EINVAL, "kdec_model_decode_back_half: the base decoder has no adapters");
+    if (ref_bs < m->style_dim) return fail(m, KDEC_EINVAL, std::string(where) + ": ref_s stride below style_dim");
+    if (m->lora_rank > 0) return fail(m, KDEC_EINVAL, std::string(where) + ": the base decoder has no adapters");
     try {
         bt::set_runtime(m->ctx);
         auto in = [&](const float* p, int cols, long ld = 0) {
@@ -735,14 +745,43 @@ int kdec_model_decode_back_half(kdec_model* m, int N, int T, const float* asr, c
         m->bb.forward(in(asr, m->asr_dim * T), in(F0, 2 * T), in(Nn, 2 * T), rs, T, gen_in);
         int sig = 0, frames = 0;
         m->hs.forward(in(F0, 2 * T), 2 * T, sig, frames, har);
-        m->gen.forward(gen_in, 2 * T, har, frames, rs, out);
+        int upr = 1;
+        for (int i = 0; i < m->n_ups; ++i) upr *= m->ups_rates[i];
+        if (frames != 2 * T * upr + 1)
+            return fail(m, KDEC_EINVAL, "brosoundml: Kokoro::decode: har_frames mismatch: hsource=" +
+                                            std::to_string(frames) + " vs expected=" +
+                                            std::to_string(2 * T * upr + 1));
+        if (cancel && cancel()) {
+            if (cancelled) *cancelled = 1;
+            return KDEC_OK;
+        }
+        m->gen.forward(gen_in, 2 * T, har, frames, rs, out, cancel);
+        if (!out.data) {  // cancelled between stages: the audio stays unwritten
+            if (cancelled) *cancelled = 1;
+            return KDEC_OK;
+        }
         if (hipMemcpyAsync(audio, out.data, out.size() * sizeof(float), hipMemcpyDeviceToDevice,
                            static_cast<hipStream_t>(kdec_get_stream(m->ctx))) != hipSuccess)
-            return fail(m, KDEC_EHIP, "kdec_model_decode_back_half: output copy");
+            return fail(m, KDEC_EHIP, std::string(where) + ": output copy");
     } catch (const std::exception& e) {
         return fail(m, KDEC_EINVAL, e.what());
     }
     return KDEC_OK;
+}
+
+}  // namespace
+
+int kdec_model_decode_back_half(kdec_model* m, int N, int T, const float* asr, const float* F0, const float* Nn,
+                                const float* ref_s, long ref_bs, float* audio) {
+    return decode_back_half(m, N, T, asr, F0, Nn, ref_s, ref_bs, audio, {}, nullptr);
+}
+
+int kdec_model_decode_back_half_cancellable(kdec_model* m, int N, int T, const float* asr, const float* F0,
+                                            const float* Nn, const float* ref_s, long ref_bs, float* audio,
+                                            kdec_cancel_fn cancel, void* user, int* cancelled) {
+    std::function<bool()> poll;
+    if (cancel) poll = [cancel, user] { return cancel(user) != 0; };
+    return decode_back_half(m, N, T, asr, F0, Nn, ref_s, ref_bs, audio, poll, cancelled);
 }
 
 int kdec_model_set_overlap(kdec_model* m, int on) {
@@ -754,6 +793,73 @@ int kdec_model_set_overlap(kdec_model* m, int on) {
 const float* kdec_model_har(const kdec_model* m) { return m ? static_cast<const float*>(m->har.data) : nullptr; }
 const float* kdec_model_gen_in(const kdec_model* m) {
     return m ? static_cast<const float*>(m->gen_in.data) : nullptr;
+}
+
+// ─── the producer step (KokoroDecodePrep) ───────────────────────────────────
+
+struct kdec_prep {
+    kdec_model* m = nullptr;
+    brosoundml::KokoroDecodePrep p;
+};
+
+int kdec_model_decode_prep(kdec_model* m, const float* t_en, int L, const int* pred_dur, const float* F0_pred,
+                           const float* N_pred, const float* F0_override, long F0_override_n,
+                           const float* N_override, long N_override_n, const float* ref_s, kdec_prep** out) {
+    if (!m || !out || !t_en || !pred_dur || !ref_s || L <= 0) return KDEC_EINVAL;
+    *out = nullptr;
+    try {
+        bt::set_runtime(m->ctx);
+        const std::vector<int32_t> dur(pred_dur, pred_dur + L);
+        long total = 0;
+        for (int d : dur) total += d;
+        const int cols = total > 0 && total < (1 << 24) ? static_cast<int>(2 * total) : 0;
+        auto view = [&](const float* p, int c) {
+            return p ? Tensor::view(Device::HIP, const_cast<float*>(p), 1, c) : Tensor{};
+        };
+        std::vector<float> f0v, nv;
+        if (F0_override) f0v.assign(F0_override, F0_override + F0_override_n);
+        if (N_override) nv.assign(N_override, N_override + N_override_n);
+        auto* pr = new kdec_prep;
+        pr->m = m;
+        try {
+            pr->p = brosoundml::prepare_decode_context(
+                m->bb, m->gen, m->hs, view(t_en, m->asr_dim * L), L, dur, view(F0_pred, cols), view(N_pred, cols),
+                view(ref_s, 2 * m->style_dim), F0_override ? &f0v : nullptr, N_override ? &nv : nullptr);
+        } catch (...) {
+            delete pr;
+            throw;
+        }
+        *out = pr;
+    } catch (const std::exception& e) {
+        return fail(m, KDEC_EINVAL, e.what());
+    }
+    return KDEC_OK;
+}
+
+int kdec_prep_destroy(kdec_prep* p) {
+    if (p) {
+        bt::set_runtime(p->m->ctx);
+        delete p;
+    }
+    return KDEC_OK;
+}
+
+int kdec_prep_total(const kdec_prep* p) { return p ? p->p.total : -1; }
+int kdec_prep_frames(const kdec_prep* p) { return p ? p->p.frames : -1; }
+
+const float* kdec_prep_ptr(const kdec_prep* p, int which) {
+    if (!p) return nullptr;
+    const brosoundml::DecoderLoraContext c = p->p.context();
+    const Tensor* t = nullptr;
+    switch (which) {
+        case 0: t = c.asr; break;
+        case 1: t = c.F0_pred; break;
+        case 2: t = c.N_pred; break;
+        case 3: t = c.har; break;
+        case 4: t = c.ref_s; break;
+        default: return nullptr;
+    }
+    return static_cast<const float*>(t->data);
 }
 
 // ─── leaky-ReLU sites (inspection) ──────────────────────────────────────────

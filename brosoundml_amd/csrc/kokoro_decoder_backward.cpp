@@ -830,7 +830,7 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
     if (static_cast<int>(naff.size()) < U || static_cast<int>(raff.size()) < U * K)
         fail(where, "one ResBlock1Affines per noise_res / resblock expected");
     check_batch(gen_in, gen.ups_C_in[0], L_in, where);
-    check_batch(har, gen.n_fft + 2, frames, where);
+    check_batch(har, gen.noise_convs.empty() ? gen.n_fft + 2 : gen.noise_convs[0].in_channels, frames, where);
     const int N = gen_in.rows;
     cache.stages.resize(U);
     if (cache.keep) cache.har = har;

@@ -21,6 +21,8 @@ def _ctype(decl: str):
         single_char = d.count("*") == 1 and d.replace("*", "").split() == ["char"]
         return ctypes.c_char_p if single_char else ctypes.c_void_p
     base = d.split()[-1] if d.split() else d
+    if base.endswith("_fn"):  # a callback typedef
+        return ctypes.c_void_p
     return {"int": ctypes.c_int, "long": ctypes.c_long, "float": ctypes.c_float,
             "double": ctypes.c_double, "size_t": ctypes.c_size_t, "void": None}[base]
 

@@ -114,6 +114,16 @@ int kdec_model_infer(kdec_model* m, int N, int T, const float* asr, const float*
  * audio (N, audio_len). For the base decoder (LoRA off). */
 int kdec_model_decode_back_half(kdec_model* m, int N, int T, const float* asr, const float* F0, const float* Nn,
                                 const float* ref_s, long ref_bs, float* audio);
+/* decode_back_half with the reference's cooperative cancellation
+ * (kokoro.cpp:387; Generator::forward, kokoro_modules.cpp:1418): cancel(user)
+ * is polled on the host before the generator and before each upsample stage
+ * (1 + n_ups polls when nothing cancels); once it returns nonzero no further
+ * work is enqueued, *cancelled is set to 1 and `audio` is left unwritten
+ * (the reference returns an empty buffer). cancel may be NULL. */
+typedef int (*kdec_cancel_fn)(void* user);
+int kdec_model_decode_back_half_cancellable(kdec_model* m, int N, int T, const float* asr, const float* F0,
+                                            const float* Nn, const float* ref_s, long ref_bs, float* audio,
+                                            kdec_cancel_fn cancel, void* user, int* cancelled);
 /* Stream overlap (no counterpart in the reference, whose calls are
  * synchronous): on = 1 (the default) runs the harmonic source and the conv
  * weight grads on a second stream beside the main chain; on = 0 keeps every
@@ -166,6 +176,30 @@ int kdec_dlora_load(kdec_dlora* d, const char* path);
  * 4 gate W1 (16, 3), 5 W2 (rank, 16), 6 dW1, 7 dW2; shape in rows, cols. */
 float* kdec_dlora_ptr(kdec_dlora* d, int which, int* rows, int* cols);
 float kdec_dlora_scale(const kdec_dlora* d);
+
+/* The producer step of Kokoro::prepare_decode_context after the predictor
+ * (kokoro.cpp:667-732; KokoroDecodePrep, kokoro.h:133-147) for one
+ * utterance: t_en (device, asr_dim x L text-encoder features), pred_dur
+ * (host, L per-phoneme frame counts), F0_pred / N_pred (device, 2*total
+ * each; may be NULL where an override is given), F0_override / N_override
+ * (host, 2*total values each, or NULL) and ref_s (device, 2*style_dim).
+ * Builds asr (length regulation on the device), the F0 / N grids and the
+ * harmonic source. Errors (KDEC_EINVAL, the reference's messages): total
+ * frame count 0 ("predicted total frame count is 0"), an override of the
+ * wrong size ("F0 override size must be 2*total (n)"), a harmonic-source
+ * frame count other than 2*total * prod(upsample rates) + 1, negative
+ * durations. The prep owns its tensors until kdec_prep_destroy; the model
+ * must outlive it. */
+typedef struct kdec_prep kdec_prep;
+int kdec_model_decode_prep(kdec_model* m, const float* t_en, int L, const int* pred_dur, const float* F0_pred,
+                           const float* N_pred, const float* F0_override, long F0_override_n,
+                           const float* N_override, long N_override_n, const float* ref_s, kdec_prep** out);
+int kdec_prep_destroy(kdec_prep* p);
+int kdec_prep_total(const kdec_prep* p);
+int kdec_prep_frames(const kdec_prep* p);
+/* The DecoderLoraContext view (kokoro.cpp:604-614): which 0 asr (asr_dim *
+ * total), 1 F0 (2*total), 2 N (2*total), 3 har ((n_fft+2) * frames), 4 ref_s. */
+const float* kdec_prep_ptr(const kdec_prep* p, int which);
 
 /* Leaky-ReLU sites of the decoder, in the order the forward visits them:
  * per AdaIN residual block (encode, decode.0, ...) the norm1 output and the
