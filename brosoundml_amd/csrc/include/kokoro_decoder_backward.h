@@ -231,6 +231,11 @@ struct GeneratorCache {
     int                        frames = 0;
     // Extension: false drops each block's cache as soon as the block is done.
     bool                       keep = true;
+    // Extension: a hipEvent_t recorded where har is produced on another
+    // stream, or null when har is ready. The forward waits on it just before
+    // the first noise conv, after stage 0's upsampling, so that work overlaps
+    // the producer; the forward clears it.
+    void*                      har_ready = nullptr;
 };
 
 void generator_forward_train(const Generator& gen,

@@ -609,12 +609,17 @@ int kdec_model_forward(kdec_model* m, int N, int T, const float* asr, const floa
         }
         bd::decoder_backbone_forward_train(m->bb, in(asr, m->asr_dim * T), in(F0, 2 * T), in(Nn, 2 * T), T,
                                            m->bbaff, 1e-5f, m->gen_in, m->bbc);
-        if (forked && hipStreamWaitEvent(ms, m->ev_join, 0) != hipSuccess)
-            return fail(m, KDEC_EHIP, "kdec_model_forward: join");
         const int init_C = m->dec_out[n_dec - 1];
         const int L_gen = m->gen_in.cols / init_C;
         Tensor out;
+        // the generator waits for har itself, after stage 0's upsampling
+        m->genc.har_ready = forked ? static_cast<void*>(m->ev_join) : nullptr;
         bd::generator_forward_train(m->gen, m->gen_in, L_gen, m->har, frames, m->naff, m->raff, out, m->genc);
+        if (m->genc.har_ready) {  // no noise conv consumed it: join here
+            m->genc.har_ready = nullptr;
+            if (hipStreamWaitEvent(ms, m->ev_join, 0) != hipSuccess)
+                return fail(m, KDEC_EHIP, "kdec_model_forward: join");
+        }
         const int alen = out.cols;
         hipStream_t s = static_cast<hipStream_t>(kdec_get_stream(m->ctx));
         hipError_t e = hipMemcpyAsync(audio, out.data, static_cast<size_t>(N) * alen * sizeof(float),

@@ -10,6 +10,7 @@
 #include "kdec_internal.hpp"
 
 #include <cmath>
+#include <type_traits>
 #include <vector>
 
 namespace kdec {
@@ -51,7 +52,10 @@ __device__ inline float env_at(const float* win, int m, int N, int hop, int fram
     return e;
 }
 
-// Per (n, frame): polar spectrum -> windowed irfft frame (N samples).
+// Per (n, frame): polar spectrum -> windowed irfft frame (N samples). NM >=
+// N bounds the per-lane arrays; their loops unroll fully so they stay in
+// registers.
+template <int NM>
 __global__ __launch_bounds__(FT) void spec_frames_k(const float* post, long post_bs,
                                                    const float* window, float* fbuf, int L, int N) {
     __shared__ float tc[MAXN / 2 + 1][MAXN], ts[MAXN / 2 + 1][MAXN], win[MAXN];
@@ -65,21 +69,29 @@ __global__ __launch_bounds__(FT) void spec_frames_k(const float* post, long post
     const int f = blockIdx.x * FT + threadIdx.x;
     if (f >= L) return;
     const float* P = post + b * post_bs;
-    float re[MAXN / 2 + 1], im[MAXN / 2 + 1];
-    for (int k = 0; k < F; ++k) {
-        const float mag = expf(P[static_cast<long>(k) * L + f]);
-        const float ang = sinf(P[static_cast<long>(F + k) * L + f]);
-        re[k] = mag * cosf(ang);
-        im[k] = mag * sinf(ang);
+    constexpr int FM = NM / 2 + 1;
+    float re[FM], im[FM];
+    float re_last = 0.0f;  // re[F - 1]
+#pragma clang loop unroll(full)
+    for (int k = 0; k < FM; ++k) {
+        re[k] = im[k] = 0.0f;
+        if (k < F) {
+            const float mag = expf(P[static_cast<long>(k) * L + f]);
+            const float ang = sinf(P[static_cast<long>(F + k) * L + f]);
+            re[k] = mag * cosf(ang);
+            im[k] = mag * sinf(ang);
+            if (k == F - 1) re_last = re[k];
+        }
     }
     float* out = fbuf + (static_cast<long>(b) * L + f) * N;
     const float invN = 1.0f / N;
+    const int kmax = (N & 1) == 0 ? F - 1 : F;
     for (int n = 0; n < N; ++n) {
         float acc = re[0];
-        if ((N & 1) == 0) acc += (n & 1) ? -re[F - 1] : re[F - 1];
-        const int kmax = (N & 1) == 0 ? F - 1 : F;
-        for (int k = 1; k < kmax; ++k)
-            acc += 2.0f * (re[k] * TC[k * N + n] - im[k] * TS[k * N + n]);
+        if ((N & 1) == 0) acc += (n & 1) ? -re_last : re_last;
+#pragma clang loop unroll(full)
+        for (int k = 1; k < FM; ++k)
+            if (k < kmax) acc += 2.0f * (re[k] * TC[k * N + n] - im[k] * TS[k * N + n]);
         out[n] = acc * invN * win[n];
     }
 }
@@ -106,7 +118,9 @@ __global__ void spec_ola_k(const float* fbuf, const float* window, float* audio,
     audio[b * audio_bs + j] = acc / e;
 }
 
-// Per (n, frame): adjoint of the frame's windowed irfft and of the polar map.
+// Per (n, frame): adjoint of the frame's windowed irfft and of the polar map
+// (NM >= N as in spec_frames_k).
+template <int NM>
 __global__ __launch_bounds__(FT) void spec_bwd_k(const float* post, long post_bs, const float* window,
                                                 const float* daudio, long da_bs, float* dpost,
                                                 long dp_bs, int L, int N, int hop) {
@@ -121,14 +135,18 @@ __global__ __launch_bounds__(FT) void spec_bwd_k(const float* post, long post_bs
     if (f >= L) return;
     const int sig_len = (L - 1) * hop;
     const float* dy = daudio + b * da_bs;
-    float dfr[MAXN];
+    float dfr[NM];
     const float invN = 1.0f / N;
-    for (int n = 0; n < N; ++n) {
-        const int m = f * hop + n;
-        const int j = m - N / 2;
-        float v = 0.0f;
-        if (j >= 0 && j < sig_len) v = dy[j] / env_at(win, m, N, hop, L);
-        dfr[n] = v * win[n] * invN;
+#pragma unroll
+    for (int n = 0; n < NM; ++n) {
+        dfr[n] = 0.0f;
+        if (n < N) {
+            const int m = f * hop + n;
+            const int j = m - N / 2;
+            float v = 0.0f;
+            if (j >= 0 && j < sig_len) v = dy[j] / env_at(win, m, N, hop, L);
+            dfr[n] = v * win[n] * invN;
+        }
     }
     const float* P = post + b * post_bs;
     float* D = dpost + b * dp_bs;
@@ -136,9 +154,12 @@ __global__ __launch_bounds__(FT) void spec_bwd_k(const float* post, long post_bs
         const bool edge = (k == 0) || ((N & 1) == 0 && k == F - 1);
         const float c = edge ? 1.0f : 2.0f;
         float re = 0.0f, im = 0.0f;
-        for (int n = 0; n < N; ++n) {
-            re += dfr[n] * TC[k * N + n];
-            im -= dfr[n] * TS[k * N + n];
+#pragma unroll
+        for (int n = 0; n < NM; ++n) {
+            if (n < N) {
+                re += dfr[n] * TC[k * N + n];
+                im -= dfr[n] * TS[k * N + n];
+            }
         }
         const float dRe = c * re;
         const float dIm = edge ? 0.0f : c * im;
@@ -155,62 +176,106 @@ __global__ __launch_bounds__(FT) void spec_bwd_k(const float* post, long post_bs
 }
 
 // ─── harmonic source ───
-// One lane per (utterance, harmonic) chain i = b*H + h: the reference's
-// sequential float phase recurrence (kokoro_modules.cpp:1602-1617), evaluated
-// with contraction off so each step rounds exactly as the host loop does.
-// Layout groups four steps per chain: phase[((t/4)*NH + i)*4 + t%4], so a
-// wave writes four steps of all its chains with one contiguous float4 store
-// (a store per step would leave the lone wave waiting on its store queue).
+// The reference's phase recurrence (kokoro_modules.cpp:1602-1617) is a
+// sequential float accumulation per (utterance, harmonic) chain i = b*H + h:
+// per sample ph = fl(ph + omega), then ph = fl(ph - 2pi) when ph > 2pi, with
+// omega = fl(fl(fl(2pi * (h+1)) * f0) / sr) constant over a frame of `us`
+// samples. Each step's rounding is reproduced exactly, in three passes:
+//   1. hs_start_k runs every chain, one lane each, through all samples in
+//      registers and keeps only the phase entering each frame;
+//   2. hs_phase_k gives one thread each (frame, chain): it re-runs that
+//      frame's steps from the stored start (the same operations, so the same
+//      values) and writes every phase;
+//   3. hs_merge_k forms the merged source per sample.
+// Pass 1 is the serial part; it issues three VALU operations per step and
+// stores nothing but the frame starts.
+constexpr float kHsTwoPi = 6.28318530717958647692f;
+
+__device__ inline float hs_omega(int h, float f0, float sr) {
+#pragma clang fp contract(off)
+    float omega = kHsTwoPi * static_cast<float>(h + 1);
+    omega = omega * f0;
+    return omega / sr;
+}
+
+// One step, branch free: y = fl(ph + omega); s = clamp((y - 2pi) * 2^21, 0,
+// 1) is exactly 1 when y > fl(2pi) and 0 otherwise (fl(2pi) and every float
+// y >= 4 are multiples of 2^-21, so a positive difference is at least 2^-21,
+// and the fma's product and sum are exact); fma(s, -2pi, y) is then
+// fl(y - 2pi) or y, the reference's wrap.
+__device__ inline float hs_step(float ph, float omega) {
+#pragma clang fp contract(off)
+    const float y = ph + omega;
+    const float s = __builtin_amdgcn_fmed3f(__builtin_fmaf(y, 0x1p21f, -kHsTwoPi * 0x1p21f), 0.0f, 1.0f);
+    return __builtin_fmaf(s, -kHsTwoPi, y);
+}
+
+// Layout of the per-sample phases: four steps of a chain are contiguous,
+// phase[((t/4)*NH + i)*4 + t%4], so a thread writes a chain's steps as float4
+// runs and the lanes of a wave (consecutive chains) write contiguous memory.
 __device__ inline long hs_index(int t, int i, int NH) {
     return (static_cast<long>(t >> 2) * NH + i) * 4 + (t & 3);
 }
 
-__global__ void hs_phase_k(const float* F0, long f0_bs, float* phase, int N, int H, int frame_count,
-                           int us, int sig_len, float sr) {
-#pragma clang fp contract(off)
+// Pass 1: start[fr * NH + i] = the phase of chain i entering frame fr.
+__global__ __launch_bounds__(64) void hs_start_k(const float* F0, long f0_bs, float* start, int N, int H,
+                                                 int frame_count, int us, int sig_len, int nfr, float sr) {
     const int NH = N * H;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= NH) return;
     const int b = i / H, h = i - b * H;
-    const float kTwoPi = 6.28318530717958647692f;
     const float* f0r = F0 + b * f0_bs;
     float ph = 0.0f;
-    for (int fr = 0; fr * us < sig_len; ++fr) {
-        const float f0 = f0r[fr < frame_count ? fr : frame_count - 1];
-        float omega = kTwoPi * static_cast<float>(h + 1);
-        omega = omega * f0;
-        omega = omega / sr;
-        const int t0 = fr * us;
-        const int t1 = min(t0 + us, sig_len);
-        int t = t0;
-        if ((t0 & 3) == 0) {
-            float4* out4 = reinterpret_cast<float4*>(phase) + static_cast<long>(t0 >> 2) * NH + i;
-            for (; t + 4 <= t1; t += 4, out4 += NH) {
-                float4 v;
-                ph = ph + omega;
-                if (ph > kTwoPi) ph = ph - kTwoPi;
-                v.x = ph;
-                ph = ph + omega;
-                if (ph > kTwoPi) ph = ph - kTwoPi;
-                v.y = ph;
-                ph = ph + omega;
-                if (ph > kTwoPi) ph = ph - kTwoPi;
-                v.z = ph;
-                ph = ph + omega;
-                if (ph > kTwoPi) ph = ph - kTwoPi;
-                v.w = ph;
-                *out4 = v;
-            }
+    float f0 = f0r[0];
+    for (int fr = 0; fr < nfr; ++fr) {
+        const float omega = hs_omega(h, f0, sr);
+        f0 = f0r[min(fr + 1, frame_count - 1)];  // next frame's, used after this frame's chain
+        start[static_cast<long>(fr) * NH + i] = ph;
+        const int n = min(us, sig_len - fr * us);
+        int t = 0;
+        for (; t + 4 <= n; t += 4) {
+            ph = hs_step(ph, omega);
+            ph = hs_step(ph, omega);
+            ph = hs_step(ph, omega);
+            ph = hs_step(ph, omega);
         }
-        for (; t < t1; ++t) {
-            ph = ph + omega;
-            if (ph > kTwoPi) ph = ph - kTwoPi;
-            phase[hs_index(t, i, NH)] = ph;
-        }
+        for (; t < n; ++t) ph = hs_step(ph, omega);
     }
 }
 
-// merged[b, t] = tanh(lb + sum_h lW[h] * sin(phase) * amp * uv)
+// Pass 2: thread g = fr * NH + i re-runs frame fr of chain i.
+__global__ void hs_phase_k(const float* start, const float* F0, long f0_bs, float* phase, int N, int H,
+                           int frame_count, int us, int sig_len, int nfr, float sr) {
+    const int NH = N * H;
+    const long g = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (g >= static_cast<long>(nfr) * NH) return;
+    const int fr = static_cast<int>(g / NH), i = static_cast<int>(g - static_cast<long>(fr) * NH);
+    const int b = i / H, h = i - b * H;
+    const float omega = hs_omega(h, F0[b * f0_bs + min(fr, frame_count - 1)], sr);
+    float ph = start[g];
+    const int t0 = fr * us;
+    const int t1 = min(t0 + us, sig_len);
+    int t = t0;
+    for (; t < t1 && (t & 3) != 0; ++t) {
+        ph = hs_step(ph, omega);
+        phase[hs_index(t, i, NH)] = ph;
+    }
+    float4* out4 = reinterpret_cast<float4*>(phase) + static_cast<long>(t >> 2) * NH + i;
+    for (; t + 4 <= t1; t += 4, out4 += NH) {
+        float4 v;
+        v.x = ph = hs_step(ph, omega);
+        v.y = ph = hs_step(ph, omega);
+        v.z = ph = hs_step(ph, omega);
+        v.w = ph = hs_step(ph, omega);
+        *out4 = v;
+    }
+    for (; t < t1; ++t) {
+        ph = hs_step(ph, omega);
+        phase[hs_index(t, i, NH)] = ph;
+    }
+}
+
+// Pass 3: merged[b, t] = tanh(lb + sum_h lW[h] * sin(phase) * amp * uv)
 __global__ void hs_merge_k(const float* phase, const float* F0, long f0_bs, const float* lW,
                            const float* lb, float* merged, int N, int H, int frame_count, int us,
                            int sig_len) {
@@ -234,6 +299,8 @@ __global__ void hs_merge_k(const float* phase, const float* F0, long f0_bs, cons
 }
 
 // STFT (center, reflect pad) -> har[b, k, f] = |X|, har[b, F+k, f] = atan2
+// (NM >= N as in spec_frames_k)
+template <int NM>
 __global__ __launch_bounds__(FT) void hs_stft_k(const float* merged, float* har, long har_bs,
                                                int sig_len, int N, int hop, int frames) {
     __shared__ float tc[MAXN / 2 + 1][MAXN], ts[MAXN / 2 + 1][MAXN], win[MAXN];
@@ -247,19 +314,26 @@ __global__ __launch_bounds__(FT) void hs_stft_k(const float* merged, float* har,
     if (f >= frames) return;
     const float* x = merged + static_cast<long>(b) * sig_len;
     const int pad = N / 2;
-    float v[MAXN];
-    for (int n = 0; n < N; ++n) {
-        int j = f * hop + n - pad;
-        if (j < 0) j = -j;
-        if (j >= sig_len) j = 2 * (sig_len - 1) - j;
-        v[n] = win[n] * x[j];
+    float v[NM];
+#pragma unroll
+    for (int n = 0; n < NM; ++n) {
+        v[n] = 0.0f;
+        if (n < N) {
+            int j = f * hop + n - pad;
+            if (j < 0) j = -j;
+            if (j >= sig_len) j = 2 * (sig_len - 1) - j;
+            v[n] = win[n] * x[j];
+        }
     }
     float* out = har + b * har_bs;
     for (int k = 0; k < F; ++k) {
         double re = 0.0, im = 0.0;
-        for (int n = 0; n < N; ++n) {
-            re += static_cast<double>(v[n]) * TC[k * N + n];
-            im -= static_cast<double>(v[n]) * TS[k * N + n];
+#pragma unroll
+        for (int n = 0; n < NM; ++n) {
+            if (n < N) {
+                re += static_cast<double>(v[n]) * TC[k * N + n];
+                im -= static_cast<double>(v[n]) * TS[k * N + n];
+            }
         }
         const float ref = static_cast<float>(re), imf = static_cast<float>(im);
         out[static_cast<long>(k) * frames + f] =
@@ -431,6 +505,24 @@ unsigned g1(long n, long per = 256, long cap = 65535) {
 }  // namespace
 }  // namespace kdec
 
+namespace kdec {
+namespace {
+// Calls fn with the smallest per-lane array bound (8, 16, 32 or 64) that
+// holds an n_fft-point frame.
+template <typename Fn>
+void with_nfft_bound(int n_fft, Fn&& fn) {
+    if (n_fft <= 8)
+        fn(std::integral_constant<int, 8>{});
+    else if (n_fft <= 16)
+        fn(std::integral_constant<int, 16>{});
+    else if (n_fft <= 32)
+        fn(std::integral_constant<int, 32>{});
+    else
+        fn(std::integral_constant<int, MAXN>{});
+}
+}  // namespace
+}  // namespace kdec
+
 using namespace kdec;
 
 extern "C" {
@@ -445,8 +537,10 @@ int kdec_spectral_fwd(kdec_ctx* ctx, const float* post, long post_bs,
     Workspace fb(ctx, static_cast<size_t>(N) * L * n_fft * sizeof(float));
     if (!fb.p) return KDEC_ENOMEM;
     ProfScope ps(ctx, "spectral", 0);
-    hipLaunchKernelGGL(spec_frames_k, dim3(static_cast<unsigned>(cdiv(L, FT)), N), dim3(FT), 0, ctx->stream,
-                       post, post_bs, window, fb.as<float>(), L, n_fft);
+    with_nfft_bound(n_fft, [&](auto nm) {
+        hipLaunchKernelGGL(spec_frames_k<decltype(nm)::value>, dim3(static_cast<unsigned>(cdiv(L, FT)), N),
+                           dim3(FT), 0, ctx->stream, post, post_bs, window, fb.as<float>(), L, n_fft);
+    });
     if (int rc = launch_check(ctx, "spec_frames")) return rc;
     hipLaunchKernelGGL(spec_ola_k, dim3(static_cast<unsigned>(cdiv(sig, 256)), N), dim3(256), 0, ctx->stream,
                        fb.as<float>(), window, audio, audio_bs, L, n_fft, hop, sig);
@@ -462,8 +556,10 @@ int kdec_spectral_bwd(kdec_ctx* ctx, const float* post, long post_bs,
                         hop <= n_fft,
                "kdec_spectral_bwd: bad arguments");
     ProfScope ps(ctx, "spectral", 0);
-    hipLaunchKernelGGL(spec_bwd_k, dim3(static_cast<unsigned>(cdiv(L, FT)), N), dim3(FT), 0, ctx->stream, post,
-                       post_bs, window, daudio, daudio_bs, dpost, dpost_bs, L, n_fft, hop);
+    with_nfft_bound(n_fft, [&](auto nm) {
+        hipLaunchKernelGGL(spec_bwd_k<decltype(nm)::value>, dim3(static_cast<unsigned>(cdiv(L, FT)), N), dim3(FT),
+                           0, ctx->stream, post, post_bs, window, daudio, daudio_bs, dpost, dpost_bs, L, n_fft, hop);
+    });
     return launch_check(ctx, "spec_bwd");
 }
 
@@ -481,19 +577,27 @@ int kdec_harmonic_source(kdec_ctx* ctx, const float* F0, long f0_bs,
     KDEC_CHECK(ctx, sig > n_fft / 2, "kdec_harmonic_source: signal shorter than the STFT pad");
     const int frames = sig / hop + 1;
     KDEC_CHECK(ctx, har_bs >= static_cast<long>(n_fft + 2) * frames, "kdec_harmonic_source: har stride too small");
+    const int nfr = static_cast<int>(cdiv(sig, upsample_scale));
+    Workspace st(ctx, static_cast<size_t>(nfr) * N * H * sizeof(float));
     Workspace ph(ctx, static_cast<size_t>(N) * H * ((sig + 3) / 4 * 4) * sizeof(float));
     Workspace mg(ctx, static_cast<size_t>(N) * sig * sizeof(float));
-    if (!ph.p || !mg.p) return KDEC_ENOMEM;
+    if (!st.p || !ph.p || !mg.p) return KDEC_ENOMEM;
     ProfScope ps(ctx, "harmonic_source", 0);
-    hipLaunchKernelGGL(hs_phase_k, dim3(static_cast<unsigned>(cdiv(N * H, 64))), dim3(64), 0, ctx->stream, F0,
-                       f0_bs, ph.as<float>(), N, H, frame_count, upsample_scale, sig,
-                       static_cast<float>(sample_rate));
+    const float sr = static_cast<float>(sample_rate);
+    hipLaunchKernelGGL(hs_start_k, dim3(static_cast<unsigned>(cdiv(N * H, 64))), dim3(64), 0, ctx->stream, F0,
+                       f0_bs, st.as<float>(), N, H, frame_count, upsample_scale, sig, nfr, sr);
+    if (int rc = launch_check(ctx, "hs_start")) return rc;
+    hipLaunchKernelGGL(hs_phase_k, dim3(static_cast<unsigned>(cdiv(static_cast<long>(nfr) * N * H, 256))), dim3(256), 0,
+                       ctx->stream, st.as<float>(), F0, f0_bs, ph.as<float>(), N, H, frame_count, upsample_scale, sig,
+                       nfr, sr);
     if (int rc = launch_check(ctx, "hs_phase")) return rc;
     hipLaunchKernelGGL(hs_merge_k, dim3(static_cast<unsigned>(cdiv(sig, 256)), N), dim3(256), 0, ctx->stream,
                        ph.as<float>(), F0, f0_bs, lW, lb, mg.as<float>(), N, H, frame_count, upsample_scale, sig);
     if (int rc = launch_check(ctx, "hs_merge")) return rc;
-    hipLaunchKernelGGL(hs_stft_k, dim3(static_cast<unsigned>(cdiv(frames, FT)), N), dim3(FT), 0, ctx->stream,
-                       mg.as<float>(), har, har_bs, sig, n_fft, hop, frames);
+    with_nfft_bound(n_fft, [&](auto nm) {
+        hipLaunchKernelGGL(hs_stft_k<decltype(nm)::value>, dim3(static_cast<unsigned>(cdiv(frames, FT)), N),
+                           dim3(FT), 0, ctx->stream, mg.as<float>(), har, har_bs, sig, n_fft, hop, frames);
+    });
     return launch_check(ctx, "hs_stft");
 }
 

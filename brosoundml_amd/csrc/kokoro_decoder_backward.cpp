@@ -846,15 +846,8 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
         const int C_out = gen.ups_C_out[i];
         Tensor a = leaky(x, 0.1f);
 
-        // noise branch
-        Tensor x_source = conv_fwd(gen.noise_convs[i], har, frames);
-        const int L_src = x_source.cols / C_out;
-        Tensor src;
-        adain_resblock1_forward_train(gen.noise_res[i], x_source, C_out, L_src, naff[i].g1, naff[i].b1, naff[i].g2,
-                                      naff[i].b2, src, sc.noise);
-        if (!cache.keep) sc.noise = AdainResBlock1Cache{};
-
-        // ups (+ left reflect pad on the last stage)
+        // ups (+ left reflect pad on the last stage); it does not read har, so
+        // it goes first and overlaps a producer still writing har
         const int kL = gen.ups_k[i], s = gen.ups_stride[i], p = gen.ups_pad[i];
         int L_x = (L - 1) * s - 2 * p + (kL - 1) + 1;
         Tensor u = dev(N, C_out * L_x);
@@ -868,6 +861,20 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
             u = padded;
             L_x += 1;
         }
+
+        // noise branch
+        if (cache.har_ready) {
+            if (hipStreamWaitEvent(static_cast<hipStream_t>(kdec_get_stream(kctx())),
+                                   static_cast<hipEvent_t>(cache.har_ready), 0) != hipSuccess)
+                fail(where, "waiting for the harmonic source");
+            cache.har_ready = nullptr;
+        }
+        Tensor x_source = conv_fwd(gen.noise_convs[i], har, frames);
+        const int L_src = x_source.cols / C_out;
+        Tensor src;
+        adain_resblock1_forward_train(gen.noise_res[i], x_source, C_out, L_src, naff[i].g1, naff[i].b1, naff[i].g2,
+                                      naff[i].b2, src, sc.noise);
+        if (!cache.keep) sc.noise = AdainResBlock1Cache{};
         if (L_src != L_x)
             fail(where, "noise source length " + std::to_string(L_src) + " != upsampled length " +
                             std::to_string(L_x) + " at stage " + std::to_string(i));
