@@ -349,33 +349,68 @@ __device__ inline void row_st_grp(__amdgpu_buffer_rsrc_t r, int j, const float* 
     }
 }
 
+// Rows longer than the register part (TT > 0): registers hold the NTB*EPR
+// elements [head, head + NTB*EPR), 16-B aligned when V = 4 (head: the 0..3
+// elements before the row's first 16-B boundary, given 16-B aligned bases and
+// batch strides), and the rest of the row -- the head elements, then the
+// elements past the register part -- is dealt out as i = tid + j*NTB, i < the
+// rest's length, element rest_elem(i).
+__device__ inline int row_head(int c, int L) { return (4 - (((c & 3) * (L & 3)) & 3)) & 3; }
+__device__ inline int rest_elem(int i, int head, int rb) { return i < head ? i : i + rb; }
+
 // stats[row] = (mean, rstd); Y = act((1 + gamma) * xhat + beta), the row held
 // in registers between the statistics and the affine pass (V as for the
-// backward: 16-B groups on aligned rows of a multiple of 4 floats).
-template <int NTB, int EPR, int V>
+// backward: 16-B groups on aligned rows of a multiple of 4 floats, or past
+// the head of a long row). TT > 0: up to TT rest elements per thread, also
+// held in registers.
+template <int NTB, int EPR, int V, int TT>
 __global__ __launch_bounds__(NTB) void adain_fwd_row_k(AdainArgs g, float eps, float2* stats, float* Y, long y_bs,
                                                       float* Yp, long yp_bs) {
     static_assert(EPR % V == 0, "whole groups per thread");
     __shared__ double red[NTB / 64];
+    constexpr int RB = NTB * EPR;
     const int row = blockIdx.x;
     const int n = row / g.C, c = row - n * g.C;
     const long off = static_cast<long>(c) * g.L;
     const float* x = g.X + n * g.x_bs + off;
-    const __amdgpu_buffer_rsrc_t xr = row_rsrc(x, g.L);
+    const int head = (TT > 0 && V == 4) ? row_head(c, g.L) : 0;
+    const int Lr = TT > 0 ? RB : g.L;      // register-part length
+    const int nrest = TT > 0 ? g.L - RB : 0;
+    const __amdgpu_buffer_rsrc_t xr = row_rsrc(x + head, Lr);
     const double x0 = x[0];  // shift for a well-conditioned variance
     float v[EPR];
 #pragma unroll
     for (int j = 0; j < EPR / V; ++j) row_ld_grp<V, NTB>(xr, j, v + V * j);
+    // the rest through a descriptor over the whole row: one offset register
+    // per element, and lanes past the rest read 0
+    const __amdgpu_buffer_rsrc_t xw = row_rsrc(x, TT > 0 ? g.L : 0);
+    float t[TT > 0 ? TT : 1];
+#pragma unroll
+    for (int j = 0; j < TT; ++j) {
+        const int i = threadIdx.x + j * NTB;
+        t[j] = row_ld(xw, i < nrest ? rest_elem(i, head, RB) * 4 : g.L * 4, 0, NTB);
+    }
     double s1 = 0.0, s2 = 0.0;
 #pragma unroll
     for (int j = 0; j < EPR / V; ++j) {
-        if (V * (j * NTB + threadIdx.x) >= g.L) continue;  // past the row (a group lies wholly in or out)
+        if (V * (j * NTB + threadIdx.x) >= Lr) continue;  // past the row (a group lies wholly in or out)
 #pragma unroll
         for (int e = 0; e < V; ++e) {
             const double d = static_cast<double>(v[V * j + e]) - x0;
             s1 += d;
             s2 += d * d;
+            // one difference live at a time (else all EPR + TT of them are
+            // kept in double between a sum pass and a square pass)
+            asm volatile("" : "+v"(s1), "+v"(s2));
         }
+    }
+#pragma unroll
+    for (int j = 0; j < TT; ++j) {
+        if (threadIdx.x + j * NTB >= nrest) continue;
+        const double d = static_cast<double>(t[j]) - x0;
+        s1 += d;
+        s2 += d * d;
+        asm volatile("" : "+v"(s1), "+v"(s2));
     }
     s1 = block_sum_n<NTB>(s1, red);
     s2 = block_sum_n<NTB>(s2, red);
@@ -388,8 +423,10 @@ __global__ __launch_bounds__(NTB) void adain_fwd_row_k(AdainArgs g, float eps, f
     const float bt = g.beta ? g.beta[n * g.gb_bs + c] : 0.0f;
     const float a = g.act == KDEC_ACT_SNAKE ? g.alpha[c] : 1.0f;
     const float ia = 1.0f / a;
-    const __amdgpu_buffer_rsrc_t yr = row_rsrc(Y + n * y_bs + off, g.L);
-    const __amdgpu_buffer_rsrc_t pr = row_rsrc(Yp ? Yp + n * yp_bs + off : Y, Yp ? g.L : 0);
+    float* yrow = Y + n * y_bs + off;
+    float* prow = Yp ? Yp + n * yp_bs + off : nullptr;
+    const __amdgpu_buffer_rsrc_t yr = row_rsrc(yrow + head, Lr);
+    const __amdgpu_buffer_rsrc_t pr = row_rsrc(prow ? prow + head : Y, prow ? Lr : 0);
 #pragma unroll
     for (int j = 0; j < EPR / V; ++j) {
         float yv[V], sv[V];
@@ -402,14 +439,31 @@ __global__ __launch_bounds__(NTB) void adain_fwd_row_k(AdainArgs g, float eps, f
         row_st_grp<V, NTB>(yr, j, yv);
         row_st_grp<V, NTB>(pr, j, sv);  // dropped without a pre-activation output
     }
+    const __amdgpu_buffer_rsrc_t yw = row_rsrc(yrow, TT > 0 ? g.L : 0);
+    const __amdgpu_buffer_rsrc_t pw = row_rsrc(prow ? prow : Y, (TT > 0 && prow) ? g.L : 0);
+#pragma unroll
+    for (int j = 0; j < TT; ++j) {
+        const int i = threadIdx.x + j * NTB;
+        if (i >= nrest) continue;
+        const int lo = rest_elem(i, head, RB) * 4;
+        const float xh = (t[j] - st.x) * st.y;
+        const float sv = g1 * xh + bt;
+        row_st(yw, act_fwd(g.act, sv, g.slope, a, ia), lo, 0, NTB);
+        row_st(pw, sv, lo, 0, NTB);  // dropped without a pre-activation output
+    }
 }
 
-template <int NTB, int EPR, bool BOTH, int V>
+// TT > 0: a long row (layout as adain_fwd_row_k); the rest's x and ds stay
+// in dynamic LDS, [0, nrest) and [nrest, 2*nrest), each thread touching only
+// its own elements.
+template <int NTB, int EPR, bool BOTH, int V, int TT>
 __global__ __launch_bounds__(NTB) void adain_bwd_row_k(AdainArgs g, const float* dY, long dy_bs, const float* R,
                                                       long r_bs, float* dX, long dx_bs, float* dgamma,
                                                       float* dbeta, long dgb_bs, float* dalpha_part,
                                                       float* dalpha_acc) {
     __shared__ double red[NTB / 64];
+    extern __shared__ float rest[];
+    constexpr int RB = NTB * EPR;
     const int row = blockIdx.x;
     const int n = row / g.C, c = row - n * g.C;
     const float2 st = g.stats[row];
@@ -417,9 +471,15 @@ __global__ __launch_bounds__(NTB) void adain_bwd_row_k(AdainArgs g, const float*
     const float bt = g.beta ? g.beta[n * g.gb_bs + c] : 0.0f;
     const float a = g.act == KDEC_ACT_SNAKE ? g.alpha[c] : 0.0f;
     const long off = static_cast<long>(c) * g.L;
-    const __amdgpu_buffer_rsrc_t xr = row_rsrc(g.X + n * g.x_bs + off, g.L);
-    const __amdgpu_buffer_rsrc_t dr = row_rsrc(dY + n * dy_bs + off, g.L);
+    const float* xrow = g.X + n * g.x_bs + off;
+    const float* dyrow = dY + n * dy_bs + off;
+    const int head = (TT > 0 && V == 4) ? row_head(c, g.L) : 0;
+    const int Lr = TT > 0 ? RB : g.L;      // register-part length
+    const int nrest = TT > 0 ? g.L - RB : 0;
+    const __amdgpu_buffer_rsrc_t xr = row_rsrc(xrow + head, Lr);
+    const __amdgpu_buffer_rsrc_t dr = row_rsrc(dyrow + head, Lr);
     static_assert(V == 1 || (BOTH && EPR % 4 == 0), "16-B row access holds both rows");
+    static_assert(TT == 0 || BOTH, "long rows hold both rows");
     const int vo = threadIdx.x * 4;
     float xv[EPR], dv[BOTH ? EPR : 1];
 #pragma unroll
@@ -427,8 +487,23 @@ __global__ __launch_bounds__(NTB) void adain_bwd_row_k(AdainArgs g, const float*
         row_ld_grp<V, NTB>(xr, j, xv + V * j);
         if (BOTH) row_ld_grp<V, NTB>(dr, j, dv + V * j);  // zero past the row: no contribution
     }
-    // per-thread sums of at most EPR terms in float, across the block in double
+    // per-thread sums of at most EPR + TT terms in float, across the block in double
     float fsd = 0.0f, fsdx = 0.0f, fsa = 0.0f;
+    const __amdgpu_buffer_rsrc_t xw = row_rsrc(xrow, TT > 0 ? g.L : 0);
+    const __amdgpu_buffer_rsrc_t dw = row_rsrc(dyrow, TT > 0 ? g.L : 0);
+#pragma unroll
+    for (int j = 0; j < TT; ++j) {
+        const int i = threadIdx.x + j * NTB;
+        if (i >= nrest) continue;
+        const int lo = rest_elem(i, head, RB) * 4;
+        const float xl = row_ld(xw, lo, 0, NTB);
+        const float xh = (xl - st.x) * st.y;
+        const float ds = act_bwd(g.act, row_ld(dw, lo, 0, NTB), g1 * xh + bt, g.slope, a, fsa);
+        rest[i] = xl;
+        rest[nrest + i] = ds;
+        fsd += ds;
+        fsdx += ds * xh;
+    }
 #pragma unroll
     for (int j = 0; j < EPR; ++j) {
         const float dyj = BOTH ? dv[j] : row_ld(dr, vo, j, NTB);
@@ -451,9 +526,22 @@ __global__ __launch_bounds__(NTB) void adain_bwd_row_k(AdainArgs g, const float*
     const float mds = static_cast<float>(sd / g.L);
     const float mdsx = static_cast<float>(sdx / g.L);
     const float k1 = st.y * g1;
-    const __amdgpu_buffer_rsrc_t xo = row_rsrc(dX + n * dx_bs + off, g.L);
+    float* dxrow = dX + n * dx_bs + off;
+    const float* rrow = R ? R + n * r_bs + off : nullptr;
+    const __amdgpu_buffer_rsrc_t xo = row_rsrc(dxrow + head, Lr);
     // without a residual the descriptor covers nothing and its loads read 0
-    const __amdgpu_buffer_rsrc_t rr = row_rsrc(R ? R + n * r_bs + off : dY, R ? g.L : 0);
+    const __amdgpu_buffer_rsrc_t rr = row_rsrc(rrow ? rrow + head : dY, rrow ? Lr : 0);
+    const __amdgpu_buffer_rsrc_t ow = row_rsrc(dxrow, TT > 0 ? g.L : 0);
+    const __amdgpu_buffer_rsrc_t rw = row_rsrc(rrow ? rrow : dY, (TT > 0 && rrow) ? g.L : 0);
+#pragma unroll
+    for (int j = 0; j < TT; ++j) {
+        const int i = threadIdx.x + j * NTB;
+        if (i >= nrest) continue;
+        const int lo = rest_elem(i, head, RB) * 4;
+        const float xh = (rest[i] - st.x) * st.y;
+        const float val = k1 * (rest[nrest + i] - mds - xh * mdsx) + row_ld(rw, lo, 0, NTB);  // R or 0
+        row_st(ow, val, lo, 0, NTB);
+    }
 #pragma unroll
     for (int j = 0; j < EPR / V; ++j) {
         float val[V];
@@ -585,45 +673,76 @@ __global__ void fill_k(float* Y, long n, float v) {
 // decoder's shapes: the forward up to 4096 with 4-byte accesses, up to 49152
 // with 16-byte ones; the backward up to 49152 with x and dY both held).
 struct RowShape {
-    int ntb, epr;
+    int ntb, epr, tt = 0;
 };
+// Long rows: 1024 threads, each with EPR register elements and up to TT
+// rest elements (the forward keeps them in registers, the backward holds x
+// and dY for its register part and stores the rest's x and ds in LDS).
+constexpr int FWD_LONG_EPR = 48, FWD_LONG_TT = 13;
+constexpr int BWD_LONG_EPR = 44, BWD_LONG_TT = 17;
+static_assert(FWD_LONG_EPR + FWD_LONG_TT == BWD_LONG_EPR + BWD_LONG_TT, "one long-row limit");
+// A long row holds its register part [head, head + 1024*EPR) with a head of
+// up to 3 elements, so it is at least 1024*EPR + 3 long (both shapes' first
+// long length, 49155, lies past the register-only kernels), and at most the
+// register part plus 1024*TT rest elements, the head among them.
+constexpr int ROW_LONG_MIN = 1024 * FWD_LONG_EPR + 3;
+constexpr int ROW_LONG_MAX = 1024 * (FWD_LONG_EPR + FWD_LONG_TT);
+static_assert(ROW_LONG_MIN >= 1024 * BWD_LONG_EPR + 3, "the backward's register part fits every long row");
 bool aligned16(const void* p) { return (reinterpret_cast<unsigned long long>(p) & 15) == 0; }
 
-RowShape row_shape_fwd(int L, bool v4) {
+// v4: 16-B accesses are possible (every row starts on 16 B); v4_long: every
+// row's register part does (16-B aligned bases and batch strides, any L).
+RowShape row_shape_fwd(int L, bool v4, bool v4_long) {
     if (L <= 1024) return {256, 4};
     if (L <= 4096) return {256, 16};
+    if (L > 49152)
+        return (v4_long && L >= ROW_LONG_MIN && L <= ROW_LONG_MAX) ? RowShape{1024, FWD_LONG_EPR, FWD_LONG_TT}
+                                                                    : RowShape{0, 0};
     if (!v4) return {0, 0};
     if (L <= 16384) return {1024, 16};
-    if (L <= 49152) return {1024, 48};
-    return {0, 0};
+    return {1024, 48};
 }
-bool fwd_v4(const AdainArgs& g, const float* Y, long y_bs, const float* Yp, long yp_bs) {
-    return g.L % 4 == 0 && g.x_bs % 4 == 0 && y_bs % 4 == 0 && aligned16(g.X) && aligned16(Y) &&
+bool fwd_v4_long(const AdainArgs& g, const float* Y, long y_bs, const float* Yp, long yp_bs) {
+    return g.x_bs % 4 == 0 && y_bs % 4 == 0 && aligned16(g.X) && aligned16(Y) &&
            (!Yp || (yp_bs % 4 == 0 && aligned16(Yp)));
 }
-RowShape row_shape_bwd(int L) {
+bool fwd_v4(const AdainArgs& g, const float* Y, long y_bs, const float* Yp, long yp_bs) {
+    return g.L % 4 == 0 && fwd_v4_long(g, Y, y_bs, Yp, yp_bs);
+}
+RowShape row_shape_fwd(const AdainArgs& g, const float* Y, long y_bs, const float* Yp, long yp_bs) {
+    return row_shape_fwd(g.L, fwd_v4(g, Y, y_bs, Yp, yp_bs), fwd_v4_long(g, Y, y_bs, Yp, yp_bs));
+}
+bool bwd_v4_long(const AdainArgs& g, const float* dY, long dy_bs, const float* R, long r_bs, const float* dX,
+                 long dx_bs) {
+    return g.x_bs % 4 == 0 && dy_bs % 4 == 0 && dx_bs % 4 == 0 && aligned16(g.X) && aligned16(dY) &&
+           aligned16(dX) && (!R || (r_bs % 4 == 0 && aligned16(R)));
+}
+// long rows need the 16-B register part (v4_long)
+RowShape row_shape_bwd(int L, bool v4_long) {
     if (L <= 1024) return {256, 4};
     if (L <= 4096) return {256, 16};
     if (L <= 16384) return {1024, 16};
     if (L <= 49152) return {1024, 48};
+    if (v4_long && L >= ROW_LONG_MIN && L <= ROW_LONG_MAX) return {1024, BWD_LONG_EPR, BWD_LONG_TT};
     return {0, 0};
 }
 
 int launch_fwd_row(kdec_ctx* ctx, RowShape rsh, unsigned rows, const AdainArgs& g, float eps, float2* st, float* Y,
                    long y_bs, float* Yp, long yp_bs) {
-    const bool v4 = fwd_v4(g, Y, y_bs, Yp, yp_bs);
-#define KDEC_FWD_ROW(T, E, V)                                                                                  \
-    if (rsh.ntb == T && rsh.epr == E && (V == 4) == v4) {                                                      \
-        hipLaunchKernelGGL((adain_fwd_row_k<T, E, V>), dim3(rows), dim3(T), 0, ctx->stream, g, eps, st, Y, y_bs, \
-                           Yp, yp_bs);                                                                         \
+    const bool v4 = rsh.tt ? true : fwd_v4(g, Y, y_bs, Yp, yp_bs);
+#define KDEC_FWD_ROW(T, E, V, TT)                                                                              \
+    if (rsh.ntb == T && rsh.epr == E && rsh.tt == TT && (V == 4) == v4) {                                      \
+        hipLaunchKernelGGL((adain_fwd_row_k<T, E, V, TT>), dim3(rows), dim3(T), 0, ctx->stream, g, eps, st, Y,  \
+                           y_bs, Yp, yp_bs);                                                                   \
         return launch_check(ctx, "adain_fwd_row");                                                            \
     }
-    KDEC_FWD_ROW(256, 4, 1)
-    KDEC_FWD_ROW(256, 16, 1)
-    KDEC_FWD_ROW(256, 4, 4)
-    KDEC_FWD_ROW(256, 16, 4)
-    KDEC_FWD_ROW(1024, 16, 4)
-    KDEC_FWD_ROW(1024, 48, 4)
+    KDEC_FWD_ROW(256, 4, 1, 0)
+    KDEC_FWD_ROW(256, 16, 1, 0)
+    KDEC_FWD_ROW(256, 4, 4, 0)
+    KDEC_FWD_ROW(256, 16, 4, 0)
+    KDEC_FWD_ROW(1024, 16, 4, 0)
+    KDEC_FWD_ROW(1024, 48, 4, 0)
+    KDEC_FWD_ROW(1024, FWD_LONG_EPR, 4, FWD_LONG_TT)
 #undef KDEC_FWD_ROW
     return fail(ctx, KDEC_EINVAL, "adain forward: no row kernel for this length");
 }
@@ -631,17 +750,31 @@ int launch_fwd_row(kdec_ctx* ctx, RowShape rsh, unsigned rows, const AdainArgs& 
 int launch_bwd_row(kdec_ctx* ctx, RowShape rsh, unsigned rows, const AdainArgs& g, const float* dY, long dy_bs,
                    const float* R, long r_bs, float* dX, long dx_bs, float* dgamma, float* dbeta, long dgb_bs,
                    float* apart, float* aacc) {
+    if (rsh.tt) {  // long rows: the 16-B register part, the rest in LDS
+        if (rsh.ntb != 1024 || rsh.epr != BWD_LONG_EPR || rsh.tt != BWD_LONG_TT)
+            return fail(ctx, KDEC_EINVAL, "adain backward: no row kernel for this length");
+        const void* kern =
+            reinterpret_cast<const void*>(&adain_bwd_row_k<1024, BWD_LONG_EPR, true, 4, BWD_LONG_TT>);
+        const size_t lds = 2 * static_cast<size_t>(g.L - 1024 * BWD_LONG_EPR) * sizeof(float);
+        static std::once_flag once;
+        std::call_once(once, [&] {
+            (void)hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      2 * 1024 * BWD_LONG_TT * static_cast<int>(sizeof(float)));
+        });
+        hipLaunchKernelGGL((adain_bwd_row_k<1024, BWD_LONG_EPR, true, 4, BWD_LONG_TT>), dim3(rows), dim3(1024), lds,
+                           ctx->stream, g, dY, dy_bs, R, r_bs, dX, dx_bs, dgamma, dbeta, dgb_bs, apart, aacc);
+        return launch_check(ctx, "adain_bwd_row");
+    }
     // 16-B accesses when every row of every tensor starts on 16 B
-    const bool v4 = g.L % 4 == 0 && g.x_bs % 4 == 0 && dy_bs % 4 == 0 && dx_bs % 4 == 0 && aligned16(g.X) &&
-                    aligned16(dY) && aligned16(dX) && (!R || (r_bs % 4 == 0 && aligned16(R)));
+    const bool v4 = g.L % 4 == 0 && bwd_v4_long(g, dY, dy_bs, R, r_bs, dX, dx_bs);
 #define KDEC_BWD_ROW(T, E, B)                                                                                  \
     if (rsh.ntb == T && rsh.epr == E) {                                                                        \
         if (v4)                                                                                                \
-            hipLaunchKernelGGL((adain_bwd_row_k<T, E, B, 4>), dim3(rows), dim3(T), 0, ctx->stream, g, dY, dy_bs, \
-                               R, r_bs, dX, dx_bs, dgamma, dbeta, dgb_bs, apart, aacc);                        \
+            hipLaunchKernelGGL((adain_bwd_row_k<T, E, B, 4, 0>), dim3(rows), dim3(T), 0, ctx->stream, g, dY,    \
+                               dy_bs, R, r_bs, dX, dx_bs, dgamma, dbeta, dgb_bs, apart, aacc);                 \
         else                                                                                                   \
-            hipLaunchKernelGGL((adain_bwd_row_k<T, E, B, 1>), dim3(rows), dim3(T), 0, ctx->stream, g, dY, dy_bs, \
-                               R, r_bs, dX, dx_bs, dgamma, dbeta, dgb_bs, apart, aacc);                        \
+            hipLaunchKernelGGL((adain_bwd_row_k<T, E, B, 1, 0>), dim3(rows), dim3(T), 0, ctx->stream, g, dY,    \
+                               dy_bs, R, r_bs, dX, dx_bs, dgamma, dbeta, dgb_bs, apart, aacc);                 \
         return launch_check(ctx, "adain_bwd_row");                                                            \
     }
     KDEC_BWD_ROW(256, 4, true)
@@ -660,13 +793,13 @@ struct BwdScratchLayout {
     size_t apart = 0, part = 0, rowv = 0, total = 0;  // byte offsets, total size
 };
 size_t round256(size_t b) { return (b + 255) & ~size_t(255); }
-BwdScratchLayout bwd_scratch_layout(int N, int C, int L, bool want_alpha) {
+BwdScratchLayout bwd_scratch_layout(int N, int C, int L, bool want_alpha, bool v4_long) {
     const size_t rows = static_cast<size_t>(N) * C;
     BwdScratchLayout s;
     size_t off = 0;
     s.apart = off;
     off += want_alpha ? round256(rows * sizeof(float)) : 0;
-    if (!row_shape_bwd(L).ntb) {
+    if (!row_shape_bwd(L, v4_long).ntb) {
         s.part = off;
         off += round256(rows * static_cast<size_t>(cdiv(L, CH)) * 3 * sizeof(double));
         s.rowv = off;
@@ -703,14 +836,14 @@ int bwd_check(kdec_ctx* ctx, const AdainArgs& g, const float* dY, const float* d
 }
 
 // The AdaIN(+activation) backward over caller-provided scratch (laid out by
-// bwd_scratch_layout for the same N, C, L and alpha-grad flag).
+// bwd_scratch_layout for the same N, C, L, alpha-grad flag and bwd_v4_long).
 int bwd_run(kdec_ctx* ctx, const AdainArgs& g, const float* dY, long dy_bs, const float* R, long r_bs, float* dX,
             long dx_bs, float* dgamma, float* dbeta, long dgb_bs, float* dalpha, int N, BwdScratch sc, bool prof) {
     const int C = g.C, L = g.L;
     const int rows = N * C;
     const int nch = static_cast<int>(cdiv(L, CH));
     const bool want_alpha = dalpha && g.act == KDEC_ACT_SNAKE;
-    const RowShape rsh = row_shape_bwd(L);
+    const RowShape rsh = row_shape_bwd(L, bwd_v4_long(g, dY, dy_bs, R, r_bs, dX, dx_bs));
     const double bytes = 4.0 * static_cast<double>(rows) * L * 3 +
                          (R ? 4.0 * static_cast<double>(rows) * L : 0.0);
     if (rsh.ntb) {
@@ -836,8 +969,8 @@ int kdec_adain_act_fwd_stats(kdec_ctx* ctx, const float* X, long x_bs, float eps
     KDEC_CHECK(ctx, act >= KDEC_ACT_NONE && act <= KDEC_ACT_SNAKE && (act != KDEC_ACT_SNAKE || alpha),
                "kdec_adain_act_fwd_stats: bad activation");
     AdainArgs g{X, x_bs, reinterpret_cast<const float2*>(stats), gamma, beta, gb_bs, act, slope, alpha, C, L};
-    const RowShape rsh = row_shape_fwd(L, fwd_v4(g, Y, y_bs, Ypre, ypre_bs));
-    if (!rsh.ntb) {  // long rows: statistics pass, then the affine pass
+    const RowShape rsh = row_shape_fwd(g, Y, y_bs, Ypre, ypre_bs);
+    if (!rsh.ntb) {  // rows the row kernels do not hold: statistics pass, then the affine pass
         if (int rc = kdec_instnorm_stats(ctx, X, x_bs, N, C, L, eps, stats)) return rc;
         return kdec_adain_act_fwd(ctx, X, x_bs, stats, gamma, beta, gb_bs, act, slope, alpha, Y, y_bs, Ypre, ypre_bs,
                                   N, C, L);
@@ -857,7 +990,8 @@ int kdec_adain_act_bwd(kdec_ctx* ctx, const float* X, long x_bs,
     if (!ctx) return KDEC_EINVAL;
     AdainArgs g{X, x_bs, reinterpret_cast<const float2*>(stats), gamma, beta, gb_bs, act, slope, alpha, C, L};
     if (int rc = bwd_check(ctx, g, dY, dX, N, "kdec_adain_act_bwd")) return rc;
-    const BwdScratchLayout lay = bwd_scratch_layout(N, C, L, dalpha && act == KDEC_ACT_SNAKE);
+    const BwdScratchLayout lay = bwd_scratch_layout(N, C, L, dalpha && act == KDEC_ACT_SNAKE,
+                                                    bwd_v4_long(g, dY, dy_bs, R, r_bs, dX, dx_bs));
     Workspace ws(ctx, lay.total);
     if (lay.total && !ws.p) return KDEC_ENOMEM;
     return bwd_run(ctx, g, dY, dy_bs, R, r_bs, dX, dx_bs, dgamma, dbeta, dgb_bs, dalpha, N,
@@ -874,7 +1008,8 @@ int kdec_adain_act_bwd_noalloc(kdec_ctx* ctx, const float* X, long x_bs,
     if (!ctx) return KDEC_EINVAL;
     AdainArgs g{X, x_bs, reinterpret_cast<const float2*>(stats), gamma, beta, gb_bs, act, slope, alpha, C, L};
     if (int rc = bwd_check(ctx, g, dY, dX, N, "kdec_adain_act_bwd_noalloc")) return rc;
-    const BwdScratchLayout lay = bwd_scratch_layout(N, C, L, dalpha && act == KDEC_ACT_SNAKE);
+    const BwdScratchLayout lay = bwd_scratch_layout(N, C, L, dalpha && act == KDEC_ACT_SNAKE,
+                                                    bwd_v4_long(g, dY, dy_bs, R, r_bs, dX, dx_bs));
     if (lay.total > static_cast<size_t>(KDEC_NOALLOC_SCRATCH_BYTES))
         return fail(ctx, KDEC_EINVAL,
                     "kdec_adain_act_bwd_noalloc: N*C = " + std::to_string(static_cast<long>(N) * C) + ", L = " +

@@ -250,7 +250,13 @@ ACTS = {"none": 0, "leaky": 1, "snake": 2}
 # lengths cover every row-kernel shape (256x4, 256x16, 1024x16, 1024x48),
 # with 4-byte accesses (L not a multiple of 4) and 16-byte ones, and the
 # chunked path for longer rows
-@pytest.mark.parametrize("C,L", [(5, 31), (3, 1500), (16, 4099), (3, 8192), (2, 48000), (2, 61441), (2, 70000)])
+# rows held by one block up to 49152; rows of 49155..62464 with 16-B aligned
+# bases and batch strides (C a multiple of 4 here) add a per-row head and
+# rest, at every head offset c*L mod 4 (4 x 61441, the shortest such row
+# 8 x 49155, the longest 4 x 62464); other long rows take the chunked passes
+# (C = 2, 49153, and 70000)
+@pytest.mark.parametrize("C,L", [(5, 31), (3, 1500), (16, 4099), (3, 8192), (2, 48000), (2, 61441), (2, 70000),
+                                 (4, 61441), (8, 49155), (4, 49153), (4, 62464)])
 def test_adain_act(K, act, C, L):
     N = 2
     x = rnd(N, C, L, scale=1.7) + 0.3
@@ -307,8 +313,9 @@ def test_adain_act(K, act, C, L):
 
 
 @pytest.mark.parametrize("act", ["leaky", "snake"])
-# 4-byte row kernel (1500), 16-byte row kernel (8192), chunked passes (70000)
-@pytest.mark.parametrize("C,L", [(3, 1500), (4, 8192), (2, 70000)])
+# 4-byte row kernel (1500), 16-byte row kernel (8192), chunked passes (70000),
+# long row with a head and rest (4 x 61441)
+@pytest.mark.parametrize("C,L", [(3, 1500), (4, 8192), (2, 70000), (4, 61441)])
 def test_adain_act_pre_activation_output(K, act, C, L):
     # Ypre, the AdaIN output before the activation, written beside Y
     N = 2
