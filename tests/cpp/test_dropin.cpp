@@ -8,7 +8,9 @@
 //   2. the same atom of the CPU oracle (oracle/kdec_oracle.hpp) on the same
 //      inputs: forward rel-L2 <= 1e-5, grads <= 1e-4;
 //   3. the inference twins (kokoro_infer.cpp) against the training forward,
-//      and the producer step's frame-count error.
+//      and the producer step's frame-count error;
+//   4. the closed-form special cases of closed_forms.hpp (the same runner as
+//      the oracle's CPU check) through the HIP assemblies.
 // Built by __graft_entry__.build() into tests/cpp/build/test_dropin and run by
 // tests/test_gpu_dropin_cpp.py on a GPU. Prints one line per failure and
 // exits non-zero if any check fails.
@@ -16,6 +18,8 @@
 
 #include "brosoundml/decoder_lora.h"
 #include "brosoundml/kokoro.h"
+#include "closed_forms.hpp"
+#include "kdec.h"
 #include "kdec_oracle.hpp"
 
 #include <array>
@@ -737,6 +741,147 @@ static void test_prep_frames_mismatch() {
                  "F0 override size must be 2*total (14)", "prep override size");
 }
 
+// ─── the closed-form cases through the HIP drop-in ───
+namespace {
+bs::Conv1d hconv(const cf::ConvSpec& c) {
+    bs::Conv1d g;
+    g.in_channels = c.in, g.out_channels = c.out, g.kernel_size = c.k;
+    g.stride = c.s, g.padding = c.p, g.dilation = c.d;
+    g.W = dev(c.W, c.out, c.in * c.k);
+    if (!c.b.empty()) g.b = dev(c.b, c.out, 1);
+    return g;
+}
+bs::AdainResBlk1dWeights hresblk(const cf::ResblkSpec& s) {
+    bs::AdainResBlk1dWeights w;
+    w.channels_in = s.Ci, w.channels_out = s.Co, w.upsample = s.upsample, w.learned_sc = s.learned_sc;
+    w.norm1.channels = s.Ci, w.norm2.channels = s.Co;
+    w.conv1 = hconv(s.conv1), w.conv2 = hconv(s.conv2);
+    if (s.learned_sc) w.conv1x1 = hconv(s.conv1x1);
+    if (s.upsample) w.pool_W = dev(s.pool_W, s.Ci, 3), w.pool_b = dev(s.pool_b, s.Ci, 1);
+    return w;
+}
+bs::AdaINResBlock1Weights hrb1(const cf::Rb1Spec& s) {
+    bs::AdaINResBlock1Weights w;
+    w.channels = s.C, w.kernel_size = s.k;
+    w.dilations = {s.dil[0], s.dil[1], s.dil[2]};
+    for (int j = 0; j < 3; ++j) {
+        w.convs1[j] = hconv(s.convs1[j]), w.convs2[j] = hconv(s.convs2[j]);
+        w.alpha1[j] = dev(s.alpha1[j], s.C, 1), w.alpha2[j] = dev(s.alpha2[j], s.C, 1);
+        w.adain1[j].channels = w.adain2[j].channels = s.C;
+    }
+    return w;
+}
+bd::ResBlock1Affines haff(const cf::Rb1Spec& s) {
+    bd::ResBlock1Affines a;
+    for (int j = 0; j < 3; ++j) {
+        a.g1[j] = dev(s.g1[j], s.C, 1), a.b1[j] = dev(s.b1[j], s.C, 1);
+        a.g2[j] = dev(s.g2[j], s.C, 1), a.b2[j] = dev(s.b2[j], s.C, 1);
+    }
+    return a;
+}
+
+struct HipBackend {
+    const float eps = 1e-5f;
+    cf::ResblkOut resblk(const cf::ResblkSpec& s) {
+        const bs::AdainResBlk1dWeights w = hresblk(s);
+        const Tensor g1 = dev(s.g1, s.Ci, 1), b1 = dev(s.b1, s.Ci, 1), g2 = dev(s.g2, s.Co, 1), b2 = dev(s.b2, s.Co, 1);
+        bd::AdainResBlkCache c;
+        Tensor y, dX, dG1, dB1, dG2, dB2;
+        int Lo = 0;
+        bd::adain_resblk_1d_forward_train(w, dev(s.x, 1, s.Ci * s.L), s.L, g1, b1, g2, b2, eps, Lo, y, c);
+        bd::adain_resblk_1d_backward(w, c, g1, g2, dev(s.dY, 1, s.Co * s.L_out()), eps, dX, dG1, dB1, dG2, dB2);
+        return {host(y), host(dX), host(dG1), host(dB1), host(dG2), host(dB2)};
+    }
+    cf::Rb1Out resblock1(const cf::Rb1Spec& s) {
+        const bs::AdaINResBlock1Weights w = hrb1(s);
+        const bd::ResBlock1Affines a = haff(s);
+        bd::AdainResBlock1Cache c;
+        Tensor y, dX;
+        std::array<Tensor, 3> dG1, dB1, dG2, dB2;
+        bd::adain_resblock1_forward_train(w, dev(s.x, 1, s.C * s.L), s.C, s.L, a.g1, a.b1, a.g2, a.b2, y, c);
+        bd::adain_resblock1_backward(w, c, a.g1, a.g2, dev(s.dY, 1, s.C * s.L), dX, dG1, dB1, dG2, dB2);
+        return {host(y), host(dX)};
+    }
+    void generator(const cf::GenSpec& g, HVec& stage1_in, HVec& head_in) {
+        bs::Generator gen;
+        gen.n_fft = g.n_fft, gen.hop_size = g.hop, gen.win_size = g.win;
+        gen.num_upsamples = g.U, gen.num_kernels = g.K;
+        for (int i = 0; i < g.U; ++i) {
+            gen.ups_W.push_back(dev(g.ups_W[i], g.C_in[i], g.C_out[i] * g.k[i]));
+            gen.ups_b.push_back(dev(g.ups_b[i], g.C_out[i], 1));
+            gen.noise_convs.push_back(hconv(g.noise_convs[i]));
+            gen.noise_res.push_back(hrb1(g.noise_res[i]));
+        }
+        gen.ups_C_in = g.C_in, gen.ups_C_out = g.C_out, gen.ups_k = g.k, gen.ups_stride = g.s, gen.ups_pad = g.p;
+        std::vector<bd::ResBlock1Affines> naff, raff;
+        for (const auto& r : g.noise_res) naff.push_back(haff(r));
+        for (const auto& r : g.resblocks) {
+            gen.resblocks.push_back(hrb1(r));
+            raff.push_back(haff(r));
+        }
+        gen.conv_post = hconv(g.conv_post);
+        bd::GeneratorCache c;
+        Tensor audio;
+        bd::generator_forward_train(gen, dev(g.gen_in, 1, g.C0 * g.L0), g.L0, dev(g.har, 1, (g.n_fft + 2) * g.frames),
+                                    g.frames, naff, raff, audio, c);
+        stage1_in = host(c.stages[1].x_in);
+        head_in = host(c.head.x_pre);
+    }
+    HVec head(const cf::HeadSpec& h, const HVec& x, const HVec& W) {
+        cf::ConvSpec cs = h.conv_post;
+        cs.W = W;
+        HVec window(static_cast<std::size_t>(h.win));
+        for (int n = 0; n < h.win; ++n) window[n] = static_cast<float>(0.5 - 0.5 * std::cos(2.0 * M_PI * n / h.win));
+        bd::SpectralHeadCache c;
+        Tensor audio;
+        bd::spectral_head_forward_train(hconv(cs), dev(x, 1, h.C * h.L), h.C, h.L, dev(window, 1, h.win), h.n_fft,
+                                        h.hop, h.win, audio, c);
+        return host(audio);
+    }
+    HVec backbone(const cf::BbSpec& b) {
+        bs::DecoderBackbone bb;
+        bb.F0_conv = hconv(b.F0_conv), bb.N_conv = hconv(b.N_conv), bb.asr_res = hconv(b.asr_res);
+        bb.encode = hresblk(b.encode);
+        std::vector<bd::BlockAffines> aff;
+        auto push = [&](const cf::ResblkSpec& r) {
+            bd::BlockAffines a;
+            a.g1 = dev(r.g1, r.Ci, 1), a.b1 = dev(r.b1, r.Ci, 1), a.g2 = dev(r.g2, r.Co, 1), a.b2 = dev(r.b2, r.Co, 1);
+            aff.push_back(a);
+        };
+        push(b.encode);
+        for (const auto& d : b.decode) {
+            bb.decode.push_back(hresblk(d));
+            push(d);
+        }
+        bd::BackboneCache c;
+        Tensor gen_in;
+        bd::decoder_backbone_forward_train(bb, dev(b.asr, 1, b.A * b.T), dev(b.F0, 1, 2 * b.T), dev(b.N, 1, 2 * b.T),
+                                           b.T, aff, eps, gen_in, c);
+        return host(gen_in);
+    }
+    HVec pad(const HVec& x, int C, int L) {
+        kdec_ctx* ctx = nullptr;
+        if (kdec_ctx_create(0, &ctx) != KDEC_OK) throw std::runtime_error("kdec_ctx_create");
+        const Tensor xt = dev(x, 1, C * L);
+        Tensor yt = Tensor::zeros_on(Device::HIP, 1, C * (L + 1));
+        const int rc = kdec_pad_reflect_left1_fwd(ctx, static_cast<const float*>(xt.data), C * L,
+                                                  static_cast<float*>(yt.data), C * (L + 1), 1, C, L);
+        kdec_synchronize(ctx);
+        kdec_ctx_destroy(ctx);
+        if (rc != KDEC_OK) throw std::runtime_error("kdec_pad_reflect_left1_fwd");
+        return host(yt);
+    }
+};
+
+void test_closed_forms() {
+    HipBackend be;
+    cf::Report r;
+    cf::run_closed_forms(be, r);
+    g_checks += r.checks;
+    g_failures += r.failures;
+}
+}  // namespace
+
 int main() {
     brotensor::init(0);
     struct Case {
@@ -752,6 +897,7 @@ int main() {
         {"generator", test_generator},
         {"inference_twins", test_inference_twins},
         {"prep", test_prep_frames_mismatch},
+        {"closed_forms", test_closed_forms},
     };
     for (auto& c : cases) {
         const int before = g_failures;

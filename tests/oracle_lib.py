@@ -13,7 +13,9 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_DIR = os.path.join(ROOT, "oracle")
-LIB_PATH = os.path.join(ORACLE_DIR, "build", "libkdec_oracle.so")
+# KDEC_ORACLE_LIB selects another build of the same sources (the sanitizer
+# build of test_oracle_sanitize.py)
+LIB_PATH = os.environ.get("KDEC_ORACLE_LIB") or os.path.join(ORACLE_DIR, "build", "libkdec_oracle.so")
 
 _fp = ctypes.POINTER(ctypes.c_float)
 _lib = None
