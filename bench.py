@@ -35,30 +35,184 @@ def make_inputs(cfg, N, T, tag, unvoiced=0.2):
     return synth.decoder_inputs(cfg, N, T, tag, unvoiced)
 
 
-def cpu_baseline(cfg, params):
-    """The oracle (CPU restatement of the reference path, OpenMP) on a bounded
-    sample of the benchmarked workload: one of the B utterances at the same
-    T = 512 (12.8 s of audio), forward + backward with the same extensions,
-    timed once on this host's cores (about half a minute). A reported
-    baseline, not the target."""
+def cpu_info():
+    """Host cores this process may use and the CPU model (lscpu)."""
+    import subprocess
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count() or 1
+    model = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return {"nproc": avail, "cpu_count": os.cpu_count(), "lscpu_model": model}
+
+
+def _oracle():
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
-    from brosoundml_amd import config as C
+    return O
+
+
+def _median(xs):
+    xs = sorted(xs)
+    return xs[len(xs) // 2]
+
+
+def _progress(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_decoder_time(cfg, params, T, ext, threads, runs, warmup=0, tag="bench.cpu", verbose=False):
+    """Seconds per decoder forward + backward of one utterance of T frames on
+    the oracle at `threads` OpenMP threads (0: all): the median of `runs`
+    timed runs after `warmup` untimed ones. ext: the extension's grads
+    (conv/convT/pool weights, Snake alphas, d(style)); else the reference's
+    semantics (conv dgrad only)."""
+    O = _oracle()
+    n = O.set_threads(threads)
     om = O.OracleModel(cfg)
     om.set_params(params)
-    asr, F0, Nn, style, dA = make_inputs(cfg, 1, T, "bench.cpu")
-    t0 = time.perf_counter()
-    om.zero_grad()
-    om.forward(asr[0], F0[0], Nn[0], style[0], T)
-    om.backward(dA[0], wgrad=True, dalpha=True, dstyle=True)
-    dt = time.perf_counter() - t0
-    audio_s = C.lengths(cfg, T)["audio_seconds"]
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": round(audio_s / dt, 5), "unit": "audio-s/s", "cores": threads, "kind": "port",
-            "seconds": round(dt, 3),
-            "sample": f"1 of the {B} utterances at T={T} ({audio_s} audio-s), decoder fwd+bwd with "
-                      f"wgrad/dalpha/dstyle, CPU oracle (double-accumulating C++, OpenMP {threads} threads), "
-                      f"one timed run"}
+    asr, F0, Nn, style, dA = make_inputs(cfg, 1, T, tag)
+    ts = []
+    for i in range(warmup + runs):
+        t0 = time.perf_counter()
+        om.zero_grad()
+        om.forward(asr[0], F0[0], Nn[0], style[0], T)
+        om.backward(dA[0], wgrad=ext, dalpha=ext, dstyle=ext)
+        if i >= warmup:
+            ts.append(time.perf_counter() - t0)
+        if verbose:
+            _progress(f"cpu: decoder T={T} ext={ext} threads={n} run {i}: {time.perf_counter() - t0:.2f} s")
+    return _median(ts), n, ts
+
+
+def cpu_baseline(cfg, params):
+    """The oracle (CPU restatement of the reference path, OpenMP) on a bounded
+    sample of the benchmarked workload: one utterance of T = 64 frames
+    (1.6 s of audio, the config-0 shape) through the decoder forward +
+    backward with the same extensions, on this host's cores. All cores: the
+    median of 3 after a warm-up; one thread: one run of T = 16 (its cost is
+    linear in T, so audio-s/s carries over). About half a minute in all.
+    A reported baseline, not the target; `python bench.py --cpu-plan` runs
+    the full plan (configs 0-4, both modes, both thread counts)."""
+    from brosoundml_amd import config as C
+    info = cpu_info()
+    T_all, T_one = 64, 16
+    med, n_all, ts = cpu_decoder_time(cfg, params, T_all, True, 0, 3, warmup=1)
+    one, _, _ = cpu_decoder_time(cfg, params, T_one, True, 1, 1)
+    a_all, a_one = C.lengths(cfg, T_all)["audio_seconds"], C.lengths(cfg, T_one)["audio_seconds"]
+    _oracle().set_threads(0)
+    return {"value": round(a_all / med, 5), "unit": "audio-s/s", "cores": n_all, "kind": "port",
+            "seconds": round(med, 3), "runs_s": [round(t, 3) for t in ts],
+            "one_thread": {"value": round(a_one / one, 5), "unit": "audio-s/s", "cores": 1, "seconds": round(one, 3),
+                           "sample": f"B=1, T={T_one} ({a_one} audio-s), one run"},
+            **info,
+            "sample": f"B=1, T={T_all} ({a_all} audio-s) of the B={B}, T={T} workload: decoder fwd+bwd with "
+                      f"wgrad/dalpha/dstyle on the CPU oracle (double-accumulating C++, OpenMP {n_all} threads), "
+                      f"median of 3 after 1 warm-up"}
+
+
+def cpu_plan(cfg, params, runs=3):
+    """The full CPU baseline plan: configs 0-3 in full and config 4 at B = 1
+    in full (all cores), at 1 thread and all cores, medians of `runs` after a
+    warm-up, both semantics for the decoder. The 1-thread config-4 figure is
+    config 0's (cost linear in T), labelled extrapolated, as is the B = 8
+    figure (B independent utterances). Long: several minutes."""
+    from brosoundml_amd import config as C
+    O = _oracle()
+    out = {"cpu": cpu_info(), "runs": runs}
+    rng = np.random.default_rng(20260)
+
+    def timed(fn, threads, what):
+        n = O.set_threads(threads)
+        ts = []
+        for i in range(runs + 1):  # the first is the warm-up
+            t0 = time.perf_counter()
+            fn()
+            dt = time.perf_counter() - t0
+            _progress(f"cpu: {what} threads={n} run {i}: {dt:.2f} s")
+            if i:
+                ts.append(dt)
+        return {"median_s": round(_median(ts), 4), "runs_s": [round(t, 4) for t in ts], "threads": n}
+
+    # config 0 / 4: the decoder, both semantics
+    dec = {}
+    for name, T in (("config0_B1_T64", 64), ("config4_B1_T512", 512)):
+        a = C.lengths(cfg, T)["audio_seconds"]
+        for mode, ext in (("extension", True), ("reference_semantics", False)):
+            for threads in ((0, 1) if T == 64 else (0,)):
+                med, n, ts = cpu_decoder_time(cfg, params, T, ext, threads, runs, warmup=1, tag=f"plan.{name}",
+                                              verbose=True)
+                dec[f"{name}.{mode}.{'1thread' if threads == 1 else 'all'}"] = {
+                    "median_s": round(med, 3), "runs_s": [round(t, 3) for t in ts], "threads": n,
+                    "audio_s_per_s": round(a / med, 5)}
+    for mode in ("extension", "reference_semantics"):
+        c0 = dec[f"config0_B1_T64.{mode}.1thread"]
+        c4 = dec[f"config4_B1_T512.{mode}.all"]
+        dec[f"config4_B1_T512.{mode}.1thread"] = {"audio_s_per_s": c0["audio_s_per_s"],
+                                                   "extrapolated": "config 0's 1-thread rate; cost is linear in T"}
+        dec[f"config4_B8_T512.{mode}.all"] = {"audio_s_per_s": c4["audio_s_per_s"],
+                                              "seconds": round(8 * c4["median_s"], 3),
+                                              "extrapolated": "8 independent utterances x the B=1 time"}
+    out["decoder"] = dec
+
+    # config 1: Snake + AdaIN1d backward, x [1,256,48000], style 128 -> 2*256
+    Cc, L = 256, 48000
+    x = rng.normal(size=(Cc, L)).astype(np.float32)
+    dy = rng.normal(size=(Cc, L)).astype(np.float32)
+    alpha = rng.uniform(0.5, 2.0, Cc).astype(np.float32)
+    Wfc = (rng.uniform(-1, 1, (2 * Cc, 128)) / np.sqrt(128)).astype(np.float32)
+    bfc = np.zeros(2 * Cc, np.float32)
+    st = rng.normal(0, 0.3, 128).astype(np.float32)
+
+    def c1():
+        gb = Wfc @ st + bfc
+        s = O.adain_affine(x, gb[:Cc], gb[Cc:], Cc, L)
+        ds, _ = O.snake_bwd(s, alpha, dy.ravel(), Cc, L)
+        _, dg, db = O.adain_affine_bwd(x, gb[:Cc], ds, Cc, L)
+        return Wfc.T @ np.concatenate([dg, db])
+    out["config1_snake_adain_bwd"] = {t: timed(c1, th, "config1") for t, th in (("all", 0), ("1thread", 1))}
+
+    # config 2: Conv1d 512->512 k3 d{1,3,5} dgrad + wgrad on [4,512,2048]
+    N2, C2, L2, k = 4, 512, 2048, 3
+    X2 = rng.normal(size=(N2, C2 * L2)).astype(np.float32)
+    G2 = rng.normal(size=(N2, C2 * L2)).astype(np.float32)
+    W2 = (rng.uniform(-1, 1, (C2, C2 * k)) / np.sqrt(C2 * k)).astype(np.float32)
+
+    def c2():
+        for d in (1, 3, 5):
+            for n in range(N2):
+                O.conv1d_dgrad(W2, G2[n], C2, L2, C2, k, 1, d, d)
+                O.conv1d_wgrad(X2[n], G2[n], C2, L2, C2, k, 1, d, d)
+    out["config2_conv1d_bwd"] = {t: timed(c2, th, "config2") for t, th in (("all", 0), ("1thread", 1))}
+    out["config2_conv1d_bwd"]["gflop"] = round(3 * 2 * 2.0 * N2 * C2 * C2 * k * L2 / 1e9, 2)
+
+    # config 3: ConvTranspose1d upsampler backwards (dgrad + wgrad)
+    cases = {"ups0_512to256_k20_s10_x4x512": (512, 256, 512, 20, 10, 5),
+             "ups1_256to128_k12_s6_x4x5120": (256, 128, 5120, 12, 6, 3)}
+    c3 = {}
+    for name, (Ci, Co, Lin, kk, ss, pp) in cases.items():
+        Lo = (Lin - 1) * ss - 2 * pp + kk
+        Xt = rng.normal(size=(4, Ci * Lin)).astype(np.float32)
+        Gt = rng.normal(size=(4, Co * Lo)).astype(np.float32)
+        Wt = (rng.uniform(-1, 1, (Ci, Co * kk)) * 0.05).astype(np.float32)
+
+        def run(Xt=Xt, Gt=Gt, Wt=Wt, Ci=Ci, Co=Co, Lin=Lin, kk=kk, ss=ss, pp=pp):
+            for n in range(4):
+                O.convt1d_dgrad(Wt, Gt[n], Ci, Lin, Co, kk, ss, pp)
+                O.convt1d_wgrad(Xt[n], Gt[n], Ci, Lin, Co, kk, ss, pp)
+        c3[name] = {t: timed(run, th, f"config3 {name}") for t, th in (("all", 0), ("1thread", 1))}
+        c3[name]["gflop"] = round(2 * 2.0 * 4 * Ci * Co * kk * Lin / 1e9, 2)
+    out["config3_convt_bwd"] = c3
+    O.set_threads(0)
+    return out
 
 
 def micro_benches(ctx, reps=10):
@@ -174,6 +328,9 @@ def main(argv=None):
                     help="run only the per-kernel-class microbenchmarks and print their JSON (for profiling them)")
     ap.add_argument("--serial", action="store_true",
                     help="one stream (no harmonic-source / weight-grad overlap): per-family times without sharing")
+    ap.add_argument("--cpu-plan", action="store_true",
+                    help="run only the full CPU baseline plan (configs 0-4 on the oracle, 1 thread and all cores, "
+                         "medians of 3) and print its JSON; several minutes")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB (3 times): the reference kernel for "
                          "scaling HBM byte counters")
@@ -183,6 +340,14 @@ def main(argv=None):
         print("bench.py measures one MI355X: the decoder path shards by utterance with no exchange, "
               "and this build runs on a single GPU; use --gpus 1.", file=sys.stderr)
         return 2
+
+    if a.cpu_plan:
+        from brosoundml_amd import config as C, synth
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        import oracle_lib as O
+        shapes = O.OracleModel(C.KOKORO).param_shapes()
+        print(json.dumps({"cpu_plan": cpu_plan(C.KOKORO, synth.init_params(shapes))}), flush=True)
+        return 0
 
     import torch
     from brosoundml_amd import config as C, native, synth

@@ -4,6 +4,8 @@
 // error (message via ko_last_error()).
 #include "kdec_oracle.hpp"
 
+#include <omp.h>
+
 #include <cstring>
 #include <exception>
 #include <stdexcept>
@@ -31,6 +33,13 @@ Vec vec(const float* p, std::size_t n) { return Vec(p, p + n); }
 extern "C" {
 
 const char* ko_last_error() { return g_err.c_str(); }
+
+// OpenMP threads for the oracle's parallel loops: n > 0 sets n, n <= 0 all
+// the process may use; returns the number now in effect.
+int ko_set_threads(int n) {
+    omp_set_num_threads(n > 0 ? n : omp_get_num_procs());
+    return omp_get_max_threads();
+}
 
 int ko_conv1d_out_len(int L, int k, int s, int p, int d) { return conv1d_out_len(L, k, s, p, d); }
 int ko_convt1d_out_len(int L, int k, int s, int p, int op, int d) { return convt1d_out_len(L, k, s, p, op, d); }

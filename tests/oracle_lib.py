@@ -88,6 +88,11 @@ def lib():
     return _lib
 
 
+def set_threads(n: int) -> int:
+    """OpenMP threads of the oracle (n <= 0: all); returns the count in effect."""
+    return int(lib().ko_set_threads(int(n)))
+
+
 def P(a):
     """float32 pointer for a numpy array (None -> NULL)."""
     if a is None:
