@@ -41,6 +41,7 @@ namespace kdec {
 namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128;   // output-channel tile
 constexpr int BN = 128;   // output-position tile
@@ -96,6 +97,7 @@ struct GemmArgs {
     int ybuf;                // (C_out + BM) * L_y * 4 < 2^31: the epilogue addresses Y through a descriptor
     // octet mode (corr_gemm): K chunk = one input-channel octet x up to G taps
     int G, n_tg, n_oct, span8;  // taps per chunk, tap groups, octets, staged positions
+    int quad;                // conv_gemm_q: weights packed in quads of k-steps (stride 1, k = KT)
 };
 
 // Logical block order with consecutive ids on one XCD: the dispatcher deals
@@ -263,8 +265,11 @@ __device__ inline void store_tile(const GemmArgs& g, const TileGeo& T, int tile,
 // Inner loop: the chunk's KR/2 k-steps (2 packed rows each) run as a
 // ping-pong over two register sets, each step's LDS reads issued between the
 // MFMAs of the step before, so the read latency hides behind matrix work.
+#ifndef CG_WPE
+#define CG_WPE 5
+#endif
 template <int CK>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(5)))
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(CG_WPE)))
 void conv_gemm(GemmArgs g) {
     extern __shared__ float smem[];
     const int tid = threadIdx.x;
@@ -309,11 +314,16 @@ void conv_gemm(GemmArgs g) {
     // Stage chunk `ch` at LDS float offset `sb`: the weight slab two rows
     // (1 KB) per instruction, the input window 256 (16-B path) or 64 positions
     // per instruction.
-    auto issue = [&](int ch, int sb) {
+    auto issue_a = [&](int ch, int sb) {
         const float* Ag = A + static_cast<long>(ch) * KR * g.m_pad + m0;
         for (int pr = wave; pr < KR / 2; pr += 4)
             __builtin_amdgcn_global_load_lds(Ag + static_cast<long>(2 * pr) * g.m_pad + a_lane,
                                              smem + sb + pr * 256, 16, 0, 0);
+    };
+    auto issue = [&](int ch, int sb) {
+#ifndef CG_XFIRST
+        issue_a(ch, sb);
+#endif
         if (x4) {
             const int seg4 = span_p >> 8;
             for (int it = wave; it < CK * seg4; it += 4) {
@@ -325,6 +335,9 @@ void conv_gemm(GemmArgs g) {
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + KR * BM + r * span_p + sg * 256, 16,
                                                              static_cast<int>(off), 0, 0, 0);
             }
+#ifdef CG_XFIRST
+            issue_a(ch, sb);
+#endif
             return;
         }
         for (int it = wave; it < nitems; it += 4) {
@@ -337,6 +350,9 @@ void conv_gemm(GemmArgs g) {
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + KR * BM + r * span_p + sg * 64, 4,
                                                          static_cast<int>(off), 0, 0, 0);
         }
+#ifdef CG_XFIRST
+        issue_a(ch, sb);
+#endif
     };
 
     f32x16 acc[2][2];
@@ -404,6 +420,168 @@ void conv_gemm(GemmArgs g) {
             __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
         }
         if (live && u < S) mm(pa0, pa1, pb0, pb1);
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's staging loads landed
+        __syncthreads();
+    }
+
+    store_tile(g, T, tile, part, acc, wm, wn, hi, l32);
+}
+
+// Stride-1 correlation of KT taps with the weights read 16 B per lane.
+//
+// As conv_gemm (tile plan, input staging, epilogue), but the chunk's weight
+// slab is stored in LDS as quads of k-steps: quad g holds k-steps 4g..4g+3 as
+// [hi][m (128)][j (4)], element j being packed row 2(4g + j) + hi of the
+// chunk (tap (2(4g+j)+hi) / CK, channel (2(4g+j)+hi) % CK). One ds_read_b128
+// then gives a lane its A operand for four MFMA steps, so a wave issues two
+// weight reads per 16 MFMAs instead of eight; the input operand stays one
+// ds_read2 per k-step. The global panel is the LDS image of each chunk,
+// m-tile major ([m_tile][chunk][quad][hi][128][4], see pack_quad), so a
+// chunk's slab is one contiguous copy. The last quad of a chunk is partial
+// when CK*KT/2 is not a multiple of 4; its unused slots are zeros that no
+// MFMA reads.
+#ifndef CGQ_WPE
+#define CGQ_WPE 4
+#endif
+#ifndef CGQ_PF
+#define CGQ_PF 2
+#endif
+template <int CK, int KT>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(CGQ_WPE)))
+void conv_gemm_q(GemmArgs g) {
+    constexpr int S = CK * KT / 2;  // k-steps per chunk
+    constexpr int Q = (S + 3) / 4;  // weight quads per chunk
+    constexpr int QA = Q * 1024;    // LDS floats of a chunk's weights
+    constexpr int HS = CK / 2;      // k-steps per tap
+    extern __shared__ float smem[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, wn = wave >> 1;
+    const int l32 = lane & 31, hi = lane >> 5;
+
+    int tile, part;
+    if (!block_work(g, tile, part)) return;  // uniform per block
+    TileGeo T;
+    decode_tile(g, tile, T);
+    const int b = T.b, d = T.d, p = T.p, n_q = T.n_q;
+    const int m0 = T.m0;
+    const int q0 = T.q0;
+    if (q0 >= n_q) return;  // uniform per block
+
+    const int span = BN + (KT - 1) * d;  // staged input window (stride 1)
+    const int span_p = (span + 3 + 255) & ~255;
+    const int segs = span_p >> 6;
+    const int stage = QA + CK * span_p;
+    const float* Xb = g.X + static_cast<long>(b) * g.x_bs;
+    const int x0 = q0 - p;
+    const int nchunks = g.cin_pad / CK;
+    const float* Ablk = g.A + static_cast<long>(m0 / BM) * nchunks * QA + lane * 4;
+    const __amdgpu_buffer_rsrc_t xrs = uniform_rsrc(Xb, g.C_in * g.L_in * 4);
+    const bool x4 = x0 >= 3 && x0 + span <= g.L_in;  // uniform per tile
+    const int base_f = static_cast<int>((reinterpret_cast<unsigned long long>(Xb) >> 2) & 3);
+    const int Lm = x4 ? (g.L_in & 3) : 0;
+    const int xm = x4 ? ((base_f + x0) & 3) : 0;
+
+    // Stage chunk `ch` at LDS float offset `sb`: the weight slab 1 KB per
+    // instruction, the input window as conv_gemm stages it.
+    auto issue = [&](int ch, int sb) {
+        const float* Ag = Ablk + static_cast<long>(ch) * QA;
+        for (int i = wave; i < QA / 256; i += 4)
+            __builtin_amdgcn_global_load_lds(Ag + i * 256, smem + sb + i * 256, 16, 0, 0);
+        if (x4) {
+            const int seg4 = span_p >> 8;
+            for (int it = wave; it < CK * seg4; it += 4) {
+                const int r = it / seg4, sg = it - r * seg4;
+                const int c = ch * CK + r;
+                const int pos = x0 - ((c * Lm + xm) & 3) + sg * 256 + lane * 4;
+                const unsigned off = c < g.C_in ? static_cast<unsigned>(c * g.L_in + pos) * 4u : 0x80000000u;
+                if (sg * 256 + lane * 4 < span + 3)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + QA + r * span_p + sg * 256, 16,
+                                                             static_cast<int>(off), 0, 0, 0);
+            }
+            return;
+        }
+        for (int it = wave; it < CK * segs; it += 4) {
+            const int r = it / segs, sg = it - r * segs;
+            const int c = ch * CK + r;
+            const int pos = x0 + sg * 64 + lane;
+            const unsigned off = (c < g.C_in && pos >= 0 && pos < g.L_in)
+                                     ? static_cast<unsigned>(c * g.L_in + pos) * 4u : 0x80000000u;
+            if (sg * 64 + lane < span)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + QA + r * span_p + sg * 64, 4,
+                                                         static_cast<int>(off), 0, 0, 0);
+        }
+    };
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    const int am = wm * 64 + l32;
+    const int bq = wn * 64 + l32;
+    const int nparts = part < 0 ? 1 : g.fsplit;
+    const int pp = part < 0 ? 0 : part;
+    const int ch0 = pp * nchunks / nparts;
+    const int ch1 = (pp + 1) * nchunks / nparts;
+    const bool live = q0 + wn * 64 < n_q;  // wave-uniform
+
+    if (ch0 < ch1) issue(ch0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int ch = ch0; ch < ch1; ++ch) {
+        const int sb = ((ch - ch0) & 1) * stage;
+        if (ch + 1 < ch1) issue(ch + 1, stage - sb);
+        if (live) {
+            const f32x4* Aq = reinterpret_cast<const f32x4*>(smem + sb) + hi * BM + am;
+            const int xb = sb + QA + hi * span_p + bq;
+            const int dl = (ch * CK + hi) * Lm + xm;
+            auto ldb = [&](int u, float& b0, float& b1) {
+                const int t = u / HS;
+                const int cc = (u - t * HS) * 2;
+                int xo = xb + cc * span_p + t * d + ((dl + cc * Lm) & 3);
+                asm volatile("" : "+v"(xo));
+                b0 = smem[xo];
+                b1 = smem[xo + 32];
+            };
+            // the input operand is read CGQ_PF k-steps ahead (a ring of
+            // CGQ_PF + 1 register pairs), the next weight quad at the first
+            // step of the current one; each step issues one MFMA, its reads,
+            // then three MFMAs
+            constexpr int PF = CGQ_PF;
+            f32x4 qa[2][2];
+            float bb[PF + 1][2];
+            qa[0][0] = Aq[0];
+            qa[0][1] = Aq[32];
+#pragma unroll
+            for (int u = 0; u < PF && u < S; ++u) ldb(u, bb[u][0], bb[u][1]);
+#pragma unroll
+            for (int u = 0; u < S; ++u) {
+                const int gq = u / 4, j = u % 4;
+                const float a0 = qa[gq & 1][0][j], a1 = qa[gq & 1][1][j];
+                const float b0 = bb[u % (PF + 1)][0], b1 = bb[u % (PF + 1)][1];
+                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
+                if (j == 0 && gq + 1 < Q) {
+                    qa[(gq + 1) & 1][0] = Aq[(gq + 1) * 2 * BM];
+                    qa[(gq + 1) & 1][1] = Aq[(gq + 1) * 2 * BM + 32];
+                }
+                if (u + PF < S) ldb(u + PF, bb[(u + PF) % (PF + 1)][0], bb[(u + PF) % (PF + 1)][1]);
+                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
+                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
+                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+#ifndef CGQ_NOSCHED
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (j == 0 && gq + 1 < Q) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                if (u + PF < S) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+                __builtin_amdgcn_sched_barrier(0);  // nothing crosses into the next step
+#endif
+            }
+        }
         __builtin_amdgcn_s_waitcnt(0);  // this wave's staging loads landed
         __syncthreads();
     }
@@ -632,6 +810,43 @@ __global__ void pack_dgrad(const float* W, float* A, int C_in, int C_out, int k,
         float v = 0.0f;
         if (m < C_in && c < C_out) v = W[(static_cast<long>(c) * C_in + m) * k + (k - 1 - t)];
         A[i] = v;
+    }
+}
+
+// The quad panel of conv_gemm_q: A[m_tile][chunk][quad][hi][128][4], element
+// j of (quad g, hi, m) being packed row r = 2(4g + j) + hi of the chunk, i.e.
+// tap r / CK of channel chunk*CK + r % CK; zero past the chunk's CK*k/2
+// k-steps, past the channels or past the output rows. mode 0: conv1d forward
+// (A[(ci, t), co] = W[co, ci*k + t]); mode 1: conv1d input-grad at stride 1
+// (A[(co, t'), ci] = W[co, ci*k + k-1-t']). One thread writes one 16-B run.
+__global__ void pack_quad(const float* W, float* A, int mode, int C_in, int C_out, int k, int CK, int nchunks,
+                          int Q, long total4) {
+    const int S = CK * k / 2;
+    const int Cg = mode == 0 ? C_in : C_out;   // GEMM input channels
+    const int Mg = mode == 0 ? C_out : C_in;   // GEMM output rows
+    for (long e = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; e < total4;
+         e += static_cast<long>(gridDim.x) * blockDim.x) {
+        const int ml = static_cast<int>(e % BM);
+        long r2 = e / BM;
+        const int hi = static_cast<int>(r2 & 1);
+        r2 >>= 1;
+        const int gq = static_cast<int>(r2 % Q);
+        r2 /= Q;
+        const int ch = static_cast<int>(r2 % nchunks);
+        const int m = static_cast<int>(r2 / nchunks) * BM + ml;
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int u = 4 * gq + j;
+            const int r = 2 * u + hi;
+            const int t = r / CK, c = ch * CK + r % CK;
+            float x = 0.0f;
+            if (u < S && c < Cg && m < Mg)
+                x = mode == 0 ? W[(static_cast<long>(m) * C_in + c) * k + t]
+                              : W[(static_cast<long>(c) * C_in + m) * k + (k - 1 - t)];
+            v[j] = x;
+        }
+        reinterpret_cast<float4*>(A)[e] = make_float4(v[0], v[1], v[2], v[3]);
     }
 }
 
@@ -1194,6 +1409,53 @@ size_t conv_lds_bytes(int CK, int kk, int ss, int dd) {
     return 2 * (static_cast<size_t>(CK) * kk * BM + static_cast<size_t>(CK) * span_p) * sizeof(float);
 }
 
+// LDS bytes of one conv_gemm_q block (two stages): the chunk's weight quads
+// and its CK input rows.
+size_t quad_lds_bytes(int CK, int k, int d) {
+    const long S = static_cast<long>(CK) * k / 2, Q = (S + 3) / 4;
+    const long span = BN + static_cast<long>(k - 1) * d;
+    const long span_p = (span + 3 + 255) / 256 * 256;
+    return 2 * (static_cast<size_t>(Q) * 1024 + static_cast<size_t>(CK) * span_p) * sizeof(float);
+}
+
+#ifndef CGQ_CK3
+#define CGQ_CK3 4
+#endif
+#ifndef CGQ_CK7
+#define CGQ_CK7 2
+#endif
+// Channel chunk of conv_gemm_q for a k-tap stride-1 correlation, or 0 where
+// no instance exists (conv_gemm serves those).
+int pick_ck_q(int k) {
+#ifdef CGQ_OFF
+    return 0 * k;
+#endif
+    switch (k) {
+        case 3: return CGQ_CK3;
+        case 7: return CGQ_CK7;
+        case 11: return 2;
+        default: return 0;
+    }
+}
+
+template <int CK, int KT>
+const void* conv_q_kernel() {
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_gemm_q<CK, KT>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        attr = true;
+    }
+    return reinterpret_cast<const void*>(&conv_gemm_q<CK, KT>);
+}
+
+const void* conv_q_kernel_for(int CK, int k) {
+    if (k == 3 && CK == CGQ_CK3) return conv_q_kernel<CGQ_CK3, 3>();
+    if (k == 7 && CK == CGQ_CK7) return conv_q_kernel<CGQ_CK7, 7>();
+    if (k == 11 && CK == 2) return conv_q_kernel<2, 11>();
+    return nullptr;
+}
+
 // Input channels per K chunk: a power of two in [2, 32] so that it divides
 // the 32-padded channel count of the packed weights (no chunk runs past them),
 // at most 32 weight rows (CK*k) per chunk, and the largest such chunk whose two
@@ -1306,13 +1568,17 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
     if (octet ? (ss != 1 || g.G > kk || g.span8 < BN + (g.G - 1) * dd || g.span8 % 16)
               : (CK * kk > 64 || (CK * kk) % 2))
         return fail(ctx, KDEC_EINVAL, "conv: bad chunk geometry");
+    const bool quad = g.quad != 0;
+    if (quad && (octet || g.n_phase > 1 || g.s != 1 || !conv_q_kernel_for(CK, g.k)))
+        return fail(ctx, KDEC_EINVAL, "conv: bad quad geometry");
     const size_t lds = octet ? 2 * (static_cast<size_t>(g.G) * 1024 + 8 * static_cast<size_t>(g.span8)) * sizeof(float)
-                             : conv_lds_bytes(CK, kk, ss, dd);
+                     : quad ? quad_lds_bytes(CK, g.k, g.d)
+                            : conv_lds_bytes(CK, kk, ss, dd);
     if (lds > 160 * 1024) return fail(ctx, KDEC_EINVAL, "conv: tile does not fit LDS");
     if (static_cast<long>(g.C_in) * g.L_in * 4 > 0x7fffffffL)
         return fail(ctx, KDEC_EINVAL, "conv: input too large for one buffer descriptor");
     g.ybuf = (static_cast<long>(g.C_out) + BM) * g.L_y * 4 < 0x7fffffffL ? 1 : 0;
-    const void* kern = octet ? corr_kernel() : conv_kernel_for(CK);
+    const void* kern = octet ? corr_kernel() : quad ? conv_q_kernel_for(CK, g.k) : conv_kernel_for(CK);
     if (!kern) return fail(ctx, KDEC_EINVAL, "conv: unsupported channel chunk");
     int max_q = g.n_q;
     if (g.n_phase > 1) max_q = static_cast<int>(cdiv(g.L_y + g.ph_s, g.ph_s)) + 1;
@@ -1388,17 +1654,26 @@ int kdec_conv1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
     g.scale = scale; g.beta = beta; g.n_phase = 1;
     if (stride == 1) {
         choose_chunks(ctx, g, C_in, k, dil, cdiv(C_out, BM) * cdiv(L_out, BN) * N);
+        if (g.G == 0 && pick_ck_q(k) > 0) {
+            g.quad = 1;
+            g.CK = pick_ck_q(k);
+        }
     } else {
         g.CK = pick_ck(k, stride, dil);
         g.cin_pad = static_cast<int>(cdiv(C_in, 32) * 32);
     }
-    const long tot = static_cast<long>(g.cin_pad) * k * m_pad;
+    const int nq = static_cast<int>(cdiv(static_cast<long>(g.CK) * k / 2, 4));
+    const long tot = g.quad ? (m_pad / BM) * static_cast<long>(g.cin_pad / g.CK) * nq * 1024
+                            : static_cast<long>(g.cin_pad) * k * m_pad;
     Workspace A(ctx, static_cast<size_t>(tot) * sizeof(float));
     if (!A.p) return KDEC_ENOMEM;
     g.A = A.as<float>();
     KDEC_CHECK(ctx, tot <= 0x7fffffffL && static_cast<long>(C_out) * C_in * k <= 0x7fffffffL,
                "kdec_conv1d_fwd: weights too large");
-    if (g.G > 0)
+    if (g.quad)
+        hipLaunchKernelGGL(pack_quad, dim3(grid1d(tot / 4)), dim3(256), 0, ctx->stream, W, A.as<float>(), 0, C_in,
+                           C_out, k, g.CK, g.cin_pad / g.CK, nq, tot / 4);
+    else if (g.G > 0)
         hipLaunchKernelGGL(pack_octet, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), 0, C_in,
                            C_out, k, 1, k, m_pad, static_cast<int>(tot), 1);
     else
@@ -1437,13 +1712,22 @@ int kdec_conv1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
     g.k = k; g.s = 1; g.d = dil; g.p = pp; g.n_q = L;
     g.scale = scale; g.beta = beta; g.n_phase = 1;
     choose_chunks(ctx, g, C_out, k, dil, cdiv(C_in, BM) * cdiv(L, BN) * N);
-    const long tot = static_cast<long>(g.cin_pad) * k * m_pad;
+    if (g.G == 0 && pick_ck_q(k) > 0) {
+        g.quad = 1;
+        g.CK = pick_ck_q(k);
+    }
+    const int nq = static_cast<int>(cdiv(static_cast<long>(g.CK) * k / 2, 4));
+    const long tot = g.quad ? (m_pad / BM) * static_cast<long>(g.cin_pad / g.CK) * nq * 1024
+                            : static_cast<long>(g.cin_pad) * k * m_pad;
     Workspace A(ctx, static_cast<size_t>(tot) * sizeof(float));
     if (!A.p) return KDEC_ENOMEM;
     g.A = A.as<float>();
     KDEC_CHECK(ctx, tot <= 0x7fffffffL && static_cast<long>(C_out) * C_in * k <= 0x7fffffffL,
                "kdec_conv1d_dgrad: weights too large");
-    if (g.G > 0)
+    if (g.quad)
+        hipLaunchKernelGGL(pack_quad, dim3(grid1d(tot / 4)), dim3(256), 0, ctx->stream, W, A.as<float>(), 1, C_in,
+                           C_out, k, g.CK, g.cin_pad / g.CK, nq, tot / 4);
+    else if (g.G > 0)
         hipLaunchKernelGGL(pack_octet, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), 1, C_in,
                            C_out, k, 1, k, m_pad, static_cast<int>(tot), 1);
     else

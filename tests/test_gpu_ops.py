@@ -142,6 +142,32 @@ def test_conv1d_grid_beyond_one_round(K, k, d):
     assert_close(h(dX), ref.numpy(), GRAD_TOL, "conv1d backward_input, split tail tiles")
 
 
+@pytest.mark.parametrize("k,d", [(11, 5), (3, 3)])
+def test_conv1d_quad_panel_multi_tile(K, k, d):
+    # Grids past one round of resident blocks at k = 3 / 7 / 11 run the
+    # quad-packed weight kernel. Two output-channel tiles (C_out = 200) and
+    # 40 input channels exercise the m-tile-major panel, the zero rows past
+    # C_out and the zero channels past C_in, in the forward and (with the
+    # roles swapped: 200 GEMM input channels, 40 output rows) the input grad.
+    N, C_in, C_out, L = 2, 40, 200, 128 * 650 + 5
+    p = d * (k - 1) // 2
+    x, W, b = rnd(N, C_in, L), rnd(C_out, C_in * k, scale=0.1), rnd(C_out)
+    Y = torch.empty(N, C_out, L, device="cuda")
+    K.call("kdec_conv1d_fwd", P(g(x)), C_in * L, P(g(W)), P(g(b)), P(Y), C_out * L, N, C_in, L, C_out, k, 1,
+           p, d, None, 0, 1.0, 0.0)
+    F = torch.nn.functional
+    xt = torch.from_numpy(x).double()
+    Wt = torch.from_numpy(W).double().reshape(C_out, C_in, k)
+    ref = F.conv1d(xt, Wt, torch.from_numpy(b).double(), padding=p, dilation=d)
+    assert_close(h(Y), ref.numpy(), FWD_TOL, "conv1d forward, quad panel")
+    dY = rnd(N, C_out, L)
+    dX = torch.empty(N, C_in, L, device="cuda")
+    K.call("kdec_conv1d_dgrad", P(g(W)), P(g(dY)), C_out * L, P(dX), C_in * L, N, C_in, L, C_out, k, 1, p, d,
+           1.0, 0.0)
+    ref = F.conv_transpose1d(torch.from_numpy(dY).double(), Wt, padding=p, dilation=d)
+    assert_close(h(dX), ref.numpy(), GRAD_TOL, "conv1d backward_input, quad panel")
+
+
 @pytest.mark.parametrize("k,d", [(3, 5), (11, 1)])
 def test_conv1d_small_grid_split_parts(K, k, d):
     # 200 (forward) and 400 (input-grad) output tiles: fewer than one round of
