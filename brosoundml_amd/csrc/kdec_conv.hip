@@ -992,9 +992,11 @@ __global__ void pack_octet(const float* W, float* A, int mode, int C_in, int C_o
 // ─── weight grad ─────────────────────────────────────────────────────────
 
 constexpr int KC = 32;       // positions per K chunk
-constexpr int WG_WN = 4;                 // waves along n (2 along m)
-constexpr int WG_NT = 128 * WG_WN;       // threads per wgrad block
-constexpr int WG_BN = 64 * WG_WN;        // n columns per wgrad block
+// Waves along n (2 along m): 4 (256 columns per block) or 2 (128 columns,
+// for column counts C_x * k that 256-wide tiles would leave partly idle).
+constexpr int WG_WN = 4;
+constexpr int WG_NT = 128 * WG_WN;       // threads per wide wgrad block
+constexpr int WG_BN = 64 * WG_WN;        // n columns per wide wgrad block
 // G tile in LDS: 64 row pairs (m, m + 64) of 2*KC positions at a pair stride
 // of 2*KC + 4 floats: one 64-lane load fills a whole pair, rows stay 16-B
 // aligned for ds_read_b128, and 16 consecutive m of one such read cover all
@@ -1027,8 +1029,8 @@ struct WgradArgs {
 // (buffer_load_dword ... lds, zero past each row's end): G as 128 rows of KC
 // positions at an odd row stride, the input window as XR channel rows at a
 // stride rs chosen so that column n = c*k + t lands on bank n*d.
-template <bool S1>  // S1: stride 1 (the four input values of a group are adjacent)
-__global__ __launch_bounds__(WG_NT) __attribute__((amdgpu_waves_per_eu(4)))
+template <bool S1, int WN>  // S1: stride 1 (the four input values of a group are adjacent)
+__global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(4)))
 void wgrad_gemm(WgradArgs g) {
     extern __shared__ float smem[];
     const int tid = threadIdx.x;
@@ -1043,7 +1045,7 @@ void wgrad_gemm(WgradArgs g) {
     const int mt = lid % g.m_tiles;
     const int z = lid / g.m_tiles;
     const int m0 = mt * BM;
-    const int n0 = nt * WG_BN;
+    const int n0 = nt * (64 * WN);
     const int k = g.k, s = S1 ? 1 : g.s, d = g.d;
     const int ci_lo = n0 / k;
     const int gsz = 64 * GP;
@@ -1074,22 +1076,22 @@ void wgrad_gemm(WgradArgs g) {
     // input window is staged packed: instruction j fills LDS floats
     // [64j, 64j + 64) of the [row][rs] window, lanes past a row's span (and
     // rows past C_x) read out of range and stage zeros.
-    constexpr int GI = 64 / (2 * WG_WN);  // G pair rows per wave
+    constexpr int GI = 64 / (2 * WN);  // G pair rows per wave
     const bool g_rows_in = m0 + BM <= g.M;  // uniform: whole m-tile (else the checked path)
     // pair row wave + 8j of this lane: g_off + j * 8 * L_g * 4
     const unsigned g_off = static_cast<unsigned>((m0 + wave + 64 * g_row_lane) * g.L_g + g_pos_lane) * 4u;
-    const unsigned g_step = static_cast<unsigned>(2 * WG_WN * g.L_g) * 4u;
+    const unsigned g_step = static_cast<unsigned>(2 * WN * g.L_g) * 4u;
     // Stride 1: the wave's packed-instruction offsets are held (windows of up
     // to WG_XI * 8 * 64 floats; larger ones take the checked path). Strided:
     // this lane's slot of the wave's first instruction as (row, position),
     // each further instruction of the wave 8 * 64 slots on.
     const int nxi = (g.XR * g.rs + 63) / 64;  // packed-window instructions
-    const bool fast_x = !S1 || nxi <= WG_XI * 2 * WG_WN;  // uniform per launch
+    const bool fast_x = !S1 || nxi <= WG_XI * 2 * WN;  // uniform per launch
     unsigned x_off[S1 ? WG_XI : 1];
     if (S1) {
 #pragma unroll
         for (int j = 0; j < WG_XI; ++j) {
-            const int slot = (wave + 2 * WG_WN * j) * 64 + lane;
+            const int slot = (wave + 2 * WN * j) * 64 + lane;
             const int r = slot / g.rs, pos = slot - r * g.rs;
             const int c = ci_lo + r;
             x_off[S1 ? j : 0] = (r < g.XR && pos < g.span && c < g.C_x)
@@ -1098,7 +1100,7 @@ void wgrad_gemm(WgradArgs g) {
     }
     const int xs0 = wave * 64 + lane;
     const int xr0 = xs0 / g.rs, xp0 = xs0 - xr0 * g.rs;
-    const int xqd = (2 * WG_WN * 64) / g.rs, xrd = (2 * WG_WN * 64) - xqd * g.rs;
+    const int xqd = (2 * WN * 64) / g.rs, xrd = (2 * WN * 64) - xqd * g.rs;
     auto issue = [&](int ch, int sb) {
         const int b = ch / g.chunks_per_n;
         const int l0 = (ch - b * g.chunks_per_n) * KC;
@@ -1108,12 +1110,12 @@ void wgrad_gemm(WgradArgs g) {
         if (S1 && fast_x && x0 >= 0 && x0 + g.span <= g.L_x) {  // uniform
 #pragma unroll
             for (int j = 0; j < WG_XI; ++j)
-                if (wave + 2 * WG_WN * j < nxi)
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + gsz + (wave + 2 * WG_WN * j) * 64, 4,
+                if (wave + 2 * WN * j < nxi)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + gsz + (wave + 2 * WN * j) * 64, 4,
                                                              static_cast<int>(x_off[S1 ? j : 0]), x0 * 4, 0, 0);
         } else if (!S1 && x0 >= 0 && x0 + g.span <= g.L_x) {  // uniform
             int r = xr0, pp = xp0;
-            for (int jj = wave; jj < nxi; jj += 2 * WG_WN) {
+            for (int jj = wave; jj < nxi; jj += 2 * WN) {
                 const int c = ci_lo + r;
                 const unsigned off = (r < g.XR && pp < g.span && c < g.C_x)
                                          ? static_cast<unsigned>(c * g.L_x + pp) * 4u : OOB;
@@ -1128,7 +1130,7 @@ void wgrad_gemm(WgradArgs g) {
             }
         } else {
             const bool x_in = x0 >= 0 && x0 + g.span <= g.L_x;  // uniform
-            for (int r = wave; r < g.XR; r += 2 * WG_WN) {
+            for (int r = wave; r < g.XR; r += 2 * WN) {
                 const int c = ci_lo + r;
                 const bool c_in = c < g.C_x;  // uniform
                 int pos = x0 + lane;
@@ -1144,12 +1146,12 @@ void wgrad_gemm(WgradArgs g) {
         if (g_rows_in && l0 + KC <= g.L_g) {  // uniform
 #pragma unroll
             for (int j = 0; j < GI; ++j)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(grs, smem + sb + (wave + 2 * WG_WN * j) * GP, 4,
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(grs, smem + sb + (wave + 2 * WN * j) * GP, 4,
                                                          static_cast<int>(g_off + j * g_step), l0 * 4, 0, 0);
             return;
         }
         const int l = l0 + g_pos_lane;  // a partial m-tile or the last chunk of a row: checked
-        for (int i = wave; i < 64; i += 2 * WG_WN) {
+        for (int i = wave; i < 64; i += 2 * WN) {
             const int m = m0 + i + 64 * g_row_lane;
             const unsigned off = (m < g.M && l < g.L_g) ? static_cast<unsigned>(m * g.L_g + l) * 4u : OOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(grs, smem + sb + i * GP, 4, static_cast<int>(off), 0, 0, 0);
@@ -1750,9 +1752,9 @@ struct WgradLayout {
     size_t lds;
 };
 
-WgradLayout wgrad_layout(int k, int s, int d) {
+WgradLayout wgrad_layout(int k, int s, int d, int wn) {
     WgradLayout w{};
-    w.XR = (WG_BN - 1) / k + 2;
+    w.XR = (64 * wn - 1) / k + 2;
     w.span = static_cast<int>(static_cast<long>(KC - 1) * s + static_cast<long>(k - 1) * d + 1);
     w.segs = static_cast<int>(cdiv(w.span, 64));
     // Column n = c*k + t sits at c*rs + t*d: with rs = k*d (mod 32) that is
@@ -1773,28 +1775,45 @@ WgradLayout wgrad_layout(int k, int s, int d) {
     return w;
 }
 
-size_t wgrad_lds_bytes(int k, int s, int d) { return wgrad_layout(k, s, d).lds; }
+size_t wgrad_lds_bytes(int k, int s, int d, int wn) { return wgrad_layout(k, s, d, wn).lds; }
 
 #ifndef WG_ROUNDS
 #define WG_ROUNDS 2
 #endif
-const void* wgrad_kernel(bool s1) {
+const void* wgrad_kernel(bool s1, int wn) {
     static bool done = false;
+    const void* k[2][2] = {{reinterpret_cast<const void*>(&wgrad_gemm<false, 2>),
+                            reinterpret_cast<const void*>(&wgrad_gemm<false, 4>)},
+                           {reinterpret_cast<const void*>(&wgrad_gemm<true, 2>),
+                            reinterpret_cast<const void*>(&wgrad_gemm<true, 4>)}};
     if (!done) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_gemm<true>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&wgrad_gemm<false>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        for (auto& r : k)
+            for (const void* f : r)
+                (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         done = true;
     }
-    return s1 ? reinterpret_cast<const void*>(&wgrad_gemm<true>) : reinterpret_cast<const void*>(&wgrad_gemm<false>);
+    return k[s1 ? 1 : 0][wn == 4 ? 1 : 0];
 }
 
-int wgrad_splits(kdec_ctx* ctx, int total_chunks, long tiles, size_t lds, bool s1) {
+// Waves along the column axis (C_x * k columns): the narrow 128-column tile
+// where it leaves fewer idle columns than the 256-column one (the stage-1
+// convs' 128 * {3, 7, 11} columns), else the wide tile.
+int wgrad_wn(int NN) {
+#ifdef WG_NARROW_OFF
+    return 4 + 0 * NN;
+#endif
+    const long w4 = cdiv(NN, 256) * 256 - NN, w2 = cdiv(NN, 128) * 128 - NN;
+    return w2 < w4 ? 2 : 4;
+}
+
+int wgrad_splits(kdec_ctx* ctx, int total_chunks, long tiles, size_t lds, bool s1, int wn) {
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, wgrad_kernel(s1), WG_NT, lds) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, wgrad_kernel(s1, wn), 128 * wn, lds) != hipSuccess ||
         per_cu < 1)
         per_cu = 1;
+#ifdef WG_PER_CU_CAP
+    per_cu = std::min(per_cu, WG_PER_CU_CAP);
+#endif
     // The most whole rounds of resident blocks, up to WG_ROUNDS, whose splits
     // keep at least 8 chunks each (shorter runs spend more on the partial
     // tile's write-out and reduction than on the GEMM); never a block past the
@@ -1814,14 +1833,15 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
                         long g_bs, int N, int M, int C_x, int L_x, int L_g, int k,
                         int s, int d, int p, float* out, float* db, const char* fam) {
     const int NN = C_x * k;
+    const int wn = wgrad_wn(NN);
     const int m_tiles = static_cast<int>(cdiv(M, BM));
-    const int n_tiles = static_cast<int>(cdiv(NN, WG_BN));
+    const int n_tiles = static_cast<int>(cdiv(NN, 64 * wn));
     const int chunks_per_n = static_cast<int>(cdiv(L_g, KC));
     const int total_chunks = chunks_per_n * N;
     // split the position chunks so that the blocks fill WG_ROUNDS rounds of
     // the resident slots
     const int splits = wgrad_splits(ctx, total_chunks, static_cast<long>(m_tiles) * n_tiles,
-                                    wgrad_lds_bytes(k, s, d), s == 1);
+                                    wgrad_lds_bytes(k, s, d, wn), s == 1, wn);
     const long MN = static_cast<long>(M) * NN;
     Workspace P(ctx, static_cast<size_t>(splits) * MN * sizeof(float));
     Workspace Pb(ctx, db ? static_cast<size_t>(splits) * M * sizeof(float) : 0);
@@ -1834,7 +1854,7 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
     a.splits = splits;
     a.n_tiles = n_tiles;
     a.m_tiles = m_tiles;
-    const WgradLayout lay = wgrad_layout(k, s, d);
+    const WgradLayout lay = wgrad_layout(k, s, d, wn);
     a.XR = lay.XR;
     a.span = lay.span;
     a.segs = lay.segs;
@@ -1851,7 +1871,7 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
                      4.0 * (static_cast<double>(N) * C_x * L_x + static_cast<double>(N) * M * L_g +
                             static_cast<double>(M) * NN));
         void* args[] = {&a};
-        if (hipLaunchKernel(wgrad_kernel(s == 1), dim3(static_cast<unsigned>(blocks)), dim3(WG_NT), args, lds,
+        if (hipLaunchKernel(wgrad_kernel(s == 1, wn), dim3(static_cast<unsigned>(blocks)), dim3(128 * wn), args, lds,
                             ctx->stream) != hipSuccess)
             return fail(ctx, KDEC_EHIP, std::string(fam) + ": launch failed");
         if (int rc2 = launch_check(ctx, fam)) return rc2;
