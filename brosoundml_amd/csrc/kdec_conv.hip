@@ -29,6 +29,7 @@
 // split over K into deterministic partial tiles that a second kernel sums in
 // a fixed order; the bias grad (row sums of dY) rides along in the same pass.
 #include "kdec_internal.hpp"
+#include "kdec_snake_math.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -98,6 +99,24 @@ struct GemmArgs {
     // octet mode (corr_gemm): K chunk = one input-channel octet x up to G taps
     int G, n_tg, n_oct, span8;  // taps per chunk, tap groups, octets, staged positions
     int quad;                // conv_gemm_q: weights packed in quads of k-steps (stride 1, k = KT)
+    // AdaIN backward epilogue (conv input grads that feed an AdaIN +
+    // activation backward; off when part is null): Y receives
+    // ds = dY * act'(s) of the AdaIN whose input rows x have Y's layout, and
+    // part[((n*C_out + m)*nch + 2*q_tile + half)*3 + j] the tile half's sums
+    // of ds, ds * xh and (Snake) dY (th sin 2th - sin^2 th) / a^2.
+    struct {
+        const float* x;
+        long x_bs;
+        const float2* st;    // (mean, rstd) per n*C_out + m
+        const float* gam;    // gamma / beta at n*gb_bs + m; beta may be null
+        const float* bet;
+        long gb_bs;
+        const float* alpha;  // per m (Snake)
+        int act;
+        float slope;
+        double* part;
+        int nch;             // partial slots per row: 2 per q-tile
+    } ad;
 };
 
 // Logical block order with consecutive ids on one XCD: the dispatcher deals
@@ -253,6 +272,130 @@ __device__ inline void store_tile(const GemmArgs& g, const TileGeo& T, int tile,
                 v *= g.scale;
                 if (g.beta != 0.0f) v += g.beta * Yb[yi];
                 Yb[yi] = v;
+            }
+        }
+    }
+}
+
+// The activation derivative of the AdaIN backward: ds = dy * act'(s) with
+// s the affine output; for Snake, sa takes dy (th sin 2th - sin^2 th), the
+// alpha-grad integrand before its 1/a^2 (the same arithmetic as the AdaIN
+// backward kernels).
+__device__ inline float epi_act_bwd(int act, float dy, float s, float slope, float a, float& sa) {
+    if (act == KDEC_ACT_LEAKY) return s > 0.0f ? dy : slope * dy;
+    if (act == KDEC_ACT_SNAKE) {
+        const float th = a * s;
+        float sq, s2;
+        snake_sin2_sin2x(th, sq, s2);
+        sa += dy * (th * s2 - sq);
+        return dy * (1.0f + s2);
+    }
+    return dy;
+}
+
+// Lane l's value from lane l ^ K within its 32-lane half (ds_swizzle, bit mode).
+template <int K>
+__device__ inline float xor_lane(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (K << 10)));
+}
+
+// One halving step of a transpose-reduce over the 32 lanes of a half: each
+// lane keeps the upper or lower half of its N values (by lane bit K) and adds
+// the partner's copy of that half.
+template <int K, int N>
+__device__ inline void halve(float (&v)[16], int l32) {
+    const bool up = (l32 & K) != 0;
+#pragma unroll
+    for (int j = 0; j < N / 2; ++j) {
+        const float send = up ? v[j] : v[j + N / 2];
+        const float keep = up ? v[j + N / 2] : v[j];
+        v[j] = keep + xor_lane<K>(send);
+    }
+}
+
+// Sums of 16 values per lane over the 32 lanes of a half: afterwards lanes
+// l and l ^ 1 both hold the total of value l >> 1 in v[0].
+__device__ inline void reduce16(float (&v)[16], int l32) {
+    halve<16, 16>(v, l32);
+    halve<8, 8>(v, l32);
+    halve<4, 4>(v, l32);
+    halve<2, 2>(v, l32);
+    v[0] += xor_lane<1>(v[0]);
+}
+
+// Whole-tile epilogue of an input-grad GEMM feeding an AdaIN backward (the
+// g.ad fields): the rows' (mean, rstd, 1 + gamma, beta, alpha) pass through
+// LDS, each output dY = scale * acc becomes ds = dY * act'(s) (stored in Y)
+// with s = (1 + gamma) xh + beta, xh = (x - mean) rstd, and the sums of ds,
+// ds * xh and the alpha-grad integrand over the wave's 64 columns go to the
+// row's partial slot 2 * q_tile + wn. Every lane takes part in the
+// cross-lane reduction; positions past n_q add nothing.
+__device__ inline void store_tile_adain(const GemmArgs& g, const TileGeo& T, const f32x16 (&acc)[2][2], int wm,
+                                        int wn, int hi, int l32, float* smem) {
+    const int b = T.b, n_q = T.n_q, m0 = T.m0, q0 = T.q0;
+    const int tid = threadIdx.x;
+    float4* prm = reinterpret_cast<float4*>(smem);
+    float* pal = smem + 4 * BM;
+    __syncthreads();  // every wave is past its last read of the staged operands
+    if (tid < BM) {
+        const int m = m0 + tid;
+        float4 v = make_float4(0.0f, 0.0f, 1.0f, 0.0f);
+        float a = 1.0f;
+        if (m < g.C_out) {
+            const float2 st = g.ad.st[b * g.C_out + m];
+            v.x = st.x;
+            v.y = st.y;
+            v.z = 1.0f + g.ad.gam[b * g.ad.gb_bs + m];
+            v.w = g.ad.bet ? g.ad.bet[b * g.ad.gb_bs + m] : 0.0f;
+            if (g.ad.act == KDEC_ACT_SNAKE) a = g.ad.alpha[m];
+        }
+        prm[tid] = v;
+        pal[tid] = a;
+    }
+    __syncthreads();
+    const int rowb = g.C_out * g.L_y * 4;
+    const __amdgpu_buffer_rsrc_t yr = uniform_rsrc(g.Y + static_cast<long>(b) * g.y_bs, rowb);
+    const __amdgpu_buffer_rsrc_t xr = uniform_rsrc(g.ad.x + static_cast<long>(b) * g.ad.x_bs, rowb);
+    const int mrow = m0 + wm * 64 + 4 * hi;
+    const int slot = (q0 / BN) * 2 + wn;
+#pragma unroll
+    for (int tm = 0; tm < 2; ++tm) {
+        float sd[16], sdx[16], sa[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sd[e] = sdx[e] = sa[e] = 0.0f;
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn) {
+            const int q = q0 + wn * 64 + tn * 32 + l32;
+            if (q >= n_q) continue;
+            const int vo = (mrow * g.L_y + q) * 4;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int dm = tm * 32 + 8 * (e >> 2) + (e & 3);
+                const int o = vo + dm * g.L_y * 4;
+                const int rl = wm * 64 + 4 * hi + dm;
+                const float4 pr = prm[rl];
+                const float x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, o, 0, 0));
+                const float dy = acc[tm][tn][e] * g.scale;
+                const float xh = (x - pr.x) * pr.y;
+                const float ds = epi_act_bwd(g.ad.act, dy, pr.z * xh + pr.w, g.ad.slope, pal[rl], sa[e]);
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, ds), yr, o, 0, 0);
+                sd[e] += ds;
+                sdx[e] += ds * xh;
+            }
+        }
+        reduce16(sd, l32);
+        reduce16(sdx, l32);
+        if (g.ad.act == KDEC_ACT_SNAKE) reduce16(sa, l32);  // uniform
+        if ((l32 & 1) == 0) {
+            const int e = l32 >> 1;
+            const int rl = wm * 64 + tm * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
+            const int m = m0 + rl;
+            if (m < g.C_out) {
+                double* pp = g.ad.part + ((static_cast<long>(b) * g.C_out + m) * g.ad.nch + slot) * 3;
+                const double a = pal[rl];
+                pp[0] = sd[0];
+                pp[1] = sdx[0];
+                pp[2] = g.ad.act == KDEC_ACT_SNAKE ? static_cast<double>(sa[0]) / (a * a) : 0.0;
             }
         }
     }
@@ -586,7 +729,10 @@ void conv_gemm_q(GemmArgs g) {
         __syncthreads();
     }
 
-    store_tile(g, T, tile, part, acc, wm, wn, hi, l32);
+    if (part < 0 && g.ad.part)  // uniform per block
+        store_tile_adain(g, T, acc, wm, wn, hi, l32, smem);
+    else
+        store_tile(g, T, tile, part, acc, wm, wn, hi, l32);
 }
 
 // Stride-1 correlation (conv forward, conv input-grad, each transposed-conv
@@ -767,6 +913,76 @@ __global__ void tile_reduce(GemmArgs g) {
             if (g.beta != 0.0f) x += g.beta * Yb[yi];
             Yb[yi] = x;
         }
+    }
+}
+
+// Split tiles whose GEMM feeds an AdaIN backward: the parts summed in order
+// (as tile_reduce), then the epilogue of store_tile_adain on the tile's
+// values. One float4 of the tile per thread (grid (BM * BN / 1024,
+// split_tiles) of 256 threads), so the 32 lanes of a half-wave hold one
+// row's 128 columns: their sums go to slot 2 * q_tile, zeros to the other.
+__global__ __launch_bounds__(256) void tile_reduce_adain(GemmArgs g) {
+    const int ti = blockIdx.y;
+    TileGeo T;
+    decode_tile(g, g.full_tiles + ti, T);
+    if (T.q0 >= T.n_q) return;  // uniform per block
+    const int e4 = blockIdx.x * blockDim.x + threadIdx.x;
+    const int l32 = threadIdx.x & 31;
+    const int m = T.m0 + e4 / (BN / 4), qb = T.q0 + (e4 % (BN / 4)) * 4;
+    const float4* Pt = reinterpret_cast<const float4*>(g.P + static_cast<long>(ti) * g.fsplit * (BM * BN));
+    float sd = 0.0f, sdx = 0.0f, sa = 0.0f, a = 1.0f;
+    if (m < g.C_out) {
+        float4 v = Pt[e4];
+        for (int sp = 1; sp < g.fsplit; ++sp) {
+            const float4 w = Pt[sp * (BM * BN / 4) + e4];
+            v.x += w.x;
+            v.y += w.y;
+            v.z += w.z;
+            v.w += w.w;
+        }
+        const int row = T.b * g.C_out + m;
+        const float2 st = g.ad.st[row];
+        const float g1 = 1.0f + g.ad.gam[T.b * g.ad.gb_bs + m];
+        const float bt = g.ad.bet ? g.ad.bet[T.b * g.ad.gb_bs + m] : 0.0f;
+        if (g.ad.act == KDEC_ACT_SNAKE) a = g.ad.alpha[m];
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+        float* Yb = g.Y + static_cast<long>(T.b) * g.y_bs;
+        const float* xb = g.ad.x + static_cast<long>(T.b) * g.ad.x_bs;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int q = qb + j;
+            if (q >= T.n_q) break;
+            const long yi = static_cast<long>(m) * g.L_y + q;
+            const float xh = (xb[yi] - st.x) * st.y;
+            const float ds = epi_act_bwd(g.ad.act, vv[j] * g.scale, g1 * xh + bt, g.ad.slope, a, sa);
+            Yb[yi] = ds;
+            sd += ds;
+            sdx += ds * xh;
+        }
+    }
+    sd += xor_lane<16>(sd);
+    sd += xor_lane<8>(sd);
+    sd += xor_lane<4>(sd);
+    sd += xor_lane<2>(sd);
+    sd += xor_lane<1>(sd);
+    sdx += xor_lane<16>(sdx);
+    sdx += xor_lane<8>(sdx);
+    sdx += xor_lane<4>(sdx);
+    sdx += xor_lane<2>(sdx);
+    sdx += xor_lane<1>(sdx);
+    sa += xor_lane<16>(sa);
+    sa += xor_lane<8>(sa);
+    sa += xor_lane<4>(sa);
+    sa += xor_lane<2>(sa);
+    sa += xor_lane<1>(sa);
+    if (l32 == 0 && m < g.C_out) {
+        double* pp = g.ad.part + ((static_cast<long>(T.b) * g.C_out + m) * g.ad.nch + (T.q0 / BN) * 2) * 3;
+        pp[0] = sd;
+        pp[1] = sdx;
+        pp[2] = g.ad.act == KDEC_ACT_SNAKE ? static_cast<double>(sa) / (static_cast<double>(a) * a) : 0.0;
+        pp[3] = 0.0;
+        pp[4] = 0.0;
+        pp[5] = 0.0;
     }
 }
 
@@ -1421,10 +1637,13 @@ size_t quad_lds_bytes(int CK, int k, int d) {
 }
 
 #ifndef CGQ_CK3
-#define CGQ_CK3 4
+#define CGQ_CK3 8
 #endif
 #ifndef CGQ_CK7
-#define CGQ_CK7 2
+#define CGQ_CK7 4
+#endif
+#ifndef CGQ_CK11
+#define CGQ_CK11 2
 #endif
 // Channel chunk of conv_gemm_q for a k-tap stride-1 correlation, or 0 where
 // no instance exists (conv_gemm serves those).
@@ -1435,7 +1654,7 @@ int pick_ck_q(int k) {
     switch (k) {
         case 3: return CGQ_CK3;
         case 7: return CGQ_CK7;
-        case 11: return 2;
+        case 11: return CGQ_CK11;
         default: return 0;
     }
 }
@@ -1454,7 +1673,7 @@ const void* conv_q_kernel() {
 const void* conv_q_kernel_for(int CK, int k) {
     if (k == 3 && CK == CGQ_CK3) return conv_q_kernel<CGQ_CK3, 3>();
     if (k == 7 && CK == CGQ_CK7) return conv_q_kernel<CGQ_CK7, 7>();
-    if (k == 11 && CK == 2) return conv_q_kernel<2, 11>();
+    if (k == 11 && CK == CGQ_CK11) return conv_q_kernel<CGQ_CK11, 11>();
     return nullptr;
 }
 
@@ -1622,7 +1841,10 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
     }
     if (g.split_tiles > 0) {
         ProfScope ps(ctx, "tile_reduce", 0.0);
-        hipLaunchKernelGGL(tile_reduce, dim3(BM * BN / 1024, g.split_tiles), dim3(256), 0, ctx->stream, g);
+        if (g.ad.part)
+            hipLaunchKernelGGL(tile_reduce_adain, dim3(BM * BN / 1024, g.split_tiles), dim3(256), 0, ctx->stream, g);
+        else
+            hipLaunchKernelGGL(tile_reduce, dim3(BM * BN / 1024, g.split_tiles), dim3(256), 0, ctx->stream, g);
         return launch_check(ctx, "tile_reduce");
     }
     return KDEC_OK;
@@ -1691,11 +1913,38 @@ int kdec_conv1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
                     2.0 * N * C_out * static_cast<double>(L_out) * C_in * k);
 }
 
-int kdec_conv1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
-                      long dy_bs, float* dX, long dx_bs, int N, int C_in,
-                      int L, int C_out, int k, int stride, int pad, int dil,
-                      float scale, float beta) {
-    if (!ctx) return KDEC_EINVAL;
+}  // extern "C"
+
+namespace kdec {
+namespace {
+// Per-call inputs of the AdaIN backward epilogue of an input-grad GEMM.
+struct AdainBwdIn {
+    const float* X;
+    long x_bs;
+    const float* stats;
+    const float* gamma;
+    const float* beta;
+    long gb_bs;
+    int act;
+    float slope;
+    const float* alpha;
+};
+
+// Whether an input-grad GEMM of this geometry runs conv_gemm_q (whose
+// epilogue, and tile_reduce_adain's, can apply an AdaIN backward).
+bool dgrad_is_quad(kdec_ctx* ctx, int N, int C_in, int L, int C_out, int k, int dil) {
+    if (pick_ck_q(k) <= 0) return false;
+    GemmArgs g{};
+    choose_chunks(ctx, g, C_out, k, dil, cdiv(C_in, BM) * cdiv(L, BN) * N);
+    return g.G == 0;
+}
+
+// The input grad as a correlation of dY with the flipped weights; with `ad`
+// (only where dgrad_is_quad) dX receives ds = dX * act'(s) of that AdaIN and
+// `part` its row partial sums (2 * q_tiles slots per row).
+int conv_dgrad_impl(kdec_ctx* ctx, const float* W, const float* dY, long dy_bs, float* dX, long dx_bs, int N,
+                    int C_in, int L, int C_out, int k, int stride, int pad, int dil, float scale, float beta,
+                    const AdainBwdIn* ad, double* part, int nch) {
     KDEC_CHECK(ctx, W && dY && dX && N > 0 && C_in > 0 && C_out > 0 && k > 0 && dil > 0 && pad >= 0,
                "kdec_conv1d_dgrad: bad arguments");
     KDEC_CHECK(ctx, stride == 1, "kdec_conv1d_dgrad: only stride 1 is on the decoder path");
@@ -1717,6 +1966,20 @@ int kdec_conv1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
     if (g.G == 0 && pick_ck_q(k) > 0) {
         g.quad = 1;
         g.CK = pick_ck_q(k);
+    }
+    if (ad) {
+        if (!g.quad || beta != 0.0f) return fail(ctx, KDEC_EINVAL, "conv dgrad: no AdaIN epilogue for this geometry");
+        g.ad.x = ad->X;
+        g.ad.x_bs = ad->x_bs;
+        g.ad.st = reinterpret_cast<const float2*>(ad->stats);
+        g.ad.gam = ad->gamma;
+        g.ad.bet = ad->beta;
+        g.ad.gb_bs = ad->gb_bs;
+        g.ad.alpha = ad->alpha;
+        g.ad.act = ad->act;
+        g.ad.slope = ad->slope;
+        g.ad.part = part;
+        g.ad.nch = nch;
     }
     const int nq = static_cast<int>(cdiv(static_cast<long>(g.CK) * k / 2, 4));
     const long tot = g.quad ? (m_pad / BM) * static_cast<long>(g.cin_pad / g.CK) * nq * 1024
@@ -1744,6 +2007,61 @@ int kdec_conv1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
     if (int rc = launch_check(ctx, "pack_dgrad")) return rc;
     return run_gemm(ctx, g, N, m_pad / BM, "conv_dgrad",
                     2.0 * N * C_out * static_cast<double>(L_out) * C_in * k);
+}
+
+}  // namespace
+}  // namespace kdec
+
+extern "C" {
+
+int kdec_conv1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
+                      long dy_bs, float* dX, long dx_bs, int N, int C_in,
+                      int L, int C_out, int k, int stride, int pad, int dil,
+                      float scale, float beta) {
+    if (!ctx) return KDEC_EINVAL;
+    return conv_dgrad_impl(ctx, W, dY, dy_bs, dX, dx_bs, N, C_in, L, C_out, k, stride, pad, dil, scale, beta, nullptr,
+                           nullptr, 0);
+}
+
+int kdec_conv1d_dgrad_adain_bwd(kdec_ctx* ctx, const float* W, const float* dY, long dy_bs, int N, int C_in, int L,
+                                int C_out, int k, int stride, int pad, int dil, const float* X, long x_bs,
+                                const float* stats, const float* gamma, const float* beta, long gb_bs, int act,
+                                float slope, const float* alpha, const float* R, long r_bs, float* dX, long dx_bs,
+                                float* dgamma, float* dbeta, long dgb_bs, float* dalpha) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, W && dY && X && stats && gamma && dX && N > 0 && C_in > 0 && C_out > 0 && k > 0 && L > 0,
+               "kdec_conv1d_dgrad_adain_bwd: bad arguments");
+    KDEC_CHECK(ctx, act == KDEC_ACT_NONE || act == KDEC_ACT_LEAKY || act == KDEC_ACT_SNAKE,
+               "kdec_conv1d_dgrad_adain_bwd: unknown activation");
+    KDEC_CHECK(ctx, act != KDEC_ACT_SNAKE || alpha, "kdec_conv1d_dgrad_adain_bwd: snake needs alpha");
+    KDEC_CHECK(ctx, act == KDEC_ACT_NONE || beta, "kdec_conv1d_dgrad_adain_bwd: the activation needs beta");
+    KDEC_CHECK(ctx, x_bs >= static_cast<long>(C_in) * L && dx_bs >= static_cast<long>(C_in) * L &&
+                        (!R || r_bs >= static_cast<long>(C_in) * L),
+               "kdec_conv1d_dgrad_adain_bwd: batch stride too small");
+    // fused where the input grad runs conv_gemm_q and dX aliases neither the
+    // AdaIN input nor R (ds is staged in dX); else the two calls it replaces
+    const bool fuse = stride == 1 && dX != X && dX != R &&
+                      (static_cast<long>(C_in) + BM) * L * 4 < 0x7fffffffL &&
+                      dgrad_is_quad(ctx, N, C_in, L, C_out, k, dil);
+    if (!fuse) {
+        Workspace t(ctx, static_cast<size_t>(N) * C_in * L * sizeof(float));
+        if (!t.p) return KDEC_ENOMEM;
+        if (int rc = kdec_conv1d_dgrad(ctx, W, dY, dy_bs, t.as<float>(), static_cast<long>(C_in) * L, N, C_in, L,
+                                       C_out, k, stride, pad, dil, 1.0f, 0.0f))
+            return rc;
+        return kdec_adain_act_bwd(ctx, X, x_bs, stats, gamma, beta, gb_bs, act, slope, alpha, t.as<float>(),
+                                  static_cast<long>(C_in) * L, R, r_bs, dX, dx_bs, dgamma, dbeta, dgb_bs, dalpha, N,
+                                  C_in, L);
+    }
+    const int nch = 2 * static_cast<int>(cdiv(L, BN));
+    Workspace part(ctx, static_cast<size_t>(N) * C_in * nch * 3 * sizeof(double));
+    if (!part.p) return KDEC_ENOMEM;
+    const AdainBwdIn ad{X, x_bs, stats, gamma, beta, gb_bs, act, slope, alpha};
+    if (int rc = conv_dgrad_impl(ctx, W, dY, dy_bs, dX, dx_bs, N, C_in, L, C_out, k, stride, pad, dil, 1.0f, 0.0f,
+                                 &ad, part.as<double>(), nch))
+        return rc;
+    return adain_bwd_finish(ctx, X, x_bs, stats, gamma, gb_bs, act, part.as<double>(), nch, dX, dx_bs, R, r_bs, dX,
+                            dx_bs, dgamma, dbeta, dgb_bs, dalpha, N, C_in, L);
 }
 
 // LDS bytes of one wgrad_gemm block (two stages) and its input-row layout.

@@ -121,4 +121,13 @@ int guard_check_all(kdec_ctx* ctx, const char* where);
 
 inline long cdiv(long a, long b) { return (a + b - 1) / b; }
 
+// The AdaIN backward after a GEMM epilogue wrote ds = dY * act'(s) and the
+// per-row partial sums part[(row*nch + slot)*3 + {sum ds, sum ds*xh, alpha
+// term / a^2}] (kdec_norm.hip): dgamma / dbeta overwritten, dalpha
+// accumulated, dX = rstd (1 + gamma) (ds - mean ds - xh mean(ds xh)) + R.
+int adain_bwd_finish(kdec_ctx* ctx, const float* X, long x_bs, const float* stats, const float* gamma, long gb_bs,
+                     int act, const double* part, int nch, const float* ds, long ds_bs, const float* R, long r_bs,
+                     float* dX, long dx_bs, float* dgamma, float* dbeta, long dgb_bs, float* dalpha, int N, int C,
+                     int L);
+
 }  // namespace kdec

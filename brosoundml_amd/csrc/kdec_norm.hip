@@ -132,15 +132,15 @@ __device__ inline float act_fwd(int act, float s, float slope, float a, float ia
 // Snake, y = s + sin^2(th) / a with th = a * s:
 //   dy/ds = 1 + sin(2 th),   dy/da = (th * sin(2 th) - sin^2(th)) / a^2,
 // and `sa` accumulates dY times the numerator (the row sum is scaled by 1/a^2
-// once). sin / cos are the hardware ones: |th| stays small here, where their
-// error is ~1e-6 absolute, far inside the gradient tolerance.
+// once). sin^2 and sin 2th come from the forward's reduced argument
+// (snake_sin2_sin2x), accurate for any |th| the forward handles.
 __device__ inline float act_bwd(int act, float dy, float s, float slope, float a, float& sa) {
     if (act == KDEC_ACT_LEAKY) return s > 0.0f ? dy : slope * dy;
     if (act == KDEC_ACT_SNAKE) {
         const float th = a * s;
-        const float sn = __sinf(th), cs = __cosf(th);
-        const float s2 = 2.0f * sn * cs;
-        sa += dy * (th * s2 - sn * sn);
+        float sq, s2;
+        snake_sin2_sin2x(th, sq, s2);
+        sa += dy * (th * s2 - sq);
         return dy * (1.0f + s2);
     }
     return dy;
@@ -887,7 +887,69 @@ int bwd_run(kdec_ctx* ctx, const AdainArgs& g, const float* dY, long dy_bs, cons
     return KDEC_OK;
 }
 
+// adain_bwd_fin_k for many slots per row (the partials of a GEMM epilogue):
+// one wave per row, lane j summing slots j, j + 64, ... in double, the lanes'
+// sums then added in a fixed tree.
+__global__ __launch_bounds__(64) void adain_bwd_fin_wide_k(const double* part, int nch, int C, int L,
+                                                           float* dgamma, float* dbeta, long dgb_bs,
+                                                           float* dalpha_part, float2* rowv) {
+    const int row = blockIdx.x;
+    const int n = row / C, c = row - n * C;
+    const double* p = part + static_cast<long>(row) * nch * 3;
+    double sd = 0.0, sdx = 0.0, sa = 0.0;
+    for (int j = threadIdx.x; j < nch; j += 64) {
+        sd += p[j * 3];
+        sdx += p[j * 3 + 1];
+        sa += p[j * 3 + 2];
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        sd += __shfl_xor(sd, o, 64);
+        sdx += __shfl_xor(sdx, o, 64);
+        sa += __shfl_xor(sa, o, 64);
+    }
+    if (threadIdx.x == 0) {
+        if (dgamma) dgamma[n * dgb_bs + c] = static_cast<float>(sdx);
+        if (dbeta) dbeta[n * dgb_bs + c] = static_cast<float>(sd);
+        if (dalpha_part) dalpha_part[row] = static_cast<float>(sa);
+        rowv[row] = make_float2(static_cast<float>(sd / L), static_cast<float>(sdx / L));
+    }
+}
+
 }  // namespace
+
+// The AdaIN backward after a GEMM epilogue produced ds = dY * act'(s) and the
+// per-row partial sums (see store_tile_adain): dgamma / dbeta overwritten,
+// dalpha accumulated (Snake, when non-null), and
+//   dX = rstd (1 + gamma) (ds - mean(ds) - xh mean(ds xh)) + R.
+// ds and dX may be the same buffer (each element is read before it is written).
+int adain_bwd_finish(kdec_ctx* ctx, const float* X, long x_bs, const float* stats, const float* gamma, long gb_bs,
+                     int act, const double* part, int nch, const float* ds, long ds_bs, const float* R, long r_bs,
+                     float* dX, long dx_bs, float* dgamma, float* dbeta, long dgb_bs, float* dalpha, int N, int C,
+                     int L) {
+    const int rows = N * C;
+    const bool want_alpha = dalpha && act == KDEC_ACT_SNAKE;
+    Workspace rv(ctx, static_cast<size_t>(rows) * sizeof(float2));
+    Workspace ap(ctx, want_alpha ? static_cast<size_t>(rows) * sizeof(float) : 0);
+    if (!rv.p || (want_alpha && !ap.p)) return KDEC_ENOMEM;
+    ProfScope ps(ctx, "adain_bwd", 0, 4.0 * static_cast<double>(rows) * L * (R ? 4 : 3));
+    hipLaunchKernelGGL(adain_bwd_fin_wide_k, dim3(static_cast<unsigned>(rows)), dim3(64), 0, ctx->stream, part, nch,
+                       C, L, dgamma, dbeta, dgb_bs, want_alpha ? ap.as<float>() : nullptr, rv.as<float2>());
+    if (int rc = launch_check(ctx, "adain_bwd_fin")) return rc;
+    // the apply with no activation: ds already carries act'
+    const AdainArgs ga{X, x_bs, reinterpret_cast<const float2*>(stats), gamma, nullptr, gb_bs, KDEC_ACT_NONE, 0.0f,
+                       nullptr, C, L};
+    hipLaunchKernelGGL(adain_bwd_apply_k, dim3(static_cast<unsigned>(cdiv(L, CH)), static_cast<unsigned>(rows)),
+                       dim3(RT), 0, ctx->stream, ga, ds, ds_bs, R, r_bs, dX, dx_bs, rv.as<float2>());
+    if (int rc = launch_check(ctx, "adain_bwd_apply")) return rc;
+    if (want_alpha) {
+        hipLaunchKernelGGL(dalpha_reduce, dim3(static_cast<unsigned>(cdiv(C, 256))), dim3(256), 0, ctx->stream,
+                           ap.as<float>(), dalpha, N, C);
+        return launch_check(ctx, "dalpha_reduce");
+    }
+    return KDEC_OK;
+}
+
 }  // namespace kdec
 
 using namespace kdec;

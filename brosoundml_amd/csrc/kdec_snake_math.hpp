@@ -18,22 +18,47 @@
 
 namespace kdec {
 
-KDEC_HD inline float snake_sin2(float th) {
+// th = q (pi/2) + r with |r| <= pi/4; sets sin r, cos r and returns whether
+// q is odd. The parity test compares q / 2 with its rounding (exact in float), so
+// no integer conversion of q is needed.
+KDEC_HD inline bool snake_reduce(float th, float& sn, float& cs) {
     const float q = rintf(th * 0.636619746685028076f);  // nearest multiple of pi/2
     float r = fmaf(-q, 1.57079637050628662f, th);        // pi/2 = c1 + c2 + c3
     r = fmaf(-q, -4.37113882867379300e-08f, r);
     r = fmaf(-q, -1.71512451000588190e-15f, r);
+    // |r| stays within pi/4 plus the rounding of th * 2/pi (a few 1e-3 at
+    // |th| = 30000) wherever th carries its phase; far past that the split
+    // cancels nothing, and clamping to [-1, 1] (where the series still holds
+    // to 3e-8) keeps the results bounded
+    r = fminf(fmaxf(r, -1.0f), 1.0f);
     const float w = r * r;
     // sin r = r + r w (-1/3! + w (1/5! + w (-1/7! + w / 9!)))
     const float ps = fmaf(w, fmaf(w, fmaf(w, 2.75573188e-06f, -1.98412701e-04f), 8.33333377e-03f), -1.66666672e-01f);
-    const float sn = fmaf(r * w, ps, r);
+    sn = fmaf(r * w, ps, r);
     // cos r = 1 + w (-1/2! + w (1/4! + w (-1/6! + w (1/8! - w / 10!))))
     const float pc = fmaf(w, fmaf(w, fmaf(w, fmaf(w, -2.75573199e-07f, 2.48015876e-05f), -1.38888892e-03f),
                                   4.16666679e-02f),
                           -0.5f);
-    const float cs = fmaf(w, pc, 1.0f);
-    const float v = (static_cast<int>(q) & 1) ? cs : sn;
+    cs = fmaf(w, pc, 1.0f);
+    const float h = 0.5f * q;
+    return h != rintf(h);
+}
+
+KDEC_HD inline float snake_sin2(float th) {
+    float sn, cs;
+    const float v = snake_reduce(th, sn, cs) ? cs : sn;
     return v * v;
+}
+
+// sin^2(th) and sin(2 th) from the same reduction: for odd q, sin th = +-cos r
+// and cos th = -+sin r, so sin^2 th = cos^2 r and sin 2th = -sin 2r.
+KDEC_HD inline void snake_sin2_sin2x(float th, float& s2, float& sin2x) {
+    float sn, cs;
+    const bool odd = snake_reduce(th, sn, cs);
+    const float v = odd ? cs : sn;
+    s2 = v * v;
+    const float t = 2.0f * sn * cs;
+    sin2x = odd ? -t : t;
 }
 
 }  // namespace kdec

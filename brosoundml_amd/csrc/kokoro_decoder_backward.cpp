@@ -309,6 +309,33 @@ Tensor adain_act_bwd(const Tensor& x, const Tensor& st, const Tensor& g, const T
     return dX;
 }
 
+// conv_dgrad of `c` followed by the adain_act_bwd of the AdaIN + activation
+// that feeds it (C = c.in_channels), as one kdec call: where the input-grad
+// GEMM allows, its epilogue applies the activation derivative and sums the
+// AdaIN's rows, so the intermediate grad is not written separately.
+Tensor conv_dgrad_adain_bwd(const Conv1d& c, const Tensor& dY, int L, const Tensor& x, const Tensor& st,
+                            const Tensor& g, const Tensor* b, int act, float slope, const Tensor* alpha,
+                            const Tensor* R, Tensor& dG, Tensor& dB, float* dalpha, const char* where) {
+    if (c.groups != 1) fail(where, "grouped conv1d is not on the decoder path");
+    const int N = x.rows, C = c.in_channels;
+    const Affine ga = affine_in(g, N, C, where);
+    Affine ba{nullptr, ga.bs};
+    if (b) {
+        ba = affine_in(*b, N, C, where);
+        if (ga.bs != ba.bs) fail(where, "gamma and beta must share one layout");
+    }
+    if (static_cast<long>(st.size()) != 2L * N * C) fail(where, "statistics cache does not match the input");
+    Tensor dX = dev(N, C * L);
+    AffineGrads out(dG, dB, g, N, C);
+    ck(kdec_conv1d_dgrad_adain_bwd(kctx(), cp(c.W), cp(dY), rs(dY), N, C, L, c.out_channels, c.kernel_size,
+                                   c.stride, c.padding, c.dilation, cp(x), rs(x), cp(st), ga.p, ba.p, ga.bs, act,
+                                   slope, alpha ? cp(*alpha) : nullptr, R ? cp(*R) : nullptr, R ? rs(*R) : 0,
+                                   mp(dX), rs(dX), out.pg, out.pb, out.bs, dalpha),
+       where);
+    out.finish();
+    return dX;
+}
+
 Tensor leaky(const Tensor& x, float slope) {
     Tensor y = dev(x.rows, x.cols);
     ck(kdec_leaky_fwd(kctx(), cp(x), rs(x), mp(y), rs(y), x.rows, x.cols, slope), "leaky_relu forward");
@@ -604,28 +631,26 @@ Tensor resblock1_bwd(const AdaINResBlock1Weights& w, const AdainResBlock1Cache& 
     Tensor dx = dX_out;
     for (int i = 2; i >= 0; --i) {
         // convs2[i] -> snake2 -> adain2
-        Tensor d_xt2 = conv_dgrad(w.convs2[i], dx, L);
         if (wg && (grad_of(wg, w.convs2[i].W) || grad_of(wg, w.convs2[i].b))) {
             const Tensor xt2 = cache.act2[i].data ? cache.act2[i]
                                                   : adain_act(cache.c1_out[i], cache.x_seq2[i], g2[i], cache.beta2[i],
                                                               C, L, KDEC_ACT_SNAKE, 0.0f, &w.alpha2[i], where);
             conv_wgrad(w.convs2[i], wg, xt2, L, dx);
         }
-        Tensor d_c1 = adain_act_bwd(cache.c1_out[i], cache.x_seq2[i], g2[i], &cache.beta2[i], C, L,
-                                    KDEC_ACT_SNAKE, 0.0f, &w.alpha2[i], d_xt2, nullptr, dG2[i], dB2[i],
-                                    grad_of(wg, w.alpha2[i]), where);
-        d_xt2 = Tensor();
+        Tensor d_c1 = conv_dgrad_adain_bwd(w.convs2[i], dx, L, cache.c1_out[i], cache.x_seq2[i], g2[i],
+                                           &cache.beta2[i], KDEC_ACT_SNAKE, 0.0f, &w.alpha2[i], nullptr, dG2[i],
+                                           dB2[i], grad_of(wg, w.alpha2[i]), where);
         // convs1[i] -> snake1 -> adain1 (+ the residual skip)
-        Tensor d_xt1 = conv_dgrad(w.convs1[i], d_c1, L);
         if (wg && (grad_of(wg, w.convs1[i].W) || grad_of(wg, w.convs1[i].b))) {
             const Tensor xt1 = cache.act1[i].data ? cache.act1[i]
                                                   : adain_act(cache.x_in[i], cache.x_seq1[i], g1[i], cache.beta1[i],
                                                               C, L, KDEC_ACT_SNAKE, 0.0f, &w.alpha1[i], where);
             conv_wgrad(w.convs1[i], wg, xt1, L, d_c1);
         }
+        dx = conv_dgrad_adain_bwd(w.convs1[i], d_c1, L, cache.x_in[i], cache.x_seq1[i], g1[i], &cache.beta1[i],
+                                  KDEC_ACT_SNAKE, 0.0f, &w.alpha1[i], &dx, dG1[i], dB1[i], grad_of(wg, w.alpha1[i]),
+                                  where);
         d_c1 = Tensor();
-        dx = adain_act_bwd(cache.x_in[i], cache.x_seq1[i], g1[i], &cache.beta1[i], C, L, KDEC_ACT_SNAKE, 0.0f,
-                           &w.alpha1[i], d_xt1, &dx, dG1[i], dB1[i], grad_of(wg, w.alpha1[i]), where);
     }
     return dx;
 }

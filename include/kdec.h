@@ -92,6 +92,28 @@ int kdec_conv1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
                       int L, int C_out, int k, int stride, int pad, int dil,
                       float scale, float beta);
 
+/* The input grad of a stride-1 conv1d followed by the backward of the
+ * AdaIN + activation whose output feeds that conv:
+ *   dX = kdec_adain_act_bwd(X, ..., dY' = conv1d_dgrad(W, dY)) (+ R)
+ * with dgamma / dbeta overwritten and dalpha accumulated, as the two calls
+ * kdec_conv1d_dgrad + kdec_adain_act_bwd (same arguments). Where the GEMM
+ * runs the quad-packed kernel, its epilogue applies the activation
+ * derivative and forms the AdaIN's per-row partial sums, so dY' is never
+ * written separately and the AdaIN pass reads it once; elsewhere it makes
+ * those two calls. dX must not alias X or R.
+ * Replaces bt::conv1d_backward_input followed by bt::snake_backward and
+ * adain_affine_backward at kokoro_decoder_backward.cpp:347-356 and :360-369
+ * (leaky: :230-241, :244-266). */
+int kdec_conv1d_dgrad_adain_bwd(kdec_ctx* ctx, const float* W, const float* dY,
+                                long dy_bs, int N, int C_in, int L, int C_out,
+                                int k, int stride, int pad, int dil,
+                                const float* X, long x_bs, const float* stats,
+                                const float* gamma, const float* beta,
+                                long gb_bs, int act, float slope,
+                                const float* alpha, const float* R, long r_bs,
+                                float* dX, long dx_bs, float* dgamma,
+                                float* dbeta, long dgb_bs, float* dalpha);
+
 /* dW (C_out, C_in*k) and db (C_out) accumulated over the batch; either may
  * be NULL.
  * North-star extension: the reference freezes conv weights; the signature of

@@ -168,6 +168,54 @@ def test_conv1d_quad_panel_multi_tile(K, k, d):
     assert_close(h(dX), ref.numpy(), GRAD_TOL, "conv1d backward_input, quad panel")
 
 
+@pytest.mark.parametrize("case", ["quad_snake_residual", "split_tiles_leaky", "small_grid_none"])
+def test_conv1d_dgrad_adain_bwd_fused(K, case):
+    # kdec_conv1d_dgrad_adain_bwd against the two calls it replaces
+    # (kdec_conv1d_dgrad, then kdec_adain_act_bwd, each checked against the
+    # oracle elsewhere): the quad-packed GEMM with the AdaIN epilogue on whole
+    # tiles (C = 128, 1400 tiles, Snake, residual grad R), with split tail
+    # tiles reduced by tile_reduce_adain (C = 256: two output-channel tiles,
+    # leaky), and the unfused fallback on a small grid. dX, dgamma, dbeta and
+    # dalpha (accumulated onto a nonzero start) agree to summation order.
+    N, C, Co, L, k, d, act, with_r = {
+        "quad_snake_residual": (2, 128, 128, 128 * 700, 11, 5, "snake", True),
+        "split_tiles_leaky": (2, 256, 256, 128 * 330 - 9, 7, 3, "leaky", False),
+        "small_grid_none": (1, 64, 96, 1000, 3, 1, "none", True),
+    }[case]
+    p = d * (k - 1) // 2
+    x = rnd(N, C, L, scale=1.3) + 0.2
+    W = rnd(Co, C * k, scale=1.0 / np.sqrt(C * k))
+    dYc = rnd(N, Co, L)
+    gm, bt = rnd(N, C, scale=0.4), rnd(N, C, scale=0.3)
+    alpha = rng.uniform(0.5, 2.0, C).astype(np.float32)
+    R = rnd(N, C, L) if with_r else None
+    st = torch.empty(N * C, 2, device="cuda")
+    K.call("kdec_instnorm_stats", P(g(x)), C * L, N, C, L, 1e-5, P(st))
+    a0 = rng.standard_normal(C).astype(np.float32)
+    outs = []
+    for fused in (False, True):
+        dX = torch.empty(N, C, L, device="cuda")
+        dg = torch.empty(N, C, device="cuda")
+        db = torch.empty(N, C, device="cuda")
+        da = g(a0).clone()
+        if fused:
+            K.call("kdec_conv1d_dgrad_adain_bwd", P(g(W)), P(g(dYc)), Co * L, N, C, L, Co, k, 1, p, d, P(g(x)),
+                   C * L, P(st), P(g(gm)), P(g(bt)), C, ACTS[act], 0.2, P(g(alpha)), P(g(R) if with_r else None),
+                   C * L, P(dX), C * L, P(dg), P(db), C, P(da))
+        else:
+            t = torch.empty(N, C, L, device="cuda")
+            K.call("kdec_conv1d_dgrad", P(g(W)), P(g(dYc)), Co * L, P(t), C * L, N, C, L, Co, k, 1, p, d, 1.0, 0.0)
+            K.call("kdec_adain_act_bwd", P(g(x)), C * L, P(st), P(g(gm)), P(g(bt)), C, ACTS[act], 0.2, P(g(alpha)),
+                   P(t), C * L, P(g(R) if with_r else None), C * L, P(dX), C * L, P(dg), P(db), C, P(da), N, C, L)
+        outs.append([h(dX), h(dg), h(db), h(da)])
+    ref, got = outs
+    for i, what in enumerate(("dX", "dgamma", "dbeta", "dalpha")):
+        if what == "dalpha" and act != "snake":
+            assert np.array_equal(got[i], a0), "dalpha changed for a non-Snake activation"
+            continue
+        assert_close(got[i], ref[i], 2e-6, f"fused dgrad + adain backward ({case}) {what}")
+
+
 @pytest.mark.parametrize("k,d", [(3, 5), (11, 1)])
 def test_conv1d_small_grid_split_parts(K, k, d):
     # 200 (forward) and 400 (input-grad) output tiles: fewer than one round of

@@ -1,7 +1,8 @@
-"""The Snake forward's sin^2 (brosoundml_amd/csrc/kdec_snake_math.hpp), built
-for the host with g++ and checked against double-precision sin^2: the error
-bound over wide argument ranges, the values at multiples of pi/2 and the tiny
-argument limit. The GPU kernels compile the same header; their forward parity
+"""The Snake forward's sin^2 and the backward's (sin^2, sin 2th) pair
+(brosoundml_amd/csrc/kdec_snake_math.hpp), built for the host with g++ and
+checked against double precision: the error bound over wide argument ranges,
+the values at multiples of pi/2, the tiny argument limit and arguments past
+2^31. The GPU kernels compile the same header; their forward parity
 is in test_gpu_ops.py."""
 import os
 import subprocess
@@ -20,15 +21,28 @@ int main() {
     const double ranges[] = {1.0, 100.0, 30000.0};
     for (double R : ranges) {
         std::uniform_real_distribution<float> U(-R, R);
-        double max_abs = 0.0;
+        double max_abs = 0.0, max_s2 = 0.0, max_sq = 0.0;
         for (int i = 0; i < 400000; ++i) {
             float th = U(g);
             if (i % 4 == 0)  // next to a multiple of pi/2, where the reduction cancels most
                 th = static_cast<float>(std::nearbyint(th / (M_PI / 2)) * (M_PI / 2)) + U(g) * 1e-6f;
             const double ex = std::sin(static_cast<double>(th));
             max_abs = std::fmax(max_abs, std::fabs(kdec::snake_sin2(th) - ex * ex));
+            float sq, s2;
+            kdec::snake_sin2_sin2x(th, sq, s2);
+            max_sq = std::fmax(max_sq, std::fabs(sq - ex * ex));
+            max_s2 = std::fmax(max_s2, std::fabs(s2 - std::sin(2.0 * static_cast<double>(th))));
         }
         std::printf("range %g %.6e\n", R, max_abs);
+        std::printf("pair %g %.6e %.6e\n", R, max_sq, max_s2);
+    }
+    // past 2^31 the quadrant index exceeds int range: results stay finite and in range
+    const float huge[] = {3.0e9f, -7.5e12f, 1.0e30f};
+    for (float th : huge) {
+        float sq, s2;
+        kdec::snake_sin2_sin2x(th, sq, s2);
+        std::printf("huge %d\n", std::isfinite(sq) && std::isfinite(s2) && sq >= 0.0f && sq <= 1.0f + 1e-6f &&
+                                     std::fabs(s2) <= 1.0f + 1e-6f ? 1 : 0);
     }
     for (int q = -8; q <= 8; ++q) {
         const float th = static_cast<float>(q * (M_PI / 2));
@@ -58,6 +72,20 @@ def test_error_bound(results):
     for r in results:
         if r[0] == "range":
             assert float(r[2]) < 2e-7, r
+
+
+def test_sin2_and_sin2x_pair(results):
+    # the backward's pair from one reduction: sin^2 as the forward's, sin 2th
+    # (the derivative 1 + sin 2th and the alpha-grad term) within 3e-7
+    rows = [r for r in results if r[0] == "pair"]
+    assert len(rows) == 3
+    for r in rows:
+        assert float(r[2]) < 2e-7 and float(r[3]) < 3e-7, r
+
+
+def test_huge_arguments(results):
+    rows = [r for r in results if r[0] == "huge"]
+    assert rows and all(r[1] == "1" for r in rows), rows
 
 
 def test_quadrants(results):
