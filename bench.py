@@ -328,6 +328,9 @@ def main(argv=None):
                     help="run only the per-kernel-class microbenchmarks and print their JSON (for profiling them)")
     ap.add_argument("--serial", action="store_true",
                     help="one stream (no harmonic-source / weight-grad overlap): per-family times without sharing")
+    ap.add_argument("--batch-split", type=int, default=0,
+                    help="1: run the batch as two half-batch chains on two streams (kdec_model_set_batch_split); "
+                         "0 (default): one chain")
     ap.add_argument("--cpu-plan", action="store_true",
                     help="run only the full CPU baseline plan (configs 0-4 on the oracle, 1 thread and all cores, "
                          "medians of 3) and print its JSON; several minutes")
@@ -372,6 +375,7 @@ def main(argv=None):
     model.set_params(params)
     if a.serial:
         model.set_overlap(False)
+    model.set_batch_split(a.batch_split)
     asr, F0, Nn, style, dA = make_inputs(cfg, B, T, "bench")
     dev = lambda x: torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
     t_asr, t_F0, t_N, t_style, t_dA = (dev(x) for x in (asr, F0, Nn, style, dA))

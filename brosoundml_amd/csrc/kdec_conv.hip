@@ -1633,7 +1633,11 @@ size_t quad_lds_bytes(int CK, int k, int d) {
     const long S = static_cast<long>(CK) * k / 2, Q = (S + 3) / 4;
     const long span = BN + static_cast<long>(k - 1) * d;
     const long span_p = (span + 3 + 255) / 256 * 256;
-    return 2 * (static_cast<size_t>(Q) * 1024 + static_cast<size_t>(CK) * span_p) * sizeof(float);
+    size_t b = 2 * (static_cast<size_t>(Q) * 1024 + static_cast<size_t>(CK) * span_p) * sizeof(float);
+#ifdef CGQ_MIN_LDS
+    b = std::max(b, static_cast<size_t>(CGQ_MIN_LDS));
+#endif
+    return b;
 }
 
 #ifndef CGQ_CK3

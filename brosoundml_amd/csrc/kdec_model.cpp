@@ -36,12 +36,16 @@ struct kdec_model {
     struct Param {
         Tensor* value = nullptr;  // points into a module struct
         Tensor grad;
+        Tensor grad2;             // the second batch part's share (gbuf2)
         int rows = 0, cols = 0;
         long offset = 0;          // into the flat buffers
     };
     std::vector<std::string> order;
     std::map<std::string, Param> params;
     Tensor pbuf, gbuf;            // flat parameter / grad storage
+    // The second batch part's conv / alpha weight grads accumulate here while
+    // the two parts' backwards run concurrently; gbuf then adds it.
+    Tensor gbuf2;
     long total = 0;
 
     struct Unit {
@@ -54,15 +58,34 @@ struct kdec_model {
     std::vector<brosoundml::AdaIN1dWeights*> unit_w;  // same order as units
 
     bd::WeightGrads wg_all, wg_conv, wg_alpha;
+    bd::WeightGrads wg_all2, wg_conv2, wg_alpha2;  // into gbuf2
 
     // per forward
     int N = 0, T = 0;
     Tensor style_v, gb, dgb;
-    std::vector<bd::BlockAffines> bbaff, dbbaff;
-    std::vector<bd::ResBlock1Affines> naff, raff, dnaff, draff;
-    bd::BackboneCache bbc;
-    bd::GeneratorCache genc;
-    Tensor gen_in, har;
+    // The batch runs as one or (kdec_model_set_batch_split) two parts:
+    // contiguous row ranges, each a whole backbone + generator chain with its
+    // own affine views and caches on its own context (part 0 on ctx, part 1
+    // on ctx2, each with its allocator and stream), forwards and backwards
+    // concurrent; part 1's conv weight grads accumulate into gbuf2 (on side2)
+    // and are added to gbuf at the end.
+    struct Part {
+        int n0 = 0, n = 0;          // rows [n0, n0 + n)
+        kdec_ctx* ctx = nullptr;
+        std::vector<bd::BlockAffines> bbaff, dbbaff;
+        std::vector<bd::ResBlock1Affines> naff, raff, dnaff, draff;
+        bd::BackboneCache bbc;
+        bd::GeneratorCache genc;
+        Tensor gen_in;
+    };
+    Part part[2];
+    int parts = 0;                  // of the last training forward
+    bool split = false;             // kdec_model_set_batch_split
+    kdec_ctx* ctx2 = nullptr;
+    kdec_ctx* side2 = nullptr;      // part 1's conv weight-grad stream
+    hipEvent_t ev_split = nullptr, ev_part1 = nullptr;
+    Tensor har;
+    mutable Tensor gen_in_all;      // both parts' generator inputs, on demand
     std::string err;
 
     // The harmonic source depends only on F0: it runs on a side context's
@@ -301,14 +324,23 @@ int kdec_model_create(kdec_ctx* ctx, const int* v, int n, kdec_model** out) {
         delete m;
         return KDEC_EINVAL;
     }
-    if (kdec_ctx_create(ctx->device, &m->side) != KDEC_OK ||
+    if (kdec_ctx_create(ctx->device, &m->side) != KDEC_OK || kdec_ctx_create(ctx->device, &m->ctx2) != KDEC_OK ||
+        kdec_ctx_create(ctx->device, &m->side2) != KDEC_OK ||
         hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&m->ev_join, hipEventDisableTiming) != hipSuccess) {
+        hipEventCreateWithFlags(&m->ev_join, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&m->ev_split, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&m->ev_part1, hipEventDisableTiming) != hipSuccess) {
         kdec_model_destroy(m);
-        return kdec::fail(ctx, KDEC_EHIP, "kdec_model_create: side stream");
+        return kdec::fail(ctx, KDEC_EHIP, "kdec_model_create: side streams");
     }
     m->side->prof = ctx->prof;
+    m->ctx2->prof = ctx->prof;
+    m->side2->prof = ctx->prof;
     ctx->peers.push_back(m->side);
+    ctx->peers.push_back(m->ctx2);
+    ctx->peers.push_back(m->side2);
+    m->part[0].ctx = ctx;
+    m->part[1].ctx = m->ctx2;
     try {
         bt::set_runtime(ctx);
         std::vector<Spec> specs;
@@ -318,6 +350,7 @@ int kdec_model_create(kdec_ctx* ctx, const int* v, int n, kdec_model** out) {
         m->total = total;
         m->pbuf = Tensor::zeros_on(Device::HIP, 1, static_cast<int>(total));
         m->gbuf = Tensor::zeros_on(Device::HIP, 1, static_cast<int>(total));
+        m->gbuf2 = Tensor::zeros_on(Device::HIP, 1, static_cast<int>(total));
         long off = 0;
         for (auto& s : specs) {
             kdec_model::Param p;
@@ -327,6 +360,7 @@ int kdec_model_create(kdec_ctx* ctx, const int* v, int n, kdec_model** out) {
             p.offset = off;
             *s.t = view_of(m->pbuf, off, s.rows, s.cols);
             p.grad = view_of(m->gbuf, off, s.rows, s.cols);
+            p.grad2 = view_of(m->gbuf2, off, s.rows, s.cols);
             off += static_cast<long>(s.rows) * s.cols;
             m->order.push_back(s.name);
             auto& slot = m->params[s.name];
@@ -334,9 +368,13 @@ int kdec_model_create(kdec_ctx* ctx, const int* v, int n, kdec_model** out) {
             if (s.kind == 0) {
                 m->wg_all.add(*s.t, slot.grad);
                 m->wg_conv.add(*s.t, slot.grad);
+                m->wg_all2.add(*s.t, slot.grad2);
+                m->wg_conv2.add(*s.t, slot.grad2);
             } else if (s.kind == 1) {
                 m->wg_all.add(*s.t, slot.grad);
                 m->wg_alpha.add(*s.t, slot.grad);
+                m->wg_all2.add(*s.t, slot.grad2);
+                m->wg_alpha2.add(*s.t, slot.grad2);
             }
         }
     } catch (const std::exception& e) {
@@ -349,19 +387,21 @@ int kdec_model_create(kdec_ctx* ctx, const int* v, int n, kdec_model** out) {
 
 int kdec_model_destroy(kdec_model* m) {
     if (!m) return KDEC_OK;
-    if (m->side) {
-        hipStreamSynchronize(m->side->stream);
+    for (kdec_ctx** sp : {&m->side, &m->ctx2, &m->side2}) {
+        kdec_ctx* sc = *sp;
+        if (!sc) continue;
+        (void)hipStreamSynchronize(sc->stream);
         auto& pv = m->ctx->peers;
         for (auto it = pv.begin(); it != pv.end(); ++it)
-            if (*it == m->side) {
+            if (*it == sc) {
                 pv.erase(it);
                 break;
             }
-        kdec_ctx_destroy(m->side);
-        m->side = nullptr;
+        kdec_ctx_destroy(sc);  // blocks still held by the caches release it later
+        *sp = nullptr;
     }
-    if (m->ev_fork) hipEventDestroy(m->ev_fork);
-    if (m->ev_join) hipEventDestroy(m->ev_join);
+    for (hipEvent_t e : {m->ev_fork, m->ev_join, m->ev_split, m->ev_part1})
+        if (e) (void)hipEventDestroy(e);
     delete m;
     return KDEC_OK;
 }
@@ -552,54 +592,30 @@ int kdec_model_forward(kdec_model* m, int N, int T, const float* asr, const floa
                                                           N, R, S))) {
             return rc;
         }
-        auto gv = [&](const Tensor& buf, int off, int C) {
-            Tensor t = Tensor::view(Device::HIP, static_cast<float*>(buf.data) + off, N, C, bt::Dtype::FP32, R);
-            t.storage = buf.storage;
-            return t;
-        };
-        const int n_dec = m->n_decode;
-        m->bbaff.assign(1 + n_dec, bd::BlockAffines{});
-        m->naff.assign(m->n_ups, bd::ResBlock1Affines{});
-        m->raff.assign(static_cast<std::size_t>(m->n_ups) * m->n_kernels, bd::ResBlock1Affines{});
-        std::size_t u = 0;
-        auto pair = [&](Tensor& g, Tensor& bb) {
-            const auto& un = m->units[u++];
-            g = gv(m->gb, un.offset, un.C);
-            bb = gv(m->gb, un.offset + un.C, un.C);
-        };
-        for (auto& a : m->bbaff) { pair(a.g1, a.b1); pair(a.g2, a.b2); }
-        auto rb = [&](bd::ResBlock1Affines& a) {
-            for (int j = 0; j < 3; ++j) pair(a.g1[j], a.b1[j]);
-            for (int j = 0; j < 3; ++j) pair(a.g2[j], a.b2[j]);
-        };
-        for (auto& a : m->naff) rb(a);
-        for (auto& a : m->raff) rb(a);
-
         // harmonic source (side stream) -- HarmonicSource::forward's work
         const auto& hs = m->hs;
         const int sig = 2 * T * hs.upsample_scale;
         const int frames = sig / hs.hop_size + 1;
+        const int har_cols = (m->n_fft + 2) * frames;
         hipStream_t ms = static_cast<hipStream_t>(kdec_get_stream(m->ctx));
         bool forked = false;
         if (har_in) {
-            Tensor h = in(har_in, (m->n_fft + 2) * frames);
+            Tensor h = in(har_in, har_cols);
             m->har = h.clone();
         } else if (!m->overlap) {
-            m->har = Tensor::empty_on(Device::HIP, N, (m->n_fft + 2) * frames);
-            const int rc = kdec_harmonic_source(m->ctx, F0, 2 * T, static_cast<float*>(m->har.data),
-                                                (m->n_fft + 2) * frames, N, 2 * T,
-                                                static_cast<const float*>(hs.l_linear.W.data),
+            m->har = Tensor::empty_on(Device::HIP, N, har_cols);
+            const int rc = kdec_harmonic_source(m->ctx, F0, 2 * T, static_cast<float*>(m->har.data), har_cols, N,
+                                                2 * T, static_cast<const float*>(hs.l_linear.W.data),
                                                 static_cast<const float*>(hs.l_linear.b.data), hs.harmonic_num,
                                                 hs.sample_rate, hs.upsample_scale, hs.n_fft, hs.hop_size);
             if (rc != KDEC_OK) return rc;
         } else {
-            m->har = Tensor::empty_on(Device::HIP, N, (m->n_fft + 2) * frames);
+            m->har = Tensor::empty_on(Device::HIP, N, har_cols);
             if (hipEventRecord(m->ev_fork, ms) != hipSuccess ||
                 hipStreamWaitEvent(m->side->stream, m->ev_fork, 0) != hipSuccess)
                 return fail(m, KDEC_EHIP, "kdec_model_forward: fork");
-            const int rc = kdec_harmonic_source(m->side, F0, 2 * T, static_cast<float*>(m->har.data),
-                                                (m->n_fft + 2) * frames, N, 2 * T,
-                                                static_cast<const float*>(hs.l_linear.W.data),
+            const int rc = kdec_harmonic_source(m->side, F0, 2 * T, static_cast<float*>(m->har.data), har_cols, N,
+                                                2 * T, static_cast<const float*>(hs.l_linear.W.data),
                                                 static_cast<const float*>(hs.l_linear.b.data), hs.harmonic_num,
                                                 hs.sample_rate, hs.upsample_scale, hs.n_fft, hs.hop_size);
             if (rc != KDEC_OK) return fail(m, rc, std::string("harmonic source: ") + kdec_last_error(m->side));
@@ -607,24 +623,86 @@ int kdec_model_forward(kdec_model* m, int N, int T, const float* asr, const floa
                 return fail(m, KDEC_EHIP, "kdec_model_forward: join");
             forked = true;
         }
-        bd::decoder_backbone_forward_train(m->bb, in(asr, m->asr_dim * T), in(F0, 2 * T), in(Nn, 2 * T), T,
-                                           m->bbaff, 1e-5f, m->gen_in, m->bbc);
-        const int init_C = m->dec_out[n_dec - 1];
-        const int L_gen = m->gen_in.cols / init_C;
-        Tensor out;
-        // the generator waits for har itself, after stage 0's upsampling
-        m->genc.har_ready = forked ? static_cast<void*>(m->ev_join) : nullptr;
-        bd::generator_forward_train(m->gen, m->gen_in, L_gen, m->har, frames, m->naff, m->raff, out, m->genc);
-        if (m->genc.har_ready) {  // no noise conv consumed it: join here
-            m->genc.har_ready = nullptr;
-            if (hipStreamWaitEvent(ms, m->ev_join, 0) != hipSuccess)
-                return fail(m, KDEC_EHIP, "kdec_model_forward: join");
+
+        // the parts: two halves of the batch on two streams, or one
+        m->parts = (m->overlap && m->split && N >= 2) ? 2 : 1;
+        if (m->parts == 1) {  // an earlier forward's second-part caches go
+            kdec_model::Part& p1 = m->part[1];
+            const bool keep_b = p1.bbc.keep, keep_g = p1.genc.keep;
+            p1.bbc = bd::BackboneCache{};
+            p1.genc = bd::GeneratorCache{};
+            p1.bbc.keep = keep_b;
+            p1.genc.keep = keep_g;
+            p1.gen_in = Tensor();
+            p1.bbaff.clear();
+            p1.naff.clear();
+            p1.raff.clear();
         }
-        const int alen = out.cols;
-        hipStream_t s = static_cast<hipStream_t>(kdec_get_stream(m->ctx));
-        hipError_t e = hipMemcpyAsync(audio, out.data, static_cast<size_t>(N) * alen * sizeof(float),
-                                      hipMemcpyDeviceToDevice, s);
-        if (e != hipSuccess) return fail(m, KDEC_EHIP, hipGetErrorString(e));
+        m->part[0].n0 = 0;
+        m->part[0].n = m->parts == 2 ? N - N / 2 : N;
+        m->part[1].n0 = m->part[0].n;
+        m->part[1].n = N - m->part[0].n;
+        if (m->parts == 2 && (hipEventRecord(m->ev_split, ms) != hipSuccess ||
+                              hipStreamWaitEvent(m->ctx2->stream, m->ev_split, 0) != hipSuccess))
+            return fail(m, KDEC_EHIP, "kdec_model_forward: fork of the second part");
+        const int n_dec = m->n_decode;
+        int alen = 0;
+        kdec_model_lengths(m, T, nullptr, nullptr, &alen);
+        for (int pi = 0; pi < m->parts; ++pi) {
+            kdec_model::Part& pt = m->part[pi];
+            bt::set_runtime(pt.ctx);
+            const int n0 = pt.n0, n = pt.n;
+            auto rows = [&](const float* base, int cols, long ld) {
+                return Tensor::view(Device::HIP, const_cast<float*>(base) + static_cast<long>(n0) * ld, n, cols,
+                                    bt::Dtype::FP32, ld);
+            };
+            auto gv = [&](const Tensor& buf, int off, int C) {
+                Tensor t = rows(static_cast<const float*>(buf.data) + off, C, R);
+                t.storage = buf.storage;
+                return t;
+            };
+            pt.bbaff.assign(1 + n_dec, bd::BlockAffines{});
+            pt.naff.assign(m->n_ups, bd::ResBlock1Affines{});
+            pt.raff.assign(static_cast<std::size_t>(m->n_ups) * m->n_kernels, bd::ResBlock1Affines{});
+            std::size_t u = 0;
+            auto pair = [&](Tensor& g, Tensor& bb) {
+                const auto& un = m->units[u++];
+                g = gv(m->gb, un.offset, un.C);
+                bb = gv(m->gb, un.offset + un.C, un.C);
+            };
+            for (auto& a : pt.bbaff) { pair(a.g1, a.b1); pair(a.g2, a.b2); }
+            auto rb = [&](bd::ResBlock1Affines& a) {
+                for (int j = 0; j < 3; ++j) pair(a.g1[j], a.b1[j]);
+                for (int j = 0; j < 3; ++j) pair(a.g2[j], a.b2[j]);
+            };
+            for (auto& a : pt.naff) rb(a);
+            for (auto& a : pt.raff) rb(a);
+            Tensor har_p = rows(static_cast<const float*>(m->har.data), har_cols, har_cols);
+            har_p.storage = m->har.storage;
+            bd::decoder_backbone_forward_train(m->bb, rows(asr, m->asr_dim * T, static_cast<long>(m->asr_dim) * T),
+                                               rows(F0, 2 * T, 2 * T), rows(Nn, 2 * T, 2 * T), T, pt.bbaff, 1e-5f,
+                                               pt.gen_in, pt.bbc);
+            const int init_C = m->dec_out[n_dec - 1];
+            const int L_gen = pt.gen_in.cols / init_C;
+            Tensor out;
+            // the generator waits for har itself, after stage 0's upsampling
+            pt.genc.har_ready = forked ? static_cast<void*>(m->ev_join) : nullptr;
+            bd::generator_forward_train(m->gen, pt.gen_in, L_gen, har_p, frames, pt.naff, pt.raff, out, pt.genc);
+            hipStream_t ps = static_cast<hipStream_t>(kdec_get_stream(pt.ctx));
+            if (pt.genc.har_ready) {  // no noise conv consumed it: join here
+                pt.genc.har_ready = nullptr;
+                if (hipStreamWaitEvent(ps, m->ev_join, 0) != hipSuccess)
+                    return fail(m, KDEC_EHIP, "kdec_model_forward: join");
+            }
+            if (out.cols != alen) return fail(m, KDEC_EINVAL, "kdec_model_forward: audio length mismatch");
+            hipError_t e = hipMemcpyAsync(audio + static_cast<long>(n0) * alen, out.data,
+                                          static_cast<size_t>(n) * alen * sizeof(float), hipMemcpyDeviceToDevice, ps);
+            if (e != hipSuccess) return fail(m, KDEC_EHIP, hipGetErrorString(e));
+        }
+        bt::set_runtime(m->ctx);
+        if (m->parts == 2 && (hipEventRecord(m->ev_part1, m->ctx2->stream) != hipSuccess ||
+                              hipStreamWaitEvent(ms, m->ev_part1, 0) != hipSuccess))
+            return fail(m, KDEC_EHIP, "kdec_model_forward: join of the second part");
     } catch (const std::exception& e) {
         return fail(m, KDEC_EINVAL, e.what());
     }
@@ -641,47 +719,78 @@ int kdec_model_backward(kdec_model* m, const float* daudio, int wgrad, int dalph
         const int S = m->style_dim;
         int alen = 0;
         kdec_model_lengths(m, m->T, nullptr, nullptr, &alen);
-        Tensor dA = Tensor::view(Device::HIP, const_cast<float*>(daudio), N, alen);
         const bd::WeightGrads* wg = wgrad ? (dalpha ? &m->wg_all : &m->wg_conv) : (dalpha ? &m->wg_alpha : nullptr);
+        const bd::WeightGrads* wg2 =
+            wgrad ? (dalpha ? &m->wg_all2 : &m->wg_conv2) : (dalpha ? &m->wg_alpha2 : nullptr);
         // affine grads land in place in the packed dgb buffer
         m->dgb = Tensor::empty_on(Device::HIP, N, R);
-        auto gv = [&](int off, int C) {
-            Tensor t = Tensor::view(Device::HIP, static_cast<float*>(m->dgb.data) + off, N, C, bt::Dtype::FP32, R);
-            t.storage = m->dgb.storage;
-            return t;
-        };
-        m->dbbaff.assign(1 + m->n_decode, bd::BlockAffines{});
-        m->dnaff.assign(m->n_ups, bd::ResBlock1Affines{});
-        m->draff.assign(static_cast<std::size_t>(m->n_ups) * m->n_kernels, bd::ResBlock1Affines{});
-        std::size_t u = 0;
-        auto pair = [&](Tensor& g, Tensor& bb) {
-            const auto& un = m->units[u++];
-            g = gv(un.offset, un.C);
-            bb = gv(un.offset + un.C, un.C);
-        };
-        for (auto& a : m->dbbaff) { pair(a.g1, a.b1); pair(a.g2, a.b2); }
-        auto rb = [&](bd::ResBlock1Affines& a) {
-            for (int j = 0; j < 3; ++j) pair(a.g1[j], a.b1[j]);
-            for (int j = 0; j < 3; ++j) pair(a.g2[j], a.b2[j]);
-        };
-        for (auto& a : m->dnaff) rb(a);
-        for (auto& a : m->draff) rb(a);
-
-        Tensor dGenIn;
-        // conv weight grads overlap the input-grad chain on the side stream
-        struct LaneGuard {
-            explicit LaneGuard(kdec_ctx* side) { bd::set_wgrad_lane(side); }
-            ~LaneGuard() {
+        hipStream_t ms = static_cast<hipStream_t>(kdec_get_stream(m->ctx));
+        // Both parts' backwards run concurrently, each with its conv weight
+        // grads on its own side stream; part 1's weight grads go to gbuf2
+        // (cleared first), which gbuf adds once both are done.
+        if (m->parts == 2 && (hipEventRecord(m->ev_split, ms) != hipSuccess ||
+                              hipStreamWaitEvent(m->ctx2->stream, m->ev_split, 0) != hipSuccess))
+            return fail(m, KDEC_EHIP, "kdec_model_backward: fork of the second part");
+        struct LaneReset {  // the weight-grad lane never outlives this call
+            ~LaneReset() {
                 try {
                     bd::join_wgrad_lane();
                     bd::set_wgrad_lane(nullptr);
                 } catch (...) {
                 }
             }
-        } lane(wg && m->overlap ? m->side : nullptr);
-        bd::generator_backward(m->gen, m->genc, m->naff, m->raff, dA, dGenIn, m->dnaff, m->draff, wg);
-        bd::decoder_backbone_backward(m->bb, m->bbc, m->bbaff, dGenIn, 1e-5f, m->dbbaff, wg);
-        bd::join_wgrad_lane();
+        } lane_reset;
+        for (int pi = 0; pi < m->parts; ++pi) {
+            kdec_model::Part& pt = m->part[pi];
+            bt::set_runtime(pt.ctx);
+            const bd::WeightGrads* pwg = pi == 0 ? wg : wg2;
+            if (pi == 1 && pwg)
+                if (int rc = check(m, kdec_fill(pt.ctx, static_cast<float*>(m->gbuf2.data), m->total, 0.0f)))
+                    return rc;
+            bd::set_wgrad_lane(pwg && m->overlap ? (pi == 0 ? m->side : m->side2) : nullptr);
+            const int n0 = pt.n0, n = pt.n;
+            auto gv = [&](int off, int C) {
+                Tensor t = Tensor::view(Device::HIP, static_cast<float*>(m->dgb.data) + static_cast<long>(n0) * R + off,
+                                        n, C, bt::Dtype::FP32, R);
+                t.storage = m->dgb.storage;
+                return t;
+            };
+            pt.dbbaff.assign(1 + m->n_decode, bd::BlockAffines{});
+            pt.dnaff.assign(m->n_ups, bd::ResBlock1Affines{});
+            pt.draff.assign(static_cast<std::size_t>(m->n_ups) * m->n_kernels, bd::ResBlock1Affines{});
+            std::size_t u = 0;
+            auto pair = [&](Tensor& g, Tensor& bb) {
+                const auto& un = m->units[u++];
+                g = gv(un.offset, un.C);
+                bb = gv(un.offset + un.C, un.C);
+            };
+            for (auto& a : pt.dbbaff) { pair(a.g1, a.b1); pair(a.g2, a.b2); }
+            auto rb = [&](bd::ResBlock1Affines& a) {
+                for (int j = 0; j < 3; ++j) pair(a.g1[j], a.b1[j]);
+                for (int j = 0; j < 3; ++j) pair(a.g2[j], a.b2[j]);
+            };
+            for (auto& a : pt.dnaff) rb(a);
+            for (auto& a : pt.draff) rb(a);
+            Tensor dA = Tensor::view(Device::HIP, const_cast<float*>(daudio) + static_cast<long>(n0) * alen, n, alen);
+            Tensor dGenIn;
+            bd::generator_backward(m->gen, pt.genc, pt.naff, pt.raff, dA, dGenIn, pt.dnaff, pt.draff, pwg);
+            bd::decoder_backbone_backward(m->bb, pt.bbc, pt.bbaff, dGenIn, 1e-5f, pt.dbbaff, pwg);
+            // the part's stream waits for its lane; the lane is released here,
+            // before the next part sets its own
+            bd::join_wgrad_lane();
+            bd::set_wgrad_lane(nullptr);
+        }
+        bt::set_runtime(m->ctx);
+        if (m->parts == 2) {
+            if (hipEventRecord(m->ev_part1, m->ctx2->stream) != hipSuccess ||
+                hipStreamWaitEvent(ms, m->ev_part1, 0) != hipSuccess)
+                return fail(m, KDEC_EHIP, "kdec_model_backward: join of the second part");
+            if (wg2)
+                if (int rc = check(m, kdec_axpby(m->ctx, 1.0f, static_cast<const float*>(m->gbuf.data), m->total,
+                                                 1.0f, static_cast<const float*>(m->gbuf2.data), m->total,
+                                                 static_cast<float*>(m->gbuf.data), m->total, 1, m->total)))
+                    return rc;
+        }
         // style projection adjoint over every unit
         const long fc_off = m->params.at(m->units[0].name + ".fc.weight").offset;
         const long fcb_off = m->params.at(m->units[0].name + ".fc.bias").offset;
@@ -718,11 +827,15 @@ int kdec_model_infer(kdec_model* m, int N, int T, const float* asr, const float*
                      const float* style, const float* har, float* audio) {
     if (!m) return KDEC_EINVAL;
     // the training forward with every block's cache dropped once the block is done
-    m->bbc.keep = false;
-    m->genc.keep = false;
+    for (auto& pt : m->part) {
+        pt.bbc.keep = false;
+        pt.genc.keep = false;
+    }
     const int rc = kdec_model_forward(m, N, T, asr, F0, Nn, style, har, audio);
-    m->bbc.keep = true;
-    m->genc.keep = true;
+    for (auto& pt : m->part) {
+        pt.bbc.keep = true;
+        pt.genc.keep = true;
+    }
     m->N = 0;  // nothing to differentiate
     return rc;
 }
@@ -795,9 +908,32 @@ int kdec_model_set_overlap(kdec_model* m, int on) {
     return KDEC_OK;
 }
 
+int kdec_model_set_batch_split(kdec_model* m, int on) {
+    if (!m) return KDEC_EINVAL;
+    m->split = on != 0;
+    return KDEC_OK;
+}
+
 const float* kdec_model_har(const kdec_model* m) { return m ? static_cast<const float*>(m->har.data) : nullptr; }
 const float* kdec_model_gen_in(const kdec_model* m) {
-    return m ? static_cast<const float*>(m->gen_in.data) : nullptr;
+    if (!m || m->parts == 0) return nullptr;
+    if (m->parts == 1) return static_cast<const float*>(m->part[0].gen_in.data);
+    // both parts' rows in one (N, cols) buffer, assembled on the model stream
+    try {
+        bt::set_runtime(m->ctx);
+        const Tensor& a = m->part[0].gen_in;
+        const Tensor& b = m->part[1].gen_in;
+        m->gen_in_all = Tensor::empty_on(Device::HIP, m->N, a.cols);
+        hipStream_t s = static_cast<hipStream_t>(kdec_get_stream(m->ctx));
+        if (hipMemcpyAsync(m->gen_in_all.data, a.data, a.size() * sizeof(float), hipMemcpyDeviceToDevice, s) !=
+                hipSuccess ||
+            hipMemcpyAsync(static_cast<float*>(m->gen_in_all.data) + a.size(), b.data, b.size() * sizeof(float),
+                           hipMemcpyDeviceToDevice, s) != hipSuccess)
+            return nullptr;
+        return static_cast<const float*>(m->gen_in_all.data);
+    } catch (const std::exception&) {
+        return nullptr;
+    }
 }
 
 // ─── the producer step (KokoroDecodePrep) ───────────────────────────────────
@@ -874,69 +1010,86 @@ int kdec_model_leaky_site_count(const kdec_model* m) {
 }
 
 long kdec_model_leaky_size(kdec_model* m, int site) {
-    if (!m || m->N == 0 || m->genc.stages.empty() || site < 0 || site >= kdec_model_leaky_site_count(m)) {
+    if (!m || m->N == 0 || m->parts == 0 || m->part[0].genc.stages.empty() || site < 0 ||
+        site >= kdec_model_leaky_site_count(m)) {
         if (m) fail(m, KDEC_EINVAL, "kdec_model_leaky_size: no training forward or site out of range");
         return -1;
     }
     const int n_blocks = 1 + m->n_decode;
-    if (site < 2 * n_blocks) {
-        const int b = site / 2;
-        const bd::AdainResBlkCache& c = b == 0 ? m->bbc.encode : m->bbc.decode[b - 1];
-        const brosoundml::AdainResBlk1dWeights& w = b == 0 ? m->bb.encode : m->bb.decode[b - 1];
-        return site % 2 ? static_cast<long>(m->N) * w.channels_out * c.L_out
-                        : static_cast<long>(m->N) * w.channels_in * c.L_in;
+    long total = 0;
+    for (int pi = 0; pi < m->parts; ++pi) {
+        const kdec_model::Part& pt = m->part[pi];
+        if (site < 2 * n_blocks) {
+            const int b = site / 2;
+            const bd::AdainResBlkCache& c = b == 0 ? pt.bbc.encode : pt.bbc.decode[b - 1];
+            const brosoundml::AdainResBlk1dWeights& w = b == 0 ? m->bb.encode : m->bb.decode[b - 1];
+            total += site % 2 ? static_cast<long>(pt.n) * w.channels_out * c.L_out
+                              : static_cast<long>(pt.n) * w.channels_in * c.L_in;
+        } else {
+            const Tensor& t =
+                site < 2 * n_blocks + m->n_ups ? pt.genc.stages[site - 2 * n_blocks].x_in : pt.genc.head.x_pre;
+            total += static_cast<long>(t.size());
+        }
     }
-    const Tensor& t = site < 2 * n_blocks + m->n_ups ? m->genc.stages[site - 2 * n_blocks].x_in : m->genc.head.x_pre;
-    return static_cast<long>(t.size());
+    return total;
 }
 
 int kdec_model_leaky_input(kdec_model* m, int site, float* host, long n) {
     if (!m || !host) return KDEC_EINVAL;
-    if (m->N == 0 || m->genc.stages.empty())
+    if (m->N == 0 || m->parts == 0 || m->part[0].genc.stages.empty())
         return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: no training forward to inspect");
     const int n_blocks = 1 + m->n_decode;
     if (site < 0 || site >= kdec_model_leaky_site_count(m))
         return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: site out of range");
+    const long want = kdec_model_leaky_size(m, site);
+    if (n != want)
+        return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: site holds " + std::to_string(want) + " values, not " +
+                                        std::to_string(n));
     try {
-        bt::set_runtime(m->ctx);
-        const int N = m->N;
-        Tensor t;
-        if (site < 2 * n_blocks) {
-            // an AdaIN residual block's norm output, recomputed from the cached
-            // input and statistics as the backward recomputes it
-            const int b = site / 2;
-            const bool second = site % 2;
-            const bd::AdainResBlkCache& c = b == 0 ? m->bbc.encode : m->bbc.decode[b - 1];
-            const brosoundml::AdainResBlk1dWeights& w = b == 0 ? m->bb.encode : m->bb.decode[b - 1];
-            const bd::BlockAffines& a = m->bbaff[b];
-            const Tensor& x = second ? c.conv1_out : c.x;
-            const Tensor& st = second ? c.x_seq2 : c.x_seq1;
-            const Tensor& g = second ? a.g2 : a.g1;
-            const Tensor& be = second ? a.b2 : a.b1;
-            const int C = second ? w.channels_out : w.channels_in;
-            const int L = second ? c.L_out : c.L_in;
-            if (!x.data || !st.data) return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: no cache for this site");
-            t = Tensor::empty_on(Device::HIP, N, C * L);
-            const long gbs = N == 1 ? 0 : g.row_stride();
-            if (int rc = check(m, kdec_adain_act_fwd(m->ctx, static_cast<const float*>(x.data), x.row_stride(),
-                                                     static_cast<const float*>(st.data),
-                                                     static_cast<const float*>(g.data),
-                                                     static_cast<const float*>(be.data), gbs, KDEC_ACT_NONE, 0.0f,
-                                                     nullptr, static_cast<float*>(t.data), t.row_stride(), nullptr,
-                                                     0, N, C, L)))
-                return rc;
-        } else if (site < 2 * n_blocks + m->n_ups) {
-            t = m->genc.stages[site - 2 * n_blocks].x_in;  // the stage input (leaky 0.1)
-        } else {
-            t = m->genc.head.x_pre;  // the spectral head input (leaky 0.01)
+        long at = 0;
+        for (int pi = 0; pi < m->parts; ++pi) {
+            kdec_model::Part& pt = m->part[pi];
+            bt::set_runtime(pt.ctx);
+            const int N = pt.n;
+            Tensor t;
+            if (site < 2 * n_blocks) {
+                // an AdaIN residual block's norm output, recomputed from the
+                // cached input and statistics as the backward recomputes it
+                const int b = site / 2;
+                const bool second = site % 2;
+                const bd::AdainResBlkCache& c = b == 0 ? pt.bbc.encode : pt.bbc.decode[b - 1];
+                const brosoundml::AdainResBlk1dWeights& w = b == 0 ? m->bb.encode : m->bb.decode[b - 1];
+                const bd::BlockAffines& a = pt.bbaff[b];
+                const Tensor& x = second ? c.conv1_out : c.x;
+                const Tensor& st = second ? c.x_seq2 : c.x_seq1;
+                const Tensor& g = second ? a.g2 : a.g1;
+                const Tensor& be = second ? a.b2 : a.b1;
+                const int C = second ? w.channels_out : w.channels_in;
+                const int L = second ? c.L_out : c.L_in;
+                if (!x.data || !st.data)
+                    return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: no cache for this site");
+                t = Tensor::empty_on(Device::HIP, N, C * L);
+                const long gbs = N == 1 ? 0 : g.row_stride();
+                if (int rc = check(m, kdec_adain_act_fwd(pt.ctx, static_cast<const float*>(x.data), x.row_stride(),
+                                                         static_cast<const float*>(st.data),
+                                                         static_cast<const float*>(g.data),
+                                                         static_cast<const float*>(be.data), gbs, KDEC_ACT_NONE, 0.0f,
+                                                         nullptr, static_cast<float*>(t.data), t.row_stride(),
+                                                         nullptr, 0, N, C, L)))
+                    return rc;
+            } else if (site < 2 * n_blocks + m->n_ups) {
+                t = pt.genc.stages[site - 2 * n_blocks].x_in;  // the stage input (leaky 0.1)
+            } else {
+                t = pt.genc.head.x_pre;  // the spectral head input (leaky 0.01)
+            }
+            if (!t.data) return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: no cache for this site");
+            const std::vector<float> h = t.to_host_vector();
+            std::copy(h.begin(), h.end(), host + at);
+            at += static_cast<long>(h.size());
         }
-        if (!t.data) return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: no cache for this site");
-        if (n != static_cast<long>(t.size()))
-            return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: site holds " + std::to_string(t.size()) +
-                                            " values, not " + std::to_string(n));
-        const std::vector<float> h = t.to_host_vector();
-        std::copy(h.begin(), h.end(), host);
+        bt::set_runtime(m->ctx);
     } catch (const std::exception& e) {
+        bt::set_runtime(m->ctx);
         return fail(m, KDEC_EHIP, e.what());
     }
     return KDEC_OK;
@@ -975,7 +1128,7 @@ int kdec_dlora_create(kdec_model* m, int rank, float scale, unsigned long long s
 int kdec_dlora_destroy(kdec_dlora* d) {
     if (!d) return KDEC_EINVAL;
     bt::set_runtime(d->m->ctx);
-    hipStreamSynchronize(static_cast<hipStream_t>(kdec_get_stream(d->m->ctx)));
+    (void)hipStreamSynchronize(static_cast<hipStream_t>(kdec_get_stream(d->m->ctx)));
     delete d;
     return KDEC_OK;
 }

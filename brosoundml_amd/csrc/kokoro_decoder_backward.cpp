@@ -366,14 +366,6 @@ void copy_channels(Tensor& dst, int c0, const Tensor& x, int C, int L) {
        "cat_channels");
 }
 
-Tensor hann_periodic_dev(int n) {
-    std::vector<float> w(static_cast<std::size_t>(n));
-    constexpr float kTwoPi = 6.28318530717958647692f;
-    for (int i = 0; i < n; ++i)
-        w[i] = 0.5f - 0.5f * std::cos(kTwoPi * static_cast<float>(i) / static_cast<float>(n));
-    return Tensor::from_host_on(Device::HIP, w.data(), 1, n);
-}
-
 }  // namespace
 
 // ─── nn-module forwards used by the atoms ───────────────────────────────────
@@ -920,7 +912,11 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
         x = xs;
         L = L_x;
     }
-    cache.window = hann_periodic_dev(gen.win_size);
+    // an empty window: the spectral kernels form the periodic Hann of
+    // kokoro_decoder_backward.cpp:580-588 themselves (hann_at, the same float
+    // formula), so no host-built window is uploaded (an upload would block
+    // the host until the stream drains)
+    cache.window = Tensor();
     spectral_head_forward_train(gen.conv_post, x, gen.ups_C_out[U - 1], L, cache.window, gen.n_fft, gen.hop_size,
                                 gen.win_size, audio, cache.head);
     if (!cache.keep) cache.head = SpectralHeadCache{};

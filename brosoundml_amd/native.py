@@ -239,6 +239,11 @@ class Model:
         stream; False: every launch on the context's stream in program order."""
         self._c(self.ctx.L.kdec_model_set_overlap(self.h, int(on)))
 
+    def set_batch_split(self, on: bool):
+        """True: with overlap on, forwards and backwards of N >= 2 run as two
+        half-batch chains on two streams; False (default): one chain."""
+        self._c(self.ctx.L.kdec_model_set_batch_split(self.h, int(on)))
+
     # ─── DecoderLora adapters (kdec_model_lora_*) ───
     def lora_enable(self, rank: int, scale: float):
         self.lora_rank = rank

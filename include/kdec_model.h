@@ -130,6 +130,18 @@ int kdec_model_decode_back_half_cancellable(kdec_model* m, int N, int T, const f
  * launch on the context's stream, in program order. Results are identical
  * either way (every reduction sums in a fixed order). */
 int kdec_model_set_overlap(kdec_model* m, int on);
+/* on = 1 (with overlap on and N >= 2): forwards run the batch as two
+ * halves (rows [0, N - N/2) and the rest), each a whole backbone + generator
+ * chain on its own stream, concurrently, and so do their backwards (the
+ * second half's conv weight grads accumulate in a second buffer that is
+ * added at the end). 0 (the default) keeps one chain for the whole batch.
+ * On one MI355X at B = 8, T = 512 the halves shorten the forward and the
+ * backward without weight grads, and lengthen the backward with them (the
+ * concurrent weight-grad GEMMs contend), so the training step keeps one
+ * chain. Results agree either way to the rounding of the GEMMs' split
+ * choices. No counterpart in the reference (its decoder runs one utterance
+ * at a time); the per-utterance work is unchanged. */
+int kdec_model_set_batch_split(kdec_model* m, int on);
 /* DecoderLora's adapters on every AdaIN unit (the adapter contract of
  * decoder_lora.h:63-77; the adapter_fwd / adapter_bwd sequence of
  * decoder_lora.cpp:184-207): (gamma, beta) = fc(style) + scale * B_i (g *

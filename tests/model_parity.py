@@ -62,15 +62,16 @@ def oracle_har_of(cfg, params, F0):
 
 
 def run_pair(ctx, cfg, N, T, tag, wgrad=True, dalpha=True, lora=None, unvoiced=0.0, params=None,
-             oracle_har=True, kinks=True):
+             oracle_har=True, kinks=True, split=False):
     """Forward + backward on both sides. oracle_har: both sides take the
     oracle's harmonic-source output (the model's own is compared separately,
     since the atan2 of a near-empty STFT bin is noise in any float
     evaluation and the phase channels enter the noise convs at full
-    weight)."""
+    weight). split: the model's two half-batch chains, or one (the default)."""
     import torch
     from brosoundml_amd import native
     m = native.Model(ctx, cfg)
+    m.set_batch_split(split)
     shapes = m.param_shapes()
     om = O.OracleModel(cfg)
     assert shapes == om.param_shapes()

@@ -104,8 +104,8 @@ def test_in_model_harmonic_source_matches_op(ctx):
 
 def test_single_stream_equals_overlapped(ctx):
     # kdec_model_set_overlap(0) keeps every launch on one stream; with the
-    # default two-stream schedule the waveform, d(style) and every grad are
-    # the same bits (all reductions sum in a fixed order).
+    # two-stream schedule (one chain for the batch) the waveform, d(style) and
+    # every grad are the same bits (all reductions sum in a fixed order).
     from brosoundml_amd import native
     cfg, N, T = C.SMALL, 2, 6
     m = native.Model(ctx, cfg)
@@ -128,6 +128,20 @@ def test_single_stream_equals_overlapped(ctx):
     np.testing.assert_array_equal(res[0][1], res[1][1])
     for n in shapes:
         np.testing.assert_array_equal(res[0][2][n], res[1][2][n], err_msg=n)
+
+
+@pytest.mark.parametrize("split", [True, False])
+def test_batch_split_vs_oracle(ctx, split):
+    # kdec_model_set_batch_split(1) runs a batch of N >= 2 as two half-batch
+    # chains (rows [0, N - N//2) and the rest) on two streams, forwards and
+    # backwards concurrent, the second half's weight grads in a second buffer
+    # added at the end. With N = 3 (parts of 2 and 1 rows) and with one chain
+    # for the whole batch, every output against the oracle at the usual bars
+    # (the leaky kinks reconciled from the model's own site inputs, which
+    # the two schedules may round to opposite sides of zero).
+    r = run_pair(ctx, C.SMALL, 3, 6, "gm.split", split=split)
+    report = check_pair(r)
+    print(f"split={split}: " + ", ".join(f"{k}={v}" for k, v in report.items()), flush=True)
 
 
 def test_inference_forwards(ctx):
