@@ -117,6 +117,15 @@ struct GemmArgs {
         double* part;
         int nch;             // partial slots per row: 2 per q-tile
     } ad;
+    // Instance-norm statistics epilogue (forward convs whose output feeds an
+    // AdaIN; off when part is null, needs beta = 0): beside Y, per row and
+    // tile half part[((n*C_out + m)*nch + 2*q_tile + half)*3 + {0, 1, 2}] =
+    // (count, mean, sum of squared deviations from that mean) of the stored
+    // values.
+    struct {
+        double* part;
+        int nch;
+    } fs;
 };
 
 // Logical block order with consecutive ids on one XCD: the dispatcher deals
@@ -401,6 +410,89 @@ __device__ inline void store_tile_adain(const GemmArgs& g, const TileGeo& T, con
     }
 }
 
+// Lane `src`'s float, read by every lane.
+__device__ inline float lane_value(float v, int src) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+}
+
+// Whole-tile epilogue of a forward conv whose output rows feed an instance
+// norm (g.fs): Y stored as store_tile stores it (bias, residual, scale;
+// beta = 0), and per row and wave (64 columns) the count, mean and sum of
+// squared deviations of the stored values go to slot 2 * q_tile + wn: the
+// row sums by a transpose-reduce, the means read back from the two lanes
+// that hold them, then the squared deviations likewise. Every lane takes part
+// in the cross-lane steps; positions past n_q add nothing.
+__device__ inline void store_tile_stats(const GemmArgs& g, const TileGeo& T, f32x16 (&acc)[2][2], int wm, int wn,
+                                        int hi, int l32) {
+    const int b = T.b, n_q = T.n_q, m0 = T.m0, q0 = T.q0;
+    const int rowb = g.C_out * g.L_y * 4;
+    const float* Rb = g.R ? g.R + static_cast<long>(b) * g.r_bs : nullptr;
+    const __amdgpu_buffer_rsrc_t yr = uniform_rsrc(g.Y + static_cast<long>(b) * g.y_bs, rowb);
+    const __amdgpu_buffer_rsrc_t rr = uniform_rsrc(Rb ? Rb : g.Y, Rb ? rowb : 0);
+    const __amdgpu_buffer_rsrc_t br = uniform_rsrc(g.bias ? g.bias : g.Y, g.bias ? g.C_out * 4 : 0);
+    const int mrow = m0 + wm * 64 + 4 * hi;
+    const int cnt = min(max(n_q - (q0 + wn * 64), 0), 64);  // wave-uniform
+    const float inv = cnt > 0 ? 1.0f / static_cast<float>(cnt) : 0.0f;
+    const int slot = (q0 / BN) * 2 + wn;
+#pragma unroll
+    for (int tm = 0; tm < 2; ++tm) {
+        float sx[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sx[e] = 0.0f;
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn) {
+            const int q = q0 + wn * 64 + tn * 32 + l32;
+            const bool qin = q < n_q;
+            const int vo = (mrow * g.L_y + q) * 4;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int dm = tm * 32 + 8 * (e >> 2) + (e & 3);
+                const int o = vo + dm * g.L_y * 4;
+                float v = acc[tm][tn][e];
+                if (g.bias)
+                    v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(br, (mrow + dm) * 4, 0, 0));
+                if (Rb && qin) v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, o, 0, 0));
+                v *= g.scale;
+                if (qin) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), yr, o, 0, 0);
+                v = qin ? v : 0.0f;
+                acc[tm][tn][e] = v;
+                sx[e] += v;
+            }
+        }
+        reduce16(sx, l32);  // lanes 2e, 2e + 1 of each half: the sum of row e
+        const float my_mean = sx[0] * inv;
+        float mean[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const float lo = lane_value(sx[0], 2 * e), up = lane_value(sx[0], 32 + 2 * e);
+            mean[e] = (hi ? up : lo) * inv;
+        }
+        float sq[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sq[e] = 0.0f;
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn) {
+            const bool qin = q0 + wn * 64 + tn * 32 + l32 < n_q;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float dv = acc[tm][tn][e] - mean[e];
+                sq[e] += qin ? dv * dv : 0.0f;
+            }
+        }
+        reduce16(sq, l32);
+        if ((l32 & 1) == 0) {
+            const int e = l32 >> 1;
+            const int m = m0 + wm * 64 + tm * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
+            if (m < g.C_out) {
+                double* pp = g.fs.part + ((static_cast<long>(b) * g.C_out + m) * g.fs.nch + slot) * 3;
+                pp[0] = cnt;
+                pp[1] = my_mean;
+                pp[2] = sq[0];
+            }
+        }
+    }
+}
+
 // Grid of 8 * (full_per_xcd + parts_per_xcd) blocks. Two LDS stages;
 // weights arrive packed chunk-major (row ((chunk*k + t)*CK + c_local)), so a
 // chunk's KR = CK*k rows are one contiguous slab of the panel.
@@ -464,9 +556,7 @@ void conv_gemm(GemmArgs g) {
                                              smem + sb + pr * 256, 16, 0, 0);
     };
     auto issue = [&](int ch, int sb) {
-#ifndef CG_XFIRST
         issue_a(ch, sb);
-#endif
         if (x4) {
             const int seg4 = span_p >> 8;
             for (int it = wave; it < CK * seg4; it += 4) {
@@ -478,9 +568,6 @@ void conv_gemm(GemmArgs g) {
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + KR * BM + r * span_p + sg * 256, 16,
                                                              static_cast<int>(off), 0, 0, 0);
             }
-#ifdef CG_XFIRST
-            issue_a(ch, sb);
-#endif
             return;
         }
         for (int it = wave; it < nitems; it += 4) {
@@ -493,9 +580,6 @@ void conv_gemm(GemmArgs g) {
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + KR * BM + r * span_p + sg * 64, 4,
                                                          static_cast<int>(off), 0, 0, 0);
         }
-#ifdef CG_XFIRST
-        issue_a(ch, sb);
-#endif
     };
 
     f32x16 acc[2][2];
@@ -589,7 +673,14 @@ void conv_gemm(GemmArgs g) {
 #ifndef CGQ_PF
 #define CGQ_PF 2
 #endif
-template <int CK, int KT>
+// EPI picks the whole tiles' epilogue at compile time (split tiles always
+// store partials): QEPI_STORE the plain store, QEPI_ADAIN_BWD the AdaIN
+// backward row sums (store_tile_adain), QEPI_STATS the instance-norm moments
+// (store_tile_stats). One epilogue per instantiation keeps the live ranges of
+// the others out of the k-loop's register allocation.
+enum { QEPI_STORE = 0, QEPI_ADAIN_BWD = 1, QEPI_STATS = 2 };
+
+template <int CK, int KT, int EPI>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(CGQ_WPE)))
 void conv_gemm_q(GemmArgs g) {
     constexpr int S = CK * KT / 2;  // k-steps per chunk
@@ -716,23 +807,29 @@ void conv_gemm_q(GemmArgs g) {
                 acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
                 acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
                 acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
-#ifndef CGQ_NOSCHED
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 if (j == 0 && gq + 1 < Q) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
                 if (u + PF < S) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
                 __builtin_amdgcn_sched_barrier(0);  // nothing crosses into the next step
-#endif
             }
         }
         __builtin_amdgcn_s_waitcnt(0);  // this wave's staging loads landed
         __syncthreads();
     }
 
-    if (part < 0 && g.ad.part)  // uniform per block
-        store_tile_adain(g, T, acc, wm, wn, hi, l32, smem);
-    else
-        store_tile(g, T, tile, part, acc, wm, wn, hi, l32);
+    if constexpr (EPI == QEPI_ADAIN_BWD) {
+        if (part < 0) {  // uniform per block
+            store_tile_adain(g, T, acc, wm, wn, hi, l32, smem);
+            return;
+        }
+    } else if constexpr (EPI == QEPI_STATS) {
+        if (part < 0) {
+            store_tile_stats(g, T, acc, wm, wn, hi, l32);
+            return;
+        }
+    }
+    store_tile(g, T, tile, part, acc, wm, wn, hi, l32);
 }
 
 // Stride-1 correlation (conv forward, conv input-grad, each transposed-conv
@@ -983,6 +1080,106 @@ __global__ __launch_bounds__(256) void tile_reduce_adain(GemmArgs g) {
         pp[3] = 0.0;
         pp[4] = 0.0;
         pp[5] = 0.0;
+    }
+}
+
+// Split tiles of a forward conv with the statistics epilogue: the parts
+// summed in order and stored as tile_reduce stores them, then per row the
+// count, mean and sum of squared deviations over the tile's columns (the 32
+// lanes of a half-wave hold one row's 128 columns) into slot 2 * q_tile, an
+// empty record into the other. Grid (BM * BN / 1024, split_tiles) x 256.
+__global__ __launch_bounds__(256) void tile_reduce_stats(GemmArgs g) {
+    const int ti = blockIdx.y;
+    TileGeo T;
+    decode_tile(g, g.full_tiles + ti, T);
+    if (T.q0 >= T.n_q) return;  // uniform per block
+    const int e4 = blockIdx.x * blockDim.x + threadIdx.x;
+    const int l32 = threadIdx.x & 31;
+    const int m = T.m0 + e4 / (BN / 4), qb = T.q0 + (e4 % (BN / 4)) * 4;
+    const int cnt = min(T.n_q - T.q0, BN);
+    const float4* Pt = reinterpret_cast<const float4*>(g.P + static_cast<long>(ti) * g.fsplit * (BM * BN));
+    float vv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (m < g.C_out) {
+        float4 v = Pt[e4];
+        for (int sp = 1; sp < g.fsplit; ++sp) {
+            const float4 w = Pt[sp * (BM * BN / 4) + e4];
+            v.x += w.x;
+            v.y += w.y;
+            v.z += w.z;
+            v.w += w.w;
+        }
+        const float raw[4] = {v.x, v.y, v.z, v.w};
+        const float bs = g.bias ? g.bias[m] : 0.0f;
+        float* Yb = g.Y + static_cast<long>(T.b) * g.y_bs;
+        const float* Rb = g.R ? g.R + static_cast<long>(T.b) * g.r_bs : nullptr;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int q = qb + j;
+            if (q >= T.n_q) break;
+            const long yi = static_cast<long>(m) * g.L_y + q;
+            float x = raw[j] + bs;
+            if (Rb) x += Rb[yi];
+            x *= g.scale;
+            Yb[yi] = x;
+            vv[j] = x;
+        }
+    }
+    float s = vv[0] + vv[1] + vv[2] + vv[3];
+    s += xor_lane<16>(s);
+    s += xor_lane<8>(s);
+    s += xor_lane<4>(s);
+    s += xor_lane<2>(s);
+    s += xor_lane<1>(s);
+    const float mean = s / static_cast<float>(cnt);
+    float d = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float dv = vv[j] - mean;
+        d += qb + j < T.n_q ? dv * dv : 0.0f;
+    }
+    d += xor_lane<16>(d);
+    d += xor_lane<8>(d);
+    d += xor_lane<4>(d);
+    d += xor_lane<2>(d);
+    d += xor_lane<1>(d);
+    if (l32 == 0 && m < g.C_out) {
+        double* pp = g.fs.part + ((static_cast<long>(T.b) * g.C_out + m) * g.fs.nch + (T.q0 / BN) * 2) * 3;
+        pp[0] = cnt;
+        pp[1] = mean;
+        pp[2] = d;
+        pp[3] = 0.0;
+        pp[4] = 0.0;
+        pp[5] = 0.0;
+    }
+}
+
+// Merges (count, mean, sum of squared deviations) records (Chan et al.'s
+// pairwise update, in double): a at b's side, in place.
+__device__ inline void chan_merge(double& n, double& mean, double& m2, double nb, double mb, double m2b) {
+    if (nb <= 0.0) return;
+    const double nt = n + nb;
+    const double delta = mb - mean;
+    mean += delta * (nb / nt);
+    m2 += m2b + delta * delta * (n * nb / nt);
+    n = nt;
+}
+
+// stats[row] = (mean, 1 / sqrt(var + eps)) from the row's slot records: one
+// wave per row, lane j merging slots j, j + 64, ... in order, then the lanes
+// in a fixed tree.
+__global__ __launch_bounds__(64) void instnorm_fin_slots_k(const double* part, int nch, float eps, float2* stats) {
+    const int row = blockIdx.x;
+    const double* p = part + static_cast<long>(row) * nch * 3;
+    double n = 0.0, mean = 0.0, m2 = 0.0;
+    for (int j = threadIdx.x; j < nch; j += 64) chan_merge(n, mean, m2, p[3 * j], p[3 * j + 1], p[3 * j + 2]);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const double n2 = __shfl_xor(n, o, 64), mean2 = __shfl_xor(mean, o, 64), m22 = __shfl_xor(m2, o, 64);
+        chan_merge(n, mean, m2, n2, mean2, m22);
+    }
+    if (threadIdx.x == 0) {
+        const double var = n > 0.0 ? m2 / n : 0.0;
+        stats[row] = make_float2(static_cast<float>(mean), static_cast<float>(1.0 / sqrt(var + static_cast<double>(eps))));
     }
 }
 
@@ -1633,11 +1830,7 @@ size_t quad_lds_bytes(int CK, int k, int d) {
     const long S = static_cast<long>(CK) * k / 2, Q = (S + 3) / 4;
     const long span = BN + static_cast<long>(k - 1) * d;
     const long span_p = (span + 3 + 255) / 256 * 256;
-    size_t b = 2 * (static_cast<size_t>(Q) * 1024 + static_cast<size_t>(CK) * span_p) * sizeof(float);
-#ifdef CGQ_MIN_LDS
-    b = std::max(b, static_cast<size_t>(CGQ_MIN_LDS));
-#endif
-    return b;
+    return 2 * (static_cast<size_t>(Q) * 1024 + static_cast<size_t>(CK) * span_p) * sizeof(float);
 }
 
 #ifndef CGQ_CK3
@@ -1652,9 +1845,6 @@ size_t quad_lds_bytes(int CK, int k, int d) {
 // Channel chunk of conv_gemm_q for a k-tap stride-1 correlation, or 0 where
 // no instance exists (conv_gemm serves those).
 int pick_ck_q(int k) {
-#ifdef CGQ_OFF
-    return 0 * k;
-#endif
     switch (k) {
         case 3: return CGQ_CK3;
         case 7: return CGQ_CK7;
@@ -1663,21 +1853,28 @@ int pick_ck_q(int k) {
     }
 }
 
-template <int CK, int KT>
+template <int CK, int KT, int EPI>
 const void* conv_q_kernel() {
     static bool attr = false;
     if (!attr) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_gemm_q<CK, KT>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_gemm_q<CK, KT, EPI>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         attr = true;
     }
-    return reinterpret_cast<const void*>(&conv_gemm_q<CK, KT>);
+    return reinterpret_cast<const void*>(&conv_gemm_q<CK, KT, EPI>);
 }
 
-const void* conv_q_kernel_for(int CK, int k) {
-    if (k == 3 && CK == CGQ_CK3) return conv_q_kernel<CGQ_CK3, 3>();
-    if (k == 7 && CK == CGQ_CK7) return conv_q_kernel<CGQ_CK7, 7>();
-    if (k == 11 && CK == CGQ_CK11) return conv_q_kernel<CGQ_CK11, 11>();
+template <int CK, int KT>
+const void* conv_q_kernel_epi(int epi) {
+    if (epi == QEPI_ADAIN_BWD) return conv_q_kernel<CK, KT, QEPI_ADAIN_BWD>();
+    if (epi == QEPI_STATS) return conv_q_kernel<CK, KT, QEPI_STATS>();
+    return conv_q_kernel<CK, KT, QEPI_STORE>();
+}
+
+const void* conv_q_kernel_for(int CK, int k, int epi) {
+    if (k == 3 && CK == CGQ_CK3) return conv_q_kernel_epi<CGQ_CK3, 3>(epi);
+    if (k == 7 && CK == CGQ_CK7) return conv_q_kernel_epi<CGQ_CK7, 7>(epi);
+    if (k == 11 && CK == CGQ_CK11) return conv_q_kernel_epi<CGQ_CK11, 11>(epi);
     return nullptr;
 }
 
@@ -1794,7 +1991,9 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
               : (CK * kk > 64 || (CK * kk) % 2))
         return fail(ctx, KDEC_EINVAL, "conv: bad chunk geometry");
     const bool quad = g.quad != 0;
-    if (quad && (octet || g.n_phase > 1 || g.s != 1 || !conv_q_kernel_for(CK, g.k)))
+    const int epi = g.ad.part ? QEPI_ADAIN_BWD : g.fs.part ? QEPI_STATS : QEPI_STORE;
+    if (!quad && epi != QEPI_STORE) return fail(ctx, KDEC_EINVAL, "conv: fused epilogue needs the quad kernel");
+    if (quad && (octet || g.n_phase > 1 || g.s != 1 || !conv_q_kernel_for(CK, g.k, epi)))
         return fail(ctx, KDEC_EINVAL, "conv: bad quad geometry");
     const size_t lds = octet ? 2 * (static_cast<size_t>(g.G) * 1024 + 8 * static_cast<size_t>(g.span8)) * sizeof(float)
                      : quad ? quad_lds_bytes(CK, g.k, g.d)
@@ -1803,7 +2002,7 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
     if (static_cast<long>(g.C_in) * g.L_in * 4 > 0x7fffffffL)
         return fail(ctx, KDEC_EINVAL, "conv: input too large for one buffer descriptor");
     g.ybuf = (static_cast<long>(g.C_out) + BM) * g.L_y * 4 < 0x7fffffffL ? 1 : 0;
-    const void* kern = octet ? corr_kernel() : quad ? conv_q_kernel_for(CK, g.k) : conv_kernel_for(CK);
+    const void* kern = octet ? corr_kernel() : quad ? conv_q_kernel_for(CK, g.k, epi) : conv_kernel_for(CK);
     if (!kern) return fail(ctx, KDEC_EINVAL, "conv: unsupported channel chunk");
     int max_q = g.n_q;
     if (g.n_phase > 1) max_q = static_cast<int>(cdiv(g.L_y + g.ph_s, g.ph_s)) + 1;
@@ -1847,6 +2046,8 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
         ProfScope ps(ctx, "tile_reduce", 0.0);
         if (g.ad.part)
             hipLaunchKernelGGL(tile_reduce_adain, dim3(BM * BN / 1024, g.split_tiles), dim3(256), 0, ctx->stream, g);
+        else if (g.fs.part)
+            hipLaunchKernelGGL(tile_reduce_stats, dim3(BM * BN / 1024, g.split_tiles), dim3(256), 0, ctx->stream, g);
         else
             hipLaunchKernelGGL(tile_reduce, dim3(BM * BN / 1024, g.split_tiles), dim3(256), 0, ctx->stream, g);
         return launch_check(ctx, "tile_reduce");
@@ -1861,11 +2062,16 @@ using namespace kdec;
 
 extern "C" {
 
-int kdec_conv1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
-                    const float* bias, float* Y, long y_bs, int N, int C_in,
-                    int L, int C_out, int k, int stride, int pad, int dil,
-                    const float* R, long r_bs, float scale, float beta) {
-    if (!ctx) return KDEC_EINVAL;
+}  // extern "C"
+
+namespace kdec {
+namespace {
+// The conv1d forward; with `part` (only where the GEMM runs conv_gemm_q and
+// beta = 0) its epilogue also writes the output rows' statistics records
+// (2 * q_tiles slots per row, see store_tile_stats).
+int conv_fwd_impl(kdec_ctx* ctx, const float* X, long x_bs, const float* W, const float* bias, float* Y, long y_bs,
+                  int N, int C_in, int L, int C_out, int k, int stride, int pad, int dil, const float* R, long r_bs,
+                  float scale, float beta, double* part, int nch) {
     KDEC_CHECK(ctx, X && W && Y && N > 0 && C_in > 0 && C_out > 0 && k > 0 && stride > 0 && dil > 0 && pad >= 0,
                "kdec_conv1d_fwd: bad arguments");
     const int L_out = (L + 2 * pad - dil * (k - 1) - 1) / stride + 1;
@@ -1889,6 +2095,11 @@ int kdec_conv1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
     } else {
         g.CK = pick_ck(k, stride, dil);
         g.cin_pad = static_cast<int>(cdiv(C_in, 32) * 32);
+    }
+    if (part) {
+        if (!g.quad || beta != 0.0f) return fail(ctx, KDEC_EINVAL, "conv forward: no statistics epilogue here");
+        g.fs.part = part;
+        g.fs.nch = nch;
     }
     const int nq = static_cast<int>(cdiv(static_cast<long>(g.CK) * k / 2, 4));
     const long tot = g.quad ? (m_pad / BM) * static_cast<long>(g.cin_pad / g.CK) * nq * 1024
@@ -1915,6 +2126,61 @@ int kdec_conv1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
     if (int rc = launch_check(ctx, "pack_fwd")) return rc;
     return run_gemm(ctx, g, N, m_pad / BM, "conv_fwd",
                     2.0 * N * C_out * static_cast<double>(L_out) * C_in * k);
+}
+
+
+// Whether a forward conv of this geometry runs conv_gemm_q.
+bool fwd_is_quad(kdec_ctx* ctx, int N, int C_in, int L, int C_out, int k, int dil) {
+    if (pick_ck_q(k) <= 0) return false;
+    GemmArgs g{};
+    choose_chunks(ctx, g, C_in, k, dil, cdiv(C_out, BM) * cdiv(L, BN) * N);
+    return g.G == 0;
+}
+}  // namespace
+}  // namespace kdec
+
+extern "C" {
+
+int kdec_conv1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
+                    const float* bias, float* Y, long y_bs, int N, int C_in,
+                    int L, int C_out, int k, int stride, int pad, int dil,
+                    const float* R, long r_bs, float scale, float beta) {
+    if (!ctx) return KDEC_EINVAL;
+    return conv_fwd_impl(ctx, X, x_bs, W, bias, Y, y_bs, N, C_in, L, C_out, k, stride, pad, dil, R, r_bs, scale,
+                         beta, nullptr, 0);
+}
+
+int kdec_conv1d_fwd_stats_fused(kdec_ctx* ctx, int N, int C_in, int L, int C_out, int k, int stride, int pad,
+                                int dil) {
+    if (!ctx || N <= 0 || C_in <= 0 || C_out <= 0 || k <= 0 || stride <= 0 || dil <= 0 || L <= 0) return 0;
+    const int L_out = (L + 2 * pad - dil * (k - 1) - 1) / stride + 1;
+    return stride == 1 && L_out == L && (static_cast<long>(C_out) + BM) * L_out * 4 < 0x7fffffffL &&
+           fwd_is_quad(ctx, N, C_in, L, C_out, k, dil);
+}
+
+int kdec_conv1d_fwd_stats(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
+                          const float* bias, float* Y, long y_bs, int N, int C_in,
+                          int L, int C_out, int k, int stride, int pad, int dil,
+                          const float* R, long r_bs, float scale, float eps, float* stats) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, stats && Y && N > 0 && C_out > 0, "kdec_conv1d_fwd_stats: bad arguments");
+    const int L_out = (L + 2 * pad - dil * (k - 1) - 1) / stride + 1;
+    if (!kdec_conv1d_fwd_stats_fused(ctx, N, C_in, L, C_out, k, stride, pad, dil)) {
+        if (int rc = kdec_conv1d_fwd(ctx, X, x_bs, W, bias, Y, y_bs, N, C_in, L, C_out, k, stride, pad, dil, R, r_bs,
+                                     scale, 0.0f))
+            return rc;
+        return kdec_instnorm_stats(ctx, Y, y_bs, N, C_out, L_out, eps, stats);
+    }
+    const int nch = 2 * static_cast<int>(cdiv(L_out, BN));
+    Workspace part(ctx, static_cast<size_t>(N) * C_out * nch * 3 * sizeof(double));
+    if (!part.p) return KDEC_ENOMEM;
+    if (int rc = conv_fwd_impl(ctx, X, x_bs, W, bias, Y, y_bs, N, C_in, L, C_out, k, stride, pad, dil, R, r_bs, scale,
+                               0.0f, part.as<double>(), nch))
+        return rc;
+    ProfScope ps(ctx, "adain_fwd", 0, 0.0);
+    hipLaunchKernelGGL(instnorm_fin_slots_k, dim3(static_cast<unsigned>(N * C_out)), dim3(64), 0, ctx->stream,
+                       part.as<double>(), nch, eps, reinterpret_cast<float2*>(stats));
+    return launch_check(ctx, "instnorm_fin_slots");
 }
 
 }  // extern "C"
@@ -2121,9 +2387,6 @@ const void* wgrad_kernel(bool s1, int wn) {
 // where it leaves fewer idle columns than the 256-column one (the stage-1
 // convs' 128 * {3, 7, 11} columns), else the wide tile.
 int wgrad_wn(int NN) {
-#ifdef WG_NARROW_OFF
-    return 4 + 0 * NN;
-#endif
     const long w4 = cdiv(NN, 256) * 256 - NN, w2 = cdiv(NN, 128) * 128 - NN;
     return w2 < w4 ? 2 : 4;
 }
@@ -2133,9 +2396,6 @@ int wgrad_splits(kdec_ctx* ctx, int total_chunks, long tiles, size_t lds, bool s
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, wgrad_kernel(s1, wn), 128 * wn, lds) != hipSuccess ||
         per_cu < 1)
         per_cu = 1;
-#ifdef WG_PER_CU_CAP
-    per_cu = std::min(per_cu, WG_PER_CU_CAP);
-#endif
     // The most whole rounds of resident blocks, up to WG_ROUNDS, whose splits
     // keep at least 8 chunks each (shorter runs spend more on the partial
     // tile's write-out and reduction than on the GEMM); never a block past the

@@ -719,9 +719,6 @@ bool bwd_v4_long(const AdainArgs& g, const float* dY, long dy_bs, const float* R
 }
 // long rows need the 16-B register part (v4_long)
 RowShape row_shape_bwd(int L, bool v4_long) {
-#ifdef KDEC_BWD_ROW_MAX
-    if (L > KDEC_BWD_ROW_MAX) return {0, 0};
-#endif
     if (L <= 1024) return {256, 4};
     if (L <= 4096) return {256, 16};
     if (L <= 16384) return {1024, 16};

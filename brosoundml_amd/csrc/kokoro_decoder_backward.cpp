@@ -94,6 +94,26 @@ Tensor conv_fwd(const Conv1d& c, const Tensor& X, int L) {
     return Y;
 }
 
+// conv_fwd (beta = 0) that also returns the instance-norm statistics of its
+// output rows, (N*C_out, 2) (mean, rstd) with eps, where the GEMM's epilogue
+// forms them (kdec_conv1d_fwd_stats_fused); elsewhere the plain conv and an
+// empty tensor, leaving the statistics to the one-pass AdaIN forward.
+Tensor conv_fwd_stats(const Conv1d& c, const Tensor& X, int L, float* Y, long y_bs, const float* R, long r_bs,
+                      float eps) {
+    if (c.groups != 1) fail("Conv1d", "grouped conv1d is not on the decoder path");
+    if (!kdec_conv1d_fwd_stats_fused(kctx(), X.rows, c.in_channels, L, c.out_channels, c.kernel_size, c.stride,
+                                     c.padding, c.dilation)) {
+        conv_fwd(c, X, L, Y, y_bs, R, r_bs);
+        return Tensor();
+    }
+    Tensor st = dev(X.rows * c.out_channels, 2);
+    ck(kdec_conv1d_fwd_stats(kctx(), cp(X), rs(X), cp(c.W), bias_of(c), Y, y_bs, X.rows, c.in_channels, L,
+                             c.out_channels, c.kernel_size, c.stride, c.padding, c.dilation, R, r_bs, 1.0f, eps,
+                             mp(st)),
+       "conv1d forward");
+    return st;
+}
+
 // dX = scale * dgrad(dY) + beta * dX; L = input length
 void conv_dgrad(const Conv1d& c, const Tensor& dY, int L, float* dX, long dx_bs, float scale = 1.0f,
                 float beta = 0.0f) {
@@ -588,25 +608,39 @@ void resblock1_fwd(const AdaINResBlock1Weights& w, const Tensor& x_in, int C, in
     const int N = x_in.rows;
     cache.C = C;
     cache.L = L;
+    auto eps_of = [](const AdaIN1dWeights& a) { return a.eps > 0.0f ? a.eps : 1e-5f; };
     Tensor x = x_in;
+    Tensor x_st;  // statistics of x, when the conv that produced it formed them
     for (int i = 0; i < 3; ++i) {
         cache.x_in[i] = x;
         cache.beta1[i] = b1[i];
         cache.beta2[i] = b2[i];
         cache.s1_pre[i] = Tensor();
         cache.s2_pre[i] = Tensor();
-        const float eps1 = w.adain1[i].eps > 0.0f ? w.adain1[i].eps : 1e-5f;
-        const float eps2 = w.adain2[i].eps > 0.0f ? w.adain2[i].eps : 1e-5f;
-        Tensor xt1 = adain_act_stats(x, eps1, cache.x_seq1[i], g1[i], b1[i], C, L, KDEC_ACT_SNAKE, 0.0f, &w.alpha1[i],
-                                     where);
-        cache.c1_out[i] = conv_fwd(w.convs1[i], xt1, L);
+        Tensor xt1;
+        if (x_st.data) {
+            cache.x_seq1[i] = x_st;
+            xt1 = adain_act(x, x_st, g1[i], b1[i], C, L, KDEC_ACT_SNAKE, 0.0f, &w.alpha1[i], where);
+        } else {
+            xt1 = adain_act_stats(x, eps_of(w.adain1[i]), cache.x_seq1[i], g1[i], b1[i], C, L, KDEC_ACT_SNAKE, 0.0f,
+                                  &w.alpha1[i], where);
+        }
+        Tensor c1 = dev(N, C * L);
+        const Tensor st2 = conv_fwd_stats(w.convs1[i], xt1, L, mp(c1), rs(c1), nullptr, 0, eps_of(w.adain2[i]));
+        cache.c1_out[i] = c1;
         cache.act1[i] = xt1;
-        Tensor xt2 = adain_act_stats(cache.c1_out[i], eps2, cache.x_seq2[i], g2[i], b2[i], C, L, KDEC_ACT_SNAKE,
-                                     0.0f, &w.alpha2[i], where);
+        Tensor xt2;
+        if (st2.data) {
+            cache.x_seq2[i] = st2;
+            xt2 = adain_act(c1, st2, g2[i], b2[i], C, L, KDEC_ACT_SNAKE, 0.0f, &w.alpha2[i], where);
+        } else {
+            xt2 = adain_act_stats(c1, eps_of(w.adain2[i]), cache.x_seq2[i], g2[i], b2[i], C, L, KDEC_ACT_SNAKE, 0.0f,
+                                  &w.alpha2[i], where);
+        }
         cache.act2[i] = xt2;
         if (i < 2) {
             Tensor xn = dev(N, C * L);
-            conv_fwd(w.convs2[i], xt2, L, mp(xn), rs(xn), cp(x), rs(x), 1.0f, 0.0f);
+            x_st = conv_fwd_stats(w.convs2[i], xt2, L, mp(xn), rs(xn), cp(x), rs(x), eps_of(w.adain1[i + 1]));
             x = xn;
         } else {
             conv_fwd(w.convs2[i], xt2, L, out, out_bs, cp(x), rs(x), out_scale, out_beta);

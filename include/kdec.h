@@ -84,6 +84,25 @@ int kdec_conv1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
                     int L, int C_out, int k, int stride, int pad, int dil,
                     const float* R, long r_bs, float scale, float beta);
 
+/* kdec_conv1d_fwd (beta = 0) that also writes the instance-norm statistics
+ * of its output rows, stats[n*C_out + c] = (mean, 1/sqrt(var + eps)) as
+ * kdec_instnorm_stats computes them. Where the GEMM runs the quad-packed
+ * kernel, its epilogue records each tile's per-row count, mean and squared
+ * deviations and a wave per row merges them (in double), so Y is not read
+ * again; elsewhere it is the two calls. For the conv outputs that feed an
+ * AdaIN (kokoro_decoder_backward.cpp:307-313, the ResBlock1 convs whose
+ * output the next adain_affine_forward normalises, :100-120). */
+int kdec_conv1d_fwd_stats(kdec_ctx* ctx, const float* X, long x_bs,
+                          const float* W, const float* bias, float* Y,
+                          long y_bs, int N, int C_in, int L, int C_out, int k,
+                          int stride, int pad, int dil, const float* R,
+                          long r_bs, float scale, float eps, float* stats);
+/* 1 where kdec_conv1d_fwd_stats takes the fused path for this geometry, else
+ * 0 (a caller may then prefer the one-pass kdec_adain_act_fwd_stats). */
+int kdec_conv1d_fwd_stats_fused(kdec_ctx* ctx, int N, int C_in, int L,
+                                int C_out, int k, int stride, int pad,
+                                int dil);
+
 /* dX = scale * conv1d_backward_input(W, dY) + beta * dX   (stride 1)
  * Replaces bt::conv1d_backward_input at kokoro_decoder_backward.cpp:230-234,
  * 244-248, 271-275, 347-350, 360-363, 453-456. L is the input length. */

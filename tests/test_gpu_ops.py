@@ -168,6 +168,40 @@ def test_conv1d_quad_panel_multi_tile(K, k, d):
     assert_close(h(dX), ref.numpy(), GRAD_TOL, "conv1d backward_input, quad panel")
 
 
+@pytest.mark.parametrize("case", ["quad_residual", "split_tiles", "small_grid"])
+def test_conv1d_fwd_stats(K, case):
+    # kdec_conv1d_fwd_stats against kdec_conv1d_fwd + kdec_instnorm_stats:
+    # Y bit for bit (the epilogue stores what the plain conv stores) and the
+    # per-row (mean, rstd) within 1e-6, on the quad GEMM's whole tiles (C =
+    # 128, 1400 tiles, residual and scale, rows with a large common offset),
+    # with split tail tiles reduced by tile_reduce_stats (C = 256), and on a
+    # small grid (the two calls). kdec_conv1d_fwd_stats_fused reports which.
+    N, C_in, C_out, L, k, d, with_r, fused = {
+        "quad_residual": (2, 128, 128, 128 * 700, 11, 5, True, 1),
+        "split_tiles": (2, 256, 256, 128 * 330 - 9, 7, 3, False, 1),
+        "small_grid": (1, 64, 96, 1000, 3, 1, True, 0),
+    }[case]
+    p = d * (k - 1) // 2
+    x = rnd(N, C_in, L)
+    W = rnd(C_out, C_in * k, scale=1.0 / np.sqrt(C_in * k))
+    b = rnd(C_out) + 4.0  # an offset much larger than the rows' spread
+    R = rnd(N, C_out, L) if with_r else None
+    assert K.L.kdec_conv1d_fwd_stats_fused(K.h, N, C_in, L, C_out, k, 1, p, d) == fused
+    Y0 = torch.empty(N, C_out, L, device="cuda")
+    K.call("kdec_conv1d_fwd", P(g(x)), C_in * L, P(g(W)), P(g(b)), P(Y0), C_out * L, N, C_in, L, C_out, k, 1, p, d,
+           P(g(R) if with_r else None), C_out * L, 0.75, 0.0)
+    st0 = torch.empty(N * C_out, 2, device="cuda")
+    K.call("kdec_instnorm_stats", P(Y0), C_out * L, N, C_out, L, 1e-5, P(st0))
+    Y1 = torch.empty(N, C_out, L, device="cuda")
+    st1 = torch.empty(N * C_out, 2, device="cuda")
+    K.call("kdec_conv1d_fwd_stats", P(g(x)), C_in * L, P(g(W)), P(g(b)), P(Y1), C_out * L, N, C_in, L, C_out, k, 1,
+           p, d, P(g(R) if with_r else None), C_out * L, 0.75, 1e-5, P(st1))
+    np.testing.assert_array_equal(h(Y1), h(Y0))
+    a, r = h(st1), h(st0)
+    assert_close(a[:, 0], r[:, 0], 1e-6, f"fused statistics ({case}) mean")
+    assert_close(a[:, 1], r[:, 1], 1e-6, f"fused statistics ({case}) rstd")
+
+
 @pytest.mark.parametrize("case", ["quad_snake_residual", "split_tiles_leaky", "small_grid_none"])
 def test_conv1d_dgrad_adain_bwd_fused(K, case):
     # kdec_conv1d_dgrad_adain_bwd against the two calls it replaces
