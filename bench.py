@@ -10,6 +10,12 @@ d(style)) besides the reference's AdaIN affine grads. Inputs are synthetic
 style ~ N(0, 0.3), dL/dwav ~ N(0, 1)) and the weights are random-init FP32
 at the real shapes; everything is resident in HBM before the timed region.
 
+`value` / `ms_per_step` come from K steps with nothing recorded between
+launches. The per-family times and the roofline come from a second pass of
+the same K steps with a HIP event pair around each kernel family launch
+(`profiled_ms_per_step`), and `serial` repeats both on one stream (no
+weight-grad / harmonic-source lanes), where no family shares the CUs.
+
 Prints one JSON line (rank 0). Usage: python bench.py [--steps K] [--warmup W]
 """
 from __future__ import annotations
@@ -328,6 +334,8 @@ def main(argv=None):
                     help="run only the per-kernel-class microbenchmarks and print their JSON (for profiling them)")
     ap.add_argument("--serial", action="store_true",
                     help="one stream (no harmonic-source / weight-grad overlap): per-family times without sharing")
+    ap.add_argument("--serial-steps", type=int, default=3,
+                    help="steps of a one-stream pass after the timed region (serial family times and GEMM rate)")
     ap.add_argument("--batch-split", type=int, default=0,
                     help="1: run the batch as two half-batch chains on two streams (kdec_model_set_batch_split); "
                          "0 (default): one chain")
@@ -390,19 +398,54 @@ def main(argv=None):
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()
-    ctx.profile(True)
-    ctx.profile_reset()
-    torch.cuda.synchronize()
+    # timed region: K steps with nothing recorded between launches
     t0 = time.perf_counter()
     for _ in range(a.steps):
         step()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    prof = ctx.profile_read()
-    ctx.profile(False)
     if not torch.isfinite(audio).all() or not torch.isfinite(dstyle).all():
         print("non-finite output", file=sys.stderr)
         return 1
+    # profiled region: the same K steps again with a HIP event pair around
+    # every kernel family launch, on the stream it runs on (the per-family
+    # times and the roofline); the events themselves lengthen a step by a
+    # millisecond or two, which is why the throughput is timed without them
+    ctx.profile(True)
+    ctx.profile_reset()
+    torch.cuda.synchronize()
+    p0 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    torch.cuda.synchronize()
+    pdt = time.perf_counter() - p0
+    prof = ctx.profile_read()
+    ctx.profile(False)
+
+    # the same step on one stream after the timed region: per-family times
+    # and the conv GEMM rate without the weight-grad lane sharing the CUs
+    serial = {}
+    if a.serial_steps > 0 and not a.serial:
+        model.set_overlap(False)
+        step()
+        torch.cuda.synchronize()
+        s0 = time.perf_counter()
+        for _ in range(a.serial_steps):
+            step()
+        torch.cuda.synchronize()
+        sdt = (time.perf_counter() - s0) / a.serial_steps
+        ctx.profile(True)
+        ctx.profile_reset()
+        s0 = time.perf_counter()
+        for _ in range(a.serial_steps):
+            step()
+        torch.cuda.synchronize()
+        spdt = (time.perf_counter() - s0) / a.serial_steps
+        sprof = ctx.profile_read()
+        ctx.profile(False)
+        model.set_overlap(True)
+        serial = {"ms_per_step": round(sdt * 1e3, 3), "profiled_ms_per_step": round(spdt * 1e3, 3),
+                  "steps": a.serial_steps, "prof": sprof}
 
     # reference semantics (conv dgrad only, alpha grad dropped, no d(style))
     ref = {}
@@ -421,7 +464,8 @@ def main(argv=None):
     value = audio_per_step / (dt / a.steps)
 
     # dominant kernel: the conv implicit GEMM family with the most time
-    conv_fams = {k: v for k, v in prof.items() if k in ("conv_fwd", "conv_dgrad", "convt_fwd", "convt_dgrad")}
+    GEMM_FAMS = ("conv_fwd", "conv_dgrad", "convt_fwd", "convt_dgrad")
+    conv_fams = {k: v for k, v in prof.items() if k in GEMM_FAMS}
     gemm_ms = sum(v["ms"] for v in conv_fams.values())
     gemm_flops = sum(v["flops"] for v in conv_fams.values())
     gemm_bytes = sum(v["bytes"] for v in conv_fams.values())
@@ -460,6 +504,7 @@ def main(argv=None):
         "roofline": {"bound": "mfma", "kernel": "conv_gemm (conv1d fwd / dgrad, convT fwd / dgrad)",
                      "achieved": round(achieved / 1e12, 3), "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": traffic,
+                     "region": "profiled pass of the same K steps (events around every family launch)",
                      "algorithmic_bytes_per_launch": round(gemm_bytes / max(gemm_launches, 1)),
                      "launches_per_step": gemm_launches // a.steps,
                      "ms_per_step": round(gemm_ms / a.steps, 3),
@@ -470,10 +515,26 @@ def main(argv=None):
         "step_roofline": {"ideal_ms": round(ideal_s * 1e3, 3), "frac": round(ideal_s * 1e3 / ms, 4),
                           "conv_tflop_per_step": round(total_conv_flops / a.steps / 1e12, 4),
                           "elementwise_gb_per_step": round(20.0 * elems / 1e9, 3)},
+        "profiled_ms_per_step": round(pdt / a.steps * 1e3, 3),
         "families_ms_per_step": {k: round(v["ms"] / a.steps, 3) for k, v in sorted(prof.items())},
         "reference_semantics": ref,
         "streams": 1 if a.serial else 2,
     }
+    if serial:
+        sp, n = serial.pop("prof"), serial["steps"]
+        s_ms = sum(v["ms"] for k, v in sp.items() if k in GEMM_FAMS)
+        s_fl = sum(v["flops"] for k, v in sp.items() if k in GEMM_FAMS)
+        swg = [sp.get(k, {"ms": 0, "flops": 0}) for k in ("conv_wgrad", "convt_wgrad")]
+        w_ms, w_fl = sum(v["ms"] for v in swg), sum(v["flops"] for v in swg)
+        serial["roofline"] = {"kernel": out["roofline"]["kernel"], "achieved": round(s_fl / (s_ms * 1e-3) / 1e12, 3)
+                              if s_ms else 0.0, "frac": round(s_fl / (s_ms * 1e-3) / PEAK_FP32_MFMA, 4) if s_ms else 0.0,
+                              "ms_per_step": round(s_ms / n, 3)}
+        serial["wgrad_roofline"] = {"achieved": round(w_fl / max(w_ms * 1e-3, 1e-12) / 1e12, 3),
+                                    "frac": round(w_fl / max(w_ms * 1e-3, 1e-12) / PEAK_FP32_MFMA, 4),
+                                    "ms_per_step": round(w_ms / n, 3)}
+        serial["families_ms_per_step"] = {k: round(v["ms"] / n, 3) for k, v in sorted(sp.items())}
+        out["serial"] = serial
+    out["step_roofline"]["frac_serial"] = round(ideal_s * 1e3 / serial["ms_per_step"], 4) if serial else None
     if not a.no_serving:
         out["inference"] = inference_bench(ctx, model, t_asr, t_F0, t_N, t_style, audio, audio_per_step)
         out["lora_train_step"] = lora_bench(model, t_asr, t_F0, t_N, t_style, t_dA, audio_per_step)

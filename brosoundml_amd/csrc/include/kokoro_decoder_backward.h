@@ -58,6 +58,14 @@ struct WeightGrads {
 void set_wgrad_lane(kdec_ctx* side);
 void join_wgrad_lane();
 
+// ─── extension: the K resblocks of a generator stage on concurrent streams ─
+// While set, generator_forward_train runs resblock j > 0 of each upsample
+// stage on lane (j - 1) % 2's stream, forked from the runtime stream once the
+// stage input exists and joined before the stage output is read; their
+// accumulating last convs keep the order j = 0, 1, ..., so the output bits are
+// those of the one-stream schedule. (nullptr, nullptr) turns it off.
+void set_resblock_lanes(kdec_ctx* a, kdec_ctx* b);
+
 // ─── AdaIN affine (instance-norm + style-conditioned scale/shift) ───────────
 //   x_ncl:(N, C*L)   gamma,beta:(C,1) or (N,C)   ->   y_ncl:(N, C*L)
 void adain_affine_forward(const brotensor::Tensor& x_ncl,

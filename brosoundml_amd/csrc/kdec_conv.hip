@@ -1493,7 +1493,7 @@ void wgrad_gemm(WgradArgs g) {
     const bool g_rows_in = m0 + BM <= g.M;  // uniform: whole m-tile (else the checked path)
     // pair row wave + 8j of this lane: g_off + j * 8 * L_g * 4
     const unsigned g_off = static_cast<unsigned>((m0 + wave + 64 * g_row_lane) * g.L_g + g_pos_lane) * 4u;
-    const unsigned g_step = static_cast<unsigned>(2 * WN * g.L_g) * 4u;
+    const int g_step = 2 * WN * g.L_g * 4;
     // Stride 1: the wave's packed-instruction offsets are held (windows of up
     // to WG_XI * 8 * 64 floats; larger ones take the checked path). Strided:
     // this lane's slot of the wave's first instruction as (row, position),
@@ -1557,10 +1557,11 @@ void wgrad_gemm(WgradArgs g) {
             }
         }
         if (g_rows_in && l0 + KC <= g.L_g) {  // uniform
+            // the row step rides in the scalar offset: one lane offset for all
 #pragma unroll
             for (int j = 0; j < GI; ++j)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(grs, smem + sb + (wave + 2 * WN * j) * GP, 4,
-                                                         static_cast<int>(g_off + j * g_step), l0 * 4, 0, 0);
+                                                         static_cast<int>(g_off), l0 * 4 + j * g_step, 0, 0);
             return;
         }
         const int l = l0 + g_pos_lane;  // a partial m-tile or the last chunk of a row: checked
@@ -2034,6 +2035,11 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
     double bytes = 4.0 * (static_cast<double>(N) * g.C_in * g.L_in + static_cast<double>(g.C_in) * kk_all * g.C_out +
                           static_cast<double>(N) * g.C_out * g.L_y * (g.beta != 0.0f ? 2 : 1));
     if (g.R) bytes += 4.0 * static_cast<double>(N) * g.C_out * g.L_y;
+    // fused epilogues: the AdaIN backward reads the normalised layer's input
+    // x; both write (count / sum, mean / sum, m2) slot records per row
+    if (g.ad.part) bytes += 4.0 * static_cast<double>(N) * g.C_out * g.L_y;
+    if (g.ad.part || g.fs.part)
+        bytes += 24.0 * static_cast<double>(N) * g.C_out * (g.ad.part ? g.ad.nch : g.fs.nch);
     {  // the GEMM kernel alone (the profile's FLOP rate is this launch's)
         ProfScope ps(ctx, fam, flops, bytes);
         void* args[] = {&g};

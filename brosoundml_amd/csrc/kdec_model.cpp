@@ -648,6 +648,16 @@ int kdec_model_forward(kdec_model* m, int N, int T, const float* asr, const floa
         const int n_dec = m->n_decode;
         int alen = 0;
         kdec_model_lengths(m, T, nullptr, nullptr, &alen);
+        // one chain: the stages' resblocks run beside the runtime stream on
+        // the second part's context and on the side context (whose harmonic
+        // source, queued first, is done before the generator needs it). Each
+        // context's stream was created on its own hardware queue; the second
+        // part's weight-grad context shares the runtime stream's.
+        struct ResblockLanes {
+            explicit ResblockLanes(kdec_ctx* a, kdec_ctx* b) { bd::set_resblock_lanes(a, b); }
+            ~ResblockLanes() { bd::set_resblock_lanes(nullptr, nullptr); }
+        } resblock_lanes(m->parts == 1 && m->overlap ? m->ctx2 : nullptr,
+                         m->parts == 1 && m->overlap ? m->side : nullptr);
         for (int pi = 0; pi < m->parts; ++pi) {
             kdec_model::Part& pt = m->part[pi];
             bt::set_runtime(pt.ctx);

@@ -608,6 +608,27 @@ __global__ void axpby_k(float a, const float* A, long a_bs, float b, const float
     }
 }
 
+// Y = (A + B) + C, the two float adds in that order; V = 4: whole float4s
+// (every row base 16-B aligned, len a multiple of 4).
+template <int V>
+__global__ void add3_k(const float* A, long a_bs, const float* B, long b_bs, const float* C, long c_bs, float* Y,
+                       long y_bs, long len) {
+    const int n = blockIdx.y;
+    const long nv = len / V;
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < nv;
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        if constexpr (V == 4) {
+            const float4 a = reinterpret_cast<const float4*>(A + n * a_bs)[i];
+            const float4 b = reinterpret_cast<const float4*>(B + n * b_bs)[i];
+            const float4 c = reinterpret_cast<const float4*>(C + n * c_bs)[i];
+            reinterpret_cast<float4*>(Y + n * y_bs)[i] =
+                make_float4((a.x + b.x) + c.x, (a.y + b.y) + c.y, (a.z + b.z) + c.z, (a.w + b.w) + c.w);
+        } else {
+            Y[n * y_bs + i] = (A[n * a_bs + i] + B[n * b_bs + i]) + C[n * c_bs + i];
+        }
+    }
+}
+
 // y[c][0] = x[c][1]; y[c][j+1] = x[c][j]
 __global__ void pad_fwd_k(const float* X, long x_bs, float* Y, long y_bs, int C, int L) {
     const int n = blockIdx.y;
@@ -1123,6 +1144,21 @@ int kdec_axpby(kdec_ctx* ctx, float a, const float* A, long a_bs, float b,
     hipLaunchKernelGGL(axpby_k, dim3(chunks(len), N), dim3(256), 0, ctx->stream, a, A, a_bs, b, B, b_bs, Y,
                        y_bs, len);
     return launch_check(ctx, "axpby");
+}
+
+int kdec_add3(kdec_ctx* ctx, const float* A, long a_bs, const float* B, long b_bs, const float* C, long c_bs,
+              float* Y, long y_bs, int N, long len) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, A && B && C && Y && N > 0 && len > 0, "kdec_add3: bad arguments");
+    ProfScope ps(ctx, "elementwise", 0);
+    auto al = [](const float* p, long bs) { return (reinterpret_cast<unsigned long long>(p) & 15) == 0 && bs % 4 == 0; };
+    if (len % 4 == 0 && al(A, a_bs) && al(B, b_bs) && al(C, c_bs) && al(Y, y_bs))
+        hipLaunchKernelGGL(add3_k<4>, dim3(chunks(len / 4), N), dim3(256), 0, ctx->stream, A, a_bs, B, b_bs, C, c_bs,
+                           Y, y_bs, len);
+    else
+        hipLaunchKernelGGL(add3_k<1>, dim3(chunks(len), N), dim3(256), 0, ctx->stream, A, a_bs, B, b_bs, C, c_bs, Y,
+                           y_bs, len);
+    return launch_check(ctx, "add3");
 }
 
 int kdec_pad_reflect_left1_fwd(kdec_ctx* ctx, const float* X, long x_bs,

@@ -188,6 +188,75 @@ struct WgradLane {
 };
 WgradLane g_lane;
 
+// Extension: the K resblocks of a generator stage read the same input u and
+// only meet in the sum of their outputs, so while lanes are set they run on
+// up to three streams (forked from the runtime stream once u exists; see
+// ctx_for), and so do the stages' noise branches, which read only har. For
+// K = 3 each resblock's last conv writes its own buffer (1/K applied) and
+// kdec_add3 forms (x0 + x1) + x2 after the join, on one stream as well, so
+// both schedules run the same kernels and give the same bits. Other K keep
+// the accumulating convs, each waiting for the previous one's event. The
+// lanes' streams overlap one branch's epilogues, statistics finalizes and
+// AdaIN passes with another branch's GEMM rounds.
+//
+// Tensors crossing streams: u, the output and the affine views belong to the
+// runtime context and are reused only after the join; the branch caches
+// belong to the lane contexts, whose next allocation is ordered after the
+// next fork, i.e. after every kernel the runtime stream had queued by then.
+struct BranchLanes {
+    kdec_ctx* lane[2] = {nullptr, nullptr};  // noise branches: stage 0 on [1], later stages on [0]
+    std::vector<hipEvent_t> ev;  // [0]: fork, [1 + j]: branch j's last conv done
+    std::vector<hipEvent_t> noise_ev;  // [i]: stage i's noise branch done
+
+    bool on() const { return lane[0] != nullptr && lane[1] != nullptr; }
+    static hipEvent_t grow(std::vector<hipEvent_t>& v, std::size_t i) {
+        while (v.size() <= i) {
+            hipEvent_t e = nullptr;
+            if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess)
+                fail("resblock lanes", "hipEventCreate failed");
+            v.push_back(e);
+        }
+        return v[i];
+    }
+    hipEvent_t event(std::size_t i) { return grow(ev, i); }
+    hipEvent_t noise_event(std::size_t i) { return grow(noise_ev, i); }
+    kdec_ctx* noise_lane(int stage) const { return stage == 0 ? lane[1] : lane[0]; }
+    // One branch per stream (0 on the runtime stream, 1 on lane 0, 2 on lane
+    // 1) once lane 0 has no later stage's noise branch queued; before that,
+    // branches 0 and 1 on the runtime stream and 2 on lane 1 (the kernel sizes
+    // grow with j, so the two streams get about equal work).
+    kdec_ctx* ctx_for(int j, kdec_ctx* main, bool noise_pending) const {
+        if (noise_pending) return j < 2 ? main : lane[1];
+        if (j == 0) return main;
+        return lane[(j - 1) % 2];
+    }
+    static void wait_on(kdec_ctx* c, hipEvent_t e) {
+        if (hipStreamWaitEvent(static_cast<hipStream_t>(kdec_get_stream(c)), e, 0) != hipSuccess)
+            fail("resblock lanes", "stream wait failed");
+    }
+    void fork(kdec_ctx* main) {
+        hipEvent_t e = event(0);
+        if (hipEventRecord(e, static_cast<hipStream_t>(kdec_get_stream(main))) != hipSuccess)
+            fail("resblock lanes", "fork failed");
+        for (kdec_ctx* c : lane) wait_on(c, e);
+    }
+    // the runtime stream waits for every branch's last conv
+    void join(kdec_ctx* main, int K) {
+        for (int j = 1; j <= K; ++j) wait_on(main, event(static_cast<std::size_t>(j)));
+    }
+};
+BranchLanes g_branch;
+
+// Makes `c` the runtime context for a scope (the previous one comes back on
+// exit, also when the scope throws).
+struct RuntimeScope {
+    kdec_ctx* prev;
+    explicit RuntimeScope(kdec_ctx* c) : prev(bt::runtime()) { bt::set_runtime(c); }
+    ~RuntimeScope() { bt::set_runtime(prev); }
+    RuntimeScope(const RuntimeScope&) = delete;
+    RuntimeScope& operator=(const RuntimeScope&) = delete;
+};
+
 void conv_wgrad(const Conv1d& c, const detail::WeightGrads* wg, const Tensor& X, int L, const Tensor& dY) {
     float* dW = grad_of(wg, c.W);
     float* db = bias_of(c) ? grad_of(wg, c.b) : nullptr;
@@ -421,6 +490,11 @@ void set_wgrad_lane(kdec_ctx* side) {
 
 void join_wgrad_lane() { g_lane.join(); }
 
+void set_resblock_lanes(kdec_ctx* a, kdec_ctx* b) {
+    g_branch.lane[0] = a && b ? a : nullptr;
+    g_branch.lane[1] = a && b ? b : nullptr;
+}
+
 // ─── AdaIN affine ───────────────────────────────────────────────────────────
 
 void adain_affine_forward(const Tensor& x_ncl, const Tensor& gamma, const Tensor& beta, int C, int L,
@@ -600,9 +674,12 @@ using Arr3 = std::array<Tensor, 3>;
 
 // Forward of one AdaINResBlock1; the last sub-block writes
 // out = out_scale * (conv2 + bias + x) + out_beta * out.
+// With `out_wait`, the last conv waits for that event first; with
+// `out_done`, the event is recorded after it (the resblock lanes' order).
 void resblock1_fwd(const AdaINResBlock1Weights& w, const Tensor& x_in, int C, int L, const Arr3& g1,
                    const Arr3& b1, const Arr3& g2, const Arr3& b2, float* out, long out_bs, float out_scale,
-                   float out_beta, AdainResBlock1Cache& cache) {
+                   float out_beta, AdainResBlock1Cache& cache, hipEvent_t out_wait = nullptr,
+                   hipEvent_t out_done = nullptr) {
     const char* where = "adain_resblock1_forward_train";
     check_batch(x_in, C, L, where);
     const int N = x_in.rows;
@@ -643,7 +720,11 @@ void resblock1_fwd(const AdaINResBlock1Weights& w, const Tensor& x_in, int C, in
             x_st = conv_fwd_stats(w.convs2[i], xt2, L, mp(xn), rs(xn), cp(x), rs(x), eps_of(w.adain1[i + 1]));
             x = xn;
         } else {
+            hipStream_t st = static_cast<hipStream_t>(kdec_get_stream(kctx()));
+            if (out_wait && hipStreamWaitEvent(st, out_wait, 0) != hipSuccess)
+                fail(where, "waiting for the previous resblock's output");
             conv_fwd(w.convs2[i], xt2, L, out, out_bs, cp(x), rs(x), out_scale, out_beta);
+            if (out_done && hipEventRecord(out_done, st) != hipSuccess) fail(where, "event record failed");
         }
     }
 }
@@ -887,6 +968,35 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
     if (cache.keep) cache.har = har;
     cache.frames = frames;
 
+    // With the lanes set, every stage's noise branch (noise_convs[i] ->
+    // noise_res[i]) reads only har, so all of them are queued first, in stage
+    // order (stage 0 on lane 1, the others on lane 0, so that stage 1's runs
+    // beside stage 0's); each stage's runtime stream waits for its own.
+    kdec_ctx* const main_ctx = kctx();
+    const bool par = g_branch.on();
+    std::vector<Tensor> srcs(static_cast<std::size_t>(U));
+    std::vector<int> src_len(static_cast<std::size_t>(U), 0);
+    if (par) {
+        g_branch.fork(main_ctx);  // har may have been written on the runtime stream
+        if (cache.har_ready) {
+            for (kdec_ctx* c : g_branch.lane) BranchLanes::wait_on(c, static_cast<hipEvent_t>(cache.har_ready));
+            cache.har_ready = nullptr;  // the runtime stream joins through the noise events
+        }
+        for (int i = 0; i < U; ++i) {
+            kdec_ctx* const nl = g_branch.noise_lane(i);
+            RuntimeScope scope(nl);
+            const int C_out = gen.ups_C_out[i];
+            Tensor x_source = conv_fwd(gen.noise_convs[i], har, frames);
+            src_len[i] = x_source.cols / C_out;
+            adain_resblock1_forward_train(gen.noise_res[i], x_source, C_out, src_len[i], naff[i].g1, naff[i].b1,
+                                          naff[i].g2, naff[i].b2, srcs[i], cache.stages[i].noise);
+            if (!cache.keep) cache.stages[i].noise = AdainResBlock1Cache{};
+            if (hipEventRecord(g_branch.noise_event(static_cast<std::size_t>(i)),
+                               static_cast<hipStream_t>(kdec_get_stream(nl))) != hipSuccess)
+                fail(where, "event record failed");
+        }
+    }
+
     Tensor x = gen_in;
     int L = L_in;
     for (int i = 0; i < U; ++i) {
@@ -914,18 +1024,26 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
         }
 
         // noise branch
-        if (cache.har_ready) {
-            if (hipStreamWaitEvent(static_cast<hipStream_t>(kdec_get_stream(kctx())),
-                                   static_cast<hipEvent_t>(cache.har_ready), 0) != hipSuccess)
-                fail(where, "waiting for the harmonic source");
-            cache.har_ready = nullptr;
-        }
-        Tensor x_source = conv_fwd(gen.noise_convs[i], har, frames);
-        const int L_src = x_source.cols / C_out;
         Tensor src;
-        adain_resblock1_forward_train(gen.noise_res[i], x_source, C_out, L_src, naff[i].g1, naff[i].b1, naff[i].g2,
-                                      naff[i].b2, src, sc.noise);
-        if (!cache.keep) sc.noise = AdainResBlock1Cache{};
+        int L_src = 0;
+        if (par) {
+            BranchLanes::wait_on(main_ctx, g_branch.noise_event(static_cast<std::size_t>(i)));
+            src = srcs[i];
+            srcs[i] = Tensor();
+            L_src = src_len[i];
+        } else {
+            if (cache.har_ready) {
+                if (hipStreamWaitEvent(static_cast<hipStream_t>(kdec_get_stream(kctx())),
+                                       static_cast<hipEvent_t>(cache.har_ready), 0) != hipSuccess)
+                    fail(where, "waiting for the harmonic source");
+                cache.har_ready = nullptr;
+            }
+            Tensor x_source = conv_fwd(gen.noise_convs[i], har, frames);
+            L_src = x_source.cols / C_out;
+            adain_resblock1_forward_train(gen.noise_res[i], x_source, C_out, L_src, naff[i].g1, naff[i].b1,
+                                          naff[i].g2, naff[i].b2, src, sc.noise);
+            if (!cache.keep) sc.noise = AdainResBlock1Cache{};
+        }
         if (L_src != L_x)
             fail(where, "noise source length " + std::to_string(L_src) + " != upsampled length " +
                             std::to_string(L_x) + " at stage " + std::to_string(i));
@@ -935,14 +1053,32 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
         src = Tensor();
 
         // x = mean_j resblocks[i*K + j](u): each block's last conv accumulates
+        // (on the resblock lanes when they are set, in the same accumulation order)
         sc.res.resize(K);
         Tensor xs = dev(N, C_out * L_x);
+        const bool par_rb = par && K > 1;
+        const bool sep = K == 3;  // separate outputs summed by kdec_add3, on one stream too
+        const bool noise_pending = i + 1 < U;  // later stages' noise branches queued on lane 0
+        Tensor outs[2];
+        if (sep)
+            for (Tensor& o : outs) o = dev(N, C_out * L_x);
+        if (par_rb) g_branch.fork(main_ctx);
         for (int j = 0; j < K; ++j) {
             const ResBlock1Affines& ra = raff[static_cast<std::size_t>(i) * K + j];
+            RuntimeScope scope(par_rb ? g_branch.ctx_for(j, main_ctx, noise_pending) : main_ctx);
+            const Tensor& dst = sep && j > 0 ? outs[j - 1] : xs;
+            const bool acc = j > 0 && !sep;
             resblock1_fwd(gen.resblocks[static_cast<std::size_t>(i) * K + j], u, C_out, L_x, ra.g1, ra.b1, ra.g2,
-                          ra.b2, mp(xs), rs(xs), 1.0f / static_cast<float>(K), j == 0 ? 0.0f : 1.0f, sc.res[j]);
+                          ra.b2, mp(dst), rs(dst), 1.0f / static_cast<float>(K), acc ? 1.0f : 0.0f, sc.res[j],
+                          par_rb && acc ? g_branch.event(static_cast<std::size_t>(j)) : nullptr,
+                          par_rb ? g_branch.event(static_cast<std::size_t>(j) + 1) : nullptr);
             if (!cache.keep) sc.res[j] = AdainResBlock1Cache{};
         }
+        if (par_rb) g_branch.join(main_ctx, K);
+        if (sep)
+            ck(kdec_add3(main_ctx, cp(xs), rs(xs), cp(outs[0]), rs(outs[0]), cp(outs[1]), rs(outs[1]), mp(xs), rs(xs),
+                         N, static_cast<long>(C_out) * L_x),
+               "resblock sum");
         x = xs;
         L = L_x;
     }

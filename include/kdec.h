@@ -258,6 +258,15 @@ int kdec_leaky_bwd(kdec_ctx* ctx, const float* X, long x_bs, const float* dY,
 int kdec_axpby(kdec_ctx* ctx, float a, const float* A, long a_bs, float b,
                const float* B, long b_bs, float* Y, long y_bs, int N,
                long len);
+/* Y = (A + B) + C over N rows of `len`, the float adds in that order (Y may
+ * alias A). The generator stage's resblock sum (kokoro_decoder_backward.cpp:
+ * 644-657, xs = x0; xs += x1; xs += x2) when the K = 3 resblocks run on
+ * concurrent streams into separate buffers, each with the 1/K already applied
+ * by its last conv: the same two roundings as the one-stream schedule, whose
+ * last convs accumulate into one buffer in that order. */
+int kdec_add3(kdec_ctx* ctx, const float* A, long a_bs, const float* B,
+              long b_bs, const float* C, long c_bs, float* Y, long y_bs,
+              int N, long len);
 /* Left reflect pad by one sample, C rows of L -> L+1 (bt::pad1d_* mode 1 at
  * :633-634 / :720-721). */
 int kdec_pad_reflect_left1_fwd(kdec_ctx* ctx, const float* X, long x_bs,
