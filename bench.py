@@ -534,6 +534,11 @@ def main(argv=None):
                                     "ms_per_step": round(w_ms / n, 3)}
         serial["families_ms_per_step"] = {k: round(v["ms"] / n, 3) for k, v in sorted(sp.items())}
         out["serial"] = serial
+        # the same kernels with the GPU to themselves: on the default schedule
+        # up to three conv GEMMs (and the weight-grad GEMMs) share the CUs, so
+        # each launch's duration above also holds the others' work
+        out["roofline"]["achieved_one_stream"] = serial["roofline"]["achieved"]
+        out["roofline"]["frac_one_stream"] = serial["roofline"]["frac"]
     out["step_roofline"]["frac_serial"] = round(ideal_s * 1e3 / serial["ms_per_step"], 4) if serial else None
     if not a.no_serving:
         out["inference"] = inference_bench(ctx, model, t_asr, t_F0, t_N, t_style, audio, audio_per_step)

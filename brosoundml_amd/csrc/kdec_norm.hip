@@ -12,8 +12,11 @@
 #include "kdec_internal.hpp"
 #include "kdec_snake_math.hpp"
 
+#include <algorithm>
+#include <initializer_list>
 #include <mutex>
 #include <string>
+#include <utility>
 
 namespace kdec {
 namespace {
@@ -151,16 +154,36 @@ __device__ inline double alpha_scale(int act, float a) {
     return act == KDEC_ACT_SNAKE ? 1.0 / (static_cast<double>(a) * a) : 0.0;
 }
 
+// One row's constants of the AdaIN(+activation) forward apply.
+struct FwdRow {
+    float mean, rstd, g1, bt, a, ia;
+};
+
+__device__ inline FwdRow fwd_row(const AdainArgs& g, int row, int n, int c) {
+    const float2 st = g.stats[row];
+    FwdRow r;
+    r.mean = st.x;
+    r.rstd = st.y;
+    r.g1 = 1.0f + g.gamma[n * g.gb_bs + c];
+    r.bt = g.beta ? g.beta[n * g.gb_bs + c] : 0.0f;
+    r.a = g.act == KDEC_ACT_SNAKE ? g.alpha[c] : 1.0f;
+    r.ia = 1.0f / r.a;
+    return r;
+}
+
+// s = (1 + gamma) * xhat + beta (returned in s) and the activation of s
+__device__ inline float fwd_elem(const AdainArgs& g, const FwdRow& r, float xv, float& s) {
+    const float xh = (xv - r.mean) * r.rstd;
+    s = r.g1 * xh + r.bt;
+    return act_fwd(g.act, s, g.slope, r.a, r.ia);
+}
+
 // grid (chunks of CH, N*C)
 __global__ __launch_bounds__(RT) void adain_act_fwd_k(AdainArgs g, float* Y, long y_bs, float* Yp,
                                                      long yp_bs) {
     const int row = blockIdx.y;
     const int n = row / g.C, c = row - n * g.C;
-    const float2 st = g.stats[row];
-    const float g1 = 1.0f + g.gamma[n * g.gb_bs + c];
-    const float bt = g.beta ? g.beta[n * g.gb_bs + c] : 0.0f;
-    const float a = g.act == KDEC_ACT_SNAKE ? g.alpha[c] : 1.0f;
-    const float ia = 1.0f / a;
+    const FwdRow rc = fwd_row(g, row, n, c);
     const long off = static_cast<long>(c) * g.L;
     const float* x = g.X + n * g.x_bs + off;
     float* y = Y + n * y_bs + off;
@@ -176,10 +199,66 @@ __global__ __launch_bounds__(RT) void adain_act_fwd_k(AdainArgs g, float* Y, lon
     for (int j = 0; j < EPT; ++j) {
         const int l = l0 + j * RT;
         if (l >= g.L) break;
-        const float xh = (v[j] - st.x) * st.y;
-        const float s = g1 * xh + bt;
+        float s;
+        const float yv = fwd_elem(g, rc, v[j], s);
         if (yp) yp[l] = s;
-        y[l] = act_fwd(g.act, s, g.slope, a, ia);
+        y[l] = yv;
+    }
+}
+
+// The 16-byte form of a row's chunked pass. Every operand of a row shares
+// the row's offset modulo 4 floats (16-B aligned bases, batch strides equal
+// modulo 4; the launcher checks), so a row splits into a head of up to 3
+// elements, whole float4s and a tail of up to 3; block 0 of the row does
+// the head and tail. grid (cdiv(float4s, RT * EPT / 4), N*C).
+__device__ inline int row_head(const float* p, int L) {
+    return min(static_cast<int>((4u - ((reinterpret_cast<unsigned long long>(p) >> 2) & 3u)) & 3u), L);
+}
+
+__global__ __launch_bounds__(RT) void adain_act_fwd_v4_k(AdainArgs g, float* Y, long y_bs, float* Yp,
+                                                        long yp_bs) {
+    constexpr int Q = EPT / 4;  // float4s per thread
+    const int row = blockIdx.y;
+    const int n = row / g.C, c = row - n * g.C;
+    const long off = static_cast<long>(c) * g.L;
+    const float* x = g.X + n * g.x_bs + off;
+    float* y = Y + n * y_bs + off;
+    float* yp = Yp ? Yp + n * yp_bs + off : nullptr;
+    const int head = row_head(x, g.L);
+    const int nq = (g.L - head) >> 2;
+    // the data loads go out before the row's constants are fetched
+    const float4* x4 = reinterpret_cast<const float4*>(x + head);
+    float4* y4 = reinterpret_cast<float4*>(y + head);
+    float4* yp4 = yp ? reinterpret_cast<float4*>(yp + head) : nullptr;
+    const int q0 = blockIdx.x * (RT * Q) + threadIdx.x;
+    float4 v[Q];
+#pragma unroll
+    for (int j = 0; j < Q; ++j) {
+        const int q = q0 + j * RT;
+        v[j] = q < nq ? x4[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    const FwdRow rc = fwd_row(g, row, n, c);
+    if (blockIdx.x == 0) {
+        const int t = threadIdx.x;
+        const int l = t < 4 ? t : head + 4 * nq + (t - 4);
+        if ((t < 4 && l < head) || (t >= 4 && t < 8 && l < g.L)) {
+            float s;
+            const float yv = fwd_elem(g, rc, x[l], s);
+            if (yp) yp[l] = s;
+            y[l] = yv;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < Q; ++j) {
+        const int q = q0 + j * RT;
+        if (q >= nq) break;
+        float4 s, o;
+        o.x = fwd_elem(g, rc, v[j].x, s.x);
+        o.y = fwd_elem(g, rc, v[j].y, s.y);
+        o.z = fwd_elem(g, rc, v[j].z, s.z);
+        o.w = fwd_elem(g, rc, v[j].w, s.w);
+        if (yp4) yp4[q] = s;
+        y4[q] = o;
     }
 }
 
@@ -247,18 +326,56 @@ __global__ void adain_bwd_fin_k(const double* part, int rows, int nch, int C, in
     rowv[row] = make_float2(static_cast<float>(sd / L), static_cast<float>(sdx / L));
 }
 
-// dx = rstd * g1 * (ds - mean(ds) - xh * mean(ds*xh)) (+ R); grid (chunks, N*C)
+// One row's constants of the AdaIN(+activation) backward apply.
+struct BwdRow {
+    float mean, rstd, g1, bt, a, k1, mds, mdsx;
+};
+
+__device__ inline BwdRow bwd_row(const AdainArgs& g, const float2* rowv, int row, int n, int c) {
+    const float2 st = g.stats[row];
+    const float2 mv = rowv[row];
+    BwdRow r;
+    r.mean = st.x;
+    r.rstd = st.y;
+    r.g1 = 1.0f + g.gamma[n * g.gb_bs + c];
+    r.bt = g.beta ? g.beta[n * g.gb_bs + c] : 0.0f;
+    r.a = g.act == KDEC_ACT_SNAKE ? g.alpha[c] : 0.0f;
+    r.k1 = st.y * r.g1;
+    r.mds = mv.x;
+    r.mdsx = mv.y;
+    return r;
+}
+
+// dx = rstd * g1 * (ds - mean(ds) - xh * mean(ds*xh)) (+ the residual grad)
+__device__ inline float bwd_elem(const AdainArgs& g, const BwdRow& r, float xv, float dv, bool has_r, float rv) {
+    const float xh = (xv - r.mean) * r.rstd;
+    const float s = r.g1 * xh + r.bt;
+    float unused = 0.0f;
+    const float ds = act_bwd(g.act, dv, s, g.slope, r.a, unused);
+    float v = r.k1 * (ds - r.mds - xh * r.mdsx);
+    if (has_r) v += rv;
+    return v;
+}
+
+// grid (chunks, N*C)
+// With `ap`, the block of row (0, c), chunk 0, also adds dalpha[c] +=
+// sum_n ap[n*C + c] in that order (as dalpha_reduce would).
+__device__ inline void dalpha_fold(const float* ap, float* dalpha, int N, int C, int n, int c) {
+    if (ap && n == 0 && blockIdx.x == 0 && threadIdx.x == 0) {
+        double acc = 0.0;
+        for (int k = 0; k < N; ++k) acc += ap[k * C + c];
+        dalpha[c] += static_cast<float>(acc);
+    }
+}
+
 __global__ __launch_bounds__(RT) void adain_bwd_apply_k(AdainArgs g, const float* dY, long dy_bs,
                                                        const float* R, long r_bs, float* dX, long dx_bs,
-                                                       const float2* rowv) {
+                                                       const float2* rowv, const float* ap, float* dalpha,
+                                                       int N) {
     const int row = blockIdx.y;
     const int n = row / g.C, c = row - n * g.C;
-    const float2 st = g.stats[row];
-    const float g1 = 1.0f + g.gamma[n * g.gb_bs + c];
-    const float bt = g.beta ? g.beta[n * g.gb_bs + c] : 0.0f;
-    const float a = g.act == KDEC_ACT_SNAKE ? g.alpha[c] : 0.0f;
-    const float2 mv = rowv[row];
-    const float k1 = st.y * g1;
+    dalpha_fold(ap, dalpha, N, g.C, n, c);
+    const BwdRow rc = bwd_row(g, rowv, row, n, c);
     const long off = static_cast<long>(c) * g.L;
     const float* x = g.X + n * g.x_bs + off;
     const float* dy = dY + n * dy_bs + off;
@@ -278,15 +395,78 @@ __global__ __launch_bounds__(RT) void adain_bwd_apply_k(AdainArgs g, const float
     for (int j = 0; j < EPT; ++j) {
         const int l = l0 + j * RT;
         if (l >= g.L) break;
-        const float xh = (xv[j] - st.x) * st.y;
-        const float s = g1 * xh + bt;
-        float unused = 0.0f;
-        const float ds = act_bwd(g.act, dv[j], s, g.slope, a, unused);
-        float v = k1 * (ds - mv.x - xh * mv.y);
-        if (r) v += rv[j];
-        dx[l] = v;
+        dx[l] = bwd_elem(g, rc, xv[j], dv[j], r != nullptr, rv[j]);
     }
 }
+
+// The 16-byte form (head / float4s / tail as adain_act_fwd_v4_k).
+__global__ __launch_bounds__(RT) void adain_bwd_apply_v4_k(AdainArgs g, const float* dY, long dy_bs,
+                                                          const float* R, long r_bs, float* dX, long dx_bs,
+                                                          const float2* rowv, const float* ap, float* dalpha,
+                                                          int N) {
+    constexpr int Q = EPT / 4;
+    const int row = blockIdx.y;
+    const int n = row / g.C, c = row - n * g.C;
+    dalpha_fold(ap, dalpha, N, g.C, n, c);
+    const long off = static_cast<long>(c) * g.L;
+    const float* x = g.X + n * g.x_bs + off;
+    const float* dy = dY + n * dy_bs + off;
+    const float* r = R ? R + n * r_bs + off : nullptr;
+    float* dx = dX + n * dx_bs + off;
+    const bool has_r = r != nullptr;
+    const int head = row_head(x, g.L);
+    const int nq = (g.L - head) >> 2;
+    // the data loads go out before the row's constants are fetched
+    const float4* x4 = reinterpret_cast<const float4*>(x + head);
+    const float4* d4 = reinterpret_cast<const float4*>(dy + head);
+    const float4* r4 = has_r ? reinterpret_cast<const float4*>(r + head) : nullptr;
+    float4* o4 = reinterpret_cast<float4*>(dx + head);
+    const int q0 = blockIdx.x * (RT * Q) + threadIdx.x;
+    const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 xv[Q], dv[Q], rv[Q];
+#pragma unroll
+    for (int j = 0; j < Q; ++j) {
+        const int q = q0 + j * RT;
+        const bool in = q < nq;
+        xv[j] = in ? x4[q] : z;
+        dv[j] = in ? d4[q] : z;
+        rv[j] = (in && has_r) ? r4[q] : z;
+    }
+    const BwdRow rc = bwd_row(g, rowv, row, n, c);
+    if (blockIdx.x == 0) {
+        const int t = threadIdx.x;
+        const int l = t < 4 ? t : head + 4 * nq + (t - 4);
+        if ((t < 4 && l < head) || (t >= 4 && t < 8 && l < g.L))
+            dx[l] = bwd_elem(g, rc, x[l], dy[l], has_r, has_r ? r[l] : 0.0f);
+    }
+#pragma unroll
+    for (int j = 0; j < Q; ++j) {
+        const int q = q0 + j * RT;
+        if (q >= nq) break;
+        float4 o;
+        o.x = bwd_elem(g, rc, xv[j].x, dv[j].x, has_r, rv[j].x);
+        o.y = bwd_elem(g, rc, xv[j].y, dv[j].y, has_r, rv[j].y);
+        o.z = bwd_elem(g, rc, xv[j].z, dv[j].z, has_r, rv[j].z);
+        o.w = bwd_elem(g, rc, xv[j].w, dv[j].w, has_r, rv[j].w);
+        o4[q] = o;
+    }
+}
+
+// Whether the 16-byte row passes apply: every base 16-B aligned and every
+// batch stride equal to the first modulo 4 floats (then a row's operands all
+// start at the same offset modulo 4).
+bool rows_v4(std::initializer_list<std::pair<const void*, long>> ops) {
+    long bs0 = -1;
+    for (const auto& o : ops) {
+        if (!o.first) continue;
+        if (reinterpret_cast<unsigned long long>(o.first) & 15u) return false;
+        if (bs0 < 0) bs0 = o.second & 3;
+        else if ((o.second & 3) != bs0) return false;
+    }
+    return true;
+}
+
+unsigned v4_blocks(int L) { return static_cast<unsigned>(std::max(1L, cdiv(static_cast<long>(L) / 4, RT * EPT / 4))); }
 
 // ─── one block per row, the row held in registers ───────────────────────
 // For rows of up to NTB*EPR elements: the forward reads x once (statistics
@@ -893,14 +1073,15 @@ int bwd_run(kdec_ctx* ctx, const AdainArgs& g, const float* dY, long dy_bs, cons
                            ctx->stream, sc.part, rows, nch, C, L, dgamma, dbeta, dgb_bs,
                            want_alpha ? sc.apart : nullptr, sc.rowv);
         if (int rc = launch_check(ctx, "adain_bwd_fin")) return rc;
-        hipLaunchKernelGGL(adain_bwd_apply_k, dim3(nch, rows), dim3(RT), 0, ctx->stream, g, dY, dy_bs, R, r_bs,
-                           dX, dx_bs, sc.rowv);
+        // the apply also folds the per-row alpha shares into dalpha
+        const float* ap = want_alpha ? sc.apart : nullptr;
+        if (rows_v4({{g.X, g.x_bs}, {dY, dy_bs}, {R, r_bs}, {dX, dx_bs}}))
+            hipLaunchKernelGGL(adain_bwd_apply_v4_k, dim3(v4_blocks(L), rows), dim3(RT), 0, ctx->stream, g, dY,
+                               dy_bs, R, r_bs, dX, dx_bs, sc.rowv, ap, dalpha, N);
+        else
+            hipLaunchKernelGGL(adain_bwd_apply_k, dim3(nch, rows), dim3(RT), 0, ctx->stream, g, dY, dy_bs, R, r_bs,
+                               dX, dx_bs, sc.rowv, ap, dalpha, N);
         if (int rc = launch_check(ctx, "adain_bwd_apply")) return rc;
-    }
-    if (want_alpha) {
-        hipLaunchKernelGGL(dalpha_reduce, dim3(static_cast<unsigned>(cdiv(C, 256))), dim3(256), 0, ctx->stream,
-                           sc.apart, dalpha, N, C);
-        return launch_check(ctx, "dalpha_reduce");
     }
     return KDEC_OK;
 }
@@ -957,15 +1138,16 @@ int adain_bwd_finish(kdec_ctx* ctx, const float* X, long x_bs, const float* stat
     // the apply with no activation: ds already carries act'
     const AdainArgs ga{X, x_bs, reinterpret_cast<const float2*>(stats), gamma, nullptr, gb_bs, KDEC_ACT_NONE, 0.0f,
                        nullptr, C, L};
-    hipLaunchKernelGGL(adain_bwd_apply_k, dim3(static_cast<unsigned>(cdiv(L, CH)), static_cast<unsigned>(rows)),
-                       dim3(RT), 0, ctx->stream, ga, ds, ds_bs, R, r_bs, dX, dx_bs, rv.as<float2>());
-    if (int rc = launch_check(ctx, "adain_bwd_apply")) return rc;
-    if (want_alpha) {
-        hipLaunchKernelGGL(dalpha_reduce, dim3(static_cast<unsigned>(cdiv(C, 256))), dim3(256), 0, ctx->stream,
-                           ap.as<float>(), dalpha, N, C);
-        return launch_check(ctx, "dalpha_reduce");
-    }
-    return KDEC_OK;
+    // (and dalpha += the per-row alpha shares, summed over utterances in order)
+    const float* apf = want_alpha ? ap.as<float>() : nullptr;
+    if (rows_v4({{X, x_bs}, {ds, ds_bs}, {R, r_bs}, {dX, dx_bs}}))
+        hipLaunchKernelGGL(adain_bwd_apply_v4_k, dim3(v4_blocks(L), static_cast<unsigned>(rows)), dim3(RT), 0,
+                           ctx->stream, ga, ds, ds_bs, R, r_bs, dX, dx_bs, rv.as<float2>(), apf, dalpha, N);
+    else
+        hipLaunchKernelGGL(adain_bwd_apply_k, dim3(static_cast<unsigned>(cdiv(L, CH)), static_cast<unsigned>(rows)),
+                           dim3(RT), 0, ctx->stream, ga, ds, ds_bs, R, r_bs, dX, dx_bs, rv.as<float2>(), apf, dalpha,
+                           N);
+    return launch_check(ctx, "adain_bwd_apply");
 }
 
 }  // namespace kdec
@@ -1037,8 +1219,12 @@ int kdec_adain_act_fwd(kdec_ctx* ctx, const float* X, long x_bs,
                "kdec_adain_act_fwd: bad activation");
     AdainArgs g{X, x_bs, reinterpret_cast<const float2*>(stats), gamma, beta, gb_bs, act, slope, alpha, C, L};
     ProfScope ps(ctx, "adain_fwd", 0);
-    hipLaunchKernelGGL(adain_act_fwd_k, dim3(static_cast<unsigned>(cdiv(L, CH)), N * C), dim3(RT), 0, ctx->stream,
-                       g, Y, y_bs, Ypre, ypre_bs);
+    if (rows_v4({{X, x_bs}, {Y, y_bs}, {Ypre, ypre_bs}}))
+        hipLaunchKernelGGL(adain_act_fwd_v4_k, dim3(v4_blocks(L), N * C), dim3(RT), 0, ctx->stream, g, Y, y_bs, Ypre,
+                           ypre_bs);
+    else
+        hipLaunchKernelGGL(adain_act_fwd_k, dim3(static_cast<unsigned>(cdiv(L, CH)), N * C), dim3(RT), 0,
+                           ctx->stream, g, Y, y_bs, Ypre, ypre_bs);
     return launch_check(ctx, "adain_act_fwd");
 }
 

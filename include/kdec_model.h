@@ -126,19 +126,21 @@ int kdec_model_decode_back_half_cancellable(kdec_model* m, int N, int T, const f
                                             kdec_cancel_fn cancel, void* user, int* cancelled);
 /* Stream overlap (no counterpart in the reference, whose calls are
  * synchronous): on = 1 (the default) runs the harmonic source and the conv
- * weight grads on a second stream beside the main chain; on = 0 keeps every
- * launch on the context's stream, in program order. Results are identical
- * either way (every reduction sums in a fixed order). */
+ * weight grads on a second stream beside the main chain, and the
+ * generator's noise branches and per-stage resblocks on that stream and a
+ * third one; on = 0 keeps every launch on the context's stream, in program
+ * order. Results are identical either way (every reduction sums in a fixed
+ * order, and the resblock outputs are summed in one order). */
 int kdec_model_set_overlap(kdec_model* m, int on);
 /* on = 1 (with overlap on and N >= 2): forwards run the batch as two
  * halves (rows [0, N - N/2) and the rest), each a whole backbone + generator
  * chain on its own stream, concurrently, and so do their backwards (the
  * second half's conv weight grads accumulate in a second buffer that is
  * added at the end). 0 (the default) keeps one chain for the whole batch.
- * On one MI355X at B = 8, T = 512 the halves shorten the forward and the
- * backward without weight grads, and lengthen the backward with them (the
- * concurrent weight-grad GEMMs contend), so the training step keeps one
- * chain. Results agree either way to the rounding of the GEMMs' split
+ * On one MI355X at B = 8, T = 512 the halves lengthen the backward with
+ * weight grads (the concurrent weight-grad GEMMs contend), and the one-chain
+ * forward already runs its resblocks on three streams, so the training step
+ * keeps one chain. Results agree either way to the rounding of the GEMMs' split
  * choices. No counterpart in the reference (its decoder runs one utterance
  * at a time); the per-utterance work is unchanged. */
 int kdec_model_set_batch_split(kdec_model* m, int on);

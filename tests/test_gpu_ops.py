@@ -466,6 +466,22 @@ def test_elementwise(K):
     assert np.all(h(F) == 3.5)
 
 
+@pytest.mark.parametrize("cols,bs,off", [(4096, 4096, 0), (4099, 4100, 0), (1024, 1028, 1)])
+def test_add3_in_order(K, cols, bs, off):
+    # (A + B) + C in float32, bit for bit: whole float4s on aligned rows of a
+    # multiple of 4, the scalar path on a ragged row and on an offset base;
+    # the output aliases A, as the generator's resblock sum uses it
+    N = 3
+    a, b, c = (rnd(N, bs + off) for _ in range(3))
+    ref = (a[:, off:off + cols] + b[:, off:off + cols]) + c[:, off:off + cols]
+    ta, tb, tc = g(a), g(b), g(c)
+    pa, pb, pc = (ctypes.c_void_p(t.data_ptr() + 4 * off) for t in (ta, tb, tc))
+    K.call("kdec_add3", pa, bs + off, pb, bs + off, pc, bs + off, pa, bs + off, N, cols)
+    out = h(ta)
+    assert np.array_equal(out[:, off:off + cols], ref.astype(np.float32))
+    assert np.array_equal(out[:, :off], a[:, :off]) and np.array_equal(out[:, off + cols:], a[:, off + cols:])
+
+
 @pytest.mark.parametrize("n_fft,hop,L,C", [(20, 5, 301, 24), (8, 2, 65, 6)])
 def test_spectral_head(K, n_fft, hop, L, C):
     N = 2
