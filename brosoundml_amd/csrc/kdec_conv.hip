@@ -501,7 +501,7 @@ __device__ inline void store_tile_stats(const GemmArgs& g, const TileGeo& T, f32
 // ping-pong over two register sets, each step's LDS reads issued between the
 // MFMAs of the step before, so the read latency hides behind matrix work.
 #ifndef CG_WPE
-#define CG_WPE 5
+#define CG_WPE 4  // 128 VGPRs: no spills (at five waves the tile spilled 8-11 registers, for no speed)
 #endif
 template <int CK>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(CG_WPE)))
@@ -1882,8 +1882,9 @@ const void* conv_q_kernel_for(int CK, int k, int epi) {
 // Input channels per K chunk: a power of two in [2, 32] so that it divides
 // the 32-padded channel count of the packed weights (no chunk runs past them),
 // at most 32 weight rows (CK*k) per chunk, and the largest such chunk whose two
-// stages fit 32 KB of LDS: five blocks per CU, the most the kernel's ~96 VGPRs
-// allow. Only when even CK = 2 is larger does the stage size set occupancy.
+// stages fit 32 KB of LDS, well inside the 40 KB per block that four blocks
+// per CU (the kernel's 128-VGPR budget) leave. Only when even CK = 2 is larger
+// does the stage size set occupancy.
 int pick_ck(int k, int s, int d) {
     int ck = 32;
     while (ck > 2 && (ck * k > 32 || conv_lds_bytes(ck, k, s, d) > 32 * 1024)) ck >>= 1;
