@@ -1672,10 +1672,29 @@ void wgrad_gemm(WgradArgs g) {
 // out[i] += sum_z P[z][i] in a fixed order.  `transpose_k`: when non-zero the
 // element i = m*NN + (c*k + t) is stored at the conv-transpose layout
 // [c][m*k + t] instead (M = C_out of the transpose, c = its input channel).
+// db[m] += sum_y part[y*M + m] (one wave per row, four rows per 256-thread
+// block `blk`; double sums in a fixed lane order)
+__device__ inline void bias_rows(const float* part, float* db, int M, int S, int blk) {
+    const int m = blk * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (m >= M) return;
+    double acc = 0.0;
+    for (int y = lane; y < S; y += 64) acc += part[static_cast<long>(y) * M + m];
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_down(acc, o, 64);
+    if (lane == 0) db[m] += static_cast<float>(acc);
+}
+
+// Blocks at and past `main_blocks` (when Pb is given) sum the bias
+// partials Pb[splits][M] into db instead, as bias_reduce would.
 __global__ void wgrad_reduce(const float* P, float* out, long MN, int splits,
-                             int transpose_k, int M, int NN) {
+                             int transpose_k, int M, int NN, const float* Pb, float* db,
+                             unsigned main_blocks) {
+    if (blockIdx.x >= main_blocks) {
+        bias_rows(Pb, db, M, splits, static_cast<int>(blockIdx.x - main_blocks));
+        return;
+    }
     for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < MN;
-         i += static_cast<long>(gridDim.x) * blockDim.x) {
+         i += static_cast<long>(main_blocks) * blockDim.x) {
         float acc = 0.0f;
         int z = 0;
         for (; z + 8 <= splits; z += 8) {  // 8 loads in flight, summed in order
@@ -1739,13 +1758,7 @@ __global__ void bias_partial(const float* G, long g_bs, float* part, int N, int 
 // db[m] += sum_y part[y, m]: one wave per m; lane j sums y = j, j+64, ... in
 // order, then a fixed shuffle tree adds the 64 lane sums.
 __global__ void bias_reduce(const float* part, float* db, int M, int S) {
-    const int m = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (m >= M) return;
-    double acc = 0.0;
-    for (int y = lane; y < S; y += 64) acc += part[static_cast<long>(y) * M + m];
-    for (int o = 32; o > 0; o >>= 1) acc += __shfl_down(acc, o, 64);
-    if (lane == 0) db[m] += static_cast<float>(acc);
+    bias_rows(part, db, M, S, static_cast<int>(blockIdx.x));
 }
 
 // ─── depthwise pool: ConvTranspose1d k3 s2 p1 op1, groups = C ──────────────
@@ -2465,16 +2478,13 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
             return fail(ctx, KDEC_EHIP, std::string(fam) + ": launch failed");
         if (int rc2 = launch_check(ctx, fam)) return rc2;
     }
+    // the weight-grad partials and, in extra blocks, the bias partials
     ProfScope ps(ctx, "wgrad_reduce", 0.0);
-    hipLaunchKernelGGL(wgrad_reduce, dim3(grid1d(MN)), dim3(256), 0, ctx->stream, P.as<float>(), out, MN,
-                       splits, 0, M, NN);
-    if (int rc = launch_check(ctx, "wgrad_reduce")) return rc;
-    if (db) {
-        hipLaunchKernelGGL(bias_reduce, dim3(static_cast<unsigned>(cdiv(M, 4))), dim3(256), 0, ctx->stream,
-                           Pb.as<float>(), db, M, splits);
-        return launch_check(ctx, "bias_reduce");
-    }
-    return KDEC_OK;
+    const unsigned mb = grid1d(MN);
+    const unsigned bb = db ? static_cast<unsigned>(cdiv(M, 4)) : 0u;
+    hipLaunchKernelGGL(wgrad_reduce, dim3(mb + bb), dim3(256), 0, ctx->stream, P.as<float>(), out, MN, splits, 0, M,
+                       NN, db ? Pb.as<float>() : nullptr, db, mb);
+    return launch_check(ctx, "wgrad_reduce");
 }
 
 // db (M) += sum over (n, l) of G[n, m, l]
