@@ -1107,15 +1107,24 @@ void generator_backward(const Generator& gen, const GeneratorCache& cache, const
         const int C_out = sc.C_out;
         Tensor d_scaled = scaled(dX, 1.0f / static_cast<float>(K));
         dX = Tensor();
-        Tensor d_m;
+        // d_m = sum_j of the resblocks' input grads, in the order j = 0, 1, ...
+        // (one pass for K = 3)
+        std::vector<Tensor> dxin(static_cast<std::size_t>(K));
         for (int j = 0; j < K; ++j) {
             const std::size_t idx = static_cast<std::size_t>(i) * K + j;
             ResBlock1Affines& dr = draff[idx];
-            Tensor dxin = resblock1_bwd(gen.resblocks[idx], sc.res[j], raff[idx].g1, raff[idx].g2, d_scaled, dr.g1,
-                                        dr.b1, dr.g2, dr.b2, wg);
-            if (j == 0) d_m = dxin;
-            else add_into(d_m, dxin);
+            dxin[static_cast<std::size_t>(j)] = resblock1_bwd(gen.resblocks[idx], sc.res[j], raff[idx].g1,
+                                                              raff[idx].g2, d_scaled, dr.g1, dr.b1, dr.g2, dr.b2, wg);
         }
+        Tensor d_m = dxin[0];
+        if (K == 3) {
+            ck(kdec_add3(kctx(), cp(d_m), rs(d_m), cp(dxin[1]), rs(dxin[1]), cp(dxin[2]), rs(dxin[2]), mp(d_m), rs(d_m),
+                         N, d_m.cols),
+               "resblock grad sum");
+        } else {
+            for (int j = 1; j < K; ++j) add_into(d_m, dxin[static_cast<std::size_t>(j)]);
+        }
+        dxin.clear();
         d_scaled = Tensor();
         {
             ResBlock1Affines& dn = dnaff[i];
