@@ -1148,10 +1148,20 @@ void generator_backward(const Generator& gen, const GeneratorCache& cache, const
             float* dW = grad_of(wg, gen.ups_W[i]);
             float* db = grad_of(wg, gen.ups_b[i]);
             if (dW || db) {
-                Tensor a = leaky(sc.x_in, 0.1f);
-                ck(kdec_convt1d_wgrad(kctx(), cp(a), rs(a), cp(du), rs(du), dW, db, N, sc.C_in, sc.L_in, C_out,
-                                      gen.ups_k[i], gen.ups_stride[i], gen.ups_pad[i], 0),
-                   "conv_transpose1d backward_weight");
+                // on the weight-grad lane when one is set (as the conv weight
+                // grads), with the leaky input recomputed there
+                kdec_ctx* k = kctx();
+                if (g_lane.side) {
+                    g_lane.fork();
+                    k = g_lane.side;
+                }
+                Tensor a = dev(N, sc.C_in * sc.L_in);
+                const int rc1 = kdec_leaky_fwd(k, cp(sc.x_in), rs(sc.x_in), mp(a), rs(a), N, a.cols, 0.1f);
+                if (rc1 != KDEC_OK) fail("generator_backward", kdec_last_error(k));
+                const int rc2 = kdec_convt1d_wgrad(k, cp(a), rs(a), cp(du), rs(du), dW, db, N, sc.C_in, sc.L_in, C_out,
+                                                   gen.ups_k[i], gen.ups_stride[i], gen.ups_pad[i], 0);
+                if (rc2 != KDEC_OK) fail("conv_transpose1d backward_weight", kdec_last_error(k));
+                if (g_lane.side) g_lane.done(a, du);  // both held until the lane is past them
             }
         }
         dX = leaky_bwd(sc.x_in, da, 0.1f);
