@@ -750,6 +750,14 @@ int kdec_model_backward(kdec_model* m, const float* daudio, int wgrad, int dalph
                 }
             }
         } lane_reset;
+        // without conv weight grads the second stream would idle: the
+        // generator's resblock and noise-branch backwards use it and the
+        // second part's context instead (one chain only)
+        const bool rb_lanes = m->parts == 1 && m->overlap && !wgrad;
+        struct ResblockLanes {
+            explicit ResblockLanes(kdec_ctx* a, kdec_ctx* b) { bd::set_resblock_lanes(a, b); }
+            ~ResblockLanes() { bd::set_resblock_lanes(nullptr, nullptr); }
+        } resblock_lanes(rb_lanes ? m->ctx2 : nullptr, rb_lanes ? m->side : nullptr);
         for (int pi = 0; pi < m->parts; ++pi) {
             kdec_model::Part& pt = m->part[pi];
             bt::set_runtime(pt.ctx);
@@ -1143,6 +1151,16 @@ int kdec_dlora_destroy(kdec_dlora* d) {
     return KDEC_OK;
 }
 
+// The resblock lanes for a DecoderLora call (one chain; none with overlap off).
+struct DlLanes {
+    explicit DlLanes(kdec_model* m) {
+        if (m->overlap) bd::set_resblock_lanes(m->ctx2, m->side);
+    }
+    ~DlLanes() { bd::set_resblock_lanes(nullptr, nullptr); }
+    DlLanes(const DlLanes&) = delete;
+    DlLanes& operator=(const DlLanes&) = delete;
+};
+
 int kdec_dlora_forward(kdec_dlora* d, int N, int T, const float* asr, const float* F0, const float* Nn,
                        const float* ref_s, long ref_bs, const float* har, const float* cond, float* audio) {
     if (!d || N <= 0 || T <= 0 || !asr || !F0 || !Nn || !ref_s || !cond || !audio) return KDEC_EINVAL;
@@ -1171,7 +1189,12 @@ int kdec_dlora_forward(kdec_dlora* d, int N, int T, const float* asr, const floa
         const Tensor rs = Tensor::view(Device::HIP, const_cast<float*>(ref_s), N, m->style_dim, bt::Dtype::FP32, ref_bs);
         brosoundml::DecoderLoraContext c{&asr_t, &F0_t, &N_t, &rs, &h, T, frames};
         d->cond = Tensor::view(Device::HIP, const_cast<float*>(cond), N, d->lora.gate().in_dim);
-        d->lora.forward(m->bb, m->gen, c, d->cond, d->audio);
+        {
+            // the generator's noise branches and resblocks on three streams,
+            // as in kdec_model_forward (forked after har exists)
+            DlLanes lanes(m);
+            d->lora.forward(m->bb, m->gen, c, d->cond, d->audio);
+        }
         d->N = N;
         d->T = T;
         if (hipMemcpyAsync(audio, d->audio.data, static_cast<size_t>(N) * alen * sizeof(float),
@@ -1191,6 +1214,7 @@ int kdec_dlora_backward(kdec_dlora* d, const float* daudio) {
         int alen = 0;
         kdec_model_lengths(m, d->T, nullptr, nullptr, &alen);
         const Tensor dA = Tensor::view(Device::HIP, const_cast<float*>(daudio), d->N, alen);
+        DlLanes lanes(m);  // the frozen decoder computes no weight grads: the side stream is free
         d->lora.backward(m->bb, m->gen, d->cond, dA);
     } catch (const std::exception& e) {
         return dlora_fail(d, KDEC_EINVAL, e.what());

@@ -1101,6 +1101,20 @@ void generator_backward(const Generator& gen, const GeneratorCache& cache, const
     spectral_head_backward(gen.conv_post, cache.head, cache.window, gen.n_fft, gen.hop_size, gen.win_size, dAudio,
                            dX, wg);
     const int N = dAudio.rows;
+    // With the resblock lanes set (the caller does so when no conv weight
+    // grads occupy a second stream), each stage's resblock backwards run on
+    // the runtime stream and both lanes, and every stage's noise branch
+    // backward on lane 1 (its input grad feeds only weight grads, so the
+    // runtime stream joins it once, at the end). The tensors lane work reads
+    // are held until that join.
+    kdec_ctx* const main_ctx = kctx();
+    const bool par = g_branch.on() && K == 3;
+    std::vector<Tensor> lane_inputs;
+    hipEvent_t noise_last = nullptr;
+    auto record_on = [](hipEvent_t e, kdec_ctx* c) {
+        if (hipEventRecord(e, static_cast<hipStream_t>(kdec_get_stream(c))) != hipSuccess)
+            fail("generator_backward", "event record failed");
+    };
     for (int i = U - 1; i >= 0; --i) {
         const GenStageCache& sc = cache.stages[i];
         const int L = sc.L_out;
@@ -1109,13 +1123,19 @@ void generator_backward(const Generator& gen, const GeneratorCache& cache, const
         dX = Tensor();
         // d_m = sum_j of the resblocks' input grads, in the order j = 0, 1, ...
         // (one pass for K = 3)
+        if (par) g_branch.fork(main_ctx);
         std::vector<Tensor> dxin(static_cast<std::size_t>(K));
         for (int j = 0; j < K; ++j) {
             const std::size_t idx = static_cast<std::size_t>(i) * K + j;
             ResBlock1Affines& dr = draff[idx];
+            kdec_ctx* const cj = par ? g_branch.ctx_for(j, main_ctx) : main_ctx;
+            RuntimeScope scope(cj);
             dxin[static_cast<std::size_t>(j)] = resblock1_bwd(gen.resblocks[idx], sc.res[j], raff[idx].g1,
                                                               raff[idx].g2, d_scaled, dr.g1, dr.b1, dr.g2, dr.b2, wg);
+            if (par && j > 0) record_on(g_branch.event(static_cast<std::size_t>(j) + 1), cj);
         }
+        if (par)
+            for (int j = 1; j < K; ++j) BranchLanes::wait_on(main_ctx, g_branch.event(static_cast<std::size_t>(j) + 1));
         Tensor d_m = dxin[0];
         if (K == 3) {
             ck(kdec_add3(kctx(), cp(d_m), rs(d_m), cp(dxin[1]), rs(dxin[1]), cp(dxin[2]), rs(dxin[2]), mp(d_m), rs(d_m),
@@ -1128,9 +1148,20 @@ void generator_backward(const Generator& gen, const GeneratorCache& cache, const
         d_scaled = Tensor();
         {
             ResBlock1Affines& dn = dnaff[i];
+            kdec_ctx* const nl = par ? g_branch.lane[1] : main_ctx;
+            if (par) {
+                record_on(g_branch.noise_event(static_cast<std::size_t>(i)), main_ctx);
+                BranchLanes::wait_on(nl, g_branch.noise_event(static_cast<std::size_t>(i)));
+                lane_inputs.push_back(d_m);
+            }
+            RuntimeScope scope(nl);
             Tensor dsrc_in = resblock1_bwd(gen.noise_res[i], sc.noise, naff[i].g1, naff[i].g2, d_m, dn.g1, dn.b1,
                                            dn.g2, dn.b2, wg);
             if (wg) conv_wgrad(gen.noise_convs[i], wg, cache.har, cache.frames, dsrc_in);
+            if (par) {
+                noise_last = g_branch.noise_event(static_cast<std::size_t>(U + i));
+                record_on(noise_last, nl);
+            }
         }
         Tensor du = d_m;
         if (i == U - 1) {
@@ -1166,6 +1197,8 @@ void generator_backward(const Generator& gen, const GeneratorCache& cache, const
         }
         dX = leaky_bwd(sc.x_in, da, 0.1f);
     }
+    if (noise_last) BranchLanes::wait_on(main_ctx, noise_last);  // lane 1 is in order: its last event covers all
+    lane_inputs.clear();
     dGenIn = dX;
 }
 

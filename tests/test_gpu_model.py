@@ -130,6 +130,44 @@ def test_single_stream_equals_overlapped(ctx):
         np.testing.assert_array_equal(res[0][2][n], res[1][2][n], err_msg=n)
 
 
+def test_reference_semantics_three_resblock_streams(ctx):
+    # without conv weight grads the generator's resblock and noise-branch
+    # backwards run on three streams (K = 3 here): the affine grads and
+    # d(style) the reference returns, against the oracle at the usual bars
+    r = run_pair(ctx, C.SMALL, 2, 6, "gm.ref3", wgrad=False, dalpha=False)
+    check_pair(r, wgrad=False)
+
+
+def test_no_weight_grad_backward_single_stream_equals_overlapped(ctx):
+    # the same bit-for-bit property as above for the backward without conv
+    # weight grads (its resblocks on three streams), with alpha grads on and off
+    from brosoundml_amd import native
+    cfg, N, T = C.SMALL, 2, 6
+    m = native.Model(ctx, cfg)
+    shapes = m.param_shapes()
+    m.set_params(synth.init_params(shapes))
+    asr, F0, Nn, style, dA = inputs(cfg, N, T, "gm.ovl2")
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    t = [dev(a) for a in (asr, F0, Nn, style)]
+    d = dev(dA)
+    for dalpha in (False, True):
+        res = []
+        for on in (True, False):
+            m.set_overlap(on)
+            m.zero_grad()
+            m.forward(*t, T)
+            ds = torch.empty_like(t[3])
+            m.backward(d, wgrad=False, dalpha=dalpha, dstyle=ds)
+            torch.cuda.synchronize()
+            _, dgb = m.affines(N)
+            res.append((ds.cpu().numpy(), np.array(dgb), {n: m.grad(n, s) for n, s in shapes.items() if "alpha" in n}))
+        m.set_overlap(True)
+        np.testing.assert_array_equal(res[0][0], res[1][0])
+        np.testing.assert_array_equal(res[0][1], res[1][1])
+        for n in res[0][2]:
+            np.testing.assert_array_equal(res[0][2][n], res[1][2][n], err_msg=n)
+
+
 @pytest.mark.parametrize("split", [True, False])
 def test_batch_split_vs_oracle(ctx, split):
     # kdec_model_set_batch_split(1) runs a batch of N >= 2 as two half-batch
