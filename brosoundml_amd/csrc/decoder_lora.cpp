@@ -288,8 +288,10 @@ DecoderLora& DecoderLora::operator=(DecoderLora&& o) noexcept {
         style_keep_ = std::move(o.style_keep_);
         bb_cache_ = o.bb_cache_;
         gen_cache_ = o.gen_cache_;
+        har_ready_ = o.har_ready_;
         o.bb_cache_ = nullptr;
         o.gen_cache_ = nullptr;
+        o.har_ready_ = nullptr;
     }
     return *this;
 }
@@ -378,8 +380,15 @@ void DecoderLora::forward(const DecoderBackbone& bb, const Generator& gen, const
     if (!gen_cache_) gen_cache_ = new bd::GeneratorCache();
     bd::decoder_backbone_forward_train(bb, *ctx.asr, *ctx.F0_pred, *ctx.N_pred, ctx.total, bba, 1e-5f, gen_in_,
                                        *static_cast<bd::BackboneCache*>(bb_cache_));
-    bd::generator_forward_train(gen, gen_in_, 2 * ctx.total, *ctx.har, ctx.frames, na, ra, audio,
-                                *static_cast<bd::GeneratorCache*>(gen_cache_));
+    auto& gc = *static_cast<bd::GeneratorCache*>(gen_cache_);
+    gc.har_ready = har_ready_;  // the generator waits for it before reading har
+    har_ready_ = nullptr;
+    bd::generator_forward_train(gen, gen_in_, 2 * ctx.total, *ctx.har, ctx.frames, na, ra, audio, gc);
+    if (gc.har_ready) {  // not consumed (no upsample stage read har): join here
+        if (hipStreamWaitEvent(stream(), static_cast<hipEvent_t>(gc.har_ready), 0) != hipSuccess)
+            fail("DecoderLora::forward", "waiting for the harmonic source");
+        gc.har_ready = nullptr;
+    }
 }
 
 void DecoderLora::backward(const DecoderBackbone& bb, const Generator& gen, const Tensor& cond, const Tensor& dAudio) {

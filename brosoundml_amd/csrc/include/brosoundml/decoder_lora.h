@@ -113,6 +113,11 @@ public:
 
     // Stacked device buffers (for bindings and tests): 0 A, 1 B, 2 dA, 3 dB.
     const brotensor::Tensor& stacked(int which) const;
+    // Extension (the reference computes har before the call): a hipEvent_t
+    // recorded after the work that writes the context's har on another
+    // stream; the next forward makes the generator's noise branches wait for
+    // it instead of assuming har is complete. Used once, then cleared.
+    void set_har_ready(void* hip_event) { har_ready_ = hip_event; }
     // Unit i's first row in B / the affine buffers.
     const std::vector<int>& unit_offsets() const { return unit_off_host_; }
 
@@ -141,6 +146,7 @@ private:
     brotensor::Tensor style_keep_;
     void* bb_cache_ = nullptr;   // detail::BackboneCache
     void* gen_cache_ = nullptr;  // detail::GeneratorCache
+    void* har_ready_ = nullptr;  // see set_har_ready
 };
 
 }  // namespace brosoundml

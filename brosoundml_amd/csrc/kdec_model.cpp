@@ -1178,11 +1178,26 @@ int kdec_dlora_forward(kdec_dlora* d, int N, int T, const float* asr, const floa
         } else {  // HarmonicSource::forward on the model's l_linear
             d->har = Tensor::empty_on(Device::HIP, N, har_cols);
             const auto& hs = m->hs;
-            if (int rc = kdec_harmonic_source(m->ctx, F0, 2 * T, d->har.f32(), har_cols, N, 2 * T,
+            // with overlap, on the side stream beside the backbone (as
+            // kdec_model_forward runs it); the generator waits for its event
+            kdec_ctx* hc = m->ctx;
+            hipStream_t ms = static_cast<hipStream_t>(kdec_get_stream(m->ctx));
+            if (m->overlap) {
+                if (hipEventRecord(m->ev_fork, ms) != hipSuccess ||
+                    hipStreamWaitEvent(m->side->stream, m->ev_fork, 0) != hipSuccess)
+                    return dlora_fail(d, KDEC_EHIP, "kdec_dlora_forward: fork");
+                hc = m->side;
+            }
+            if (int rc = kdec_harmonic_source(hc, F0, 2 * T, d->har.f32(), har_cols, N, 2 * T,
                                               static_cast<const float*>(hs.l_linear.W.data),
                                               static_cast<const float*>(hs.l_linear.b.data), hs.harmonic_num,
                                               hs.sample_rate, hs.upsample_scale, hs.n_fft, hs.hop_size))
-                return rc;
+                return dlora_fail(d, rc, std::string("harmonic source: ") + kdec_last_error(hc));
+            if (m->overlap) {
+                if (hipEventRecord(m->ev_join, m->side->stream) != hipSuccess)
+                    return dlora_fail(d, KDEC_EHIP, "kdec_dlora_forward: join");
+                d->lora.set_har_ready(m->ev_join);
+            }
             h = d->har;
         }
         const Tensor asr_t = in(asr, m->asr_dim * T), F0_t = in(F0, 2 * T), N_t = in(Nn, 2 * T);
