@@ -420,6 +420,44 @@ def test_adain_act(K, act, C, L):
         assert_close(h(da), rda, GRAD_TOL, "snake dAlpha")
 
 
+@pytest.mark.parametrize("C,L", [(3, 1500), (2, 70000)])
+def test_adain_snake_large_arguments(K, C, L):
+    # alpha in [6, 10] and (1 + gamma) ~ 9: |alpha * s| reaches several hundred,
+    # where the Snake's sin^2 and the backward's (sin^2, sin 2th) come from a
+    # multi-turn argument reduction; row kernel (1500) and chunked passes
+    N = 2
+    x = rnd(N, C, L, scale=1.1)
+    gm = (8.0 + rnd(N, C, scale=0.5)).astype(np.float32)
+    bt = rnd(N, C, scale=2.0)
+    alpha = rng.uniform(6.0, 10.0, C).astype(np.float32)
+    st = torch.empty(N * C, 2, device="cuda")
+    K.call("kdec_instnorm_stats", P(g(x)), C * L, N, C, L, 1e-5, P(st))
+    Y = torch.empty(N, C, L, device="cuda")
+    K.call("kdec_adain_act_fwd", P(g(x)), C * L, P(st), P(g(gm)), P(g(bt)), C, ACTS["snake"], 0.0, P(g(alpha)),
+           P(Y), C * L, None, 0, N, C, L)
+    pre = [O.adain_affine(x[n], gm[n], bt[n], C, L) for n in range(N)]
+    assert max(float(np.abs(p.reshape(C, L) * alpha[:, None]).max()) for p in pre) > 150.0
+    assert_close(h(Y), np.stack([O.snake(pre[n], alpha, C, L) for n in range(N)]), FWD_TOL, "snake forward")
+    dY = rnd(N, C, L)
+    dX = torch.empty(N, C, L, device="cuda")
+    dg, db = torch.empty(N, C, device="cuda"), torch.empty(N, C, device="cuda")
+    da = torch.zeros(C, device="cuda")
+    K.call("kdec_adain_act_bwd", P(g(x)), C * L, P(st), P(g(gm)), P(g(bt)), C, ACTS["snake"], 0.0, P(g(alpha)),
+           P(g(dY)), C * L, None, 0, P(dX), C * L, P(dg), P(db), C, P(da), N, C, L)
+    rdx, rdg, rdb, rda = [], [], [], np.zeros(C)
+    for n in range(N):
+        ds, a_ = O.snake_bwd(pre[n], alpha, dY[n].ravel(), C, L)
+        rda += a_
+        dx, dgg, dbb = O.adain_affine_bwd(x[n], gm[n], ds, C, L)
+        rdx.append(dx)
+        rdg.append(dgg)
+        rdb.append(dbb)
+    assert_close(h(dX), np.stack(rdx), GRAD_TOL, "snake dX")
+    assert_close(h(dg), np.stack(rdg), GRAD_TOL, "snake dGamma")
+    assert_close(h(db), np.stack(rdb), GRAD_TOL, "snake dBeta")
+    assert_close(h(da), rda, GRAD_TOL, "snake dAlpha")
+
+
 @pytest.mark.parametrize("act", ["leaky", "snake"])
 # 4-byte row kernel (1500), 16-byte row kernel (8192), chunked passes (70000),
 # long row with a head and rest (4 x 61441)
