@@ -218,6 +218,7 @@ __device__ inline long hs_index(int t, int i, int NH) {
 }
 
 // Pass 1: start[fr * NH + i] = the phase of chain i entering frame fr.
+constexpr int HS_UNROLL = 150;  // steps per unrolled trip (divides the 300-sample frames)
 __global__ __launch_bounds__(64) void hs_start_k(const float* F0, long f0_bs, float* start, int N, int H,
                                                  int frame_count, int us, int sig_len, int nfr, float sr) {
     const int NH = N * H;
@@ -232,7 +233,14 @@ __global__ __launch_bounds__(64) void hs_start_k(const float* F0, long f0_bs, fl
         f0 = f0r[min(fr + 1, frame_count - 1)];  // next frame's, used after this frame's chain
         start[static_cast<long>(fr) * NH + i] = ph;
         const int n = min(us, sig_len - fr * us);
+        // long unrolled runs: the loop's scalar count / compare / branch
+        // otherwise take issue cycles between the chain's dependent
+        // operations (150 steps per trip: 3.18 -> 1.97 ms at 8 x 307200)
         int t = 0;
+        for (; t + HS_UNROLL <= n; t += HS_UNROLL) {
+#pragma unroll
+            for (int u = 0; u < HS_UNROLL; ++u) ph = hs_step(ph, omega);
+        }
         for (; t + 4 <= n; t += 4) {
             ph = hs_step(ph, omega);
             ph = hs_step(ph, omega);
