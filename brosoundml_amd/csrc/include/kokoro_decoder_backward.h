@@ -244,6 +244,12 @@ struct GeneratorCache {
     // the first noise conv, after stage 0's upsampling, so that work overlaps
     // the producer; the forward clears it.
     void*                      har_ready = nullptr;
+    // Extension: a hipEvent_t recorded on the runtime stream after the
+    // generator's affine inputs are written (and after everything an earlier
+    // step left on that stream). With it and har_ready set, the noise branches
+    // on the resblock lanes wait for these two only, not for the runtime
+    // stream's backbone work queued since; the forward clears it.
+    void*                      inputs_ready = nullptr;
 };
 
 void generator_forward_train(const Generator& gen,

@@ -695,8 +695,10 @@ int kdec_model_forward(kdec_model* m, int N, int T, const float* asr, const floa
             const int init_C = m->dec_out[n_dec - 1];
             const int L_gen = pt.gen_in.cols / init_C;
             Tensor out;
-            // the generator waits for har itself, after stage 0's upsampling
+            // the generator waits for har itself, after stage 0's upsampling;
+            // ev_fork (recorded after the style projection) covers its affines
             pt.genc.har_ready = forked ? static_cast<void*>(m->ev_join) : nullptr;
+            pt.genc.inputs_ready = forked && m->parts == 1 ? static_cast<void*>(m->ev_fork) : nullptr;
             bd::generator_forward_train(m->gen, pt.gen_in, L_gen, har_p, frames, pt.naff, pt.raff, out, pt.genc);
             hipStream_t ps = static_cast<hipStream_t>(kdec_get_stream(pt.ctx));
             if (pt.genc.har_ready) {  // no noise conv consumed it: join here

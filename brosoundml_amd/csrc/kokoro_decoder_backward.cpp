@@ -971,14 +971,24 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
     // beside stage 0's); each stage's runtime stream waits for its own.
     kdec_ctx* const main_ctx = kctx();
     const bool par = g_branch.on();
+    if (!par) cache.inputs_ready = nullptr;
     std::vector<Tensor> srcs(static_cast<std::size_t>(U));
     std::vector<int> src_len(static_cast<std::size_t>(U), 0);
     if (par) {
-        g_branch.fork(main_ctx);  // har may have been written on the runtime stream
-        if (cache.har_ready) {
-            for (kdec_ctx* c : g_branch.lane) BranchLanes::wait_on(c, static_cast<hipEvent_t>(cache.har_ready));
-            cache.har_ready = nullptr;  // the runtime stream joins through the noise events
+        if (cache.har_ready && cache.inputs_ready) {
+            // har and the affines are all the noise branches read besides
+            // their weights: they need not wait for the backbone
+            for (kdec_ctx* c : g_branch.lane) {
+                BranchLanes::wait_on(c, static_cast<hipEvent_t>(cache.inputs_ready));
+                BranchLanes::wait_on(c, static_cast<hipEvent_t>(cache.har_ready));
+            }
+        } else {
+            g_branch.fork(main_ctx);  // har may have been written on the runtime stream
+            if (cache.har_ready)
+                for (kdec_ctx* c : g_branch.lane) BranchLanes::wait_on(c, static_cast<hipEvent_t>(cache.har_ready));
         }
+        cache.har_ready = nullptr;  // the runtime stream joins through the noise events
+        cache.inputs_ready = nullptr;
         for (int i = 0; i < U; ++i) {
             kdec_ctx* const nl = g_branch.noise_lane(i);
             RuntimeScope scope(nl);
