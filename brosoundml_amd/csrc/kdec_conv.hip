@@ -234,7 +234,11 @@ __device__ inline void store_tile(const GemmArgs& g, const TileGeo& T, int tile,
         // read 0. The whole byte offset goes in the VGPR offset, since the
         // scalar offset of a buffer access is not range checked; ybuf keeps
         // it below 2^31 for every row of the tile.
-        const int rowb = g.C_out * g.L_y * 4;
+        // L_y through an empty asm: the row offsets below are then formed
+        // here, not hoisted to the kernel's start and held through the k-loop
+        int Ly = g.L_y;
+        asm volatile("" : "+s"(Ly));
+        const int rowb = g.C_out * Ly * 4;
         const __amdgpu_buffer_rsrc_t yr = uniform_rsrc(Yb, rowb);
         const __amdgpu_buffer_rsrc_t rr = uniform_rsrc(Rb ? Rb : Yb, Rb ? rowb : 0);
         const __amdgpu_buffer_rsrc_t br = uniform_rsrc(g.bias ? g.bias : Yb, g.bias ? g.C_out * 4 : 0);
@@ -243,13 +247,13 @@ __device__ inline void store_tile(const GemmArgs& g, const TileGeo& T, int tile,
         for (int tn = 0; tn < 2; ++tn) {
             const int q = q0 + wn * 64 + tn * 32 + l32;
             if (q >= n_q) continue;
-            const int vo = (mrow * g.L_y + q * os + oo) * 4;
+            const int vo = (mrow * Ly + q * os + oo) * 4;
 #pragma unroll
             for (int tm = 0; tm < 2; ++tm) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int dm = tm * 32 + 8 * (e >> 2) + (e & 3);  // uniform row step
-                    const int o = vo + dm * g.L_y * 4;
+                    const int o = vo + dm * Ly * 4;
                     float v = acc[tm][tn][e];
                     if (g.bias)
                         v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(br, (mrow + dm) * 4, 0, 0));
@@ -362,7 +366,9 @@ __device__ inline void store_tile_adain(const GemmArgs& g, const TileGeo& T, con
         pal[tid] = a;
     }
     __syncthreads();
-    const int rowb = g.C_out * g.L_y * 4;
+    int Ly = g.L_y;  // through an empty asm, as in store_tile
+    asm volatile("" : "+s"(Ly));
+    const int rowb = g.C_out * Ly * 4;
     const __amdgpu_buffer_rsrc_t yr = uniform_rsrc(g.Y + static_cast<long>(b) * g.y_bs, rowb);
     const __amdgpu_buffer_rsrc_t xr = uniform_rsrc(g.ad.x + static_cast<long>(b) * g.ad.x_bs, rowb);
     const int mrow = m0 + wm * 64 + 4 * hi;
@@ -376,11 +382,11 @@ __device__ inline void store_tile_adain(const GemmArgs& g, const TileGeo& T, con
         for (int tn = 0; tn < 2; ++tn) {
             const int q = q0 + wn * 64 + tn * 32 + l32;
             if (q >= n_q) continue;
-            const int vo = (mrow * g.L_y + q) * 4;
+            const int vo = (mrow * Ly + q) * 4;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int dm = tm * 32 + 8 * (e >> 2) + (e & 3);
-                const int o = vo + dm * g.L_y * 4;
+                const int o = vo + dm * Ly * 4;
                 const int rl = wm * 64 + 4 * hi + dm;
                 const float4 pr = prm[rl];
                 const float x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, o, 0, 0));
@@ -425,7 +431,9 @@ __device__ inline float lane_value(float v, int src) {
 __device__ inline void store_tile_stats(const GemmArgs& g, const TileGeo& T, f32x16 (&acc)[2][2], int wm, int wn,
                                         int hi, int l32) {
     const int b = T.b, n_q = T.n_q, m0 = T.m0, q0 = T.q0;
-    const int rowb = g.C_out * g.L_y * 4;
+    int Ly = g.L_y;  // through an empty asm, as in store_tile
+    asm volatile("" : "+s"(Ly));
+    const int rowb = g.C_out * Ly * 4;
     const float* Rb = g.R ? g.R + static_cast<long>(b) * g.r_bs : nullptr;
     const __amdgpu_buffer_rsrc_t yr = uniform_rsrc(g.Y + static_cast<long>(b) * g.y_bs, rowb);
     const __amdgpu_buffer_rsrc_t rr = uniform_rsrc(Rb ? Rb : g.Y, Rb ? rowb : 0);
@@ -443,11 +451,11 @@ __device__ inline void store_tile_stats(const GemmArgs& g, const TileGeo& T, f32
         for (int tn = 0; tn < 2; ++tn) {
             const int q = q0 + wn * 64 + tn * 32 + l32;
             const bool qin = q < n_q;
-            const int vo = (mrow * g.L_y + q) * 4;
+            const int vo = (mrow * Ly + q) * 4;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int dm = tm * 32 + 8 * (e >> 2) + (e & 3);
-                const int o = vo + dm * g.L_y * 4;
+                const int o = vo + dm * Ly * 4;
                 float v = acc[tm][tn][e];
                 if (g.bias)
                     v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(br, (mrow + dm) * 4, 0, 0));
@@ -680,6 +688,29 @@ void conv_gemm(GemmArgs g) {
 // the others out of the k-loop's register allocation.
 enum { QEPI_STORE = 0, QEPI_ADAIN_BWD = 1, QEPI_STATS = 2 };
 
+// Where a conv_gemm_q tile stages its operands from (wave-uniform): the
+// m-tile's weight panel, the utterance's input rows and the input window.
+struct QSrc {
+    const float* A;
+    __amdgpu_buffer_rsrc_t xrs;
+    int x0;      // first staged position
+    int Lm, xm;  // 16-B staging: row length and window start, mod 4 (0 otherwise)
+    bool x4;     // the window lies inside the row: staged 16 B per lane
+};
+
+__device__ inline QSrc q_src(const GemmArgs& g, const TileGeo& T, int span, int chunk_floats) {
+    QSrc s;
+    const float* Xb = g.X + static_cast<long>(T.b) * g.x_bs;
+    s.A = g.A + static_cast<long>(T.m0 / BM) * (g.cin_pad / g.CK) * chunk_floats;
+    s.xrs = uniform_rsrc(Xb, g.C_in * g.L_in * 4);
+    s.x0 = T.q0 - T.p;
+    s.x4 = s.x0 >= 3 && s.x0 + span <= g.L_in;
+    const int base_f = static_cast<int>((reinterpret_cast<unsigned long long>(Xb) >> 2) & 3);
+    s.Lm = s.x4 ? (g.L_in & 3) : 0;
+    s.xm = s.x4 ? ((base_f + s.x0) & 3) : 0;
+    return s;
+}
+
 template <int CK, int KT, int EPI>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(CGQ_WPE)))
 void conv_gemm_q(GemmArgs g) {
@@ -691,47 +722,38 @@ void conv_gemm_q(GemmArgs g) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave & 1, wn = wave >> 1;
-    const int l32 = lane & 31, hi = lane >> 5;
+    const int wm0 = wave & 1, wn0 = wave >> 1;
+    const int l320 = lane & 31, hi0 = lane >> 5;
 
     int tile, part;
     if (!block_work(g, tile, part)) return;  // uniform per block
-    TileGeo T;
-    decode_tile(g, tile, T);
-    const int b = T.b, d = T.d, p = T.p, n_q = T.n_q;
-    const int m0 = T.m0;
-    const int q0 = T.q0;
-    if (q0 >= n_q) return;  // uniform per block
 
-    const int span = BN + (KT - 1) * d;  // staged input window (stride 1)
-    const int span_p = (span + 3 + 255) & ~255;
-    const int segs = span_p >> 6;
-    const int stage = QA + CK * span_p;
-    const float* Xb = g.X + static_cast<long>(b) * g.x_bs;
-    const int x0 = q0 - p;
+    const int span = BN + (KT - 1) * g.d;  // staged input window (stride 1)
+    const int span_p0 = (span + 3 + 255) & ~255;
+    const int segs = span_p0 >> 6;
+    const int stage = QA + CK * span_p0;
     const int nchunks = g.cin_pad / CK;
-    const float* Ablk = g.A + static_cast<long>(m0 / BM) * nchunks * QA + lane * 4;
-    const __amdgpu_buffer_rsrc_t xrs = uniform_rsrc(Xb, g.C_in * g.L_in * 4);
-    const bool x4 = x0 >= 3 && x0 + span <= g.L_in;  // uniform per tile
-    const int base_f = static_cast<int>((reinterpret_cast<unsigned long long>(Xb) >> 2) & 3);
-    const int Lm = x4 ? (g.L_in & 3) : 0;
-    const int xm = x4 ? ((base_f + x0) & 3) : 0;
+    const int nparts = part < 0 ? 1 : g.fsplit;
+    const int pp = part < 0 ? 0 : part;
+    const int ch0 = pp * nchunks / nparts;
+    const int ch1 = (pp + 1) * nchunks / nparts;
 
-    // Stage chunk `ch` at LDS float offset `sb`: the weight slab 1 KB per
-    // instruction, the input window as conv_gemm stages it.
-    auto issue = [&](int ch, int sb) {
-        const float* Ag = Ablk + static_cast<long>(ch) * QA;
+    // Stage chunk `ch` of tile Tg at LDS float offset `sb`: the weight slab
+    // 1 KB per instruction, the input window as conv_gemm stages it.
+    auto issue = [&](const TileGeo& Tg, int ch, int sb) {
+        const QSrc s = q_src(g, Tg, span, QA);
+        const float* Ag = s.A + static_cast<long>(ch) * QA + lane * 4;
         for (int i = wave; i < QA / 256; i += 4)
             __builtin_amdgcn_global_load_lds(Ag + i * 256, smem + sb + i * 256, 16, 0, 0);
-        if (x4) {
-            const int seg4 = span_p >> 8;
+        if (s.x4) {
+            const int seg4 = span_p0 >> 8;
             for (int it = wave; it < CK * seg4; it += 4) {
                 const int r = it / seg4, sg = it - r * seg4;
                 const int c = ch * CK + r;
-                const int pos = x0 - ((c * Lm + xm) & 3) + sg * 256 + lane * 4;
+                const int pos = s.x0 - ((c * s.Lm + s.xm) & 3) + sg * 256 + lane * 4;
                 const unsigned off = c < g.C_in ? static_cast<unsigned>(c * g.L_in + pos) * 4u : 0x80000000u;
                 if (sg * 256 + lane * 4 < span + 3)
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + QA + r * span_p + sg * 256, 16,
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.xrs, smem + sb + QA + r * span_p0 + sg * 256, 16,
                                                              static_cast<int>(off), 0, 0, 0);
             }
             return;
@@ -739,15 +761,31 @@ void conv_gemm_q(GemmArgs g) {
         for (int it = wave; it < CK * segs; it += 4) {
             const int r = it / segs, sg = it - r * segs;
             const int c = ch * CK + r;
-            const int pos = x0 + sg * 64 + lane;
+            const int pos = s.x0 + sg * 64 + lane;
             const unsigned off = (c < g.C_in && pos >= 0 && pos < g.L_in)
                                      ? static_cast<unsigned>(c * g.L_in + pos) * 4u : 0x80000000u;
             if (sg * 64 + lane < span)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, smem + sb + QA + r * span_p + sg * 64, 4,
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(s.xrs, smem + sb + QA + r * span_p0 + sg * 64, 4,
                                                          static_cast<int>(off), 0, 0, 0);
         }
     };
 
+    TileGeo T;
+    decode_tile(g, tile, T);
+    if (T.q0 >= T.n_q) return;  // uniform per block (stride-1 plain tiles never are)
+    if (ch0 < ch1) issue(T, ch0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    // The lane coordinates and the staging geometry pass through an empty asm
+    // after the prologue, the tile is decoded again for the epilogue from a
+    // laundered index, and the staging source is formed at each issue: what
+    // the MFMA loop and the epilogue derive from these (per-step LDS offsets,
+    // per-element row offsets, descriptors) is then formed where it is used,
+    // not hoisted to the kernel's start and held live through the MFMA loop
+    // (measured: 2-3% on the stride-1 decoder convs).
+    int wm = wm0, wn = wn0, hi = hi0, l32 = l320, span_p = span_p0, d = g.d;
+    asm volatile("" : "+s"(wm), "+s"(wn), "+v"(hi), "+v"(l32), "+s"(span_p), "+s"(d));
+    int sb = 0;  // LDS stage of the chunk in hand
     f32x16 acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -758,22 +796,15 @@ void conv_gemm_q(GemmArgs g) {
 
     const int am = wm * 64 + l32;
     const int bq = wn * 64 + l32;
-    const int nparts = part < 0 ? 1 : g.fsplit;
-    const int pp = part < 0 ? 0 : part;
-    const int ch0 = pp * nchunks / nparts;
-    const int ch1 = (pp + 1) * nchunks / nparts;
-    const bool live = q0 + wn * 64 < n_q;  // wave-uniform
-
-    if (ch0 < ch1) issue(ch0, 0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    const bool live = T.q0 + wn * 64 < T.n_q;  // wave-uniform
     for (int ch = ch0; ch < ch1; ++ch) {
-        const int sb = ((ch - ch0) & 1) * stage;
-        if (ch + 1 < ch1) issue(ch + 1, stage - sb);
+        if (ch + 1 < ch1) issue(T, ch + 1, stage - sb);
         if (live) {
+            const QSrc cur = q_src(g, T, span, QA);
             const f32x4* Aq = reinterpret_cast<const f32x4*>(smem + sb) + hi * BM + am;
             const int xb = sb + QA + hi * span_p + bq;
-            const int dl = (ch * CK + hi) * Lm + xm;
+            const int dl = (ch * CK + hi) * cur.Lm + cur.xm;
+            const int Lm = cur.Lm;
             auto ldb = [&](int u, float& b0, float& b1) {
                 const int t = u / HS;
                 const int cc = (u - t * HS) * 2;
@@ -816,20 +847,27 @@ void conv_gemm_q(GemmArgs g) {
         }
         __builtin_amdgcn_s_waitcnt(0);  // this wave's staging loads landed
         __syncthreads();
+        sb = stage - sb;
     }
 
+    int te = tile;
+    asm volatile("" : "+s"(te));
+    TileGeo Te;
+    decode_tile(g, te, Te);
     if constexpr (EPI == QEPI_ADAIN_BWD) {
         if (part < 0) {  // uniform per block
-            store_tile_adain(g, T, acc, wm, wn, hi, l32, smem);
-            return;
+            store_tile_adain(g, Te, acc, wm, wn, hi, l32, smem);
+        } else {
+            store_tile(g, Te, te, part, acc, wm, wn, hi, l32);
         }
     } else if constexpr (EPI == QEPI_STATS) {
-        if (part < 0) {
-            store_tile_stats(g, T, acc, wm, wn, hi, l32);
-            return;
-        }
+        if (part < 0)
+            store_tile_stats(g, Te, acc, wm, wn, hi, l32);
+        else
+            store_tile(g, Te, te, part, acc, wm, wn, hi, l32);
+    } else {
+        store_tile(g, Te, te, part, acc, wm, wn, hi, l32);
     }
-    store_tile(g, T, tile, part, acc, wm, wn, hi, l32);
 }
 
 // Stride-1 correlation (conv forward, conv input-grad, each transposed-conv

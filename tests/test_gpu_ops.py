@@ -424,12 +424,14 @@ def test_adain_act(K, act, C, L):
 def test_adain_snake_large_arguments(K, C, L):
     # alpha in [6, 10] and (1 + gamma) ~ 9: |alpha * s| reaches several hundred,
     # where the Snake's sin^2 and the backward's (sin^2, sin 2th) come from a
-    # multi-turn argument reduction; row kernel (1500) and chunked passes
+    # multi-turn argument reduction; row kernel (1500) and chunked passes.
+    # Inputs from a generator of the test's own, whatever ran before it.
     N = 2
-    x = rnd(N, C, L, scale=1.1)
-    gm = (8.0 + rnd(N, C, scale=0.5)).astype(np.float32)
-    bt = rnd(N, C, scale=2.0)
-    alpha = rng.uniform(6.0, 10.0, C).astype(np.float32)
+    r = np.random.default_rng(1000 + L)
+    x = (r.standard_normal((N, C, L)) * 1.1).astype(np.float32)
+    gm = (8.0 + r.standard_normal((N, C)) * 0.5).astype(np.float32)
+    bt = (r.standard_normal((N, C)) * 2.0).astype(np.float32)
+    alpha = r.uniform(6.0, 10.0, C).astype(np.float32)
     st = torch.empty(N * C, 2, device="cuda")
     K.call("kdec_instnorm_stats", P(g(x)), C * L, N, C, L, 1e-5, P(st))
     Y = torch.empty(N, C, L, device="cuda")
@@ -438,7 +440,7 @@ def test_adain_snake_large_arguments(K, C, L):
     pre = [O.adain_affine(x[n], gm[n], bt[n], C, L) for n in range(N)]
     assert max(float(np.abs(p.reshape(C, L) * alpha[:, None]).max()) for p in pre) > 150.0
     assert_close(h(Y), np.stack([O.snake(pre[n], alpha, C, L) for n in range(N)]), FWD_TOL, "snake forward")
-    dY = rnd(N, C, L)
+    dY = r.standard_normal((N, C, L)).astype(np.float32)
     dX = torch.empty(N, C, L, device="cuda")
     dg, db = torch.empty(N, C, device="cuda"), torch.empty(N, C, device="cuda")
     da = torch.zeros(C, device="cuda")
@@ -455,7 +457,22 @@ def test_adain_snake_large_arguments(K, C, L):
     assert_close(h(dX), np.stack(rdx), GRAD_TOL, "snake dX")
     assert_close(h(dg), np.stack(rdg), GRAD_TOL, "snake dGamma")
     assert_close(h(db), np.stack(rdb), GRAD_TOL, "snake dBeta")
-    assert_close(h(da), rda, GRAD_TOL, "snake dAlpha")
+    # d(alpha) = sum dY (th sin 2th - sin^2 th) / a^2 moves by about 2 th^2
+    # times the rounding of s: at these arguments one ulp of s on half the
+    # elements shifts it by 1e-5 to 4e-5 rel-L2 (measured with the oracle), and
+    # the kernel's statistics differ from the oracle's by a few ulp in step
+    # across a row. Against the oracle's own s it is therefore held to 4e-4,
+    # and to the 1e-4 bar against s formed from the kernel's statistics
+    # (float32, the kernel's order of operations), which leaves only the
+    # kernel's own arithmetic.
+    assert_close(h(da), rda, 4 * GRAD_TOL, "snake dAlpha (oracle statistics)")
+    sk = h(st).reshape(N, C, 2)
+    rda_k = np.zeros(C)
+    for n in range(N):
+        xh = (x[n] - sk[n, :, 0:1]) * sk[n, :, 1:2]
+        s_k = ((np.float32(1.0) + gm[n])[:, None] * xh + bt[n][:, None]).astype(np.float32)
+        rda_k += O.snake_bwd(s_k.ravel(), alpha, dY[n].ravel(), C, L)[1]
+    assert_close(h(da), rda_k, GRAD_TOL, "snake dAlpha (kernel statistics)")
 
 
 @pytest.mark.parametrize("act", ["leaky", "snake"])
