@@ -221,12 +221,14 @@ def cpu_plan(cfg, params, runs=3):
     return out
 
 
-def micro_benches(ctx, reps=10):
+def micro_benches(ctx, reps=50):
     """The per-kernel-class cases quoted beside the headline: Snake + AdaIN1d
     backward (x [1,256,48000]), Conv1d 512->512 k3 backward (dgrad + wgrad,
     dilations 1/3/5, X [4,512,2048]) and the two ConvTranspose1d upsampler
-    backwards, each timed alone with HIP events on the context stream and
-    priced against its roofline (algorithmic bytes at 8 TB/s or FLOP at the
+    backwards, each timed alone with HIP events on the context stream over
+    `reps` back-to-back calls after 3 untimed ones (the cases take 20-450 us,
+    so a shorter run would weigh the queue's start-up on them) and priced
+    against its roofline (algorithmic bytes at 8 TB/s or FLOP at the
     FP32-MFMA peak)."""
     import torch
     from brosoundml_amd import native, synth
@@ -234,7 +236,8 @@ def micro_benches(ctx, reps=10):
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
 
     def timed(fn):
-        fn()
+        for _ in range(3):
+            fn()
         torch.cuda.synchronize()
         s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s0.record()
