@@ -99,6 +99,7 @@ struct GemmArgs {
     // octet mode (corr_gemm): K chunk = one input-channel octet x up to G taps
     int G, n_tg, n_oct, span8;  // taps per chunk, tap groups, octets, staged positions
     int quad;                // conv_gemm_q: weights packed in quads of k-steps (stride 1, k = KT)
+    int single;              // conv_gemm: one LDS stage (where two would leave at most two blocks per CU)
     // AdaIN backward epilogue (conv input grads that feed an AdaIN +
     // activation backward; off when part is null): Y receives
     // ds = dY * act'(s) of the AdaIN whose input rows x have Y's layout, and
@@ -609,12 +610,17 @@ void conv_gemm(GemmArgs g) {
     const bool live = q0 + wn * 64 < n_q;  // wave-uniform
     constexpr int HS = CK / 2;
 
+    // Two stages: chunk ch + 1 lands while ch is multiplied. One stage (where
+    // two would fit only two blocks per CU, the long strided windows): each
+    // chunk is staged after every wave has read the previous one, and the
+    // other resident blocks' MFMA work covers the wait.
+    const bool single = g.single != 0;  // uniform
     if (ch0 < ch1) issue(ch0, 0);
     __builtin_amdgcn_s_waitcnt(0);  // staging loads landed in LDS
     __syncthreads();
     for (int ch = ch0; ch < ch1; ++ch) {
-        const int sb = ((ch - ch0) & 1) * stage;
-        if (ch + 1 < ch1) issue(ch + 1, stage - sb);
+        const int sb = single ? 0 : ((ch - ch0) & 1) * stage;
+        if (!single && ch + 1 < ch1) issue(ch + 1, stage - sb);
         const int wb = sb + hi * BM + am;
         const int xb = sb + KR * BM + hi * span_p + bq;
         const int dl = (ch * CK + hi) * Lm + xm;  // row shift of the 16-B path: (dl + cc*Lm) mod 4
@@ -655,6 +661,10 @@ void conv_gemm(GemmArgs g) {
             __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
         }
         if (live && u < S) mm(pa0, pa1, pb0, pb1);
+        if (single && ch + 1 < ch1) {
+            __syncthreads();  // every wave has read the stage
+            issue(ch + 1, 0);
+        }
         __builtin_amdgcn_s_waitcnt(0);  // this wave's staging loads landed
         __syncthreads();
     }
@@ -2048,15 +2058,22 @@ int run_gemm(kdec_ctx* ctx, GemmArgs g, int N, int m_tiles, const char* fam,
     if (!quad && epi != QEPI_STORE) return fail(ctx, KDEC_EINVAL, "conv: fused epilogue needs the quad kernel");
     if (quad && (octet || g.n_phase > 1 || g.s != 1 || !conv_q_kernel_for(CK, g.k, epi)))
         return fail(ctx, KDEC_EINVAL, "conv: bad quad geometry");
-    const size_t lds = octet ? 2 * (static_cast<size_t>(g.G) * 1024 + 8 * static_cast<size_t>(g.span8)) * sizeof(float)
-                     : quad ? quad_lds_bytes(CK, g.k, g.d)
-                            : conv_lds_bytes(CK, kk, ss, dd);
-    if (lds > 160 * 1024) return fail(ctx, KDEC_EINVAL, "conv: tile does not fit LDS");
+    size_t lds = octet ? 2 * (static_cast<size_t>(g.G) * 1024 + 8 * static_cast<size_t>(g.span8)) * sizeof(float)
+               : quad ? quad_lds_bytes(CK, g.k, g.d)
+                      : conv_lds_bytes(CK, kk, ss, dd);
     if (static_cast<long>(g.C_in) * g.L_in * 4 > 0x7fffffffL)
         return fail(ctx, KDEC_EINVAL, "conv: input too large for one buffer descriptor");
     g.ybuf = (static_cast<long>(g.C_out) + BM) * g.L_y * 4 < 0x7fffffffL ? 1 : 0;
     const void* kern = octet ? corr_kernel() : quad ? conv_q_kernel_for(CK, g.k, epi) : conv_kernel_for(CK);
     if (!kern) return fail(ctx, KDEC_EINVAL, "conv: unsupported channel chunk");
+    // conv_gemm with one LDS stage where two leave at most two blocks per CU
+    // and one leaves more (the long windows of large strides)
+    g.single = 0;
+    if (!octet && !quad && blocks_per_cu(kern, lds) <= 2 && blocks_per_cu(kern, lds / 2) > blocks_per_cu(kern, lds)) {
+        g.single = 1;
+        lds /= 2;
+    }
+    if (lds > 160 * 1024) return fail(ctx, KDEC_EINVAL, "conv: tile does not fit LDS");
     int max_q = g.n_q;
     if (g.n_phase > 1) max_q = static_cast<int>(cdiv(g.L_y + g.ph_s, g.ph_s)) + 1;
     g.m_tiles = m_tiles;
