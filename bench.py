@@ -537,11 +537,19 @@ def main(argv=None):
                                     "ms_per_step": round(w_ms / n, 3)}
         serial["families_ms_per_step"] = {k: round(v["ms"] / n, 3) for k, v in sorted(sp.items())}
         out["serial"] = serial
-        # the same kernels with the GPU to themselves: on the default schedule
-        # up to three conv GEMMs (and the weight-grad GEMMs) share the CUs, so
-        # each launch's duration above also holds the others' work
-        out["roofline"]["achieved_one_stream"] = serial["roofline"]["achieved"]
-        out["roofline"]["frac_one_stream"] = serial["roofline"]["frac"]
+        # The roofline figure is the one-stream pass's: there each conv GEMM
+        # launch has the GPU to itself, so the family's launch time per step
+        # stays within the step. On the default schedule up to three conv
+        # GEMMs and the weight-grad GEMMs share the CUs, each launch's
+        # duration also holds the others' work, and the family's summed
+        # launch time exceeds the step; that figure is kept, labelled.
+        rf = out["roofline"]
+        rf["frac_overlapped"], rf["achieved_overlapped"] = rf["frac"], rf["achieved"]
+        rf["ms_per_step_overlapped"] = rf["ms_per_step"]
+        rf["achieved"], rf["frac"] = serial["roofline"]["achieved"], serial["roofline"]["frac"]
+        rf["ms_per_step"] = serial["roofline"]["ms_per_step"]
+        rf["region"] = ("one-stream pass of the same step after the timed region (events around every family "
+                        "launch); *_overlapped: the profiled pass of the default schedule")
     out["step_roofline"]["frac_serial"] = round(ideal_s * 1e3 / serial["ms_per_step"], 4) if serial else None
     if not a.no_serving:
         out["inference"] = inference_bench(ctx, model, t_asr, t_F0, t_N, t_style, audio, audio_per_step)

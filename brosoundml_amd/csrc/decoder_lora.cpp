@@ -414,6 +414,20 @@ void DecoderLora::backward(const DecoderBackbone& bb, const Generator& gen, cons
     gate_.backward(cond, dG_);
 }
 
+const bd::BackboneCache* DecoderLora::backbone_cache() const {
+    return static_cast<const bd::BackboneCache*>(bb_cache_);
+}
+
+const bd::GeneratorCache* DecoderLora::generator_cache() const {
+    return static_cast<const bd::GeneratorCache*>(gen_cache_);
+}
+
+void DecoderLora::backbone_affines(const DecoderBackbone& bb, const Generator& gen,
+                                   std::vector<bd::BlockAffines>& out) const {
+    std::vector<bd::ResBlock1Affines> na, ra;
+    affine_views(bb, gen, gb_, unit_off_host_, out, na, ra);
+}
+
 void DecoderLora::zero_grad() {
     zero(dA_, "DecoderLora::zero_grad");
     zero(dB_, "DecoderLora::zero_grad");

@@ -26,6 +26,11 @@ namespace brosoundml {
 struct Linear;
 struct DecoderBackbone;
 struct Generator;
+namespace detail {
+struct BackboneCache;
+struct GeneratorCache;
+struct BlockAffines;
+}  // namespace detail
 
 // g(v) = W2 tanh(W1 v), no biases, so g(0) = 0 exactly; W2 starts at zero.
 //   v (in_dim, 1) or (N, in_dim); W1 (hidden, in_dim); W2 (gate_dim, hidden)
@@ -120,6 +125,13 @@ public:
     void set_har_ready(void* hip_event) { har_ready_ = hip_event; }
     // Unit i's first row in B / the affine buffers.
     const std::vector<int>& unit_offsets() const { return unit_off_host_; }
+    // Extension (inspection): the last forward's backbone and generator
+    // caches (null before the first forward) and the backbone blocks'
+    // adapted AdaIN affines, as views of the forward's (gamma, beta) buffer.
+    const detail::BackboneCache* backbone_cache() const;
+    const detail::GeneratorCache* generator_cache() const;
+    void backbone_affines(const DecoderBackbone& bb, const Generator& gen,
+                          std::vector<detail::BlockAffines>& out) const;
 
 private:
     int rank_ = 0;

@@ -1029,90 +1029,120 @@ int kdec_model_leaky_site_count(const kdec_model* m) {
     return m ? 2 * (1 + m->n_decode) + m->n_ups + 1 : 0;
 }
 
+namespace {
+
+// One training forward's caches, as the leaky-site inspection reads them.
+struct ChainView {
+    kdec_ctx* ctx;
+    int n;
+    const bd::BackboneCache* bbc;
+    const std::vector<bd::BlockAffines>* bbaff;
+    const bd::GeneratorCache* genc;
+};
+
+long leaky_site_size(const kdec_model* m, const ChainView& cv, int site) {
+    const int n_blocks = 1 + m->n_decode;
+    if (site < 2 * n_blocks) {
+        const int b = site / 2;
+        const bd::AdainResBlkCache& c = b == 0 ? cv.bbc->encode : cv.bbc->decode[b - 1];
+        const brosoundml::AdainResBlk1dWeights& w = b == 0 ? m->bb.encode : m->bb.decode[b - 1];
+        return site % 2 ? static_cast<long>(cv.n) * w.channels_out * c.L_out
+                        : static_cast<long>(cv.n) * w.channels_in * c.L_in;
+    }
+    const Tensor& t = site < 2 * n_blocks + m->n_ups ? cv.genc->stages[site - 2 * n_blocks].x_in : cv.genc->head.x_pre;
+    return static_cast<long>(t.size());
+}
+
+// Site `site`'s input of the chain's forward, copied to host + at. An AdaIN
+// residual block's norm output is recomputed from the cached input and
+// statistics, as the backward recomputes it; the generator sites are cached.
+void leaky_site_copy(const kdec_model* m, const ChainView& cv, int site, float* host) {
+    const int n_blocks = 1 + m->n_decode;
+    bt::set_runtime(cv.ctx);
+    Tensor t;
+    if (site < 2 * n_blocks) {
+        const int b = site / 2;
+        const bool second = site % 2;
+        const bd::AdainResBlkCache& c = b == 0 ? cv.bbc->encode : cv.bbc->decode[b - 1];
+        const brosoundml::AdainResBlk1dWeights& w = b == 0 ? m->bb.encode : m->bb.decode[b - 1];
+        const bd::BlockAffines& a = (*cv.bbaff)[b];
+        const Tensor& x = second ? c.conv1_out : c.x;
+        const Tensor& st = second ? c.x_seq2 : c.x_seq1;
+        const Tensor& g = second ? a.g2 : a.g1;
+        const Tensor& be = second ? a.b2 : a.b1;
+        const int C = second ? w.channels_out : w.channels_in;
+        const int L = second ? c.L_out : c.L_in;
+        if (!x.data || !st.data) throw std::runtime_error("leaky_input: no cache for this site");
+        t = Tensor::empty_on(Device::HIP, cv.n, C * L);
+        const long gbs = cv.n == 1 ? 0 : g.row_stride();
+        if (kdec_adain_act_fwd(cv.ctx, static_cast<const float*>(x.data), x.row_stride(),
+                               static_cast<const float*>(st.data), static_cast<const float*>(g.data),
+                               static_cast<const float*>(be.data), gbs, KDEC_ACT_NONE, 0.0f, nullptr,
+                               static_cast<float*>(t.data), t.row_stride(), nullptr, 0, cv.n, C, L) != KDEC_OK)
+            throw std::runtime_error(std::string("leaky_input: ") + kdec_last_error(cv.ctx));
+    } else if (site < 2 * n_blocks + m->n_ups) {
+        t = cv.genc->stages[site - 2 * n_blocks].x_in;  // the stage input (leaky 0.1)
+    } else {
+        t = cv.genc->head.x_pre;  // the spectral head input (leaky 0.01)
+    }
+    if (!t.data) throw std::runtime_error("leaky_input: no cache for this site");
+    const std::vector<float> h = t.to_host_vector();
+    std::copy(h.begin(), h.end(), host);
+}
+
+std::vector<ChainView> model_chains(kdec_model* m) {
+    std::vector<ChainView> v;
+    for (int pi = 0; pi < m->parts; ++pi) {
+        kdec_model::Part& pt = m->part[pi];
+        v.push_back({pt.ctx, pt.n, &pt.bbc, &pt.bbaff, &pt.genc});
+    }
+    return v;
+}
+
+// kdec_model_leaky_input / kdec_dlora_leaky_input over the chains of one forward.
+int leaky_input_of(kdec_model* m, const std::vector<ChainView>& chains, int site, float* host, long n,
+                   const char* who) {
+    if (site < 0 || site >= kdec_model_leaky_site_count(m))
+        return fail(m, KDEC_EINVAL, std::string(who) + ": site out of range");
+    long want = 0;
+    for (const auto& cv : chains) want += leaky_site_size(m, cv, site);
+    if (n != want)
+        return fail(m, KDEC_EINVAL, std::string(who) + ": site holds " + std::to_string(want) + " values, not " +
+                                        std::to_string(n));
+    try {
+        long at = 0;
+        for (const auto& cv : chains) {
+            leaky_site_copy(m, cv, site, host + at);
+            at += leaky_site_size(m, cv, site);
+        }
+        bt::set_runtime(m->ctx);
+    } catch (const std::exception& e) {
+        bt::set_runtime(m->ctx);
+        return fail(m, KDEC_EHIP, std::string(who) + ": " + e.what());
+    }
+    return KDEC_OK;
+}
+
+bool model_has_forward(const kdec_model* m) {
+    return m->N != 0 && m->parts != 0 && !m->part[0].genc.stages.empty();
+}
+
+}  // namespace
+
 long kdec_model_leaky_size(kdec_model* m, int site) {
-    if (!m || m->N == 0 || m->parts == 0 || m->part[0].genc.stages.empty() || site < 0 ||
-        site >= kdec_model_leaky_site_count(m)) {
+    if (!m || !model_has_forward(m) || site < 0 || site >= kdec_model_leaky_site_count(m)) {
         if (m) fail(m, KDEC_EINVAL, "kdec_model_leaky_size: no training forward or site out of range");
         return -1;
     }
-    const int n_blocks = 1 + m->n_decode;
     long total = 0;
-    for (int pi = 0; pi < m->parts; ++pi) {
-        const kdec_model::Part& pt = m->part[pi];
-        if (site < 2 * n_blocks) {
-            const int b = site / 2;
-            const bd::AdainResBlkCache& c = b == 0 ? pt.bbc.encode : pt.bbc.decode[b - 1];
-            const brosoundml::AdainResBlk1dWeights& w = b == 0 ? m->bb.encode : m->bb.decode[b - 1];
-            total += site % 2 ? static_cast<long>(pt.n) * w.channels_out * c.L_out
-                              : static_cast<long>(pt.n) * w.channels_in * c.L_in;
-        } else {
-            const Tensor& t =
-                site < 2 * n_blocks + m->n_ups ? pt.genc.stages[site - 2 * n_blocks].x_in : pt.genc.head.x_pre;
-            total += static_cast<long>(t.size());
-        }
-    }
+    for (const auto& cv : model_chains(m)) total += leaky_site_size(m, cv, site);
     return total;
 }
 
 int kdec_model_leaky_input(kdec_model* m, int site, float* host, long n) {
     if (!m || !host) return KDEC_EINVAL;
-    if (m->N == 0 || m->parts == 0 || m->part[0].genc.stages.empty())
-        return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: no training forward to inspect");
-    const int n_blocks = 1 + m->n_decode;
-    if (site < 0 || site >= kdec_model_leaky_site_count(m))
-        return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: site out of range");
-    const long want = kdec_model_leaky_size(m, site);
-    if (n != want)
-        return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: site holds " + std::to_string(want) + " values, not " +
-                                        std::to_string(n));
-    try {
-        long at = 0;
-        for (int pi = 0; pi < m->parts; ++pi) {
-            kdec_model::Part& pt = m->part[pi];
-            bt::set_runtime(pt.ctx);
-            const int N = pt.n;
-            Tensor t;
-            if (site < 2 * n_blocks) {
-                // an AdaIN residual block's norm output, recomputed from the
-                // cached input and statistics as the backward recomputes it
-                const int b = site / 2;
-                const bool second = site % 2;
-                const bd::AdainResBlkCache& c = b == 0 ? pt.bbc.encode : pt.bbc.decode[b - 1];
-                const brosoundml::AdainResBlk1dWeights& w = b == 0 ? m->bb.encode : m->bb.decode[b - 1];
-                const bd::BlockAffines& a = pt.bbaff[b];
-                const Tensor& x = second ? c.conv1_out : c.x;
-                const Tensor& st = second ? c.x_seq2 : c.x_seq1;
-                const Tensor& g = second ? a.g2 : a.g1;
-                const Tensor& be = second ? a.b2 : a.b1;
-                const int C = second ? w.channels_out : w.channels_in;
-                const int L = second ? c.L_out : c.L_in;
-                if (!x.data || !st.data)
-                    return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: no cache for this site");
-                t = Tensor::empty_on(Device::HIP, N, C * L);
-                const long gbs = N == 1 ? 0 : g.row_stride();
-                if (int rc = check(m, kdec_adain_act_fwd(pt.ctx, static_cast<const float*>(x.data), x.row_stride(),
-                                                         static_cast<const float*>(st.data),
-                                                         static_cast<const float*>(g.data),
-                                                         static_cast<const float*>(be.data), gbs, KDEC_ACT_NONE, 0.0f,
-                                                         nullptr, static_cast<float*>(t.data), t.row_stride(),
-                                                         nullptr, 0, N, C, L)))
-                    return rc;
-            } else if (site < 2 * n_blocks + m->n_ups) {
-                t = pt.genc.stages[site - 2 * n_blocks].x_in;  // the stage input (leaky 0.1)
-            } else {
-                t = pt.genc.head.x_pre;  // the spectral head input (leaky 0.01)
-            }
-            if (!t.data) return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: no cache for this site");
-            const std::vector<float> h = t.to_host_vector();
-            std::copy(h.begin(), h.end(), host + at);
-            at += static_cast<long>(h.size());
-        }
-        bt::set_runtime(m->ctx);
-    } catch (const std::exception& e) {
-        bt::set_runtime(m->ctx);
-        return fail(m, KDEC_EHIP, e.what());
-    }
-    return KDEC_OK;
+    if (!model_has_forward(m)) return fail(m, KDEC_EINVAL, "kdec_model_leaky_input: no training forward to inspect");
+    return leaky_input_of(m, model_chains(m), site, host, n, "kdec_model_leaky_input");
 }
 
 // ─── DecoderLora over the model's weights ───────────────────────────────────
@@ -1301,5 +1331,34 @@ float* kdec_dlora_ptr(kdec_dlora* d, int which, int* rows, int* cols) {
 }
 
 float kdec_dlora_scale(const kdec_dlora* d) { return d ? d->lora.scale() : 0.0f; }
+
+namespace {
+bool dlora_chain(kdec_dlora* d, ChainView& cv, std::vector<bd::BlockAffines>& bba) {
+    const bd::BackboneCache* bbc = d->lora.backbone_cache();
+    const bd::GeneratorCache* genc = d->lora.generator_cache();
+    if (d->N == 0 || !bbc || !genc || genc->stages.empty()) return false;
+    d->lora.backbone_affines(d->m->bb, d->m->gen, bba);
+    cv = {d->m->ctx, d->N, bbc, &bba, genc};
+    return true;
+}
+}  // namespace
+
+long kdec_dlora_leaky_size(kdec_dlora* d, int site) {
+    ChainView cv{};
+    std::vector<bd::BlockAffines> bba;
+    if (!d || !dlora_chain(d, cv, bba) || site < 0 || site >= kdec_model_leaky_site_count(d->m)) {
+        if (d) dlora_fail(d, KDEC_EINVAL, "kdec_dlora_leaky_size: no forward or site out of range");
+        return -1;
+    }
+    return leaky_site_size(d->m, cv, site);
+}
+
+int kdec_dlora_leaky_input(kdec_dlora* d, int site, float* host, long n) {
+    if (!d || !host) return KDEC_EINVAL;
+    ChainView cv{};
+    std::vector<bd::BlockAffines> bba;
+    if (!dlora_chain(d, cv, bba)) return dlora_fail(d, KDEC_EINVAL, "kdec_dlora_leaky_input: no forward to inspect");
+    return leaky_input_of(d->m, {cv}, site, host, n, "kdec_dlora_leaky_input");
+}
 
 }  // extern "C"

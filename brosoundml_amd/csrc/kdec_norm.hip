@@ -996,11 +996,14 @@ struct BwdScratchLayout {
 size_t round256(size_t b) { return (b + 255) & ~size_t(255); }
 BwdScratchLayout bwd_scratch_layout(int N, int C, int L, bool want_alpha, bool v4_long) {
     const size_t rows = static_cast<size_t>(N) * C;
+    const bool chunked = !row_shape_bwd(L, v4_long).ntb;
     BwdScratchLayout s;
     size_t off = 0;
     s.apart = off;
-    off += want_alpha ? round256(rows * sizeof(float)) : 0;
-    if (!row_shape_bwd(L, v4_long).ntb) {
+    // the row kernels add one utterance's alpha grads directly; shares are
+    // kept for N > 1 and for the chunked passes
+    off += want_alpha && (N > 1 || chunked) ? round256(rows * sizeof(float)) : 0;
+    if (chunked) {
         s.part = off;
         off += round256(rows * static_cast<size_t>(cdiv(L, CH)) * 3 * sizeof(double));
         s.rowv = off;

@@ -49,11 +49,14 @@ void need_device(const Tensor& t, const char* where) {
 }
 
 // (gamma, beta) of one AdaIN unit for N utterances: rows of C at stride bs
-// (0: one row for every utterance).
+// (0: one row for every utterance), and the unit's instance-norm epsilon
+// (AdaIN1dWeights::eps, as ada_in_1d_styled passes it to the group norm,
+// kokoro_modules.cpp:618; 1e-5 when unset).
 struct Affine {
     const float* gamma;
     const float* beta;
     long bs;
+    float eps = 1e-5f;
     Tensor keep;  // owns the projection buffer
 };
 
@@ -72,6 +75,7 @@ Affine project(const AdaIN1dWeights& w, const Tensor& style, const char* where) 
     a.gamma = cf(a.keep);
     a.beta = cf(a.keep) + C;
     a.bs = 2 * C;
+    a.eps = w.eps > 0.0f ? w.eps : 1e-5f;
     return a;
 }
 
@@ -81,7 +85,7 @@ Tensor adain(const Tensor& x, int C, int L, const Affine& a, int act, float slop
     const int N = x.rows;
     Tensor st = make(N * C, 2);
     Tensor y = make(N, C * L);
-    ok(kdec_adain_act_fwd_stats(rt(), cf(x), ld(x), 1e-5f, mf(st), a.gamma, a.beta, a.bs, act, slope,
+    ok(kdec_adain_act_fwd_stats(rt(), cf(x), ld(x), a.eps, mf(st), a.gamma, a.beta, a.bs, act, slope,
                                 alpha ? cf(*alpha) : nullptr, mf(y), ld(y), nullptr, 0, N, C, L),
        where);
     return y;

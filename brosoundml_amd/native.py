@@ -228,6 +228,10 @@ class Model:
             audio = torch.empty(N, self.lengths(T)["audio"], device=asr.device, dtype=torch.float32)
         self._c(self.ctx.L.kdec_model_forward(self.h, N, T, ptr(asr), ptr(F0), ptr(Nn), ptr(style), ptr(har),
                                               ptr(audio)))
+        # the training caches refer to the inputs (asr, F0 and N feed the
+        # backbone's input-conv weight grads): held until the next forward,
+        # as the reference's cache tensors share their storage
+        self._keep = (asr, F0, Nn, style, har)
         self.N_last = N
         return audio
 
@@ -384,12 +388,28 @@ class DecoderLora:
         if audio is None:
             audio = torch.empty(N, self.model.lengths(T)["audio"], device=asr.device, dtype=torch.float32)
         self._keep = (asr, F0, Nn, ref_s, cond, har)
+        self._N = N
         self._c(self.ctx.L.kdec_dlora_forward(self.h, N, T, ptr(asr), ptr(F0), ptr(Nn), ptr(ref_s),
                                               ref_s.stride(0), ptr(har), ptr(cond), ptr(audio)))
         return audio
 
     def backward(self, daudio):
         self._c(self.ctx.L.kdec_dlora_backward(self.h, ptr(daudio)))
+
+    def leaky_inputs(self):
+        """Host copies of every leaky-ReLU site's input of the last DecoderLora
+        forward (kdec_dlora_leaky_input), in site order: (N, C*L) arrays."""
+        import numpy as np
+        L = self.ctx.L
+        res = []
+        for site in range(L.kdec_model_leaky_site_count(self.model.h)):
+            n = L.kdec_dlora_leaky_size(self.h, site)
+            if n < 0:
+                raise KdecError(L.kdec_last_error(self.ctx.h).decode())
+            a = np.empty(n, np.float32)
+            self._c(L.kdec_dlora_leaky_input(self.h, site, a.ctypes.data_as(ctypes.c_void_p), n))
+            res.append(a.reshape(self._N, -1))
+        return res
 
     def zero_grad(self):
         self._c(self.ctx.L.kdec_dlora_zero_grad(self.h))

@@ -222,11 +222,13 @@ int kdec_adain_act_bwd(kdec_ctx* ctx, const float* X, long x_bs,
 /* kdec_adain_act_bwd without any allocation: same arguments, kernels and
  * results. No counterpart in the reference; it is for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc). Its scratch (the per-row alpha-grad
- * shares, and for rows longer than 49152 the chunk partial sums and row
- * means: 4 B per row with dalpha, plus 24 B per row and 4096-sample chunk
- * and 8 B per row) lives in a device array of KDEC_NOALLOC_SCRATCH_BYTES per
- * GPU, held until the process ends; a call that needs more returns
+ * harnesses that forbid hipMalloc). Its scratch lives in a device array of
+ * KDEC_NOALLOC_SCRATCH_BYTES per GPU: the per-row alpha-grad shares (4 B per
+ * row, with dalpha when N > 1 or the rows take the chunked passes) and, for
+ * rows that no one-block row kernel holds (longer than 62464, or longer than
+ * 49152 when a row does not start on 16 B), the chunk partial sums and row
+ * means (24 B per row and 4096-sample chunk, plus 8 B per row). The array is
+ * held until the process ends; a call that needs more returns
  * KDEC_EINVAL with the sizes in kdec_last_error. It calls no hipMalloc /
  * hipFree and records no profiling events. Every call on one GPU shares
  * that GPU's array: calls that overlap on one GPU (any two streams or

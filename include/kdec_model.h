@@ -230,6 +230,10 @@ int kdec_model_leaky_site_count(const kdec_model* m);
 /* N*C*L of site `site` after the last training forward, or -1. */
 long kdec_model_leaky_size(kdec_model* m, int site);
 int kdec_model_leaky_input(kdec_model* m, int site, float* host, long n);
+/* The same sites of the last kdec_dlora_forward (the DecoderLora's own
+ * caches and adapted affines). */
+long kdec_dlora_leaky_size(kdec_dlora* d, int site);
+int kdec_dlora_leaky_input(kdec_dlora* d, int site, float* host, long n);
 
 /* Device pointers to the last forward's har (N, (n_fft+2)*frames) and
  * generator input (N, init_C * L_gen). */

@@ -17,7 +17,15 @@ the 983 168 spectral-head inputs at T = 64. So the oracle takes every leaky
 site's branch from the GPU's own inputs at that site
 (kdec_model_leaky_input -> OracleModel.set_kinks): both sides are then
 differentiated on the same linear piece, and the report counts the elements
-whose branch this reconciled ("kink_flips").
+whose branch this reconciled ("kink_flips"). That reconciliation is bounded:
+at every element whose branch it overrode, the oracle's own input must lie
+within KINK_TOL times the site's rms of zero (a rounding-level disagreement,
+not a sign error upstream), each site's inputs must agree to the forward bar
+(rel-L2 <= 1e-5), and at most KINK_FRAC of a site's elements may flip.
+
+Every comparison is also appended to REPORT (what, rel-L2, max-abs, and the
+flip statistics), which tests/conftest.py writes out as JSON lines when
+KDEC_PARITY_REPORT names a file.
 """
 from __future__ import annotations
 
@@ -29,6 +37,15 @@ from brosoundml_amd import synth
 
 FWD_TOL = 1e-5
 GRAD_TOL = 1e-4
+KINK_TOL = 1e-5   # |oracle's own input| / site rms at a reconciled element
+KINK_FRAC = 1e-4  # reconciled elements per site element
+
+REPORT = []
+
+
+def record(what, rel=None, maxabs=None, **extra):
+    """One parity figure for the per-config report."""
+    REPORT.append(dict(what=what, rel_l2=rel, max_abs=maxabs, **extra))
 
 
 def rel_l2(a, b):
@@ -114,7 +131,7 @@ def run_pair(ctx, cfg, N, T, tag, wgrad=True, dalpha=True, lora=None, unvoiced=0
     torch.cuda.synchronize()
 
     # oracle, utterance by utterance
-    ref_audio, ref_dstyle, ref_aff, flips = [], [], [], []
+    ref_audio, ref_dstyle, ref_aff, flips, kink_stats = [], [], [], [], []
     ref_grads = {n: np.zeros(int(np.prod(s))) for n, s in shapes.items()}
     for n in range(N):
         om.zero_grad()
@@ -124,6 +141,8 @@ def run_pair(ctx, cfg, N, T, tag, wgrad=True, dalpha=True, lora=None, unvoiced=0
             om.lora_gate(gates[n])
         a = om.forward(asr[n], F0[n], Nn[n], style[n], T, har=ref_har[n] if oracle_har else None)
         flips.append(om.kink_flips())
+        if pre is not None:
+            kink_stats.append(kink_check([p[n] for p in pre], om))
         ref_audio.append(a)
         ref_dstyle.append(om.backward(dA[n], wgrad=wgrad, dalpha=dalpha, dstyle=True))
         for name, s in shapes.items():
@@ -141,51 +160,117 @@ def run_pair(ctx, cfg, N, T, tag, wgrad=True, dalpha=True, lora=None, unvoiced=0
     r = dict(m=m, om=om, shapes=shapes, audio=audio.cpu().numpy(), ref_audio=np.stack(ref_audio),
              ref_har=np.stack(ref_har), dstyle=dstyle.cpu().numpy(), ref_dstyle=np.stack(ref_dstyle),
              grads=got_grads, ref_grads=ref_grads, dgb=dgb, ref_aff=ref_aff, units=m.units(),
-             oracle_units=om.units(), inputs=(asr, F0, Nn, style, dA), params=params, kink_flips=flips)
+             oracle_units=om.units(), inputs=(asr, F0, Nn, style, dA), params=params, kink_flips=flips,
+             kink_stats=kink_stats)
     if lora:
         gA, gB = m.lora_grads()
         r.update(lora_got=(gA, gB, t_dG.cpu().numpy()), lora_ref=(ref_dA, ref_dB, np.stack(ref_dG)))
     return r
 
 
-def check_pair(r, wgrad=True):
+def kink_check(gpu_pre, om):
+    """Bounds the branch reconciliation at every leaky site of one utterance:
+    gpu_pre are the GPU's inputs at each site, the oracle's own are read back
+    after its (reconciled) forward. Returns (flips, elements, worst |x|/rms at
+    a flipped element, worst site rel-L2); asserts the bars."""
+    flips = elems = 0
+    worst_mag = worst_rel = 0.0
+    for site, g in enumerate(gpu_pre):
+        o = om.leaky_input(site).astype(np.float64)
+        g = np.asarray(g, np.float64).ravel()
+        assert o.size == g.size, (site, o.size, g.size)
+        rms = float(np.sqrt(np.mean(o * o))) or 1.0
+        flipped = (o > 0) != (g > 0)
+        nf = int(flipped.sum())
+        mag = float(np.max(np.abs(o[flipped]))) / rms if nf else 0.0
+        rel = rel_l2(g, o)
+        assert rel <= FWD_TOL, f"leaky site {site}: GPU vs oracle inputs rel-L2 {rel:.3e}"
+        assert mag <= KINK_TOL, f"leaky site {site}: reconciled element at {mag:.3e} x rms from zero"
+        assert nf <= KINK_FRAC * o.size, f"leaky site {site}: {nf} of {o.size} elements reconciled"
+        flips += nf
+        elems += o.size
+        worst_mag, worst_rel = max(worst_mag, mag), max(worst_rel, rel)
+    return flips, elems, worst_mag, worst_rel
+
+
+def grad_errors(grads, ref_grads, wgrad=True):
+    """[(err/tol, name, rel-L2, max-abs, nonzero)] over every parameter grad. The bar:
+    rel-L2 <= GRAD_TOL with an absolute floor of 1e-6 * sqrt(size); a bias
+    in front of an instance norm, whose exact grad is zero, also gets 1e-7
+    times its layer's weight-grad norm. Without weight grads only the snake
+    alphas may be nonzero."""
+    worst = []
+    for name, ref in ref_grads.items():
+        got = grads[name].astype(np.float64)
+        err = np.linalg.norm(got - ref)
+        tol = GRAD_TOL * np.linalg.norm(ref) + 1e-6 * np.sqrt(ref.size)
+        wname = name[:-len(".bias")] + ".weight"
+        if name.endswith(".bias") and wname in ref_grads:
+            # a bias in front of an instance norm has an identically zero
+            # grad; what remains is float rounding of a cancelling sum, which
+            # scales with the layer's weight grad
+            tol += 1e-7 * np.linalg.norm(ref_grads[wname])
+        # (err/tol, name, rel-L2, max-abs, not identically zero)
+        worst.append((err / max(tol, 1e-30), name, rel_l2(got, ref), max_abs(got, ref),
+                      GRAD_TOL * np.linalg.norm(ref) > 1e-6 * np.sqrt(ref.size)))
+        if not wgrad and ".alpha" not in name:
+            assert not np.any(got), f"{name}: grad produced in reference semantics"
+    return worst
+
+
+def record_grads(name, worst):
+    """Records the worst rel-L2 over the grads that are not identically zero
+    (a conv bias in front of an instance norm has an exact grad of zero, so
+    only its absolute error means anything: recorded apart) and the worst
+    error over the bar."""
+    nz = [w for w in worst if w[4]]
+    zero = [w for w in worst if not w[4]]
+    w = max(nz, key=lambda t: t[2])
+    top = max(worst)
+    extra = dict(param=w[1], worst_err_over_tol=top[0], worst_err_over_tol_param=top[1])
+    if zero:
+        z = max(zero, key=lambda t: t[3])
+        extra.update(zero_grads=len(zero), zero_grads_worst_max_abs=z[3], zero_grads_worst_param=z[1])
+    record(f"{name} parameter grads ({len(worst)}; worst rel-L2)", w[2], w[3], **extra)
+
+
+def check_pair(r, wgrad=True, name=None):
     """Asserts the bars; returns a report {what: (rel-L2, max-abs)} with the
-    worst grads."""
+    worst grads. With a name, each figure goes to REPORT before its bar is
+    asserted."""
+    rec = record if name else (lambda *a, **k: None)
     rep = {"kink_flips": r.get("kink_flips")}
+    ks = r.get("kink_stats") or []
+    if ks:
+        rep["kink"] = dict(flips=sum(k[0] for k in ks), elements=sum(k[1] for k in ks),
+                           worst_abs_over_rms=max(k[2] for k in ks), worst_site_rel_l2=max(k[3] for k in ks))
     e = rel_l2(r["audio"], r["ref_audio"])
     rep["waveform"] = (e, max_abs(r["audio"], r["ref_audio"]))
+    rec(f"{name} waveform", *rep["waveform"], **({"kink": rep["kink"]} if ks else {}))
     assert e <= FWD_TOL, f"waveform rel-L2 {e:.3e} (max-abs {rep['waveform'][1]:.3e})"
     assert [u[0] for u in r["units"]] == [u[0] for u in r["oracle_units"]]
     # affine grads (the reference semantics' outputs)
     worst_aff = (0.0, "", 0.0)
     for n, aff in enumerate(r["ref_aff"]):
-        for (name, Cc, off), (_, _, dg, db) in zip(r["units"], aff):
+        for (uname, Cc, off), (_, _, dg, db) in zip(r["units"], aff):
             got = r["dgb"][n, off:off + 2 * Cc]
             ref = np.concatenate([dg, db])
             err = np.linalg.norm(got - ref)
             tol = GRAD_TOL * np.linalg.norm(ref) + 1e-6 * np.sqrt(ref.size)
-            worst_aff = max(worst_aff, (err / tol, name, max_abs(got, ref)))
-            assert err <= tol, (n, name, err, max_abs(got, ref))
+            worst_aff = max(worst_aff, (err / tol, uname, max_abs(got, ref)))
     rep["affine_grads_worst_err_over_tol"] = worst_aff
+    rec(f"{name} AdaIN affine grads (worst unit err/tol)", None, worst_aff[2], err_over_tol=worst_aff[0],
+        unit=worst_aff[1])
+    assert worst_aff[0] <= 1.0, worst_aff
     e = rel_l2(r["dstyle"], r["ref_dstyle"])
     rep["dstyle"] = (e, max_abs(r["dstyle"], r["ref_dstyle"]))
+    rec(f"{name} d(style)", *rep["dstyle"])
     assert e <= GRAD_TOL, f"d(style) rel-L2 {e:.3e}"
-    worst = []
-    for name, ref in r["ref_grads"].items():
-        got = r["grads"][name].astype(np.float64)
-        err = np.linalg.norm(got - ref)
-        tol = GRAD_TOL * np.linalg.norm(ref) + 1e-6 * np.sqrt(ref.size)
-        wname = name[:-len(".bias")] + ".weight"
-        if name.endswith(".bias") and wname in r["ref_grads"]:
-            # a bias in front of an instance norm has an identically zero
-            # grad; what remains is float rounding of a cancelling sum, which
-            # scales with the layer's weight grad
-            tol += 1e-7 * np.linalg.norm(r["ref_grads"][wname])
-        worst.append((err / max(tol, 1e-30), name, rel_l2(got, ref), max_abs(got, ref)))
-        if not wgrad and ".alpha" not in name:
-            assert not np.any(got), f"{name}: grad produced in reference semantics"
+    worst = grad_errors(r["grads"], r["ref_grads"], wgrad)
     worst.sort(reverse=True)
     rep["grads_worst"] = worst[:3]
+    if name:
+        record_grads(name, worst)
     assert worst[0][0] <= 1.0, worst[:5]
     return rep
 

@@ -87,7 +87,7 @@ def test_adam_kernel(ctx):
         ctx.call("kdec_adam_step", P(tp), P(dev(g)), P(tm), P(tv), n, 1e-3, 0.9, 0.999, 1e-8, 0)
 
 
-def make_model(ctx, cfg, tag):
+def make_model(ctx, cfg, tag, with_params=False):
     from brosoundml_amd import native
     m = native.Model(ctx, cfg)
     shapes = m.param_shapes()
@@ -95,7 +95,7 @@ def make_model(ctx, cfg, tag):
     m.set_params(params)
     om = O.OracleModel(cfg)
     om.set_params(params)
-    return m, om
+    return (m, om, params) if with_params else (m, om)
 
 
 def inputs(cfg, N, T, tag):
@@ -135,11 +135,15 @@ def test_neutral_identity(ctx):
     assert torch.equal(audio, audio2)
 
 
-@pytest.mark.parametrize("cfg_name,N,T", [("TINY", 1, 4), ("TINY", 2, 4), ("SMALL", 2, 6)])
+@pytest.mark.parametrize("cfg_name,N,T", [("TINY", 1, 4), ("TINY", 2, 4), ("SMALL", 2, 6), ("KOKORO", 2, 64)])
 def test_grads_against_oracle(ctx, cfg_name, N, T):
+    # The GPU runs first: its leaky-site inputs (kdec_dlora_leaky_input) fix
+    # the oracle's branch at every kink, bounded as in the model tests
+    # (model_parity.kink_check); both sides take the oracle's harmonic source.
     from brosoundml_amd import native
+    from model_parity import kink_check, oracle_har_of, record
     cfg, rank, scale = getattr(C, cfg_name), 3, 0.7
-    m, om = make_model(ctx, cfg, "dl.g")
+    m, om, params = make_model(ctx, cfg, "dl.g", with_params=True)
     d = native.DecoderLora(m, rank, scale, seed=77)
     W2 = np.random.default_rng(8).uniform(-0.3, 0.3, (rank, 16)).astype(np.float32)
     d.set("W2", W2)
@@ -148,18 +152,26 @@ def test_grads_against_oracle(ctx, cfg_name, N, T):
     S = cfg["style_dim"]
     units = om.units()
     offs = [u[2] for u in m.units()]
+    har = [oracle_har_of(cfg, params, F0[n]) for n in range(N)]
+    t = [dev(a) for a in (asr, F0, Nn, ref_s, cond)]
+    d.zero_grad()
+    audio = d.forward(t[0], t[1], t[2], t[3], T, t[4], har=dev(np.stack(har)))
+    pre = d.leaky_inputs()
+    d.backward(dev(dA))
+    torch.cuda.synchronize()
     om.lora_enable(rank, scale)
     for i, (_, c) in enumerate(units):
         om.lora_set(i, A[i * rank:(i + 1) * rank], B[offs[i]:offs[i] + 2 * c])
-    ref_audio, har = [], []
+    ref_audio, kinks = [], []
     ref_dA, ref_dB = np.zeros_like(A, np.float64), np.zeros_like(B, np.float64)
     ref_dW1, ref_dW2 = np.zeros((16, 3)), np.zeros((rank, 16))
     for n in range(N):
         g, act = DL.gate_forward(W1, W2, cond[n].astype(np.float32))
         om.lora_gate(g[0])
         om.zero_grad()
-        ref_audio.append(om.forward(asr[n], F0[n], Nn[n], ref_s[n, :S], T))
-        har.append(om.har())
+        om.set_kinks([p[n] for p in pre])
+        ref_audio.append(om.forward(asr[n], F0[n], Nn[n], ref_s[n, :S], T, har=har[n]))
+        kinks.append(kink_check([p[n] for p in pre], om))
         om.backward(dA[n], wgrad=False, dalpha=False, dstyle=False)
         for i, (_, c) in enumerate(units):
             gA, gB = om.lora_grads(i, c)
@@ -168,14 +180,18 @@ def test_grads_against_oracle(ctx, cfg_name, N, T):
         dW1n, dW2n = DL.gate_backward(W2, cond[n].astype(np.float32), act, om.lora_dgate())
         ref_dW1 += dW1n
         ref_dW2 += dW2n
-    t = [dev(a) for a in (asr, F0, Nn, ref_s, cond)]
-    d.zero_grad()
-    audio = d.forward(t[0], t[1], t[2], t[3], T, t[4], har=dev(np.stack(har)))
-    d.backward(dev(dA))
-    torch.cuda.synchronize()
-    assert rel_l2(audio.cpu(), np.stack(ref_audio)) <= 1e-5
+    om.clear_kinks()
+    tag = f"DecoderLora {cfg_name} N={N} T={T}"
+    e = rel_l2(audio.cpu(), np.stack(ref_audio))
+    record(f"{tag} waveform", e, float(np.max(np.abs(audio.cpu().numpy() - np.stack(ref_audio)))),
+           kink=dict(flips=sum(k[0] for k in kinks), elements=sum(k[1] for k in kinks),
+                     worst_abs_over_rms=max(k[2] for k in kinks)))
+    assert e <= 1e-5, f"waveform rel-L2 {e:.3e}"
     for name, ref in (("dA", ref_dA), ("dB", ref_dB), ("dW1", ref_dW1), ("dW2", ref_dW2)):
-        e = rel_l2(d.get(name), ref)
+        got = d.get(name)
+        e = rel_l2(got, ref)
+        record(f"{tag} {name}", e, float(np.max(np.abs(got - ref))))
+        print(f"{tag} {name}: rel-L2 {e:.3e}", flush=True)
         assert e <= 1e-4, f"{name} rel-L2 {e:.3e}"
 
     # one Adam step over every trainable, against the oracle's on the same grads

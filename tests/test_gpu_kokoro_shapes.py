@@ -11,14 +11,25 @@
 * Config 3: the two ConvTranspose1d upsamplers (ups0 on [4, 512, 512], ups1
   on [4, 256, 5120] and on [4, 256, 512]) likewise.
 * Config 4: one utterance at T = 512 (307 200 samples, 20 % unvoiced F0)
-  against the oracle, and B = 8 at T = 512 against eight B = 1 runs of the
-  same model (batch independence; the weight grads of the batch equal the
-  sum of the single-utterance grads).
-* The weight-grad GEMM at production K (8 x 61 441 positions).
+  against the oracle, and the benchmark's own B = 8, T = 512 step: every
+  utterance's waveform and leaky-site inputs against a B = 1 run; the
+  batch's d(style) and AdaIN affine grads of utterances 0 and 7 against the
+  oracle; the batch's parameter grads (every conv, conv-transpose, pool and
+  fc weight and bias, every snake alpha) with dL/dwav nonzero on utterance
+  n only (n = 0 and 7: the B = 8 kernels, split plans and weight-grad lane,
+  with utterance n's grads alone) against the oracle's utterance n; and the
+  full batch's parameter grads against the sum of the eight one-utterance
+  backwards of the same forward (the fold over utterances).
+* The weight-grad GEMM at production K: 8 x 61 441 positions at C = 128
+  (the stage-1 instance) and 8 x 10 240 at C = 256 (stage 0).
+* The reference's own semantics (conv input grads only, no weight grads,
+  snake alpha grads on or off) at Kokoro shapes, N = 2, T = 64: against the
+  oracle, and the overlapped schedule bit for bit against one stream.
 * The inference forwards (kdec_model_infer, kdec_model_decode_back_half)
   against the oracle's forward.
 
-Each comparison prints its rel-L2 and max-abs error.
+Each comparison prints its rel-L2 and max-abs error and records it
+(model_parity.REPORT).
 """
 import ctypes
 
@@ -28,7 +39,8 @@ import pytest
 import oracle_lib as O
 from brosoundml_amd import config as C
 from brosoundml_amd import synth
-from model_parity import FWD_TOL, GRAD_TOL, check_har, check_pair, dev, inputs, max_abs, rel_l2, run_pair
+from model_parity import (FWD_TOL, GRAD_TOL, check_har, check_pair, dev, grad_errors, inputs, kink_check, max_abs,
+                          record, record_grads, rel_l2, run_pair)
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -54,6 +66,7 @@ def P(t):
 def close(got, ref, tol, what):
     e, m = rel_l2(got, ref), max_abs(got, ref)
     print(f"{what}: rel-L2 {e:.3e} max-abs {m:.3e}", flush=True)
+    record(what, e, m)
     assert e <= tol, f"{what}: rel-L2 {e:.3e} > {tol:.0e} (max-abs {m:.3e})"
 
 
@@ -74,7 +87,7 @@ def model_har(ctx, m, cfg, N, T, ins):
 def test_config0_whole_decoder(ctx, kokoro_params):
     cfg, N, T = C.KOKORO, 1, 64
     r = run_pair(ctx, cfg, N, T, "cfg0", params=kokoro_params)
-    report("config0 B=1 T=64", check_pair(r))
+    report("config0 B=1 T=64", check_pair(r, name="config 0: decoder B=1 T=64"))
     har = model_har(ctx, r["m"], cfg, N, T, r["inputs"])
     report("config0 in-model harmonic source", check_har(har[0], r["ref_har"][0], cfg["n_fft"]))
 
@@ -194,15 +207,18 @@ def test_config3_convt(ctx, name, Cin, Cout, L, k, s, p):
 
 # ─── weight grads at production K ───
 
-@pytest.mark.parametrize("k,d", [(11, 5), (3, 1)])
-def test_wgrad_production_k(ctx, k, d):
-    # stage-1 ResBlock1 geometry of a B = 8, T = 512 step: C = 128, L = 61441,
-    # K = 8 x 61441 positions (split-K over rounds of resident blocks, the
-    # in-row fast staging path and the boundary chunks)
-    N, Cc, L = 8, 128, 61441
+@pytest.mark.parametrize("Cc,L,k,d", [(128, 61441, 11, 5), (128, 61441, 3, 1), (256, 10240, 7, 3),
+                                       (256, 10240, 11, 5)])
+def test_wgrad_production_k(ctx, Cc, L, k, d):
+    # The ResBlock1 weight grads of a B = 8, T = 512 step at K = 8 x L
+    # positions (split-K over rounds of resident blocks, the in-row fast
+    # staging path and the boundary chunks): stage 1 (C = 128, L = 61441;
+    # C_in*k = 384 / 1408, the 128-column tile) and stage 0 (C = 256,
+    # L = 10240; C_in*k = 1792 / 2816, the 256-column tile)
+    N = 8
     p = d * (k - 1) // 2
-    x = synth.normal(f"wgk.x{k}", (N, Cc, L))
-    dY = synth.normal(f"wgk.dy{k}", (N, Cc, L))
+    x = synth.normal(f"wgk.x{Cc}.{k}", (N, Cc, L))
+    dY = synth.normal(f"wgk.dy{Cc}.{k}", (N, Cc, L))
     tx, tdy = dev(x), dev(dY)
     dW = torch.zeros(Cc, Cc * k, device="cuda")
     db = torch.zeros(Cc, device="cuda")
@@ -210,8 +226,8 @@ def test_wgrad_production_k(ctx, k, d):
     torch.cuda.synchronize()
     xd, dyd = torch.from_numpy(x).double(), torch.from_numpy(dY).double()
     rW = torch.nn.grad.conv1d_weight(xd, (Cc, Cc, k), dyd, padding=p, dilation=d).reshape(Cc, Cc * k)
-    close(dW.cpu().numpy(), rW.numpy(), GRAD_TOL, f"wgrad N=8 L=61441 k={k} d={d}")
-    close(db.cpu().numpy(), dyd.sum(dim=(0, 2)).numpy(), GRAD_TOL, f"bias grad N=8 L=61441 k={k}")
+    close(dW.cpu().numpy(), rW.numpy(), GRAD_TOL, f"wgrad N=8 C={Cc} L={L} k={k} d={d}")
+    close(db.cpu().numpy(), dyd.sum(dim=(0, 2)).numpy(), GRAD_TOL, f"bias grad N=8 C={Cc} L={L} k={k}")
 
 
 # ─── config 4 ───
@@ -219,54 +235,123 @@ def test_wgrad_production_k(ctx, k, d):
 def test_config4_one_utterance(ctx, kokoro_params):
     cfg, N, T = C.KOKORO, 1, 512
     r = run_pair(ctx, cfg, N, T, "cfg4", params=kokoro_params, unvoiced=0.2)
-    report("config4 B=1 T=512", check_pair(r))
+    report("config4 B=1 T=512", check_pair(r, name="config 4: decoder B=1 T=512"))
     har = model_har(ctx, r["m"], cfg, N, T, r["inputs"])
     report("config4 in-model harmonic source (307200 samples)", check_har(har[0], r["ref_har"][0], cfg["n_fft"]))
 
 
 def test_config4_batch_of_8(ctx, kokoro_params):
-    # The benchmark's workload (B = 8, T = 512, 20 % unvoiced F0).
-    # Forward: every utterance's waveform and every leaky-ReLU site input in
-    # the batch equal a B = 1 run of that utterance (the GEMMs split
-    # differently per batch size, so to rounding); the harmonic source is
-    # per-utterance lane work and equal bit for bit.
-    # Backward: utterance 0's d(style) and AdaIN affine grads in the batch
-    # against the oracle differentiated on the batch run's own linear pieces
-    # (its leaky-site inputs), the per-utterance outputs of a batched backward.
+    # The benchmark's workload (B = 8, T = 512, 20 % unvoiced F0, its inputs).
     from brosoundml_amd import native
     cfg, N, T = C.KOKORO, 8, 512
     m = native.Model(ctx, cfg)
     m.set_params(kokoro_params)
+    shapes = m.param_shapes()
     asr, F0, Nn, style, dA = inputs(cfg, N, T, "bench", unvoiced=0.2)  # the benchmark's inputs
     m.zero_grad()
     audio = m.forward(dev(asr), dev(F0), dev(Nn), dev(style), T).cpu().numpy()
     har8 = m.har(N, T)
     pre8 = m.leaky_inputs()
+    # the benchmark's backward: every output of every utterance
     dst8 = torch.empty(N, cfg["style_dim"], device="cuda")
     m.backward(dev(dA), wgrad=True, dalpha=True, dstyle=dst8)
     torch.cuda.synchronize()
     dst8 = dst8.cpu().numpy()
     _, dgb8 = m.affines(N)
+    full = {name: m.grad(name, sh).astype(np.float64) for name, sh in shapes.items()}
+    # the same forward differentiated one utterance at a time (dL/dwav zero
+    # elsewhere): the B = 8 kernels and split plans, utterance n's grads alone
+    one = {}
+    total = {name: np.zeros_like(g) for name, g in full.items()}
+    for n in range(N):
+        dAn = np.zeros_like(dA)
+        dAn[n] = dA[n]
+        m.zero_grad()
+        m.backward(dev(dAn), wgrad=True, dalpha=True)
+        torch.cuda.synchronize()
+        g = {name: m.grad(name, sh) for name, sh in shapes.items()}
+        for name in total:
+            total[name] += g[name]
+        if n in (0, N - 1):
+            one[n] = g
+    # the batch's grads are the sum of its utterances' (the fold over N)
+    worst = grad_errors(full, total)
+    record_grads("config 4 B=8: full-batch grads vs the sum of one-utterance backwards", worst)
+    assert max(worst)[0] <= 1.0, sorted(worst, reverse=True)[:5]
+    # batch independence of the forward
     for n in range(N):
         sl = slice(n, n + 1)
         a1 = m.forward(dev(asr[sl]), dev(F0[sl]), dev(Nn[sl]), dev(style[sl]), T).cpu().numpy()
         assert np.array_equal(m.har(1, T)[0], har8[n]), f"utterance {n}: harmonic source depends on the batch"
-        close(audio[n], a1[0], FWD_TOL, f"config4 utterance {n} waveform, B=8 vs B=1")
+        close(audio[n], a1[0], FWD_TOL, f"config 4 utterance {n} waveform, B=8 vs B=1")
         pre1 = m.leaky_inputs()
-        worst = max(rel_l2(p8[n], p1[0]) for p8, p1 in zip(pre8, pre1))
-        assert worst <= FWD_TOL, f"utterance {n}: leaky-site inputs B=8 vs B=1 rel-L2 {worst:.3e}"
-    # utterance 0 of the batched backward against the oracle
+        worst_pre = max(rel_l2(p8[n], p1[0]) for p8, p1 in zip(pre8, pre1))
+        assert worst_pre <= FWD_TOL, f"utterance {n}: leaky-site inputs B=8 vs B=1 rel-L2 {worst_pre:.3e}"
+    # utterances 0 and 7 of the batched step against the oracle, on the batch
+    # run's own linear pieces (its leaky-site inputs) and harmonic source
     om = O.OracleModel(cfg)
     om.set_params(kokoro_params)
-    om.set_kinks([p[0] for p in pre8])
-    ra = om.forward(asr[0], F0[0], Nn[0], style[0], T, har=har8[0])
-    print(f"config4 utterance 0: kink flips reconciled {om.kink_flips()}", flush=True)
-    close(audio[0], ra, FWD_TOL, "config4 B=8 utterance 0 waveform vs oracle (GPU harmonic source)")
-    rds = om.backward(dA[0], wgrad=True, dalpha=True, dstyle=True)
-    close(dst8[0], rds, GRAD_TOL, "config4 B=8 utterance 0 d(style) vs oracle")
-    got = np.concatenate([dgb8[0, off:off + 2 * c] for _, c, off in m.units()])
-    ref = np.concatenate([np.concatenate(om.affine(i, c)[2:]) for i, (_, c) in enumerate(om.units())])
-    close(got, ref, GRAD_TOL, "config4 B=8 utterance 0 AdaIN affine grads vs oracle")
+    for n in (0, N - 1):
+        om.zero_grad()
+        om.set_kinks([p[n] for p in pre8])
+        ra = om.forward(asr[n], F0[n], Nn[n], style[n], T, har=har8[n])
+        fl, el, mag, srel = kink_check([p[n] for p in pre8], om)
+        print(f"config 4 B=8 utterance {n}: {fl} of {el} leaky inputs reconciled, worst |x|/rms {mag:.2e}, "
+              f"worst site rel-L2 {srel:.2e}", flush=True)
+        record(f"config 4 B=8 utterance {n} leaky sites", srel, None, flips=fl, elements=el, worst_abs_over_rms=mag)
+        close(audio[n], ra, FWD_TOL, f"config 4 B=8 utterance {n} waveform vs oracle")
+        rds = om.backward(dA[n], wgrad=True, dalpha=True, dstyle=True)
+        close(dst8[n], rds, GRAD_TOL, f"config 4 B=8 utterance {n} d(style) vs oracle")
+        got = np.concatenate([dgb8[n, off:off + 2 * c] for _, c, off in m.units()])
+        ref = np.concatenate([np.concatenate(om.affine(i, c)[2:]) for i, (_, c) in enumerate(om.units())])
+        close(got, ref, GRAD_TOL, f"config 4 B=8 utterance {n} AdaIN affine grads vs oracle")
+        ref_grads = {name: om.grad(name, sh).astype(np.float64) for name, sh in shapes.items()}
+        worst = grad_errors(one[n], ref_grads)
+        record_grads(f"config 4 B=8 utterance {n} (one-utterance backward) vs oracle", worst)
+        top = sorted(worst, reverse=True)
+        print(f"config 4 B=8 utterance {n} parameter grads: worst err/tol {top[0][0]:.3f} ({top[0][1]}), "
+              f"worst rel-L2 {max(w[2] for w in worst if w[4]):.2e} (grads not identically zero)", flush=True)
+        assert top[0][0] <= 1.0, top[:5]
+    om.clear_kinks()
+
+
+# ─── the reference's own semantics at Kokoro shapes ───
+
+@pytest.mark.parametrize("dalpha", [False, True])
+def test_reference_semantics_kokoro(ctx, kokoro_params, dalpha):
+    # conv input grads only (no weight grads): the generator's resblock and
+    # noise-branch backwards run on three streams; against the oracle
+    r = run_pair(ctx, C.KOKORO, 2, 64, f"refsem{int(dalpha)}", wgrad=False, dalpha=dalpha, params=kokoro_params)
+    report(f"reference semantics dalpha={dalpha}",
+           check_pair(r, wgrad=False, name=f"reference semantics (dalpha={'on' if dalpha else 'off'}) KOKORO N=2 T=64"))
+
+
+def test_reference_semantics_kokoro_single_stream_equals_overlapped(ctx, kokoro_params):
+    from brosoundml_amd import native
+    cfg, N, T = C.KOKORO, 2, 64
+    m = native.Model(ctx, cfg)
+    shapes = m.param_shapes()
+    m.set_params(kokoro_params)
+    asr, F0, Nn, style, dA = inputs(cfg, N, T, "refsem.ovl")
+    t = [dev(a) for a in (asr, F0, Nn, style)]
+    d = dev(dA)
+    for dalpha in (False, True):
+        res = []
+        for on in (True, False):
+            m.set_overlap(on)
+            m.zero_grad()
+            a = m.forward(*t, T).cpu().numpy()
+            ds = torch.empty_like(t[3])
+            m.backward(d, wgrad=False, dalpha=dalpha, dstyle=ds)
+            torch.cuda.synchronize()
+            _, dgb = m.affines(N)
+            res.append((a, ds.cpu().numpy(), np.array(dgb),
+                        {n: m.grad(n, s) for n, s in shapes.items() if "alpha" in n}))
+        m.set_overlap(True)
+        for i in range(3):
+            np.testing.assert_array_equal(res[0][i], res[1][i])
+        for n in res[0][3]:
+            np.testing.assert_array_equal(res[0][3][n], res[1][3][n], err_msg=n)
 
 
 # ─── inference forwards ───

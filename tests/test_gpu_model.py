@@ -27,7 +27,7 @@ def ctx():
 
 
 def test_tiny_full_extension(ctx):
-    check_pair(run_pair(ctx, C.TINY, 2, 4, "gm.tiny"))
+    check_pair(run_pair(ctx, C.TINY, 2, 4, "gm.tiny"), name="TINY N=2 T=4")
 
 
 def test_tiny_with_lora_adapters(ctx):
@@ -41,7 +41,7 @@ def test_tiny_with_lora_adapters(ctx):
 
 
 def test_small_full_extension(ctx):
-    check_pair(run_pair(ctx, C.SMALL, 2, 6, "gm.small"))
+    check_pair(run_pair(ctx, C.SMALL, 2, 6, "gm.small"), name="SMALL N=2 T=6")
 
 
 def test_reference_semantics_single_utterance(ctx):

@@ -1,10 +1,13 @@
 """kdec_adain_act_bwd_noalloc (the AdaIN + activation backward with its
 scratch in a fixed device array) against kdec_adain_act_bwd on the same
-inputs: two calls in a row, the second with a smaller input and on the other
-kernel path (chunked passes for rows longer than 49152, then one block per
-row), each equal to the allocating entry point bit for bit (same kernels,
-same summation order); and a call beyond the array's size is refused before
-anything is launched.
+inputs: calls in a row, each smaller than the one before and on another
+kernel path -- rows of 70000 (longer than every row kernel: the chunked
+passes, whose chunk partials, row means and alpha shares sit in the array),
+rows of 61441 (one block per row holding the whole row; alpha shares of two
+utterances), rows of 3000 (one block per row, one utterance, leaky) -- each
+equal to the allocating entry point bit for bit (same kernels, same
+summation order); and a call whose scratch exceeds the array is refused
+before anything is launched.
 """
 import ctypes
 
@@ -52,23 +55,22 @@ def run_pair(ctx, N, C, L, act, tag):
 def test_noalloc_equals_allocating_backward():
     from brosoundml_amd import native
     ctx = native.Context(0)
-    # first call: rows of 61441 (chunked passes), alpha grads over 2 utterances
-    (a, b) = run_pair(ctx, 2, 128, 61441, ACT_SNAKE, "noalloc.1")
-    for u, v in zip(a, b):
-        assert np.array_equal(u, v)
-    # second call, smaller: rows of 3000 (one block per row), leaky
-    (a, b) = run_pair(ctx, 1, 64, 3000, ACT_LEAKY, "noalloc.2")
-    for u, v in zip(a, b):
-        assert np.array_equal(u, v)
-    # beyond the scratch array: 2^21 rows need 8 MiB of alpha-grad shares
-    # alone; refused with the sizes in the message before anything launches
-    # (the buffers are real and sized for the call all the same)
-    C, L = 1 << 21, 4
-    x = torch.zeros(C * L, device="cuda")
-    big = [torch.zeros(C * L, device="cuda") for _ in range(2)]
-    st = torch.zeros(C, 2, device="cuda")
-    small = [torch.zeros(C, device="cuda") for _ in range(6)]
+    for N, C, L, act, tag in ((2, 64, 70000, ACT_SNAKE, "noalloc.0"),     # chunked passes
+                              (2, 128, 61441, ACT_SNAKE, "noalloc.1"),    # one block per long row
+                              (1, 64, 3000, ACT_LEAKY, "noalloc.2")):     # one block per row
+        print(f"noalloc: N={N} C={C} L={L} act={act}", flush=True)
+        (a, b) = run_pair(ctx, N, C, L, act, tag)
+        for u, v in zip(a, b):
+            assert np.array_equal(u, v)
+    # beyond the scratch array: two utterances of 2^20 rows with alpha grads
+    # keep 8 MiB of alpha-grad shares alone; refused with the sizes in the
+    # message before anything launches (the buffers are real and sized for
+    # the call all the same)
+    N, C, L = 2, 1 << 20, 4
+    x, dy, dx = (torch.zeros(N * C * L, device="cuda") for _ in range(3))
+    st = torch.zeros(N * C, 2, device="cuda")
+    gam, bet, alpha, dalpha = (torch.zeros(C, device="cuda") for _ in range(4))
+    dgam, dbet = (torch.zeros(N * C, device="cuda") for _ in range(2))
     with pytest.raises(native.KdecError, match="scratch"):
-        ctx.call("kdec_adain_act_bwd_noalloc", P(x), C * L, P(st), P(small[0]), P(small[1]), 0, ACT_SNAKE, 0.0,
-                 P(small[2]), P(big[0]), C * L, None, 0, P(big[1]), C * L, P(small[3]), P(small[4]), 0,
-                 P(small[5]), 1, C, L)
+        ctx.call("kdec_adain_act_bwd_noalloc", P(x), C * L, P(st), P(gam), P(bet), 0, ACT_SNAKE, 0.0,
+                 P(alpha), P(dy), C * L, None, 0, P(dx), C * L, P(dgam), P(dbet), C, P(dalpha), N, C, L)
