@@ -224,8 +224,9 @@ def cpu_plan(cfg, params, runs=3):
 def micro_benches(ctx, reps=50):
     """The per-kernel-class cases quoted beside the headline: Snake + AdaIN1d
     backward (x [1,256,48000]), Conv1d 512->512 k3 backward (dgrad + wgrad,
-    dilations 1/3/5, X [4,512,2048]) and the two ConvTranspose1d upsampler
-    backwards, each timed alone with HIP events on the context stream over
+    dilations 1/3/5, X [4,512,2048]), the two ConvTranspose1d upsampler
+    backwards, the iSTFT head backward and forward and the style projection
+    at the benchmark's B = 8 shapes, each timed alone with HIP events on the context stream over
     `reps` back-to-back calls after 3 untimed ones (the cases take 20-450 us,
     so a shorter run would weigh the queue's start-up on them) and priced
     against its roofline (algorithmic bytes at 8 TB/s or FLOP at the
@@ -320,6 +321,48 @@ def micro_benches(ctx, reps=50):
         res[name] = {"ms": round(t * 1e3, 4), "TFLOP/s": round(fl / t / 1e12, 2),
                      "frac_mfma": round(fl / t / PEAK_FP32_MFMA, 4), "flop": fl}
     out["convT_bwd"] = res
+    del Xt, Gt, Wt, dXt, dWt
+
+    # iSTFT head (n_fft 20, hop 5) at the benchmark's shape, B = 8 utterances
+    # of 61 441 frames: backward reads post [8, 22, 61441] and dAudio
+    # [8, 307200] and writes dpost; forward reads post and writes audio
+    Nb, Lf, nfft, hop = 8, 61441, 20, 5
+    sig = (Lf - 1) * hop
+    post = dev(synth.normal("micro.post", (Nb, nfft + 2, Lf), 0.5))
+    da = dev(synth.normal("micro.daudio", (Nb, sig)))
+    dpost = torch.empty_like(post)
+    aud = torch.empty(Nb, sig, device="cuda")
+    t = timed(lambda: ctx.call("kdec_spectral_bwd", P(post), (nfft + 2) * Lf, None, P(da), sig, P(dpost),
+                               (nfft + 2) * Lf, Nb, Lf, nfft, hop))
+    by = 4.0 * Nb * (2.0 * (nfft + 2) * Lf + sig)
+    out["istft_bwd_x8x22x61441"] = {"ms": round(t * 1e3, 4), "GB/s": round(by / t / 1e9, 1),
+                                    "frac_hbm": round(by / t / PEAK_HBM, 4), "algorithmic_bytes": by}
+    t = timed(lambda: ctx.call("kdec_spectral_fwd", P(post), (nfft + 2) * Lf, None, P(aud), sig, Nb, Lf, nfft,
+                               hop))
+    by = 4.0 * Nb * ((nfft + 2) * Lf + sig)
+    out["istft_fwd_x8x22x61441"] = {"ms": round(t * 1e3, 4), "GB/s": round(by / t / 1e9, 1),
+                                    "frac_hbm": round(by / t / PEAK_HBM, 4), "algorithmic_bytes": by}
+    del post, da, dpost, aud
+
+    # style projection of every AdaIN unit at once (R rows of the stacked fc,
+    # S = 128, B = 8): forward (gamma, beta) and d(style)
+    from brosoundml_amd import config as Cfg
+    R, S = Cfg.affine_rows(Cfg.KOKORO), 128
+    Wf = dev(synth.uniform("micro.fcw", (R, S), -0.09, 0.09))
+    bf = dev(synth.uniform("micro.fcb", (R,), -0.09, 0.09))
+    st = dev(synth.normal("micro.style", (Nb, S), 0.3))
+    gbv = torch.empty(Nb, R, device="cuda")
+    dgbv = dev(synth.normal("micro.dgb", (Nb, R)))
+    dst = torch.empty(Nb, S, device="cuda")
+    t = timed(lambda: ctx.call("kdec_style_proj_fwd", P(Wf), P(bf), P(st), S, P(gbv), R, Nb, R, S))
+    by = 4.0 * (R * S + R + Nb * (S + R))
+    out["style_proj_fwd_R%d_x8" % R] = {"ms": round(t * 1e3, 4), "GB/s": round(by / t / 1e9, 1),
+                                        "frac_hbm": round(by / t / PEAK_HBM, 4), "algorithmic_bytes": by}
+    t = timed(lambda: ctx.call("kdec_style_proj_bwd", P(Wf), P(st), S, P(dgbv), R, P(dst), S, 0.0, None, None, Nb,
+                               R, S))
+    by = 4.0 * (R * S + Nb * (S + R))
+    out["style_proj_dstyle_R%d_x8" % R] = {"ms": round(t * 1e3, 4), "GB/s": round(by / t / 1e9, 1),
+                                           "frac_hbm": round(by / t / PEAK_HBM, 4), "algorithmic_bytes": by}
     return out
 
 

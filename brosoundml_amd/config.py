@@ -79,3 +79,24 @@ def lengths(cfg: dict, T: int) -> dict:
     audio = (frames - 1) * cfg["hop"]
     return dict(L_gen=L_gen, frames=frames, audio=audio,
                 audio_seconds=audio / cfg["sample_rate"])
+
+
+def affine_rows(cfg: dict) -> int:
+    """Rows of the stacked AdaIN style projection, sum over units of 2C:
+    the encode block's norms on C_in = asr_dim + 2 and enc_dim, each decode
+    block's on its input (the previous output cat'd with asr_res, F0 and N
+    up to and including the upsampling block) and output, and six units per
+    generator ResBlock1 (the noise_res block and K resblocks of each stage,
+    C = the last decode block's output / 2^(i+1) at stage i)."""
+    C = [cfg["asr_dim"] + 2, cfg["enc_dim"]]
+    prev, res = cfg["enc_dim"], True
+    for i in range(cfg["n_decode"]):
+        cin = prev + (cfg["asr_res_dim"] + 2 if res else 0)
+        C += [cin, cfg["dec_out"][i]]
+        prev = cfg["dec_out"][i]
+        if i == cfg["dec_up_at"]:
+            res = False
+    for i in range(cfg["n_ups"]):
+        c = cfg["dec_out"][cfg["n_decode"] - 1] // (2 ** (i + 1))
+        C += [c] * 6 * (1 + cfg["n_kernels"])
+    return 2 * sum(C)

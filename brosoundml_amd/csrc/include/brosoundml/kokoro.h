@@ -11,6 +11,7 @@
 #include <brotensor/tensor.h>
 
 #include <cstdint>
+#include <string>
 #include <vector>
 
 namespace brosoundml {
@@ -32,6 +33,37 @@ struct KokoroDecodePrep {
     // (kokoro.cpp:604-614).
     DecoderLoraContext context() const;
 };
+
+// Per-stage capture of the decoder pipeline's intermediates, the
+// reference's KokoroTrace (include/brosoundml/kokoro.h:149-185): each stage is
+// a host copy, row-major (h x w) FP32. decode_back_half records "gen_in"
+// (hidden x 2T), "har" ((n_fft + 2) x frames) and "audio" (1 x samples), in
+// that order; a batch of N > 1 utterances records each stage per utterance
+// as "<name>.<n>". A capture copies to host (a stream synchronisation), so it
+// happens only when a trace is passed.
+struct KokoroTrace {
+    struct Stage {
+        std::string name;
+        int h = 0;
+        int w = 0;
+        std::vector<float> data;  // h*w, row-major (row r = channel r)
+    };
+    std::vector<Stage> stages;
+
+    // Copy a tensor to host and record it as an (h x w) stage; a tensor of
+    // another element count is recorded as one (1 x size) row.
+    void add(std::string name, int h, int w, const brotensor::Tensor& t);
+    // Record an integer vector (e.g. pred_dur) as a (1 x n) stage.
+    void add_ints(std::string name, const std::vector<int32_t>& v);
+};
+
+// The reference's BROSOUNDML_DEBUG_STAGES diagnostics (kokoro.cpp:46-90):
+// when that environment variable is set (and not "0"), prints
+//   [stage] <tag> rows=.. cols=..  min=..  max=..  mean=..  std=..  nonfinite=..
+// for `t` to stderr (a host copy of the tensor); the count of NaN / Inf
+// elements is an addition (min / max / mean / std are over the finite ones).
+// No effect otherwise.
+void debug_stats(const char* tag, const brotensor::Tensor& t);
 
 // The producer step of Kokoro::prepare_decode_context after the predictor
 // (kokoro.cpp:667-732): length regulation of the text-encoder output t_en

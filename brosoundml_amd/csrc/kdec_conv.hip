@@ -151,11 +151,31 @@ struct TileGeo {
 
 // Logical tile order: m-tile fastest, then q-tile, then (utterance, phase),
 // with every last q-tile (usually partly empty: its idle waves skip their
-// MFMAs) moved to the end so that the short tiles come last.
+// MFMAs) moved to the end so that the short tiles come last. Polyphase
+// transposed convs take the phase right after the m-tile: the s phase tiles
+// of one q range store interleaved columns of the same output rows, and
+// consecutive tiles run side by side on one XCD (block_work), so their
+// partial cache lines meet in that XCD's L2 instead of each going to HBM.
 __device__ inline void decode_tile(const GemmArgs& g, int tile, TileGeo& T) {
     const int full = (g.q_tiles - 1) * g.m_tiles * g.nz;
     int mt, qt, zz, lid = tile;
-    if (lid < full) {
+    if (g.n_phase > 1) {
+        const bool last = lid >= full;
+        if (last) lid -= full;
+        mt = lid % g.m_tiles;
+        lid /= g.m_tiles;
+        const int r = lid % g.n_phase;
+        lid /= g.n_phase;
+        int b;
+        if (last) {
+            b = lid;
+            qt = g.q_tiles - 1;
+        } else {
+            qt = lid % (g.q_tiles - 1);
+            b = lid / (g.q_tiles - 1);
+        }
+        zz = b * g.n_phase + r;
+    } else if (lid < full) {
         mt = lid % g.m_tiles;
         lid /= g.m_tiles;
         qt = lid % (g.q_tiles - 1);

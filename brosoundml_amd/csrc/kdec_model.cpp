@@ -865,9 +865,12 @@ namespace {
 // Kokoro::Impl::decode_back_half (kokoro.cpp:352-407): DecoderBackbone,
 // HarmonicSource and Generator inference forwards; `cancel` is polled before
 // the generator (:387) and by the generator before each upsample stage.
+// With `trace`, the stages the reference records (kokoro.cpp:366, 389-390,
+// 396) are copied to it; with BROSOUNDML_DEBUG_STAGES set, each is also
+// summarised on stderr under the reference's tags (:365, 388, 395).
 int decode_back_half(kdec_model* m, int N, int T, const float* asr, const float* F0, const float* Nn,
                      const float* ref_s, long ref_bs, float* audio, const std::function<bool()>& cancel,
-                     int* cancelled) {
+                     int* cancelled, brosoundml::KokoroTrace* trace = nullptr) {
     const char* where = "kdec_model_decode_back_half";
     if (cancelled) *cancelled = 0;
     if (!m || N <= 0 || T <= 0 || !asr || !F0 || !Nn || !ref_s || !audio) return KDEC_EINVAL;
@@ -880,7 +883,21 @@ int decode_back_half(kdec_model* m, int N, int T, const float* asr, const float*
         };
         const Tensor rs = in(ref_s, m->style_dim, ref_bs);
         Tensor gen_in, har, out;
+        // stage `name` of each utterance: (h x w) per utterance row
+        auto record = [&](const char* tag, const char* name, const Tensor& t, int h, int w) {
+            brosoundml::debug_stats(tag, t);
+            if (!trace) return;
+            if (N == 1) {
+                trace->add(name, h, w, t);
+                return;
+            }
+            for (int n = 0; n < N; ++n) {
+                Tensor row = Tensor::view(Device::HIP, static_cast<float*>(t.data) + n * t.row_stride(), 1, t.cols);
+                trace->add(std::string(name) + "." + std::to_string(n), h, w, row);
+            }
+        };
         m->bb.forward(in(asr, m->asr_dim * T), in(F0, 2 * T), in(Nn, 2 * T), rs, T, gen_in);
+        record("09_gen_in", "gen_in", gen_in, gen_in.cols / (2 * T), 2 * T);
         int sig = 0, frames = 0;
         m->hs.forward(in(F0, 2 * T), 2 * T, sig, frames, har);
         int upr = 1;
@@ -889,6 +906,7 @@ int decode_back_half(kdec_model* m, int N, int T, const float* asr, const float*
             return fail(m, KDEC_EINVAL, "brosoundml: Kokoro::decode: har_frames mismatch: hsource=" +
                                             std::to_string(frames) + " vs expected=" +
                                             std::to_string(2 * T * upr + 1));
+        record("10_har_stub", "har", har, m->n_fft + 2, frames);
         if (cancel && cancel()) {
             if (cancelled) *cancelled = 1;
             return KDEC_OK;
@@ -898,6 +916,7 @@ int decode_back_half(kdec_model* m, int N, int T, const float* asr, const float*
             if (cancelled) *cancelled = 1;
             return KDEC_OK;
         }
+        record("11_audio", "audio", out, 1, out.cols);
         if (hipMemcpyAsync(audio, out.data, out.size() * sizeof(float), hipMemcpyDeviceToDevice,
                            static_cast<hipStream_t>(kdec_get_stream(m->ctx))) != hipSuccess)
             return fail(m, KDEC_EHIP, std::string(where) + ": output copy");
@@ -920,6 +939,47 @@ int kdec_model_decode_back_half_cancellable(kdec_model* m, int N, int T, const f
     std::function<bool()> poll;
     if (cancel) poll = [cancel, user] { return cancel(user) != 0; };
     return decode_back_half(m, N, T, asr, F0, Nn, ref_s, ref_bs, audio, poll, cancelled);
+}
+
+// ─── stage traces ───────────────────────────────────────────────────────────
+
+struct kdec_trace {
+    brosoundml::KokoroTrace t;
+};
+
+int kdec_trace_create(kdec_trace** out) {
+    if (!out) return KDEC_EINVAL;
+    *out = new kdec_trace();
+    return KDEC_OK;
+}
+
+int kdec_trace_destroy(kdec_trace* t) {
+    delete t;
+    return KDEC_OK;
+}
+
+int kdec_trace_count(const kdec_trace* t) { return t ? static_cast<int>(t->t.stages.size()) : -1; }
+
+const char* kdec_trace_stage(const kdec_trace* t, int i, int* h, int* w) {
+    if (!t || i < 0 || i >= static_cast<int>(t->t.stages.size())) return nullptr;
+    const auto& st = t->t.stages[static_cast<std::size_t>(i)];
+    if (h) *h = st.h;
+    if (w) *w = st.w;
+    return st.name.c_str();
+}
+
+const float* kdec_trace_data(const kdec_trace* t, int i) {
+    if (!t || i < 0 || i >= static_cast<int>(t->t.stages.size())) return nullptr;
+    return t->t.stages[static_cast<std::size_t>(i)].data.data();
+}
+
+int kdec_model_decode_back_half_traced(kdec_model* m, int N, int T, const float* asr, const float* F0,
+                                       const float* Nn, const float* ref_s, long ref_bs, float* audio,
+                                       kdec_cancel_fn cancel, void* user, int* cancelled, kdec_trace* trace) {
+    std::function<bool()> poll;
+    if (cancel) poll = [cancel, user] { return cancel(user) != 0; };
+    return decode_back_half(m, N, T, asr, F0, Nn, ref_s, ref_bs, audio, poll, cancelled,
+                            trace ? &trace->t : nullptr);
 }
 
 int kdec_model_set_overlap(kdec_model* m, int on) {

@@ -1,4 +1,5 @@
-// sin^2 for the Snake activation y = s + sin^2(a s) / a on gfx950.
+// sin^2 for the Snake activation y = s + sin^2(a s) / a on gfx950, and the
+// sin / cos pair of the spectral head's polar map, from one reduction.
 //
 // Cody-Waite reduction of th by pi/2 with a three-part split of pi/2 (each
 // product folded in by fma), then the Taylor series of sin or of cos on
@@ -59,6 +60,20 @@ KDEC_HD inline void snake_sin2_sin2x(float th, float& s2, float& sin2x) {
     s2 = v * v;
     const float t = 2.0f * sn * cs;
     sin2x = odd ? -t : t;
+}
+
+// sin th and cos th from one reduction: with th = q (pi/2) + r, the quadrant
+// q mod 4 (formed in float: q / 4, its floor and the difference are exact)
+// rotates (sin r, cos r) by q quarter turns.
+KDEC_HD inline void kdec_sincos(float th, float& s, float& c) {
+    float sn, cs;
+    snake_reduce(th, sn, cs);
+    const float q = rintf(th * 0.636619746685028076f);
+    const float qm = q - 4.0f * floorf(0.25f * q);  // 0, 1, 2 or 3
+    const bool odd = qm == 1.0f || qm == 3.0f;
+    const float s0 = odd ? cs : sn, c0 = odd ? sn : cs;
+    s = qm >= 2.0f ? -s0 : s0;
+    c = (qm == 1.0f || qm == 2.0f) ? -c0 : c0;
 }
 
 }  // namespace kdec

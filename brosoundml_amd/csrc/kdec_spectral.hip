@@ -8,7 +8,9 @@
 // The transforms are n_fft = 20 direct sums with twiddles staged in LDS:
 // far too small for an FFT to pay, and direct sums keep the order fixed.
 #include "kdec_internal.hpp"
+#include "kdec_snake_math.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <type_traits>
 #include <vector>
@@ -172,6 +174,200 @@ __global__ __launch_bounds__(FT) void spec_bwd_k(const float* post, long post_bs
         const float dang = mag * (-dRe * sa + dIm * ca);
         D[static_cast<long>(k) * L + f] = dmag * mag;
         D[static_cast<long>(F + k) * L + f] = dang * cosf(pp);
+    }
+}
+
+// ─── n_fft = 20, hop = 5 (the Kokoro head), specialised ───
+// The same arithmetic as spec_frames_k / spec_ola_k / spec_bwd_k with the
+// transform size known at compile time: every loop unrolls, the real DFT is
+// folded on its symmetry (n and N - n share the cosine and negate the sine,
+// so a bin's sums run over N/2 - 1 pairs), a frame's sin / cos of one angle
+// come from one sincosf, and each block stages what its frames share in LDS:
+// the forward keeps its frames (plus the K - 1 = N/H - 1 frames before them
+// that overlap its samples) and overlap-adds them there, so no frame buffer
+// goes through HBM; the backward stages dY / envelope over its frames'
+// sample span once, so each sample's envelope is formed once per block.
+
+// cos / sin(2 pi r / N), r < N, formed on the host in double and rounded to
+// float (the values load_twiddles forms on the device), passed by value so
+// that they sit in scalar registers
+template <int N>
+struct Tw {
+    float c[N], s[N];
+};
+template <int N>
+Tw<N> make_tw() {
+    Tw<N> t;
+    for (int r = 0; r < N; ++r) {
+        t.c[r] = static_cast<float>(std::cos(2.0 * M_PI * r / N));
+        t.s[r] = static_cast<float>(std::sin(2.0 * M_PI * r / N));
+    }
+    return t;
+}
+
+template <int N>
+__device__ inline void load_win(float* win, const float* window) {
+    if (threadIdx.x < N) win[threadIdx.x] = window ? window[threadIdx.x] : hann_at(threadIdx.x, N);
+}
+
+// Frames per forward block: the block forms FT frames, FT - KB of them its
+// own and the KB before them, whose tails overlap its first samples.
+template <int N, int H>
+constexpr int fwd_own_frames() {
+    return FT - ((N + H - 1) / H - 1);
+}
+
+template <int N, int H>
+__global__ __launch_bounds__(FT) void spec_fwd_fixed_k(const float* post, long post_bs, const float* window,
+                                                      float* audio, long audio_bs, int L, Tw<N> tw) {
+    constexpr int F = N / 2 + 1;
+    constexpr int KB = (N + H - 1) / H - 1;  // earlier frames overlapping the block's samples
+    constexpr int OWN = fwd_own_frames<N, H>();
+    constexpr int NP = N + 1;                // LDS frame stride (odd: no bank conflicts)
+    __shared__ float win[N];
+    __shared__ float fr[FT * NP];
+    __shared__ float ienv[H];  // 1 / envelope at interior positions, by m mod H
+    load_win<N>(win, window);
+    const int b = blockIdx.y;
+    const int f0 = blockIdx.x * OWN;  // first own frame
+    const float* P = post + b * post_bs;
+    {
+        const int f = f0 - KB + static_cast<int>(threadIdx.x);
+        float* out = fr + threadIdx.x * NP;
+        float re[F], im[F];
+        const bool in = f >= 0 && f < L;
+#pragma unroll
+        for (int k = 0; k < F; ++k) {
+            re[k] = im[k] = 0.0f;
+            if (in) {
+                const float mag = expf(P[static_cast<long>(k) * L + f]);
+                float spp, cpp, sa, ca;
+                kdec_sincos(P[static_cast<long>(F + k) * L + f], spp, cpp);
+                kdec_sincos(spp, sa, ca);
+                re[k] = mag * ca;
+                im[k] = mag * sa;
+            }
+        }
+        __syncthreads();  // win
+        if (threadIdx.x < H) ienv[threadIdx.x] = 1.0f / env_at(win, N + ((threadIdx.x - N) % H + H) % H, N, H, L);
+        // x[n] = (re0 + (-1)^n re_{N/2} + 2 sum_k re_k cos) - 2 sum_k im_k sin,
+        // x[N - n] the same with the sine sum added
+        constexpr float invN = 1.0f / N;
+        const float e0 = re[0] + re[F - 1], e1 = re[0] - re[F - 1];
+#pragma unroll
+        for (int n = 0; n <= N / 2; n += N / 2) {  // the two points without a sine term
+            float a = (n & 1) ? e1 : e0;
+#pragma unroll
+            for (int k = 1; k < F - 1; ++k) a += 2.0f * re[k] * tw.c[(k * n) % N];
+            out[n] = a * invN * win[n];
+        }
+#pragma unroll
+        for (int n = 1; n < N / 2; ++n) {
+            float a = (n & 1) ? e1 : e0, bb = 0.0f;
+#pragma unroll
+            for (int k = 1; k < F - 1; ++k) {
+                a += 2.0f * re[k] * tw.c[(k * n) % N];
+                bb += 2.0f * im[k] * tw.s[(k * n) % N];
+            }
+            out[n] = (a - bb) * invN * win[n];
+            out[N - n] = (a + bb) * invN * win[N - n];
+        }
+    }
+    __syncthreads();
+    // samples j with ola position m = j + N/2 in [f0 * H, (f0 + OWN) * H)
+    const int sig_len = (L - 1) * H;
+    float* A = audio + b * audio_bs;
+    for (int i = threadIdx.x; i < OWN * H; i += FT) {
+        const int m = f0 * H + i;
+        const int j = m - N / 2;
+        if (j < 0 || j >= sig_len) continue;
+        int f_hi = m / H;
+        if (f_hi > L - 1) f_hi = L - 1;
+        float acc = 0.0f, e = 0.0f;
+        for (int f = f_hi; f >= 0 && m - f * H < N; --f) {
+            const int n = m - f * H;
+            acc += fr[(f - f0 + KB) * NP + n];
+            e += win[n] * win[n];
+        }
+        A[j] = (m >= N && m <= (L - 1) * H) ? acc * ienv[m % H] : acc / e;
+    }
+}
+
+// The backward, one block per FT frames of one utterance: the block's polar
+// inputs are loaded first (their loads fly while dY / envelope over the
+// frames' sample span is staged in LDS), then each thread forms its frame's
+// grads. At most 64 VGPRs, so that every block of the decoder's head is
+// resident at once.
+template <int N, int H>
+__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(8)))
+void spec_bwd_fixed_k(const float* post, long post_bs, const float* window, const float* daudio, long da_bs,
+                      float* dpost, long dp_bs, int L, Tw<N> tw) {
+    constexpr int F = N / 2 + 1;
+    constexpr int M = FT * H + N;  // ola positions the block's frames cover
+    __shared__ float win[N];
+    __shared__ float ienv[H];  // 1 / envelope at interior positions, by m mod H
+    __shared__ float u[M];
+    load_win<N>(win, window);
+    const int b = blockIdx.y;
+    const int f0 = blockIdx.x * FT;
+    const int f = f0 + threadIdx.x;
+    const float* P = post + b * post_bs + min(f, L - 1);
+    float pm[F], pp[F];
+#pragma unroll
+    for (int k = 0; k < F; ++k) {
+        pm[k] = P[static_cast<long>(k) * L];
+        pp[k] = P[static_cast<long>(F + k) * L];
+    }
+    __syncthreads();  // win
+    // an interior position m (every frame that could cover it exists:
+    // N <= m <= (L - 1) H) sees the same windows as m + H
+    if (threadIdx.x < H) ienv[threadIdx.x] = 1.0f / env_at(win, N + ((threadIdx.x - N) % H + H) % H, N, H, L);
+    __syncthreads();
+    const int sig_len = (L - 1) * H;
+    // u[i] = dY[j] / envelope(m) at ola position m = f0 * H + i (j = m - N/2;
+    // 0 outside the signal, where the envelope may be 0)
+    const float* dy = daudio + b * da_bs;
+    for (int i = threadIdx.x; i < M; i += FT) {
+        const int m = f0 * H + i;
+        const int j = m - N / 2;
+        float v = 0.0f;
+        if (j >= 0 && j < sig_len)
+            v = (m >= N && m <= (L - 1) * H) ? dy[j] * ienv[m % H] : dy[j] / env_at(win, m, N, H, L);
+        u[i] = v;
+    }
+    __syncthreads();
+    if (f >= L) return;
+    constexpr float invN = 1.0f / N;
+    float dfr[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n) dfr[n] = u[threadIdx.x * H + n] * win[n] * invN;
+    float sp[N / 2], dm[N / 2];  // pair sums / differences, n = 1 .. N/2 - 1
+#pragma unroll
+    for (int n = 1; n < N / 2; ++n) {
+        sp[n] = dfr[n] + dfr[N - n];
+        dm[n] = dfr[n] - dfr[N - n];
+    }
+    float* D = dpost + b * dp_bs + f;
+#pragma unroll
+    for (int k = 0; k < F; ++k) {
+        const bool edge = k == 0 || k == F - 1;
+        float re = dfr[0] + ((k & 1) ? -dfr[N / 2] : dfr[N / 2]);
+        float im = 0.0f;
+#pragma unroll
+        for (int n = 1; n < N / 2; ++n) {
+            re += sp[n] * tw.c[(k * n) % N];
+            im -= dm[n] * tw.s[(k * n) % N];
+        }
+        const float dRe = edge ? re : 2.0f * re;
+        const float dIm = edge ? 0.0f : 2.0f * im;
+        const float mag = expf(pm[k]);
+        float spp, cpp, sa, ca;
+        kdec_sincos(pp[k], spp, cpp);
+        kdec_sincos(spp, sa, ca);
+        const float dmag = dRe * ca + dIm * sa;
+        const float dang = mag * (-dRe * sa + dIm * ca);
+        D[static_cast<long>(k) * L] = dmag * mag;
+        D[static_cast<long>(F + k) * L] = dang * cpp;
     }
 }
 
@@ -411,6 +607,151 @@ __global__ void style_bwd_w_k(const float* style, long s_bs, const float* dout, 
     }
 }
 
+// The same projections reading each fc row once for all N utterances (the
+// wave-per-(row, utterance) kernels above read the fc block N times): a block
+// owns STR consecutive rows. Forward: the rows' [STR][S] slab and the styles
+// [N][S] are staged in LDS (slab stride S + 1: a lane per row, conflict
+// free), each thread then forms its row's dot products for every fourth
+// utterance in double, in column order. d(style): threads own (row phase,
+// column) and accumulate over the block's rows, in order, for up to STN
+// utterances at a time in double; the phases are combined in order and the
+// blocks' partials are summed, in block order, by style_bwd_x_sum_k.
+constexpr int STR = 64;   // forward rows per block
+constexpr int STB = 64;   // d(style) rows per block
+constexpr int STN = 8;    // utterances per d(style) pass
+
+__global__ __launch_bounds__(256) void style_fwd_rows_k(const float* W, const float* bias, const float* style,
+                                                        long s_bs, float* out, long o_bs, int N, int rows, int S) {
+    extern __shared__ float sm[];
+    float* wt = sm;                   // [STR][S + 1]
+    float* st = sm + STR * (S + 1);   // [N][S]
+    const int r0 = blockIdx.x * STR;
+    const int nr = min(STR, rows - r0);
+    // the slab's loads issued eight at a time before their LDS stores; thread
+    // t stages column t % S of rows t / S, t / S + 256 / S, ... (256 % S == 0)
+    const float* Wb = W + static_cast<long>(r0) * S;
+    const int j = threadIdx.x % S, rstep = 256 / S;
+    for (int r = threadIdx.x / S; r < nr; r += 32 * rstep) {
+        float v[32];
+#pragma unroll
+        for (int q = 0; q < 32; ++q) {
+            const int rr = r + q * rstep;
+            v[q] = rr < nr ? Wb[static_cast<long>(rr) * S + j] : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < 32; ++q) {
+            const int rr = r + q * rstep;
+            if (rr < nr) wt[rr * (S + 1) + j] = v[q];
+        }
+    }
+    for (int n = threadIdx.x / S; n < N; n += rstep) st[n * S + j] = style[n * s_bs + j];
+    __syncthreads();
+    const int r = threadIdx.x & (STR - 1);
+    if (r >= nr) return;
+    const float* w = wt + r * (S + 1);
+    const float b = bias ? bias[r0 + r] : 0.0f;
+    for (int n = threadIdx.x / STR; n < N; n += 256 / STR) {  // wave-uniform n: st reads broadcast
+        const float* sn = st + n * S;
+        double a0 = 0.0, a1 = 0.0;  // even / odd columns: two independent chains
+#pragma unroll 8
+        for (int jj = 0; jj + 1 < S; jj += 2) {
+            a0 += static_cast<double>(w[jj]) * sn[jj];
+            a1 += static_cast<double>(w[jj + 1]) * sn[jj + 1];
+        }
+        if (S & 1) a0 += static_cast<double>(w[S - 1]) * sn[S - 1];
+        out[n * o_bs + r0 + r] = static_cast<float>((a0 + a1) + b);
+    }
+}
+
+// part[blk][n][j] = sum over the block's rows r of W[r, j] dout[n, r]
+__global__ __launch_bounds__(256) void style_bwd_x_rows_k(const float* W, const float* dout, long d_bs, float* part,
+                                                          int N, int rows, int S) {
+    extern __shared__ float sm[];
+    const int PH = 256 / S;           // row phases
+    float* dsl = sm;                  // [N][STB]
+    float* red = sm + N * STB;        // [PH][STN][S]
+    const int r0 = blockIdx.x * STB;
+    const int nr = min(STB, rows - r0);
+    for (int i = threadIdx.x; i < N * STB; i += 256) {
+        const int n = i / STB, rr = i - n * STB;
+        dsl[i] = rr < nr ? dout[n * d_bs + r0 + rr] : 0.0f;
+    }
+    __syncthreads();
+    const int j = threadIdx.x % S, ph = threadIdx.x / S;
+    for (int n0 = 0; n0 < N; n0 += STN) {
+        const int nn = min(STN, N - n0);
+        double acc[STN];
+#pragma unroll
+        for (int q = 0; q < STN; ++q) acc[q] = 0.0;
+        // the thread's column of the block's rows, loaded 32 at a time before use
+        for (int rb = ph; rb < nr; rb += 32 * PH) {
+            float w[32];
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const int rr = rb + i * PH;
+                w[i] = rr < nr ? W[static_cast<long>(r0 + rr) * S + j] : 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const int rr = rb + i * PH;
+                if (rr < nr) {
+#pragma unroll
+                    for (int q = 0; q < STN; ++q)
+                        if (q < nn) acc[q] += static_cast<double>(w[i]) * dsl[(n0 + q) * STB + rr];
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < STN; ++q)
+            if (q < nn) red[(ph * STN + q) * S + j] = static_cast<float>(acc[q]);
+        __syncthreads();
+        for (int i = threadIdx.x; i < nn * S; i += 256) {
+            const int q = i / S, jj = i - q * S;
+            double t = 0.0;
+            for (int h = 0; h < PH; ++h) t += red[(h * STN + q) * S + jj];
+            part[(static_cast<long>(blockIdx.x) * N + n0 + q) * S + jj] = static_cast<float>(t);
+        }
+        __syncthreads();
+    }
+}
+
+// dstyle[n, j] = beta * dstyle[n, j] + the sum over blocks q of
+// part[q][n][j] in a fixed order: 64 outputs per block, its 16 waves each
+// summing a contiguous sixteenth of the block range (eight partials in
+// flight per lane), the waves' sums then added in a fixed tree
+__global__ __launch_bounds__(1024) void style_bwd_x_sum_k(const float* part, int nblk, float* dstyle, long ds_bs,
+                                                          float beta, int N, int S) {
+    __shared__ double red[16][64];
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nj = blockIdx.x * 64 + lane;
+    const int NS = N * S;
+    double acc = 0.0;
+    if (nj < NS) {
+        const int q0 = wv * nblk / 16, q1 = (wv + 1) * nblk / 16;
+        double a8[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a8[i] = 0.0;
+        int q = q0;
+        for (; q + 8 <= q1; q += 8) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a8[i] += part[static_cast<long>(q + i) * NS + nj];
+        }
+        for (int i = 0; q < q1; ++q, ++i) a8[i] += part[static_cast<long>(q) * NS + nj];
+        acc = ((a8[0] + a8[1]) + (a8[2] + a8[3])) + ((a8[4] + a8[5]) + (a8[6] + a8[7]));
+    }
+    red[wv][lane] = acc;
+    __syncthreads();
+    for (int h = 8; h >= 1; h >>= 1) {
+        if (wv < h) red[wv][lane] += red[wv + h][lane];
+        __syncthreads();
+    }
+    if (wv == 0 && nj < NS) {
+        const int n = nj / S, j = nj - n * S;
+        float* d = dstyle + n * ds_bs + j;
+        *d = static_cast<float>(red[0][lane]) + (beta != 0.0f ? beta * *d : 0.0f);
+    }
+}
+
 // ─── LoRA term of the style projection ───────────────────────────────────
 // Units are stacked row-wise: unit u owns rows [off[u], off[u+1]) of W, b, B
 // and rows [u*rank, (u+1)*rank) of A; H[n, u*rank + j] = A[u*rank + j] . s[n].
@@ -542,9 +883,18 @@ int kdec_spectral_fwd(kdec_ctx* ctx, const float* post, long post_bs,
     KDEC_CHECK(ctx, post && audio && N > 0 && L > 1 && n_fft >= 2 && n_fft <= MAXN && hop > 0 && hop <= n_fft,
                "kdec_spectral_fwd: bad arguments");
     const int sig = (L - 1) * hop;
+    // post in, audio out
+    const double bytes = 4.0 * N * (static_cast<double>(n_fft + 2) * L + sig);
+    if (n_fft == 20 && hop == 5) {
+        ProfScope ps(ctx, "spectral", 0, bytes);
+        hipLaunchKernelGGL((spec_fwd_fixed_k<20, 5>),
+                           dim3(static_cast<unsigned>(cdiv(L, fwd_own_frames<20, 5>())), N), dim3(FT), 0, ctx->stream,
+                           post, post_bs, window, audio, audio_bs, L, make_tw<20>());
+        return launch_check(ctx, "spec_fwd");
+    }
     Workspace fb(ctx, static_cast<size_t>(N) * L * n_fft * sizeof(float));
     if (!fb.p) return KDEC_ENOMEM;
-    ProfScope ps(ctx, "spectral", 0);
+    ProfScope ps(ctx, "spectral", 0, bytes);
     with_nfft_bound(n_fft, [&](auto nm) {
         hipLaunchKernelGGL(spec_frames_k<decltype(nm)::value>, dim3(static_cast<unsigned>(cdiv(L, FT)), N),
                            dim3(FT), 0, ctx->stream, post, post_bs, window, fb.as<float>(), L, n_fft);
@@ -563,7 +913,14 @@ int kdec_spectral_bwd(kdec_ctx* ctx, const float* post, long post_bs,
     KDEC_CHECK(ctx, post && daudio && dpost && N > 0 && L > 1 && n_fft >= 2 && n_fft <= MAXN && hop > 0 &&
                         hop <= n_fft,
                "kdec_spectral_bwd: bad arguments");
-    ProfScope ps(ctx, "spectral", 0);
+    // post in, dAudio in, dpost out
+    const double bytes = 4.0 * N * (2.0 * (n_fft + 2) * L + static_cast<double>(L - 1) * hop);
+    ProfScope ps(ctx, "spectral_bwd", 0, bytes);
+    if (n_fft == 20 && hop == 5) {
+        hipLaunchKernelGGL((spec_bwd_fixed_k<20, 5>), dim3(static_cast<unsigned>(cdiv(L, FT)), N), dim3(FT), 0,
+                           ctx->stream, post, post_bs, window, daudio, daudio_bs, dpost, dpost_bs, L, make_tw<20>());
+        return launch_check(ctx, "spec_bwd");
+    }
     with_nfft_bound(n_fft, [&](auto nm) {
         hipLaunchKernelGGL(spec_bwd_k<decltype(nm)::value>, dim3(static_cast<unsigned>(cdiv(L, FT)), N), dim3(FT),
                            0, ctx->stream, post, post_bs, window, daudio, daudio_bs, dpost, dpost_bs, L, n_fft, hop);
@@ -614,7 +971,14 @@ int kdec_style_proj_fwd(kdec_ctx* ctx, const float* W, const float* b,
                         long out_bs, int N, int rows, int S) {
     if (!ctx) return KDEC_EINVAL;
     KDEC_CHECK(ctx, W && style && out && N > 0 && rows > 0 && S > 0, "kdec_style_proj_fwd: bad arguments");
-    ProfScope ps(ctx, "style_proj", 0);
+    // W once, style and out per utterance
+    ProfScope ps(ctx, "style_proj", 0, 4.0 * (static_cast<double>(rows) * S + static_cast<double>(N) * (S + rows)));
+    const size_t lds = (static_cast<size_t>(STR) * (S + 1) + static_cast<size_t>(N) * S) * sizeof(float);
+    if (lds <= 64 * 1024 && S <= 256 && 256 % S == 0) {
+        hipLaunchKernelGGL(style_fwd_rows_k, dim3(static_cast<unsigned>(cdiv(rows, STR))), dim3(256), lds,
+                           ctx->stream, W, b, style, style_bs, out, out_bs, N, rows, S);
+        return launch_check(ctx, "style_proj_fwd");
+    }
     const long waves = static_cast<long>(rows) * N;
     hipLaunchKernelGGL(style_fwd_k, dim3(static_cast<unsigned>(cdiv(waves * 64, 256))), dim3(256), 0,
                        ctx->stream, W, b, style, style_bs, out, out_bs, N, rows, S);
@@ -627,8 +991,22 @@ int kdec_style_proj_bwd(kdec_ctx* ctx, const float* W, const float* style,
                         float* db, int N, int rows, int S) {
     if (!ctx) return KDEC_EINVAL;
     KDEC_CHECK(ctx, W && style && dout && N > 0 && rows > 0 && S > 0, "kdec_style_proj_bwd: bad arguments");
-    ProfScope ps(ctx, "style_proj", 0);
-    if (dstyle) {
+    ProfScope ps(ctx, "style_proj", 0,
+                 4.0 * (static_cast<double>(rows) * S * ((dstyle ? 1 : 0) + (dW ? 2 : 0)) +
+                        static_cast<double>(N) * (rows + S)));
+    const size_t xlds = (static_cast<size_t>(N) * STB + static_cast<size_t>(256 / std::max(S, 1)) * STN * S) *
+                        sizeof(float);
+    if (dstyle && S <= 256 && 256 % S == 0 && xlds <= 64 * 1024) {
+        const int nblk = static_cast<int>(cdiv(rows, STB));
+        Workspace part(ctx, static_cast<size_t>(nblk) * N * S * sizeof(float));
+        if (!part.p) return KDEC_ENOMEM;
+        hipLaunchKernelGGL(style_bwd_x_rows_k, dim3(nblk), dim3(256), xlds, ctx->stream, W, dout, dout_bs,
+                           part.as<float>(), N, rows, S);
+        if (int rc = launch_check(ctx, "style_bwd_x")) return rc;
+        hipLaunchKernelGGL(style_bwd_x_sum_k, dim3(static_cast<unsigned>(cdiv(static_cast<long>(N) * S, 64))),
+                           dim3(1024), 0, ctx->stream, part.as<float>(), nblk, dstyle, dstyle_bs, beta, N, S);
+        if (int rc = launch_check(ctx, "style_bwd_x_reduce")) return rc;
+    } else if (dstyle) {
         const int nblk = static_cast<int>(cdiv(rows, SR));
         Workspace part(ctx, static_cast<size_t>(nblk) * N * S * sizeof(float));
         if (!part.p) return KDEC_ENOMEM;

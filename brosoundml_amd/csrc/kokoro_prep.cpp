@@ -7,6 +7,9 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <numeric>
 #include <stdexcept>
 #include <string>
@@ -24,6 +27,62 @@ namespace {
 }
 
 }  // namespace
+
+void KokoroTrace::add(std::string name, int h, int w, const bt::Tensor& t) {
+    Stage st;
+    st.name = std::move(name);
+    st.data = t.to_host_vector();
+    const long n = static_cast<long>(st.data.size());
+    if (h > 0 && w > 0 && static_cast<long>(h) * w == n) {
+        st.h = h;
+        st.w = w;
+    } else {
+        st.h = 1;
+        st.w = static_cast<int>(n);
+    }
+    stages.push_back(std::move(st));
+}
+
+void KokoroTrace::add_ints(std::string name, const std::vector<int32_t>& v) {
+    Stage st;
+    st.name = std::move(name);
+    st.h = 1;
+    st.w = static_cast<int>(v.size());
+    st.data.assign(v.begin(), v.end());
+    stages.push_back(std::move(st));
+}
+
+void debug_stats(const char* tag, const bt::Tensor& t) {
+    static const bool on = [] {
+        const char* v = std::getenv("BROSOUNDML_DEBUG_STAGES");
+        return v && v[0] && v[0] != '0';
+    }();
+    if (!on) return;
+    if (!t.data || t.size() == 0) {
+        std::fprintf(stderr, "[stage] %-24s empty\n", tag);
+        return;
+    }
+    const std::vector<float> d = t.to_host_vector();
+    long bad = 0, n = 0;
+    float mn = 0.0f, mx = 0.0f;
+    double sum = 0.0, sumsq = 0.0;
+    for (float v : d) {
+        if (!std::isfinite(v)) {
+            ++bad;
+            continue;
+        }
+        if (n == 0 || v < mn) mn = v;
+        if (n == 0 || v > mx) mx = v;
+        sum += v;
+        sumsq += static_cast<double>(v) * v;
+        ++n;
+    }
+    const double mean = n ? sum / n : 0.0;
+    const double var = n ? sumsq / n - mean * mean : 0.0;
+    std::fprintf(stderr,
+                 "[stage] %-24s rows=%d cols=%d  min=%+.4f  max=%+.4f  mean=%+.4f  std=%.4f  nonfinite=%ld\n", tag,
+                 t.rows, t.cols, mn, mx, mean, var > 0 ? std::sqrt(var) : 0.0, bad);
+}
 
 DecoderLoraContext KokoroDecodePrep::context() const {
     DecoderLoraContext c;

@@ -124,6 +124,27 @@ typedef int (*kdec_cancel_fn)(void* user);
 int kdec_model_decode_back_half_cancellable(kdec_model* m, int N, int T, const float* asr, const float* F0,
                                             const float* Nn, const float* ref_s, long ref_bs, float* audio,
                                             kdec_cancel_fn cancel, void* user, int* cancelled);
+/* Stage traces (the reference's KokoroTrace, kokoro.h:149-185, filled by
+ * decode_back_half at kokoro.cpp:366, 389-390, 396): a trace holds named
+ * host copies of the pipeline's intermediates as row-major (h x w) floats.
+ * kdec_model_decode_back_half_traced is decode_back_half with cancellation
+ * that also appends "gen_in" (hidden x 2T), "har" ((n_fft+2) x frames) and
+ * "audio" (1 x samples) to `trace` (per utterance "<name>.<n>" when N > 1;
+ * each capture synchronises the stream). trace may be NULL. With the
+ * environment variable BROSOUNDML_DEBUG_STAGES set (not "0"), every
+ * decode_back_half also prints those stages' min / max / mean / std and
+ * non-finite count to stderr (kokoro.cpp:46-90, tags 09_gen_in, 10_har_stub,
+ * 11_audio). kdec_trace_stage returns stage i's name (valid while the trace
+ * lives) and shape, kdec_trace_data its h*w floats. */
+typedef struct kdec_trace kdec_trace;
+int kdec_trace_create(kdec_trace** out);
+int kdec_trace_destroy(kdec_trace* t);
+int kdec_trace_count(const kdec_trace* t);
+const char* kdec_trace_stage(const kdec_trace* t, int i, int* h, int* w);
+const float* kdec_trace_data(const kdec_trace* t, int i);
+int kdec_model_decode_back_half_traced(kdec_model* m, int N, int T, const float* asr, const float* F0,
+                                       const float* Nn, const float* ref_s, long ref_bs, float* audio,
+                                       kdec_cancel_fn cancel, void* user, int* cancelled, kdec_trace* trace);
 /* Stream overlap (no counterpart in the reference, whose calls are
  * synchronous): on = 1 (the default) runs the harmonic source and the conv
  * weight grads on a second stream beside the main chain, and the

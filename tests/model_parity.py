@@ -225,13 +225,17 @@ def record_grads(name, worst):
     error over the bar."""
     nz = [w for w in worst if w[4]]
     zero = [w for w in worst if not w[4]]
-    w = max(nz, key=lambda t: t[2])
     top = max(worst)
-    extra = dict(param=w[1], worst_err_over_tol=top[0], worst_err_over_tol_param=top[1])
+    extra = dict(worst_err_over_tol=top[0], worst_err_over_tol_param=top[1])
+    rel = mx = None
+    if nz:  # (none in the reference semantics without alpha grads)
+        w = max(nz, key=lambda t: t[2])
+        rel, mx = w[2], w[3]
+        extra["param"] = w[1]
     if zero:
         z = max(zero, key=lambda t: t[3])
         extra.update(zero_grads=len(zero), zero_grads_worst_max_abs=z[3], zero_grads_worst_param=z[1])
-    record(f"{name} parameter grads ({len(worst)}; worst rel-L2)", w[2], w[3], **extra)
+    record(f"{name} parameter grads ({len(worst)}; worst rel-L2)", rel, mx, **extra)
 
 
 def check_pair(r, wgrad=True, name=None):

@@ -9,6 +9,8 @@ returns, and d(style). Both sides take the oracle's harmonic-source output so
 the comparison is not exposed to the atan2 of near-empty STFT bins (the
 harmonic source itself is compared in test_gpu_ops).
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -260,3 +262,83 @@ def test_decode_back_half_cancellation(ctx):
         else:
             assert flag.value == 1 and len(polls) == cancel_at
             assert torch.all(out == 7.0)
+
+
+def test_decode_back_half_trace(ctx):
+    # the reference's KokoroTrace from decode_back_half (kokoro.cpp:366,
+    # 389-390, 396): "gen_in", "har" and "audio" per utterance, equal to the
+    # untraced call's audio, the harmonic-source op's output and the oracle's
+    # backbone output
+    import ctypes
+    import oracle_lib as O
+    from brosoundml_amd import native
+    cfg, N, T = C.SMALL, 2, 6
+    m = native.Model(ctx, cfg)
+    params = synth.init_params(m.param_shapes())
+    m.set_params(params)
+    asr, F0, Nn, style, _ = inputs(cfg, N, T, "gm.trace")
+    S = cfg["style_dim"]
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    t = [dev(a) for a in (asr, F0, Nn)]
+    ref_s = dev(np.concatenate([style, style], axis=1))
+    L = C.lengths(cfg, T)
+    P = native.ptr
+    plain = torch.empty(N, L["audio"], device="cuda")
+    m._c(ctx.L.kdec_model_decode_back_half(m.h, N, T, P(t[0]), P(t[1]), P(t[2]), P(ref_s), 2 * S, P(plain)))
+    tr = ctypes.c_void_p()
+    ctx.check(ctx.L.kdec_trace_create(ctypes.byref(tr)))
+    traced = torch.empty_like(plain)
+    m._c(ctx.L.kdec_model_decode_back_half_traced(m.h, N, T, P(t[0]), P(t[1]), P(t[2]), P(ref_s), 2 * S,
+                                                  P(traced), None, None, None, tr))
+    torch.cuda.synchronize()
+    assert torch.equal(plain, traced)
+    stages = {}
+    for i in range(ctx.L.kdec_trace_count(tr)):
+        h, w = ctypes.c_int(), ctypes.c_int()
+        name = ctx.L.kdec_trace_stage(tr, i, ctypes.cast(ctypes.pointer(h), ctypes.c_void_p),
+                                      ctypes.cast(ctypes.pointer(w), ctypes.c_void_p)).decode()
+        p = ctypes.cast(ctx.L.kdec_trace_data(tr, i), ctypes.POINTER(ctypes.c_float))
+        stages[name] = np.ctypeslib.as_array(p, shape=(h.value * w.value,)).copy().reshape(h.value, w.value)
+    ctx.check(ctx.L.kdec_trace_destroy(tr))
+    assert list(stages) == [f"{s}.{n}" for s in ("gen_in", "har", "audio") for n in range(N)]
+    om = O.OracleModel(cfg)
+    om.set_params(params)
+    for n in range(N):
+        assert stages[f"audio.{n}"].shape == (1, L["audio"])
+        np.testing.assert_array_equal(stages[f"audio.{n}"][0], plain[n].cpu().numpy())
+        assert stages[f"har.{n}"].shape == (cfg["n_fft"] + 2, L["frames"])
+        om.forward(asr[n], F0[n], Nn[n], style[n], T)
+        assert rel_l2(stages[f"har.{n}"][: cfg["n_fft"] // 2 + 1], om.har().reshape(cfg["n_fft"] + 2, -1)[
+            : cfg["n_fft"] // 2 + 1]) <= 1e-5
+        gi = stages[f"gen_in.{n}"]
+        assert gi.shape == (cfg["dec_out"][-1], 2 * T)
+        assert rel_l2(gi.ravel(), om.gen_in()) <= 1e-5
+
+
+def test_debug_stages_env():
+    # BROSOUNDML_DEBUG_STAGES=1: decode_back_half prints the reference's
+    # per-stage summaries (kokoro.cpp:46-90) plus the non-finite count, in a
+    # child process so the environment is read fresh
+    import subprocess
+    import sys
+    code = (
+        "import sys, numpy as np, torch\n"
+        "sys.path[:0] = [%r, %r]\n"
+        "from brosoundml_amd import native, config as C, synth\n"
+        "from model_parity import inputs\n"
+        "ctx = native.Context(0); cfg = C.SMALL; N, T = 1, 5\n"
+        "m = native.Model(ctx, cfg); m.set_params(synth.init_params(m.param_shapes()))\n"
+        "asr, F0, Nn, st, _ = inputs(cfg, N, T, 'gm.dbg')\n"
+        "d = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()\n"
+        "rs = d(np.concatenate([st, st], axis=1)); a = torch.empty(N, C.lengths(cfg, T)['audio'], device='cuda')\n"
+        "P = native.ptr\n"
+        "m._c(ctx.L.kdec_model_decode_back_half(m.h, N, T, P(d(asr)), P(d(F0)), P(d(Nn)), P(rs), 2 * cfg['style_dim'], P(a)))\n"
+        "torch.cuda.synchronize()\n" % (os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                                        os.path.dirname(os.path.abspath(__file__))))
+    env = dict(os.environ, BROSOUNDML_DEBUG_STAGES="1")
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, r.stderr[-2000:]
+    lines = [ln for ln in r.stderr.splitlines() if ln.startswith("[stage]")]
+    assert [ln.split()[1] for ln in lines] == ["09_gen_in", "10_har_stub", "11_audio"], r.stderr[-2000:]
+    for ln in lines:
+        assert "nonfinite=0" in ln and "std=" in ln, ln

@@ -294,3 +294,11 @@ def test_fd_lora_gate_and_style(lora64):
     fd = central(lambda hh: loss64(m, r["inputs"], r["har"], style + hh * vs)[0])
     an = float(np.dot(r["dstyle"].astype(np.float64), vs))
     assert abs(an - fd) <= TOL * max(abs(an), abs(fd), 1e-2), ("style", an, fd)
+
+
+@pytest.mark.parametrize("name", ["TINY", "SMALL", "KOKORO"])
+def test_affine_rows_match_the_units(name):
+    # config.affine_rows (the bench's style-projection case) against the
+    # oracle model's own AdaIN units
+    cfg = getattr(C, name)
+    assert C.affine_rows(cfg) == 2 * sum(c for _, c in O.OracleModel(cfg).units())

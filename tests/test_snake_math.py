@@ -1,8 +1,8 @@
-"""The Snake forward's sin^2 and the backward's (sin^2, sin 2th) pair
-(brosoundml_amd/csrc/kdec_snake_math.hpp), built for the host with g++ and
-checked against double precision: the error bound over wide argument ranges,
-the values at multiples of pi/2, the tiny argument limit and arguments past
-2^31. The GPU kernels compile the same header; their forward parity
+"""The Snake forward's sin^2 and the backward's (sin^2, sin 2th) pair, and
+the spectral head's (sin, cos) pair (brosoundml_amd/csrc/kdec_snake_math.hpp),
+built for the host with g++ and checked against double precision: the error
+bound over wide argument ranges, the values at multiples of pi/2 (every
+quadrant's signs), the tiny argument limit and arguments past 2^31. The GPU kernels compile the same header; their forward parity
 is in test_gpu_ops.py."""
 import os
 import subprocess
@@ -21,7 +21,7 @@ int main() {
     const double ranges[] = {1.0, 100.0, 30000.0};
     for (double R : ranges) {
         std::uniform_real_distribution<float> U(-R, R);
-        double max_abs = 0.0, max_s2 = 0.0, max_sq = 0.0;
+        double max_abs = 0.0, max_s2 = 0.0, max_sq = 0.0, max_sc = 0.0;
         for (int i = 0; i < 400000; ++i) {
             float th = U(g);
             if (i % 4 == 0)  // next to a multiple of pi/2, where the reduction cancels most
@@ -32,8 +32,12 @@ int main() {
             kdec::snake_sin2_sin2x(th, sq, s2);
             max_sq = std::fmax(max_sq, std::fabs(sq - ex * ex));
             max_s2 = std::fmax(max_s2, std::fabs(s2 - std::sin(2.0 * static_cast<double>(th))));
+            float sv, cv;
+            kdec::kdec_sincos(th, sv, cv);
+            max_sc = std::fmax(max_sc, std::fmax(std::fabs(sv - ex), std::fabs(cv - std::cos(static_cast<double>(th)))));
         }
         std::printf("range %g %.6e\n", R, max_abs);
+        std::printf("sincos %g %.6e\n", R, max_sc);
         std::printf("pair %g %.6e %.6e\n", R, max_sq, max_s2);
     }
     // past 2^31 the quadrant index exceeds int range: results stay finite and in range
@@ -48,6 +52,9 @@ int main() {
         const float th = static_cast<float>(q * (M_PI / 2));
         const double ex = std::sin(static_cast<double>(th));
         std::printf("quad %d %.9e %.9e\n", q, kdec::snake_sin2(th), ex * ex);
+        float sv, cv;
+        kdec::kdec_sincos(th, sv, cv);
+        std::printf("quadsc %d %.9e %.9e %.9e %.9e\n", q, sv, ex, cv, std::cos(static_cast<double>(th)));
     }
     std::printf("tiny %.9e\n", kdec::snake_sin2(1e-10f) / 1e-20);
     return 0;
@@ -100,3 +107,16 @@ def test_tiny_argument(results):
     # sin^2(th) / th^2 -> 1
     tiny = [r for r in results if r[0] == "tiny"][0]
     assert abs(float(tiny[1]) - 1.0) < 1e-6
+
+
+def test_sincos_pair(results):
+    # the spectral head's sin and cos from one reduction: within 2e-7 of
+    # double up to |th| = 30000, with every quadrant's signs
+    rows = [r for r in results if r[0] == "sincos"]
+    assert len(rows) == 3
+    for r in rows:
+        assert float(r[2]) < 2e-7, r
+    quads = [r for r in results if r[0] == "quadsc"]
+    assert len(quads) == 17
+    for r in quads:
+        assert abs(float(r[2]) - float(r[3])) < 2e-7 and abs(float(r[4]) - float(r[5])) < 2e-7, r
