@@ -99,6 +99,11 @@ struct GemmArgs {
     // octet mode (corr_gemm): K chunk = one input-channel octet x up to G taps
     int G, n_tg, n_oct, span8;  // taps per chunk, tap groups, octets, staged positions
     int quad;                // conv_gemm_q: weights packed in quads of k-steps (stride 1, k = KT)
+    // Output placement (polyphase transposed convs): every column lands y_off
+    // positions on (a left pad of the output rows, whose length L_y counts
+    // it), and with refl the column of unpadded index 1 is also stored, with
+    // the residual of column 0, at column 0 (a one-sample left reflect pad).
+    int y_off, refl;
     int single;              // conv_gemm: one LDS stage (where two would leave at most two blocks per CU)
     // AdaIN backward epilogue (conv input grads that feed an AdaIN +
     // activation backward; off when part is null): Y receives
@@ -193,14 +198,14 @@ __device__ inline void decode_tile(const GemmArgs& g, int tile, TileGeo& T) {
         const int r = zz % g.n_phase;
         T.b = zz / g.n_phase;
         const int qmin = -floordiv_i(r - g.ph_p, g.ph_s);          // ceil((p - r)/s)
-        const int qmax = floordiv_i(g.L_y - 1 + g.ph_p - r, g.ph_s);
+        const int qmax = floordiv_i(g.L_y - g.y_off - 1 + g.ph_p - r, g.ph_s);
         T.n_q = qmax - qmin + 1;
         T.k = g.ph_kt;
         T.s = 1;
         T.d = 1;
         T.p = g.ph_kt - 1 - qmin;
         T.os = g.ph_s;
-        T.oo = qmin * g.ph_s + r - g.ph_p;
+        T.oo = qmin * g.ph_s + r - g.ph_p + g.y_off;
         T.A += static_cast<long>(r) * g.a_phase_stride;
     }
     T.m0 = mt * BM;
@@ -285,6 +290,22 @@ __device__ inline void store_tile(const GemmArgs& g, const TileGeo& T, int tile,
                     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), yr, o, 0, 0);
                 }
             }
+            if (g.refl && q * os + oo == 1 + g.y_off) {  // the reflected column 0 (beta = 0)
+#pragma unroll
+                for (int tm = 0; tm < 2; ++tm) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int dm = tm * 32 + 8 * (e >> 2) + (e & 3);
+                        const int o0 = (mrow + dm) * Ly * 4;
+                        float v = acc[tm][tn][e];
+                        if (g.bias)
+                            v += __builtin_bit_cast(float,
+                                                    __builtin_amdgcn_raw_buffer_load_b32(br, (mrow + dm) * 4, 0, 0));
+                        if (Rb) v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, o0, 0, 0));
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v * g.scale), yr, o0, 0, 0);
+                    }
+                }
+            }
         }
         return;
     }
@@ -306,6 +327,10 @@ __device__ inline void store_tile(const GemmArgs& g, const TileGeo& T, int tile,
                 v *= g.scale;
                 if (g.beta != 0.0f) v += g.beta * Yb[yi];
                 Yb[yi] = v;
+                if (g.refl && j == 1 + g.y_off) {  // the reflected column 0 (beta = 0)
+                    const long y0 = static_cast<long>(m) * g.L_y;
+                    Yb[y0] = (acc[tm][tn][e] + (g.bias ? g.bias[m] : 0.0f) + (Rb ? Rb[y0] : 0.0f)) * g.scale;
+                }
             }
         }
     }
@@ -1072,7 +1097,12 @@ __global__ void tile_reduce(GemmArgs g) {
             const int q = qb + j;
             if (q >= T.n_q) break;
             float x = vv[j] + bs;
-            const long yi = static_cast<long>(m) * g.L_y + static_cast<long>(q) * T.os + T.oo;
+            const long col = static_cast<long>(q) * T.os + T.oo;
+            const long yi = static_cast<long>(m) * g.L_y + col;
+            if (g.refl && col == 1 + g.y_off) {  // the reflected column 0 (beta = 0)
+                const long y0 = static_cast<long>(m) * g.L_y;
+                Yb[y0] = (x + (Rb ? Rb[y0] : 0.0f)) * g.scale;
+            }
             if (Rb) x += Rb[yi];
             x *= g.scale;
             if (g.beta != 0.0f) x += g.beta * Yb[yi];
@@ -2603,16 +2633,27 @@ int kdec_conv1d_wgrad(kdec_ctx* ctx, const float* X, long x_bs,
     return KDEC_OK;
 }
 
-int kdec_convt1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
-                     const float* bias, float* Y, long y_bs, int N, int C_in,
-                     int L, int C_out, int k, int stride, int pad, int op) {
+namespace kdec {
+namespace {
+// The transposed-conv forward; with pad_left = 1 the output rows are
+// L_out + 1 long, column 0 the reflection of column 2 (reflection_pad
+// (1, 0) of the result), and R (same layout as Y, or null) is added to
+// every stored column.
+int convt_fwd_impl(kdec_ctx* ctx, const float* X, long x_bs, const float* W, const float* bias, float* Y, long y_bs,
+                   int N, int C_in, int L, int C_out, int k, int stride, int pad, int op, const float* R, long r_bs,
+                   int pad_left, const char* where) {
     if (!ctx) return KDEC_EINVAL;
-    KDEC_CHECK(ctx, X && W && Y && N > 0 && C_in > 0 && C_out > 0 && k > 0 && stride > 0 && pad >= 0 && op >= 0,
-               "kdec_convt1d_fwd: bad arguments");
+    const std::string w(where);
+    KDEC_CHECK(ctx, X && W && Y && N > 0 && C_in > 0 && C_out > 0 && k > 0 && stride > 0 && pad >= 0 && op >= 0 &&
+                        (pad_left == 0 || pad_left == 1),
+               w + ": bad arguments");
     const int L_out = (L - 1) * stride - 2 * pad + (k - 1) + op + 1;
-    KDEC_CHECK(ctx, L > 0 && L_out > 0, "kdec_convt1d_fwd: empty output");
-    KDEC_CHECK(ctx, y_bs >= static_cast<long>(C_out) * L_out && x_bs >= static_cast<long>(C_in) * L,
-               "kdec_convt1d_fwd: batch stride too small");
+    KDEC_CHECK(ctx, L > 0 && L_out > 0, w + ": empty output");
+    KDEC_CHECK(ctx, pad_left == 0 || (stride > 1 && L_out >= 2), w + ": the reflect pad needs a strided output of 2+");
+    const long L_y = L_out + pad_left;
+    KDEC_CHECK(ctx, y_bs >= static_cast<long>(C_out) * L_y && x_bs >= static_cast<long>(C_in) * L &&
+                        (!R || r_bs >= static_cast<long>(C_out) * L_y),
+               w + ": batch stride too small");
     const int kt = static_cast<int>(cdiv(k, stride));
     const int m_pad = static_cast<int>(cdiv(C_out, BM) * BM);
     GemmArgs g{};
@@ -2633,17 +2674,35 @@ int kdec_convt1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
     if (int rc = launch_check(ctx, "pack_convt_fwd")) return rc;
     g.X = X; g.x_bs = x_bs; g.A = A.as<float>(); g.a_phase_stride = ph;
     g.bias = bias; g.Y = Y; g.y_bs = y_bs;
-    g.C_in = C_in; g.L_in = L; g.C_out = C_out; g.L_y = L_out;
+    g.R = R; g.r_bs = r_bs;
+    g.C_in = C_in; g.L_in = L; g.C_out = C_out; g.L_y = static_cast<int>(L_y);
+    g.y_off = pad_left; g.refl = pad_left;
     g.m_pad = m_pad;
     g.k = kt; g.s = 1; g.d = 1; g.p = 0; g.n_q = 0;
     g.scale = 1.0f; g.beta = 0.0f;
     g.n_phase = stride; g.ph_s = stride; g.ph_p = pad; g.ph_kt = kt;
     if (stride == 1) {  // plain correlation: taps reversed, p' = k-1-pad
         g.n_phase = 1; g.k = k; g.p = k - 1 - pad; g.n_q = L_out; g.a_phase_stride = 0;
-        KDEC_CHECK(ctx, g.p >= 0, "kdec_convt1d_fwd: padding larger than the kernel");
+        KDEC_CHECK(ctx, g.p >= 0, w + ": padding larger than the kernel");
     }
     return run_gemm(ctx, g, N, m_pad / BM, "convt_fwd",
                     2.0 * N * C_in * static_cast<double>(L) * C_out * k);
+}
+}  // namespace
+}  // namespace kdec
+
+int kdec_convt1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
+                     const float* bias, float* Y, long y_bs, int N, int C_in,
+                     int L, int C_out, int k, int stride, int pad, int op) {
+    return convt_fwd_impl(ctx, X, x_bs, W, bias, Y, y_bs, N, C_in, L, C_out, k, stride, pad, op, nullptr, 0, 0,
+                          "kdec_convt1d_fwd");
+}
+
+int kdec_convt1d_fwd_res(kdec_ctx* ctx, const float* X, long x_bs, const float* W, const float* bias, float* Y,
+                         long y_bs, int N, int C_in, int L, int C_out, int k, int stride, int pad, int op,
+                         const float* R, long r_bs, int pad_left) {
+    return convt_fwd_impl(ctx, X, x_bs, W, bias, Y, y_bs, N, C_in, L, C_out, k, stride, pad, op, R, r_bs, pad_left,
+                          "kdec_convt1d_fwd_res");
 }
 
 int kdec_convt1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,

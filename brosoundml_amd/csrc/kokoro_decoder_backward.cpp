@@ -1014,20 +1014,23 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
         const int C_out = gen.ups_C_out[i];
         Tensor a = leaky(x, 0.1f);
 
-        // ups (+ left reflect pad on the last stage); it does not read har, so
-        // it goes first and overlaps a producer still writing har
+        // ups (+ left reflect pad on the last stage) + the noise source. Before
+        // the last stage it does not read har, so it goes first and overlaps
+        // a producer still writing har, and the source is added after; the
+        // last stage's transposed conv writes the padded rows with the source
+        // added in its epilogue (kdec_convt1d_fwd_res), so it runs once the
+        // noise branch is done.
         const int kL = gen.ups_k[i], s = gen.ups_stride[i], p = gen.ups_pad[i];
+        const bool last = i == U - 1;
         int L_x = (L - 1) * s - 2 * p + (kL - 1) + 1;
-        Tensor u = dev(N, C_out * L_x);
-        ck(kdec_convt1d_fwd(kctx(), cp(a), rs(a), cp(gen.ups_W[i]), gen.ups_b[i].data ? cp(gen.ups_b[i]) : nullptr,
-                            mp(u), rs(u), N, sc.C_in, L, C_out, kL, s, p, 0),
-           "conv_transpose1d forward");
-        a = Tensor();
-        if (i == U - 1) {
-            Tensor padded = dev(N, C_out * (L_x + 1));
-            ck(kdec_pad_reflect_left1_fwd(kctx(), cp(u), rs(u), mp(padded), rs(padded), N, C_out, L_x), "pad1d");
-            u = padded;
-            L_x += 1;
+        const float* ub = gen.ups_b[i].data ? cp(gen.ups_b[i]) : nullptr;
+        Tensor u;
+        if (!last) {
+            u = dev(N, C_out * L_x);
+            ck(kdec_convt1d_fwd(kctx(), cp(a), rs(a), cp(gen.ups_W[i]), ub, mp(u), rs(u), N, sc.C_in, L, C_out, kL, s,
+                                p, 0),
+               "conv_transpose1d forward");
+            a = Tensor();
         }
 
         // noise branch
@@ -1051,12 +1054,21 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
                                           naff[i].g2, naff[i].b2, src, sc.noise);
             if (!cache.keep) sc.noise = AdainResBlock1Cache{};
         }
+        if (last) L_x += 1;  // reflection_pad (1, 0)
         if (L_src != L_x)
             fail(where, "noise source length " + std::to_string(L_src) + " != upsampled length " +
                             std::to_string(L_x) + " at stage " + std::to_string(i));
         sc.C_out = C_out;
         sc.L_out = L_x;
-        add_into(u, src);
+        if (last) {
+            u = dev(N, C_out * L_x);
+            ck(kdec_convt1d_fwd_res(kctx(), cp(a), rs(a), cp(gen.ups_W[i]), ub, mp(u), rs(u), N, sc.C_in, L, C_out,
+                                    kL, s, p, 0, cp(src), rs(src), 1),
+               "conv_transpose1d forward + reflection_pad + noise source");
+            a = Tensor();
+        } else {
+            add_into(u, src);
+        }
         src = Tensor();
 
         // x = mean_j resblocks[i*K + j](u): each block's last conv accumulates

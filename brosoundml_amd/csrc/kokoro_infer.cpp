@@ -282,24 +282,19 @@ void Generator::forward(const Tensor& gen_in, int L_in, const Tensor& har, int f
                       mf(out), ld(out), 1.0f, 0.0f);
             src = out;
         }
-        // ups: ConvTranspose1d (+ left reflect pad by 1 on the last stage)
+        // ups: ConvTranspose1d (+ left reflect pad by 1 on the last stage) with
+        // the noise source added, in one pass (kdec_convt1d_fwd_res)
         const int kL = ups_k[i], s = ups_stride[i], p = ups_pad[i];
-        int L_x = (L - 1) * s - 2 * p + (kL - 1) + 1;
-        Tensor u = make(N, C_out * L_x);
-        ok(kdec_convt1d_fwd(rt(), cf(a), ld(a), cf(ups_W[i]), ups_b[i].data ? cf(ups_b[i]) : nullptr, mf(u), ld(u), N,
-                            ups_C_in[i], L, C_out, kL, s, p, 0),
-           "conv_transpose1d_forward");
-        a = Tensor();
-        if (i == num_upsamples - 1) {
-            Tensor padded = make(N, C_out * (L_x + 1));
-            ok(kdec_pad_reflect_left1_fwd(rt(), cf(u), ld(u), mf(padded), ld(padded), N, C_out, L_x), "pad1d_forward");
-            u = padded;
-            L_x += 1;
-        }
+        const int pad_left = i == num_upsamples - 1 ? 1 : 0;
+        const int L_x = (L - 1) * s - 2 * p + (kL - 1) + 1 + pad_left;
         if (L_src != L_x)
             fail(where, "noise source length " + std::to_string(L_src) + " != upsampled length " +
                             std::to_string(L_x) + " at stage " + std::to_string(i));
-        ok(kdec_axpby(rt(), 1.0f, cf(u), ld(u), 1.0f, cf(src), ld(src), mf(u), ld(u), N, u.cols), "add_inplace");
+        Tensor u = make(N, C_out * L_x);
+        ok(kdec_convt1d_fwd_res(rt(), cf(a), ld(a), cf(ups_W[i]), ups_b[i].data ? cf(ups_b[i]) : nullptr, mf(u),
+                                ld(u), N, ups_C_in[i], L, C_out, kL, s, p, 0, cf(src), ld(src), pad_left),
+           "conv_transpose1d_forward");
+        a = Tensor();
         src = Tensor();
         // x = mean of the stage's K resblocks: each block's last conv adds its share
         Tensor xs = make(N, C_out * L_x);

@@ -149,6 +149,16 @@ int kdec_conv1d_wgrad(kdec_ctx* ctx, const float* X, long x_bs,
 int kdec_convt1d_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
                      const float* bias, float* Y, long y_bs, int N, int C_in,
                      int L, int C_out, int k, int stride, int pad, int op);
+/* The generator's last upsample stage in one pass (kokoro_decoder_backward.cpp
+ * :627-642): Y = reflection_pad_left1(convT(X, W) + bias) + R, i.e. with
+ * pad_left = 1 each output row is L_out + 1 long, column j + 1 holds the
+ * transposed conv's column j and column 0 its column 1, and R (the noise
+ * source, Y's layout and length, or NULL) is added to every column; with
+ * pad_left = 0, Y = convT(X, W) + bias + R. Same polyphase GEMM as
+ * kdec_convt1d_fwd, with the pad and the add in its epilogue. */
+int kdec_convt1d_fwd_res(kdec_ctx* ctx, const float* X, long x_bs, const float* W, const float* bias, float* Y,
+                         long y_bs, int N, int C_in, int L, int C_out, int k, int stride, int pad, int op,
+                         const float* R, long r_bs, int pad_left);
 /* dX = conv_transpose1d_backward_input(W, dY) (= strided conv1d of dY with W).
  * Replaces bt::conv_transpose1d_backward_input at :725-728. */
 int kdec_convt1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,

@@ -393,3 +393,37 @@ def test_inference_forwards_vs_oracle(ctx, kokoro_params, cfg_name, N, T):
         ref = om.forward(asr[n], F0[n], Nn[n], style[n], T, har=h_gpu[n])
         close(a_inf[n].cpu().numpy(), ref, FWD_TOL, f"{cfg_name} kdec_model_infer utt {n} vs oracle")
         close(a_dbh[n].cpu().numpy(), ref, FWD_TOL, f"{cfg_name} decode_back_half utt {n} vs oracle")
+
+
+@pytest.mark.parametrize("name,N,Cin,Cout,L,k,s,p,pad_left", [
+    ("ups1", 4, 256, 128, 5120, 12, 6, 3, 1),
+    ("ups1_b8", 8, 256, 128, 10240, 12, 6, 3, 1),
+    ("ups0", 4, 512, 256, 512, 20, 10, 5, 0),
+    ("ups1_small", 2, 256, 128, 40, 12, 6, 3, 1),
+])
+def test_convt_fwd_pad_source_fused(ctx, name, N, Cin, Cout, L, k, s, p, pad_left):
+    # kdec_convt1d_fwd_res: the transposed conv, the one-sample left reflect
+    # pad and the noise-source add in one epilogue, equal bit for bit to the
+    # transposed conv followed by the pad and a float32 add (the epilogue adds
+    # bias then the source, as the separate passes round), at the decoder's
+    # B = 8 stage-1 shape and smaller grids (whole and split tiles)
+    Lo = O.convt1d_out_len(L, k, s, p, 0, 1)
+    Ly = Lo + pad_left
+    bound = 1.0 / np.sqrt(Cout * k)
+    x = synth.normal(f"cvtr.{name}.x", (N, Cin, L))
+    W = synth.uniform(f"cvtr.{name}.W", (Cin, Cout * k), -bound, bound)
+    b = synth.uniform(f"cvtr.{name}.b", (Cout,), -bound, bound)
+    R = synth.normal(f"cvtr.{name}.r", (N, Cout, Ly))
+    tx, tW, tb, tR = (dev(a) for a in (x, W, b, R))
+    Y = torch.empty(N, Cout, Lo, device="cuda")
+    ctx.call("kdec_convt1d_fwd", P(tx), Cin * L, P(tW), P(tb), P(Y), Cout * Lo, N, Cin, L, Cout, k, s, p, 0)
+    Yf = torch.full((N, Cout, Ly), float("nan"), device="cuda")
+    ctx.call("kdec_convt1d_fwd_res", P(tx), Cin * L, P(tW), P(tb), P(Yf), Cout * Ly, N, Cin, L, Cout, k, s, p, 0,
+             P(tR), Cout * Ly, pad_left)
+    torch.cuda.synchronize()
+    y = Y.cpu().numpy()
+    if pad_left:
+        y = np.concatenate([y[:, :, 1:2], y], axis=2)
+    want = (y + R).astype(np.float32)
+    got = Yf.cpu().numpy()
+    assert np.array_equal(got, want), f"{name}: max |diff| {np.nanmax(np.abs(got - want)):.3e}"
