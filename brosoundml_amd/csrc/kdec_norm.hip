@@ -837,6 +837,41 @@ __global__ void pad_bwd_k(const float* dY, long dy_bs, float* dX, long dx_bs, in
     }
 }
 
+// add3_k over rows of L + 1 that also writes the left reflect pad's adjoint:
+// Y = (A + B) + C, and Z[c][j] = Y[c][j + 1] (+ Y[c][0] at j = 1), rows of L.
+// Block (row, x): positions [x * 1024, x * 1024 + 1024) of row `row` (of N*C),
+// four per thread. Y may alias A, so Y[c][0] reaches the lane that forms
+// Z[c][1] (lane 2 of block x = 0's first wave) by a shuffle from lane 0,
+// never by a read of A after lane 0 has stored over it.
+__global__ __launch_bounds__(256) void add3_unpad_k(const float* A, long a_bs, const float* B, long b_bs,
+                                                    const float* Cc, long c_bs, float* Y, long y_bs, float* Z,
+                                                    long z_bs, int C, int L) {
+    const int row = blockIdx.x;
+    const int n = row / C, c = row - n * C;
+    const long ro = static_cast<long>(c) * (L + 1);
+    const float* a = A + n * a_bs + ro;
+    const float* b = B + n * b_bs + ro;
+    const float* cc = Cc + n * c_bs + ro;
+    float* y = Y + n * y_bs + ro;
+    float* z = Z + n * z_bs + static_cast<long>(c) * L;
+    const int j0 = blockIdx.y * 1024 + threadIdx.x;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int j = j0 + q * 256;
+        const bool in = j <= L;
+        const float v = in ? (a[j] + b[j]) + cc[j] : 0.0f;
+        float vz = v;
+        if (q == 0 && blockIdx.y == 0) {
+            const float y0 = __shfl(v, 0);
+            if (j == 2) vz = v + y0;
+        }
+        if (in) {
+            y[j] = v;
+            if (j >= 1) z[j - 1] = vz;
+        }
+    }
+}
+
 __global__ void near2_fwd_k(const float* X, long x_bs, float* Y, long y_bs, int C, int L) {
     const int n = blockIdx.y;
     const long tot = static_cast<long>(C) * 2 * L;
@@ -1348,6 +1383,22 @@ int kdec_add3(kdec_ctx* ctx, const float* A, long a_bs, const float* B, long b_b
         hipLaunchKernelGGL(add3_k<1>, dim3(chunks(len), N), dim3(256), 0, ctx->stream, A, a_bs, B, b_bs, C, c_bs, Y,
                            y_bs, len);
     return launch_check(ctx, "add3");
+}
+
+int kdec_add3_unpad_left1(kdec_ctx* ctx, const float* A, long a_bs, const float* B, long b_bs, const float* C,
+                          long c_bs, float* Y, long y_bs, float* Z, long z_bs, int N, int Cn, int L) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, A && B && C && Y && Z && N > 0 && Cn > 0 && L > 1, "kdec_add3_unpad_left1: bad arguments");
+    KDEC_CHECK(ctx, y_bs >= static_cast<long>(Cn) * (L + 1) && z_bs >= static_cast<long>(Cn) * L &&
+                        a_bs >= static_cast<long>(Cn) * (L + 1) && b_bs >= static_cast<long>(Cn) * (L + 1) &&
+                        c_bs >= static_cast<long>(Cn) * (L + 1),
+               "kdec_add3_unpad_left1: batch stride too small");
+    KDEC_CHECK(ctx, static_cast<long>(N) * Cn < (1L << 31) && cdiv(L + 1, 1024) <= 65535,
+               "kdec_add3_unpad_left1: too many rows or too long a row");
+    ProfScope ps(ctx, "elementwise", 0, 4.0 * static_cast<double>(N) * Cn * (4.0 * (L + 1) + L));
+    hipLaunchKernelGGL(add3_unpad_k, dim3(static_cast<unsigned>(N * Cn), static_cast<unsigned>(cdiv(L + 1, 1024))),
+                       dim3(256), 0, ctx->stream, A, a_bs, B, b_bs, C, c_bs, Y, y_bs, Z, z_bs, Cn, L);
+    return launch_check(ctx, "add3_unpad");
 }
 
 int kdec_pad_reflect_left1_fwd(kdec_ctx* ctx, const float* X, long x_bs,

@@ -1159,7 +1159,15 @@ void generator_backward(const Generator& gen, const GeneratorCache& cache, const
         if (par)
             for (int j = 1; j < K; ++j) BranchLanes::wait_on(main_ctx, g_branch.event(static_cast<std::size_t>(j) + 1));
         Tensor d_m = dxin[0];
-        if (K == 3) {
+        // the last stage's input was left reflect padded by one sample: its
+        // adjoint (du_pre) comes out of the pass that sums the resblock grads
+        Tensor du_pre;
+        if (K == 3 && i == U - 1) {
+            du_pre = dev(N, C_out * (L - 1));
+            ck(kdec_add3_unpad_left1(kctx(), cp(d_m), rs(d_m), cp(dxin[1]), rs(dxin[1]), cp(dxin[2]), rs(dxin[2]),
+                                     mp(d_m), rs(d_m), mp(du_pre), rs(du_pre), N, C_out, L - 1),
+               "resblock grad sum and pad1d backward");
+        } else if (K == 3) {
             ck(kdec_add3(kctx(), cp(d_m), rs(d_m), cp(dxin[1]), rs(dxin[1]), cp(dxin[2]), rs(dxin[2]), mp(d_m), rs(d_m),
                          N, d_m.cols),
                "resblock grad sum");
@@ -1187,9 +1195,11 @@ void generator_backward(const Generator& gen, const GeneratorCache& cache, const
         }
         Tensor du = d_m;
         if (i == U - 1) {
-            Tensor du_pre = dev(N, C_out * (L - 1));
-            ck(kdec_pad_reflect_left1_bwd(kctx(), cp(d_m), rs(d_m), mp(du_pre), rs(du_pre), N, C_out, L - 1),
-               "pad1d backward");
+            if (!du_pre.data) {
+                du_pre = dev(N, C_out * (L - 1));
+                ck(kdec_pad_reflect_left1_bwd(kctx(), cp(d_m), rs(d_m), mp(du_pre), rs(du_pre), N, C_out, L - 1),
+                   "pad1d backward");
+            }
             du = du_pre;
         }
         d_m = Tensor();

@@ -279,6 +279,14 @@ int kdec_axpby(kdec_ctx* ctx, float a, const float* A, long a_bs, float b,
 int kdec_add3(kdec_ctx* ctx, const float* A, long a_bs, const float* B,
               long b_bs, const float* C, long c_bs, float* Y, long y_bs,
               int N, long len);
+/* kdec_add3 over N x C rows of L + 1 that also writes the left reflect
+ * pad's adjoint in the same pass (the generator's last stage backward,
+ * :716-728): Y = (A + B) + C (as kdec_add3), and Z (rows of L) = the
+ * gradient of the unpadded rows, Z[j] = Y[j + 1] + (j == 1 ? Y[0] : 0), the
+ * bits kdec_pad_reflect_left1_bwd(Y) gives. Y may alias A; Z aliases
+ * none of the others. */
+int kdec_add3_unpad_left1(kdec_ctx* ctx, const float* A, long a_bs, const float* B, long b_bs, const float* C,
+                          long c_bs, float* Y, long y_bs, float* Z, long z_bs, int N, int Cn, int L);
 /* Left reflect pad by one sample, C rows of L -> L+1 (bt::pad1d_* mode 1 at
  * :633-634 / :720-721). */
 int kdec_pad_reflect_left1_fwd(kdec_ctx* ctx, const float* X, long x_bs,

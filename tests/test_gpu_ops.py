@@ -537,6 +537,28 @@ def test_add3_in_order(K, cols, bs, off):
     assert np.array_equal(out[:, :off], a[:, :off]) and np.array_equal(out[:, off + cols:], a[:, off + cols:])
 
 
+@pytest.mark.parametrize("N,C,L", [(2, 3, 17), (1, 2, 2), (2, 5, 1023), (3, 4, 1024), (2, 128, 10240)])
+def test_add3_unpad_left1(K, N, C, L):
+    # the fused resblock-grad sum and reflect-pad adjoint against the two
+    # passes it replaces, bit for bit, with Y aliasing A as the generator's
+    # last stage calls it; row lengths either side of the 1024-sample blocks
+    a, b, c = (rnd(N, C * (L + 1)) for _ in range(3))
+    y_ref = ((a + b) + c).astype(np.float32).reshape(N, C, L + 1)
+    z_ref = y_ref[..., 1:].copy()
+    z_ref[..., 1] = z_ref[..., 1] + y_ref[..., 0]
+    ta, tb, tc = g(a), g(b), g(c)
+    Z = torch.empty(N, C * L, device="cuda")
+    K.call("kdec_add3_unpad_left1", P(ta), C * (L + 1), P(tb), C * (L + 1), P(tc), C * (L + 1), P(ta), C * (L + 1),
+           P(Z), C * L, N, C, L)
+    assert np.array_equal(h(ta).reshape(N, C, L + 1), y_ref)
+    assert np.array_equal(h(Z).reshape(N, C, L), z_ref)
+    a2 = g(a)
+    Z2 = torch.empty(N, C * L, device="cuda")
+    K.call("kdec_add3", P(a2), C * (L + 1), P(tb), C * (L + 1), P(tc), C * (L + 1), P(a2), C * (L + 1), N, C * (L + 1))
+    K.call("kdec_pad_reflect_left1_bwd", P(a2), C * (L + 1), P(Z2), C * L, N, C, L)
+    assert torch.equal(Z, Z2) and torch.equal(ta, a2)
+
+
 @pytest.mark.parametrize("n_fft,hop,L,C", [(20, 5, 301, 24), (8, 2, 65, 6)])
 def test_spectral_head(K, n_fft, hop, L, C):
     N = 2
