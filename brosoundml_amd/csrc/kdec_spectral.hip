@@ -608,147 +608,223 @@ __global__ void style_bwd_w_k(const float* style, long s_bs, const float* dout, 
 }
 
 // The same projections reading each fc row once for all N utterances (the
-// wave-per-(row, utterance) kernels above read the fc block N times): a block
-// owns STR consecutive rows. Forward: the rows' [STR][S] slab and the styles
-// [N][S] are staged in LDS (slab stride S + 1: a lane per row, conflict
-// free), each thread then forms its row's dot products for every fourth
-// utterance in double, in column order. d(style): threads own (row phase,
-// column) and accumulate over the block's rows, in order, for up to STN
-// utterances at a time in double; the phases are combined in order and the
-// blocks' partials are summed, in block order, by style_bwd_x_sum_k.
-constexpr int STR = 64;   // forward rows per block
-constexpr int STB = 64;   // d(style) rows per block
-constexpr int STN = 8;    // utterances per d(style) pass
+// wave-per-(row, utterance) kernels above read the fc block N times).
+//
+// Forward: a block owns STR = 64 consecutive rows, staged in LDS as
+// [STR][S + 4] with 16-byte loads, all in flight before the first store (the
+// padded stride spreads a wave's 16-byte row reads over the 32 banks eight
+// lanes at a time). Lane r of wave c forms row r's dot products over column
+// group c (S / STG consecutive columns) for STQ utterances at a time: float
+// sums of S / STG terms in column order, the row operands read 16 bytes at a
+// time from LDS and the style operands, uniform across the wave, by scalar
+// loads. The STG groups' sums are added in group order in double, with the
+// bias.
+// d(style): thread (ph, j) = (t / S, t % S) sums, in
+// float and in row order, rows ph, ph + PH, ... of the block's STB rows
+// (PH = 256 / S phases) for STN utterances at a time, its column's weights
+// loaded all at once and the d(out) operands read from LDS; the phases' sums
+// are added in phase order in double, and the blocks' partials summed, in
+// block order, by style_bwd_x_sum_k.
+constexpr int STR = 64;           // forward rows per block (a wave's lanes)
+constexpr int STG = 4;            // forward column groups (one per wave)
+constexpr int STQ = 8;            // forward utterances per pass
+constexpr int STB = 64;           // d(style) rows per block
+constexpr int STN = 8;            // d(style) utterances per pass
 
-__global__ __launch_bounds__(256) void style_fwd_rows_k(const float* W, const float* bias, const float* style,
-                                                        long s_bs, float* out, long o_bs, int N, int rows, int S) {
+// LDS floats of the forward kernel: slab, styles, group sums
+inline size_t style_fwd_lds_floats(int S) {
+    return static_cast<size_t>(STR) * (S + 4) + static_cast<size_t>(STG) * STQ * STR;
+}
+
+// Raw buffer descriptor over [base, base + bytes) from wave-uniform values
+// (out-of-range loads return 0).
+__device__ inline __amdgpu_buffer_rsrc_t style_rsrc(const float* base, int bytes) {
+    const unsigned long long a = reinterpret_cast<unsigned long long>(base);
+    const unsigned lo = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(a));
+    const unsigned hi = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(a >> 32));
+    float* p = reinterpret_cast<float*>((static_cast<unsigned long long>(hi) << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(p, static_cast<short>(0), __builtin_amdgcn_readfirstlane(bytes),
+                                             0x00020000);
+}
+
+__device__ inline float style_ld(__amdgpu_buffer_rsrc_t r, int byte_off, int soff = 0) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, soff, 0));
+}
+
+// Every global load below is issued unconditionally (a buffer load past the
+// end of its array returns 0) and the bounds decide only how the value is
+// used: a load under a branch is followed by a wait for it at the branch's
+// join, which turns a run of guarded loads into one memory round trip each.
+
+// Forward; KQ = STR * S / 1024 slab float4s per thread (S <= 128).
+template <int KQ>
+__global__ __launch_bounds__(256) void style_fwd_rows_k(const float* __restrict__ W, const float* __restrict__ bias,
+                                                        const float* __restrict__ style, long s_bs,
+                                                        float* __restrict__ out, long o_bs, int N, int rows, int S) {
     extern __shared__ float sm[];
-    float* wt = sm;                   // [STR][S + 1]
-    float* st = sm + STR * (S + 1);   // [N][S]
+    const int SP = S + 4;
+    float* wt = sm;                           // [STR][S + 4]
+    float* red = wt + STR * SP;               // [STG][STQ][STR]
+    const int t = threadIdx.x;
     const int r0 = blockIdx.x * STR;
     const int nr = min(STR, rows - r0);
-    // the slab's loads issued eight at a time before their LDS stores; thread
-    // t stages column t % S of rows t / S, t / S + 256 / S, ... (256 % S == 0)
-    const float* Wb = W + static_cast<long>(r0) * S;
-    const int j = threadIdx.x % S, rstep = 256 / S;
-    for (int r = threadIdx.x / S; r < nr; r += 32 * rstep) {
-        float v[32];
+    const int S4 = S >> 2;
+    {  // the slab, STR * S4 == 256 * KQ float4s, all in flight
+        const __amdgpu_buffer_rsrc_t wr = style_rsrc(W, rows * S * 4);
+        const int wb = r0 * S * 4;
+        float4 v[KQ];
 #pragma unroll
-        for (int q = 0; q < 32; ++q) {
-            const int rr = r + q * rstep;
-            v[q] = rr < nr ? Wb[static_cast<long>(rr) * S + j] : 0.0f;
-        }
+        for (int k = 0; k < KQ; ++k)
+            v[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(wr, wb + (t + 256 * k) * 16, 0, 0));
 #pragma unroll
-        for (int q = 0; q < 32; ++q) {
-            const int rr = r + q * rstep;
-            if (rr < nr) wt[rr * (S + 1) + j] = v[q];
+        for (int k = 0; k < KQ; ++k) {
+            const int i = t + 256 * k;
+            const int row = i / S4, c4 = i - row * S4;
+            *reinterpret_cast<float4*>(wt + row * SP + c4 * 4) = v[k];
         }
     }
-    for (int n = threadIdx.x / S; n < N; n += rstep) st[n * S + j] = style[n * s_bs + j];
     __syncthreads();
-    const int r = threadIdx.x & (STR - 1);
-    if (r >= nr) return;
-    const float* w = wt + r * (S + 1);
-    const float b = bias ? bias[r0 + r] : 0.0f;
-    for (int n = threadIdx.x / STR; n < N; n += 256 / STR) {  // wave-uniform n: st reads broadcast
-        const float* sn = st + n * S;
-        double a0 = 0.0, a1 = 0.0;  // even / odd columns: two independent chains
-#pragma unroll 8
-        for (int jj = 0; jj + 1 < S; jj += 2) {
-            a0 += static_cast<double>(w[jj]) * sn[jj];
-            a1 += static_cast<double>(w[jj + 1]) * sn[jj + 1];
+    const int c = __builtin_amdgcn_readfirstlane(t >> 6), r = t & 63;
+    constexpr int cw = 4 * KQ;  // columns per wave: S / STG
+    const float* w = wt + r * SP + c * cw;
+    const float* sg = style + c * cw;  // wave-uniform: the style operands are scalar loads
+    for (int n0 = 0; n0 < N; n0 += STQ) {
+        const int nn = min(STQ, N - n0);
+        float acc[STQ];
+#pragma unroll
+        for (int q = 0; q < STQ; ++q) acc[q] = 0.0f;
+#pragma unroll
+        for (int jj = 0; jj < cw; jj += 4) {
+            // every utterance slot's operands loaded before the first use (a
+            // slot past N repeats the last utterance; its sums are not stored)
+            float4 y[STQ];
+#pragma unroll
+            for (int q = 0; q < STQ; ++q)
+                y[q] = *reinterpret_cast<const float4*>(sg + min(n0 + q, N - 1) * s_bs + jj);
+            const float4 x = *reinterpret_cast<const float4*>(w + jj);
+#pragma unroll
+            for (int q = 0; q < STQ; ++q) {
+                float a = acc[q];
+                a = __builtin_fmaf(x.x, y[q].x, a);
+                a = __builtin_fmaf(x.y, y[q].y, a);
+                a = __builtin_fmaf(x.z, y[q].z, a);
+                acc[q] = __builtin_fmaf(x.w, y[q].w, a);
+            }
         }
-        if (S & 1) a0 += static_cast<double>(w[S - 1]) * sn[S - 1];
-        out[n * o_bs + r0 + r] = static_cast<float>((a0 + a1) + b);
+#pragma unroll
+        for (int q = 0; q < STQ; ++q)
+            if (q < nn) red[(c * STQ + q) * STR + r] = acc[q];
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < STQ * STR / 256; ++k) {
+            const int i = t + 256 * k, q = i / STR, rr = i - q * STR;
+            if (q < nn && rr < nr) {
+                double sum = 0.0;
+#pragma unroll
+                for (int cc = 0; cc < STG; ++cc) sum += static_cast<double>(red[(cc * STQ + q) * STR + rr]);
+                out[(n0 + q) * o_bs + r0 + rr] = static_cast<float>(sum + (bias ? bias[r0 + rr] : 0.0f));
+            }
+        }
+        __syncthreads();
     }
 }
 
-// part[blk][n][j] = sum over the block's rows r of W[r, j] dout[n, r]
+// part[blk][n][j] = sum over the block's rows r of W[r, j] dout[n, r];
+// PER = STB * S / 256 rows per thread (S divides 256, S >= 64)
+template <int PER>
 __global__ __launch_bounds__(256) void style_bwd_x_rows_k(const float* W, const float* dout, long d_bs, float* part,
                                                           int N, int rows, int S) {
     extern __shared__ float sm[];
-    const int PH = 256 / S;           // row phases
-    float* dsl = sm;                  // [N][STB]
-    float* red = sm + N * STB;        // [PH][STN][S]
+    const int PH = 256 / S;           // row phases (PH * S == 256)
+    float* dsl = sm;                  // [STB][STN] of the pass's utterances
+    float* red = sm + STB * STN;      // [PH][STN][S]
     const int r0 = blockIdx.x * STB;
     const int nr = min(STB, rows - r0);
-    for (int i = threadIdx.x; i < N * STB; i += 256) {
-        const int n = i / STB, rr = i - n * STB;
-        dsl[i] = rr < nr ? dout[n * d_bs + r0 + rr] : 0.0f;
-    }
-    __syncthreads();
-    const int j = threadIdx.x % S, ph = threadIdx.x / S;
+    const int j = threadIdx.x % S, ph = __builtin_amdgcn_readfirstlane(threadIdx.x / S);  // S >= 64
+    const __amdgpu_buffer_rsrc_t wr = style_rsrc(W, rows * S * 4);
+    const __amdgpu_buffer_rsrc_t dr = style_rsrc(dout, static_cast<int>(((N - 1) * d_bs + rows) * 4));
+    // row ph + i * PH of the block is 1 KB * i past the thread's first one
+    const int vo = ((r0 + ph) * S + j) * 4;
+    float w[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) w[i] = style_ld(wr, vo, i * 1024);
     for (int n0 = 0; n0 < N; n0 += STN) {
         const int nn = min(STN, N - n0);
-        double acc[STN];
+        {  // STB * STN == 2 * 256 d(out) values
+            float dv[2];
 #pragma unroll
-        for (int q = 0; q < STN; ++q) acc[q] = 0.0;
-        // the thread's column of the block's rows, loaded 32 at a time before use
-        for (int rb = ph; rb < nr; rb += 32 * PH) {
-            float w[32];
-#pragma unroll
-            for (int i = 0; i < 32; ++i) {
-                const int rr = rb + i * PH;
-                w[i] = rr < nr ? W[static_cast<long>(r0 + rr) * S + j] : 0.0f;
+            for (int k = 0; k < 2; ++k) {
+                const int i = threadIdx.x + 256 * k, rr = i / STN, q = i - rr * STN;
+                dv[k] = style_ld(dr, static_cast<int>(((n0 + q) * d_bs + r0 + rr) * 4));
             }
 #pragma unroll
-            for (int i = 0; i < 32; ++i) {
-                const int rr = rb + i * PH;
-                if (rr < nr) {
-#pragma unroll
-                    for (int q = 0; q < STN; ++q)
-                        if (q < nn) acc[q] += static_cast<double>(w[i]) * dsl[(n0 + q) * STB + rr];
-                }
+            for (int k = 0; k < 2; ++k) {
+                const int i = threadIdx.x + 256 * k, rr = i / STN, q = i - rr * STN;
+                dsl[i] = (rr < nr && q < nn) ? dv[k] : 0.0f;
             }
         }
+        __syncthreads();
+        float acc[STN];
 #pragma unroll
-        for (int q = 0; q < STN; ++q)
-            if (q < nn) red[(ph * STN + q) * S + j] = static_cast<float>(acc[q]);
+        for (int q = 0; q < STN; ++q) acc[q] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int rr = ph + i * PH;
+            const float x = rr < nr ? w[i] : 0.0f;  // another block's row, or past the end
+            const float4 d0 = *reinterpret_cast<const float4*>(dsl + rr * STN);
+            const float4 d1 = *reinterpret_cast<const float4*>(dsl + rr * STN + 4);
+            acc[0] = __builtin_fmaf(x, d0.x, acc[0]);
+            acc[1] = __builtin_fmaf(x, d0.y, acc[1]);
+            acc[2] = __builtin_fmaf(x, d0.z, acc[2]);
+            acc[3] = __builtin_fmaf(x, d0.w, acc[3]);
+            acc[4] = __builtin_fmaf(x, d1.x, acc[4]);
+            acc[5] = __builtin_fmaf(x, d1.y, acc[5]);
+            acc[6] = __builtin_fmaf(x, d1.z, acc[6]);
+            acc[7] = __builtin_fmaf(x, d1.w, acc[7]);
+        }
+#pragma unroll
+        for (int q = 0; q < STN; ++q) red[(ph * STN + q) * S + j] = acc[q];
         __syncthreads();
         for (int i = threadIdx.x; i < nn * S; i += 256) {
             const int q = i / S, jj = i - q * S;
-            double t = 0.0;
-            for (int h = 0; h < PH; ++h) t += red[(h * STN + q) * S + jj];
-            part[(static_cast<long>(blockIdx.x) * N + n0 + q) * S + jj] = static_cast<float>(t);
+            double tsum = 0.0;
+            for (int h = 0; h < PH; ++h) tsum += static_cast<double>(red[(h * STN + q) * S + jj]);
+            part[(static_cast<long>(blockIdx.x) * N + n0 + q) * S + jj] = static_cast<float>(tsum);
         }
         __syncthreads();
     }
 }
 
 // dstyle[n, j] = beta * dstyle[n, j] + the sum over blocks q of
-// part[q][n][j] in a fixed order: 64 outputs per block, its 16 waves each
-// summing a contiguous sixteenth of the block range (eight partials in
-// flight per lane), the waves' sums then added in a fixed tree
+// part[q][n][j] in a fixed order: 16 outputs per block; lane group p (64 of
+// them) sums the p-th sixty-fourth of the block range in order, up to 16
+// partials in flight per lane, and the groups' sums are added in a fixed tree
 __global__ __launch_bounds__(1024) void style_bwd_x_sum_k(const float* part, int nblk, float* dstyle, long ds_bs,
                                                           float beta, int N, int S) {
-    __shared__ double red[16][64];
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int nj = blockIdx.x * 64 + lane;
+    __shared__ double red[64][16];
+    const int o = threadIdx.x & 15, p = threadIdx.x >> 4;
+    const int nj = blockIdx.x * 16 + o;
     const int NS = N * S;
+    const int q0 = p * nblk / 64, q1 = (p + 1) * nblk / 64;
+    const __amdgpu_buffer_rsrc_t pr = style_rsrc(part, nblk * NS * 4);
     double acc = 0.0;
-    if (nj < NS) {
-        const int q0 = wv * nblk / 16, q1 = (wv + 1) * nblk / 16;
-        double a8[8];
+    for (int qb = q0; qb < q1; qb += 16) {
+        float v[16];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) a8[i] = 0.0;
-        int q = q0;
-        for (; q + 8 <= q1; q += 8) {
+        for (int i = 0; i < 16; ++i) v[i] = style_ld(pr, ((qb + i) * NS + nj) * 4);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) a8[i] += part[static_cast<long>(q + i) * NS + nj];
-        }
-        for (int i = 0; q < q1; ++q, ++i) a8[i] += part[static_cast<long>(q) * NS + nj];
-        acc = ((a8[0] + a8[1]) + (a8[2] + a8[3])) + ((a8[4] + a8[5]) + (a8[6] + a8[7]));
+        for (int i = 0; i < 16; ++i) acc += qb + i < q1 ? static_cast<double>(v[i]) : 0.0;
     }
-    red[wv][lane] = acc;
+    red[p][o] = acc;
     __syncthreads();
-    for (int h = 8; h >= 1; h >>= 1) {
-        if (wv < h) red[wv][lane] += red[wv + h][lane];
+    for (int h = 32; h >= 1; h >>= 1) {
+        if (p < h) red[p][o] += red[p + h][o];
         __syncthreads();
     }
-    if (wv == 0 && nj < NS) {
+    if (p == 0 && nj < NS) {
         const int n = nj / S, j = nj - n * S;
         float* d = dstyle + n * ds_bs + j;
-        *d = static_cast<float>(red[0][lane]) + (beta != 0.0f ? beta * *d : 0.0f);
+        *d = static_cast<float>(red[0][o]) + (beta != 0.0f ? beta * *d : 0.0f);
     }
 }
 
@@ -973,10 +1049,25 @@ int kdec_style_proj_fwd(kdec_ctx* ctx, const float* W, const float* b,
     KDEC_CHECK(ctx, W && style && out && N > 0 && rows > 0 && S > 0, "kdec_style_proj_fwd: bad arguments");
     // W once, style and out per utterance
     ProfScope ps(ctx, "style_proj", 0, 4.0 * (static_cast<double>(rows) * S + static_cast<double>(N) * (S + rows)));
-    const size_t lds = (static_cast<size_t>(STR) * (S + 1) + static_cast<size_t>(N) * S) * sizeof(float);
-    if (lds <= 64 * 1024 && S <= 256 && 256 % S == 0) {
-        hipLaunchKernelGGL(style_fwd_rows_k, dim3(static_cast<unsigned>(cdiv(rows, STR))), dim3(256), lds,
-                           ctx->stream, W, b, style, style_bs, out, out_bs, N, rows, S);
+    const size_t lds = style_fwd_lds_floats(S) * sizeof(float);
+    if (lds <= 64 * 1024 && S <= 128 && S % 16 == 0 && (reinterpret_cast<unsigned long long>(W) & 15) == 0 &&
+        (reinterpret_cast<unsigned long long>(style) & 15) == 0 && style_bs % 4 == 0 &&
+        static_cast<long>(rows) * S * 4 < (1L << 31)) {
+        const void* k = nullptr;
+        switch (S / 16) {  // slab float4s per thread
+            case 1: k = reinterpret_cast<const void*>(&style_fwd_rows_k<1>); break;
+            case 2: k = reinterpret_cast<const void*>(&style_fwd_rows_k<2>); break;
+            case 3: k = reinterpret_cast<const void*>(&style_fwd_rows_k<3>); break;
+            case 4: k = reinterpret_cast<const void*>(&style_fwd_rows_k<4>); break;
+            case 5: k = reinterpret_cast<const void*>(&style_fwd_rows_k<5>); break;
+            case 6: k = reinterpret_cast<const void*>(&style_fwd_rows_k<6>); break;
+            case 7: k = reinterpret_cast<const void*>(&style_fwd_rows_k<7>); break;
+            default: k = reinterpret_cast<const void*>(&style_fwd_rows_k<8>); break;
+        }
+        void* args[] = {&W, &b, &style, &style_bs, &out, &out_bs, &N, &rows, &S};
+        if (hipLaunchKernel(k, dim3(static_cast<unsigned>(cdiv(rows, STR))), dim3(256), args, lds, ctx->stream) !=
+            hipSuccess)
+            return fail(ctx, KDEC_EHIP, "style_proj_fwd: launch failed");
         return launch_check(ctx, "style_proj_fwd");
     }
     const long waves = static_cast<long>(rows) * N;
@@ -994,16 +1085,23 @@ int kdec_style_proj_bwd(kdec_ctx* ctx, const float* W, const float* style,
     ProfScope ps(ctx, "style_proj", 0,
                  4.0 * (static_cast<double>(rows) * S * ((dstyle ? 1 : 0) + (dW ? 2 : 0)) +
                         static_cast<double>(N) * (rows + S)));
-    const size_t xlds = (static_cast<size_t>(N) * STB + static_cast<size_t>(256 / std::max(S, 1)) * STN * S) *
+    const size_t xlds = (static_cast<size_t>(STB) * STN + static_cast<size_t>(256 / std::max(S, 1)) * STN * S) *
                         sizeof(float);
-    if (dstyle && S <= 256 && 256 % S == 0 && xlds <= 64 * 1024) {
+    if (dstyle && S >= 64 && S <= 256 && 256 % S == 0 && xlds <= 64 * 1024 &&
+        static_cast<long>(rows) * S * 4 < (1L << 31) && cdiv(rows, STB) * N * S * 4 < (1L << 31) &&
+        dout_bs >= rows && (static_cast<long>(N) * dout_bs + rows) * 4 < (1L << 31)) {
         const int nblk = static_cast<int>(cdiv(rows, STB));
         Workspace part(ctx, static_cast<size_t>(nblk) * N * S * sizeof(float));
         if (!part.p) return KDEC_ENOMEM;
-        hipLaunchKernelGGL(style_bwd_x_rows_k, dim3(nblk), dim3(256), xlds, ctx->stream, W, dout, dout_bs,
-                           part.as<float>(), N, rows, S);
+        float* pp = part.as<float>();
+        const void* k = S == 64    ? reinterpret_cast<const void*>(&style_bwd_x_rows_k<STB * 64 / 256>)
+                        : S == 128 ? reinterpret_cast<const void*>(&style_bwd_x_rows_k<STB * 128 / 256>)
+                                   : reinterpret_cast<const void*>(&style_bwd_x_rows_k<STB * 256 / 256>);
+        void* args[] = {&W, &dout, &dout_bs, &pp, &N, &rows, &S};
+        if (hipLaunchKernel(k, dim3(static_cast<unsigned>(nblk)), dim3(256), args, xlds, ctx->stream) != hipSuccess)
+            return fail(ctx, KDEC_EHIP, "style_bwd_x: launch failed");
         if (int rc = launch_check(ctx, "style_bwd_x")) return rc;
-        hipLaunchKernelGGL(style_bwd_x_sum_k, dim3(static_cast<unsigned>(cdiv(static_cast<long>(N) * S, 64))),
+        hipLaunchKernelGGL(style_bwd_x_sum_k, dim3(static_cast<unsigned>(cdiv(static_cast<long>(N) * S, 16))),
                            dim3(1024), 0, ctx->stream, part.as<float>(), nblk, dstyle, dstyle_bs, beta, N, S);
         if (int rc = launch_check(ctx, "style_bwd_x_reduce")) return rc;
     } else if (dstyle) {

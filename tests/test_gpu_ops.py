@@ -616,8 +616,11 @@ def test_harmonic_source(K):
         assert np.max(np.abs(dphi)) < 1e-3, f"phase error {np.max(np.abs(dphi))}"
 
 
-def test_style_projection(K):
-    N, rows, S = 3, 700, 128
+@pytest.mark.parametrize("N,rows,S", [(3, 700, 128), (8, 37396, 128), (11, 1001, 128), (2, 95, 64), (4, 300, 256),
+                                      (3, 77, 40), (2, 50, 16)])
+def test_style_projection(K, N, rows, S):
+    # the decoder's 37 396 fc rows at B = 8, ragged row blocks, more than one
+    # pass of utterances, and style widths for both kernel families
     W, b = rnd(rows, S, scale=0.1), rnd(rows)
     st = rnd(N, S, scale=0.3)
     out = torch.empty(N, rows, device="cuda")
