@@ -269,6 +269,20 @@ __device__ inline void store_tile(const GemmArgs& g, const TileGeo& T, int tile,
         const __amdgpu_buffer_rsrc_t rr = uniform_rsrc(Rb ? Rb : Yb, Rb ? rowb : 0);
         const __amdgpu_buffer_rsrc_t br = uniform_rsrc(g.bias ? g.bias : Yb, g.bias ? g.C_out * 4 : 0);
         const int mrow = m0 + wm * 64 + 4 * hi;  // the lane's first row
+        // Operand loads go in runs under one uniform branch each (bias, then
+        // per 16 elements residual and old Y), so a run costs one memory
+        // round trip: a load under a branch of its own is waited for at the
+        // branch's join.
+        const bool hb = g.bias != nullptr, hr = Rb != nullptr, hy = g.beta != 0.0f;
+        float bv[2][16];
+        if (hb) {
+#pragma unroll
+            for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    bv[tm][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                              br, (mrow + tm * 32 + 8 * (e >> 2) + (e & 3)) * 4, 0, 0));
+        }
 #pragma unroll
         for (int tn = 0; tn < 2; ++tn) {
             const int q = q0 + wn * 64 + tn * 32 + l32;
@@ -276,17 +290,28 @@ __device__ inline void store_tile(const GemmArgs& g, const TileGeo& T, int tile,
             const int vo = (mrow * Ly + q * os + oo) * 4;
 #pragma unroll
             for (int tm = 0; tm < 2; ++tm) {
+                float rv[16], yv[16];
+                if (hr) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        rv[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                              rr, vo + (tm * 32 + 8 * (e >> 2) + (e & 3)) * Ly * 4, 0, 0));
+                }
+                if (hy) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        yv[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                              yr, vo + (tm * 32 + 8 * (e >> 2) + (e & 3)) * Ly * 4, 0, 0));
+                }
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int dm = tm * 32 + 8 * (e >> 2) + (e & 3);  // uniform row step
                     const int o = vo + dm * Ly * 4;
                     float v = acc[tm][tn][e];
-                    if (g.bias)
-                        v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(br, (mrow + dm) * 4, 0, 0));
-                    if (Rb) v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, o, 0, 0));
+                    if (hb) v += bv[tm][e];
+                    if (hr) v += rv[e];
                     v *= g.scale;
-                    if (g.beta != 0.0f)
-                        v += g.beta * __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(yr, o, 0, 0));
+                    if (hy) v += g.beta * yv[e];
                     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), yr, o, 0, 0);
                 }
             }
@@ -488,24 +513,41 @@ __device__ inline void store_tile_stats(const GemmArgs& g, const TileGeo& T, f32
     const int cnt = min(max(n_q - (q0 + wn * 64), 0), 64);  // wave-uniform
     const float inv = cnt > 0 ? 1.0f / static_cast<float>(cnt) : 0.0f;
     const int slot = (q0 / BN) * 2 + wn;
+    // operand loads in runs under one uniform branch each, as in store_tile
+    // (the residual of a column past n_q reads whatever lies there and is
+    // not used)
+    const bool hb = g.bias != nullptr, hr = Rb != nullptr;
 #pragma unroll
     for (int tm = 0; tm < 2; ++tm) {
         float sx[16];
 #pragma unroll
         for (int e = 0; e < 16; ++e) sx[e] = 0.0f;
+        float bv[16];
+        if (hb) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                bv[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                      br, (mrow + tm * 32 + 8 * (e >> 2) + (e & 3)) * 4, 0, 0));
+        }
 #pragma unroll
         for (int tn = 0; tn < 2; ++tn) {
             const int q = q0 + wn * 64 + tn * 32 + l32;
             const bool qin = q < n_q;
             const int vo = (mrow * Ly + q) * 4;
+            float rv[16];
+            if (hr) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    rv[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                          rr, vo + (tm * 32 + 8 * (e >> 2) + (e & 3)) * Ly * 4, 0, 0));
+            }
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int dm = tm * 32 + 8 * (e >> 2) + (e & 3);
                 const int o = vo + dm * Ly * 4;
                 float v = acc[tm][tn][e];
-                if (g.bias)
-                    v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(br, (mrow + dm) * 4, 0, 0));
-                if (Rb && qin) v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, o, 0, 0));
+                if (hb) v += bv[e];
+                if (hr && qin) v += rv[e];
                 v *= g.scale;
                 if (qin) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), yr, o, 0, 0);
                 v = qin ? v : 0.0f;
