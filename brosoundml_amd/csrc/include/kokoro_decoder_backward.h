@@ -162,22 +162,31 @@ struct SpectralHeadCache {
     brotensor::Tensor post;    // conv_post output (N, (n_fft+2)*L)
     int C = 0;
     int L = 0;
+    // Extension: leaky_relu(x_pre, 0.01), the conv_post input, kept for the
+    // conv_post weight grad (recomputed from x_pre when empty)
+    brotensor::Tensor x_act;
 };
 
+// Extension: x_act, when given, is leaky_relu(x, 0.01) already formed (the
+// generator's last resblock sum writes it in the same pass).
 void spectral_head_forward_train(const Conv1d& conv_post,
                                  const brotensor::Tensor& x, int C, int L,
                                  const brotensor::Tensor& window,
                                  int n_fft, int hop, int win,
                                  brotensor::Tensor& audio,
-                                 SpectralHeadCache& cache);
+                                 SpectralHeadCache& cache,
+                                 const brotensor::Tensor* x_act = nullptr);
 
+// Extension: dX comes out multiplied by dx_scale (the generator divides it by
+// its K resblocks right away), the same two roundings as a separate pass.
 void spectral_head_backward(const Conv1d& conv_post,
                             const SpectralHeadCache& cache,
                             const brotensor::Tensor& window,
                             int n_fft, int hop, int win,
                             const brotensor::Tensor& dAudio,
                             brotensor::Tensor& dX,
-                            const WeightGrads* wgrads = nullptr);
+                            const WeightGrads* wgrads = nullptr,
+                            float dx_scale = 1.0f);
 
 // ─── DecoderBackbone assembly ───────────────────────────────────────────────
 struct BlockAffines {
@@ -224,6 +233,9 @@ struct ResBlock1Affines {
 
 struct GenStageCache {
     brotensor::Tensor               x_in;
+    // Extension: leaky_relu(x_in, 0.1), the ups input, kept for the ups
+    // weight grad (recomputed from x_in when empty)
+    brotensor::Tensor               a;
     AdainResBlock1Cache             noise;
     std::vector<AdainResBlock1Cache> res;
     int C_in = 0, L_in = 0;

@@ -763,15 +763,19 @@ __global__ void leaky_fwd_k(const float* X, long x_bs, float* Y, long y_bs, long
     }
 }
 
+// dx = (x > 0 ? dy : slope * dy) * scale (scale 1: the plain backward; any
+// other: the same two roundings as the backward and a separate scaling pass)
 __global__ void leaky_bwd_k(const float* X, long x_bs, const float* dY, long dy_bs, float* dX,
-                            long dx_bs, long len, float slope) {
+                            long dx_bs, long len, float slope, float scale) {
     const int n = blockIdx.y;
     const float* x = X + n * x_bs;
     const float* dy = dY + n * dy_bs;
     float* dx = dX + n * dx_bs;
     for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < len;
-         i += static_cast<long>(gridDim.x) * blockDim.x)
-        dx[i] = x[i] > 0.0f ? dy[i] : slope * dy[i];
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        const float g = x[i] > 0.0f ? dy[i] : slope * dy[i];
+        dx[i] = scale * g;
+    }
 }
 
 __global__ void axpby_k(float a, const float* A, long a_bs, float b, const float* B, long b_bs,
@@ -805,6 +809,31 @@ __global__ void add3_k(const float* A, long a_bs, const float* B, long b_bs, con
                 make_float4((a.x + b.x) + c.x, (a.y + b.y) + c.y, (a.z + b.z) + c.z, (a.w + b.w) + c.w);
         } else {
             Y[n * y_bs + i] = (A[n * a_bs + i] + B[n * b_bs + i]) + C[n * c_bs + i];
+        }
+    }
+}
+
+// add3_k that also writes Z = leaky_relu(Y, slope): the generator stage's
+// resblock sum and the next layer's activation in one pass.
+template <int V>
+__global__ void add3_leaky_k(const float* A, long a_bs, const float* B, long b_bs, const float* C, long c_bs,
+                             float* Y, long y_bs, float* Z, long z_bs, long len, float slope) {
+    const int n = blockIdx.y;
+    const long nv = len / V;
+    auto lk = [slope](float v) { return v > 0.0f ? v : slope * v; };
+    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < nv;
+         i += static_cast<long>(gridDim.x) * blockDim.x) {
+        if constexpr (V == 4) {
+            const float4 a = reinterpret_cast<const float4*>(A + n * a_bs)[i];
+            const float4 b = reinterpret_cast<const float4*>(B + n * b_bs)[i];
+            const float4 c = reinterpret_cast<const float4*>(C + n * c_bs)[i];
+            const float4 y = make_float4((a.x + b.x) + c.x, (a.y + b.y) + c.y, (a.z + b.z) + c.z, (a.w + b.w) + c.w);
+            reinterpret_cast<float4*>(Y + n * y_bs)[i] = y;
+            reinterpret_cast<float4*>(Z + n * z_bs)[i] = make_float4(lk(y.x), lk(y.y), lk(y.z), lk(y.w));
+        } else {
+            const float y = (A[n * a_bs + i] + B[n * b_bs + i]) + C[n * c_bs + i];
+            Y[n * y_bs + i] = y;
+            Z[n * z_bs + i] = lk(y);
         }
     }
 }
@@ -1355,8 +1384,18 @@ int kdec_leaky_bwd(kdec_ctx* ctx, const float* X, long x_bs, const float* dY,
     KDEC_CHECK(ctx, X && dY && dX && N > 0 && len > 0, "kdec_leaky_bwd: bad arguments");
     ProfScope ps(ctx, "elementwise", 0);
     hipLaunchKernelGGL(leaky_bwd_k, dim3(chunks(len), N), dim3(256), 0, ctx->stream, X, x_bs, dY, dy_bs, dX,
-                       dx_bs, len, slope);
+                       dx_bs, len, slope, 1.0f);
     return launch_check(ctx, "leaky_bwd");
+}
+
+int kdec_leaky_bwd_scaled(kdec_ctx* ctx, const float* X, long x_bs, const float* dY, long dy_bs, float* dX,
+                          long dx_bs, int N, long len, float slope, float scale) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, X && dY && dX && N > 0 && len > 0, "kdec_leaky_bwd_scaled: bad arguments");
+    ProfScope ps(ctx, "elementwise", 0);
+    hipLaunchKernelGGL(leaky_bwd_k, dim3(chunks(len), N), dim3(256), 0, ctx->stream, X, x_bs, dY, dy_bs, dX,
+                       dx_bs, len, slope, scale);
+    return launch_check(ctx, "leaky_bwd_scaled");
 }
 
 int kdec_axpby(kdec_ctx* ctx, float a, const float* A, long a_bs, float b,
@@ -1383,6 +1422,21 @@ int kdec_add3(kdec_ctx* ctx, const float* A, long a_bs, const float* B, long b_b
         hipLaunchKernelGGL(add3_k<1>, dim3(chunks(len), N), dim3(256), 0, ctx->stream, A, a_bs, B, b_bs, C, c_bs, Y,
                            y_bs, len);
     return launch_check(ctx, "add3");
+}
+
+int kdec_add3_leaky(kdec_ctx* ctx, const float* A, long a_bs, const float* B, long b_bs, const float* C, long c_bs,
+                    float* Y, long y_bs, float* Z, long z_bs, int N, long len, float slope) {
+    if (!ctx) return KDEC_EINVAL;
+    KDEC_CHECK(ctx, A && B && C && Y && Z && N > 0 && len > 0, "kdec_add3_leaky: bad arguments");
+    ProfScope ps(ctx, "elementwise", 0);
+    auto al = [](const float* p, long bs) { return (reinterpret_cast<unsigned long long>(p) & 15) == 0 && bs % 4 == 0; };
+    if (len % 4 == 0 && al(A, a_bs) && al(B, b_bs) && al(C, c_bs) && al(Y, y_bs) && al(Z, z_bs))
+        hipLaunchKernelGGL(add3_leaky_k<4>, dim3(chunks(len / 4), N), dim3(256), 0, ctx->stream, A, a_bs, B, b_bs, C,
+                           c_bs, Y, y_bs, Z, z_bs, len, slope);
+    else
+        hipLaunchKernelGGL(add3_leaky_k<1>, dim3(chunks(len), N), dim3(256), 0, ctx->stream, A, a_bs, B, b_bs, C,
+                           c_bs, Y, y_bs, Z, z_bs, len, slope);
+    return launch_check(ctx, "add3_leaky");
 }
 
 int kdec_add3_unpad_left1(kdec_ctx* ctx, const float* A, long a_bs, const float* B, long b_bs, const float* C,

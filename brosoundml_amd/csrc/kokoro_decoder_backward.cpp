@@ -428,10 +428,15 @@ Tensor leaky(const Tensor& x, float slope) {
     return y;
 }
 
-Tensor leaky_bwd(const Tensor& x, const Tensor& dy, float slope) {
+// dx = scale * leaky_relu_backward(x, dy) (scale 1: the plain backward)
+Tensor leaky_bwd(const Tensor& x, const Tensor& dy, float slope, float scale = 1.0f) {
     Tensor dx = dev(x.rows, x.cols);
-    ck(kdec_leaky_bwd(kctx(), cp(x), rs(x), cp(dy), rs(dy), mp(dx), rs(dx), x.rows, x.cols, slope),
-       "leaky_relu backward");
+    if (scale == 1.0f)
+        ck(kdec_leaky_bwd(kctx(), cp(x), rs(x), cp(dy), rs(dy), mp(dx), rs(dx), x.rows, x.cols, slope),
+           "leaky_relu backward");
+    else
+        ck(kdec_leaky_bwd_scaled(kctx(), cp(x), rs(x), cp(dy), rs(dy), mp(dx), rs(dx), x.rows, x.cols, slope, scale),
+           "leaky_relu backward, scaled");
     return dx;
 }
 
@@ -792,7 +797,8 @@ const float* window_ptr(const Tensor& window, int n_fft, int win, const char* wh
 }  // namespace
 
 void spectral_head_forward_train(const Conv1d& conv_post, const Tensor& x, int C, int L, const Tensor& window,
-                                 int n_fft, int hop, int win, Tensor& audio, SpectralHeadCache& cache) {
+                                 int n_fft, int hop, int win, Tensor& audio, SpectralHeadCache& cache,
+                                 const Tensor* x_act) {
     const char* where = "spectral_head_forward_train";
     check_batch(x, C, L, where);
     if (conv_post.out_channels != n_fft + 2) fail(where, "conv_post must produce n_fft + 2 channels");
@@ -800,7 +806,9 @@ void spectral_head_forward_train(const Conv1d& conv_post, const Tensor& x, int C
     cache.C = C;
     cache.L = L;
     cache.x_pre = x;
-    Tensor xl = leaky(x, 0.01f);
+    if (x_act && x_act->data) check_batch(*x_act, C, L, where);
+    Tensor xl = x_act && x_act->data ? *x_act : leaky(x, 0.01f);
+    cache.x_act = xl;
     cache.post = conv_fwd(conv_post, xl, L);
     audio = dev(x.rows, (L - 1) * hop);
     ck(kdec_spectral_fwd(kctx(), cp(cache.post), rs(cache.post), wp, mp(audio), rs(audio), x.rows, L, n_fft, hop),
@@ -809,7 +817,7 @@ void spectral_head_forward_train(const Conv1d& conv_post, const Tensor& x, int C
 
 void spectral_head_backward(const Conv1d& conv_post, const SpectralHeadCache& cache, const Tensor& window,
                             int n_fft, int hop, int win, const Tensor& dAudio, Tensor& dX,
-                            const WeightGrads* wgrads) {
+                            const WeightGrads* wgrads, float dx_scale) {
     const char* where = "spectral_head_backward";
     const int C = cache.C, L = cache.L;
     check_batch(dAudio, 1, (L - 1) * hop, where);
@@ -821,10 +829,10 @@ void spectral_head_backward(const Conv1d& conv_post, const SpectralHeadCache& ca
        where);
     Tensor dXl = conv_dgrad(conv_post, dpost, L);
     if (wgrads && (grad_of(wgrads, conv_post.W) || grad_of(wgrads, conv_post.b))) {
-        Tensor xl = leaky(cache.x_pre, 0.01f);
+        const Tensor xl = cache.x_act.data ? cache.x_act : leaky(cache.x_pre, 0.01f);
         conv_wgrad(conv_post, wgrads, xl, L, dpost);
     }
-    dX = leaky_bwd(cache.x_pre, dXl, 0.01f);
+    dX = leaky_bwd(cache.x_pre, dXl, 0.01f, dx_scale);
     (void)C;
 }
 
@@ -1005,6 +1013,7 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
     }
 
     Tensor x = gen_in;
+    Tensor x_act;  // leaky_relu of x for the next layer, when already formed
     int L = L_in;
     for (int i = 0; i < U; ++i) {
         GenStageCache& sc = cache.stages[i];
@@ -1012,26 +1021,21 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
         sc.C_in = gen.ups_C_in[i];
         sc.L_in = L;
         const int C_out = gen.ups_C_out[i];
-        Tensor a = leaky(x, 0.1f);
+        // leaky_relu(x, 0.1): formed by the previous stage's resblock sum when
+        // that ran as one kdec_add3_leaky pass
+        Tensor a = x_act.data ? x_act : leaky(x, 0.1f);
+        x_act = Tensor();
+        if (cache.keep) sc.a = a;
 
-        // ups (+ left reflect pad on the last stage) + the noise source. Before
-        // the last stage it does not read har, so it goes first and overlaps
-        // a producer still writing har, and the source is added after; the
-        // last stage's transposed conv writes the padded rows with the source
-        // added in its epilogue (kdec_convt1d_fwd_res), so it runs once the
-        // noise branch is done.
+        // ups (+ left reflect pad on the last stage) + the noise source: the
+        // transposed conv adds the source in its epilogue (kdec_convt1d_fwd_res;
+        // on the last stage it also writes the reflected column), so it runs
+        // once the noise branch is done.
         const int kL = gen.ups_k[i], s = gen.ups_stride[i], p = gen.ups_pad[i];
         const bool last = i == U - 1;
         int L_x = (L - 1) * s - 2 * p + (kL - 1) + 1;
         const float* ub = gen.ups_b[i].data ? cp(gen.ups_b[i]) : nullptr;
         Tensor u;
-        if (!last) {
-            u = dev(N, C_out * L_x);
-            ck(kdec_convt1d_fwd(kctx(), cp(a), rs(a), cp(gen.ups_W[i]), ub, mp(u), rs(u), N, sc.C_in, L, C_out, kL, s,
-                                p, 0),
-               "conv_transpose1d forward");
-            a = Tensor();
-        }
 
         // noise branch
         Tensor src;
@@ -1060,15 +1064,11 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
                             std::to_string(L_x) + " at stage " + std::to_string(i));
         sc.C_out = C_out;
         sc.L_out = L_x;
-        if (last) {
-            u = dev(N, C_out * L_x);
-            ck(kdec_convt1d_fwd_res(kctx(), cp(a), rs(a), cp(gen.ups_W[i]), ub, mp(u), rs(u), N, sc.C_in, L, C_out,
-                                    kL, s, p, 0, cp(src), rs(src), 1),
-               "conv_transpose1d forward + reflection_pad + noise source");
-            a = Tensor();
-        } else {
-            add_into(u, src);
-        }
+        u = dev(N, C_out * L_x);
+        ck(kdec_convt1d_fwd_res(kctx(), cp(a), rs(a), cp(gen.ups_W[i]), ub, mp(u), rs(u), N, sc.C_in, L, C_out, kL,
+                                s, p, 0, cp(src), rs(src), last ? 1 : 0),
+           last ? "conv_transpose1d forward + reflection_pad + noise source" : "conv_transpose1d forward + noise source");
+        a = Tensor();
         src = Tensor();
 
         // x = mean_j resblocks[i*K + j](u): each block's last conv accumulates
@@ -1093,10 +1093,15 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
             if (!cache.keep) sc.res[j] = AdainResBlock1Cache{};
         }
         if (par_rb) g_branch.join(main_ctx, K);
-        if (sep)
-            ck(kdec_add3(main_ctx, cp(xs), rs(xs), cp(outs[0]), rs(outs[0]), cp(outs[1]), rs(outs[1]), mp(xs), rs(xs),
-                         N, static_cast<long>(C_out) * L_x),
+        if (sep) {
+            // the sum and the activation the next layer reads (the next
+            // stage's ups: slope 0.1; conv_post: 0.01), in one pass
+            x_act = dev(N, C_out * L_x);
+            ck(kdec_add3_leaky(main_ctx, cp(xs), rs(xs), cp(outs[0]), rs(outs[0]), cp(outs[1]), rs(outs[1]), mp(xs),
+                               rs(xs), mp(x_act), rs(x_act), N, static_cast<long>(C_out) * L_x,
+                               last ? 0.01f : 0.1f),
                "resblock sum");
+        }
         x = xs;
         L = L_x;
     }
@@ -1106,7 +1111,8 @@ void generator_forward_train(const Generator& gen, const Tensor& gen_in, int L_i
     // the host until the stream drains)
     cache.window = Tensor();
     spectral_head_forward_train(gen.conv_post, x, gen.ups_C_out[U - 1], L, cache.window, gen.n_fft, gen.hop_size,
-                                gen.win_size, audio, cache.head);
+                                gen.win_size, audio, cache.head, &x_act);
+    x_act = Tensor();
     if (!cache.keep) cache.head = SpectralHeadCache{};
 }
 
@@ -1119,9 +1125,12 @@ void generator_backward(const Generator& gen, const GeneratorCache& cache, const
     dnaff.resize(U);
     draff.resize(static_cast<std::size_t>(U) * K);
 
+    // dX: the grad into the stage output x already divided by the K
+    // resblocks (mean over the resblocks) for every stage but the first
+    // one's input: the leaky backwards that form it apply the 1/K
     Tensor dX;
     spectral_head_backward(gen.conv_post, cache.head, cache.window, gen.n_fft, gen.hop_size, gen.win_size, dAudio,
-                           dX, wg);
+                           dX, wg, 1.0f / static_cast<float>(K));
     const int N = dAudio.rows;
     // With the resblock lanes set (the caller does so when no conv weight
     // grads occupy a second stream), each stage's resblock backwards run on
@@ -1141,7 +1150,7 @@ void generator_backward(const Generator& gen, const GeneratorCache& cache, const
         const GenStageCache& sc = cache.stages[i];
         const int L = sc.L_out;
         const int C_out = sc.C_out;
-        Tensor d_scaled = scaled(dX, 1.0f / static_cast<float>(K));
+        Tensor d_scaled = dX;
         dX = Tensor();
         // d_m = sum_j of the resblocks' input grads, in the order j = 0, 1, ...
         // (one pass for K = 3)
@@ -1212,22 +1221,26 @@ void generator_backward(const Generator& gen, const GeneratorCache& cache, const
             float* db = grad_of(wg, gen.ups_b[i]);
             if (dW || db) {
                 // on the weight-grad lane when one is set (as the conv weight
-                // grads), with the leaky input recomputed there
+                // grads), with the leaky input the forward kept (or
+                // recomputed there)
                 kdec_ctx* k = kctx();
                 if (g_lane.side) {
                     g_lane.fork();
                     k = g_lane.side;
                 }
-                Tensor a = dev(N, sc.C_in * sc.L_in);
-                const int rc1 = kdec_leaky_fwd(k, cp(sc.x_in), rs(sc.x_in), mp(a), rs(a), N, a.cols, 0.1f);
-                if (rc1 != KDEC_OK) fail("generator_backward", kdec_last_error(k));
+                Tensor a = sc.a;
+                if (!a.data) {
+                    a = dev(N, sc.C_in * sc.L_in);
+                    const int rc1 = kdec_leaky_fwd(k, cp(sc.x_in), rs(sc.x_in), mp(a), rs(a), N, a.cols, 0.1f);
+                    if (rc1 != KDEC_OK) fail("generator_backward", kdec_last_error(k));
+                }
                 const int rc2 = kdec_convt1d_wgrad(k, cp(a), rs(a), cp(du), rs(du), dW, db, N, sc.C_in, sc.L_in, C_out,
                                                    gen.ups_k[i], gen.ups_stride[i], gen.ups_pad[i], 0);
                 if (rc2 != KDEC_OK) fail("conv_transpose1d backward_weight", kdec_last_error(k));
                 if (g_lane.side) g_lane.done(a, du);  // both held until the lane is past them
             }
         }
-        dX = leaky_bwd(sc.x_in, da, 0.1f);
+        dX = leaky_bwd(sc.x_in, da, 0.1f, i > 0 ? 1.0f / static_cast<float>(K) : 1.0f);
     }
     if (noise_last) BranchLanes::wait_on(main_ctx, noise_last);  // lane 1 is in order: its last event covers all
     lane_inputs.clear();

@@ -265,6 +265,13 @@ int kdec_leaky_fwd(kdec_ctx* ctx, const float* X, long x_bs, float* Y,
 int kdec_leaky_bwd(kdec_ctx* ctx, const float* X, long x_bs, const float* dY,
                    long dy_bs, float* dX, long dx_bs, int N, long len,
                    float slope);
+/* kdec_leaky_bwd followed by a scaling pass, in one: dX = scale * ((X > 0 ?
+ * 1 : slope) * dY), the same two roundings. The generator's backward, whose
+ * stage output grad is divided by the K resblocks right after a leaky
+ * backward forms it (kokoro_decoder_backward.cpp:457 and :731, then
+ * :689-690). */
+int kdec_leaky_bwd_scaled(kdec_ctx* ctx, const float* X, long x_bs, const float* dY, long dy_bs, float* dX,
+                          long dx_bs, int N, long len, float slope, float scale);
 /* Y = a*A + b*B (B may be NULL) over N rows of `len` (bt::add_inplace /
  * bt::scale_inplace, copy_d2d for concat / slice). */
 int kdec_axpby(kdec_ctx* ctx, float a, const float* A, long a_bs, float b,
@@ -279,6 +286,12 @@ int kdec_axpby(kdec_ctx* ctx, float a, const float* A, long a_bs, float b,
 int kdec_add3(kdec_ctx* ctx, const float* A, long a_bs, const float* B,
               long b_bs, const float* C, long c_bs, float* Y, long y_bs,
               int N, long len);
+/* kdec_add3 that also writes Z = leaky_relu(Y, slope) (Y may alias A): the
+ * generator stage's resblock sum (kokoro_decoder_backward.cpp:645-655) and
+ * the activation the next stage's transposed conv (slope 0.1, :613) or
+ * conv_post (0.01, :388) reads. */
+int kdec_add3_leaky(kdec_ctx* ctx, const float* A, long a_bs, const float* B, long b_bs, const float* C, long c_bs,
+                    float* Y, long y_bs, float* Z, long z_bs, int N, long len, float slope);
 /* kdec_add3 over N x C rows of L + 1 that also writes the left reflect
  * pad's adjoint in the same pass (the generator's last stage backward,
  * :716-728): Y = (A + B) + C (as kdec_add3), and Z (rows of L) = the

@@ -537,6 +537,39 @@ def test_add3_in_order(K, cols, bs, off):
     assert np.array_equal(out[:, :off], a[:, :off]) and np.array_equal(out[:, off + cols:], a[:, off + cols:])
 
 
+@pytest.mark.parametrize("cols,bs", [(4096, 4096), (4099, 4100), (128 * 10241, 128 * 10241)])
+def test_fused_elementwise_passes(K, cols, bs):
+    # kdec_leaky_bwd_scaled against kdec_leaky_bwd and a scaling pass, and
+    # kdec_add3_leaky against kdec_add3 and kdec_leaky_fwd, bit for bit (the
+    # fused passes the generator runs in place of the pairs); aligned rows of
+    # a multiple of 4 (the float4 path) and a ragged one; zeros and negative
+    # zeros in the inputs
+    N = 2
+    x = rnd(N, bs)
+    x[:, ::97] = 0.0
+    x[:, 5::101] = -0.0
+    dy = rnd(N, bs)
+    tx, tdy = g(x), g(dy)
+    got = torch.empty(N, bs, device="cuda")
+    K.call("kdec_leaky_bwd_scaled", P(tx), bs, P(tdy), bs, P(got), bs, N, cols, 0.1, 1.0 / 3.0)
+    t = torch.empty(N, bs, device="cuda")
+    ref = torch.empty(N, bs, device="cuda")
+    K.call("kdec_leaky_bwd", P(tx), bs, P(tdy), bs, P(t), bs, N, cols, 0.1)
+    K.call("kdec_axpby", 1.0 / 3.0, P(t), bs, 0.0, None, 0, P(ref), bs, N, cols)
+    assert torch.equal(got[:, :cols], ref[:, :cols])
+    a, b, c = g(rnd(N, bs)), g(rnd(N, bs)), g(rnd(N, bs))
+    y, z = torch.empty(N, bs, device="cuda"), torch.empty(N, bs, device="cuda")
+    K.call("kdec_add3_leaky", P(a), bs, P(b), bs, P(c), bs, P(y), bs, P(z), bs, N, cols, 0.01)
+    y2, z2 = torch.empty(N, bs, device="cuda"), torch.empty(N, bs, device="cuda")
+    K.call("kdec_add3", P(a), bs, P(b), bs, P(c), bs, P(y2), bs, N, cols)
+    K.call("kdec_leaky_fwd", P(y2), bs, P(z2), bs, N, cols, 0.01)
+    assert torch.equal(y[:, :cols], y2[:, :cols]) and torch.equal(z[:, :cols], z2[:, :cols])
+    # Y aliasing A, as the generator calls it
+    K.call("kdec_add3_leaky", P(a), bs, P(b), bs, P(c), bs, P(a), bs, P(z), bs, N, cols, 0.1)
+    K.call("kdec_leaky_fwd", P(y2), bs, P(z2), bs, N, cols, 0.1)
+    assert torch.equal(a[:, :cols], y2[:, :cols]) and torch.equal(z[:, :cols], z2[:, :cols])
+
+
 @pytest.mark.parametrize("N,C,L", [(2, 3, 17), (1, 2, 2), (2, 5, 1023), (3, 4, 1024), (2, 128, 10240)])
 def test_add3_unpad_left1(K, N, C, L):
     # the fused resblock-grad sum and reflect-pad adjoint against the two
