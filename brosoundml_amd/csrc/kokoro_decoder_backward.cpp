@@ -859,17 +859,21 @@ void decoder_backbone_forward_train(const DecoderBackbone& bb, const Tensor& asr
         cache.N = N_pred;
     }
 
-    Tensor F0_dn = conv_fwd(bb.F0_conv, F0_pred, 2 * T);
-    Tensor N_dn = conv_fwd(bb.N_conv, N_pred, 2 * T);
-    Tensor asr_res_out = conv_fwd(bb.asr_res, asr, T);
-    if (F0_dn.cols != T || N_dn.cols != T) fail(where, "F0/N downsample length mismatch");
+    // the channels every residual decode block appends, cat[asr_res, F0_dn,
+    // N_dn], written in place by their convs (one copy per block after)
     const int C_res = bb.asr_res.out_channels;
+    if (bb.F0_conv.out_channels != 1 || bb.N_conv.out_channels != 1 || bb.F0_conv.out_length(2 * T) != T ||
+        bb.N_conv.out_length(2 * T) != T || bb.asr_res.out_length(T) != T)
+        fail(where, "F0/N downsample length mismatch");
+    Tensor tail = dev(N, (C_res + 2) * T);
+    conv_fwd(bb.asr_res, asr, T, mp(tail), rs(tail));
+    conv_fwd(bb.F0_conv, F0_pred, 2 * T, mp(tail) + static_cast<long>(C_res) * T, rs(tail));
+    conv_fwd(bb.N_conv, N_pred, 2 * T, mp(tail) + static_cast<long>(C_res + 1) * T, rs(tail));
 
     // encode over cat[asr, F0_dn, N_dn]
     Tensor dec_pre = dev(N, (C_asr + 2) * T);
     copy_channels(dec_pre, 0, asr, C_asr, T);
-    copy_channels(dec_pre, C_asr, F0_dn, 1, T);
-    copy_channels(dec_pre, C_asr + 1, N_dn, 1, T);
+    copy_channels(dec_pre, C_asr, chan_view(tail, C_res, 2, T), 2, T);
     int L_after = 0;
     Tensor x;
     adain_resblk_1d_forward_train(bb.encode, dec_pre, T, aff[0].g1, aff[0].b1, aff[0].g2, aff[0].b2, eps, L_after,
@@ -883,11 +887,10 @@ void decoder_backbone_forward_train(const DecoderBackbone& bb, const Tensor& asr
         Tensor blk_in;
         if (res) {
             cache.res_applied[i] = 1;
+            if (L_now != T) fail(where, "a residual decode block after the upsampling one");
             blk_in = dev(N, (Cx + C_res + 2) * L_now);
             copy_channels(blk_in, 0, x, Cx, L_now);
-            copy_channels(blk_in, Cx, asr_res_out, C_res, L_now);
-            copy_channels(blk_in, Cx + C_res, F0_dn, 1, L_now);
-            copy_channels(blk_in, Cx + C_res + 1, N_dn, 1, L_now);
+            copy_channels(blk_in, Cx, tail, C_res + 2, L_now);
         } else {
             blk_in = x;
         }
@@ -913,12 +916,10 @@ void decoder_backbone_backward(const DecoderBackbone& bb, const BackboneCache& c
     const int C_res = bb.asr_res.out_channels;
     const bool front = wg && (grad_of(wg, bb.F0_conv.W) || grad_of(wg, bb.N_conv.W) || grad_of(wg, bb.asr_res.W) ||
                               grad_of(wg, bb.F0_conv.b) || grad_of(wg, bb.N_conv.b) || grad_of(wg, bb.asr_res.b));
-    Tensor d_asr_res, d_F0dn, d_Ndn;
-    if (front) {
-        d_asr_res = devz(N, C_res * T);
-        d_F0dn = devz(N, T);
-        d_Ndn = devz(N, T);
-    }
+    // grads of the appended channels cat[asr_res, F0_dn, N_dn], summed over
+    // the residual blocks (and the encoder's F0 / N channels) in block order
+    Tensor d_tail;
+    if (front) d_tail = devz(N, (C_res + 2) * T);
 
     Tensor dX = dGenIn;
     for (int i = n_dec - 1; i >= 0; --i) {
@@ -929,11 +930,7 @@ void decoder_backbone_backward(const DecoderBackbone& bb, const BackboneCache& c
         if (cache.res_applied[i]) {
             const int Cx = cache.x_channels[i];
             const int L_in = cache.decode[i].L_in;
-            if (front) {
-                add_into(d_asr_res, chan_view(blk_dX, Cx, C_res, L_in));
-                add_into(d_F0dn, chan_view(blk_dX, Cx + C_res, 1, L_in));
-                add_into(d_Ndn, chan_view(blk_dX, Cx + C_res + 1, 1, L_in));
-            }
+            if (front) add_into(d_tail, chan_view(blk_dX, Cx, C_res + 2, L_in));
             // the leading x channels flow on; the frozen-input channels drop
             Tensor sliced = chan_view(blk_dX, 0, Cx, L_in);
             sliced.storage = blk_dX.storage;
@@ -948,11 +945,11 @@ void decoder_backbone_backward(const DecoderBackbone& bb, const BackboneCache& c
                              ge.b2, wg);
     if (front) {
         const int C_asr = bb.asr_res.in_channels;
-        add_into(d_F0dn, chan_view(enc_dX, C_asr, 1, T));
-        add_into(d_Ndn, chan_view(enc_dX, C_asr + 1, 1, T));
-        conv_wgrad(bb.F0_conv, wg, cache.F0, 2 * T, d_F0dn);
-        conv_wgrad(bb.N_conv, wg, cache.N, 2 * T, d_Ndn);
-        conv_wgrad(bb.asr_res, wg, cache.asr, T, d_asr_res);
+        Tensor d_fn = chan_view(d_tail, C_res, 2, T);
+        add_into(d_fn, chan_view(enc_dX, C_asr, 2, T));
+        conv_wgrad(bb.F0_conv, wg, cache.F0, 2 * T, chan_view(d_tail, C_res, 1, T));
+        conv_wgrad(bb.N_conv, wg, cache.N, 2 * T, chan_view(d_tail, C_res + 1, 1, T));
+        conv_wgrad(bb.asr_res, wg, cache.asr, T, chan_view(d_tail, 0, C_res, T));
     }
 }
 
