@@ -76,6 +76,23 @@ KDEC_HD inline void kdec_sincos(float th, float& s, float& c) {
     c = (qm == 1.0f || qm == 2.0f) ? -c0 : c0;
 }
 
+// sin x and cos x for |x| <= 1 (the spectral head's second map, whose
+// argument is a sine), by their Taylor series without a reduction: through
+// x^11 / 11! and x^12 / 12!, whose first omitted terms are below 1.7e-10 and
+// 1.2e-11 at |x| = 1. About half the operations of kdec_sincos.
+KDEC_HD inline void kdec_sincos_unit(float x, float& s, float& c) {
+    const float w = x * x;
+    const float ps = fmaf(w, fmaf(w, fmaf(w, fmaf(w, -2.50521084e-08f, 2.75573192e-06f), -1.98412698e-04f),
+                                  8.33333333e-03f),
+                          -1.66666667e-01f);
+    s = fmaf(x * w, ps, x);
+    const float pc = fmaf(w, fmaf(w, fmaf(w, fmaf(w, fmaf(w, 2.08767570e-09f, -2.75573192e-07f), 2.48015873e-05f),
+                                            -1.38888889e-03f),
+                                  4.16666667e-02f),
+                          -0.5f);
+    c = fmaf(w, pc, 1.0f);
+}
+
 }  // namespace kdec
 
 #undef KDEC_HD

@@ -194,6 +194,7 @@ __global__ __launch_bounds__(FT) void spec_bwd_k(const float* post, long post_bs
 template <int N>
 struct Tw {
     float c[N], s[N];
+    float w[N];  // the periodic Hann window over N (the backward's frame weights)
 };
 template <int N>
 Tw<N> make_tw() {
@@ -201,8 +202,20 @@ Tw<N> make_tw() {
     for (int r = 0; r < N; ++r) {
         t.c[r] = static_cast<float>(std::cos(2.0 * M_PI * r / N));
         t.s[r] = static_cast<float>(std::sin(2.0 * M_PI * r / N));
+        t.w[r] = static_cast<float>((0.5 - 0.5 * std::cos(2.0 * M_PI * r / N)) / N);
     }
     return t;
+}
+
+// e^x as 2^(x log2 e) on the hardware exp2, with log2 e split in two floats
+// (hi = 1.44269502, lo = log2 e - hi) so that the rounding of x hi is
+// carried: 2^t (1 + r ln 2) with t = fl(x hi), r = (x hi - t) + x lo. Within a
+// few ulp for the log-magnitudes the head sees; about half the operations of
+// the library expf.
+__device__ inline float kdec_exp(float x) {
+    const float t = x * 1.44269502f;
+    const float r = fmaf(x, 1.44269502f, -t) + x * 1.92596299e-08f;
+    return __builtin_amdgcn_exp2f(t) * fmaf(r, 0.693147181f, 1.0f);
 }
 
 template <int N>
@@ -236,14 +249,24 @@ __global__ __launch_bounds__(FT) void spec_fwd_fixed_k(const float* post, long p
         float* out = fr + threadIdx.x * NP;
         float re[F], im[F];
         const bool in = f >= 0 && f < L;
+        // every bin's two inputs loaded before the first use, from a frame
+        // clamped into the signal (a load under the `in` branch would be
+        // waited for at the branch's join, one round trip per bin)
+        const int fc = min(max(f, 0), L - 1);
+        float lm[F], lp[F];
+#pragma unroll
+        for (int k = 0; k < F; ++k) {
+            lm[k] = P[static_cast<long>(k) * L + fc];
+            lp[k] = P[static_cast<long>(F + k) * L + fc];
+        }
 #pragma unroll
         for (int k = 0; k < F; ++k) {
             re[k] = im[k] = 0.0f;
             if (in) {
-                const float mag = expf(P[static_cast<long>(k) * L + f]);
+                const float mag = kdec_exp(lm[k]);
                 float spp, cpp, sa, ca;
-                kdec_sincos(P[static_cast<long>(F + k) * L + f], spp, cpp);
-                kdec_sincos(spp, sa, ca);
+                kdec_sincos(lp[k], spp, cpp);
+                kdec_sincos_unit(spp, sa, ca);
                 re[k] = mag * ca;
                 im[k] = mag * sa;
             }
@@ -293,81 +316,147 @@ __global__ __launch_bounds__(FT) void spec_fwd_fixed_k(const float* post, long p
     }
 }
 
-// The backward, one block per FT frames of one utterance: the block's polar
-// inputs are loaded first (their loads fly while dY / envelope over the
-// frames' sample span is staged in LDS), then each thread forms its frame's
-// grads. At most 64 VGPRs, so that every block of the decoder's head is
-// resident at once.
+// The backward over G groups of FT frames of one utterance per block (frame
+// f0 + g FT + t for thread t): every global load of a group is issued at once
+// and unconditionally (a load under a branch is waited for at the branch's
+// join), and group g + 1's loads are issued before group g's arithmetic, so
+// they fly while it runs. Per group, dY / envelope over the frames' sample
+// span is staged in LDS, then each thread forms its frame's grads.
+#ifndef SPEC_BWD_G
+#define SPEC_BWD_G 1  // frame groups per backward block
+#endif
 template <int N, int H>
-__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(8)))
+struct SpecBwdIn {
+    static constexpr int F = N / 2 + 1;
+    static constexpr int M = FT * H + N;  // ola positions a group's frames cover
+    static constexpr int R = (M + FT - 1) / FT;
+    float dv[R];        // dY samples this thread stages (clamped into the signal)
+    float pm[F], pp[F]; // the frame's polar inputs (clamped to the last frame)
+};
+
+template <int N, int H>
+__device__ inline void spec_bwd_load(SpecBwdIn<N, H>& in, const float* P0, const float* dy, int fg, int L,
+                                     int sig_len) {
+    using I = SpecBwdIn<N, H>;
+#pragma unroll
+    for (int r = 0; r < I::R; ++r) {
+        const int j = fg * H + static_cast<int>(threadIdx.x) + r * FT - N / 2;
+        in.dv[r] = dy[min(max(j, 0), sig_len - 1)];
+    }
+    const float* P = P0 + min(fg + static_cast<int>(threadIdx.x), L - 1);
+#pragma unroll
+    for (int k = 0; k < I::F; ++k) {
+        in.pm[k] = P[static_cast<long>(k) * L];
+        in.pp[k] = P[static_cast<long>(I::F + k) * L];
+    }
+}
+
+template <int N, int H, int G>
+__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(G == 1 ? 8 : 5)))
 void spec_bwd_fixed_k(const float* post, long post_bs, const float* window, const float* daudio, long da_bs,
                       float* dpost, long dp_bs, int L, Tw<N> tw) {
-    constexpr int F = N / 2 + 1;
-    constexpr int M = FT * H + N;  // ola positions the block's frames cover
+    using I = SpecBwdIn<N, H>;
+    constexpr int F = I::F, M = I::M, R = I::R;
     __shared__ float win[N];
     __shared__ float ienv[H];  // 1 / envelope at interior positions, by m mod H
     __shared__ float u[M];
     load_win<N>(win, window);
     const int b = blockIdx.y;
-    const int f0 = blockIdx.x * FT;
-    const int f = f0 + threadIdx.x;
-    const float* P = post + b * post_bs + min(f, L - 1);
-    float pm[F], pp[F];
-#pragma unroll
-    for (int k = 0; k < F; ++k) {
-        pm[k] = P[static_cast<long>(k) * L];
-        pp[k] = P[static_cast<long>(F + k) * L];
-    }
+    const int fb = blockIdx.x * FT * G;
+    const int sig_len = (L - 1) * H;  // >= H: L >= 2
+    const float* P0 = post + b * post_bs;
+    const float* dy = daudio + b * da_bs;
+    I in[2];
+    spec_bwd_load<N, H>(in[0], P0, dy, fb, L, sig_len);
     __syncthreads();  // win
     // an interior position m (every frame that could cover it exists:
     // N <= m <= (L - 1) H) sees the same windows as m + H
     if (threadIdx.x < H) ienv[threadIdx.x] = 1.0f / env_at(win, N + ((threadIdx.x - N) % H + H) % H, N, H, L);
     __syncthreads();
-    const int sig_len = (L - 1) * H;
-    // u[i] = dY[j] / envelope(m) at ola position m = f0 * H + i (j = m - N/2;
-    // 0 outside the signal, where the envelope may be 0)
-    const float* dy = daudio + b * da_bs;
-    for (int i = threadIdx.x; i < M; i += FT) {
-        const int m = f0 * H + i;
-        const int j = m - N / 2;
-        float v = 0.0f;
-        if (j >= 0 && j < sig_len)
-            v = (m >= N && m <= (L - 1) * H) ? dy[j] * ienv[m % H] : dy[j] / env_at(win, m, N, H, L);
-        u[i] = v;
-    }
-    __syncthreads();
-    if (f >= L) return;
     constexpr float invN = 1.0f / N;
-    float dfr[N];
 #pragma unroll
-    for (int n = 0; n < N; ++n) dfr[n] = u[threadIdx.x * H + n] * win[n] * invN;
-    float sp[N / 2], dm[N / 2];  // pair sums / differences, n = 1 .. N/2 - 1
+    for (int g = 0; g < G; ++g) {
+        const I& cur = in[g & 1];
+        const int f0 = fb + g * FT;
+        const int f = f0 + threadIdx.x;
+        if (g > 0) __syncthreads();  // the previous group's reads of u are done
+        // u[i] = dY[j] / envelope(m) at ola position m = f0 * H + i (j = m -
+        // N/2; 0 outside the signal, where the envelope may be 0)
 #pragma unroll
-    for (int n = 1; n < N / 2; ++n) {
-        sp[n] = dfr[n] + dfr[N - n];
-        dm[n] = dfr[n] - dfr[N - n];
-    }
-    float* D = dpost + b * dp_bs + f;
-#pragma unroll
-    for (int k = 0; k < F; ++k) {
-        const bool edge = k == 0 || k == F - 1;
-        float re = dfr[0] + ((k & 1) ? -dfr[N / 2] : dfr[N / 2]);
-        float im = 0.0f;
-#pragma unroll
-        for (int n = 1; n < N / 2; ++n) {
-            re += sp[n] * tw.c[(k * n) % N];
-            im -= dm[n] * tw.s[(k * n) % N];
+        for (int r = 0; r < R; ++r) {
+            const int i = static_cast<int>(threadIdx.x) + r * FT;
+            if (i < M) {
+                const int m = f0 * H + i;
+                const int j = m - N / 2;
+                float v = 0.0f;
+                if (j >= 0 && j < sig_len)
+                    v = (m >= N && m <= (L - 1) * H) ? cur.dv[r] * ienv[m % H] : cur.dv[r] / env_at(win, m, N, H, L);
+                u[i] = v;
+            }
         }
-        const float dRe = edge ? re : 2.0f * re;
-        const float dIm = edge ? 0.0f : 2.0f * im;
-        const float mag = expf(pm[k]);
-        float spp, cpp, sa, ca;
-        kdec_sincos(pp[k], spp, cpp);
-        kdec_sincos(spp, sa, ca);
-        const float dmag = dRe * ca + dIm * sa;
-        const float dang = mag * (-dRe * sa + dIm * ca);
-        D[static_cast<long>(k) * L] = dmag * mag;
-        D[static_cast<long>(F + k) * L] = dang * cpp;
+        __syncthreads();
+        if (g + 1 < G) spec_bwd_load<N, H>(in[(g + 1) & 1], P0, dy, f0 + FT, L, sig_len);
+        if (f < L) {
+            float dfr[N];
+#pragma unroll
+            for (int n = 0; n < N; ++n) dfr[n] = u[threadIdx.x * H + n] * (window ? win[n] * invN : tw.w[n]);
+            // Folded real DFT: with Q = N / 4, the pair sums sp and
+            // differences dm over n <-> N - n, then over n <-> N/2 - n (cos
+            // and sin at k (N/2 - n) are (-1)^k cos and -(-1)^k sin at k n):
+            // even k sees A = sp[n] + sp[N/2 - n] and C = dm[n] - dm[N/2 - n],
+            // odd k B = sp[n] - sp[N/2 - n] and E = dm[n] + dm[N/2 - n]; the
+            // middle term n = Q has cos(pi k / 2) and sin(pi k / 2) in {0, +-1}
+            static_assert(N % 4 == 0, "the folded DFT takes N a multiple of 4");
+            constexpr int Q = N / 4;
+            float sp[N / 2], dm[N / 2];  // n = 1 .. N/2 - 1
+#pragma unroll
+            for (int n = 1; n < N / 2; ++n) {
+                sp[n] = dfr[n] + dfr[N - n];
+                dm[n] = dfr[n] - dfr[N - n];
+            }
+            float A[Q], B[Q], C[Q], E[Q];  // n = 1 .. Q - 1
+#pragma unroll
+            for (int n = 1; n < Q; ++n) {
+                A[n] = sp[n] + sp[N / 2 - n];
+                B[n] = sp[n] - sp[N / 2 - n];
+                C[n] = dm[n] - dm[N / 2 - n];
+                E[n] = dm[n] + dm[N / 2 - n];
+            }
+            const float e0 = dfr[0] + dfr[N / 2], e1 = dfr[0] - dfr[N / 2];
+            float* D = dpost + b * dp_bs + f;
+#pragma unroll
+            for (int k = 0; k < F; ++k) {
+                const bool edge = k == 0 || k == F - 1;
+                float re, im;
+                if (k % 2 == 0) {
+                    re = (k % 4 == 0) ? e0 + sp[Q] : e0 - sp[Q];
+                    im = 0.0f;
+#pragma unroll
+                    for (int n = 1; n < Q; ++n) {
+                        re += A[n] * tw.c[(k * n) % N];
+                        im -= C[n] * tw.s[(k * n) % N];
+                    }
+                } else {
+                    re = e1;
+                    im = (k % 4 == 1) ? -dm[Q] : dm[Q];
+#pragma unroll
+                    for (int n = 1; n < Q; ++n) {
+                        re += B[n] * tw.c[(k * n) % N];
+                        im -= E[n] * tw.s[(k * n) % N];
+                    }
+                }
+                const float dRe = edge ? re : 2.0f * re;
+                const float dIm = edge ? 0.0f : 2.0f * im;
+                const float mag = kdec_exp(cur.pm[k]);
+                float spp, cpp, sa, ca;
+                kdec_sincos(cur.pp[k], spp, cpp);
+                kdec_sincos_unit(spp, sa, ca);
+                const float dmag = dRe * ca + dIm * sa;
+                const float dang = mag * (-dRe * sa + dIm * ca);
+                D[static_cast<long>(k) * L] = dmag * mag;
+                D[static_cast<long>(F + k) * L] = dang * cpp;
+            }
+        }
     }
 }
 
@@ -993,8 +1082,9 @@ int kdec_spectral_bwd(kdec_ctx* ctx, const float* post, long post_bs,
     const double bytes = 4.0 * N * (2.0 * (n_fft + 2) * L + static_cast<double>(L - 1) * hop);
     ProfScope ps(ctx, "spectral_bwd", 0, bytes);
     if (n_fft == 20 && hop == 5) {
-        hipLaunchKernelGGL((spec_bwd_fixed_k<20, 5>), dim3(static_cast<unsigned>(cdiv(L, FT)), N), dim3(FT), 0,
-                           ctx->stream, post, post_bs, window, daudio, daudio_bs, dpost, dpost_bs, L, make_tw<20>());
+        hipLaunchKernelGGL((spec_bwd_fixed_k<20, 5, SPEC_BWD_G>),
+                           dim3(static_cast<unsigned>(cdiv(L, FT * SPEC_BWD_G)), N), dim3(FT), 0, ctx->stream, post,
+                           post_bs, window, daudio, daudio_bs, dpost, dpost_bs, L, make_tw<20>());
         return launch_check(ctx, "spec_bwd");
     }
     with_nfft_bound(n_fft, [&](auto nm) {

@@ -1,5 +1,5 @@
 """The Snake forward's sin^2 and the backward's (sin^2, sin 2th) pair, and
-the spectral head's (sin, cos) pair (brosoundml_amd/csrc/kdec_snake_math.hpp),
+the spectral head's (sin, cos) pairs (brosoundml_amd/csrc/kdec_snake_math.hpp),
 built for the host with g++ and checked against double precision: the error
 bound over wide argument ranges, the values at multiples of pi/2 (every
 quadrant's signs), the tiny argument limit and arguments past 2^31. The GPU kernels compile the same header; their forward parity
@@ -57,6 +57,24 @@ int main() {
         std::printf("quadsc %d %.9e %.9e %.9e %.9e\n", q, sv, ex, cv, std::cos(static_cast<double>(th)));
     }
     std::printf("tiny %.9e\n", kdec::snake_sin2(1e-10f) / 1e-20);
+    {  // the unit-range pair on [-1, 1], its ends, zero and the smallest normal
+        std::uniform_real_distribution<float> U(-1.0f, 1.0f);
+        double max_u = 0.0;
+        for (int i = 0; i < 400000; ++i) {
+            float x = U(g);
+            if (i == 0) x = 1.0f;
+            if (i == 1) x = -1.0f;
+            if (i == 2) x = 0.0f;
+            if (i == 3) x = 1.17549435e-38f;
+            float sv, cv;
+            kdec::kdec_sincos_unit(x, sv, cv);
+            max_u = std::fmax(max_u, std::fmax(std::fabs(sv - std::sin(static_cast<double>(x))),
+                                               std::fabs(cv - std::cos(static_cast<double>(x)))));
+        }
+        float s0, c0;
+        kdec::kdec_sincos_unit(0.0f, s0, c0);
+        std::printf("unit %.6e %d\n", max_u, s0 == 0.0f && c0 == 1.0f ? 1 : 0);
+    }
     return 0;
 }
 """
@@ -120,3 +138,10 @@ def test_sincos_pair(results):
     assert len(quads) == 17
     for r in quads:
         assert abs(float(r[2]) - float(r[3])) < 2e-7 and abs(float(r[4]) - float(r[5])) < 2e-7, r
+
+
+def test_sincos_unit(results):
+    # the spectral head's second map, sin / cos of a sine, by the series
+    # without a reduction: within 2e-7 of double over [-1, 1], exact at 0
+    row = [r for r in results if r[0] == "unit"][0]
+    assert float(row[1]) < 2e-7 and row[2] == "1", row
