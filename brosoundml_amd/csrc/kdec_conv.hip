@@ -1112,6 +1112,27 @@ void corr_gemm(GemmArgs g) {
 
 // Split tiles: Y = scale * (sum of the parts in order + bias + R) + beta * Y.
 // Grid (BM * BN / 1024, split_tiles).
+// The split parts of one float4 of a tile summed in part order (the bits of
+// a sequential loop), their loads issued eight at a time: a loop that loads
+// one part per trip waits for each before the next.
+__device__ inline float4 sum_parts(const float4* Pt, int e4, int fsplit) {
+    float4 v = Pt[e4];
+    for (int sp = 1; sp < fsplit; sp += 8) {
+        float4 w[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) w[u] = Pt[min(sp + u, fsplit - 1) * (BM * BN / 4) + e4];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (sp + u < fsplit) {
+                v.x += w[u].x;
+                v.y += w[u].y;
+                v.z += w[u].z;
+                v.w += w[u].w;
+            }
+    }
+    return v;
+}
+
 __global__ void tile_reduce(GemmArgs g) {
     const int ti = blockIdx.y;
     TileGeo T;
@@ -1124,16 +1145,22 @@ __global__ void tile_reduce(GemmArgs g) {
     for (int e4 = blockIdx.x * blockDim.x + threadIdx.x; e4 < BM * BN / 4; e4 += gridDim.x * blockDim.x) {
         const int m = T.m0 + (e4 * 4) / BN, qb = T.q0 + (e4 * 4) % BN;
         if (m >= g.C_out || qb >= T.n_q) continue;
-        float4 v = Pt[e4];
-        for (int sp = 1; sp < g.fsplit; ++sp) {
-            const float4 w = Pt[sp * (BM * BN / 4) + e4];
-            v.x += w.x;
-            v.y += w.y;
-            v.z += w.z;
-            v.w += w.w;
-        }
+        const float4 v = sum_parts(Pt, e4, g.fsplit);
         const float vv[4] = {v.x, v.y, v.z, v.w};
         const float bs = g.bias ? g.bias[m] : 0.0f;
+        // the four columns' residual and old Y in one run each (a column
+        // past n_q reads the last valid one and is not stored)
+        float rv[4], yv[4];
+        if (Rb) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                rv[j] = Rb[static_cast<long>(m) * g.L_y + static_cast<long>(min(qb + j, T.n_q - 1)) * T.os + T.oo];
+        }
+        if (g.beta != 0.0f) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                yv[j] = Yb[static_cast<long>(m) * g.L_y + static_cast<long>(min(qb + j, T.n_q - 1)) * T.os + T.oo];
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int q = qb + j;
@@ -1145,9 +1172,9 @@ __global__ void tile_reduce(GemmArgs g) {
                 const long y0 = static_cast<long>(m) * g.L_y;
                 Yb[y0] = (x + (Rb ? Rb[y0] : 0.0f)) * g.scale;
             }
-            if (Rb) x += Rb[yi];
+            if (Rb) x += rv[j];
             x *= g.scale;
-            if (g.beta != 0.0f) x += g.beta * Yb[yi];
+            if (g.beta != 0.0f) x += g.beta * yv[j];
             Yb[yi] = x;
         }
     }
@@ -1169,14 +1196,7 @@ __global__ __launch_bounds__(256) void tile_reduce_adain(GemmArgs g) {
     const float4* Pt = reinterpret_cast<const float4*>(g.P + static_cast<long>(ti) * g.fsplit * (BM * BN));
     float sd = 0.0f, sdx = 0.0f, sa = 0.0f, a = 1.0f;
     if (m < g.C_out) {
-        float4 v = Pt[e4];
-        for (int sp = 1; sp < g.fsplit; ++sp) {
-            const float4 w = Pt[sp * (BM * BN / 4) + e4];
-            v.x += w.x;
-            v.y += w.y;
-            v.z += w.z;
-            v.w += w.w;
-        }
+        const float4 v = sum_parts(Pt, e4, g.fsplit);
         const int row = T.b * g.C_out + m;
         const float2 st = g.ad.st[row];
         const float g1 = 1.0f + g.ad.gam[T.b * g.ad.gb_bs + m];
@@ -1185,12 +1205,15 @@ __global__ __launch_bounds__(256) void tile_reduce_adain(GemmArgs g) {
         const float vv[4] = {v.x, v.y, v.z, v.w};
         float* Yb = g.Y + static_cast<long>(T.b) * g.y_bs;
         const float* xb = g.ad.x + static_cast<long>(T.b) * g.ad.x_bs;
+        float xv[4];  // one run of loads (a column past n_q reads the last valid one)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xv[j] = xb[static_cast<long>(m) * g.L_y + min(qb + j, T.n_q - 1)];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int q = qb + j;
             if (q >= T.n_q) break;
             const long yi = static_cast<long>(m) * g.L_y + q;
-            const float xh = (xb[yi] - st.x) * st.y;
+            const float xh = (xv[j] - st.x) * st.y;
             const float ds = epi_act_bwd(g.ad.act, vv[j] * g.scale, g1 * xh + bt, g.ad.slope, a, sa);
             Yb[yi] = ds;
             sd += ds;
@@ -1240,25 +1263,23 @@ __global__ __launch_bounds__(256) void tile_reduce_stats(GemmArgs g) {
     const float4* Pt = reinterpret_cast<const float4*>(g.P + static_cast<long>(ti) * g.fsplit * (BM * BN));
     float vv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (m < g.C_out) {
-        float4 v = Pt[e4];
-        for (int sp = 1; sp < g.fsplit; ++sp) {
-            const float4 w = Pt[sp * (BM * BN / 4) + e4];
-            v.x += w.x;
-            v.y += w.y;
-            v.z += w.z;
-            v.w += w.w;
-        }
+        const float4 v = sum_parts(Pt, e4, g.fsplit);
         const float raw[4] = {v.x, v.y, v.z, v.w};
         const float bs = g.bias ? g.bias[m] : 0.0f;
         float* Yb = g.Y + static_cast<long>(T.b) * g.y_bs;
         const float* Rb = g.R ? g.R + static_cast<long>(T.b) * g.r_bs : nullptr;
+        float rv[4];  // one run of loads (a column past n_q reads the last valid one)
+        if (Rb) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) rv[j] = Rb[static_cast<long>(m) * g.L_y + min(qb + j, T.n_q - 1)];
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int q = qb + j;
             if (q >= T.n_q) break;
             const long yi = static_cast<long>(m) * g.L_y + q;
             float x = raw[j] + bs;
-            if (Rb) x += Rb[yi];
+            if (Rb) x += rv[j];
             x *= g.scale;
             Yb[yi] = x;
             vv[j] = x;
