@@ -269,20 +269,12 @@ __device__ inline void store_tile(const GemmArgs& g, const TileGeo& T, int tile,
         const __amdgpu_buffer_rsrc_t rr = uniform_rsrc(Rb ? Rb : Yb, Rb ? rowb : 0);
         const __amdgpu_buffer_rsrc_t br = uniform_rsrc(g.bias ? g.bias : Yb, g.bias ? g.C_out * 4 : 0);
         const int mrow = m0 + wm * 64 + 4 * hi;  // the lane's first row
-        // Operand loads go in runs under one uniform branch each (bias, then
-        // per 16 elements residual and old Y), so a run costs one memory
-        // round trip: a load under a branch of its own is waited for at the
-        // branch's join.
+        // Operand loads go in runs of eight elements under one uniform branch
+        // each (bias, residual, old Y), so a run costs one memory round trip:
+        // a load under a branch of its own is waited for at the branch's
+        // join. Eight, not all 32 of a tile's rows at once, so that the runs'
+        // registers and the accumulators fit without spilling.
         const bool hb = g.bias != nullptr, hr = Rb != nullptr, hy = g.beta != 0.0f;
-        float bv[2][16];
-        if (hb) {
-#pragma unroll
-            for (int tm = 0; tm < 2; ++tm)
-#pragma unroll
-                for (int e = 0; e < 16; ++e)
-                    bv[tm][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                              br, (mrow + tm * 32 + 8 * (e >> 2) + (e & 3)) * 4, 0, 0));
-        }
 #pragma unroll
         for (int tn = 0; tn < 2; ++tn) {
             const int q = q0 + wn * 64 + tn * 32 + l32;
@@ -290,29 +282,38 @@ __device__ inline void store_tile(const GemmArgs& g, const TileGeo& T, int tile,
             const int vo = (mrow * Ly + q * os + oo) * 4;
 #pragma unroll
             for (int tm = 0; tm < 2; ++tm) {
-                float rv[16], yv[16];
-                if (hr) {
 #pragma unroll
-                    for (int e = 0; e < 16; ++e)
-                        rv[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                              rr, vo + (tm * 32 + 8 * (e >> 2) + (e & 3)) * Ly * 4, 0, 0));
-                }
-                if (hy) {
+                for (int e0 = 0; e0 < 16; e0 += 8) {
+                    float bv[8], rv[8], yv[8];
+                    if (hb) {
 #pragma unroll
-                    for (int e = 0; e < 16; ++e)
-                        yv[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                              yr, vo + (tm * 32 + 8 * (e >> 2) + (e & 3)) * Ly * 4, 0, 0));
-                }
+                        for (int e = 0; e < 8; ++e)
+                            bv[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                br, (mrow + tm * 32 + 8 * ((e0 + e) >> 2) + (e & 3)) * 4, 0, 0));
+                    }
+                    if (hr) {
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int dm = tm * 32 + 8 * (e >> 2) + (e & 3);  // uniform row step
-                    const int o = vo + dm * Ly * 4;
-                    float v = acc[tm][tn][e];
-                    if (hb) v += bv[tm][e];
-                    if (hr) v += rv[e];
-                    v *= g.scale;
-                    if (hy) v += g.beta * yv[e];
-                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), yr, o, 0, 0);
+                        for (int e = 0; e < 8; ++e)
+                            rv[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                rr, vo + (tm * 32 + 8 * ((e0 + e) >> 2) + (e & 3)) * Ly * 4, 0, 0));
+                    }
+                    if (hy) {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            yv[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                yr, vo + (tm * 32 + 8 * ((e0 + e) >> 2) + (e & 3)) * Ly * 4, 0, 0));
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int dm = tm * 32 + 8 * ((e0 + e) >> 2) + (e & 3);  // uniform row step
+                        const int o = vo + dm * Ly * 4;
+                        float v = acc[tm][tn][e0 + e];
+                        if (hb) v += bv[e];
+                        if (hr) v += rv[e];
+                        v *= g.scale;
+                        if (hy) v += g.beta * yv[e];
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), yr, o, 0, 0);
+                    }
                 }
             }
             if (g.refl && q * os + oo == 1 + g.y_off) {  // the reflected column 0 (beta = 0)
