@@ -274,26 +274,51 @@ __global__ __launch_bounds__(FT) void spec_fwd_fixed_k(const float* post, long p
         __syncthreads();  // win
         if (threadIdx.x < H) ienv[threadIdx.x] = 1.0f / env_at(win, N + ((threadIdx.x - N) % H + H) % H, N, H, L);
         // x[n] = (re0 + (-1)^n re_{N/2} + 2 sum_k re_k cos) - 2 sum_k im_k sin,
-        // x[N - n] the same with the sine sum added
+        // x[N - n] the same with the sine sum added; the sums folded on
+        // k <-> N/2 - k (cos and sin at (N/2 - k) n are (-1)^n cos and
+        // -(-1)^n sin at k n): even n sees A = 2(re_k + re_{N/2-k}) and C =
+        // 2(im_k - im_{N/2-k}), odd n B = 2(re_k - re_{N/2-k}) and E =
+        // 2(im_k + im_{N/2-k}); the middle bin k = N/4 has cos(pi n / 2) and
+        // sin(pi n / 2) in {0, +-1}
+        static_assert(N % 4 == 0, "the folded synthesis takes N a multiple of 4");
+        constexpr int Q = N / 4;
         constexpr float invN = 1.0f / N;
         const float e0 = re[0] + re[F - 1], e1 = re[0] - re[F - 1];
+        float A[Q], B[Q], C[Q], E[Q];  // k = 1 .. Q - 1
 #pragma unroll
-        for (int n = 0; n <= N / 2; n += N / 2) {  // the two points without a sine term
-            float a = (n & 1) ? e1 : e0;
-#pragma unroll
-            for (int k = 1; k < F - 1; ++k) a += 2.0f * re[k] * tw.c[(k * n) % N];
-            out[n] = a * invN * win[n];
+        for (int k = 1; k < Q; ++k) {
+            A[k] = 2.0f * (re[k] + re[N / 2 - k]);
+            B[k] = 2.0f * (re[k] - re[N / 2 - k]);
+            C[k] = 2.0f * (im[k] - im[N / 2 - k]);
+            E[k] = 2.0f * (im[k] + im[N / 2 - k]);
         }
+        const float r5 = 2.0f * re[Q], i5 = 2.0f * im[Q];
 #pragma unroll
-        for (int n = 1; n < N / 2; ++n) {
-            float a = (n & 1) ? e1 : e0, bb = 0.0f;
+        for (int n = 0; n <= N / 2; ++n) {
+            float a, bb;
+            if (n % 2 == 0) {
+                a = (n % 4 == 0) ? e0 + r5 : e0 - r5;
+                bb = 0.0f;
 #pragma unroll
-            for (int k = 1; k < F - 1; ++k) {
-                a += 2.0f * re[k] * tw.c[(k * n) % N];
-                bb += 2.0f * im[k] * tw.s[(k * n) % N];
+                for (int k = 1; k < Q; ++k) {
+                    a += A[k] * tw.c[(k * n) % N];
+                    bb += C[k] * tw.s[(k * n) % N];
+                }
+            } else {
+                a = e1;
+                bb = (n % 4 == 1) ? i5 : -i5;
+#pragma unroll
+                for (int k = 1; k < Q; ++k) {
+                    a += B[k] * tw.c[(k * n) % N];
+                    bb += E[k] * tw.s[(k * n) % N];
+                }
             }
-            out[n] = (a - bb) * invN * win[n];
-            out[N - n] = (a + bb) * invN * win[N - n];
+            if (n == 0 || n == N / 2) {  // the two points without a sine term
+                out[n] = a * invN * win[n];
+            } else {
+                out[n] = (a - bb) * invN * win[n];
+                out[N - n] = (a + bb) * invN * win[N - n];
+            }
         }
     }
     __syncthreads();
@@ -316,19 +341,16 @@ __global__ __launch_bounds__(FT) void spec_fwd_fixed_k(const float* post, long p
     }
 }
 
-// The backward over G groups of FT frames of one utterance per block (frame
-// f0 + g FT + t for thread t): every global load of a group is issued at once
-// and unconditionally (a load under a branch is waited for at the branch's
-// join), and group g + 1's loads are issued before group g's arithmetic, so
-// they fly while it runs. Per group, dY / envelope over the frames' sample
-// span is staged in LDS, then each thread forms its frame's grads.
-#ifndef SPEC_BWD_G
-#define SPEC_BWD_G 1  // frame groups per backward block
-#endif
+// The backward, one block per FT frames of one utterance (frame f0 + t for
+// thread t): every global load is issued at once and unconditionally (a load
+// under a branch is waited for at the branch's join), then dY / envelope over
+// the frames' sample span is staged in LDS and each thread forms its frame's
+// grads. At most 64 VGPRs, so that every block of the decoder's head is
+// resident at once.
 template <int N, int H>
 struct SpecBwdIn {
     static constexpr int F = N / 2 + 1;
-    static constexpr int M = FT * H + N;  // ola positions a group's frames cover
+    static constexpr int M = FT * H + N;  // ola positions the block's frames cover
     static constexpr int R = (M + FT - 1) / FT;
     float dv[R];        // dY samples this thread stages (clamped into the signal)
     float pm[F], pp[F]; // the frame's polar inputs (clamped to the last frame)
@@ -351,8 +373,8 @@ __device__ inline void spec_bwd_load(SpecBwdIn<N, H>& in, const float* P0, const
     }
 }
 
-template <int N, int H, int G>
-__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(G == 1 ? 8 : 5)))
+template <int N, int H>
+__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(8)))
 void spec_bwd_fixed_k(const float* post, long post_bs, const float* window, const float* daudio, long da_bs,
                       float* dpost, long dp_bs, int L, Tw<N> tw) {
     using I = SpecBwdIn<N, H>;
@@ -362,24 +384,20 @@ void spec_bwd_fixed_k(const float* post, long post_bs, const float* window, cons
     __shared__ float u[M];
     load_win<N>(win, window);
     const int b = blockIdx.y;
-    const int fb = blockIdx.x * FT * G;
+    const int f0 = blockIdx.x * FT;
+    const int f = f0 + threadIdx.x;
     const int sig_len = (L - 1) * H;  // >= H: L >= 2
     const float* P0 = post + b * post_bs;
     const float* dy = daudio + b * da_bs;
-    I in[2];
-    spec_bwd_load<N, H>(in[0], P0, dy, fb, L, sig_len);
+    I cur;
+    spec_bwd_load<N, H>(cur, P0, dy, f0, L, sig_len);
     __syncthreads();  // win
     // an interior position m (every frame that could cover it exists:
     // N <= m <= (L - 1) H) sees the same windows as m + H
     if (threadIdx.x < H) ienv[threadIdx.x] = 1.0f / env_at(win, N + ((threadIdx.x - N) % H + H) % H, N, H, L);
     __syncthreads();
     constexpr float invN = 1.0f / N;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const I& cur = in[g & 1];
-        const int f0 = fb + g * FT;
-        const int f = f0 + threadIdx.x;
-        if (g > 0) __syncthreads();  // the previous group's reads of u are done
+    {
         // u[i] = dY[j] / envelope(m) at ola position m = f0 * H + i (j = m -
         // N/2; 0 outside the signal, where the envelope may be 0)
 #pragma unroll
@@ -395,7 +413,6 @@ void spec_bwd_fixed_k(const float* post, long post_bs, const float* window, cons
             }
         }
         __syncthreads();
-        if (g + 1 < G) spec_bwd_load<N, H>(in[(g + 1) & 1], P0, dy, f0 + FT, L, sig_len);
         if (f < L) {
             float dfr[N];
 #pragma unroll
@@ -1082,9 +1099,8 @@ int kdec_spectral_bwd(kdec_ctx* ctx, const float* post, long post_bs,
     const double bytes = 4.0 * N * (2.0 * (n_fft + 2) * L + static_cast<double>(L - 1) * hop);
     ProfScope ps(ctx, "spectral_bwd", 0, bytes);
     if (n_fft == 20 && hop == 5) {
-        hipLaunchKernelGGL((spec_bwd_fixed_k<20, 5, SPEC_BWD_G>),
-                           dim3(static_cast<unsigned>(cdiv(L, FT * SPEC_BWD_G)), N), dim3(FT), 0, ctx->stream, post,
-                           post_bs, window, daudio, daudio_bs, dpost, dpost_bs, L, make_tw<20>());
+        hipLaunchKernelGGL((spec_bwd_fixed_k<20, 5>), dim3(static_cast<unsigned>(cdiv(L, FT)), N), dim3(FT), 0,
+                           ctx->stream, post, post_bs, window, daudio, daudio_bs, dpost, dpost_bs, L, make_tw<20>());
         return launch_check(ctx, "spec_bwd");
     }
     with_nfft_bound(n_fft, [&](auto nm) {
