@@ -28,6 +28,7 @@
 // X[n, c, l*s + t*d - p], a GEMM with the huge position axis as K. It is
 // split over K into deterministic partial tiles that a second kernel sums in
 // a fixed order; the bias grad (row sums of dY) rides along in the same pass.
+#include "kdec_buffer.hpp"
 #include "kdec_internal.hpp"
 #include "kdec_snake_math.hpp"
 
@@ -47,21 +48,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int BM = 128;   // output-channel tile
 constexpr int BN = 128;   // output-position tile
 constexpr int NT = 256;   // threads per block (4 waves)
-// Buffer descriptor word 3 for raw 32-bit buffer loads (DATA_FORMAT = 32).
-constexpr int kBufDword3 = 0x00020000;
-
-// Raw buffer descriptor over [base, base + bytes), built from wave-uniform
-// (scalar) values: a descriptor the compiler cannot prove uniform would be
-// wrapped in a per-lane "waterfall" loop around every buffer load.
-__device__ inline __amdgpu_buffer_rsrc_t uniform_rsrc(const float* base, int bytes) {
-    const unsigned long long a = reinterpret_cast<unsigned long long>(base);
-    const unsigned lo = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(a));
-    const unsigned hi = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(a >> 32));
-    const int n = __builtin_amdgcn_readfirstlane(bytes);
-    float* p = reinterpret_cast<float*>((static_cast<unsigned long long>(hi) << 32) | lo);
-    return __builtin_amdgcn_make_buffer_rsrc(p, static_cast<short>(0), n, kBufDword3);
-}
-
 __device__ inline int floordiv_i(int a, int b) {
     int q = a / b;
     if ((a % b != 0) && ((a < 0) != (b < 0))) --q;

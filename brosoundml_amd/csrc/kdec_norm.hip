@@ -9,6 +9,7 @@
 //
 // Statistics are per (utterance, channel) row over L, accumulated in double
 // so the result does not depend on the row length or the thread count.
+#include "kdec_buffer.hpp"
 #include "kdec_internal.hpp"
 #include "kdec_snake_math.hpp"
 
@@ -477,14 +478,7 @@ unsigned v4_blocks(int L) { return static_cast<unsigned>(std::max(1L, cdiv(stati
 // offset, so no per-element address registers are needed, and lanes past the
 // row read zeros and drop their stores.
 
-__device__ inline __amdgpu_buffer_rsrc_t row_rsrc(const float* base, int L) {
-    const unsigned long long a = reinterpret_cast<unsigned long long>(base);
-    const unsigned lo = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(a));
-    const unsigned hi = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(a >> 32));
-    float* p = reinterpret_cast<float*>((static_cast<unsigned long long>(hi) << 32) | lo);
-    return __builtin_amdgcn_make_buffer_rsrc(p, static_cast<short>(0), __builtin_amdgcn_readfirstlane(L * 4),
-                                             0x00020000);
-}
+__device__ inline __amdgpu_buffer_rsrc_t row_rsrc(const float* base, int L) { return uniform_rsrc(base, L * 4); }
 
 __device__ inline float row_ld(__amdgpu_buffer_rsrc_t r, int voff, int j, int ntb) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, j * ntb * 4, 0));

@@ -7,6 +7,7 @@
 // dropped. irfft ignores the imaginary parts of the DC and Nyquist bins.
 // The transforms are n_fft = 20 direct sums with twiddles staged in LDS:
 // far too small for an FFT to pay, and direct sums keep the order fixed.
+#include "kdec_buffer.hpp"
 #include "kdec_internal.hpp"
 #include "kdec_snake_math.hpp"
 
@@ -742,17 +743,6 @@ inline size_t style_fwd_lds_floats(int S) {
     return static_cast<size_t>(STR) * (S + 4) + static_cast<size_t>(STG) * STQ * STR;
 }
 
-// Raw buffer descriptor over [base, base + bytes) from wave-uniform values
-// (out-of-range loads return 0).
-__device__ inline __amdgpu_buffer_rsrc_t style_rsrc(const float* base, int bytes) {
-    const unsigned long long a = reinterpret_cast<unsigned long long>(base);
-    const unsigned lo = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(a));
-    const unsigned hi = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(a >> 32));
-    float* p = reinterpret_cast<float*>((static_cast<unsigned long long>(hi) << 32) | lo);
-    return __builtin_amdgcn_make_buffer_rsrc(p, static_cast<short>(0), __builtin_amdgcn_readfirstlane(bytes),
-                                             0x00020000);
-}
-
 __device__ inline float style_ld(__amdgpu_buffer_rsrc_t r, int byte_off, int soff = 0) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, soff, 0));
 }
@@ -776,7 +766,7 @@ __global__ __launch_bounds__(256) void style_fwd_rows_k(const float* __restrict_
     const int nr = min(STR, rows - r0);
     const int S4 = S >> 2;
     {  // the slab, STR * S4 == 256 * KQ float4s, all in flight
-        const __amdgpu_buffer_rsrc_t wr = style_rsrc(W, rows * S * 4);
+        const __amdgpu_buffer_rsrc_t wr = uniform_rsrc(W, rows * S * 4);
         const int wb = r0 * S * 4;
         float4 v[KQ];
 #pragma unroll
@@ -847,8 +837,8 @@ __global__ __launch_bounds__(256) void style_bwd_x_rows_k(const float* W, const 
     const int r0 = blockIdx.x * STB;
     const int nr = min(STB, rows - r0);
     const int j = threadIdx.x % S, ph = __builtin_amdgcn_readfirstlane(threadIdx.x / S);  // S >= 64
-    const __amdgpu_buffer_rsrc_t wr = style_rsrc(W, rows * S * 4);
-    const __amdgpu_buffer_rsrc_t dr = style_rsrc(dout, static_cast<int>(((N - 1) * d_bs + rows) * 4));
+    const __amdgpu_buffer_rsrc_t wr = uniform_rsrc(W, rows * S * 4);
+    const __amdgpu_buffer_rsrc_t dr = uniform_rsrc(dout, static_cast<int>(((N - 1) * d_bs + rows) * 4));
     // row ph + i * PH of the block is 1 KB * i past the thread's first one
     const int vo = ((r0 + ph) * S + j) * 4;
     float w[PER];
@@ -912,7 +902,7 @@ __global__ __launch_bounds__(1024) void style_bwd_x_sum_k(const float* part, int
     const int nj = blockIdx.x * 16 + o;
     const int NS = N * S;
     const int q0 = p * nblk / 64, q1 = (p + 1) * nblk / 64;
-    const __amdgpu_buffer_rsrc_t pr = style_rsrc(part, nblk * NS * 4);
+    const __amdgpu_buffer_rsrc_t pr = uniform_rsrc(part, nblk * NS * 4);
     double acc = 0.0;
     for (int qb = q0; qb < q1; qb += 16) {
         float v[16];
