@@ -882,7 +882,13 @@ void conv_gemm_q(GemmArgs g) {
     const int bq = wn * 64 + l32;
     const bool live = T.q0 + wn * 64 < T.n_q;  // wave-uniform
     for (int ch = ch0; ch < ch1; ++ch) {
+        // the next chunk's staging issued at a raised wave priority: a wave
+        // that reaches it gets its DMA instructions out ahead of the other
+        // waves' MFMAs and LDS reads on the SIMD, so the loads start early
+        // (one-stream conv and weight-grad families 0.5 % faster)
+        __builtin_amdgcn_s_setprio(1);
         if (ch + 1 < ch1) issue(T, ch + 1, stage - sb);
+        __builtin_amdgcn_s_setprio(0);
         if (live) {
             const QSrc cur = q_src(g, T, span, QA);
             const f32x4* Aq = reinterpret_cast<const f32x4*>(smem + sb) + hi * BM + am;
@@ -1737,7 +1743,9 @@ void wgrad_gemm(WgradArgs g) {
     __syncthreads();
     for (int ch = ch0; ch < ch1; ++ch) {
         const int sb = ((ch - ch0) & 1) * stage;
+        __builtin_amdgcn_s_setprio(1);  // as in conv_gemm_q
         if (ch + 1 < ch1) issue(ch + 1, stage - sb);
+        __builtin_amdgcn_s_setprio(0);
         if (do_bias && tid < BM) {
             float t = 0.0f;
             const int row = sb + (tid & 63) * GP + (tid >> 6) * KC;
