@@ -1127,6 +1127,7 @@ __device__ inline float4 sum_parts(const float4* Pt, int e4, int fsplit) {
 }
 
 __global__ void tile_reduce(GemmArgs g) {
+    __builtin_amdgcn_s_setprio(2);  // on the conv chain: as the AdaIN passes
     const int ti = blockIdx.y;
     TileGeo T;
     decode_tile(g, g.full_tiles + ti, T);
@@ -1179,6 +1180,7 @@ __global__ void tile_reduce(GemmArgs g) {
 // split_tiles) of 256 threads), so the 32 lanes of a half-wave hold one
 // row's 128 columns: their sums go to slot 2 * q_tile, zeros to the other.
 __global__ __launch_bounds__(256) void tile_reduce_adain(GemmArgs g) {
+    __builtin_amdgcn_s_setprio(2);  // on the conv chain: as the AdaIN passes
     const int ti = blockIdx.y;
     TileGeo T;
     decode_tile(g, g.full_tiles + ti, T);
@@ -1245,6 +1247,7 @@ __global__ __launch_bounds__(256) void tile_reduce_adain(GemmArgs g) {
 // lanes of a half-wave hold one row's 128 columns) into slot 2 * q_tile, an
 // empty record into the other. Grid (BM * BN / 1024, split_tiles) x 256.
 __global__ __launch_bounds__(256) void tile_reduce_stats(GemmArgs g) {
+    __builtin_amdgcn_s_setprio(2);  // on the conv chain: as the AdaIN passes
     const int ti = blockIdx.y;
     TileGeo T;
     decode_tile(g, g.full_tiles + ti, T);

@@ -218,6 +218,10 @@ __device__ inline int row_head(const float* p, int L) {
 
 __global__ __launch_bounds__(RT) void adain_act_fwd_v4_k(AdainArgs g, float* Y, long y_bs, float* Yp,
                                                         long yp_bs) {
+    // a raised wave priority: beside the weight-grad GEMMs of another stream,
+    // this pass sits on the conv chain, and its loads and stores win
+    // issue slots over their MFMA waves on a shared SIMD
+    __builtin_amdgcn_s_setprio(2);
     constexpr int Q = EPT / 4;  // float4s per thread
     const int row = blockIdx.y;
     const int n = row / g.C, c = row - n * g.C;
@@ -405,6 +409,10 @@ __global__ __launch_bounds__(RT) void adain_bwd_apply_v4_k(AdainArgs g, const fl
                                                           const float* R, long r_bs, float* dX, long dx_bs,
                                                           const float2* rowv, const float* ap, float* dalpha,
                                                           int N) {
+    // a raised wave priority: beside the weight-grad GEMMs of another stream,
+    // this pass sits on the conv chain, and its loads and stores win
+    // issue slots over their MFMA waves on a shared SIMD
+    __builtin_amdgcn_s_setprio(2);
     constexpr int Q = EPT / 4;
     const int row = blockIdx.y;
     const int n = row / g.C, c = row - n * g.C;
@@ -1153,6 +1161,10 @@ int bwd_run(kdec_ctx* ctx, const AdainArgs& g, const float* dY, long dy_bs, cons
 __global__ __launch_bounds__(64) void adain_bwd_fin_wide_k(const double* part, int nch, int C, int L,
                                                            float* dgamma, float* dbeta, long dgb_bs,
                                                            float* dalpha_part, float2* rowv) {
+    // a raised wave priority: beside the weight-grad GEMMs of another stream,
+    // this pass sits on the conv chain, and its loads and stores win
+    // issue slots over their MFMA waves on a shared SIMD
+    __builtin_amdgcn_s_setprio(2);
     const int row = blockIdx.x;
     const int n = row / C, c = row - n * C;
     const double* p = part + static_cast<long>(row) * nch * 3;
