@@ -373,8 +373,8 @@ __device__ inline float xor_lane(float v) {
 // One halving step of a transpose-reduce over the 32 lanes of a half: each
 // lane keeps the upper or lower half of its N values (by lane bit K) and adds
 // the partner's copy of that half.
-template <int K, int N>
-__device__ inline void halve(float (&v)[16], int l32) {
+template <int K, int N, int S>
+__device__ inline void halve(float (&v)[S], int l32) {
     const bool up = (l32 & K) != 0;
 #pragma unroll
     for (int j = 0; j < N / 2; ++j) {
@@ -391,6 +391,16 @@ __device__ inline void reduce16(float (&v)[16], int l32) {
     halve<8, 8>(v, l32);
     halve<4, 4>(v, l32);
     halve<2, 2>(v, l32);
+    v[0] += xor_lane<1>(v[0]);
+}
+
+// Sums of 8 values per lane over the 32 lanes of a half: afterwards lanes
+// 4 i .. 4 i + 3 hold the total of value i in v[0].
+__device__ inline void reduce8(float (&v)[8], int l32) {
+    halve<16, 8>(v, l32);
+    halve<8, 4>(v, l32);
+    halve<4, 2>(v, l32);
+    v[0] += xor_lane<2>(v[0]);
     v[0] += xor_lane<1>(v[0]);
 }
 
@@ -431,44 +441,58 @@ __device__ inline void store_tile_adain(const GemmArgs& g, const TileGeo& T, con
     const __amdgpu_buffer_rsrc_t xr = uniform_rsrc(g.ad.x + static_cast<long>(b) * g.ad.x_bs, rowb);
     const int mrow = m0 + wm * 64 + 4 * hi;
     const int slot = (q0 / BN) * 2 + wn;
+    // Rows in halves of 8 values per lane (e = 8 h .. 8 h + 7): the sums of
+    // one half and its x run stay within the register budget of the GEMM.
 #pragma unroll
     for (int tm = 0; tm < 2; ++tm) {
-        float sd[16], sdx[16], sa[16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) sd[e] = sdx[e] = sa[e] = 0.0f;
+        for (int h = 0; h < 2; ++h) {
+            float sd[8], sdx[8], sa[8];
 #pragma unroll
-        for (int tn = 0; tn < 2; ++tn) {
-            const int q = q0 + wn * 64 + tn * 32 + l32;
-            if (q >= n_q) continue;
-            const int vo = (mrow * Ly + q) * 4;
+            for (int j = 0; j < 8; ++j) sd[j] = sdx[j] = sa[j] = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int dm = tm * 32 + 8 * (e >> 2) + (e & 3);
-                const int o = vo + dm * Ly * 4;
-                const int rl = wm * 64 + 4 * hi + dm;
-                const float4 pr = prm[rl];
-                const float x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, o, 0, 0));
-                const float dy = acc[tm][tn][e] * g.scale;
-                const float xh = (x - pr.x) * pr.y;
-                const float ds = epi_act_bwd(g.ad.act, dy, pr.z * xh + pr.w, g.ad.slope, pal[rl], sa[e]);
-                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, ds), yr, o, 0, 0);
-                sd[e] += ds;
-                sdx[e] += ds * xh;
+            for (int tn = 0; tn < 2; ++tn) {
+                const int q = q0 + wn * 64 + tn * 32 + l32;
+                if (q >= n_q) continue;
+                const int vo = (mrow * Ly + q) * 4;
+                // x ahead of the stores: a load placed after a store to a
+                // buffer that may alias waits for that store too.
+                float xv[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int e = 8 * h + j;
+                    const int o = vo + (tm * 32 + 8 * (e >> 2) + (e & 3)) * Ly * 4;
+                    xv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, o, 0, 0));
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int e = 8 * h + j;
+                    const int dm = tm * 32 + 8 * (e >> 2) + (e & 3);
+                    const int o = vo + dm * Ly * 4;
+                    const int rl = wm * 64 + 4 * hi + dm;
+                    const float4 pr = prm[rl];
+                    const float dy = acc[tm][tn][e] * g.scale;
+                    const float xh = (xv[j] - pr.x) * pr.y;
+                    const float ds = epi_act_bwd(g.ad.act, dy, pr.z * xh + pr.w, g.ad.slope, pal[rl], sa[j]);
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, ds), yr, o, 0, 0);
+                    sd[j] += ds;
+                    sdx[j] += ds * xh;
+                }
             }
-        }
-        reduce16(sd, l32);
-        reduce16(sdx, l32);
-        if (g.ad.act == KDEC_ACT_SNAKE) reduce16(sa, l32);  // uniform
-        if ((l32 & 1) == 0) {
-            const int e = l32 >> 1;
-            const int rl = wm * 64 + tm * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
-            const int m = m0 + rl;
-            if (m < g.C_out) {
-                double* pp = g.ad.part + ((static_cast<long>(b) * g.C_out + m) * g.ad.nch + slot) * 3;
-                const double a = pal[rl];
-                pp[0] = sd[0];
-                pp[1] = sdx[0];
-                pp[2] = g.ad.act == KDEC_ACT_SNAKE ? static_cast<double>(sa[0]) / (a * a) : 0.0;
+            reduce8(sd, l32);
+            reduce8(sdx, l32);
+            if (g.ad.act == KDEC_ACT_SNAKE) reduce8(sa, l32);  // uniform
+            if ((l32 & 3) == 0) {
+                const int e = 8 * h + (l32 >> 2);
+                const int rl = wm * 64 + tm * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
+                const int m = m0 + rl;
+                if (m < g.C_out) {
+                    double* pp = g.ad.part + ((static_cast<long>(b) * g.C_out + m) * g.ad.nch + slot) * 3;
+                    const double a = pal[rl];
+                    pp[0] = sd[0];
+                    pp[1] = sdx[0];
+                    pp[2] = g.ad.act == KDEC_ACT_SNAKE ? static_cast<double>(sa[0]) / (a * a) : 0.0;
+                }
             }
         }
     }
