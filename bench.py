@@ -227,20 +227,27 @@ def micro_benches(ctx, reps=50):
     dilations 1/3/5, X [4,512,2048]), the two ConvTranspose1d upsampler
     backwards, the iSTFT head backward and forward and the style projection
     at the benchmark's B = 8 shapes, each timed alone with HIP events on the context stream over
-    `reps` back-to-back calls after 3 untimed ones (the cases take 20-450 us,
+    `reps` back-to-back calls after 3 untimed ones (the cases take 5-450 us,
     so a shorter run would weigh the queue's start-up on them) and priced
     against its roofline (algorithmic bytes at 8 TB/s or FLOP at the
-    FP32-MFMA peak)."""
+    FP32-MFMA peak). The timed calls are queued behind a ~4 ms spacer GEMM
+    (torch.mm, before the first event), so that the device runs them back to
+    back as it does inside a step, instead of at the rate the host issues
+    them: each call is one or more ctypes calls and kernel launches, which
+    take longer on the host than the few-microsecond cases take on the GPU."""
     import torch
     from brosoundml_amd import native, synth
     P = native.ptr
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    spa = torch.ones(4096, 4096, device="cuda")
 
     def timed(fn):
         for _ in range(3):
             fn()
         torch.cuda.synchronize()
         s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(4):
+            torch.mm(spa, spa)
         s0.record()
         for _ in range(reps):
             fn()

@@ -1468,29 +1468,32 @@ __device__ inline long panel_index(int c, int t, int CK, int kk) {
 
 // A[panel_index(c, t)][m] = W[m][c*k + t] (0 unless m < Mv and c < Cv): the
 // conv1d forward panel (m = co, c = ci) and the conv-transpose input-grad
-// panel (m = ci, c = co). A 64 (m) x 64 (j = c*k + t) tile passes through LDS:
-// W is read along its rows (j), A written along its rows (m). Grid
-// (cdiv(cpad*k, 64), m_pad / 64); cpad a multiple of CK, m_pad of 64.
+// panel (m = ci, c = co). A 32 (m) x 32 (j = c*k + t) tile passes through LDS:
+// W is read along its rows (j), A written along its rows (m). 32-square tiles
+// rather than 64: a single round of larger blocks spends most of its time
+// waiting on one load and one store round trip, and four times as many
+// blocks overlap one block's stores with others' loads (1.2-1.9x faster on
+// the decoder's panels). Grid (cdiv(cpad*k, 32), m_pad / 32); cpad a
+// multiple of CK, m_pad of 32.
 __global__ __launch_bounds__(256) void pack_rows_t(const float* W, float* A, int Mv, int Cv, int k, int cpad,
                                                    int m_pad, int CK) {
-    __shared__ float tile[64][65];
-    const int j0 = blockIdx.x * 64, m0 = blockIdx.y * 64;
-    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    __shared__ float tile[32][33];
+    const int j0 = blockIdx.x * 32, m0 = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
     const long ld = static_cast<long>(Cv) * k;  // W row length
-    // fixed trip counts, unrolled: all 16 loads of a thread are in flight at once
-    float v[16];
+    float v[4];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int m = m0 + ty + 4 * r, j = j0 + tx;
+    for (int r = 0; r < 4; ++r) {
+        const int m = m0 + ty + 8 * r, j = j0 + tx;
         v[r] = (m < Mv && j < ld) ? W[m * ld + j] : 0.0f;
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) tile[tx][ty + 4 * r] = v[r];
+    for (int r = 0; r < 4; ++r) tile[tx][ty + 8 * r] = v[r];
     __syncthreads();
     const long rows = static_cast<long>(cpad) * k;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int i = ty + 4 * r, j = j0 + i;
+    for (int r = 0; r < 4; ++r) {
+        const int i = ty + 8 * r, j = j0 + i;
         if (j < rows) {
             const int c = j / k, t = j - c * k;
             A[panel_index(c, t, CK, k) * m_pad + m0 + tx] = tile[i][tx];
@@ -1938,6 +1941,49 @@ __global__ void bias_partial(const float* G, long g_bs, float* part, int N, int 
     if (threadIdx.x == 0) part[static_cast<long>(y) * M + m] = static_cast<float>(red[0]);
 }
 
+// db[m] += sum over (n, l) of G[n, m, l] in one pass for rows of at most
+// 128 K positions over all utterances: one 1024-thread block per row m;
+// thread i sums, in float and in order, the vectors i, i + 1024, ... of the
+// row's N * L / V (V = 4: float4 on 16-B aligned rows of a multiple of 4
+// floats), eight loads in flight (each issued unconditionally from a clamped
+// index, only its use is bounded), and the block adds the thread sums in
+// double in a fixed tree.
+template <int V>
+__global__ __launch_bounds__(1024) void bias_rows_direct(const float* G, long g_bs, float* db, int N, int L) {
+    const int m = blockIdx.x;
+    const int Lv = L / V;
+    const int tot = N * Lv;
+    float acc = 0.0f;
+    for (int f0 = threadIdx.x; f0 < tot; f0 += 8 * 1024) {
+        float v[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const int f = min(f0 + s * 1024, tot - 1);
+            const int n = f / Lv, l = f - n * Lv;
+            const float* row = G + n * g_bs + static_cast<long>(m) * L;
+            if constexpr (V == 4) {
+                const float4 q = reinterpret_cast<const float4*>(row)[l];
+                v[s] = (q.x + q.y) + (q.z + q.w);
+            } else {
+                v[s] = row[l];
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            if (f0 + s * 1024 < tot) acc += v[s];
+    }
+    double d = acc;
+    for (int o = 32; o > 0; o >>= 1) d += __shfl_down(d, o, 64);
+    __shared__ double wsum[16];
+    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = d;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        for (int w = 0; w < 16; ++w) t += wsum[w];
+        db[m] += static_cast<float>(t);
+    }
+}
+
 // db[m] += sum_y part[y, m]: one wave per m; lane j sums y = j, j+64, ... in
 // order, then a fixed shuffle tree adds the 64 lane sums.
 __global__ void bias_reduce(const float* part, float* db, int M, int S) {
@@ -2327,9 +2373,9 @@ int conv_fwd_impl(kdec_ctx* ctx, const float* X, long x_bs, const float* W, cons
         hipLaunchKernelGGL(pack_octet, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), 0, C_in,
                            C_out, k, 1, k, m_pad, static_cast<int>(tot), 1);
     else
-        if (g.cin_pad % g.CK == 0 && m_pad % 64 == 0)
-            hipLaunchKernelGGL(pack_rows_t, dim3(static_cast<unsigned>(cdiv(static_cast<long>(g.cin_pad) * k, 64)),
-                                                 static_cast<unsigned>(m_pad / 64)),
+        if (g.cin_pad % g.CK == 0 && m_pad % 32 == 0)
+            hipLaunchKernelGGL(pack_rows_t, dim3(static_cast<unsigned>(cdiv(static_cast<long>(g.cin_pad) * k, 32)),
+                                                 static_cast<unsigned>(m_pad / 32)),
                                dim3(256), 0, ctx->stream, W, A.as<float>(), C_out, C_in, k, g.cin_pad, m_pad, g.CK);
         else
             hipLaunchKernelGGL(pack_fwd, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(), C_in,
@@ -2680,11 +2726,21 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
 
 // db (M) += sum over (n, l) of G[n, m, l]
 static int bias_grad_only(kdec_ctx* ctx, const float* G, long g_bs, float* db, int N, int M, int L) {
+    const bool v4 = L % 4 == 0 && g_bs % 4 == 0 && (reinterpret_cast<unsigned long long>(G) & 15) == 0;
+    if (2L * M >= ctx->num_cus && static_cast<long>(N) * L <= 128L * 1024) {
+        // a row per block on at least half the CUs, each row short enough for one block
+        if (v4)
+            hipLaunchKernelGGL(bias_rows_direct<4>, dim3(static_cast<unsigned>(M)), dim3(1024), 0, ctx->stream, G,
+                               g_bs, db, N, L);
+        else
+            hipLaunchKernelGGL(bias_rows_direct<1>, dim3(static_cast<unsigned>(M)), dim3(1024), 0, ctx->stream, G,
+                               g_bs, db, N, L);
+        return launch_check(ctx, "bias_rows_direct");
+    }
     // slices of at least 1024 positions, enough of them for ~4 blocks per CU
     long S = std::min(cdiv(4L * ctx->num_cus, M), cdiv(L, 1024));
     if (S > 256) S = 256;
     if (S < 1) S = 1;
-    const bool v4 = L % 4 == 0 && g_bs % 4 == 0 && (reinterpret_cast<unsigned long long>(G) & 15) == 0;
     int per = static_cast<int>(cdiv(L, S));
     if (v4) per = (per + 3) & ~3;
     S = cdiv(L, per);
@@ -2804,9 +2860,9 @@ int kdec_convt1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
     const long tot = static_cast<long>(cpad) * k * m_pad;
     Workspace A(ctx, static_cast<size_t>(tot) * sizeof(float));
     if (!A.p) return KDEC_ENOMEM;
-    if (cpad % CK == 0 && m_pad % 64 == 0)
-        hipLaunchKernelGGL(pack_rows_t, dim3(static_cast<unsigned>(cdiv(static_cast<long>(cpad) * k, 64)),
-                                             static_cast<unsigned>(m_pad / 64)),
+    if (cpad % CK == 0 && m_pad % 32 == 0)
+        hipLaunchKernelGGL(pack_rows_t, dim3(static_cast<unsigned>(cdiv(static_cast<long>(cpad) * k, 32)),
+                                             static_cast<unsigned>(m_pad / 32)),
                            dim3(256), 0, ctx->stream, W, A.as<float>(), C_in, C_out, k, cpad, m_pad, CK);
     else
         hipLaunchKernelGGL(pack_convt_dgrad, dim3(grid1d(tot)), dim3(256), 0, ctx->stream, W, A.as<float>(),

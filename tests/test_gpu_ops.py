@@ -327,6 +327,25 @@ def test_convt1d(K, N, C_in, C_out, L, k, s, p):
     assert_close(h(db), rb, GRAD_TOL, "conv_transpose1d backward_bias")
 
 
+@pytest.mark.parametrize("N,C_out,L,k,s,p", [
+    (4, 256, 512, 20, 10, 5),    # one block per row, float4 reads (the ups0 backward case, 5120 outputs)
+    (3, 130, 167, 12, 6, 3),     # one block per row, scalar reads (1002 outputs)
+    (2, 128, 11667, 12, 6, 3),   # rows past 128 K positions (2 x 70002): slice partials, then their sum
+])
+def test_convt1d_bias_grad(K, N, C_out, L, k, s, p):
+    """The transposed conv's bias grad alone (dW null): db += sum over (n, l)
+    of dY[n, c, l], against a float64 sum, for both of its reduction plans."""
+    C_in = 8
+    Lo = O.convt1d_out_len(L, k, s, p, 0, 1)
+    dY = rnd(N, C_out, Lo)
+    db0 = rnd(C_out)
+    db = g(db0)
+    K.call("kdec_convt1d_wgrad", P(g(rnd(N, C_in, L))), C_in * L, P(g(dY)), C_out * Lo, None, P(db), N, C_in, L,
+           C_out, k, s, p, 0)
+    ref = db0.astype(np.float64) + dY.astype(np.float64).sum(axis=(0, 2))
+    assert_close(h(db), ref, GRAD_TOL, "conv_transpose1d backward_bias")
+
+
 def test_pool(K):
     N, C, L = 2, 9, 33
     x, W, b = rnd(N, C, L), rnd(C, 3), rnd(C)
