@@ -39,7 +39,7 @@
 namespace brosoundml {
 namespace detail {
 
-// ─── north-star extension: weight grads ────────────────────────────────────
+// ─── extension: weight grads ───────────────────────────────────────────────
 struct WeightGrads {
     // weight storage (Tensor::data) -> tensor its grad accumulates into
     std::unordered_map<const void*, brotensor::Tensor*> grads;

@@ -135,7 +135,7 @@ int kdec_conv1d_dgrad_adain_bwd(kdec_ctx* ctx, const float* W, const float* dY,
 
 /* dW (C_out, C_in*k) and db (C_out) accumulated over the batch; either may
  * be NULL.
- * North-star extension: the reference freezes conv weights; the signature of
+ * Extension: the reference freezes conv weights; the signature of
  * its accumulating bt::conv1d_backward_weight/_bias is the one used in
  * src/bc_resnet.cpp:1006-1007, 1020-1025. */
 int kdec_conv1d_wgrad(kdec_ctx* ctx, const float* X, long x_bs,
@@ -164,7 +164,7 @@ int kdec_convt1d_fwd_res(kdec_ctx* ctx, const float* X, long x_bs, const float* 
 int kdec_convt1d_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
                        long dy_bs, float* dX, long dx_bs, int N, int C_in,
                        int L, int C_out, int k, int stride, int pad, int op);
-/* dW (C_in, C_out*k), db (C_out) accumulated. North-star extension. */
+/* dW (C_in, C_out*k), db (C_out) accumulated. Extension of the reference. */
 int kdec_convt1d_wgrad(kdec_ctx* ctx, const float* X, long x_bs,
                        const float* dY, long dy_bs, float* dW, float* db,
                        int N, int C_in, int L, int C_out, int k, int stride,
@@ -177,7 +177,7 @@ int kdec_pool_fwd(kdec_ctx* ctx, const float* X, long x_bs, const float* W,
                   const float* bias, float* Y, long y_bs, int N, int C, int L);
 int kdec_pool_dgrad(kdec_ctx* ctx, const float* W, const float* dY,
                     long dy_bs, float* dX, long dx_bs, int N, int C, int L);
-/* dW (C,3), db (C) accumulated. North-star extension. */
+/* dW (C,3), db (C) accumulated. Extension of the reference. */
 int kdec_pool_wgrad(kdec_ctx* ctx, const float* X, long x_bs, const float* dY,
                     long dy_bs, float* dW, float* db, int N, int C, int L);
 
@@ -374,7 +374,7 @@ int kdec_lora_proj_fwd(kdec_ctx* ctx, const float* W, const float* b,
                        int rank, const float* style, long style_bs, float* H,
                        float* out, long out_bs, int N, int rows, int S);
 /* Its adjoint (adapter_bwd, decoder_lora.cpp:198-207, over bt::lora_backward)
- * plus the north-star d(style). With dHG[n, u*rank+j] = scale * sum_{r in u}
+ * plus the d(style) extension. With dHG[n, u*rank+j] = scale * sum_{r in u}
  * B[r, j] dout[n, r]:
  *   dB[r, j] += scale * sum_n dout[n, r] g[n, j] H[n, u(r)*rank + j]
  *   dG[n, j] += sum_u dHG[n, u*rank+j] H[n, u*rank+j]   (summed over n when g_bs = 0)

@@ -2,7 +2,7 @@
 // src/kokoro_decoder_backward.cpp. TEST INFRASTRUCTURE ONLY (parity oracle).
 //
 // The reference semantics (conv dgrad only, snake dAlpha discarded) are the
-// default; an `Ext` adds the north-star extensions: conv/convT/pool weight and
+// default; an `Ext` adds the extensions: conv/convT/pool weight and
 // bias grads and snake alpha grads, accumulated into the weight structs.
 #include "kdec_oracle.hpp"
 

@@ -6,7 +6,7 @@
 // HarmonicSource::load_from (:1556-1572); parameter names are the upstream
 // state-dict keys those loaders read. The style projection
 // (gamma, beta) = chunk(fc.W s + fc.b) follows compute_style_affine
-// (kokoro_modules.cpp:563-572); its adjoint (the north-star d(style)) follows
+// (kokoro_modules.cpp:563-572); its adjoint (the d(style) extension) follows
 // the lora_backward contract with the LoRA term absent
 // (decoder_lora.cpp:198-207).
 #include "kdec_oracle.hpp"

@@ -138,7 +138,7 @@ struct Conv1d {
     int in_channels = 0, out_channels = 0, kernel_size = 0;
     int stride = 1, padding = 0, dilation = 1, groups = 1;
     Vec W, b;    // W (out, in/groups*k); b (out) or empty
-    Vec dW, db;  // grad accumulators (north-star extension)
+    Vec dW, db;  // grad accumulators (extension)
     int L_out(int L) const {
         return conv1d_out_len(L, kernel_size, stride, padding, dilation);
     }
@@ -148,7 +148,7 @@ struct AdaIN1dWeights {
     int channels = 0, style_dim = 0;
     float eps = 1e-5f;
     Vec fcW, fcb;    // (2C, style_dim), (2C)
-    Vec dfcW, dfcb;  // grads (north-star extension)
+    Vec dfcW, dfcb;  // grads (extension)
 };
 
 struct AdainResBlk1dWeights {
@@ -193,7 +193,7 @@ struct HarmonicSource {
     Vec dlW, dlb;  // always zero: the harmonic source is forward-only
 };
 
-// Which north-star extensions the backward computes on top of the reference
+// Which extensions the backward computes on top of the reference
 // semantics (conv dgrad only, snake dalpha discarded, no d(style)).
 struct Ext {
     bool wgrad = false;   // conv / convT / pool weight+bias grads

@@ -2,9 +2,9 @@
 lines written by tests/conftest.py from model_parity.REPORT) into the
 markdown table kept under profiles/.
 
-    KDEC_PARITY_REPORT=gpurun_out/parity_report.jsonl \
+    KDEC_PARITY_REPORT=parity_report.jsonl \
         python -m pytest tests -m gpu -x -q
-    python tests/parity_report.py gpurun_out/parity_report.jsonl > profiles/parity_configs.md
+    python tests/parity_report.py parity_report.jsonl > profiles/parity_configs.md
 """
 from __future__ import annotations
 
@@ -28,8 +28,8 @@ def main(path):
            "cases), as recorded by one run of the suite on an MI355X:",
            "",
            "```",
-           "KDEC_PARITY_REPORT=gpurun_out/parity_report.jsonl python -m pytest tests -m gpu -x -q",
-           "python tests/parity_report.py gpurun_out/parity_report.jsonl > profiles/parity_configs.md",
+           "KDEC_PARITY_REPORT=parity_report.jsonl python -m pytest tests -m gpu -x -q",
+           "python tests/parity_report.py parity_report.jsonl > profiles/parity_configs.md",
            "```",
            "",
            "Bars: waveform and forward rel-L2 <= 1e-5, grads rel-L2 <= 1e-4 (a grad that is identically zero",

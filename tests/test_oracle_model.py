@@ -1,4 +1,4 @@
-"""Pins the oracle's assemblies and north-star extensions by finite differences.
+"""Pins the oracle's assemblies and their extensions by finite differences.
 
 The reference verifies its backward atoms with directional finite differences
 of an MSE loss (tests/test_kokoro_decoder_backward.cpp:97-125). The same check
