@@ -416,7 +416,6 @@ __global__ __launch_bounds__(RT) void adain_bwd_apply_v4_k(AdainArgs g, const fl
     constexpr int Q = EPT / 4;
     const int row = blockIdx.y;
     const int n = row / g.C, c = row - n * g.C;
-    dalpha_fold(ap, dalpha, N, g.C, n, c);
     const long off = static_cast<long>(c) * g.L;
     const float* x = g.X + n * g.x_bs + off;
     const float* dy = dY + n * dy_bs + off;
@@ -425,22 +424,25 @@ __global__ __launch_bounds__(RT) void adain_bwd_apply_v4_k(AdainArgs g, const fl
     const bool has_r = r != nullptr;
     const int head = row_head(x, g.L);
     const int nq = (g.L - head) >> 2;
-    // the data loads go out before the row's constants are fetched
-    const float4* x4 = reinterpret_cast<const float4*>(x + head);
-    const float4* d4 = reinterpret_cast<const float4*>(dy + head);
-    const float4* r4 = has_r ? reinterpret_cast<const float4*>(r + head) : nullptr;
+    // The data loads go out before the row's constants are fetched, as
+    // 16-byte buffer loads over the row's float4 body issued unconditionally
+    // (past the body, or with no residual grad, they read 0): written as
+    // guarded float4 loads they were split into four exec-masked 4-byte
+    // loads each, a quarter of the bytes per request.
+    const __amdgpu_buffer_rsrc_t xr = uniform_rsrc(x + head, nq * 16);
+    const __amdgpu_buffer_rsrc_t dr = uniform_rsrc(dy + head, nq * 16);
+    const __amdgpu_buffer_rsrc_t rr = uniform_rsrc(has_r ? r + head : x + head, has_r ? nq * 16 : 0);
     float4* o4 = reinterpret_cast<float4*>(dx + head);
     const int q0 = blockIdx.x * (RT * Q) + threadIdx.x;
-    const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     float4 xv[Q], dv[Q], rv[Q];
 #pragma unroll
     for (int j = 0; j < Q; ++j) {
-        const int q = q0 + j * RT;
-        const bool in = q < nq;
-        xv[j] = in ? x4[q] : z;
-        dv[j] = in ? d4[q] : z;
-        rv[j] = (in && has_r) ? r4[q] : z;
+        const int o = (q0 + j * RT) * 16;
+        xv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, o, 0, 0));
+        dv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(dr, o, 0, 0));
+        rv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rr, o, 0, 0));
     }
+    dalpha_fold(ap, dalpha, N, g.C, n, c);
     const BwdRow rc = bwd_row(g, rowv, row, n, c);
     if (blockIdx.x == 0) {
         const int t = threadIdx.x;
