@@ -35,6 +35,7 @@
 #include <algorithm>
 #include <cmath>
 #include <map>
+#include <type_traits>
 #include <mutex>
 #include <string>
 #include <utility>
@@ -1855,9 +1856,6 @@ void wgrad_gemm(WgradArgs g) {
         g.Pb[static_cast<long>(z) * g.M + m0 + tid] = static_cast<float>(bsum);
 }
 
-// out[i] += sum_z P[z][i] in a fixed order.  `transpose_k`: when non-zero the
-// element i = m*NN + (c*k + t) is stored at the conv-transpose layout
-// [c][m*k + t] instead (M = C_out of the transpose, c = its input channel).
 // db[m] += sum_y part[y*M + m] (one wave per row, four rows per 256-thread
 // block `blk`; double sums in a fixed lane order)
 __device__ inline void bias_rows(const float* part, float* db, int M, int S, int blk) {
@@ -1870,36 +1868,54 @@ __device__ inline void bias_rows(const float* part, float* db, int M, int S, int
     if (lane == 0) db[m] += static_cast<float>(acc);
 }
 
-// Blocks at and past `main_blocks` (when Pb is given) sum the bias
-// partials Pb[splits][M] into db instead, as bias_reduce would.
-__global__ void wgrad_reduce(const float* P, float* out, long MN, int splits,
-                             int transpose_k, int M, int NN, const float* Pb, float* db,
-                             unsigned main_blocks) {
+// out[i] += sum_z P[z][i] over the splits z, for V-float columns i (V = 4:
+// 16-byte accesses, MN a multiple of 4 and both arrays 16-B aligned). A
+// 256-thread block takes 256 / ZG columns and ZG split groups: thread (q, c)
+// sums its group's contiguous range of z in order, eight loads in flight
+// (each issued unconditionally from a clamped z, only its use bounded), and
+// the groups' sums are added in group order. The stage-1 weight grads have
+// hundreds of splits over a few thousand columns: the split groups turn one
+// long chain of memory round trips per column into ZG shorter ones. Blocks at
+// and past `main_blocks` (when Pb is given) sum the bias partials
+// Pb[splits][M] into db instead, as bias_reduce would.
+template <int V, int ZG>
+__global__ __launch_bounds__(256) void wgrad_reduce(const float* P, float* out, long MN, int splits, int M,
+                                                    const float* Pb, float* db, unsigned main_blocks) {
     if (blockIdx.x >= main_blocks) {
         bias_rows(Pb, db, M, splits, static_cast<int>(blockIdx.x - main_blocks));
         return;
     }
-    for (long i = blockIdx.x * static_cast<long>(blockDim.x) + threadIdx.x; i < MN;
-         i += static_cast<long>(main_blocks) * blockDim.x) {
-        float acc = 0.0f;
-        int z = 0;
-        for (; z + 8 <= splits; z += 8) {  // 8 loads in flight, summed in order
-            float v[8];
+    using T = typename std::conditional<V == 4, float4, float>::type;
+    constexpr int CW = 256 / ZG;
+    const T* Pv = reinterpret_cast<const T*>(P);
+    T* ov = reinterpret_cast<T*>(out);
+    const long MV = MN / V;
+    const int c = threadIdx.x % CW, q = threadIdx.x / CW;
+    const long i = static_cast<long>(blockIdx.x) * CW + c;
+    const long ic = i < MV ? i : MV - 1;
+    const int z0 = static_cast<int>(static_cast<long>(q) * splits / ZG);
+    const int z1 = static_cast<int>(static_cast<long>(q + 1) * splits / ZG);
+    T acc{};
+    for (int z = z0; z < z1; z += 8) {
+        T v[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = P[(z + j) * MN + i];
+        for (int j = 0; j < 8; ++j) v[j] = Pv[min(z + j, z1 - 1) * MV + ic];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc += v[j];
+        for (int j = 0; j < 8; ++j)
+            if (z + j < z1) acc += v[j];
+    }
+    if constexpr (ZG == 1) {
+        if (i < MV) ov[i] += acc;
+    } else {
+        __shared__ T red[ZG][CW];
+        red[q][c] = acc;
+        __syncthreads();
+        if (q == 0 && i < MV) {
+            T t = red[0][c];
+#pragma unroll
+            for (int g = 1; g < ZG; ++g) t += red[g][c];
+            ov[i] += t;
         }
-        for (; z < splits; ++z) acc += P[z * MN + i];
-        long o = i;
-        if (transpose_k) {
-            const int k = transpose_k;
-            const int m = static_cast<int>(i / NN);
-            const int n = static_cast<int>(i - static_cast<long>(m) * NN);
-            const int c = n / k, t = n - (n / k) * k;
-            o = (static_cast<long>(c) * M + m) * k + t;
-        }
-        out[o] += acc;
     }
 }
 
@@ -2717,10 +2733,26 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
     }
     // the weight-grad partials and, in extra blocks, the bias partials
     ProfScope ps(ctx, "wgrad_reduce", 0.0);
-    const unsigned mb = grid1d(MN);
+    const bool v4 = MN % 4 == 0 && ((reinterpret_cast<unsigned long long>(P.p) |
+                                     reinterpret_cast<unsigned long long>(out)) & 15) == 0;
+    const int zg = splits >= 64 ? 8 : splits >= 16 ? 4 : 1;
+    const long cols = v4 ? MN / 4 : MN;
+    const unsigned mb = static_cast<unsigned>(cdiv(cols, 256 / zg));
     const unsigned bb = db ? static_cast<unsigned>(cdiv(M, 4)) : 0u;
-    hipLaunchKernelGGL(wgrad_reduce, dim3(mb + bb), dim3(256), 0, ctx->stream, P.as<float>(), out, MN, splits, 0, M,
-                       NN, db ? Pb.as<float>() : nullptr, db, mb);
+    const void* kern = v4 ? (zg == 8   ? reinterpret_cast<const void*>(&wgrad_reduce<4, 8>)
+                             : zg == 4 ? reinterpret_cast<const void*>(&wgrad_reduce<4, 4>)
+                                       : reinterpret_cast<const void*>(&wgrad_reduce<4, 1>))
+                          : (zg == 8   ? reinterpret_cast<const void*>(&wgrad_reduce<1, 8>)
+                             : zg == 4 ? reinterpret_cast<const void*>(&wgrad_reduce<1, 4>)
+                                       : reinterpret_cast<const void*>(&wgrad_reduce<1, 1>));
+    const float* Pp = P.as<float>();
+    const float* Pbp = db ? Pb.as<float>() : nullptr;
+    long mn = MN;
+    int sp = splits, mrows = M;
+    unsigned mbk = mb;
+    void* args[] = {&Pp, &out, &mn, &sp, &mrows, &Pbp, &db, &mbk};
+    if (hipLaunchKernel(kern, dim3(mb + bb), dim3(256), args, 0, ctx->stream) != hipSuccess)
+        return fail(ctx, KDEC_EHIP, "wgrad_reduce: launch failed");
     return launch_check(ctx, "wgrad_reduce");
 }
 
