@@ -576,6 +576,12 @@ def test_fused_elementwise_passes(K, cols, bs):
     K.call("kdec_leaky_bwd", P(tx), bs, P(tdy), bs, P(t), bs, N, cols, 0.1)
     K.call("kdec_axpby", 1.0 / 3.0, P(t), bs, 0.0, None, 0, P(ref), bs, N, cols)
     assert torch.equal(got[:, :cols], ref[:, :cols])
+    # the leaky backward against numpy's float32 arithmetic (exact), and
+    # axpby with both operands
+    xs, dys = x[:, :cols], dy[:, :cols]
+    assert np.array_equal(h(t)[:, :cols], np.where(xs > 0, dys, np.float32(0.1) * dys))
+    K.call("kdec_axpby", 0.5, P(tx), bs, -2.0, P(tdy), bs, P(ref), bs, N, cols)
+    assert_close(h(ref)[:, :cols], 0.5 * xs.astype(np.float64) - 2.0 * dys.astype(np.float64), 1e-7, "axpby")
     a, b, c = g(rnd(N, bs)), g(rnd(N, bs)), g(rnd(N, bs))
     y, z = torch.empty(N, bs, device="cuda"), torch.empty(N, bs, device="cuda")
     K.call("kdec_add3_leaky", P(a), bs, P(b), bs, P(c), bs, P(y), bs, P(z), bs, N, cols, 0.01)
