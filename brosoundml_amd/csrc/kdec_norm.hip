@@ -232,17 +232,17 @@ __global__ __launch_bounds__(RT) void adain_act_fwd_v4_k(AdainArgs g, float* Y, 
     float* yp = Yp ? Yp + n * yp_bs + off : nullptr;
     const int head = row_head(x, g.L);
     const int nq = (g.L - head) >> 2;
-    // the data loads go out before the row's constants are fetched
-    const float4* x4 = reinterpret_cast<const float4*>(x + head);
+    // the data loads go out before the row's constants are fetched, as
+    // 16-byte buffer loads issued unconditionally (past the row's float4
+    // body they read 0)
+    const __amdgpu_buffer_rsrc_t xr = uniform_rsrc(x + head, nq * 16);
     float4* y4 = reinterpret_cast<float4*>(y + head);
     float4* yp4 = yp ? reinterpret_cast<float4*>(yp + head) : nullptr;
     const int q0 = blockIdx.x * (RT * Q) + threadIdx.x;
     float4 v[Q];
 #pragma unroll
-    for (int j = 0; j < Q; ++j) {
-        const int q = q0 + j * RT;
-        v[j] = q < nq ? x4[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
+    for (int j = 0; j < Q; ++j)
+        v[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, (q0 + j * RT) * 16, 0, 0));
     const FwdRow rc = fwd_row(g, row, n, c);
     if (blockIdx.x == 0) {
         const int t = threadIdx.x;
