@@ -1617,6 +1617,7 @@ struct WgradArgs {
     int XR;              // staged input rows per n-tile
     int span, segs;      // input-row staging: `span` positions as segs loads of up to 64
     int rs;              // LDS row stride of the staged input rows
+    int blk4;            // P in row quads: [split][M / 4][NN][4] (M a multiple of 4)
 };
 
 // P[z, m, c*k + t] = sum over this split's positions l of
@@ -1840,17 +1841,35 @@ void wgrad_gemm(WgradArgs g) {
     }
 
     float* Pz = g.P + static_cast<long>(z) * g.M * g.NN;
+    if (g.blk4) {  // uniform: a lane's four consecutive rows of a column as one 16-byte store
 #pragma unroll
-    for (int tn = 0; tn < 2; ++tn) {
-        const int n = n0 + wn * 64 + tn * 32 + l32;
-        if (n >= g.NN) continue;
+        for (int tn = 0; tn < 2; ++tn) {
+            const int n = n0 + wn * 64 + tn * 32 + l32;
+            if (n >= g.NN) continue;
 #pragma unroll
-        for (int tm = 0; tm < 2; ++tm)
+            for (int tm = 0; tm < 2; ++tm)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int m = m0 + wm * 64 + tm * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
-                if (m < g.M) Pz[static_cast<long>(m) * g.NN + n] = acc[tm][tn][e];
-            }
+                for (int j = 0; j < 4; ++j) {
+                    const int m = m0 + wm * 64 + tm * 32 + 8 * j + 4 * hi;  // a multiple of 4
+                    if (m < g.M)
+                        reinterpret_cast<float4*>(Pz)[static_cast<long>(m >> 2) * g.NN + n] =
+                            make_float4(acc[tm][tn][4 * j], acc[tm][tn][4 * j + 1], acc[tm][tn][4 * j + 2],
+                                        acc[tm][tn][4 * j + 3]);
+                }
+        }
+    } else {
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn) {
+            const int n = n0 + wn * 64 + tn * 32 + l32;
+            if (n >= g.NN) continue;
+#pragma unroll
+            for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int m = m0 + wm * 64 + tm * 32 + 8 * (e >> 2) + 4 * hi + (e & 3);
+                    if (m < g.M) Pz[static_cast<long>(m) * g.NN + n] = acc[tm][tn][e];
+                }
+        }
     }
     if (do_bias && tid < BM && m0 + tid < g.M)
         g.Pb[static_cast<long>(z) * g.M + m0 + tid] = static_cast<float>(bsum);
@@ -1869,7 +1888,9 @@ __device__ inline void bias_rows(const float* part, float* db, int M, int S, int
 }
 
 // out[i] += sum_z P[z][i] over the splits z, for V-float columns i (V = 4:
-// 16-byte accesses, MN a multiple of 4 and both arrays 16-B aligned). A
+// 16-byte accesses, MN a multiple of 4 and both arrays 16-B aligned; BLK:
+// the partials in the row-quad layout the GEMM stores 16 bytes at a time,
+// each column's four sums added to four rows of out). A
 // 256-thread block takes 256 / ZG columns and ZG split groups: thread (q, c)
 // sums its group's contiguous range of z in order, eight loads in flight
 // (each issued unconditionally from a clamped z, only its use bounded), and
@@ -1878,7 +1899,7 @@ __device__ inline void bias_rows(const float* part, float* db, int M, int S, int
 // long chain of memory round trips per column into ZG shorter ones. Blocks at
 // and past `main_blocks` (when Pb is given) sum the bias partials
 // Pb[splits][M] into db instead, as bias_reduce would.
-template <int V, int ZG>
+template <int V, int ZG, bool BLK = false>
 __global__ __launch_bounds__(256) void wgrad_reduce(const float* P, float* out, long MN, int splits, int M,
                                                     const float* Pb, float* db, unsigned main_blocks) {
     if (blockIdx.x >= main_blocks) {
@@ -1904,8 +1925,22 @@ __global__ __launch_bounds__(256) void wgrad_reduce(const float* P, float* out, 
         for (int j = 0; j < 8; ++j)
             if (z + j < z1) acc += v[j];
     }
+    // BLK: P in row quads, column i = (m / 4) * NN + n holds rows m .. m + 3
+    auto put = [&](const T& t) {
+        if constexpr (BLK) {
+            const long NN = MN / M;
+            const long mq = i / NN, n = i - mq * NN;
+            float* o = out + 4 * mq * NN + n;
+            o[0] += t.x;
+            o[NN] += t.y;
+            o[2 * NN] += t.z;
+            o[3 * NN] += t.w;
+        } else {
+            ov[i] += t;
+        }
+    };
     if constexpr (ZG == 1) {
-        if (i < MV) ov[i] += acc;
+        if (i < MV) put(acc);
     } else {
         __shared__ T red[ZG][CW];
         red[q][c] = acc;
@@ -1914,7 +1949,7 @@ __global__ __launch_bounds__(256) void wgrad_reduce(const float* P, float* out, 
             T t = red[0][c];
 #pragma unroll
             for (int g = 1; g < ZG; ++g) t += red[g][c];
-            ov[i] += t;
+            put(t);
         }
     }
 }
@@ -2714,6 +2749,7 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
     a.span = lay.span;
     a.segs = lay.segs;
     a.rs = lay.rs;
+    a.blk4 = M % 4 == 0 ? 1 : 0;
     if (static_cast<long>(L_x) * 4 > 0x7fffffffL || static_cast<long>(L_g) * 4 > 0x7fffffffL)
         return fail(ctx, KDEC_EINVAL, "wgrad: rows too long");
     if (static_cast<long>(M) * L_g * 4 > 0x7fffffffL || static_cast<long>(C_x) * L_x * 4 > 0x7fffffffL)
@@ -2733,13 +2769,17 @@ static int wgrad_common(kdec_ctx* ctx, const float* X, long x_bs, const float* G
     }
     // the weight-grad partials and, in extra blocks, the bias partials
     ProfScope ps(ctx, "wgrad_reduce", 0.0);
-    const bool v4 = MN % 4 == 0 && ((reinterpret_cast<unsigned long long>(P.p) |
-                                     reinterpret_cast<unsigned long long>(out)) & 15) == 0;
+    const bool blk = a.blk4 != 0;
+    const bool v4 = blk || (MN % 4 == 0 && ((reinterpret_cast<unsigned long long>(P.p) |
+                                             reinterpret_cast<unsigned long long>(out)) & 15) == 0);
     const int zg = splits >= 64 ? 8 : splits >= 16 ? 4 : 1;
     const long cols = v4 ? MN / 4 : MN;
     const unsigned mb = static_cast<unsigned>(cdiv(cols, 256 / zg));
     const unsigned bb = db ? static_cast<unsigned>(cdiv(M, 4)) : 0u;
-    const void* kern = v4 ? (zg == 8   ? reinterpret_cast<const void*>(&wgrad_reduce<4, 8>)
+    const void* kern = blk ? (zg == 8   ? reinterpret_cast<const void*>(&wgrad_reduce<4, 8, true>)
+                              : zg == 4 ? reinterpret_cast<const void*>(&wgrad_reduce<4, 4, true>)
+                                        : reinterpret_cast<const void*>(&wgrad_reduce<4, 1, true>))
+                       : v4 ? (zg == 8   ? reinterpret_cast<const void*>(&wgrad_reduce<4, 8>)
                              : zg == 4 ? reinterpret_cast<const void*>(&wgrad_reduce<4, 4>)
                                        : reinterpret_cast<const void*>(&wgrad_reduce<4, 1>))
                           : (zg == 8   ? reinterpret_cast<const void*>(&wgrad_reduce<1, 8>)
