@@ -23,6 +23,16 @@
 namespace kdec {
 namespace {
 
+// The float4 buffer access is declared on the LLVM intrinsic itself: with
+// this compiler, __builtin_amdgcn_raw_buffer_load_b128 (and _b64) whose
+// elements are read one by one is narrowed to a single-dword load and every
+// element then reads element 0.
+using f32x4 = float __attribute__((ext_vector_type(4)));
+__device__ f32x4 buf_ld_f4(__amdgpu_buffer_rsrc_t r, int voff, int soff, int aux)
+    __asm("llvm.amdgcn.raw.ptr.buffer.load.v4f32");
+__device__ void buf_st_f4(f32x4 v, __amdgpu_buffer_rsrc_t r, int voff, int soff, int aux)
+    __asm("llvm.amdgcn.raw.ptr.buffer.store.v4f32");
+
 constexpr int RT = 256;  // threads per row block
 
 __device__ inline double block_sum(double v, double* red) {
@@ -242,7 +252,7 @@ __global__ __launch_bounds__(RT) void adain_act_fwd_v4_k(AdainArgs g, float* Y, 
     float4 v[Q];
 #pragma unroll
     for (int j = 0; j < Q; ++j)
-        v[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, (q0 + j * RT) * 16, 0, 0));
+        v[j] = __builtin_bit_cast(float4, buf_ld_f4(xr, (q0 + j * RT) * 16, 0, 0));
     const FwdRow rc = fwd_row(g, row, n, c);
     if (blockIdx.x == 0) {
         const int t = threadIdx.x;
@@ -439,9 +449,9 @@ __global__ __launch_bounds__(RT) void adain_bwd_apply_v4_k(AdainArgs g, const fl
 #pragma unroll
     for (int j = 0; j < Q; ++j) {
         const int o = (q0 + j * RT) * 16;
-        xv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, o, 0, 0));
-        dv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(dr, o, 0, 0));
-        rv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rr, o, 0, 0));
+        xv[j] = __builtin_bit_cast(float4, buf_ld_f4(xr, o, 0, 0));
+        dv[j] = __builtin_bit_cast(float4, buf_ld_f4(dr, o, 0, 0));
+        rv[j] = __builtin_bit_cast(float4, buf_ld_f4(rr, o, 0, 0));
     }
     dalpha_fold(ap, dalpha, N, g.C, n, c);
     const BwdRow rc = bwd_row(g, rowv, row, n, c);
@@ -503,15 +513,6 @@ __device__ inline void row_st(__amdgpu_buffer_rsrc_t r, float v, int voff, int j
 // V = 4 (rows of a multiple of 4 floats on 16-B aligned bases), element
 // 4*((e/4)*NTB + t) + e%4, one 16-B access per four elements. Past the row
 // the descriptor reads 0 and drops stores, a float4 wholly in either case.
-// The float4 buffer access is declared on the LLVM intrinsic itself: with
-// this compiler, __builtin_amdgcn_raw_buffer_load_b128 (and _b64) whose
-// elements are read one by one is narrowed to a single-dword load and every
-// element then reads element 0.
-using f32x4 = float __attribute__((ext_vector_type(4)));
-__device__ f32x4 buf_ld_f4(__amdgpu_buffer_rsrc_t r, int voff, int soff, int aux)
-    __asm("llvm.amdgcn.raw.ptr.buffer.load.v4f32");
-__device__ void buf_st_f4(f32x4 v, __amdgpu_buffer_rsrc_t r, int voff, int soff, int aux)
-    __asm("llvm.amdgcn.raw.ptr.buffer.store.v4f32");
 
 template <int V, int NTB>
 __device__ inline void row_ld_grp(__amdgpu_buffer_rsrc_t r, int j, float* v) {
