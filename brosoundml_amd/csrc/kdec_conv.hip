@@ -1347,13 +1347,27 @@ __device__ inline void chan_merge(double& n, double& mean, double& m2, double nb
 }
 
 // stats[row] = (mean, 1 / sqrt(var + eps)) from the row's slot records: one
-// wave per row, lane j merging slots j, j + 64, ... in order, then the lanes
-// in a fixed tree.
+// wave per row, lane j merging slots j, j + 64, ... in order (eight slots'
+// loads in flight, issued unconditionally from clamped indices), then the
+// lanes in a fixed tree.
 __global__ __launch_bounds__(64) void instnorm_fin_slots_k(const double* part, int nch, float eps, float2* stats) {
+    __builtin_amdgcn_s_setprio(2);  // on the conv chain: as the AdaIN passes
     const int row = blockIdx.x;
     const double* p = part + static_cast<long>(row) * nch * 3;
     double n = 0.0, mean = 0.0, m2 = 0.0;
-    for (int j = threadIdx.x; j < nch; j += 64) chan_merge(n, mean, m2, p[3 * j], p[3 * j + 1], p[3 * j + 2]);
+    for (int j0 = threadIdx.x; j0 < nch; j0 += 8 * 64) {
+        double a[8], b[8], c[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int j = min(j0 + 64 * u, nch - 1);
+            a[u] = p[3 * j];
+            b[u] = p[3 * j + 1];
+            c[u] = p[3 * j + 2];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (j0 + 64 * u < nch) chan_merge(n, mean, m2, a[u], b[u], c[u]);
+    }
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
         const double n2 = __shfl_xor(n, o, 64), mean2 = __shfl_xor(mean, o, 64), m22 = __shfl_xor(m2, o, 64);

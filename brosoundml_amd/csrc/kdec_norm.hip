@@ -1218,10 +1218,24 @@ __global__ __launch_bounds__(64) void adain_bwd_fin_wide_k(const double* part, i
     const int n = row / C, c = row - n * C;
     const double* p = part + static_cast<long>(row) * nch * 3;
     double sd = 0.0, sdx = 0.0, sa = 0.0;
-    for (int j = threadIdx.x; j < nch; j += 64) {
-        sd += p[j * 3];
-        sdx += p[j * 3 + 1];
-        sa += p[j * 3 + 2];
+    // slots j, j + 64, ... in order, eight slots' loads in flight (issued
+    // unconditionally from clamped indices)
+    for (int j0 = threadIdx.x; j0 < nch; j0 += 8 * 64) {
+        double a[8], b[8], c[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int j = min(j0 + 64 * u, nch - 1);
+            a[u] = p[j * 3];
+            b[u] = p[j * 3 + 1];
+            c[u] = p[j * 3 + 2];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (j0 + 64 * u < nch) {
+                sd += a[u];
+                sdx += b[u];
+                sa += c[u];
+            }
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
