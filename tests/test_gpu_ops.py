@@ -116,6 +116,27 @@ def test_conv1d_fwd_dgrad_wgrad(K, N, C_in, C_out, L, k, s, p, d):
     assert_close(h(db), rb, GRAD_TOL, "conv1d backward_bias")
 
 
+@pytest.mark.parametrize("C_out,L", [
+    (128, 4000),    # ~31 splits: partials in row quads, four split groups per column
+    (22, 30000),    # C_out not a multiple of 4: row-major partials, 16-byte reduce, eight groups
+    (128, 61441),   # hundreds of splits: row quads, eight groups
+])
+def test_conv1d_wgrad_split_plans(K, C_out, L):
+    # The weight grad's split-K partial layouts and reduce plans against
+    # torch's float64 weight grad, with the bias grad.
+    N, C_in, k, d = 2, 128, 7, 3
+    p = d * (k - 1) // 2
+    x, dY = rnd(N, C_in, L, scale=0.5), rnd(N, C_out, L, scale=0.5)
+    dW = torch.zeros(C_out, C_in * k, device="cuda")
+    db = torch.zeros(C_out, device="cuda")
+    K.call("kdec_conv1d_wgrad", P(g(x)), C_in * L, P(g(dY)), C_out * L, P(dW), P(db), N, C_in, L, C_out, k, 1, p,
+           d)
+    ref = torch.nn.grad.conv1d_weight(torch.from_numpy(x).double(), (C_out, C_in, k),
+                                      torch.from_numpy(dY).double(), padding=p, dilation=d)
+    assert_close(h(dW), ref.reshape(C_out, C_in * k).numpy(), GRAD_TOL, "conv1d backward_weight, split plans")
+    assert_close(h(db), dY.astype(np.float64).sum(axis=(0, 2)), GRAD_TOL, "conv1d backward_bias, split plans")
+
+
 @pytest.mark.parametrize("k,d", [(7, 3), (3, 1)])
 def test_conv1d_grid_beyond_one_round(K, k, d):
     # 1301 output tiles: more than one round of resident blocks, so the last
