@@ -415,7 +415,13 @@ __global__ __launch_bounds__(RT) void adain_bwd_apply_k(AdainArgs g, const float
     }
 }
 
-// The 16-byte form (head / float4s / tail as adain_act_fwd_v4_k).
+// The 16-byte form (head / float4s / tail as adain_act_fwd_v4_k), with
+// BWD_Q float4s of each operand per thread: two rather than four gives twice
+// the blocks at the same bytes in flight per CU, so blocks that start late
+// (beside the weight-grad GEMMs) hold less of the pass (one-stream family
+// 5.20 -> 5.12 ms/step, overlapped 16.1 -> 12.7; eight: 5.50).
+constexpr int BWD_Q = 2;
+unsigned v4_blocks_bwd(int L) { return static_cast<unsigned>(std::max(1L, cdiv(static_cast<long>(L) / 4, RT * BWD_Q))); }
 __global__ __launch_bounds__(RT) void adain_bwd_apply_v4_k(AdainArgs g, const float* dY, long dy_bs,
                                                           const float* R, long r_bs, float* dX, long dx_bs,
                                                           const float2* rowv, const float* ap, float* dalpha,
@@ -424,7 +430,7 @@ __global__ __launch_bounds__(RT) void adain_bwd_apply_v4_k(AdainArgs g, const fl
     // this pass sits on the conv chain, and its loads and stores win
     // issue slots over their MFMA waves on a shared SIMD
     __builtin_amdgcn_s_setprio(2);
-    constexpr int Q = EPT / 4;
+    constexpr int Q = BWD_Q;
     const int row = blockIdx.y;
     const int n = row / g.C, c = row - n * g.C;
     const long off = static_cast<long>(c) * g.L;
@@ -1194,7 +1200,7 @@ int bwd_run(kdec_ctx* ctx, const AdainArgs& g, const float* dY, long dy_bs, cons
         // the apply also folds the per-row alpha shares into dalpha
         const float* ap = want_alpha ? sc.apart : nullptr;
         if (rows_v4({{g.X, g.x_bs}, {dY, dy_bs}, {R, r_bs}, {dX, dx_bs}}))
-            hipLaunchKernelGGL(adain_bwd_apply_v4_k, dim3(v4_blocks(L), rows), dim3(RT), 0, ctx->stream, g, dY,
+            hipLaunchKernelGGL(adain_bwd_apply_v4_k, dim3(v4_blocks_bwd(L), rows), dim3(RT), 0, ctx->stream, g, dY,
                                dy_bs, R, r_bs, dX, dx_bs, sc.rowv, ap, dalpha, N);
         else
             hipLaunchKernelGGL(adain_bwd_apply_k, dim3(nch, rows), dim3(RT), 0, ctx->stream, g, dY, dy_bs, R, r_bs,
@@ -1277,7 +1283,7 @@ int adain_bwd_finish(kdec_ctx* ctx, const float* X, long x_bs, const float* stat
     // (and dalpha += the per-row alpha shares, summed over utterances in order)
     const float* apf = want_alpha ? ap.as<float>() : nullptr;
     if (rows_v4({{X, x_bs}, {ds, ds_bs}, {R, r_bs}, {dX, dx_bs}}))
-        hipLaunchKernelGGL(adain_bwd_apply_v4_k, dim3(v4_blocks(L), static_cast<unsigned>(rows)), dim3(RT), 0,
+        hipLaunchKernelGGL(adain_bwd_apply_v4_k, dim3(v4_blocks_bwd(L), static_cast<unsigned>(rows)), dim3(RT), 0,
                            ctx->stream, ga, ds, ds_bs, R, r_bs, dX, dx_bs, rv.as<float2>(), apf, dalpha, N);
     else
         hipLaunchKernelGGL(adain_bwd_apply_k, dim3(static_cast<unsigned>(cdiv(L, CH)), static_cast<unsigned>(rows)),
