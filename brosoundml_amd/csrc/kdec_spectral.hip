@@ -740,7 +740,7 @@ constexpr int STN = 8;            // d(style) utterances per pass
 
 // LDS floats of the forward kernel: slab, styles, group sums
 inline size_t style_fwd_lds_floats(int S) {
-    return static_cast<size_t>(STR) * (S + 4) + static_cast<size_t>(STG) * STQ * STR;
+    return static_cast<size_t>(STR) * (S + 4) + static_cast<size_t>(STG) * STQ * STR + static_cast<size_t>(STQ) * S;
 }
 
 __device__ inline float style_ld(__amdgpu_buffer_rsrc_t r, int byte_off, int soff = 0) {
@@ -752,7 +752,10 @@ __device__ inline float style_ld(__amdgpu_buffer_rsrc_t r, int byte_off, int sof
 // used: a load under a branch is followed by a wait for it at the branch's
 // join, which turns a run of guarded loads into one memory round trip each.
 
-// Forward; KQ = STR * S / 1024 slab float4s per thread (S <= 128).
+// Forward; KQ = STR * S / 1024 slab float4s per thread (S <= 128). A
+// pass's STQ style rows are staged in LDS too and read there by broadcast
+// (a wave's lanes all read one address): read by scalar loads, each
+// utterance's operands were a round trip of their own.
 template <int KQ>
 __global__ __launch_bounds__(256) void style_fwd_rows_k(const float* __restrict__ W, const float* __restrict__ bias,
                                                         const float* __restrict__ style, long s_bs,
@@ -761,42 +764,65 @@ __global__ __launch_bounds__(256) void style_fwd_rows_k(const float* __restrict_
     const int SP = S + 4;
     float* wt = sm;                           // [STR][S + 4]
     float* red = wt + STR * SP;               // [STG][STQ][STR]
+    float* sty = red + STG * STQ * STR;       // [STQ][S]: the pass's style rows
     const int t = threadIdx.x;
     const int r0 = blockIdx.x * STR;
     const int nr = min(STR, rows - r0);
     const int S4 = S >> 2;
-    {  // the slab, STR * S4 == 256 * KQ float4s, all in flight
+    // a pass's style rows as STQ * S4 float4s, one per thread at most (a
+    // slot past N repeats the last utterance; its sums are not stored)
+    const bool sl = t < STQ * S4;
+    const int sq = t / S4, sc4 = t - (t / S4) * S4;
+    auto sty_fetch = [&](int n0) {
+        return sl ? *reinterpret_cast<const float4*>(style + min(n0 + sq, N - 1) * s_bs + 4 * sc4)
+                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    };
+    // the bias by a buffer load issued with the others (none: a descriptor
+    // over nothing, which reads 0)
+    const __amdgpu_buffer_rsrc_t br = uniform_rsrc(bias ? bias : W, bias ? rows * 4 : 0);
+    const float bv = style_ld(br, min(r0 + (t & (STR - 1)), rows - 1) * 4);
+    {  // the slab, STR * S4 == 256 * KQ float4s, and the first pass's style rows, all in flight
         const __amdgpu_buffer_rsrc_t wr = uniform_rsrc(W, rows * S * 4);
         const int wb = r0 * S * 4;
         float4 v[KQ];
 #pragma unroll
         for (int k = 0; k < KQ; ++k)
             v[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(wr, wb + (t + 256 * k) * 16, 0, 0));
+        const float4 y0 = sty_fetch(0);
 #pragma unroll
         for (int k = 0; k < KQ; ++k) {
             const int i = t + 256 * k;
             const int row = i / S4, c4 = i - row * S4;
             *reinterpret_cast<float4*>(wt + row * SP + c4 * 4) = v[k];
         }
+        if (sl) *reinterpret_cast<float4*>(sty + 4 * t) = y0;
     }
     __syncthreads();
     const int c = __builtin_amdgcn_readfirstlane(t >> 6), r = t & 63;
     constexpr int cw = 4 * KQ;  // columns per wave: S / STG
     const float* w = wt + r * SP + c * cw;
-    const float* sg = style + c * cw;  // wave-uniform: the style operands are scalar loads
+    const float* sg = sty + c * cw;  // wave-uniform address: LDS broadcast
     for (int n0 = 0; n0 < N; n0 += STQ) {
         const int nn = min(STQ, N - n0);
+        if (n0 > 0) {  // the previous pass ended at a barrier: its style rows are no longer read
+            const float4 y0 = sty_fetch(n0);
+            if (sl) *reinterpret_cast<float4*>(sty + 4 * t) = y0;
+            __syncthreads();
+        }
         float acc[STQ];
 #pragma unroll
         for (int q = 0; q < STQ; ++q) acc[q] = 0.0f;
 #pragma unroll
         for (int jj = 0; jj < cw; jj += 4) {
-            // every utterance slot's operands loaded before the first use (a
-            // slot past N repeats the last utterance; its sums are not stored)
+            // each step's LDS reads stay in the step, after the previous
+            // step's sums (hoisted, the broadcast operands of every step
+            // would take 8 * cw registers per lane)
+            static_assert(STQ == 8, "one asm operand per utterance slot");
+            asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(acc[4]), "+v"(acc[5]),
+                         "+v"(acc[6]), "+v"(acc[7])::"memory");
             float4 y[STQ];
 #pragma unroll
-            for (int q = 0; q < STQ; ++q)
-                y[q] = *reinterpret_cast<const float4*>(sg + min(n0 + q, N - 1) * s_bs + jj);
+            for (int q = 0; q < STQ; ++q) y[q] = *reinterpret_cast<const float4*>(sg + q * S + jj);
             const float4 x = *reinterpret_cast<const float4*>(w + jj);
 #pragma unroll
             for (int q = 0; q < STQ; ++q) {
@@ -813,12 +839,12 @@ __global__ __launch_bounds__(256) void style_fwd_rows_k(const float* __restrict_
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < STQ * STR / 256; ++k) {
-            const int i = t + 256 * k, q = i / STR, rr = i - q * STR;
+            const int i = t + 256 * k, q = i / STR, rr = i - q * STR;  // rr == t % STR
             if (q < nn && rr < nr) {
                 double sum = 0.0;
 #pragma unroll
                 for (int cc = 0; cc < STG; ++cc) sum += static_cast<double>(red[(cc * STQ + q) * STR + rr]);
-                out[(n0 + q) * o_bs + r0 + rr] = static_cast<float>(sum + (bias ? bias[r0 + rr] : 0.0f));
+                out[(n0 + q) * o_bs + r0 + rr] = static_cast<float>(sum + bv);
             }
         }
         __syncthreads();
