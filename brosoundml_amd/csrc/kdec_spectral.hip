@@ -717,23 +717,25 @@ __global__ void style_bwd_w_k(const float* style, long s_bs, const float* dout, 
 // The same projections reading each fc row once for all N utterances (the
 // wave-per-(row, utterance) kernels above read the fc block N times).
 //
-// Forward: a block owns STR = 64 consecutive rows, staged in LDS as
+// Forward: a block owns STR = 32 consecutive rows, staged in LDS as
 // [STR][S + 4] with 16-byte loads, all in flight before the first store (the
-// padded stride spreads a wave's 16-byte row reads over the 32 banks eight
-// lanes at a time). Lane r of wave c forms row r's dot products over column
-// group c (S / STG consecutive columns) for STQ utterances at a time: float
-// sums of S / STG terms in column order, the row operands read 16 bytes at a
-// time from LDS and the style operands, uniform across the wave, by scalar
-// loads. The STG groups' sums are added in group order in double, with the
-// bias.
+// padded stride spreads the 16-byte row reads over the banks). Lane r of
+// half-wave c forms row r's dot products over column group c (S / STG
+// consecutive columns) for STQ utterances at a time: float sums of S / STG
+// terms in column order, the row operands read 16 bytes at a time from LDS
+// and the style operands, one address per half-wave, from the pass's style
+// rows staged in LDS. The STG groups' sums are added in group order in
+// double, with the bias. 32 rows per block rather than 64: the 37 396 rows
+// then spread over 1169 blocks instead of 585 (2.3 per CU, some CUs with
+// one more than others), 5.4 -> 4.9 µs.
 // d(style): thread (ph, j) = (t / S, t % S) sums, in
 // float and in row order, rows ph, ph + PH, ... of the block's STB rows
 // (PH = 256 / S phases) for STN utterances at a time, its column's weights
 // loaded all at once and the d(out) operands read from LDS; the phases' sums
 // are added in phase order in double, and the blocks' partials summed, in
 // block order, by style_bwd_x_sum_k.
-constexpr int STR = 64;           // forward rows per block (a wave's lanes)
-constexpr int STG = 4;            // forward column groups (one per wave)
+constexpr int STR = 32;           // forward rows per block (a half-wave's lanes)
+constexpr int STG = 8;            // forward column groups (one per half-wave)
 constexpr int STQ = 8;            // forward utterances per pass
 constexpr int STB = 64;           // d(style) rows per block
 constexpr int STN = 8;            // d(style) utterances per pass
@@ -752,7 +754,8 @@ __device__ inline float style_ld(__amdgpu_buffer_rsrc_t r, int byte_off, int sof
 // used: a load under a branch is followed by a wait for it at the branch's
 // join, which turns a run of guarded loads into one memory round trip each.
 
-// Forward; KQ = STR * S / 1024 slab float4s per thread (S <= 128). A
+// Forward; KQ = STR * S / 1024 slab float4s per thread (S <= 128, a
+// multiple of 32). A
 // pass's STQ style rows are staged in LDS too and read there by broadcast
 // (a wave's lanes all read one address): read by scalar loads, each
 // utterance's operands were a round trip of their own.
@@ -798,10 +801,10 @@ __global__ __launch_bounds__(256) void style_fwd_rows_k(const float* __restrict_
         if (sl) *reinterpret_cast<float4*>(sty + 4 * t) = y0;
     }
     __syncthreads();
-    const int c = __builtin_amdgcn_readfirstlane(t >> 6), r = t & 63;
-    constexpr int cw = 4 * KQ;  // columns per wave: S / STG
+    const int c = t / STR, r = t % STR;
+    constexpr int cw = 4 * KQ;  // columns per half-wave: S / STG
     const float* w = wt + r * SP + c * cw;
-    const float* sg = sty + c * cw;  // wave-uniform address: LDS broadcast
+    const float* sg = sty + c * cw;  // one address per half-wave: LDS broadcast
     for (int n0 = 0; n0 < N; n0 += STQ) {
         const int nn = min(STQ, N - n0);
         if (n0 > 0) {  // the previous pass ended at a barrier: its style rows are no longer read
@@ -1172,19 +1175,15 @@ int kdec_style_proj_fwd(kdec_ctx* ctx, const float* W, const float* b,
     // W once, style and out per utterance
     ProfScope ps(ctx, "style_proj", 0, 4.0 * (static_cast<double>(rows) * S + static_cast<double>(N) * (S + rows)));
     const size_t lds = style_fwd_lds_floats(S) * sizeof(float);
-    if (lds <= 64 * 1024 && S <= 128 && S % 16 == 0 && (reinterpret_cast<unsigned long long>(W) & 15) == 0 &&
+    if (lds <= 64 * 1024 && S <= 128 && S % (1024 / STR) == 0 && (reinterpret_cast<unsigned long long>(W) & 15) == 0 &&
         (reinterpret_cast<unsigned long long>(style) & 15) == 0 && style_bs % 4 == 0 &&
         static_cast<long>(rows) * S * 4 < (1L << 31)) {
         const void* k = nullptr;
-        switch (S / 16) {  // slab float4s per thread
+        switch (S * STR / 1024) {  // slab float4s per thread
             case 1: k = reinterpret_cast<const void*>(&style_fwd_rows_k<1>); break;
             case 2: k = reinterpret_cast<const void*>(&style_fwd_rows_k<2>); break;
             case 3: k = reinterpret_cast<const void*>(&style_fwd_rows_k<3>); break;
-            case 4: k = reinterpret_cast<const void*>(&style_fwd_rows_k<4>); break;
-            case 5: k = reinterpret_cast<const void*>(&style_fwd_rows_k<5>); break;
-            case 6: k = reinterpret_cast<const void*>(&style_fwd_rows_k<6>); break;
-            case 7: k = reinterpret_cast<const void*>(&style_fwd_rows_k<7>); break;
-            default: k = reinterpret_cast<const void*>(&style_fwd_rows_k<8>); break;
+            default: k = reinterpret_cast<const void*>(&style_fwd_rows_k<4>); break;
         }
         void* args[] = {&W, &b, &style, &style_bs, &out, &out_bs, &N, &rows, &S};
         if (hipLaunchKernel(k, dim3(static_cast<unsigned>(cdiv(rows, STR))), dim3(256), args, lds, ctx->stream) !=
