@@ -725,9 +725,9 @@ __global__ void style_bwd_w_k(const float* style, long s_bs, const float* dout, 
 // terms in column order, the row operands read 16 bytes at a time from LDS
 // and the style operands, one address per half-wave, from the pass's style
 // rows staged in LDS. The STG groups' sums are added in group order in
-// double, with the bias. 32 rows per block rather than 64: the 37 396 rows
-// then spread over 1169 blocks instead of 585 (2.3 per CU, some CUs with
-// one more than others), 5.4 -> 4.9 µs.
+// double, with the bias. 32 rows per block rather than 64: the decoder's
+// 37 396 rows then make 1169 blocks, where 585 left some CUs a third block
+// to run after the others were done (5.4 -> 4.9 µs).
 // d(style): thread (ph, j) = (t / S, t % S) sums, in
 // float and in row order, rows ph, ph + PH, ... of the block's STB rows
 // (PH = 256 / S phases) for STN utterances at a time, its column's weights
