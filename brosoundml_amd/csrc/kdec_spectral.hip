@@ -875,15 +875,16 @@ __global__ __launch_bounds__(256) void style_bwd_x_rows_k(const float* W, const 
     for (int i = 0; i < PER; ++i) w[i] = style_ld(wr, vo, i * 1024);
     for (int n0 = 0; n0 < N; n0 += STN) {
         const int nn = min(STN, N - n0);
-        {  // STB * STN == 2 * 256 d(out) values
-            float dv[2];
+        {  // STB * STN == DK * 256 d(out) values
+            constexpr int DK = STB * STN / 256;
+            float dv[DK];
 #pragma unroll
-            for (int k = 0; k < 2; ++k) {
+            for (int k = 0; k < DK; ++k) {
                 const int i = threadIdx.x + 256 * k, rr = i / STN, q = i - rr * STN;
                 dv[k] = style_ld(dr, static_cast<int>(((n0 + q) * d_bs + r0 + rr) * 4));
             }
 #pragma unroll
-            for (int k = 0; k < 2; ++k) {
+            for (int k = 0; k < DK; ++k) {
                 const int i = threadIdx.x + 256 * k, rr = i / STN, q = i - rr * STN;
                 dsl[i] = (rr < nr && q < nn) ? dv[k] : 0.0f;
             }
